@@ -1,0 +1,103 @@
+"""Loader of the in-tree libava_amd.so and the ctypes signatures of include/ava.h.
+
+The product path has no fallback: if the HIP library is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libava_amd.so")
+
+vp = C.c_void_p
+i32 = C.c_int
+f32 = C.c_float
+sz = C.c_size_t
+
+
+class QW(C.Structure):
+    """ava_qw: one int8 weight matrix (device pointers)."""
+    _fields_ = [("din", i32), ("dout", i32), ("ldk", i32), ("qt", vp), ("scale", vp)]
+
+
+class Config(C.Structure):
+    _fields_ = [(n, i32) for n in ("vocab", "d", "layers", "hidden", "kwta_k", "head_size", "gate_rank",
+                                   "eng_block", "eng_dim", "levels", "alif", "lif_scale", "value_residual",
+                                   "dense", "relu2")] + \
+               [("momentum", f32), ("cap", f32), ("planes", i32)]
+
+
+BLOCK_FIELDS = ["lif_norm", "win", "beta_p", "theta", "arho", "again", "wout",
+                "mem_norm", "wq", "wk", "wv", "we", "wg", "wo",
+                "wa", "ba", "wb", "bb", "off", "wa1", "wa2", "wb1", "wb2", "vres",
+                "eng_norm", "ewq", "ewk", "ewv", "ewo",
+                "mlp_norm", "w1", "w2", "dense"]
+
+
+class BlockParams(C.Structure):
+    _fields_ = [(n, vp) for n in BLOCK_FIELDS]
+
+
+class Params(C.Structure):
+    _fields_ = [("tok_emb", vp), ("final_norm", vp), ("blocks", C.POINTER(BlockParams))]
+
+
+class State(C.Structure):
+    _fields_ = [("lif_v", vp), ("lif_s", vp), ("lif_a", vp), ("mem_f", vp), ("mem_s", vp),
+                ("eng_k", vp), ("eng_v", vp), ("eng_cap", i32), ("eng_len", i32)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"libava_amd.so is not built ({LIB_PATH}); run `python -m ava_amd.build`")
+    L = C.CDLL(LIB_PATH)
+    L.ava_last_error.restype = C.c_char_p
+    L.ava_version.restype = C.c_char_p
+    sig = {
+        "ava_q8_ldk": [i32],
+        "ava_q8_pack": [vp, i32, i32, vp, vp, vp],
+        "ava_q8_quant_rows": [vp, i32, i32, i32, vp, vp, vp],
+        "ava_q8_gemm_acc": [vp, i32, i32, C.POINTER(QW), vp, vp],
+        "ava_q8_matmul": [vp, i32, C.POINTER(QW), i32, vp, vp, sz, vp],
+        "ava_q8_matmul_i8": [vp, i32, C.POINTER(QW), vp, vp],
+        "ava_lif_scan": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
+        "ava_lif_scan_tuned": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, vp],
+        "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
+        "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
+        "ava_delta_chunk": [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
+        "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
+        "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
+    }
+    for name, args in sig.items():
+        fn = getattr(L, name, None)
+        if fn is None:
+            continue
+        fn.argtypes = args
+        fn.restype = i32
+    L.ava_q8_workspace.argtypes = [i32, i32, i32]
+    L.ava_q8_workspace.restype = sz
+    if hasattr(L, "ava_model_free"):
+        L.ava_model_free.argtypes = [vp]
+        L.ava_model_free.restype = None
+    if hasattr(L, "ava_model_scratch_bytes"):
+        L.ava_model_scratch_bytes.argtypes = [vp]
+        L.ava_model_scratch_bytes.restype = sz
+    _lib = L
+    return L
+
+
+class AvaError(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str = ""):
+    if rc != 0:
+        msg = lib().ava_last_error().decode(errors="replace")
+        raise AvaError(f"{what or 'ava'} failed ({rc}): {msg}")

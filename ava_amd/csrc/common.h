@@ -1,0 +1,91 @@
+// Shared host/device helpers of libava_amd (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ava.h"
+
+namespace ava {
+
+// Per-thread last error (ava_last_error).
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+
+}  // namespace ava
+
+#define AVA_REQUIRE(cond, code, ...)                     \
+    do {                                                 \
+        if (!(cond)) return ::ava::fail(code, __VA_ARGS__); \
+    } while (0)
+
+#define AVA_HIP(call)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return ::ava::fail(AVA_ERR_HIP, "%s: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                               __FILE__, __LINE__);                                      \
+    } while (0)
+
+// After a kernel launch: report a launch error as AVA_ERR_HIP.
+#define AVA_LAUNCHED(name)                                                                   \
+    do {                                                                                     \
+        hipError_t e_ = hipGetLastError();                                                   \
+        if (e_ != hipSuccess)                                                                \
+            return ::ava::fail(AVA_ERR_HIP, "%s launch: %s", name, hipGetErrorString(e_));   \
+    } while (0)
+
+namespace ava {
+
+static inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
+
+// Leading dimension of int8 operands of the i8 MFMA products: K padded to 64 with zeros.
+static inline int q8_ldk(int k) { return (k + 63) / 64 * 64; }
+
+// ---- the split-plane activation format (shared by every producer of a dense int8 product input)
+// Row exponent: the smallest e with amax * 2^-e < 127.5, so plane 0 = rint(x 2^-e) fits +-127.
+__device__ __forceinline__ int plane_exp(float amax) {
+    if (!(amax > 0.0f)) return 0;
+    int ex;
+    frexpf(amax, &ex);
+    int e = ex - 7;
+    if (ldexpf(amax, -e) >= 127.5f) e += 1;
+    return e;
+}
+
+// The planes of one value: t0 = x 2^-e, q0 = rint(t0), t1 = (t0 - q0) 128, q1 = rint(t1), ...
+// Every step is exact, so x = 2^e (q0 + q1/128 + q2/16384 + r) with |r| <= 2^-15.
+template <int P>
+__device__ __forceinline__ void to_planes(float x, int e, int (&q)[P]) {
+    float t = ldexpf(x, -e);
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        float qv = rintf(t);
+        q[p] = (int)qv;
+        t = (t - qv) * 128.0f;
+    }
+}
+
+static inline __device__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(uint8_t)(int8_t)a | ((uint32_t)(uint8_t)(int8_t)b << 8) |
+           ((uint32_t)(uint8_t)(int8_t)c << 16) | ((uint32_t)(uint8_t)(int8_t)d << 24);
+}
+
+// Wave64 reductions.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Kernels launched by other translation units of the library (host launchers).
+int launch_quant_rows(const float *x, int m, int k, int ldx, int planes, int8_t *xq, int32_t *xexp,
+                      hipStream_t st);
+
+}  // namespace ava

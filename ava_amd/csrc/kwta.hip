@@ -1,0 +1,161 @@
+// k-winners-take-all for gfx950: one wavefront per row, the row held in registers.
+//
+// The k-th largest value of a row is found exactly by a 32-step bisection over the
+// order-preserving uint32 image of the floats (larger float <=> larger key): at each step the
+// candidate key prefix|bit is kept when at least k keys are >= it, which ends at the largest key
+// with k keys at or above it, i.e. the k-th largest (duplicates counted). Each count is a wave
+// ballot per register and a popcount: no LDS, no atomics, no barriers, so a SIMD interleaves
+// several rows' waves while their loads are in flight. HBM traffic is one read of u and one
+// write of the output per element.
+//
+// The mask is then the reference's: keep u_i when u_i - kth >= 0 (ties kept: more than k units
+// can win), a = relu(u · mask), squared with relu2 (gpu/model/fstep/arch.rs:976-989,
+// gpu/lif.cu:4629-4655). Optionally the kernel emits the split-plane int8 form of a (the input
+// of the W2 product) instead of f32.
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ uint32_t key_of(float f) {
+    uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float float_of_key(uint32_t k) {
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(b);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// NV float4 chunks per lane: h <= 256 NV. OUT: 0 = f32 a, P>0 = P int8 planes + row exponent.
+template <int NV, int P>
+__global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, int n, int h, int k, int relu2,
+                                                   float *__restrict__ a, float *__restrict__ kth_out,
+                                                   int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= n) return;
+    const float *ur = u + (size_t)row * h;
+    const int nq = h >> 2;  // float4 chunks in the row
+
+    f32x4 x[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = i * 64 + lane;
+        if (c < nq) x[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(ur) + c);
+        else x[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // never counted: see below
+    }
+
+    float kth = -INFINITY;
+    const bool all = k >= h;
+    if (!all) {
+        uint32_t keys[NV][4];
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) keys[i][j] = (i * 64 + lane < nq) ? key_of(x[i][j]) : 0u;
+        // padding keys are 0, below every real key except -NaN patterns (inputs are NaN-free), and
+        // the candidates are >= 1 after the first step, so padding never counts.
+        uint32_t prefix = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t cand = prefix | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) cnt += __popcll(__ballot(keys[i][j] >= cand));
+            if (cnt >= k) prefix = cand;
+        }
+        kth = float_of_key(prefix);
+    }
+    if (kth_out && lane == 0) kth_out[row] = kth;
+
+    // a = relu(u · mask)^(1 or 2)
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float v = x[i][j];
+            const float keep = all ? 1.0f : ((v - kth >= 0.0f) ? 1.0f : 0.0f);
+            float y = v * keep;
+            y = y > 0.0f ? y : 0.0f;
+            y = relu2 ? y * y : y;
+            x[i][j] = y;
+            amax = fmaxf(amax, y);
+        }
+
+    if constexpr (P == 0) {
+        float *ar = a + (size_t)row * h;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int c = i * 64 + lane;
+            if (c < nq) __builtin_nontemporal_store(x[i], reinterpret_cast<f32x4 *>(ar) + c);
+        }
+    } else {
+        amax = ava::wave_max(amax);
+        const int e = ava::plane_exp(amax);
+        if (lane == 0) xexp[row] = e;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int c = i * 64 + lane;
+            if (c < nq) {
+                int q0[P], q1[P], q2[P], q3[P];
+                ava::to_planes<P>(x[i][0], e, q0);
+                ava::to_planes<P>(x[i][1], e, q1);
+                ava::to_planes<P>(x[i][2], e, q2);
+                ava::to_planes<P>(x[i][3], e, q3);
+#pragma unroll
+                for (int p = 0; p < P; p++)
+                    reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq)[c] =
+                        ava::pack4(q0[p], q1[p], q2[p], q3[p]);
+            }
+        }
+        // zero the K padding of the planes (ldq > h)
+        for (int c = h + lane * 4; c < ldq; c += 256)
+#pragma unroll
+            for (int p = 0; p < P; p++)
+                *reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq + c) = 0u;
+    }
+}
+
+template <int P>
+int launch(const float *u, int n, int h, int k, int relu2, float *a, float *kth, int8_t *xq, int32_t *xexp,
+           int ldq, hipStream_t st) {
+    const int nv = (h + 255) / 256;
+    dim3 grid(ava::ceil_div(n, 4)), block(256);
+#define AVA_KW(NV_)                                                                                      \
+    if (nv <= NV_) {                                                                                     \
+        kwta_kernel<NV_, P><<<grid, block, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);           \
+        AVA_LAUNCHED("kwta");                                                                            \
+        return AVA_OK;                                                                                   \
+    }
+    AVA_KW(1) AVA_KW(2) AVA_KW(4) AVA_KW(8) AVA_KW(16) AVA_KW(32)
+#undef AVA_KW
+    return ava::fail(AVA_ERR_SHAPE, "kwta: row width %d > 8192", h);
+}
+
+}  // namespace
+
+namespace ava {
+
+// kWTA with the split-plane int8 output (the W2 input of a block): xq [P][n][ldq], xexp [n].
+int kwta_planes(const float *u, int n, int h, int k, int relu2, int planes, int8_t *xq, int32_t *xexp, int ldq,
+                float *kth, hipStream_t st) {
+    AVA_REQUIRE(h % 4 == 0 && ldq % 4 == 0 && ldq >= h, AVA_ERR_SHAPE, "kwta_planes: h=%d ldq=%d", h, ldq);
+    if (planes == 1) return launch<1>(u, n, h, k, relu2, nullptr, kth, xq, xexp, ldq, st);
+    if (planes == 2) return launch<2>(u, n, h, k, relu2, nullptr, kth, xq, xexp, ldq, st);
+    if (planes == 3) return launch<3>(u, n, h, k, relu2, nullptr, kth, xq, xexp, ldq, st);
+    return fail(AVA_ERR_ARG, "kwta_planes: planes %d (1..3)", planes);
+}
+
+}  // namespace ava
+
+extern "C" int ava_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *kth_out,
+                        ava_stream stream) {
+    AVA_REQUIRE(u && a, AVA_ERR_ARG, "kwta: NULL buffer");
+    AVA_REQUIRE(n >= 0 && h > 0 && k > 0, AVA_ERR_SHAPE, "kwta: n=%d h=%d k=%d", n, h, k);
+    AVA_REQUIRE(h % 4 == 0, AVA_ERR_SHAPE, "kwta: row width %d must be a multiple of 4", h);
+    if (n == 0) return AVA_OK;
+    return launch<0>(u, n, h, k, relu2, a, kth_out, nullptr, nullptr, 0, (hipStream_t)stream);
+}

@@ -1,0 +1,203 @@
+// The general LIF scan (int2 / ternary / binary spikes, ALIF trace, per-neuron threshold, carried
+// state) for gfx950.
+//
+// Layout: cur [B][T][D] f32, channel-contiguous, so the lanes of a wavefront that own consecutive
+// channels of one stream read one contiguous span per time step (64 lanes x VEC x 4 bytes) and
+// write their int8 spikes as one contiguous span. Each lane walks T for its VEC channels with the
+// membrane, last spike, trace and reset threshold in registers (no global round trip of the
+// state); the next PF time steps are loaded while the current PF are processed, so each wave keeps
+// PF x 64 x VEC x 4 bytes of reads in flight, which is what hides HBM latency at one or two waves
+// per SIMD.
+//
+// Arithmetic: the reference's step (gpu/lif_gen.rs:171-180) with every operation rounded on its
+// own (this file is compiled with -ffp-contract=off), so spikes and final state are bit-identical
+// to the CPU loop.
+#include "common.h"
+
+namespace {
+
+template <int LEVELS, bool SIGNED>
+__device__ __forceinline__ float spike_of(float v, float th) {
+    if (!SIGNED) return (v - th >= 0.0f) ? 1.0f : 0.0f;
+    float h = 0.0f;
+#pragma unroll
+    for (int k = 1; k <= LEVELS; k++) {
+        float kth = th * (float)k;
+        h += ((v - kth >= 0.0f) ? 1.0f : 0.0f) - ((-v - kth >= 0.0f) ? 1.0f : 0.0f);
+    }
+    return h;
+}
+
+template <int VEC>
+struct Vec;
+template <>
+struct Vec<1> {
+    typedef float T;
+    static __device__ __forceinline__ float get(const T &x, int) { return x; }
+};
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <>
+struct Vec<2> {
+    typedef f32x2 T;
+    static __device__ __forceinline__ float get(const T &x, int i) { return x[i]; }
+};
+template <>
+struct Vec<4> {
+    typedef f32x4 T;
+    static __device__ __forceinline__ float get(const T &x, int i) { return x[i]; }
+};
+
+template <int VEC>
+__device__ __forceinline__ void store_spikes(int8_t *dst, const float (&s)[VEC]) {
+    if constexpr (VEC == 1) {
+        *dst = (int8_t)s[0];
+    } else if constexpr (VEC == 2) {
+        uint16_t w = (uint16_t)(uint8_t)(int8_t)s[0] | ((uint16_t)(uint8_t)(int8_t)s[1] << 8);
+        *(uint16_t *)dst = w;
+    } else {
+        uint32_t w = (uint32_t)(uint8_t)(int8_t)s[0] | ((uint32_t)(uint8_t)(int8_t)s[1] << 8) |
+                     ((uint32_t)(uint8_t)(int8_t)s[2] << 16) | ((uint32_t)(uint8_t)(int8_t)s[3] << 24);
+        *(uint32_t *)dst = w;
+    }
+}
+
+template <int VEC, int PF, int LEVELS, bool SIGNED, bool ALIF>
+__global__ __launch_bounds__(256) void lif_scan_kernel(const float *__restrict__ cur, int B, int T, int D,
+                                                       const float *__restrict__ ps, float *__restrict__ v,
+                                                       float *__restrict__ s, float *__restrict__ a,
+                                                       int8_t *__restrict__ spikes, float *__restrict__ th_out) {
+    typedef typename Vec<VEC>::T V;
+    const int nv = D / VEC;
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= B * nv) return;
+    const int b = gid / nv, c0 = (gid - b * nv) * VEC;
+
+    float bt[VEC], th0[VEC], rho[VEC], omr[VEC], gain[VEC], vv[VEC], sp[VEC], aa[VEC], thp[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; i++) {
+        const int c = c0 + i, st = b * D + c;
+        bt[i] = ps[c];
+        th0[i] = ps[D + c];
+        rho[i] = ps[2 * D + c];
+        gain[i] = ps[3 * D + c];
+        omr[i] = 1.0f - rho[i];
+        vv[i] = v[st];
+        sp[i] = s[st];
+        aa[i] = a[st];
+        thp[i] = ALIF ? th0[i] + aa[i] * gain[i] : th0[i];
+    }
+
+    const V *src = reinterpret_cast<const V *>(cur + (size_t)b * T * D + c0);
+    int8_t *dst = spikes + (size_t)b * T * D + c0;
+    const size_t stride = (size_t)nv;  // one time step, in V units
+
+    V buf[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++)
+        if (i < T) buf[i] = __builtin_nontemporal_load(src + (size_t)i * stride);
+
+    for (int t0 = 0; t0 < T; t0 += PF) {
+        V nxt[PF];
+#pragma unroll
+        for (int i = 0; i < PF; i++) {
+            const int t = t0 + PF + i;
+            if (t < T) nxt[i] = __builtin_nontemporal_load(src + (size_t)t * stride);
+        }
+#pragma unroll
+        for (int i = 0; i < PF; i++) {
+            const int t = t0 + i;
+            if (t < T) {
+                float out[VEC];
+#pragma unroll
+                for (int j = 0; j < VEC; j++) {
+                    const float x = Vec<VEC>::get(buf[i], j);
+                    float tht = th0[j];
+                    if (ALIF) {
+                        aa[j] = aa[j] * rho[j] + fabsf(sp[j]) * omr[j];
+                        tht = th0[j] + aa[j] * gain[j];
+                    }
+                    vv[j] = (vv[j] * bt[j] + x) - sp[j] * thp[j];
+                    sp[j] = spike_of<LEVELS, SIGNED>(vv[j], tht);
+                    thp[j] = tht;
+                    out[j] = sp[j];
+                }
+                store_spikes<VEC>(dst + (size_t)t * D, out);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PF; i++) buf[i] = nxt[i];
+    }
+
+#pragma unroll
+    for (int i = 0; i < VEC; i++) {
+        const int st = b * D + c0 + i;
+        v[st] = vv[i];
+        s[st] = sp[i];
+        a[st] = aa[i];
+        if (th_out) th_out[st] = thp[i];
+    }
+}
+
+template <int VEC, int PF>
+int launch_vp(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
+              int levels, int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st) {
+    const long threads = (long)B * (D / VEC);
+    dim3 grid(ava::ceil_div(threads, 256)), block(256);
+#define AVA_LIF_GO(L, S, A) \
+    lif_scan_kernel<VEC, PF, L, S, A><<<grid, block, 0, st>>>(cur, B, T, D, ps, v, s, a, spikes, th_out)
+    if (!is_signed) {
+        if (alif) AVA_LIF_GO(1, false, true);
+        else AVA_LIF_GO(1, false, false);
+    } else if (levels == 1) {
+        if (alif) AVA_LIF_GO(1, true, true);
+        else AVA_LIF_GO(1, true, false);
+    } else {
+        if (alif) AVA_LIF_GO(2, true, true);
+        else AVA_LIF_GO(2, true, false);
+    }
+#undef AVA_LIF_GO
+    AVA_LAUNCHED("lif_scan");
+    return AVA_OK;
+}
+
+}  // namespace
+
+namespace ava {
+
+// vec/pf 0 = the defaults: 1 channel per lane, 32 steps in flight.
+int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
+                   int levels, int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf,
+                   hipStream_t st) {
+    AVA_REQUIRE(cur && ps && v && s && a && spikes, AVA_ERR_ARG, "lif_scan: NULL buffer");
+    AVA_REQUIRE(B > 0 && T > 0 && D > 0, AVA_ERR_SHAPE, "lif_scan: B=%d T=%d D=%d", B, T, D);
+    AVA_REQUIRE(levels == 1 || levels == 2, AVA_ERR_ARG, "lif_scan: levels %d (1 or 2)", levels);
+    if (vec == 0) vec = 1;
+    if (pf == 0) pf = 32;
+    if (D % vec) vec = 1;
+#define AVA_VP(VV, PP)                                                                              \
+    if (vec == VV && pf == PP)                                                                      \
+        return launch_vp<VV, PP>(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, st);
+    AVA_VP(1, 8) AVA_VP(1, 16) AVA_VP(1, 32)
+    AVA_VP(2, 8) AVA_VP(2, 16) AVA_VP(2, 32)
+    AVA_VP(4, 8) AVA_VP(4, 16)
+#undef AVA_VP
+    return fail(AVA_ERR_ARG, "lif_scan: no kernel for vec=%d pf=%d", vec, pf);
+}
+
+}  // namespace ava
+
+extern "C" int ava_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
+                            float *a, int levels, int is_signed, int alif, int8_t *spikes, float *th_out,
+                            ava_stream stream) {
+    return ava::lif_scan_tuned(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, 0, 0,
+                               (hipStream_t)stream);
+}
+
+// Tuning entry (not part of ava.h): explicit lanes-per-channel-group and prefetch depth.
+extern "C" int ava_lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v,
+                                  float *s, float *a, int levels, int is_signed, int alif, int8_t *spikes,
+                                  float *th_out, int vec, int pf, ava_stream stream) {
+    return ava::lif_scan_tuned(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, vec, pf,
+                               (hipStream_t)stream);
+}

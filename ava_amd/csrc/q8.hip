@@ -1,0 +1,361 @@
+// int8 weights, split-plane activations and the i8 MFMA product for gfx950.
+//
+// Weights: W [din][dout] f32 -> qt [dout][ldk] int8 (each output column's weights contiguous in K,
+// the B operand of v_mfma_i32_32x32x32_i8) and one f32 scale per output column, the reference's
+// quantizer (parts/src/quant.rs:18-31).
+//
+// Activations: P planes of int8 under a power-of-two row scale (common.h: plane_exp / to_planes),
+// [P][m][ldk]. Every plane's products are exact int32 sums; the epilogue combines them with one
+// rounding, so a P = 3 product differs from the reference's f32 fma chain only by its 2^-22
+// relative activation error, and integer inputs (spikes) give the reference's bits exactly.
+//
+// Product kernel: 256 threads = 4 waves in 2 x 2, a 128 x 128 output tile, K in steps of 64 bytes
+// staged through LDS (double buffered: the next step's global loads are in flight during this
+// step's MFMAs). Each wave owns 64 x 64 outputs per plane: 2 x 2 32x32 MFMA blocks, 2 k-substeps of
+// 32 per LDS step, the B fragment shared by every plane. LDS rows are padded to 80 bytes so the
+// 16-byte fragment reads of 8 consecutive rows hit distinct banks. Tiles are ordered so that the
+// workgroups of one XCD (hardware id mod 8) walk consecutive tiles: the N tiles of one row block
+// run back to back on one XCD and share its L2 for the A rows.
+#include "common.h"
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ weights
+
+// One thread per output column: the column's absmax over din, then scale = amax/127 (1 if zero).
+__global__ void q8_scale_kernel(const float *__restrict__ w, int din, int dout, float *__restrict__ scale) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= dout) return;
+    float m = 0.0f;
+    for (int j = 0; j < din; j++) m = fmaxf(m, fabsf(w[(size_t)j * dout + c]));
+    scale[c] = m > 0.0f ? m / 127.0f : 1.0f;
+}
+
+// qt[c][j] = clamp(round(w[j][c] / scale[c]), +-127); 0 in the padding j >= din. A 64 x 64 tile
+// transposed through LDS so both the reads and the writes are row-contiguous.
+__global__ void q8_pack_kernel(const float *__restrict__ w, int din, int dout, int ldk,
+                               const float *__restrict__ scale, int8_t *__restrict__ qt) {
+    __shared__ int8_t tile[64][68];
+    const int j0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 256 threads: 4 rows per pass
+    for (int r = ty; r < 64; r += 4) {
+        const int j = j0 + r, c = c0 + tx;
+        int8_t q = 0;
+        if (j < din && c < dout) {
+            float t = roundf(w[(size_t)j * dout + c] / scale[c]);
+            t = fminf(fmaxf(t, -127.0f), 127.0f);
+            q = (int8_t)t;
+        }
+        tile[r][tx] = q;
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+        const int c = c0 + r, j = j0 + tx;
+        if (c < dout && j < ldk) qt[(size_t)c * ldk + j] = tile[tx][r];
+    }
+}
+
+// ------------------------------------------------------------------ activations
+
+// One wave per row: the row's absmax, its exponent, then its planes (padding zeroed).
+template <int P>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict__ x, int m, int k, int ldx,
+                                                         int8_t *__restrict__ xq, int32_t *__restrict__ xexp,
+                                                         int ldq) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const float *xr = x + (size_t)row * ldx;
+    float amax = 0.0f;
+    for (int j = lane; j < k; j += 64) amax = fmaxf(amax, fabsf(xr[j]));
+    amax = ava::wave_max(amax);
+    const int e = ava::plane_exp(amax);
+    if (lane == 0) xexp[row] = e;
+    for (int j = lane * 4; j < ldq; j += 256) {
+        int q[4][P];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float v = (j + i < k) ? xr[j + i] : 0.0f;
+            ava::to_planes<P>(v, e, q[i]);
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++)
+            *reinterpret_cast<uint32_t *>(xq + ((size_t)p * m + row) * ldq + j) =
+                ava::pack4(q[0][p], q[1][p], q[2][p], q[3][p]);
+    }
+}
+
+// ------------------------------------------------------------------ the product
+
+enum Epi { EPI_ACC = 0, EPI_STORE = 1, EPI_MUL = 2, EPI_ADD = 3 };
+
+constexpr int BM = 128, BN = 128, BK = 64, LDS_ROW = BK + 16;
+
+// Epilogue parameters: y [m][ldy] (f32 or, for EPI_ACC, int32 [P][m][n]); colv [n] (EPI_MUL).
+struct EpiArgs {
+    void *y;
+    int ldy;
+    const float *colv;
+};
+
+template <int P, int EPI>
+__global__ __launch_bounds__(256) void q8_gemm_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
+                                                      int m, int n, int ldk, const int8_t *__restrict__ qt,
+                                                      const float *__restrict__ scale, EpiArgs ep) {
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t *lds_a = smem;                              // [2][P][BM][LDS_ROW]
+    int8_t *lds_b = smem + 2 * P * BM * LDS_ROW;       // [2][BN][LDS_ROW]
+
+    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
+    const int total = tiles_m * tiles_n;
+    int tile = blockIdx.x;
+    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // global -> register staging: A: P*BM rows x 4 chunks of 16 B; B: BN rows x 4 chunks
+    constexpr int A_CHUNKS = P * BM * 4 / 256;  // per thread
+    constexpr int B_CHUNKS = BN * 4 / 256;
+    i32x4 ra[A_CHUNKS], rb[B_CHUNKS];
+
+    auto load_tile = [&](int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; i++) {
+            const int c = i * 256 + tid;
+            const int p = c / (BM * 4), rr = (c / 4) % BM, kc = c & 3;
+            const int row = m0 + rr;
+            if (row < m)
+                ra[i] = *reinterpret_cast<const i32x4 *>(xq + ((size_t)p * m + row) * ldk + k0 + kc * 16);
+            else
+                ra[i] = i32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < B_CHUNKS; i++) {
+            const int c = i * 256 + tid;
+            const int rr = c / 4, kc = c & 3;
+            const int col = n0 + rr;
+            if (col < n)
+                rb[i] = *reinterpret_cast<const i32x4 *>(qt + (size_t)col * ldk + k0 + kc * 16);
+            else
+                rb[i] = i32x4{0, 0, 0, 0};
+        }
+    };
+    auto store_tile = [&](int buf) {
+        int8_t *la = lds_a + buf * P * BM * LDS_ROW;
+        int8_t *lb = lds_b + buf * BN * LDS_ROW;
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; i++) {
+            const int c = i * 256 + tid;
+            const int p = c / (BM * 4), rr = (c / 4) % BM, kc = c & 3;
+            *reinterpret_cast<i32x4 *>(la + (p * BM + rr) * LDS_ROW + kc * 16) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_CHUNKS; i++) {
+            const int c = i * 256 + tid;
+            const int rr = c / 4, kc = c & 3;
+            *reinterpret_cast<i32x4 *>(lb + rr * LDS_ROW + kc * 16) = rb[i];
+        }
+    };
+
+    i32x16 acc[P][2][2];
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[p][i][j] = i32x16{};
+
+    const int KT = ldk / BK;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+
+    const int frow = lane & 31, fk = (lane >> 5) * 16;
+    for (int kt = 0; kt < KT; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < KT) load_tile(kt + 1);
+        const int8_t *la = lds_a + buf * P * BM * LDS_ROW;
+        const int8_t *lb = lds_b + buf * BN * LDS_ROW;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ks++) {
+            i32x4 bf[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bf[j] = *reinterpret_cast<const i32x4 *>(lb + (wn * 64 + j * 32 + frow) * LDS_ROW + ks * 32 + fk);
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                i32x4 af[2];
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    af[i] = *reinterpret_cast<const i32x4 *>(la + (p * BM + wm * 64 + i * 32 + frow) * LDS_ROW +
+                                                              ks * 32 + fk);
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[p][i][j], 0, 0, 0);
+            }
+        }
+        if (kt + 1 < KT) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds, for block (i, j), rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
+    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + wn * 64 + j * 32 + ccol;
+            if (col >= n) continue;
+            const float sc = scale[col];
+            float cv = 0.0f;
+            if (EPI == EPI_MUL) cv = ep.colv[col];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + rsub + (r & 3);
+                if (row >= m) continue;
+                if (EPI == EPI_ACC) {
+#pragma unroll
+                    for (int p = 0; p < P; p++)
+                        reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
+                    continue;
+                }
+                long long A = 0;
+#pragma unroll
+                for (int p = 0; p < P; p++) A += (long long)acc[p][i][j][r] << (7 * (P - 1 - p));
+                float v = (float)(double)A;
+                v = ldexpf(v, (xexp ? xexp[row] : 0) - 7 * (P - 1));
+                v = v * sc;
+                float *yp = reinterpret_cast<float *>(ep.y) + (size_t)row * ep.ldy + col;
+                if (EPI == EPI_STORE) *yp = v;
+                else if (EPI == EPI_MUL) *yp = v * cv;
+                else *yp = *yp + v;
+            }
+        }
+}
+
+template <int P, int EPI>
+int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                EpiArgs ep, hipStream_t st) {
+    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const size_t lds = (size_t)2 * (P * BM + BN) * LDS_ROW;
+    static bool attr = false;  // above 64 KiB of dynamic LDS the kernel must opt in (gfx950: 160 KiB)
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_kernel<P, EPI>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    q8_gemm_kernel<P, EPI><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
+}
+
+template <int EPI>
+int gemm_planes(int planes, const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt,
+                const float *scale, EpiArgs ep, hipStream_t st) {
+    if (planes == 1) return launch_gemm<1, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    if (planes == 2) return launch_gemm<2, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    if (planes == 3) return launch_gemm<3, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    return ava::fail(AVA_ERR_ARG, "q8 product: planes %d (1..3)", planes);
+}
+
+int check_qw(const ava_qw *w) {
+    AVA_REQUIRE(w && w->qt && w->scale, AVA_ERR_ARG, "q8: NULL weights");
+    AVA_REQUIRE(w->din > 0 && w->dout > 0 && w->ldk == ava::q8_ldk(w->din), AVA_ERR_SHAPE,
+                "q8: weights din=%d dout=%d ldk=%d", w->din, w->dout, w->ldk);
+    return AVA_OK;
+}
+
+}  // namespace
+
+namespace ava {
+
+int launch_quant_rows(const float *x, int m, int k, int ldx, int planes, int8_t *xq, int32_t *xexp,
+                      hipStream_t st) {
+    const int ldq = q8_ldk(k);
+    dim3 grid(ceil_div(m, 4)), block(256);
+    if (planes == 1) quant_rows_kernel<1><<<grid, block, 0, st>>>(x, m, k, ldx, xq, xexp, ldq);
+    else if (planes == 2) quant_rows_kernel<2><<<grid, block, 0, st>>>(x, m, k, ldx, xq, xexp, ldq);
+    else if (planes == 3) quant_rows_kernel<3><<<grid, block, 0, st>>>(x, m, k, ldx, xq, xexp, ldq);
+    else return fail(AVA_ERR_ARG, "quant_rows: planes %d (1..3)", planes);
+    AVA_LAUNCHED("quant_rows");
+    return AVA_OK;
+}
+
+// The product with an epilogue: kind 1 store y, 2 y = v * colv[col], 3 y += v. y [m][ldy].
+int q8_gemm(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w, int kind, float *y, int ldy,
+            const float *colv, hipStream_t st) {
+    if (int r = check_qw(w)) return r;
+    AVA_REQUIRE(xq && y, AVA_ERR_ARG, "q8 product: NULL buffer");
+    if (m == 0) return AVA_OK;
+    EpiArgs ep{y, ldy, colv};
+    if (kind == EPI_STORE) return gemm_planes<EPI_STORE>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
+    if (kind == EPI_MUL) return gemm_planes<EPI_MUL>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
+    if (kind == EPI_ADD) return gemm_planes<EPI_ADD>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
+    return fail(AVA_ERR_ARG, "q8 product: epilogue %d", kind);
+}
+
+}  // namespace ava
+
+extern "C" int ava_q8_ldk(int k) { return ava::q8_ldk(k); }
+
+extern "C" int ava_q8_pack(const float *w, int din, int dout, int8_t *qt, float *scale, ava_stream stream) {
+    AVA_REQUIRE(w && qt && scale, AVA_ERR_ARG, "q8_pack: NULL buffer");
+    AVA_REQUIRE(din > 0 && dout > 0, AVA_ERR_SHAPE, "q8_pack: din=%d dout=%d", din, dout);
+    hipStream_t st = (hipStream_t)stream;
+    const int ldk = ava::q8_ldk(din);
+    q8_scale_kernel<<<ava::ceil_div(dout, 256), 256, 0, st>>>(w, din, dout, scale);
+    AVA_LAUNCHED("q8_scale");
+    q8_pack_kernel<<<dim3(ava::ceil_div(dout, 64), ava::ceil_div(ldk, 64)), 256, 0, st>>>(w, din, dout, ldk, scale, qt);
+    AVA_LAUNCHED("q8_pack");
+    return AVA_OK;
+}
+
+extern "C" int ava_q8_quant_rows(const float *x, int m, int k, int planes, int8_t *xq, int32_t *xexp,
+                                 ava_stream stream) {
+    AVA_REQUIRE(x && xq && xexp, AVA_ERR_ARG, "quant_rows: NULL buffer");
+    AVA_REQUIRE(m >= 0 && k > 0, AVA_ERR_SHAPE, "quant_rows: m=%d k=%d", m, k);
+    if (m == 0) return AVA_OK;
+    return ava::launch_quant_rows(x, m, k, k, planes, xq, xexp, (hipStream_t)stream);
+}
+
+extern "C" int ava_q8_gemm_acc(const int8_t *xq, int planes, int m, const ava_qw *w, int32_t *acc,
+                               ava_stream stream) {
+    if (int r = check_qw(w)) return r;
+    AVA_REQUIRE(xq && acc, AVA_ERR_ARG, "q8_gemm_acc: NULL buffer");
+    if (m == 0) return AVA_OK;
+    EpiArgs ep{acc, w->dout, nullptr};
+    return gemm_planes<EPI_ACC>(planes, xq, nullptr, m, w->dout, w->ldk, w->qt, w->scale, ep, (hipStream_t)stream);
+}
+
+extern "C" size_t ava_q8_workspace(int m, int k, int planes) {
+    return (size_t)planes * m * ava::q8_ldk(k) + sizeof(int32_t) * (size_t)m + 256;
+}
+
+extern "C" int ava_q8_matmul(const float *x, int m, const ava_qw *w, int planes, float *y, void *ws,
+                             size_t ws_bytes, ava_stream stream) {
+    if (int r = check_qw(w)) return r;
+    AVA_REQUIRE(x && y && ws, AVA_ERR_ARG, "q8_matmul: NULL buffer");
+    AVA_REQUIRE(planes >= 1 && planes <= 3, AVA_ERR_ARG, "q8_matmul: planes %d (1..3)", planes);
+    AVA_REQUIRE(m >= 0, AVA_ERR_SHAPE, "q8_matmul: m=%d", m);
+    AVA_REQUIRE(ws_bytes >= ava_q8_workspace(m, w->din, planes), AVA_ERR_SHAPE,
+                "q8_matmul: workspace %zu < %zu bytes", ws_bytes, ava_q8_workspace(m, w->din, planes));
+    if (m == 0) return AVA_OK;
+    hipStream_t st = (hipStream_t)stream;
+    int8_t *xq = (int8_t *)ws;
+    int32_t *xe = (int32_t *)(((uintptr_t)(xq + (size_t)planes * m * w->ldk) + 255) & ~(uintptr_t)255);
+    if (int r = ava::launch_quant_rows(x, m, w->din, w->din, planes, xq, xe, st)) return r;
+    return ava::q8_gemm(xq, xe, planes, m, w, EPI_STORE, y, w->dout, nullptr, st);
+}
+
+extern "C" int ava_q8_matmul_i8(const int8_t *s, int m, const ava_qw *w, float *y, ava_stream stream) {
+    return ava::q8_gemm(s, nullptr, 1, m, w, EPI_STORE, y, w ? w->dout : 0, nullptr, (hipStream_t)stream);
+}

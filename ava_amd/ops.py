@@ -1,0 +1,177 @@
+"""The reference's ops on the HIP path, with the reference's names and argument meaning.
+
+Tensors are torch tensors on the GPU (torch is used for device memory and streams only); every
+op calls libava_amd.so through the C ABI of include/ava.h and raises AvaError on a non-zero
+status (the reference bail!s on shape, dtype and contiguity errors).
+
+    QW.from_tensor(w)            int8.rs:76-79   (QW::from_tensor; W [din, dout], x·W)
+    mm(x, qw, planes=3)          int8.rs:672-683 (int8::mm)
+    mm_spikes(s, qw)             int8.rs:672-683 on integer inputs (exact)
+    lif_gen(cur, beta, ...)      lif_gen.rs:86-130
+    kwta_relu(u, k, relu2)       model.rs:504-528 + arch.rs:1820-1835
+    mem_gen(q, k, e, v, la, b, m)   mem_gen.rs:127-137
+    delta_rule_from(q, k, v, la, beta, f0)   model.rs:761-799 (alpha = 1: la must be 0)
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import QW as _QWC, check, lib
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _need(t, dtype, name):
+    if not t.is_cuda:
+        raise ValueError(f"{name}: a GPU tensor is required")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: a contiguous tensor is required")
+
+
+def ldk(k: int) -> int:
+    return lib().ava_q8_ldk(k)
+
+
+class QW:
+    """One int8 weight matrix on the GPU: qt [dout][ldk] int8, scale [dout] f32."""
+
+    def __init__(self, din, dout, qt, scale):
+        self.din, self.dout, self.qt, self.scale = din, dout, qt, scale
+        self.ldk = qt.shape[1]
+        self.c = _QWC(din=din, dout=dout, ldk=self.ldk, qt=qt.data_ptr(), scale=scale.data_ptr())
+
+    @staticmethod
+    def from_tensor(w: torch.Tensor) -> "QW":
+        _need(w, torch.float32, "QW.from_tensor")
+        din, dout = w.shape
+        qt = torch.empty((dout, ldk(din)), dtype=torch.int8, device=w.device)
+        scale = torch.empty(dout, dtype=torch.float32, device=w.device)
+        check(lib().ava_q8_pack(_p(w), din, dout, _p(qt), _p(scale), _stream()), "ava_q8_pack")
+        return QW(din, dout, qt, scale)
+
+
+def quant_rows(x: torch.Tensor, planes: int = 3):
+    _need(x, torch.float32, "quant_rows")
+    m, k = x.shape
+    xq = torch.empty((planes, m, ldk(k)), dtype=torch.int8, device=x.device)
+    xe = torch.empty(m, dtype=torch.int32, device=x.device)
+    check(lib().ava_q8_quant_rows(_p(x), m, k, planes, _p(xq), _p(xe), _stream()), "ava_q8_quant_rows")
+    return xq, xe
+
+
+def gemm_acc(xq: torch.Tensor, w: QW):
+    _need(xq, torch.int8, "gemm_acc")
+    planes, m, _ = xq.shape
+    acc = torch.empty((planes, m, w.dout), dtype=torch.int32, device=xq.device)
+    check(lib().ava_q8_gemm_acc(_p(xq), planes, m, C.byref(w.c), _p(acc), _stream()), "ava_q8_gemm_acc")
+    return acc
+
+
+def mm(x: torch.Tensor, w: QW, planes: int = 3) -> torch.Tensor:
+    _need(x, torch.float32, "mm")
+    m, k = x.shape
+    if k != w.din:
+        raise ValueError(f"mm: input width {k}, the weights take {w.din}")
+    y = torch.empty((m, w.dout), dtype=torch.float32, device=x.device)
+    nbytes = lib().ava_q8_workspace(m, k, planes)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    check(lib().ava_q8_matmul(_p(x), m, C.byref(w.c), planes, _p(y), _p(ws), nbytes, _stream()), "ava_q8_matmul")
+    return y
+
+
+def mm_spikes(s: torch.Tensor, w: QW) -> torch.Tensor:
+    """s [m][din] int8 (din == ldk) or [m][ldk]."""
+    _need(s, torch.int8, "mm_spikes")
+    m, k = s.shape
+    if k != w.ldk:
+        raise ValueError(f"mm_spikes: input width {k}, expected ldk {w.ldk}")
+    y = torch.empty((m, w.dout), dtype=torch.float32, device=s.device)
+    check(lib().ava_q8_matmul_i8(_p(s), m, C.byref(w.c), _p(y), _stream()), "ava_q8_matmul_i8")
+    return y
+
+
+@dataclass
+class LifState:
+    """arch.rs:945-950: membrane v, last spikes s, ALIF trace a, each [B, d]."""
+    v: torch.Tensor
+    s: torch.Tensor
+    a: torch.Tensor
+
+
+def lif_gen(cur, beta, theta=None, alif=None, levels=2, signed=True, init=None, vec=0, pf=0, th_out=False):
+    """lif_gen.rs:86-130: the LIF scan of cur [B, T, d]. Returns (spikes int8 [B, T, d], LifState[, th_T])."""
+    _need(cur, torch.float32, "lif_gen")
+    B, T, D = cur.shape
+    dev = cur.device
+    theta = torch.ones(D, device=dev) if theta is None else theta
+    if alif is None:
+        rho = torch.zeros(D, device=dev)
+        gain = torch.zeros(D, device=dev)
+    else:
+        rho, gain = alif
+    ps = torch.cat([beta, theta, rho, gain]).to(torch.float32).contiguous()
+    if init is None:
+        v = torch.zeros((B, D), device=dev)
+        s = torch.zeros((B, D), device=dev)
+        a = torch.zeros((B, D), device=dev)
+    else:
+        v, s, a = init.v.clone(), init.s.clone(), init.a.clone()
+    spikes = torch.empty((B, T, D), dtype=torch.int8, device=dev)
+    tho = torch.empty((B, D), device=dev) if th_out else None
+    if vec or pf:
+        rc = lib().ava_lif_scan_tuned(_p(cur), B, T, D, _p(ps), _p(v), _p(s), _p(a), levels, int(signed),
+                                      int(alif is not None), _p(spikes), _p(tho), vec, pf, _stream())
+    else:
+        rc = lib().ava_lif_scan(_p(cur), B, T, D, _p(ps), _p(v), _p(s), _p(a), levels, int(signed),
+                                int(alif is not None), _p(spikes), _p(tho), _stream())
+    check(rc, "ava_lif_scan")
+    st = LifState(v, s, a)
+    return (spikes, st, tho) if th_out else (spikes, st)
+
+
+def kwta_relu(u: torch.Tensor, k: int, relu2: bool = True):
+    """relu(u · kwta_mask(u, k)), squared with relu2. Returns (a, kth)."""
+    _need(u, torch.float32, "kwta_relu")
+    n, h = u.shape
+    a = torch.empty_like(u)
+    kth = torch.empty(n, dtype=torch.float32, device=u.device)
+    check(lib().ava_kwta(_p(u), n, h, k, int(relu2), _p(a), _p(kth), _stream()), "ava_kwta")
+    return a, kth
+
+
+def mem_gen(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
+    """mem_gen.rs:127-137 with carried state: q, k, e, v [BH, T, hs]; la, b [BH, T, g].
+    Returns (y, F, S)."""
+    for t, nm in ((q, "q"), (k, "k"), (e, "e"), (v, "v"), (la, "la"), (b, "b")):
+        _need(t, torch.float32, f"mem_gen {nm}")
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    F = torch.zeros((BH, hs, hs), device=q.device) if F is None else F.clone()
+    S = torch.zeros((BH, hs, hs), device=q.device) if S is None else S.clone()
+    y = torch.empty_like(q)
+    check(lib().ava_mem_scan(_p(q), _p(k), _p(e), _p(v), _p(la), _p(b), BH, T, hs, g, float(m), float(cap),
+                             _p(F), _p(S), _p(y), _stream()), "ava_mem_scan")
+    return y, F, S
+
+
+def delta_rule_from(q, k, v, beta, f0=None):
+    """model.rs:761-799 at alpha = 1 (config[2]): q, k, v [BH, T, 64], beta [BH, T]. Returns (y, F)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
+        _need(t, torch.float32, f"delta_rule {nm}")
+    BH, T, hs = q.shape
+    F = torch.zeros((BH, hs, hs), device=q.device) if f0 is None else f0.clone()
+    y = torch.empty_like(q)
+    check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
+          "ava_delta_chunk")
+    return y, F

@@ -1,0 +1,180 @@
+/*
+ * ava.h — C ABI of the MI355X-native int8 block forward of Ava (libava_amd.so, gfx950).
+ *
+ * This header is the drop-in boundary: a host engine (the reference's is Rust, bound through a
+ * thin FFI crate) calls these entry points in place of the reference's candle ops and drivers.
+ * Each declaration names the reference interface it replaces (paths relative to the reference's
+ * design-tests/nn/gpu/src).
+ *
+ * Conventions (all entry points):
+ *   - every buffer is a caller-owned DEVICE pointer unless the comment says "host";
+ *   - work is enqueued on `stream` (NULL = the null stream) and nothing synchronises unless stated;
+ *   - the return value is an ava_status; a non-zero status leaves a message in ava_last_error()
+ *     (per thread). Shape or argument errors are returned, never aborted on (the reference
+ *     bail!s on shape/dtype errors: int8.rs:604-613, lif_gen.rs:132-141, mem_gen.rs:179-187);
+ *   - row-major layouts; "[a][b]" = a rows of b contiguous elements.
+ */
+#ifndef AVA_H
+#define AVA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *ava_stream; /* == hipStream_t */
+
+enum {
+    AVA_OK = 0,
+    AVA_ERR_ARG = 1,         /* a NULL pointer, a negative size, an unsupported option */
+    AVA_ERR_SHAPE = 2,       /* sizes that do not fit together or exceed a kernel's limits */
+    AVA_ERR_HIP = 3,         /* a HIP runtime error (launch, allocation) */
+    AVA_ERR_UNSUPPORTED = 4  /* a configuration this build does not run */
+};
+
+const char *ava_last_error(void);
+const char *ava_version(void);
+
+/* ------------------------------------------------------------------ int8 weights and products */
+
+/* One weight matrix in int8: W [din][dout] (applied x·W), stored transposed as qt [dout][din]
+ * (each output column's din weights contiguous: the K-contiguous B operand of the i8 MFMA), one
+ * f32 scale per output column. Replaces QW (int8.rs:44-54). */
+typedef struct {
+    int din, dout;
+    int ldk;      /* ava_q8_ldk(din): din padded to a multiple of 64 with zero weights */
+    int8_t *qt;   /* [dout][ldk] */
+    float *scale; /* [dout] */
+} ava_qw;
+
+/* din rounded up to a multiple of 64 (the K step of the i8 MFMA kernels). */
+int ava_q8_ldk(int k);
+
+/* Quantize W [din][dout] f32 into qt [dout][ldk] / scale [dout]: scale_c = max_j |W[j][c]| / 127
+ * (1 for an all-zero column), q = clamp(round half away from zero (W / scale_c), +-127), padding 0.
+ * Replaces QW::from_rows (int8.rs:59-72) over ava_parts::quant::quantize_int8 (parts/src/quant.rs:18-31). */
+int ava_q8_pack(const float *w, int din, int dout, int8_t *qt, float *scale, ava_stream stream);
+
+/* Split-plane activation quantizer (part of the int8 product; the reference keeps f32 activations):
+ * per row, e = the smallest exponent with max|x| 2^-e < 127.5, then planes q_p of int8 with
+ * x ~= 2^e sum_p q_p 2^(-7p). xq [planes][m][ldk] (ldk = ava_q8_ldk(k), padding 0), xexp [m].
+ * planes 1..3. */
+int ava_q8_quant_rows(const float *x, int m, int k, int planes, int8_t *xq, int32_t *xexp,
+                      ava_stream stream);
+
+/* The raw int32 accumulators acc [planes][m][n] = A_p [m][ldk] · W (i8 MFMA, exact). For checks. */
+int ava_q8_gemm_acc(const int8_t *xq, int planes, int m, const ava_qw *w, int32_t *acc,
+                    ava_stream stream);
+
+/* y [m][dout] = x [m][din] · W with f32 activations: quantize to `planes` planes (3 = the
+ * accurate default), i8 MFMA per plane, combine y = ((float)sum_p acc_p 2^(7(P-1-p))) 2^(e-7(P-1)) scale_c.
+ * `ws` is a device workspace of at least ava_q8_workspace(m, din, planes) bytes.
+ * Replaces int8::mm / int8::head over Apply "ava-int8-matmul" (int8.rs:592-626, 672-698). */
+size_t ava_q8_workspace(int m, int k, int planes);
+int ava_q8_matmul(const float *x, int m, const ava_qw *w, int planes, float *y, void *ws,
+                  size_t ws_bytes, ava_stream stream);
+
+/* y [m][dout] = s [m][ldk] · W for integer inputs (the LIF's spikes, -2..2; padding columns 0):
+ * y = (float)acc · scale_c, the reference's bits exactly (its f32 sum of integer products is
+ * exact). Replaces int8::mm on the spikes (arch.rs:1695, fstep/arch.rs:675). */
+int ava_q8_matmul_i8(const int8_t *s, int m, const ava_qw *w, float *y, ava_stream stream);
+
+/* ------------------------------------------------------------------ LIF scan */
+
+/* The general LIF scan over cur [B][T][D] (f32): ps = [beta | theta | rho | gain] ([4][D]);
+ * v, s, a [B][D]: the carried membrane, last spikes and ALIF trace on entry, the final ones on
+ * exit. Per (b, c), sequential in t, each operation rounded alone:
+ *   a = a rho + |s| (1 - rho) (alif);  th_t = theta + a gain;  v = (v beta + I) - s th_{t-1};
+ *   s = sum_{k=1..levels} [v - k th_t >= 0] - [-v - k th_t >= 0]   (binary: [v - th_t >= 0]).
+ * spikes [B][T][D] int8. th_out [B][D] (nullable): the final threshold theta + gain a_T.
+ * levels 1..2. Replaces LifGen "lif-gen" (lif_gen.rs:182-237), kernels lifg_fwd_* (lif.cu:3123-3221). */
+int ava_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
+                 int levels, int is_signed, int alif, int8_t *spikes, float *th_out, ava_stream stream);
+
+/* ------------------------------------------------------------------ kWTA */
+
+/* Per row of u [n][h]: kth = the k-th largest value (duplicates counted); keep u_i when
+ * u_i - kth >= 0 (ties kept); a = relu(u · mask), squared when relu2. kth_out [n] (nullable).
+ * k >= h keeps every unit. h <= 8192. Replaces KwtaMask "kwta-mask" (lif.rs:239-284) /
+ * model::kwta_mask (model.rs:504-528) and kwta_relu2 (lif.cu:4629-4680, fwin_ops.rs:133). */
+int ava_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *kth_out,
+             ava_stream stream);
+
+/* ------------------------------------------------------------------ fast-weight memory */
+
+/* The general fast-weight recurrence per head row-block bh (F [hs][hs], row i = key channel):
+ *   r_j = sum_i e_i F_ij;  u_ij = b_i k_i v_j - a_i b_i e_i r_j;  S <- M S + u;
+ *   F_ij <- clamp(a_i F_ij + S_ij, +-cap) (M = 0: + u_ij);  y_j = sum_i q_i F_ij.
+ * q, k, e, v [BH][T][hs]; la (log alpha), b [BH][T][g] with g = 1 (per head) or hs (per channel);
+ * F, S [BH][hs][hs] carried in and out (S ignored when m == 0); y [BH][T][hs]. hs == 64.
+ * Replaces MemGen "mem-gen" (mem_gen.rs:248-309) / delta_rec (arch.rs:1091-1136). */
+int ava_mem_scan(const float *q, const float *k, const float *e, const float *v, const float *la,
+                 const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,
+                 float *y, ava_stream stream);
+
+/* The plain delta rule W += beta (v - W k) k^T, y = W q, in its chunked (WY/UT) form, chunks of
+ * 64: q, k, v [BH][T][64], beta [BH][T], F [BH][64][64] (F = W^T) carried in and out, y [BH][T][64].
+ * T a multiple of 64. Replaces model::delta_rule_from (model.rs:700-799) for per-head gates at
+ * alpha = 1. */
+int ava_delta_chunk(const float *q, const float *k, const float *v, const float *beta, int BH, int T,
+                    int hs, float *F, float *y, ava_stream stream);
+
+/* ------------------------------------------------------------------ model */
+
+/* The block options of the path (Ava 0.4's recipe, release/ava-0.4/arch.txt:1). */
+typedef struct {
+    int vocab, d, layers, hidden, kwta_k, head_size, gate_rank;
+    int eng_block;  /* the block with the engram read, -1 for none */
+    int eng_dim;    /* the engram's single head size (64) */
+    int levels;     /* spike levels each side (2 = int2) */
+    int alif, lif_scale, value_residual, dense, relu2;
+    float momentum, cap;
+    int planes;     /* activation planes of the dense int8 products (3 = accurate) */
+} ava_config;
+
+/* f32 HOST weights, named as the reference's VarMap (arch.rs:806-860). W [din][dout] as applied x·W. */
+typedef struct {
+    const float *lif_norm, *win, *beta_p, *theta, *arho, *again, *wout;
+    const float *mem_norm, *wq, *wk, *wv, *we, *wg, *wo;
+    const float *wa, *ba, *wb, *bb, *off, *wa1, *wa2, *wb1, *wb2, *vres;
+    const float *eng_norm, *ewq, *ewk, *ewv, *ewo; /* engram block only */
+    const float *mlp_norm, *w1, *w2, *dense;
+} ava_block_params;
+
+typedef struct {
+    const float *tok_emb;    /* [vocab][d]; the head is its transpose in int8 */
+    const float *final_norm; /* [d] */
+    const ava_block_params *blocks;
+} ava_params;
+
+/* The carried state of B streams (caller-owned device buffers). Replaces State's LIF, memory and
+ * engram tensors (state.rs:94-116). The engram keys/values are fp16. */
+typedef struct {
+    float *lif_v, *lif_s, *lif_a; /* [layers][B][d] */
+    float *mem_f, *mem_s;         /* [layers][B][d/hs][hs][hs] */
+    uint16_t *eng_k, *eng_v;      /* [B][eng_cap][eng_dim] fp16 */
+    int eng_cap, eng_len;         /* eng_len advances by T per forward */
+} ava_state;
+
+typedef struct ava_model ava_model;
+
+/* Build the model: upload and quantize every int8 matrix (Model::new + set_int8, model.rs:805, 949-991). */
+int ava_model_new(const ava_config *cfg, const ava_params *params, ava_model **out);
+void ava_model_free(ava_model *m);
+
+/* Teacher-forced forward of ids [B][T] (device int32) from the carried state st (updated in place):
+ * logits [B*T][vocab] f32 (nullable). Replaces Model::forward_with_state (state.rs:684-865) and,
+ * from a zero state, Model::forward (model.rs:1171) / forward_arch (arch.rs:1407-1566).
+ * Scratch memory is allocated on first use per (B, T) and kept by the model. */
+int ava_model_forward(ava_model *m, ava_state *st, const int32_t *ids, int B, int T, float *logits,
+                      ava_stream stream);
+
+/* Bytes of scratch the model holds after forwards of up to B*T rows. */
+size_t ava_model_scratch_bytes(const ava_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,602 @@
+/*
+ * ava_oracle.c — CPU restatement of the reference's int8 block forward (TEST INFRASTRUCTURE ONLY).
+ *
+ * Checker for the HIP kernels of ava_amd; never part of the product path. Built with
+ * -ffp-contract=off so every float operation is rounded on its own unless written as fmaf(),
+ * which is used exactly where the reference uses f32::mul_add (its gemm / int8 orders).
+ * Citations are relative to the reference's design-tests/nn/ (gpu/ = design-tests/nn/gpu/src).
+ *
+ * Parity of each function is pinned in tests/test_oracle.py against the reference's own known
+ * answers and against independent brute force; see the header for the list.
+ */
+#include "ava_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define NORM_EPS 1e-5f /* gpu/model.rs:36 */
+
+/* ------------------------------------------------------------------ scalar helpers */
+
+/* candle's sigmoid as gpu/model.rs:465-467 builds it: (exp(-x)·1 + 1)^-1 (gpu/model/fstep.rs:260-262). */
+float orc_sigmoid(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }
+
+/* gpu/model.rs:618-622 / gpu/model/fstep.rs:265-268: -(relu(-x) + ln(exp(-|x|)·1 + 1)). */
+float orc_log_sigmoid(float x) {
+    float soft = logf(expf(-fabsf(x)) * 1.0f + 1.0f);
+    float r = -x > 0.0f ? -x : 0.0f;
+    return -(r + soft);
+}
+
+/* (mean(x^2) + eps)^-1/2 as gpu/model/fstep.rs:213-221: sum from 0, the mean's affine, powf. */
+static float inv_rms(const float *x, int n) {
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += x[i] * x[i];
+    float ms = s * (float)(1.0 / (double)n) + 0.0f;
+    return powf(ms * 1.0f + NORM_EPS, -0.5f);
+}
+
+/* gpu/model.rs:458-462 / gpu/model/fstep.rs:207-211: x·inv·gain per row. */
+void orc_rmsnorm(const float *x, int n, int d, const float *gain, float *out) {
+    for (int r = 0; r < n; r++) {
+        const float *xr = x + (size_t)r * d;
+        float *o = out + (size_t)r * d;
+        float inv = inv_rms(xr, d);
+        for (int c = 0; c < d; c++) o[c] = (xr[c] * inv) * gain[c];
+    }
+}
+
+/* gpu/model.rs:589-592 / gpu/model/fstep.rs:271-282: each head slice times (sum x^2 + 1e-6)^-1/2. */
+static void l2_heads(float *x, int n, int hs) {
+    for (int h = 0; h < n; h += hs) {
+        float s = 0.0f;
+        for (int i = 0; i < hs; i++) s += x[h + i] * x[h + i];
+        float inv = powf(s * 1.0f + 1e-6f, -0.5f);
+        for (int i = 0; i < hs; i++) x[h + i] = x[h + i] * inv;
+    }
+}
+
+/* gpu/model.rs:583-587 / gpu/model/fstep.rs:285-292: rmsnorm without gain per head. */
+static void head_norm(float *y, int n, int hs) {
+    for (int h = 0; h < n; h += hs) {
+        float inv = inv_rms(y + h, hs);
+        for (int i = 0; i < hs; i++) y[h + i] = y[h + i] * inv;
+    }
+}
+
+/* gpu/model/fstep.rs:223-257: one-row product out[c] = sum_j x[j] w[j][c] in gemm's order
+ * (k >= 3: w[0][c]·x[0], then fma over j = 1, 2, ...). */
+static void gemv(const float *x, int k, const float *w, int n, float *out) {
+    if (k == 0) {
+        for (int c = 0; c < n; c++) out[c] = 0.0f;
+    } else if (k == 1) {
+        for (int c = 0; c < n; c++) out[c] = w[c] * x[0];
+    } else if (k == 2) {
+        for (int c = 0; c < n; c++) out[c] = w[n + c] * x[1] + w[c] * x[0];
+    } else {
+        for (int c = 0; c < n; c++) out[c] = w[c] * x[0];
+        for (int j = 1; j < k; j++) {
+            const float *wr = w + (size_t)j * n;
+            float xj = x[j];
+            for (int c = 0; c < n; c++) out[c] = fmaf(wr[c], xj, out[c]);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ int8 weights */
+
+void orc_quantize_int8(const float *w, int din, int dout, int8_t *q, float *scale) {
+    for (int c = 0; c < dout; c++) scale[c] = 0.0f;
+    for (int r = 0; r < din; r++)
+        for (int c = 0; c < dout; c++) {
+            float a = fabsf(w[(size_t)r * dout + c]);
+            if (a > scale[c]) scale[c] = a;
+        }
+    for (int c = 0; c < dout; c++) scale[c] = scale[c] > 0.0f ? scale[c] / 127.0f : 1.0f;
+    for (size_t i = 0; i < (size_t)din * dout; i++) {
+        float t = roundf(w[i] / scale[i % dout]); /* round half away from zero, as f32::round */
+        if (t > 127.0f) t = 127.0f;
+        if (t < -127.0f) t = -127.0f;
+        q[i] = (int8_t)t;
+    }
+}
+
+#define TILE 64
+
+/* One row against one 64-column tile of q [din][dout]: the fma chain of gpu/int8.rs:313-331. */
+static void tile_row(const float *x, int din, const int8_t *q, int dout, int c0, int nc,
+                     const float *scale, float *y) {
+    float acc[TILE];
+    for (int c = 0; c < TILE; c++) acc[c] = 0.0f;
+    if (nc == TILE) {
+        for (int j = 0; j < din; j++) {
+            float xj = x[j];
+            if (xj == 0.0f) continue; /* E2: fma(0, q, acc) == acc for every acc this chain holds */
+            const int8_t *qr = q + (size_t)j * dout + c0;
+            for (int c = 0; c < TILE; c++) acc[c] = fmaf(xj, (float)qr[c], acc[c]);
+        }
+    } else {
+        for (int j = 0; j < din; j++) {
+            float xj = x[j];
+            if (xj == 0.0f) continue;
+            const int8_t *qr = q + (size_t)j * dout + c0;
+            for (int c = 0; c < nc; c++) acc[c] = fmaf(xj, (float)qr[c], acc[c]);
+        }
+    }
+    for (int c = 0; c < nc; c++) y[c0 + c] = acc[c] * scale[c0 + c];
+}
+
+void orc_q8_matmul_ref(const float *x, int m, int din, const int8_t *q, const float *scale,
+                       int dout, float *y, int threads) {
+    int tiles = (dout + TILE - 1) / TILE;
+    long units = (long)m * tiles;
+    if (threads < 1) threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (long u = 0; u < units; u++) {
+        int t = (int)(u / m), r = (int)(u % m);
+        int c0 = t * TILE, nc = dout - c0 < TILE ? dout - c0 : TILE;
+        tile_row(x + (size_t)r * din, din, q, dout, c0, nc, scale, y + (size_t)r * dout);
+    }
+}
+
+void orc_quant_planes(const float *x, int m, int k, int planes, int8_t *xq, int32_t *xexp) {
+    for (int r = 0; r < m; r++) {
+        const float *xr = x + (size_t)r * k;
+        float amax = 0.0f;
+        for (int j = 0; j < k; j++) amax = fmaxf(amax, fabsf(xr[j]));
+        int e = 0;
+        if (amax > 0.0f) {
+            int ex;
+            frexpf(amax, &ex);
+            e = ex - 7;
+            if (ldexpf(amax, -e) >= 127.5f) e += 1;
+        }
+        xexp[r] = e;
+        for (int j = 0; j < k; j++) {
+            float t = ldexpf(xr[j], -e);
+            for (int p = 0; p < planes; p++) {
+                float qv = rintf(t);
+                xq[((size_t)p * m + r) * k + j] = (int8_t)qv;
+                t = (t - qv) * 128.0f;
+            }
+        }
+    }
+}
+
+void orc_q8_acc(const int8_t *a, int m, int k, const int8_t *q, int n, int32_t *acc, int threads) {
+    if (threads < 1) threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (int r = 0; r < m; r++) {
+        int32_t *o = acc + (size_t)r * n;
+        for (int c = 0; c < n; c++) o[c] = 0;
+        const int8_t *ar = a + (size_t)r * k;
+        for (int j = 0; j < k; j++) {
+            int32_t av = ar[j];
+            if (!av) continue;
+            const int8_t *qr = q + (size_t)j * n;
+            for (int c = 0; c < n; c++) o[c] += av * (int32_t)qr[c];
+        }
+    }
+}
+
+void orc_q8_combine(const int32_t *acc, int planes, const int32_t *xexp, int m, const float *scale,
+                    int n, float *y) {
+    int sh = 7 * (planes - 1);
+    for (int r = 0; r < m; r++) {
+        int e = xexp ? xexp[r] : 0;
+        for (int c = 0; c < n; c++) {
+            int64_t A = 0;
+            for (int p = 0; p < planes; p++)
+                A += (int64_t)acc[((size_t)p * m + r) * n + c] << (7 * (planes - 1 - p));
+            float v = (float)(double)A;
+            v = ldexpf(v, e - sh);
+            y[(size_t)r * n + c] = v * scale[c];
+        }
+    }
+}
+
+void orc_q8_matmul_planes(const float *x, int m, int k, int planes, const int8_t *q,
+                          const float *scale, int n, float *y, int threads) {
+    int8_t *xq = (int8_t *)malloc((size_t)planes * m * k);
+    int32_t *xe = (int32_t *)malloc(sizeof(int32_t) * (size_t)m);
+    int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)planes * m * n);
+    orc_quant_planes(x, m, k, planes, xq, xe);
+    for (int p = 0; p < planes; p++)
+        orc_q8_acc(xq + (size_t)p * m * k, m, k, q, n, acc + (size_t)p * m * n, threads);
+    orc_q8_combine(acc, planes, xe, m, scale, n, y);
+    free(xq);
+    free(xe);
+    free(acc);
+}
+
+/* ------------------------------------------------------------------ LIF */
+
+/* gpu/lif_gen.rs:54-64 (Kind::spike). */
+static float spike_of(float v, float th, int levels, int is_signed) {
+    if (!is_signed) return v - th >= 0.0f ? 1.0f : 0.0f;
+    float h = 0.0f;
+    for (int k = 1; k <= levels; k++) {
+        float kth = th * (float)k;
+        h += (v - kth >= 0.0f ? 1.0f : 0.0f) - (-v - kth >= 0.0f ? 1.0f : 0.0f);
+    }
+    return h;
+}
+
+void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
+                  float *a, int levels, int is_signed, int alif, int8_t *spikes) {
+    for (int bi = 0; bi < B; bi++)
+        for (int c = 0; c < D; c++) {
+            int i = bi * D + c;
+            float bt = ps[c], th0 = ps[D + c], rho = ps[2 * D + c], gain = ps[3 * D + c];
+            float omr = 1.0f - rho;
+            float vv = v[i], sp = s[i], aa = a[i];
+            float thp = alif ? th0 + aa * gain : th0;
+            for (int t = 0; t < T; t++) {
+                size_t j = ((size_t)bi * T + t) * D + c;
+                float tht = th0;
+                if (alif) {
+                    aa = aa * rho + fabsf(sp) * omr;
+                    tht = th0 + aa * gain;
+                }
+                vv = (vv * bt + cur[j]) - sp * thp;
+                sp = spike_of(vv, tht, levels, is_signed);
+                thp = tht;
+                spikes[j] = (int8_t)sp;
+            }
+            v[i] = vv;
+            s[i] = sp;
+            a[i] = aa;
+        }
+}
+
+/* ------------------------------------------------------------------ kWTA */
+
+static int cmp_desc(const void *pa, const void *pb) {
+    float a = *(const float *)pa, b = *(const float *)pb;
+    return (a < b) - (a > b);
+}
+
+void orc_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *kth_out) {
+    float *buf = (float *)malloc(sizeof(float) * (size_t)h);
+    for (int r = 0; r < n; r++) {
+        const float *ur = u + (size_t)r * h;
+        float *ar = a + (size_t)r * h;
+        int keep_all = k >= h;
+        float kth = 0.0f;
+        if (!keep_all) {
+            memcpy(buf, ur, sizeof(float) * (size_t)h);
+            qsort(buf, (size_t)h, sizeof(float), cmp_desc);
+            kth = buf[k - 1];
+        }
+        if (kth_out) kth_out[r] = keep_all ? -INFINITY : kth;
+        for (int i = 0; i < h; i++) {
+            float x = ur[i];
+            float keep = keep_all ? 1.0f : (x - kth >= 0.0f ? 1.0f : 0.0f);
+            float y = x * keep;
+            y = y > 0.0f ? y : 0.0f;
+            ar[i] = relu2 ? y * y : y;
+        }
+    }
+    free(buf);
+}
+
+/* ------------------------------------------------------------------ fast-weight memory */
+
+void orc_mem_rec(const float *q, const float *k, const float *e, const float *v, const float *la,
+                 const float *b, int BH, int T, int hs, int g, float m, float cap, float *F,
+                 float *S, float *y) {
+    float *r = (float *)malloc(sizeof(float) * (size_t)hs);
+    float *al = (float *)malloc(sizeof(float) * (size_t)hs);
+    float *bb = (float *)malloc(sizeof(float) * (size_t)hs);
+    for (int bh = 0; bh < BH; bh++) {
+        float *f = F + (size_t)bh * hs * hs;
+        float *sm = S ? S + (size_t)bh * hs * hs : NULL;
+        for (int t = 0; t < T; t++) {
+            size_t o = ((size_t)bh * T + t) * hs, og = ((size_t)bh * T + t) * g;
+            const float *qt = q + o, *kt = k + o, *et = e + o, *vt = v + o;
+            for (int i = 0; i < hs; i++) {
+                al[i] = expf(la[og + (g > 1 ? i : 0)]);
+                bb[i] = b[og + (g > 1 ? i : 0)];
+            }
+            for (int j = 0; j < hs; j++) {
+                float sacc = 0.0f;
+                for (int i = 0; i < hs; i++) sacc += et[i] * f[i * hs + j];
+                r[j] = sacc;
+            }
+            for (int i = 0; i < hs; i++)
+                for (int j = 0; j < hs; j++) {
+                    float u = ((bb[i] * kt[i]) * vt[j]) - (((al[i] * bb[i]) * et[i]) * r[j]);
+                    int p = i * hs + j;
+                    float fp;
+                    if (m != 0.0f) {
+                        sm[p] = m * sm[p] + u;
+                        fp = al[i] * f[p] + sm[p];
+                    } else {
+                        fp = al[i] * f[p] + u;
+                    }
+                    f[p] = fp < -cap ? -cap : (fp > cap ? cap : fp);
+                }
+            float *yt = y + o;
+            for (int j = 0; j < hs; j++) {
+                float sacc = 0.0f;
+                for (int i = 0; i < hs; i++) sacc += qt[i] * f[i * hs + j];
+                yt[j] = sacc;
+            }
+        }
+    }
+    free(r);
+    free(al);
+    free(bb);
+}
+
+void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float *v,
+                     const float *la, const float *b, int BH, int T, int hs, int g, double m,
+                     double *F, double *S, double *y) {
+    double *r = (double *)malloc(sizeof(double) * (size_t)hs);
+    for (int bh = 0; bh < BH; bh++) {
+        double *f = F + (size_t)bh * hs * hs;
+        double *sm = S ? S + (size_t)bh * hs * hs : NULL;
+        for (int t = 0; t < T; t++) {
+            size_t o = ((size_t)bh * T + t) * hs, og = ((size_t)bh * T + t) * g;
+            for (int j = 0; j < hs; j++) {
+                double sacc = 0.0;
+                for (int i = 0; i < hs; i++) sacc += (double)e[o + i] * f[i * hs + j];
+                r[j] = sacc;
+            }
+            for (int i = 0; i < hs; i++) {
+                double al = exp((double)la[og + (g > 1 ? i : 0)]), bi = b[og + (g > 1 ? i : 0)];
+                for (int j = 0; j < hs; j++) {
+                    double u = bi * k[o + i] * v[o + j] - al * bi * e[o + i] * r[j];
+                    int p = i * hs + j;
+                    if (m != 0.0) {
+                        sm[p] = m * sm[p] + u;
+                        f[p] = al * f[p] + sm[p];
+                    } else {
+                        f[p] = al * f[p] + u;
+                    }
+                }
+            }
+            for (int j = 0; j < hs; j++) {
+                double sacc = 0.0;
+                for (int i = 0; i < hs; i++) sacc += (double)q[o + i] * f[i * hs + j];
+                y[o + j] = sacc;
+            }
+        }
+    }
+    free(r);
+}
+
+/* ------------------------------------------------------------------ model */
+
+/* x [m, din] · W: the reference's W8A32 product (planes == 0) or the build's split planes. */
+static void mm(const float *x, int m, const orc_qw *w, float *y, int planes, int threads) {
+    if (planes <= 0)
+        orc_q8_matmul_ref(x, m, w->din, w->q, w->scale, w->dout, y, threads);
+    else
+        orc_q8_matmul_planes(x, m, w->din, planes, w->q, w->scale, w->dout, y, threads);
+}
+
+/* Integer inputs (the spikes): both semantics agree exactly; the exact integer sum, times the scale. */
+static void mm_int(const int8_t *s, int m, const orc_qw *w, float *y, int threads) {
+    int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)m * w->dout);
+    orc_q8_acc(s, m, w->din, w->q, w->dout, acc, threads);
+    orc_q8_combine(acc, 1, NULL, m, w->scale, w->dout, y);
+    free(acc);
+}
+
+/* One head's causal read (gpu/model/fstep.rs:303-329: scores in gemm's order, softmax, p·V). */
+static void attend(const float *q, const float *kc, const float *vc, int n, int hs, float scale,
+                   float *sc, float *out) {
+    for (int j = 0; j < n; j++) {
+        const float *kr = kc + (size_t)j * hs;
+        float s = kr[0] * q[0];
+        for (int a = 1; a < hs; a++) s = fmaf(kr[a], q[a], s);
+        sc[j] = s * scale + 0.0f;
+    }
+    float mx = sc[0];
+    for (int j = 0; j < n; j++)
+        if (mx < sc[j]) mx = sc[j];
+    float den = 0.0f;
+    for (int j = 0; j < n; j++) {
+        sc[j] = expf(sc[j] - mx);
+        den += sc[j];
+    }
+    for (int j = 0; j < n; j++) sc[j] = sc[j] / den;
+    gemv(sc, n, vc, hs, out);
+}
+
+#define ALLOC(T_, n) ((T_ *)malloc(sizeof(T_) * (size_t)(n)))
+
+int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *ids, int B, int T,
+                      orc_state *st, float *logits, int planes, int threads, orc_trace *tr) {
+    const int d = cfg->d, H = cfg->hidden, hs = cfg->head_size, nh = d / hs, rk = cfg->gate_rank;
+    const int de = cfg->eng_dim, L = cfg->layers;
+    const size_t N = (size_t)B * T;
+    if (d % hs || B < 1 || T < 1) return 1;
+    if (cfg->eng_block >= 0 && st->eng_len + T > st->eng_cap) return 2;
+
+    float *x = ALLOC(float, N * d), *h = ALLOC(float, N * d), *y = ALLOC(float, N * d);
+    float *cur = ALLOC(float, N * d);
+    int8_t *spk = ALLOC(int8_t, N * d);
+    float *q = ALLOC(float, N * d), *kr = ALLOC(float, N * d), *k = ALLOC(float, N * d);
+    float *v = ALLOC(float, N * d), *weo = ALLOC(float, N * d), *gq = ALLOC(float, N * d);
+    float *ek = ALLOC(float, N * d), *la = ALLOC(float, N * d), *bw = ALLOC(float, N * d);
+    float *vfirst = ALLOC(float, N * d);
+    float *u = ALLOC(float, N * H), *act = ALLOC(float, N * H);
+    float *za = ALLOC(float, nh), *zb = ALLOC(float, nh), *z1 = ALLOC(float, rk);
+    float *lra = ALLOC(float, d), *lrb = ALLOC(float, d);
+    float *ps = ALLOC(float, 4 * d);
+    /* head-major copies for the recurrence: [B][nh][T][hs] */
+    float *hq = ALLOC(float, N * d), *hk = ALLOC(float, N * d), *he = ALLOC(float, N * d);
+    float *hv = ALLOC(float, N * d), *hla = ALLOC(float, N * d), *hb = ALLOC(float, N * d);
+    float *hy = ALLOC(float, N * d);
+    float **streams = NULL;
+    if (cfg->dense) {
+        streams = ALLOC(float *, L + 1);
+        for (int i = 0; i <= L; i++) streams[i] = ALLOC(float, N * d);
+    }
+
+    for (size_t n = 0; n < N; n++)
+        memcpy(x + n * d, mdl->tok_emb + (size_t)ids[n] * d, sizeof(float) * d);
+    if (cfg->dense) memcpy(streams[0], x, sizeof(float) * N * d);
+
+    for (int i = 0; i < L; i++) {
+        const orc_block *bk = &mdl->blocks[i];
+        /* ---- the spiking layer (gpu/arch.rs:1632-1695; gpu/model/fstep/arch.rs:636-681) */
+        orc_rmsnorm(x, (int)N, d, bk->lif_norm, h);
+        mm(h, (int)N, &bk->win, cur, planes, threads);
+        for (int c = 0; c < d; c++) {
+            float beta = orc_sigmoid(bk->beta_p[c]);
+            ps[c] = beta;
+            ps[d + c] = bk->theta[c];
+            ps[2 * d + c] = cfg->alif ? orc_sigmoid(bk->arho[c]) : 0.0f;
+            ps[3 * d + c] = cfg->alif ? bk->again[c] : 0.0f;
+        }
+        if (cfg->lif_scale)
+            for (size_t n = 0; n < N; n++)
+                for (int c = 0; c < d; c++) cur[n * d + c] = cur[n * d + c] * (ps[c] * -1.0f + 1.0f);
+        if (tr && tr->cur) memcpy(tr->cur + (size_t)i * N * d, cur, sizeof(float) * N * d);
+        orc_lif_scan(cur, B, T, d, ps, st->lif_v + (size_t)i * B * d, st->lif_s + (size_t)i * B * d,
+                     st->lif_a + (size_t)i * B * d, cfg->levels, 1, cfg->alif, spk);
+        if (tr && tr->spikes) memcpy(tr->spikes + (size_t)i * N * d, spk, N * d);
+        mm_int(spk, (int)N, &bk->wout, y, threads);
+        for (size_t j = 0; j < N * d; j++) x[j] = x[j] + y[j];
+
+        /* ---- the fast-weight memory (gpu/arch.rs:1873-2020; gpu/model/fstep/arch.rs:683-896) */
+        orc_rmsnorm(x, (int)N, d, bk->mem_norm, h);
+        mm(h, (int)N, &bk->wq, q, planes, threads);
+        mm(h, (int)N, &bk->wk, kr, planes, threads);
+        mm(h, (int)N, &bk->wv, v, planes, threads);
+        mm(h, (int)N, &bk->we, weo, planes, threads);
+        mm(h, (int)N, &bk->wg, gq, planes, threads);
+        memcpy(k, kr, sizeof(float) * N * d);
+        l2_heads(q, (int)(N * d), hs);
+        l2_heads(k, (int)(N * d), hs);
+        if (cfg->value_residual) {
+            if (i == 0) {
+                memcpy(vfirst, v, sizeof(float) * N * d);
+            } else {
+                float p0 = bk->vres[0] * 1.0f + 1.0f, p1 = bk->vres[1];
+                for (size_t j = 0; j < N * d; j++) v[j] = v[j] * p0 + vfirst[j] * p1;
+            }
+        }
+        for (size_t n = 0; n < N; n++) {
+            const float *hr = h + n * d;
+            gemv(hr, d, bk->wa, nh, za);
+            gemv(hr, d, bk->wb, nh, zb);
+            for (int e = 0; e < nh; e++) {
+                za[e] = za[e] + bk->ba[e];
+                zb[e] = zb[e] + bk->bb[e];
+            }
+            gemv(hr, d, bk->wa1, rk, z1);
+            gemv(z1, rk, bk->wa2, d, lra);
+            gemv(hr, d, bk->wb1, rk, z1);
+            gemv(z1, rk, bk->wb2, d, lrb);
+            for (int c = 0; c < d; c++) {
+                int e = c / hs;
+                la[n * d + c] = orc_log_sigmoid((za[e] + bk->off[c]) + lra[c]);
+                bw[n * d + c] = orc_sigmoid(zb[e] + lrb[c]) * 2.0f + 0.0f;
+                ek[n * d + c] = kr[n * d + c] + weo[n * d + c];
+            }
+        }
+        l2_heads(ek, (int)(N * d), hs);
+        /* [B*T][nh][hs] -> [B][nh][T][hs] */
+        for (int bi = 0; bi < B; bi++)
+            for (int t = 0; t < T; t++)
+                for (int e = 0; e < nh; e++) {
+                    size_t src = ((size_t)bi * T + t) * d + (size_t)e * hs;
+                    size_t dst = (((size_t)bi * nh + e) * T + t) * hs;
+                    memcpy(hq + dst, q + src, sizeof(float) * hs);
+                    memcpy(hk + dst, k + src, sizeof(float) * hs);
+                    memcpy(he + dst, ek + src, sizeof(float) * hs);
+                    memcpy(hv + dst, v + src, sizeof(float) * hs);
+                    memcpy(hla + dst, la + src, sizeof(float) * hs);
+                    memcpy(hb + dst, bw + src, sizeof(float) * hs);
+                }
+        orc_mem_rec(hq, hk, he, hv, hla, hb, B * nh, T, hs, hs, cfg->momentum, cfg->cap,
+                    st->mem_f + (size_t)i * B * nh * hs * hs,
+                    cfg->momentum != 0.0f ? st->mem_s + (size_t)i * B * nh * hs * hs : NULL, hy);
+        for (int bi = 0; bi < B; bi++)
+            for (int t = 0; t < T; t++)
+                for (int e = 0; e < nh; e++)
+                    memcpy(y + ((size_t)bi * T + t) * d + (size_t)e * hs,
+                           hy + (((size_t)bi * nh + e) * T + t) * hs, sizeof(float) * hs);
+        if (tr && tr->memy) memcpy(tr->memy + (size_t)i * N * d, y, sizeof(float) * N * d);
+        head_norm(y, (int)(N * d), hs);
+        for (size_t j = 0; j < N * d; j++) {
+            float g = gq[j];
+            y[j] = y[j] * (g / (1.0f + expf(-g)));
+        }
+        mm(y, (int)N, &bk->wo, h, planes, threads);
+        for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];
+
+        /* ---- the engram read (gpu/arch.rs:1706-1738; gpu/model/fstep/arch.rs:898-974), one head */
+        if (i == cfg->eng_block) {
+            float *eq = ALLOC(float, N * de), *ekk = ALLOC(float, N * de), *evv = ALLOC(float, N * de);
+            float *eo = ALLOC(float, N * de), *sc = ALLOC(float, st->eng_len + T);
+            orc_rmsnorm(x, (int)N, d, bk->eng_norm, h);
+            mm(h, (int)N, &bk->ewq, eq, planes, threads);
+            mm(h, (int)N, &bk->ewk, ekk, planes, threads);
+            mm(h, (int)N, &bk->ewv, evv, planes, threads);
+            int n0 = st->eng_len;
+            for (int bi = 0; bi < B; bi++)
+                for (int t = 0; t < T; t++) {
+                    size_t dst = ((size_t)bi * st->eng_cap + n0 + t) * de;
+                    memcpy(st->eng_k + dst, ekk + ((size_t)bi * T + t) * de, sizeof(float) * de);
+                    memcpy(st->eng_v + dst, evv + ((size_t)bi * T + t) * de, sizeof(float) * de);
+                }
+            float scale = (float)(1.0 / sqrt((double)de));
+            for (int bi = 0; bi < B; bi++)
+                for (int t = 0; t < T; t++) {
+                    size_t base = (size_t)bi * st->eng_cap * de;
+                    attend(eq + ((size_t)bi * T + t) * de, st->eng_k + base, st->eng_v + base,
+                           n0 + t + 1, de, scale, sc, eo + ((size_t)bi * T + t) * de);
+                }
+            st->eng_len = n0 + T;
+            mm(eo, (int)N, &bk->ewo, h, planes, threads);
+            for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];
+            free(eq);
+            free(ekk);
+            free(evv);
+            free(eo);
+            free(sc);
+        }
+
+        /* ---- the sparse MLP (gpu/arch.rs:1814-1855; gpu/model/fstep/arch.rs:976-996) */
+        orc_rmsnorm(x, (int)N, d, bk->mlp_norm, h);
+        mm(h, (int)N, &bk->w1, u, planes, threads);
+        if (tr && tr->u) memcpy(tr->u + (size_t)i * N * H, u, sizeof(float) * N * H);
+        orc_kwta(u, (int)N, H, cfg->kwta_k, cfg->relu2, act, tr && tr->kth ? tr->kth + (size_t)i * N : NULL);
+        mm(act, (int)N, &bk->w2, h, planes, threads);
+        for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];
+
+        /* ---- the dense residual (gpu/arch.rs:1492-1500; gpu/model/fstep/arch.rs:1010-1024) */
+        if (cfg->dense) {
+            memcpy(streams[i + 1], x, sizeof(float) * N * d);
+            for (int j = 0; j <= i + 1; j++) {
+                float w = bk->dense[j];
+                const float *sj = streams[j];
+                for (size_t z = 0; z < N * d; z++) x[z] = x[z] + sj[z] * w;
+            }
+        }
+        if (tr && tr->x) memcpy(tr->x + (size_t)i * N * d, x, sizeof(float) * N * d);
+    }
+
+    orc_rmsnorm(x, (int)N, d, mdl->final_norm, h);
+    if (tr && tr->hf) memcpy(tr->hf, h, sizeof(float) * N * d);
+    if (logits) mm(h, (int)N, &mdl->head, logits, planes, threads);
+
+    free(x); free(h); free(y); free(cur); free(spk); free(q); free(kr); free(k); free(v);
+    free(weo); free(gq); free(ek); free(la); free(bw); free(vfirst); free(u); free(act);
+    free(za); free(zb); free(z1); free(lra); free(lrb); free(ps);
+    free(hq); free(hk); free(he); free(hv); free(hla); free(hb); free(hy);
+    if (streams) {
+        for (int i = 0; i <= L; i++) free(streams[i]);
+        free(streams);
+    }
+    return 0;
+}

@@ -1,0 +1,170 @@
+/*
+ * ava_oracle.h — CPU oracle for the int8 block forward of Ava (nochallenge/ava).
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker the HIP kernels are compared against
+ * (tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg). The product path
+ * (ava_amd/, libava_amd.so) never links, loads or calls it.
+ *
+ * Every function restates one piece of the reference's CPU engine (Rust, design-tests/nn/):
+ * the citation next to each declaration names the file:line it follows. Reference paths are
+ * relative to design-tests/nn/ (gpu/ = design-tests/nn/gpu/src).
+ *
+ * Two int8 product semantics live here:
+ *   - the reference's: int8 weights, f32 activations, f32 fused multiply-adds in the order
+ *     j = 0, 1, ... from +0, one multiply by the column scale (gpu/int8.rs:301-331);
+ *   - the build's split-plane form: activations as P planes of int8 under a power-of-two row
+ *     scale, exact int32 accumulators per plane, one combine (no reference counterpart; it is
+ *     what the i8 MFMA kernels compute, so their accumulators are checked bit for bit here).
+ */
+#ifndef AVA_ORACLE_H
+#define AVA_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- int8 weights */
+
+/* parts/src/quant.rs:18-31. W [din][dout] row-major (applied x·W). scale[c] = max_j |W[j][c]| / 127
+ * (1 for an all-zero column); q = clamp(round_half_away(W / scale), -127, 127). */
+void orc_quantize_int8(const float *w, int din, int dout, int8_t *q, float *scale);
+
+/* gpu/int8.rs:301-331 (tile_scalar) and :166-211 (matmul_rows_with): y[r][c] = scale[c] *
+ * (fma chain over j ascending from +0 of x[r][j] * (float)q[j][c]). Zero inputs are skipped
+ * (E2, gpu/int8.rs:10-13: the same bits). q [din][dout] row-major. Rows are split over
+ * `threads` OpenMP threads; each output is written by one thread, so any count gives the same bits. */
+void orc_q8_matmul_ref(const float *x, int m, int din, const int8_t *q, const float *scale,
+                       int dout, float *y, int threads);
+
+/* The build's split-plane activation quantizer (no reference counterpart). For each row:
+ * e = the smallest exponent with max|x| * 2^-e < 127.5 (e = 0 for an all-zero row);
+ * t0 = x*2^-e, q0 = rint(t0), r0 = t0 - q0; t1 = r0*128, q1 = rint(t1), r1 = t1 - q1; ...
+ * so x ~= 2^e * sum_p q_p * 2^(-7p). xq [planes][m][k], xexp [m]. */
+void orc_quant_planes(const float *x, int m, int k, int planes, int8_t *xq, int32_t *xexp);
+
+/* Exact int32 accumulators acc [m][n] = sum_j a[m][j] * q[j][n] for int8 a [m][k], q [k][n]. */
+void orc_q8_acc(const int8_t *a, int m, int k, const int8_t *q, int n, int32_t *acc, int threads);
+
+/* The combine shared with the GPU epilogue: A = sum_p acc_p * 2^(7(P-1-p)) (int64, exact);
+ * y = (float)A; y = y * 2^(xexp - 7(P-1)) (exact); y = y * scale[n] (one rounding).
+ * acc [planes][m][n]; xexp NULL means exponent 0 for every row. */
+void orc_q8_combine(const int32_t *acc, int planes, const int32_t *xexp, int m, const float *scale,
+                    int n, float *y);
+
+/* Quantize + accumulate + combine: the build's dense int8 product. */
+void orc_q8_matmul_planes(const float *x, int m, int k, int planes, const int8_t *q,
+                          const float *scale, int n, float *y, int threads);
+
+/* ---------------------------------------------------------------- LIF scan */
+
+/* gpu/lif_gen.rs:151-214 (step + cpu_fwd). cur [B][T][D]; ps = [beta | theta | rho | gain] (each [D]);
+ * v, s, a [B][D]: the carried state on entry, the final state on exit. levels 1 or 2; is_signed 0
+ * for binary spikes; alif 0/1. spikes [B][T][D] as int8. Each operation rounded on its own. */
+void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
+                  float *a, int levels, int is_signed, int alif, int8_t *spikes);
+
+/* ---------------------------------------------------------------- kWTA */
+
+/* gpu/model/fstep.rs:295-299 (kth_largest) and gpu/model/fstep/arch.rs:976-989: per row of u [n][h],
+ * kth = the k-th largest (duplicates counted), keep u_i when u_i - kth >= 0 (ties kept), a = relu,
+ * squared when relu2. k >= h keeps every unit. kth_out [n] (NaN-free inputs). */
+void orc_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *kth_out);
+
+/* ---------------------------------------------------------------- fast-weight memory */
+
+/* gpu/mem_gen.rs:220-273 (cpu_step_h, MemGen::cpu_fwd) = gpu/arch.rs:1091-1136 (delta_rec):
+ * per head row-block bh, F [hs][hs] (row i = key channel, column j = value channel):
+ *   r_j = sum_i e_i F_ij;  u_ij = b_i k_i v_j - a_i b_i e_i r_j;  S <- M S + u (M != 0);
+ *   F_ij <- clamp(a_i F_ij + S_ij (or + u_ij), -cap, cap);  y_j = sum_i q_i F_ij (after the write).
+ * q, k, e, v [BH][T][hs]; la (log alpha) and b [BH][T][g], g = 1 (per head) or hs (per channel).
+ * F, S [BH][hs][hs] carried in and out (S unused when m == 0). y [BH][T][hs]. */
+void orc_mem_rec(const float *q, const float *k, const float *e, const float *v, const float *la,
+                 const float *b, int BH, int T, int hs, int g, float m, float cap, float *F,
+                 float *S, float *y);
+
+/* The same recurrence in float64 (the brute-force check of orc_mem_rec and of the GPU's chunked form). */
+void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float *v,
+                     const float *la, const float *b, int BH, int T, int hs, int g, double m,
+                     double *F, double *S, double *y);
+
+/* ---------------------------------------------------------------- model */
+
+typedef struct {
+    const int8_t *q;     /* [din][dout] */
+    const float *scale;  /* [dout] */
+    int din, dout;
+} orc_qw;
+
+typedef struct {
+    const float *lif_norm;                 /* [d] */
+    orc_qw win;                            /* [d, d] */
+    const float *beta_p;                   /* [d] leak logits (beta = sigmoid) */
+    const float *theta;                    /* [d] */
+    const float *arho;                     /* [d] ALIF decay logits (rho = sigmoid) */
+    const float *again;                    /* [d] ALIF gain */
+    orc_qw wout;                           /* [d, d] */
+    const float *mem_norm;                 /* [d] */
+    orc_qw wq, wk, wv, we, wg, wo;         /* [d, d] */
+    const float *wa, *ba, *wb, *bb;        /* [d, nh], [nh] */
+    const float *off;                      /* [d] */
+    const float *wa1, *wa2, *wb1, *wb2;    /* [d, r], [r, d] */
+    const float *vres;                     /* [2] */
+    const float *eng_norm;                 /* [d] (engram block only) */
+    orc_qw ewq, ewk, ewv, ewo;             /* [d, de] x3, [de, d] */
+    const float *mlp_norm;                 /* [d] */
+    orc_qw w1, w2;                         /* [d, H], [H, d] */
+    const float *dense;                    /* [i + 2] */
+} orc_block;
+
+typedef struct {
+    int vocab, d, layers, hidden, kwta_k, heads, head_size, gate_rank;
+    int eng_block;   /* -1: no engram read */
+    int eng_dim;
+    int levels;      /* spike levels each side (2 = int2) */
+    int alif, lif_scale, value_residual, dense, relu2;
+    float momentum, cap;
+} orc_cfg;
+
+typedef struct {
+    const float *tok_emb;   /* [V, d] */
+    orc_qw head;            /* E^T [d, V] */
+    const float *final_norm;
+    const orc_block *blocks;
+} orc_model;
+
+typedef struct {
+    float *lif_v, *lif_s, *lif_a;   /* [layers][B][d] */
+    float *mem_f, *mem_s;           /* [layers][B][nh][hs][hs] */
+    float *eng_k, *eng_v;           /* [B][eng_cap][de] */
+    int eng_cap, eng_len;           /* entries held per stream */
+} orc_state;
+
+/* Optional copies of what each block computed (NULL fields are skipped). Layer-major. */
+typedef struct {
+    int8_t *spikes;   /* [layers][B*T][d] */
+    float *cur;       /* [layers][B*T][d] LIF input currents */
+    float *u;         /* [layers][B*T][H] W1 outputs */
+    float *kth;       /* [layers][B*T] */
+    float *memy;      /* [layers][B*T][d] memory read-outs before the head norm */
+    float *x;         /* [layers][B*T][d] stream after each block (after the dense mix) */
+    float *hf;        /* [B*T][d] final normed state */
+} orc_trace;
+
+/* gpu/arch.rs:1407-1867 (forward_arch / block_arch / mem_arch) with carried state as in
+ * gpu/state.rs:684-1071, one op order as gpu/model/fstep/arch.rs:525-1073. ids [B][T].
+ * gemm_planes: 0 = the reference's W8A32 products; P >= 1 = the build's split-plane products.
+ * logits [B*T][V] (may be NULL). Returns 0 on success. */
+int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *ids, int B, int T,
+                      orc_state *st, float *logits, int gemm_planes, int threads, orc_trace *tr);
+
+/* The same building blocks exposed for tests. */
+void orc_rmsnorm(const float *x, int n, int d, const float *gain, float *out);
+float orc_sigmoid(float x);
+float orc_log_sigmoid(float x);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

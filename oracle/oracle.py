@@ -1,0 +1,317 @@
+"""ctypes front of the CPU oracle (oracle/libava_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, always as the checker, never as the thing measured on the GPU path.
+Each wrapper names the C function (and through it the reference file:line) it calls.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "libava_oracle.so")
+_lib = None
+
+f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc; no GPU needed)."""
+    if force or not os.path.exists(_LIB):
+        subprocess.run(["make", "-s", "-B" if force else "all"], cwd=_HERE, check=True)
+    return _LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = C.CDLL(_LIB)
+        L.orc_quantize_int8.argtypes = [f32p, C.c_int, C.c_int, i8p, f32p]
+        L.orc_q8_matmul_ref.argtypes = [f32p, C.c_int, C.c_int, i8p, f32p, C.c_int, f32p, C.c_int]
+        L.orc_quant_planes.argtypes = [f32p, C.c_int, C.c_int, C.c_int, i8p, i32p]
+        L.orc_q8_acc.argtypes = [i8p, C.c_int, C.c_int, i8p, C.c_int, i32p, C.c_int]
+        L.orc_q8_combine.argtypes = [i32p, C.c_int, C.c_void_p, C.c_int, f32p, C.c_int, f32p]
+        L.orc_q8_matmul_planes.argtypes = [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_int, f32p, C.c_int]
+        L.orc_lif_scan.argtypes = [f32p, C.c_int, C.c_int, C.c_int, f32p, f32p, f32p, f32p,
+                                   C.c_int, C.c_int, C.c_int, i8p]
+        L.orc_kwta.argtypes = [f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p]
+        L.orc_mem_rec.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_float, C.c_float, f32p, C.c_void_p, f32p]
+        L.orc_mem_rec_f64.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_double, f64p, C.c_void_p, f64p]
+        L.orc_rmsnorm.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p]
+        L.orc_sigmoid.argtypes = [C.c_float]
+        L.orc_sigmoid.restype = C.c_float
+        L.orc_log_sigmoid.argtypes = [C.c_float]
+        L.orc_log_sigmoid.restype = C.c_float
+        L.orc_model_forward.restype = C.c_int
+        L.orc_model_forward.argtypes = [C.POINTER(_Cfg), C.POINTER(_Model), C.c_void_p, C.c_int, C.c_int,
+                                        C.POINTER(_State), C.c_void_p, C.c_int, C.c_int, C.POINTER(_Trace)]
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+# --------------------------------------------------------------------------- int8 products
+
+def quantize_int8(w):
+    """parts/src/quant.rs:18-31 -> (q int8 [din, dout], scale f32 [dout])."""
+    w = _c(w, np.float32)
+    din, dout = w.shape
+    q = np.empty((din, dout), np.int8)
+    s = np.empty(dout, np.float32)
+    lib().orc_quantize_int8(w, din, dout, q, s)
+    return q, s
+
+
+def q8_matmul_ref(x, q, scale, threads=1):
+    """gpu/int8.rs:301-331: W8A32, f32 fma chain in j order, times the column scale."""
+    x = _c(x, np.float32)
+    m, din = x.shape
+    dout = q.shape[1]
+    y = np.empty((m, dout), np.float32)
+    lib().orc_q8_matmul_ref(x, m, din, _c(q, np.int8), _c(scale, np.float32), dout, y, threads)
+    return y
+
+
+def quant_planes(x, planes):
+    x = _c(x, np.float32)
+    m, k = x.shape
+    xq = np.empty((planes, m, k), np.int8)
+    xe = np.empty(m, np.int32)
+    lib().orc_quant_planes(x, m, k, planes, xq, xe)
+    return xq, xe
+
+
+def q8_acc(a, q, threads=1):
+    a = _c(a, np.int8)
+    m, k = a.shape
+    n = q.shape[1]
+    acc = np.empty((m, n), np.int32)
+    lib().orc_q8_acc(a, m, k, _c(q, np.int8), n, acc, threads)
+    return acc
+
+
+def q8_combine(acc, xexp, scale):
+    acc = _c(acc, np.int32)
+    planes, m, n = acc.shape
+    y = np.empty((m, n), np.float32)
+    xe = None if xexp is None else _c(xexp, np.int32)
+    lib().orc_q8_combine(acc, planes, None if xe is None else xe.ctypes.data, m, _c(scale, np.float32), n, y)
+    return y
+
+
+def q8_matmul_planes(x, planes, q, scale, threads=1):
+    x = _c(x, np.float32)
+    m, k = x.shape
+    n = q.shape[1]
+    y = np.empty((m, n), np.float32)
+    lib().orc_q8_matmul_planes(x, m, k, planes, _c(q, np.int8), _c(scale, np.float32), n, y, threads)
+    return y
+
+
+# --------------------------------------------------------------------------- LIF, kWTA, memory
+
+def lif_scan(cur, ps, v0=None, s0=None, a0=None, levels=2, signed=True, alif=True):
+    """gpu/lif_gen.rs:151-214. cur [B, T, D]; ps [4D] = beta|theta|rho|gain.
+    Returns (spikes int8 [B, T, D], v [B, D], s [B, D], a [B, D])."""
+    cur = _c(cur, np.float32)
+    B, T, D = cur.shape
+    v = np.zeros((B, D), np.float32) if v0 is None else _c(v0, np.float32).copy()
+    s = np.zeros((B, D), np.float32) if s0 is None else _c(s0, np.float32).copy()
+    a = np.zeros((B, D), np.float32) if a0 is None else _c(a0, np.float32).copy()
+    spk = np.empty((B, T, D), np.int8)
+    lib().orc_lif_scan(cur, B, T, D, _c(ps, np.float32), v, s, a, levels, int(signed), int(alif), spk)
+    return spk, v, s, a
+
+
+def kwta(u, k, relu2=True):
+    """gpu/model/fstep.rs:295-299 + fstep/arch.rs:976-989 -> (a [n, h], kth [n])."""
+    u = _c(u, np.float32)
+    n, h = u.shape
+    a = np.empty((n, h), np.float32)
+    kth = np.empty(n, np.float32)
+    lib().orc_kwta(u, n, h, k, int(relu2), a, kth)
+    return a, kth
+
+
+def mem_rec(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
+    """gpu/mem_gen.rs:220-273. q, k, e, v [BH, T, hs]; la, b [BH, T, g]. Returns (y, F, S)."""
+    q, k, e, v, la, b = (_c(z, np.float32) for z in (q, k, e, v, la, b))
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    F = np.zeros((BH, hs, hs), np.float32) if F is None else _c(F, np.float32).copy()
+    S = np.zeros((BH, hs, hs), np.float32) if S is None else _c(S, np.float32).copy()
+    y = np.empty((BH, T, hs), np.float32)
+    lib().orc_mem_rec(q, k, e, v, la, b, BH, T, hs, g, float(m), float(cap), F,
+                      S.ctypes.data if m != 0.0 else None, y)
+    return y, F, S
+
+
+def mem_rec_f64(q, k, e, v, la, b, m=0.0, F=None, S=None):
+    q, k, e, v, la, b = (_c(z, np.float32) for z in (q, k, e, v, la, b))
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    F = np.zeros((BH, hs, hs), np.float64) if F is None else _c(F, np.float64).copy()
+    S = np.zeros((BH, hs, hs), np.float64) if S is None else _c(S, np.float64).copy()
+    y = np.empty((BH, T, hs), np.float64)
+    lib().orc_mem_rec_f64(q, k, e, v, la, b, BH, T, hs, g, float(m), F,
+                          S.ctypes.data if m != 0.0 else None, y)
+    return y, F, S
+
+
+def rmsnorm(x, gain):
+    x = _c(x, np.float32)
+    n, d = x.shape
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(x, n, d, _c(gain, np.float32), out)
+    return out
+
+
+def sigmoid(x):
+    return np.float32(lib().orc_sigmoid(float(x)))
+
+
+def log_sigmoid(x):
+    return np.float32(lib().orc_log_sigmoid(float(x)))
+
+
+# --------------------------------------------------------------------------- model
+
+class _QW(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("scale", C.c_void_p), ("din", C.c_int), ("dout", C.c_int)]
+
+
+_BLOCK_F32 = ["lif_norm", "beta_p", "theta", "arho", "again", "mem_norm", "wa", "ba", "wb", "bb", "off",
+              "wa1", "wa2", "wb1", "wb2", "vres", "eng_norm", "mlp_norm", "dense"]
+_BLOCK_Q8 = ["win", "wout", "wq", "wk", "wv", "we", "wg", "wo", "ewq", "ewk", "ewv", "ewo", "w1", "w2"]
+
+
+class _Block(C.Structure):
+    _fields_ = [("lif_norm", C.c_void_p), ("win", _QW), ("beta_p", C.c_void_p), ("theta", C.c_void_p),
+                ("arho", C.c_void_p), ("again", C.c_void_p), ("wout", _QW), ("mem_norm", C.c_void_p),
+                ("wq", _QW), ("wk", _QW), ("wv", _QW), ("we", _QW), ("wg", _QW), ("wo", _QW),
+                ("wa", C.c_void_p), ("ba", C.c_void_p), ("wb", C.c_void_p), ("bb", C.c_void_p),
+                ("off", C.c_void_p), ("wa1", C.c_void_p), ("wa2", C.c_void_p), ("wb1", C.c_void_p),
+                ("wb2", C.c_void_p), ("vres", C.c_void_p), ("eng_norm", C.c_void_p),
+                ("ewq", _QW), ("ewk", _QW), ("ewv", _QW), ("ewo", _QW), ("mlp_norm", C.c_void_p),
+                ("w1", _QW), ("w2", _QW), ("dense", C.c_void_p)]
+
+
+class _Cfg(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab", "d", "layers", "hidden", "kwta_k", "heads", "head_size",
+                                       "gate_rank", "eng_block", "eng_dim", "levels", "alif", "lif_scale",
+                                       "value_residual", "dense", "relu2")] + \
+               [("momentum", C.c_float), ("cap", C.c_float)]
+
+
+class _Model(C.Structure):
+    _fields_ = [("tok_emb", C.c_void_p), ("head", _QW), ("final_norm", C.c_void_p), ("blocks", C.POINTER(_Block))]
+
+
+class _State(C.Structure):
+    _fields_ = [("lif_v", C.c_void_p), ("lif_s", C.c_void_p), ("lif_a", C.c_void_p), ("mem_f", C.c_void_p),
+                ("mem_s", C.c_void_p), ("eng_k", C.c_void_p), ("eng_v", C.c_void_p), ("eng_cap", C.c_int),
+                ("eng_len", C.c_int)]
+
+
+class _Trace(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("spikes", "cur", "u", "kth", "memy", "x", "hf")]
+
+
+class OracleModel:
+    """The oracle's view of a model: f32 weights (a dict from ava_amd.synth) with their int8 copies
+    made by orc_quantize_int8, as Model::set_int8 does (gpu/model.rs:949-991)."""
+
+    def __init__(self, cfg: dict, params: dict):
+        self.cfg = dict(cfg)
+        self.params = params
+        self._keep = []
+        L = cfg["layers"]
+        self.q8 = {}
+        blocks = (_Block * L)()
+        for i in range(L):
+            bp = params["blocks"][i]
+            blk = blocks[i]
+            for name in _BLOCK_F32:
+                if name in bp and bp[name] is not None:
+                    setattr(blk, name, self._ptr(bp[name]))
+            for name in _BLOCK_Q8:
+                if name in bp and bp[name] is not None:
+                    setattr(blk, name, self._qw(bp[name]))
+        self.blocks = blocks
+        self.model = _Model(tok_emb=self._ptr(params["tok_emb"]),
+                            head=self._qw(np.ascontiguousarray(params["tok_emb"].T)),
+                            final_norm=self._ptr(params["final_norm"]),
+                            blocks=C.cast(blocks, C.POINTER(_Block)))
+        c = self.cfg
+        self.ccfg = _Cfg(vocab=c["vocab"], d=c["d"], layers=L, hidden=c["hidden"], kwta_k=c["kwta_k"],
+                         heads=c["d"] // c["head_size"], head_size=c["head_size"], gate_rank=c["gate_rank"],
+                         eng_block=c["eng_block"], eng_dim=c["eng_dim"], levels=c["levels"],
+                         alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
+                         value_residual=int(c["value_residual"]), dense=int(c["dense"]),
+                         relu2=int(c["relu2"]), momentum=c["momentum"], cap=c["cap"])
+
+    def _ptr(self, a):
+        a = _c(a, np.float32)
+        self._keep.append(a)
+        return a.ctypes.data
+
+    def _qw(self, w):
+        q, s = quantize_int8(w)
+        self._keep += [q, s]
+        self.q8[id(w)] = (q, s)
+        return _QW(q=q.ctypes.data, scale=s.ctypes.data, din=w.shape[0], dout=w.shape[1])
+
+    def new_state(self, B, eng_cap=0):
+        c = self.cfg
+        L, d, hs = c["layers"], c["d"], c["head_size"]
+        nh = d // hs
+        de = c["eng_dim"]
+        st = {
+            "lif_v": np.zeros((L, B, d), np.float32), "lif_s": np.zeros((L, B, d), np.float32),
+            "lif_a": np.zeros((L, B, d), np.float32),
+            "mem_f": np.zeros((L, B, nh, hs, hs), np.float32), "mem_s": np.zeros((L, B, nh, hs, hs), np.float32),
+            "eng_k": np.zeros((B, max(eng_cap, 1), de), np.float32),
+            "eng_v": np.zeros((B, max(eng_cap, 1), de), np.float32),
+            "eng_cap": eng_cap, "eng_len": 0,
+        }
+        return st
+
+    def forward(self, ids, state=None, planes=0, threads=1, trace=False, logits=True):
+        """gpu/arch.rs:1407 forward_arch / gpu/state.rs:684 forward_with_state. ids [B, T]."""
+        ids = _c(ids, np.int32)
+        B, T = ids.shape
+        c = self.cfg
+        if state is None:
+            state = self.new_state(B, eng_cap=T if c["eng_block"] >= 0 else 0)
+        cst = _State(**{k: state[k].ctypes.data for k in ("lif_v", "lif_s", "lif_a", "mem_f", "mem_s",
+                                                         "eng_k", "eng_v")},
+                     eng_cap=state["eng_cap"], eng_len=state["eng_len"])
+        N = B * T
+        out = np.empty((N, c["vocab"]), np.float32) if logits else None
+        tr = None
+        trd = {}
+        if trace:
+            L, d, H = c["layers"], c["d"], c["hidden"]
+            trd = {"spikes": np.empty((L, N, d), np.int8), "cur": np.empty((L, N, d), np.float32),
+                   "u": np.empty((L, N, H), np.float32), "kth": np.empty((L, N), np.float32),
+                   "memy": np.empty((L, N, d), np.float32), "x": np.empty((L, N, d), np.float32),
+                   "hf": np.empty((N, d), np.float32)}
+            tr = _Trace(**{k: v.ctypes.data for k, v in trd.items()})
+        rc = lib().orc_model_forward(C.byref(self.ccfg), C.byref(self.model), ids.ctypes.data, B, T,
+                                     C.byref(cst), None if out is None else out.ctypes.data, planes, threads,
+                                     None if tr is None else C.byref(tr))
+        if rc != 0:
+            raise RuntimeError(f"orc_model_forward failed ({rc})")
+        state["eng_len"] = cst.eng_len
+        return out, state, trd
