@@ -359,3 +359,10 @@ extern "C" int ava_q8_matmul(const float *x, int m, const ava_qw *w, int planes,
 extern "C" int ava_q8_matmul_i8(const int8_t *s, int m, const ava_qw *w, float *y, ava_stream stream) {
     return ava::q8_gemm(s, nullptr, 1, m, w, EPI_STORE, y, w ? w->dout : 0, nullptr, (hipStream_t)stream);
 }
+
+extern "C" int ava_q8_matmul_planes(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w,
+                                    float *y, ava_stream stream) {
+    AVA_REQUIRE(xexp, AVA_ERR_ARG, "q8_matmul_planes: NULL row exponents");
+    AVA_REQUIRE(m >= 0, AVA_ERR_SHAPE, "q8_matmul_planes: m=%d", m);
+    return ava::q8_gemm(xq, xexp, planes, m, w, EPI_STORE, y, w ? w->dout : 0, nullptr, (hipStream_t)stream);
+}

@@ -1,0 +1,335 @@
+"""Benchmark of the int8 block-stack forward path on one MI355X (prints ONE JSON line).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+Workloads:
+    stack   config[3]: the Ava-0.4-shaped int8 block stack, teacher-forced, B=64, T=2048, d=1024
+    lif     config[1]: the standalone LIF scan, B=64, T=2048, C=2048
+    delta   config[2]: the plain delta rule, chunked, B=32, H=8, T=4096, d=64
+    kwta    the kWTA + relu2 of config[3]'s wide layer (131072 rows of 4096, k=1024)
+    gemm    one config[3] dense int8 product (131072 x 1024 x 4096)
+    copy    a plain device copy of 1 GiB (the traffic-counter calibration kernel)
+
+A "step" is one pass of the path over one batch of synthetic input resident in HBM. The timed
+region is K steps between two synchronisations; the dominant kernel's average duration comes from
+HIP events recorded on the stream the kernels are launched on (torch's current stream, which is the
+stream every ava_* call receives). The CPU baseline is the oracle (a C restatement of the
+reference's CPU loops) timed on a bounded sample on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "tokens/sec int8 block-stack forward @B=64,T=2048, 1 GPU; % HBM / MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+I8_PEAK_TOPS = 5000.0  # dense int8 MFMA, TOP/s
+FP32_PEAK_TFLOPS = 157.3
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+# ----------------------------------------------------------------------------- workloads
+
+
+class Lif:
+    """config[1]: cur ~N(0,1) [64, 2048, 2048]; beta = sigmoid(U(1.5, 4.5)); theta 1, rho 0.95,
+    gain 0.05; int2 spikes, subtract reset; outputs int8 spikes, final v and theta."""
+
+    name = "lif"
+    kernel = "lif_scan_kernel"
+
+    def __init__(self, B=64, T=2048, D=2048):
+        import torch
+        from ava_amd import _lib
+
+        self.B, self.T, self.D = B, T, D
+        self.L = _lib.lib()
+        g = torch.Generator(device="cuda").manual_seed(1)
+        self.cur = torch.randn((B, T, D), device="cuda", generator=g, dtype=torch.float32)
+        beta = torch.sigmoid(torch.rand(D, device="cuda", generator=g) * 3.0 + 1.5)
+        self.ps = torch.cat([beta, torch.ones(D, device="cuda"), torch.full((D,), 0.95, device="cuda"),
+                             torch.full((D,), 0.05, device="cuda")]).contiguous()
+        self.v = torch.zeros((B, D), device="cuda")
+        self.s = torch.zeros((B, D), device="cuda")
+        self.a = torch.zeros((B, D), device="cuda")
+        self.th = torch.empty((B, D), device="cuda")
+        self.spikes = torch.empty((B, T, D), dtype=torch.int8, device="cuda")
+        self.tokens = B * T
+        # algorithmic bytes: read cur, write spikes, write v_T and theta_T, read the 4 parameter rows
+        self.bytes = B * T * D * (4 + 1) + B * D * (4 + 4) + 4 * D * 4
+        self.config = {"workload": "lif_scan config[1]", "B": B, "T": T, "C": D, "spikes": "int2",
+                       "alif": True, "rho": 0.95, "gain": 0.05}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        from ava_amd._lib import check
+        import ctypes as C
+
+        # the state carries over from step to step (a stream read in pieces, state.rs:4-12)
+        if ev: ev[0].record()
+        check(self.L.ava_lif_scan(C.c_void_p(self.cur.data_ptr()), self.B, self.T, self.D,
+                                  C.c_void_p(self.ps.data_ptr()), C.c_void_p(self.v.data_ptr()),
+                                  C.c_void_p(self.s.data_ptr()), C.c_void_p(self.a.data_ptr()), 2, 1, 1,
+                                  C.c_void_p(self.spikes.data_ptr()), C.c_void_p(self.th.data_ptr()), stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.bytes / kernel_s / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        B = 32
+        rng = np.random.default_rng(1)
+        cur = rng.standard_normal((B, self.T, self.D), dtype=np.float32)
+        beta = (1.0 / (1.0 + np.exp(-rng.uniform(1.5, 4.5, self.D)))).astype(np.float32)
+        ps = np.concatenate([beta, np.ones(self.D), np.full(self.D, 0.95), np.full(self.D, 0.05)]).astype(np.float32)
+        t0 = time.perf_counter()
+        O.lif_scan(cur, ps, levels=2, signed=True, alif=True)
+        dt = time.perf_counter() - t0
+        return {"value": B * self.T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"oracle lif_scan (the reference's lif_gen.rs:191-214 loop), B={B} of 64, "
+                          f"T={self.T}, C={self.D}, one thread, {dt:.2f} s"}
+
+
+class Kwta:
+    """kWTA + relu2 over config[3]'s wide layer: u [131072, 4096] ~N(0,1), k = 1024."""
+
+    name = "kwta"
+    kernel = "kwta_kernel"
+
+    def __init__(self, n=131072, h=4096, k=1024):
+        import torch
+        from ava_amd import _lib
+
+        self.n, self.h, self.k = n, h, k
+        self.L = _lib.lib()
+        g = torch.Generator(device="cuda").manual_seed(2)
+        self.u = torch.randn((n, h), device="cuda", generator=g)
+        self.a = torch.empty_like(self.u)
+        self.kth = torch.empty(n, device="cuda")
+        self.tokens = n
+        self.bytes = n * h * 8 + n * 4
+        self.config = {"workload": "kwta_relu2 config[3] wide layer", "rows": n, "H": h, "k": k}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        from ava_amd._lib import check
+        import ctypes as C
+
+        if ev: ev[0].record()
+        check(self.L.ava_kwta(C.c_void_p(self.u.data_ptr()), self.n, self.h, self.k, 1,
+                              C.c_void_p(self.a.data_ptr()), C.c_void_p(self.kth.data_ptr()), stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.bytes / kernel_s / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        rows = 2048
+        u = np.random.default_rng(2).standard_normal((rows, self.h)).astype(np.float32)
+        t0 = time.perf_counter()
+        O.kwta(u, self.k, True)
+        dt = time.perf_counter() - t0
+        return {"value": rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"oracle kwta (sort per row, lif.rs:248-263), {rows} rows of {self.h}, {dt:.2f} s"}
+
+
+class Gemm:
+    """One dense int8 product of config[3]: x [131072, 1024] f32 -> 3 planes -> i8 MFMA -> y [131072, 4096]."""
+
+    name = "gemm"
+    kernel = "q8_gemm_kernel"
+
+    def __init__(self, m=131072, k=1024, n=4096, planes=3):
+        import torch
+        from ava_amd import ops
+
+        self.m, self.k, self.n, self.planes = m, k, n, planes
+        g = torch.Generator(device="cuda").manual_seed(3)
+        w = torch.randn((k, n), device="cuda", generator=g) * 0.02
+        self.qw = ops.QW.from_tensor(w)
+        self.x = torch.randn((m, k), device="cuda", generator=g)
+        self.xq, self.xe = ops.quant_rows(self.x, planes)
+        self.y = torch.empty((m, n), device="cuda")
+        self.tokens = m
+        self.ops = 2.0 * m * k * n * planes  # int8 OPs per launch
+        self.config = {"workload": "q8 product config[3] W1", "m": m, "k": k, "n": n, "planes": planes}
+        self.dtype = "i8"
+
+    def step(self, stream, ev=None):
+        import ctypes as C
+        from ava_amd import _lib
+
+        L = _lib.lib()
+        _lib.check(L.ava_q8_quant_rows(C.c_void_p(self.x.data_ptr()), self.m, self.k, self.planes,
+                                       C.c_void_p(self.xq.data_ptr()), C.c_void_p(self.xe.data_ptr()), stream))
+        if ev: ev[0].record()
+        _lib.check(L.ava_q8_matmul_planes(C.c_void_p(self.xq.data_ptr()), C.c_void_p(self.xe.data_ptr()),
+                                          self.planes, self.m, C.byref(self.qw.c), C.c_void_p(self.y.data_ptr()),
+                                          stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.ops / kernel_s / 1e12
+        return {"bound": "mfma", "achieved": a, "peak": I8_PEAK_TOPS, "unit": "TOP/s", "frac": a / I8_PEAK_TOPS}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        rows = 48
+        rng = np.random.default_rng(3)
+        x = rng.standard_normal((rows, self.k)).astype(np.float32)
+        q, s = O.quantize_int8((rng.standard_normal((self.k, self.n)) * 0.02).astype(np.float32))
+        th = cpu_threads()
+        t0 = time.perf_counter()
+        O.q8_matmul_ref(x, q, s, threads=th)
+        dt = time.perf_counter() - t0
+        return {"value": rows / dt, "unit": "rows/s", "cores": th, "kind": "port",
+                "sample": f"oracle W8A32 product (int8.rs:301-331 fma chain), {rows} rows, {dt:.2f} s"}
+
+
+class Copy:
+    """A plain 1 GiB device-to-device copy: the calibration kernel for the FETCH/WRITE_SIZE counters."""
+
+    name = "copy"
+    kernel = "copy"
+
+    def __init__(self, nbytes=1 << 30):
+        import torch
+
+        self.src = torch.ones(nbytes // 4, device="cuda")
+        self.dst = torch.empty_like(self.src)
+        self.tokens = 1
+        self.bytes = 2 * nbytes
+        self.config = {"workload": "device copy calibration", "bytes": nbytes}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        if ev: ev[0].record()
+        self.dst.copy_(self.src)
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.bytes / kernel_s / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS}
+
+    def cpu_baseline(self):
+        return None
+
+
+WORKLOADS = {"lif": Lif, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
+DEFAULT = "lif"
+
+
+def extra_workloads():
+    """Workloads whose library parts may not be built yet register themselves here."""
+    try:
+        from ava_amd import bench_workloads
+
+        WORKLOADS.update(bench_workloads.WORKLOADS)
+        return bench_workloads.DEFAULT
+    except ImportError:
+        return DEFAULT
+
+
+# ----------------------------------------------------------------------------- main
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (every path shards with no exchange; "
+              "see the sharding paragraph of the design notes); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    default = extra_workloads()
+    wname = args.workload or default
+    W = WORKLOADS[wname]()
+    stream = torch.cuda.current_stream()
+    sptr = __import__("ctypes").c_void_p(stream.cuda_stream)
+
+    log(f"bench: workload={wname} warmup={args.warmup} steps={args.steps}")
+    for _ in range(args.warmup):
+        W.step(sptr)
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        W.step(sptr, ev[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # the dominant kernel's launches: one event pair per step, or the workload's own launch timer
+    kernel_ms = W.kernel_ms() if hasattr(W, "kernel_ms") else [a.elapsed_time(b) for a, b in ev]
+    ms_per_step = wall * 1e3 / args.steps
+    value = W.tokens * args.steps / wall
+    kern_s = float(np.mean(kernel_ms)) / 1e3
+    roof = W.roofline(kern_s)
+    roof["kernel"] = W.kernel
+    roof["kernel_avg_us"] = kern_s * 1e6
+    roof["traffic"] = getattr(W, "traffic", None)
+
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        cpu = W.cpu_baseline()
+
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": W.dtype,
+        "data": "synthetic (seeded random inputs and random-init weights)",
+        "config": W.config,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    if hasattr(W, "extra"):
+        out.update(W.extra())
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

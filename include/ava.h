@@ -76,6 +76,12 @@ size_t ava_q8_workspace(int m, int k, int planes);
 int ava_q8_matmul(const float *x, int m, const ava_qw *w, int planes, float *y, void *ws,
                   size_t ws_bytes, ava_stream stream);
 
+/* y [m][dout] from activations already in split-plane form (xq [planes][m][ldk], xexp [m], as
+ * ava_q8_quant_rows writes them): the product and combine of ava_q8_matmul without the quantizer.
+ * Replaces int8::mm (int8.rs:672-683) where the producer of x writes planes directly. */
+int ava_q8_matmul_planes(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w,
+                         float *y, ava_stream stream);
+
 /* y [m][dout] = s [m][ldk] · W for integer inputs (the LIF's spikes, -2..2; padding columns 0):
  * y = (float)acc · scale_c, the reference's bits exactly (its f32 sum of integer products is
  * exact). Replaces int8::mm on the spikes (arch.rs:1695, fstep/arch.rs:675). */
