@@ -90,6 +90,11 @@ def lib():
     if hasattr(L, "ava_model_scratch_bytes"):
         L.ava_model_scratch_bytes.argtypes = [vp]
         L.ava_model_scratch_bytes.restype = sz
+    if hasattr(L, "ava_model_set_timing"):
+        L.ava_model_set_timing.argtypes = [vp, i32]
+        L.ava_model_set_timing.restype = i32
+        L.ava_model_timing.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_double), i32, i32]
+        L.ava_model_timing.restype = i32
     _lib = L
     return L
 

@@ -88,4 +88,32 @@ __device__ __forceinline__ float wave_sum(float v) {
 int launch_quant_rows(const float *x, int m, int k, int ldx, int planes, int8_t *xq, int32_t *xexp,
                       hipStream_t st);
 
+// q8.hip: the i8 MFMA product with an epilogue (kind 1 store, 2 times colv[col], 3 accumulate into y).
+enum { Q8_STORE = 1, Q8_MUL = 2, Q8_ADD = 3 };
+int q8_gemm(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w, int kind, float *y, int ldy,
+            const float *colv, hipStream_t st);
+
+// lif.hip / kwta.hip / mem.hip
+int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
+                   int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf, hipStream_t st);
+int kwta_planes(const float *u, int n, int h, int k, int relu2, int planes, int8_t *xq, int32_t *xexp, int ldq,
+                float *kth, hipStream_t st);
+int mem_scan_strided(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,
+                     int B, int T, int nh, int ld, int g, int ldg, float m, float cap, float *F, float *S, float *y,
+                     int ldy, hipStream_t st);
+
+// glue.hip
+int embed(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, hipStream_t st);
+int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
+               float *hout, hipStream_t st);
+int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st);
+int mem_prep(float *P, const float *G, int n, int d, int nh, int r, const float *ba, const float *bb, const float *off,
+             const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out, float *la, float *b,
+             hipStream_t st);
+int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, int8_t *xq, int32_t *xexp, int ldq,
+             hipStream_t st);
+int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,
+                hipStream_t st);
+int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st);
+
 }  // namespace ava

@@ -1,0 +1,206 @@
+// The general fast-weight (delta-rule) memory recurrence for gfx950, one workgroup per head.
+//
+// Per head, F [64][64] (row i = key channel, column j = value channel) and the momentum S live in
+// registers for the whole scan: 4 waves, wave w owns columns 16w..16w+15; lane l of a wave owns
+// column 16w + (l & 15) and the 16 rows 16(l >> 4)..+15, so the column reductions
+// r_j = sum_i e_i F_ij and y_j = sum_i q_i F_ij are 16 register FMAs plus two lane exchanges inside
+// the wave (no LDS, no barrier per step). Per step and element:
+//   u_ij = (b_i k_i) v_j - (a_i b_i e_i) r_j;  S <- M S + u;  F <- clamp(a_i F + S, +-cap)  (M = 0: F <- clamp(a_i F + u))
+// then y_j = sum_i q_i F_ij (the read after the write), as gpu/mem_gen.rs:220-246 / gpu/arch.rs:1091-1136.
+//
+// Inputs are staged through LDS 16 time steps at a time: one cooperative, coalesced load of
+// q, k, e, v and the gates per chunk (the next chunk's loads are in flight while this chunk is
+// scanned), with the per-row factors a_i = exp(la_i), b_i k_i and a_i b_i e_i formed once per
+// (step, row) at staging. The read-outs y are gathered in LDS and written once per chunk.
+//
+// Layout: head bh = (b, h) with b = bh / nh, h = bh % nh reads row (b T + t) of a [B T][ld] matrix at
+// columns 64h..64h+63 (ld = 64, nh = 1 is the [BH][T][64] layout of the C ABI; ld = d, nh = d / 64 is
+// the block stack's [B T][d] projection output, read in place). Per-head gates (G1) are one value
+// per (row, head) at column h of a [B T][ldg] matrix.
+#include "common.h"
+
+namespace {
+
+constexpr int HS = 64, TS = 16;
+
+struct MemArgs {
+    const float *q, *k, *e, *v, *la, *b;
+    int T, nh, ld, ldg, ldy;
+    float m, cap;
+    float *F, *S, *y;
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool G1, bool MOM>
+__global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
+    __shared__ __attribute__((aligned(16))) float s_q[TS][HS], s_e[TS][HS], s_v[TS][HS];
+    __shared__ __attribute__((aligned(16))) float s_a[TS][HS], s_bk[TS][HS], s_abe[TS][HS];
+    __shared__ __attribute__((aligned(16))) float s_y[TS][HS];
+
+    const int bh = blockIdx.x;
+    const int bi = bh / p.nh, hh = bh - bi * p.nh;
+    const size_t base = (size_t)bi * p.T * p.ld + (size_t)hh * HS;
+    const size_t gbase = G1 ? (size_t)bi * p.T * p.ldg + hh : (size_t)bi * p.T * p.ldg + (size_t)hh * HS;
+    const size_t ybase = (size_t)bi * p.T * p.ldy + (size_t)hh * HS;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = wave * 16 + (lane & 15);  // this lane's column
+    const int i0 = (lane >> 4) * 16;        // this lane's first row
+
+    float Fr[16], Sr[16];
+    float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+        Fr[m] = Fh[(i0 + m) * HS + j];
+        Sr[m] = MOM ? Sh[(i0 + m) * HS + j] : 0.0f;
+    }
+
+    // staging: thread -> (step st, rows si..si+3)
+    const int st = tid >> 4, si = (tid & 15) * 4;
+    f32x4 rq, rk, re, rv, rla, rb;
+    auto load = [&](int t0) {
+        const int t = t0 + st;
+        if (t < p.T) {
+            const size_t o = base + (size_t)t * p.ld + si;
+            rq = *reinterpret_cast<const f32x4 *>(p.q + o);
+            rk = *reinterpret_cast<const f32x4 *>(p.k + o);
+            re = *reinterpret_cast<const f32x4 *>(p.e + o);
+            rv = *reinterpret_cast<const f32x4 *>(p.v + o);
+            if (G1) {
+                const float l = p.la[gbase + (size_t)t * p.ldg], b = p.b[gbase + (size_t)t * p.ldg];
+                rla = f32x4{l, l, l, l};
+                rb = f32x4{b, b, b, b};
+            } else {
+                const size_t og = gbase + (size_t)t * p.ldg + si;
+                rla = *reinterpret_cast<const f32x4 *>(p.la + og);
+                rb = *reinterpret_cast<const f32x4 *>(p.b + og);
+            }
+        } else {
+            rq = rk = re = rv = rla = rb = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    auto stage = [&]() {
+        f32x4 a, bk, abe;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            a[c] = expf(rla[c]);
+            bk[c] = rb[c] * rk[c];
+            abe[c] = (a[c] * rb[c]) * re[c];
+        }
+        *reinterpret_cast<f32x4 *>(&s_q[st][si]) = rq;
+        *reinterpret_cast<f32x4 *>(&s_e[st][si]) = re;
+        *reinterpret_cast<f32x4 *>(&s_v[st][si]) = rv;
+        *reinterpret_cast<f32x4 *>(&s_a[st][si]) = a;
+        *reinterpret_cast<f32x4 *>(&s_bk[st][si]) = bk;
+        *reinterpret_cast<f32x4 *>(&s_abe[st][si]) = abe;
+    };
+
+    const float M = p.m, cap = p.cap;
+    load(0);
+    for (int t0 = 0; t0 < p.T; t0 += TS) {
+        __syncthreads();  // the previous chunk's LDS reads (and y writes-out) are done
+        stage();
+        __syncthreads();
+        if (t0 + TS < p.T) load(t0 + TS);  // in flight during this chunk's scan
+        const int n = min(TS, p.T - t0);
+        for (int s = 0; s < n; s++) {
+            float ev[16], qv[16], av[16], bkv[16], abev[16];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&s_e[s][i0 + 4 * c]);
+                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&s_q[s][i0 + 4 * c]);
+                const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&s_a[s][i0 + 4 * c]);
+                const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&s_bk[s][i0 + 4 * c]);
+                const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&s_abe[s][i0 + 4 * c]);
+#pragma unroll
+                for (int z = 0; z < 4; z++) {
+                    ev[4 * c + z] = e4[z];
+                    qv[4 * c + z] = q4[z];
+                    av[4 * c + z] = a4[z];
+                    bkv[4 * c + z] = k4[z];
+                    abev[4 * c + z] = x4[z];
+                }
+            }
+            const float vj = s_v[s][j];
+            // r_j = sum_i e_i F_ij: two partial chains, then the four row groups of this column
+            float r0 = 0.0f, r1 = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 16; m += 2) {
+                r0 = fmaf(ev[m], Fr[m], r0);
+                r1 = fmaf(ev[m + 1], Fr[m + 1], r1);
+            }
+            float r = r0 + r1;
+            r += __shfl_xor(r, 16, 64);
+            r += __shfl_xor(r, 32, 64);
+            float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 16; m++) {
+                const float u = bkv[m] * vj - abev[m] * r;
+                float f;
+                if (MOM) {
+                    Sr[m] = fmaf(M, Sr[m], u);
+                    f = fmaf(av[m], Fr[m], Sr[m]);
+                } else {
+                    f = fmaf(av[m], Fr[m], u);
+                }
+                f = fminf(fmaxf(f, -cap), cap);
+                Fr[m] = f;
+                if (m & 1) y1 = fmaf(qv[m], f, y1);
+                else y0 = fmaf(qv[m], f, y0);
+            }
+            float y = y0 + y1;
+            y += __shfl_xor(y, 16, 64);
+            y += __shfl_xor(y, 32, 64);
+            if (lane < 16) s_y[s][j] = y;
+        }
+        __syncthreads();
+        // write the chunk's read-outs: thread -> (step st, columns si..si+3)
+        if (st < n) *reinterpret_cast<f32x4 *>(p.y + ybase + (size_t)(t0 + st) * p.ldy + si) =
+            *reinterpret_cast<const f32x4 *>(&s_y[st][si]);
+    }
+
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+        Fh[(i0 + m) * HS + j] = Fr[m];
+        if (MOM) Sh[(i0 + m) * HS + j] = Sr[m];
+    }
+}
+
+}  // namespace
+
+namespace ava {
+
+// The scan over heads laid out in a [B T][ld] matrix (see the file comment). g = 1 or 64 gate columns.
+int mem_scan_strided(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,
+                     int B, int T, int nh, int ld, int g, int ldg, float m, float cap, float *F, float *S, float *y,
+                     int ldy, hipStream_t st) {
+    AVA_REQUIRE(q && k && e && v && la && b && F && y, AVA_ERR_ARG, "mem_scan: NULL buffer");
+    AVA_REQUIRE(m == 0.0f || S, AVA_ERR_ARG, "mem_scan: momentum %g needs S", (double)m);
+    AVA_REQUIRE(g == 1 || g == HS, AVA_ERR_ARG, "mem_scan: gate width %d (1 or 64)", g);
+    AVA_REQUIRE(B >= 0 && T >= 0 && nh > 0 && ld % 4 == 0 && ldy % 4 == 0 && (g == 1 || ldg % 4 == 0), AVA_ERR_SHAPE,
+                "mem_scan: B=%d T=%d nh=%d ld=%d ldg=%d ldy=%d", B, T, nh, ld, ldg, ldy);
+    if (B == 0 || T == 0) return AVA_OK;
+    MemArgs a{q, k, e, v, la, b, T, nh, ld, ldg, ldy, m, cap, F, S, y};
+    dim3 grid(B * nh), block(256);
+    if (g == 1) {
+        if (m != 0.0f) mem_scan_kernel<true, true><<<grid, block, 0, st>>>(a);
+        else mem_scan_kernel<true, false><<<grid, block, 0, st>>>(a);
+    } else {
+        if (m != 0.0f) mem_scan_kernel<false, true><<<grid, block, 0, st>>>(a);
+        else mem_scan_kernel<false, false><<<grid, block, 0, st>>>(a);
+    }
+    AVA_LAUNCHED("mem_scan");
+    return AVA_OK;
+}
+
+}  // namespace ava
+
+extern "C" int ava_mem_scan(const float *q, const float *k, const float *e, const float *v, const float *la,
+                            const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,
+                            float *y, ava_stream stream) {
+    AVA_REQUIRE(hs == HS, AVA_ERR_UNSUPPORTED, "mem_scan: head size %d (this build runs 64)", hs);
+    AVA_REQUIRE(BH >= 0 && T >= 0, AVA_ERR_SHAPE, "mem_scan: BH=%d T=%d", BH, T);
+    // [BH][T][64]: one head per "batch row", time stride 64; gates [BH][T][g]
+    return ava::mem_scan_strided(q, k, e, v, la, b, BH, T, 1, HS, g, g, m, cap, F, S, y, HS, (hipStream_t)stream);
+}

@@ -1,0 +1,431 @@
+// The Ava-0.4-shaped int8 block stack on one GPU: weights, scratch and the per-block launch
+// sequence (include/ava.h: ava_model_*).
+//
+// Order of operations per block, as gpu/arch.rs:1592-1867 (block_arch) with carried state as
+// gpu/state.rs:870-1071 (block_state):
+//   spiking layer   h = rms(x) -> planes -> cur = (h.Win) (1 - beta) -> LIF scan -> x += s.Wout
+//   memory          h = rms(x) -> P = h.[Wq|Wk|Wv|We|Wg] (one product), G = h.[Wa|Wb|Wa1|Wb1] (f32)
+//                   -> prep (unit q, k, e; value residual; log alpha, b) -> scan -> head norm * silu(g)
+//                   -> x += o.Wo
+//   engram (one block)  h = rms(x) -> [q|k|v] -> append k, v to the store -> causal read -> x += o.Wo
+//   sparse MLP      h = rms(x) -> u = h.W1 -> kWTA, relu^2 -> planes -> x += a.W2
+//   dense mix       stream_{i+1} = x; x += sum_j w_j stream_j
+// then the final norm and the head (E^T in int8). Every product input is produced directly in
+// split-plane form by the kernel before it (RMSNorm, the read-out, kWTA), so no f32 activation is
+// written only to be re-read by a quantizer.
+#include <math.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace {
+
+struct DevQW {
+    ava_qw w{};
+};
+
+struct Block {
+    float *lif_norm = nullptr, *ps = nullptr, *omb = nullptr;
+    DevQW win, wout;
+    float *mem_norm = nullptr;
+    DevQW wproj;  // [Wq | Wk | Wv | We | Wg], d x 5d
+    float *wgate = nullptr;  // [Wa | Wb | Wa1 | Wb1], d x (2 nh + 2 r), f32
+    float *ba = nullptr, *bb = nullptr, *off = nullptr, *wa2 = nullptr, *wb2 = nullptr, *vres = nullptr;
+    DevQW wo;
+    bool eng = false;
+    float *eng_norm = nullptr;
+    DevQW eqkv, ewo;  // [Wq | Wk | Wv] d x 3de, Wo de x d
+    float *mlp_norm = nullptr;
+    DevQW w1, w2;
+    std::vector<float> dense;  // i + 2 mixing weights (host)
+};
+
+struct Timer {
+    std::vector<std::pair<const char *, std::pair<hipEvent_t, hipEvent_t>>> pending;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    struct Sum {
+        const char *name;  // the launch site's string literal
+        int calls;
+        double ms;
+    };
+    std::map<std::string, Sum> sums;
+};
+
+}  // namespace
+
+struct ava_model {
+    ava_config cfg{};
+    int device = 0;
+    float *tok_emb = nullptr, *final_norm = nullptr;
+    DevQW head;
+    std::vector<Block> blocks;
+    std::vector<void *> allocs;  // everything the model owns
+
+    // scratch for up to `rows` rows
+    size_t rows = 0, scratch_bytes = 0;
+    std::vector<void *> scratch;
+    float *x = nullptr, *h = nullptr, *cur = nullptr, *P = nullptr, *G = nullptr, *la = nullptr, *bw = nullptr;
+    float *y = nullptr, *v0 = nullptr, *u = nullptr, *qkv = nullptr, *eo = nullptr;
+    int8_t *xq = nullptr, *spk = nullptr;
+    int32_t *xexp = nullptr;
+    std::vector<float *> streams;
+
+    bool timing = false;
+    Timer timer;
+    hipStream_t last_stream = nullptr;
+};
+
+namespace {
+
+float sigmoid_host(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }  // gpu/model.rs:465-467
+
+int dev_alloc(ava_model *m, void **p, size_t bytes, bool scratch = false) {
+    AVA_HIP(hipMalloc(p, bytes < 256 ? 256 : bytes));
+    (scratch ? m->scratch : m->allocs).push_back(*p);
+    if (scratch) m->scratch_bytes += bytes;
+    return AVA_OK;
+}
+
+int upload(ava_model *m, float **dst, const float *src, size_t n) {
+    AVA_REQUIRE(src, AVA_ERR_ARG, "model: a required parameter is NULL");
+    if (int r = dev_alloc(m, (void **)dst, n * sizeof(float))) return r;
+    AVA_HIP(hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice));
+    return AVA_OK;
+}
+
+// Quantize host W [din][dout] (several matrices side by side: parts[i] is [din][cols[i]]) into one
+// int8 matrix; per-column scales make the merged product column-for-column the separate ones
+// (gpu/int8.rs:89-102, Q8Set::merged).
+int quantize(ava_model *m, DevQW *q, int din, const std::vector<std::pair<const float *, int>> &parts) {
+    int dout = 0;
+    for (auto &p : parts) {
+        AVA_REQUIRE(p.first, AVA_ERR_ARG, "model: a required weight matrix is NULL");
+        dout += p.second;
+    }
+    std::vector<float> w((size_t)din * dout);
+    int c0 = 0;
+    for (auto &p : parts) {
+        for (int j = 0; j < din; j++) memcpy(&w[(size_t)j * dout + c0], p.first + (size_t)j * p.second, sizeof(float) * p.second);
+        c0 += p.second;
+    }
+    float *wd = nullptr;
+    AVA_HIP(hipMalloc(&wd, w.size() * sizeof(float)));
+    AVA_HIP(hipMemcpy(wd, w.data(), w.size() * sizeof(float), hipMemcpyHostToDevice));
+    q->w.din = din;
+    q->w.dout = dout;
+    q->w.ldk = ava::q8_ldk(din);
+    int r = dev_alloc(m, (void **)&q->w.qt, (size_t)dout * q->w.ldk);
+    if (!r) r = dev_alloc(m, (void **)&q->w.scale, sizeof(float) * dout);
+    if (!r) r = ava_q8_pack(wd, din, dout, q->w.qt, q->w.scale, nullptr);
+    hipError_t e1 = hipDeviceSynchronize();
+    hipError_t e2 = hipFree(wd);
+    if (r) return r;
+    AVA_REQUIRE(e1 == hipSuccess && e2 == hipSuccess, AVA_ERR_HIP, "model: weight quantization failed: %s",
+                hipGetErrorString(e1 != hipSuccess ? e1 : e2));
+    return AVA_OK;
+}
+
+int build(ava_model *m, const ava_params *prm) {
+    const ava_config &c = m->cfg;
+    const int d = c.d, nh = d / c.head_size, r = c.gate_rank, de = c.eng_dim, H = c.hidden;
+    AVA_REQUIRE(prm && prm->blocks && prm->tok_emb && prm->final_norm, AVA_ERR_ARG, "model: NULL parameters");
+    if (int e = upload(m, &m->tok_emb, prm->tok_emb, (size_t)c.vocab * d)) return e;
+    if (int e = upload(m, &m->final_norm, prm->final_norm, d)) return e;
+    {
+        std::vector<float> et((size_t)d * c.vocab);  // E^T: one scale per vocab row (int8.rs:81-84)
+        for (int v = 0; v < c.vocab; v++)
+            for (int j = 0; j < d; j++) et[(size_t)j * c.vocab + v] = prm->tok_emb[(size_t)v * d + j];
+        if (int e = quantize(m, &m->head, d, {{et.data(), c.vocab}})) return e;
+    }
+    m->blocks.resize(c.layers);
+    for (int i = 0; i < c.layers; i++) {
+        const ava_block_params &p = prm->blocks[i];
+        Block &b = m->blocks[i];
+        int e = 0;
+        if ((e = upload(m, &b.lif_norm, p.lif_norm, d))) return e;
+        AVA_REQUIRE(p.beta_p && p.theta, AVA_ERR_ARG, "model: block %d has no LIF leak/threshold", i);
+        AVA_REQUIRE(!c.alif || (p.arho && p.again), AVA_ERR_ARG, "model: block %d: alif needs arho and again", i);
+        std::vector<float> ps(4 * (size_t)d), omb(d);
+        for (int k = 0; k < d; k++) {
+            const float beta = sigmoid_host(p.beta_p[k]);
+            ps[k] = beta;
+            ps[d + k] = p.theta[k];
+            ps[2 * d + k] = c.alif ? sigmoid_host(p.arho[k]) : 0.0f;
+            ps[3 * d + k] = c.alif ? p.again[k] : 0.0f;
+            omb[k] = beta * -1.0f + 1.0f;  // beta.affine(-1, 1) (arch.rs:1636-1638)
+        }
+        if ((e = upload(m, &b.ps, ps.data(), ps.size()))) return e;
+        if ((e = upload(m, &b.omb, omb.data(), omb.size()))) return e;
+        if ((e = quantize(m, &b.win, d, {{p.win, d}}))) return e;
+        if ((e = quantize(m, &b.wout, d, {{p.wout, d}}))) return e;
+        if ((e = upload(m, &b.mem_norm, p.mem_norm, d))) return e;
+        if ((e = quantize(m, &b.wproj, d, {{p.wq, d}, {p.wk, d}, {p.wv, d}, {p.we, d}, {p.wg, d}}))) return e;
+        {
+            const int nc = 2 * nh + 2 * r;
+            AVA_REQUIRE(p.wa && p.wb && p.wa1 && p.wb1, AVA_ERR_ARG, "model: block %d has no gate projections", i);
+            std::vector<float> wg((size_t)d * nc);
+            for (int j = 0; j < d; j++) {
+                float *row = &wg[(size_t)j * nc];
+                memcpy(row, p.wa + (size_t)j * nh, sizeof(float) * nh);
+                memcpy(row + nh, p.wb + (size_t)j * nh, sizeof(float) * nh);
+                memcpy(row + 2 * nh, p.wa1 + (size_t)j * r, sizeof(float) * r);
+                memcpy(row + 2 * nh + r, p.wb1 + (size_t)j * r, sizeof(float) * r);
+            }
+            if ((e = upload(m, &b.wgate, wg.data(), wg.size()))) return e;
+        }
+        if ((e = upload(m, &b.ba, p.ba, nh))) return e;
+        if ((e = upload(m, &b.bb, p.bb, nh))) return e;
+        if ((e = upload(m, &b.off, p.off, d))) return e;
+        if ((e = upload(m, &b.wa2, p.wa2, (size_t)r * d))) return e;
+        if ((e = upload(m, &b.wb2, p.wb2, (size_t)r * d))) return e;
+        if (c.value_residual && i > 0) {
+            AVA_REQUIRE(p.vres, AVA_ERR_ARG, "model: block %d: value residual needs vres", i);
+            if ((e = upload(m, &b.vres, p.vres, 2))) return e;
+        }
+        if ((e = quantize(m, &b.wo, d, {{p.wo, d}}))) return e;
+        if (i == c.eng_block) {
+            b.eng = true;
+            if ((e = upload(m, &b.eng_norm, p.eng_norm, d))) return e;
+            if ((e = quantize(m, &b.eqkv, d, {{p.ewq, de}, {p.ewk, de}, {p.ewv, de}}))) return e;
+            if ((e = quantize(m, &b.ewo, de, {{p.ewo, d}}))) return e;
+        }
+        if ((e = upload(m, &b.mlp_norm, p.mlp_norm, d))) return e;
+        if ((e = quantize(m, &b.w1, d, {{p.w1, H}}))) return e;
+        if ((e = quantize(m, &b.w2, H, {{p.w2, d}}))) return e;
+        if (c.dense) {
+            AVA_REQUIRE(p.dense, AVA_ERR_ARG, "model: block %d: dense mix needs its weights", i);
+            b.dense.assign(p.dense, p.dense + i + 2);
+        }
+    }
+    return AVA_OK;
+}
+
+int ensure_scratch(ava_model *m, size_t rows) {
+    if (rows <= m->rows) return AVA_OK;
+    for (void *p : m->scratch) (void)hipFree(p);
+    m->scratch.clear();
+    m->streams.clear();
+    m->scratch_bytes = 0;
+    m->rows = 0;
+    const ava_config &c = m->cfg;
+    const size_t d = c.d, H = c.hidden, de = c.eng_dim, nc = 2 * (d / c.head_size) + 2 * c.gate_rank;
+    const size_t ldq = std::max<size_t>(ava::q8_ldk((int)H), std::max<size_t>(ava::q8_ldk((int)d), ava::q8_ldk((int)de)));
+    int e = 0;
+    auto A = [&](void **p, size_t bytes) {
+        if (!e) e = dev_alloc(m, p, bytes, true);
+    };
+    A((void **)&m->x, rows * d * 4);
+    A((void **)&m->h, rows * d * 4);
+    A((void **)&m->cur, rows * d * 4);
+    A((void **)&m->P, rows * 5 * d * 4);
+    A((void **)&m->G, rows * nc * 4);
+    A((void **)&m->la, rows * d * 4);
+    A((void **)&m->bw, rows * d * 4);
+    A((void **)&m->y, rows * d * 4);
+    if (c.value_residual) A((void **)&m->v0, rows * d * 4);
+    A((void **)&m->u, rows * H * 4);
+    if (c.eng_block >= 0) {
+        A((void **)&m->qkv, rows * 3 * de * 4);
+        A((void **)&m->eo, rows * de * 4);
+    }
+    A((void **)&m->xq, (size_t)c.planes * rows * ldq);
+    A((void **)&m->xexp, rows * 4);
+    A((void **)&m->spk, rows * ava::q8_ldk((int)d));
+    if (c.dense) {
+        m->streams.resize(c.layers + 1);
+        for (auto &s : m->streams) A((void **)&s, rows * d * 4);
+    }
+    if (e) return e;
+    m->rows = rows;
+    return AVA_OK;
+}
+
+// Launch timing (ava_model_set_timing).
+struct Scope {
+    ava_model *m;
+    const char *name;
+    hipStream_t st;
+    hipEvent_t b = nullptr;
+    Scope(ava_model *m_, const char *n, hipStream_t s) : m(m_), name(n), st(s) {
+        if (!m->timing) return;
+        b = ev();
+        (void)hipEventRecord(b, st);
+    }
+    hipEvent_t ev() {
+        Timer &t = m->timer;
+        if (t.used == t.pool.size()) {
+            hipEvent_t e;
+            (void)hipEventCreate(&e);
+            t.pool.push_back(e);
+        }
+        return t.pool[t.used++];
+    }
+    ~Scope() {
+        if (!m->timing) return;
+        hipEvent_t e = ev();
+        (void)hipEventRecord(e, st);
+        m->timer.pending.push_back({name, {b, e}});
+    }
+};
+
+#define AVA_RUN(name, call)                          \
+    do {                                             \
+        Scope sc_(m, name, st);                      \
+        if (int r_ = (call)) return r_;              \
+    } while (0)
+
+int collect(ava_model *m) {
+    Timer &t = m->timer;
+    if (t.pending.empty()) return AVA_OK;
+    AVA_HIP(hipStreamSynchronize(m->last_stream));
+    for (auto &p : t.pending) {
+        float ms = 0.0f;
+        AVA_HIP(hipEventElapsedTime(&ms, p.second.first, p.second.second));
+        auto it = t.sums.find(p.first);
+        if (it == t.sums.end()) it = t.sums.emplace(p.first, Timer::Sum{p.first, 0, 0.0}).first;
+        it->second.calls += 1;
+        it->second.ms += ms;
+    }
+    t.pending.clear();
+    t.used = 0;
+    return AVA_OK;
+}
+
+int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float *logits, hipStream_t st) {
+    const ava_config &c = m->cfg;
+    const int d = c.d, nh = d / c.head_size, r = c.gate_rank, H = c.hidden, de = c.eng_dim, L = c.layers;
+    const int P = c.planes, N = B * T, ldd = ava::q8_ldk(d), ldh = ava::q8_ldk(H);
+    AVA_REQUIRE(s && s->lif_v && s->lif_s && s->lif_a && s->mem_f, AVA_ERR_ARG, "forward: state buffers are NULL");
+    AVA_REQUIRE(c.momentum == 0.0f || s->mem_s, AVA_ERR_ARG, "forward: momentum needs state mem_s");
+    AVA_REQUIRE(c.eng_block < 0 || (s->eng_k && s->eng_v && s->eng_len >= 0 && s->eng_len + T <= s->eng_cap),
+                AVA_ERR_SHAPE, "forward: the engram store holds %d of %d entries, %d more do not fit", s->eng_len,
+                s->eng_cap, T);
+    if (int e = ensure_scratch(m, (size_t)N)) return e;
+    if (m->timing && m->last_stream != st) {
+        if (int e = collect(m)) return e;
+    }
+    m->last_stream = st;
+
+    AVA_RUN("embed", ava::embed(ids, m->tok_emb, N, d, c.vocab, m->x, c.dense ? m->streams[0] : nullptr, st));
+    for (int i = 0; i < L; i++) {
+        const Block &b = m->blocks[i];
+        const size_t sbd = (size_t)i * B * d;
+        // the spiking layer
+        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.lif_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.win.w, c.lif_scale ? ava::Q8_MUL : ava::Q8_STORE,
+                                        m->cur, d, b.omb, st));
+        AVA_RUN("lif_scan", ava::lif_scan_tuned(m->cur, B, T, d, b.ps, s->lif_v + sbd, s->lif_s + sbd, s->lif_a + sbd,
+                                                c.levels, 1, c.alif, m->spk, nullptr, 0, 0, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->spk, nullptr, 1, N, &b.wout.w, ava::Q8_ADD, m->x, d, nullptr, st));
+        // the fast-weight memory
+        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
+        AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, st));
+        const bool vr = c.value_residual != 0;
+        AVA_RUN("mem_prep", ava::mem_prep(m->P, m->G, N, d, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,
+                                          vr && i > 0 ? b.vres : nullptr, vr && i > 0 ? m->v0 : nullptr,
+                                          vr && i == 0 ? m->v0 : nullptr, m->la, m->bw, st));
+        const size_t sm = (size_t)i * B * nh * 64 * 64;
+        AVA_RUN("mem_scan", ava::mem_scan_strided(m->P, m->P + d, m->P + 3 * d, m->P + 2 * d, m->la, m->bw, B, T, nh,
+                                                  5 * d, 64, d, c.momentum, c.cap, s->mem_f + sm,
+                                                  c.momentum != 0.0f ? s->mem_s + sm : nullptr, m->y, d, st));
+        AVA_RUN("mem_post", ava::mem_post(m->y, N, d, m->P + 4 * d, 5 * d, P, m->xq, m->xexp, ldd, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wo.w, ava::Q8_ADD, m->x, d, nullptr, st));
+        // the engram read
+        if (b.eng) {
+            AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.eng_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+            AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.eqkv.w, ava::Q8_STORE, m->qkv, 3 * de, nullptr, st));
+            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, s->eng_cap, s->eng_len, m->eo, st));
+            AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
+            AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
+        }
+        // the sparse MLP
+        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mlp_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w1.w, ava::Q8_STORE, m->u, H, nullptr, st));
+        AVA_RUN("kwta", ava::kwta_planes(m->u, N, H, c.kwta_k, c.relu2, P, m->xq, m->xexp, ldh, nullptr, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w2.w, ava::Q8_ADD, m->x, d, nullptr, st));
+        if (c.dense)
+            AVA_RUN("dense_mix", ava::dense_mix(m->x, m->streams.data(), b.dense.data(), i + 2, (size_t)N * d, st));
+    }
+    if (c.eng_block >= 0) s->eng_len += T;
+    if (logits) {
+        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &m->head.w, ava::Q8_STORE, logits, c.vocab, nullptr, st));
+    }
+    return AVA_OK;
+}
+
+}  // namespace
+
+extern "C" int ava_model_new(const ava_config *cfg, const ava_params *params, ava_model **out) {
+    AVA_REQUIRE(cfg && params && out, AVA_ERR_ARG, "model_new: NULL argument");
+    const ava_config &c = *cfg;
+    AVA_REQUIRE(c.head_size == 64, AVA_ERR_UNSUPPORTED, "model_new: head size %d (this build runs 64)", c.head_size);
+    AVA_REQUIRE(c.d > 0 && c.d % 64 == 0 && c.d <= 1024, AVA_ERR_SHAPE, "model_new: d=%d (a multiple of 64, <= 1024)", c.d);
+    AVA_REQUIRE(c.hidden > 0 && c.hidden % 4 == 0 && c.hidden <= 8192 && c.kwta_k > 0, AVA_ERR_SHAPE,
+                "model_new: hidden=%d k=%d", c.hidden, c.kwta_k);
+    AVA_REQUIRE(c.layers > 0 && c.layers <= 16, AVA_ERR_SHAPE, "model_new: %d layers (1..16)", c.layers);
+    AVA_REQUIRE(c.vocab > 0 && c.gate_rank > 0 && c.gate_rank <= 32, AVA_ERR_SHAPE, "model_new: vocab=%d gate_rank=%d",
+                c.vocab, c.gate_rank);
+    AVA_REQUIRE(c.eng_block < c.layers && (c.eng_block < 0 || c.eng_dim == 64), AVA_ERR_UNSUPPORTED,
+                "model_new: engram block %d, dim %d (64)", c.eng_block, c.eng_dim);
+    AVA_REQUIRE(c.levels == 1 || c.levels == 2, AVA_ERR_ARG, "model_new: levels %d", c.levels);
+    AVA_REQUIRE(c.planes >= 1 && c.planes <= 3, AVA_ERR_ARG, "model_new: planes %d (1..3)", c.planes);
+    ava_model *m = new ava_model();
+    m->cfg = c;
+    (void)hipGetDevice(&m->device);
+    if (int e = build(m, params)) {
+        ava_model_free(m);
+        return e;
+    }
+    *out = m;
+    return AVA_OK;
+}
+
+extern "C" void ava_model_free(ava_model *m) {
+    if (!m) return;
+    (void)hipDeviceSynchronize();
+    for (void *p : m->allocs) (void)hipFree(p);
+    for (void *p : m->scratch) (void)hipFree(p);
+    for (hipEvent_t e : m->timer.pool) (void)hipEventDestroy(e);
+    delete m;
+}
+
+extern "C" int ava_model_forward(ava_model *m, ava_state *st, const int32_t *ids, int B, int T, float *logits,
+                                 ava_stream stream) {
+    AVA_REQUIRE(m && st && ids, AVA_ERR_ARG, "model_forward: NULL argument");
+    AVA_REQUIRE(B > 0 && T > 0 && (long)B * T <= (1L << 24), AVA_ERR_SHAPE, "model_forward: B=%d T=%d", B, T);
+    return forward(m, st, ids, B, T, logits, (hipStream_t)stream);
+}
+
+extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }
+
+extern "C" int ava_model_set_timing(ava_model *m, int on) {
+    AVA_REQUIRE(m, AVA_ERR_ARG, "set_timing: NULL model");
+    if (!on && m->timing) {
+        if (int e = collect(m)) return e;
+    }
+    m->timing = on != 0;
+    return AVA_OK;
+}
+
+extern "C" int ava_model_timing(ava_model *m, const char **names, int *calls, double *ms, int cap, int reset) {
+    if (!m) return -1;
+    if (collect(m)) return -1;
+    int n = 0;
+    for (auto &kv : m->timer.sums) {
+        if (n < cap) {
+            if (names) names[n] = kv.second.name;
+            if (calls) calls[n] = kv.second.calls;
+            if (ms) ms[n] = kv.second.ms;
+        }
+        n++;
+    }
+    if (reset) m->timer.sums.clear();
+    return n;
+}

@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
 
 // ------------------------------------------------------------------ the product
 
-enum Epi { EPI_ACC = 0, EPI_STORE = 1, EPI_MUL = 2, EPI_ADD = 3 };
+enum Epi { EPI_ACC = 0, EPI_STORE = ava::Q8_STORE, EPI_MUL = ava::Q8_MUL, EPI_ADD = ava::Q8_ADD };
 
 constexpr int BM = 128, BN = 128, BK = 64, LDS_ROW = BK + 16;
 

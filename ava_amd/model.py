@@ -1,0 +1,116 @@
+"""The block stack on the HIP path: Model and State with the reference's names (gpu/model.rs,
+gpu/state.rs), over ava_model_* of include/ava.h.
+
+    m = Model(cfg, params)              Model::new + set_int8 (model.rs:805, 949-991)
+    st = m.state(B, eng_cap)            Model::state (state.rs:593)
+    logits = m.forward_with_state(ids, st)   state.rs:684-865 (ids [B, T] int32 on the GPU)
+    logits = m.forward(ids)             model.rs:1171: a fresh state per call
+
+`params` is a dict of float32 numpy arrays keyed as ava_amd.synth (the reference's VarMap names).
+The library raises AvaError on any failure; nothing falls back to another path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from ._lib import BLOCK_FIELDS, BlockParams, Config, Params, State as _CState, check, lib
+
+
+def _ptr(a, keep):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    keep.append(a)
+    return a.ctypes.data
+
+
+class State:
+    """The carried state of B streams (state.rs:94-116), device tensors."""
+
+    def __init__(self, cfg: dict, B: int, eng_cap: int = 0, device="cuda"):
+        L, d, hs, de = cfg["layers"], cfg["d"], cfg["head_size"], cfg["eng_dim"]
+        nh = d // hs
+        z = lambda *s: torch.zeros(s, dtype=torch.float32, device=device)
+        self.B = B
+        self.lif_v, self.lif_s, self.lif_a = z(L, B, d), z(L, B, d), z(L, B, d)
+        self.mem_f = z(L, B, nh, hs, hs)
+        self.mem_s = z(L, B, nh, hs, hs)
+        cap = max(eng_cap, 1)
+        self.eng_k, self.eng_v = z(B, cap, de), z(B, cap, de)
+        self.eng_cap, self.eng_len = eng_cap, 0
+
+    def c(self):
+        p = lambda t: t.data_ptr()
+        return _CState(lif_v=p(self.lif_v), lif_s=p(self.lif_s), lif_a=p(self.lif_a), mem_f=p(self.mem_f),
+                       mem_s=p(self.mem_s), eng_k=p(self.eng_k), eng_v=p(self.eng_v), eng_cap=self.eng_cap,
+                       eng_len=self.eng_len)
+
+
+class Model:
+    def __init__(self, cfg: dict, params: dict, planes: int = 3):
+        self.cfg = dict(cfg)
+        L = cfg["layers"]
+        keep = []
+        blocks = (BlockParams * L)()
+        for i in range(L):
+            bp = params["blocks"][i]
+            for name in BLOCK_FIELDS:
+                if bp.get(name) is not None:
+                    setattr(blocks[i], name, _ptr(bp[name], keep))
+        prm = Params(tok_emb=_ptr(params["tok_emb"], keep), final_norm=_ptr(params["final_norm"], keep),
+                     blocks=C.cast(blocks, C.POINTER(BlockParams)))
+        c = self.cfg
+        ccfg = Config(vocab=c["vocab"], d=c["d"], layers=L, hidden=c["hidden"], kwta_k=c["kwta_k"],
+                      head_size=c["head_size"], gate_rank=c["gate_rank"], eng_block=c["eng_block"],
+                      eng_dim=c["eng_dim"], levels=c["levels"], alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
+                      value_residual=int(c["value_residual"]), dense=int(c["dense"]), relu2=int(c["relu2"]),
+                      momentum=c["momentum"], cap=c["cap"], planes=planes)
+        torch.cuda.init()
+        h = C.c_void_p()
+        check(lib().ava_model_new(C.byref(ccfg), C.byref(prm), C.byref(h)), "ava_model_new")
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().ava_model_free(self.h)
+            self.h = None
+
+    def state(self, B: int, eng_cap: int = 0) -> State:
+        return State(self.cfg, B, eng_cap)
+
+    def forward_with_state(self, ids: torch.Tensor, st: State, logits: torch.Tensor | None = None, want_logits=True):
+        if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
+            raise ValueError("ids: a contiguous [B, T] int32 GPU tensor is required")
+        B, T = ids.shape
+        if want_logits and logits is None:
+            logits = torch.empty((B * T, self.cfg["vocab"]), dtype=torch.float32, device=ids.device)
+        cst = st.c()
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check(lib().ava_model_forward(self.h, C.byref(cst), C.c_void_p(ids.data_ptr()), B, T,
+                                      C.c_void_p(logits.data_ptr()) if want_logits else None, stream),
+              "ava_model_forward")
+        st.eng_len = cst.eng_len
+        return logits
+
+    def forward(self, ids: torch.Tensor):
+        B, T = ids.shape
+        st = self.state(B, eng_cap=T if self.cfg["eng_block"] >= 0 else 0)
+        return self.forward_with_state(ids, st), st
+
+    # launch timing by kernel class (ava_model_set_timing / ava_model_timing)
+    def set_timing(self, on: bool):
+        check(lib().ava_model_set_timing(self.h, int(on)), "ava_model_set_timing")
+
+    def timing(self, reset: bool = False) -> dict:
+        cap = 64
+        names = (C.c_char_p * cap)()
+        calls = (C.c_int * cap)()
+        ms = (C.c_double * cap)()
+        n = lib().ava_model_timing(self.h, names, calls, ms, cap, int(reset))
+        if n < 0:
+            raise RuntimeError("ava_model_timing failed: " + lib().ava_last_error().decode())
+        return {names[i].decode(): (calls[i], ms[i]) for i in range(min(n, cap))}
+
+    def scratch_bytes(self) -> int:
+        return lib().ava_model_scratch_bytes(self.h)

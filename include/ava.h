@@ -156,11 +156,13 @@ typedef struct {
 } ava_params;
 
 /* The carried state of B streams (caller-owned device buffers). Replaces State's LIF, memory and
- * engram tensors (state.rs:94-116). The engram keys/values are fp16. */
+ * engram tensors (state.rs:94-116). The engram store is f32, as the reference's key/value store
+ * (model/fstep/arch.rs:952-961). mem_s is read and written only when momentum != 0; the engram
+ * store only when eng_block >= 0. */
 typedef struct {
     float *lif_v, *lif_s, *lif_a; /* [layers][B][d] */
     float *mem_f, *mem_s;         /* [layers][B][d/hs][hs][hs] */
-    uint16_t *eng_k, *eng_v;      /* [B][eng_cap][eng_dim] fp16 */
+    float *eng_k, *eng_v;         /* [B][eng_cap][eng_dim] */
     int eng_cap, eng_len;         /* eng_len advances by T per forward */
 } ava_state;
 
@@ -179,6 +181,14 @@ int ava_model_forward(ava_model *m, ava_state *st, const int32_t *ids, int B, in
 
 /* Bytes of scratch the model holds after forwards of up to B*T rows. */
 size_t ava_model_scratch_bytes(const ava_model *m);
+
+/* Launch timing by kernel class (the counterpart of int8::set_mm_prof, int8.rs:628-669): with `on`,
+ * every launch of ava_model_forward is bracketed by HIP events on its stream. ava_model_timing
+ * synchronises the stream of the last forward, then fills up to `cap` entries of names (static
+ * strings), launch counts and summed milliseconds since the last reset, and returns the number of
+ * classes (or -1 on error). reset clears the sums. */
+int ava_model_set_timing(ava_model *m, int on);
+int ava_model_timing(ava_model *m, const char **names, int *calls, double *ms, int cap, int reset);
 
 #ifdef __cplusplus
 }
