@@ -40,8 +40,9 @@ namespace ava {
 
 static inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
-// Leading dimension of int8 operands of the i8 MFMA products: K padded to 64 with zeros.
-static inline int q8_ldk(int k) { return (k + 63) / 64 * 64; }
+// Leading dimension of int8 operands of the i8 MFMA products: K padded to 128 with zeros (an even
+// number of 64-byte K steps).
+static inline int q8_ldk(int k) { return (k + 127) / 128 * 128; }
 
 // ---- the split-plane activation format (shared by every producer of a dense int8 product input)
 // Row exponent: the smallest e with amax * 2^-e < 127.5, so plane 0 = rint(x 2^-e) fits +-127.

@@ -366,7 +366,8 @@ extern "C" int ava_model_new(const ava_config *cfg, const ava_params *params, av
     AVA_REQUIRE(cfg && params && out, AVA_ERR_ARG, "model_new: NULL argument");
     const ava_config &c = *cfg;
     AVA_REQUIRE(c.head_size == 64, AVA_ERR_UNSUPPORTED, "model_new: head size %d (this build runs 64)", c.head_size);
-    AVA_REQUIRE(c.d > 0 && c.d % 64 == 0 && c.d <= 1024, AVA_ERR_SHAPE, "model_new: d=%d (a multiple of 64, <= 1024)", c.d);
+    AVA_REQUIRE(c.d > 0 && c.d % 128 == 0 && c.d <= 1024, AVA_ERR_SHAPE, "model_new: d=%d (a multiple of 128, <= 1024)",
+                c.d);
     AVA_REQUIRE(c.hidden > 0 && c.hidden % 4 == 0 && c.hidden <= 8192 && c.kwta_k > 0, AVA_ERR_SHAPE,
                 "model_new: hidden=%d k=%d", c.hidden, c.kwta_k);
     AVA_REQUIRE(c.layers > 0 && c.layers <= 16, AVA_ERR_SHAPE, "model_new: %d layers (1..16)", c.layers);

@@ -16,6 +16,10 @@
 // 16-byte fragment reads of 8 consecutive rows hit distinct banks. Tiles are ordered so that the
 // workgroups of one XCD (hardware id mod 8) walk consecutive tiles: the N tiles of one row block
 // run back to back on one XCD and share its L2 for the A rows.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
 
 enum Epi { EPI_ACC = 0, EPI_STORE = ava::Q8_STORE, EPI_MUL = ava::Q8_MUL, EPI_ADD = ava::Q8_ADD };
 
-constexpr int BM = 128, BN = 128, BK = 64, LDS_ROW = BK + 16;
+
 
 // Epilogue parameters: y [m][ldy] (f32 or, for EPI_ACC, int32 [P][m][n]); colv [n] (EPI_MUL).
 struct EpiArgs {
@@ -102,10 +106,24 @@ struct EpiArgs {
     const float *colv;
 };
 
-template <int P, int EPI>
-__global__ __launch_bounds__(256) void q8_gemm_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
+// LDS position of 16-byte chunk c of tile row r: the chunk index XOR a function of the row, so that
+// the fragment reads (32 consecutive rows, one chunk) and the staging writes (whole rows) touch
+// distinct banks with either 32 or 64 four-byte banks. CPR = chunks per row (4 or 8).
+template <int CPR>
+__device__ __forceinline__ int swz(int r, int c) {
+    if (CPR == 4) return c ^ (((r >> 1) ^ (r >> 3)) & 3);
+    return c ^ ((r ^ (r >> 3)) & 7);
+}
+
+// The product over one BM x BN output tile: 256 threads = 4 waves in WM x (4 / WM); wave tile
+// MW x NW = (BM / WM) x (BN * WM / 4), FM x FN blocks of 32 x 32 per plane.
+template <int P, int EPI, int BM, int BN, int WM, int BK>
+__global__ __launch_bounds__(256, 2) void q8_gemm_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
                                                       int m, int n, int ldk, const int8_t *__restrict__ qt,
                                                       const float *__restrict__ scale, EpiArgs ep) {
+    constexpr int WN = 4 / WM, MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
+    constexpr int LDS_ROW = BK;  // unpadded rows; the 16-byte chunks are XOR-swizzled per row (swz)
+    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     int8_t *lds_a = smem;                              // [2][P][BM][LDS_ROW]
     int8_t *lds_b = smem + 2 * P * BM * LDS_ROW;       // [2][BN][LDS_ROW]
@@ -117,145 +135,215 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const int8_t *__restrict__
     const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
-    // global -> register staging: A: P*BM rows x 4 chunks of 16 B; B: BN rows x 4 chunks
-    constexpr int A_CHUNKS = P * BM * 4 / 256;  // per thread
-    constexpr int B_CHUNKS = BN * 4 / 256;
-    i32x4 ra[A_CHUNKS], rb[B_CHUNKS];
-
-    auto load_tile = [&](int kt) {
+    // global -> register staging: A: P*BM rows x BK/16 chunks of 16 B; B: BN rows x BK/16 chunks.
+    // Rows past m and columns past n load the last valid row / column instead (their outputs are
+    // never stored), so every load is unconditional and the compiler can keep two K steps in flight.
+    constexpr int CPR = BK / 16;  // 16-byte chunks per row
+    constexpr int A_CH = P * BM * CPR, B_CH = BN * CPR;
+    static_assert(A_CH % 256 == 0 && B_CH % 256 == 0, "staging");
+    constexpr int A_CHUNKS = A_CH / 256, B_CHUNKS = B_CH / 256;  // per thread
+    i32x4 ra[2][A_CHUNKS], rb[2][B_CHUNKS];
+    const int8_t *a_src[A_CHUNKS];
+    const int8_t *b_src[B_CHUNKS];
+    int a_dst[A_CHUNKS], b_dst[B_CHUNKS];
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; i++) {
+        const int c = i * 256 + tid;
+        const int p = c / (BM * CPR), rr = (c / CPR) % BM, kc = c % CPR;
+        const int row = min(m0 + rr, m - 1);
+        a_src[i] = xq + ((size_t)p * m + row) * ldk + kc * 16;
+        a_dst[i] = (p * BM + rr) * LDS_ROW + swz<CPR>(rr, kc) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; i++) {
+        const int c = i * 256 + tid;
+        const int rr = c / CPR, kc = c % CPR;
+        const int col = min(n0 + rr, n - 1);
+        b_src[i] = qt + (size_t)col * ldk + kc * 16;
+        b_dst[i] = rr * LDS_ROW + swz<CPR>(rr, kc) * 16;
+    }
+    auto load_tile = [&](int kt, int set) {
         const int k0 = kt * BK;
 #pragma unroll
-        for (int i = 0; i < A_CHUNKS; i++) {
-            const int c = i * 256 + tid;
-            const int p = c / (BM * 4), rr = (c / 4) % BM, kc = c & 3;
-            const int row = m0 + rr;
-            if (row < m)
-                ra[i] = *reinterpret_cast<const i32x4 *>(xq + ((size_t)p * m + row) * ldk + k0 + kc * 16);
-            else
-                ra[i] = i32x4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < A_CHUNKS; i++) ra[set][i] = *reinterpret_cast<const i32x4 *>(a_src[i] + k0);
 #pragma unroll
-        for (int i = 0; i < B_CHUNKS; i++) {
-            const int c = i * 256 + tid;
-            const int rr = c / 4, kc = c & 3;
-            const int col = n0 + rr;
-            if (col < n)
-                rb[i] = *reinterpret_cast<const i32x4 *>(qt + (size_t)col * ldk + k0 + kc * 16);
-            else
-                rb[i] = i32x4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < B_CHUNKS; i++) rb[set][i] = *reinterpret_cast<const i32x4 *>(b_src[i] + k0);
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf, int set) {
         int8_t *la = lds_a + buf * P * BM * LDS_ROW;
         int8_t *lb = lds_b + buf * BN * LDS_ROW;
 #pragma unroll
-        for (int i = 0; i < A_CHUNKS; i++) {
-            const int c = i * 256 + tid;
-            const int p = c / (BM * 4), rr = (c / 4) % BM, kc = c & 3;
-            *reinterpret_cast<i32x4 *>(la + (p * BM + rr) * LDS_ROW + kc * 16) = ra[i];
-        }
+        for (int i = 0; i < A_CHUNKS; i++) *reinterpret_cast<i32x4 *>(la + a_dst[i]) = ra[set][i];
 #pragma unroll
-        for (int i = 0; i < B_CHUNKS; i++) {
-            const int c = i * 256 + tid;
-            const int rr = c / 4, kc = c & 3;
-            *reinterpret_cast<i32x4 *>(lb + rr * LDS_ROW + kc * 16) = rb[i];
-        }
+        for (int i = 0; i < B_CHUNKS; i++) *reinterpret_cast<i32x4 *>(lb + b_dst[i]) = rb[set][i];
     };
 
-    i32x16 acc[P][2][2];
+    i32x16 acc[P][FM][FN];
 #pragma unroll
     for (int p = 0; p < P; p++)
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) acc[p][i][j] = i32x16{};
+            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
 
-    const int KT = ldk / BK;
-    load_tile(0);
-    store_tile(0);
+    const int KT = ldk / BK;  // even: ldk is a multiple of 128, and BK is 64 or a multiple of ldk's factor
+    load_tile(0, 0);
+    load_tile(min(1, KT - 1), 1);
+    store_tile(0, 0);
     __syncthreads();
 
-    const int frow = lane & 31, fk = (lane >> 5) * 16;
-    for (int kt = 0; kt < KT; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < KT) load_tile(kt + 1);
-        const int8_t *la = lds_a + buf * P * BM * LDS_ROW;
-        const int8_t *lb = lds_b + buf * BN * LDS_ROW;
+    const int frow = lane & 31, fc = lane >> 5;  // fragment row, 16-byte chunk within the 32-byte K substep
+    // One K step on LDS buffer / register set SET (= kt & 1, a constant so the staging registers are
+    // addressed statically): refill set SET with step kt+2, multiply step kt, store step kt+1. KT is
+    // even (K is padded to 128) and the loads past the end re-read the last step, so nothing here is
+    // conditional and the compiler waits only for the older register set.
+    auto step = [&](int kt, auto set_c) {
+        constexpr int SET = decltype(set_c)::value;
+        load_tile(min(kt + 2, KT - 1), SET);
+        const int8_t *la = lds_a + SET * P * BM * LDS_ROW;
+        const int8_t *lb = lds_b + SET * BN * LDS_ROW;
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ks++) {
-            i32x4 bf[2];
+            i32x4 bf[FN];
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                bf[j] = *reinterpret_cast<const i32x4 *>(lb + (wn * 64 + j * 32 + frow) * LDS_ROW + ks * 32 + fk);
+            for (int j = 0; j < FN; j++) {
+                const int r = wn * NW + j * 32 + frow;
+                bf[j] = *reinterpret_cast<const i32x4 *>(lb + r * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
+            }
 #pragma unroll
             for (int p = 0; p < P; p++) {
-                i32x4 af[2];
+                i32x4 af[FM];
 #pragma unroll
-                for (int i = 0; i < 2; i++)
-                    af[i] = *reinterpret_cast<const i32x4 *>(la + (p * BM + wm * 64 + i * 32 + frow) * LDS_ROW +
-                                                              ks * 32 + fk);
+                for (int i = 0; i < FM; i++) {
+                    const int r = wm * MW + i * 32 + frow;  // swizzle by the row within the plane (BM % 16 == 0)
+                    af[i] = *reinterpret_cast<const i32x4 *>(la + (p * BM + r) * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
+                }
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < FN; j++)
                         acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[p][i][j], 0, 0, 0);
             }
         }
-        if (kt + 1 < KT) store_tile(buf ^ 1);
+        store_tile(SET ^ 1, SET ^ 1);
         __syncthreads();
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
     }
 
-    // epilogue: lane holds, for block (i, j), rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
+    // epilogue. The tile's row exponents are staged in LDS (free after the K loop) so no element waits
+    // on a global load of its own; per 32 x 32 block, the lane holds rows (r/4)*8 + (lane/32)*4 + r%4
+    // of column lane%32, and all 16 of its loads (the accumulated output, EPI_ADD) are issued before use.
+    int *s_exp = reinterpret_cast<int *>(smem);
+    if (EPI != EPI_ACC) {
+        for (int i = tid; i < BM; i += 256) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        __syncthreads();
+    }
     const int ccol = lane & 31, rsub = (lane >> 5) * 4;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + wn * NW + j * 32 + ccol;
+        const bool col_ok = col < n;
+        const int colc = col_ok ? col : n - 1;
+        const float sc = scale[colc];
+        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int col = n0 + wn * 64 + j * 32 + ccol;
-            if (col >= n) continue;
-            const float sc = scale[col];
-            float cv = 0.0f;
-            if (EPI == EPI_MUL) cv = ep.colv[col];
+        for (int i = 0; i < FM; i++) {
+            const int rbase = wm * MW + i * 32 + rsub;  // tile row of r = 0
+            if (EPI == EPI_ACC) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
+                    if (row < m && col_ok)
+#pragma unroll
+                        for (int p = 0; p < P; p++)
+                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
+                }
+                continue;
+            }
+            float *ybase = reinterpret_cast<float *>(ep.y);
+            float prev[16];
+            if (EPI == EPI_ADD) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
+                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + rsub + (r & 3);
-                if (row >= m) continue;
-                if (EPI == EPI_ACC) {
+                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
+                float v;
+                if (P == 1) {
+                    v = (float)acc[0][i][j][r];  // one rounding, as (float)(double) of the exact sum
+                } else {
+                    // sum_p acc_p 2^(7(P-1-p)) is exact in double (|acc_p| < 2^31, the sum < 2^46)
+                    double A = (double)acc[0][i][j][r];
 #pragma unroll
-                    for (int p = 0; p < P; p++)
-                        reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
-                    continue;
+                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
+                    v = (float)A;
                 }
-                long long A = 0;
-#pragma unroll
-                for (int p = 0; p < P; p++) A += (long long)acc[p][i][j][r] << (7 * (P - 1 - p));
-                float v = (float)(double)A;
-                v = ldexpf(v, (xexp ? xexp[row] : 0) - 7 * (P - 1));
+                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
                 v = v * sc;
-                float *yp = reinterpret_cast<float *>(ep.y) + (size_t)row * ep.ldy + col;
-                if (EPI == EPI_STORE) *yp = v;
-                else if (EPI == EPI_MUL) *yp = v * cv;
-                else *yp = *yp + v;
+                if (EPI == EPI_MUL) v = v * cv;
+                if (EPI == EPI_ADD) v = prev[r] + v;
+                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
             }
         }
+    }
+}
+
+// Tile shapes (BM, BN, WM); AVA_Q8_TILE=<index> overrides the choice per plane count (tuning).
+struct TileCfg {
+    int bm, bn, wm, bk;
+};
+constexpr TileCfg TILES[] = {{128, 128, 2, 64}, {64, 128, 2, 64},  {128, 64, 2, 64}, {64, 256, 1, 64},
+                             {64, 64, 2, 64},   {128, 128, 2, 128}, {64, 128, 2, 128}, {64, 64, 2, 128}};
+constexpr int NTILES = sizeof(TILES) / sizeof(TILES[0]);
+
+int tile_override() {
+    static int v = -2;
+    if (v == -2) {
+        const char *e = getenv("AVA_Q8_TILE");
+        v = e ? atoi(e) : -1;
+        if (v >= NTILES) v = -1;
+    }
+    return v;
+}
+
+template <int P, int EPI, int BM, int BN, int WM, int BK>
+int launch_tile(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                EpiArgs ep, hipStream_t st) {
+    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const size_t lds = (size_t)2 * (P * BM + BN) * BK;
+    static bool attr = false;  // above 64 KiB of dynamic LDS the kernel must opt in (gfx950: 160 KiB)
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_kernel<P, EPI, BM, BN, WM, BK>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    q8_gemm_kernel<P, EPI, BM, BN, WM, BK><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
 }
 
 template <int P, int EPI>
 int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                 EpiArgs ep, hipStream_t st) {
-    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    const size_t lds = (size_t)2 * (P * BM + BN) * LDS_ROW;
-    static bool attr = false;  // above 64 KiB of dynamic LDS the kernel must opt in (gfx950: 160 KiB)
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_kernel<P, EPI>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
-    q8_gemm_kernel<P, EPI><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
-    AVA_LAUNCHED("q8_gemm");
-    return AVA_OK;
+    int t = tile_override();
+    if (t < 0) t = P == 1 ? 0 : 1;  // defaults
+    if (ldk % (2 * TILES[t].bk)) t = P == 1 ? 0 : 1;  // an even number of K steps
+#define AVA_T(I)                                                                                              \
+    if (t == I)                                                                                               \
+        return launch_tile<P, EPI, TILES[I].bm, TILES[I].bn, TILES[I].wm, TILES[I].bk>(xq, xexp, m, n, ldk, qt, \
+                                                                                      scale, ep, st);
+    AVA_T(0) AVA_T(1) AVA_T(2) AVA_T(3) AVA_T(4) AVA_T(5) AVA_T(6) AVA_T(7)
+#undef AVA_T
+    return ava::fail(AVA_ERR_ARG, "q8 product: tile %d", t);
 }
 
 template <int EPI>

@@ -44,12 +44,12 @@ const char *ava_version(void);
  * f32 scale per output column. Replaces QW (int8.rs:44-54). */
 typedef struct {
     int din, dout;
-    int ldk;      /* ava_q8_ldk(din): din padded to a multiple of 64 with zero weights */
+    int ldk;      /* ava_q8_ldk(din): din padded to a multiple of 128 with zero weights */
     int8_t *qt;   /* [dout][ldk] */
     float *scale; /* [dout] */
 } ava_qw;
 
-/* din rounded up to a multiple of 64 (the K step of the i8 MFMA kernels). */
+/* din rounded up to a multiple of 128 (two K steps of the i8 MFMA kernels). */
 int ava_q8_ldk(int k);
 
 /* Quantize W [din][dout] f32 into qt [dout][ldk] / scale [dout]: scale_c = max_j |W[j][c]| / 127
