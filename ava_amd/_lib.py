@@ -72,7 +72,7 @@ def lib():
         "ava_lif_scan_tuned": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, vp],
         "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
-        "ava_delta_chunk": [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
+        "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
     }

@@ -1,9 +1,10 @@
 // k-winners-take-all for gfx950: one wavefront per row, the row held in registers.
 //
-// The k-th largest value of a row is found exactly by a 32-step bisection over the
-// order-preserving uint32 image of the floats (larger float <=> larger key): at each step the
-// candidate key prefix|bit is kept when at least k keys are >= it, which ends at the largest key
-// with k keys at or above it, i.e. the k-th largest (duplicates counted). Each count is a wave
+// The k-th largest value of a row is found exactly by a bisection over the order-preserving uint32
+// image of the floats (larger float <=> larger key): at each step the candidate key prefix|bit is
+// kept when at least k keys are >= it, which ends at the largest key with k keys at or above it,
+// i.e. the k-th largest (duplicates counted). As soon as a candidate has exactly k keys at or above
+// it, the answer is the smallest of those keys (one wave min), which ends the search early. Each count is a wave
 // ballot per register and a popcount: no LDS, no atomics, no barriers, so a SIMD interleaves
 // several rows' waves while their loads are in flight. HBM traffic is one read of u and one
 // write of the output per element.
@@ -65,6 +66,19 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
 #pragma unroll
                 for (int j = 0; j < 4; j++) cnt += __popcll(__ballot(keys[i][j] >= cand));
             if (cnt >= k) prefix = cand;
+            if (cnt == k) {
+                // exactly k keys are >= cand: the k-th largest is the smallest of them (typically after
+                // about log2(h) of the 32 steps)
+                uint32_t mn = 0xffffffffu;
+#pragma unroll
+                for (int i = 0; i < NV; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) mn = keys[i][j] >= cand ? min(mn, keys[i][j]) : mn;
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) mn = min(mn, (uint32_t)__shfl_xor((int)mn, o, 64));
+                prefix = mn;
+                break;
+            }
         }
         kth = float_of_key(prefix);
     }

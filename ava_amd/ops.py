@@ -10,7 +10,7 @@ status (the reference bail!s on shape, dtype and contiguity errors).
     lif_gen(cur, beta, ...)      lif_gen.rs:86-130
     kwta_relu(u, k, relu2)       model.rs:504-528 + arch.rs:1820-1835
     mem_gen(q, k, e, v, la, b, m)   mem_gen.rs:127-137
-    delta_rule_from(q, k, v, la, beta, f0)   model.rs:761-799 (alpha = 1: la must be 0)
+    delta_rule_from(q, k, v, beta, la, f0)   model.rs:744-799 (chunked, per-head gates)
 """
 from __future__ import annotations
 
@@ -165,13 +165,14 @@ def mem_gen(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
     return y, F, S
 
 
-def delta_rule_from(q, k, v, beta, f0=None):
-    """model.rs:761-799 at alpha = 1 (config[2]): q, k, v [BH, T, 64], beta [BH, T]. Returns (y, F)."""
-    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
+def delta_rule_from(q, k, v, beta, la=None, f0=None):
+    """model.rs:744-799 (per-head gates): q, k, v [BH, T, 64], beta and la (log alpha, None: alpha = 1)
+    [BH, T]. Returns (y, F)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")) + (((la, "la"),) if la is not None else ()):
         _need(t, torch.float32, f"delta_rule {nm}")
     BH, T, hs = q.shape
     F = torch.zeros((BH, hs, hs), device=q.device) if f0 is None else f0.clone()
     y = torch.empty_like(q)
-    check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
+    check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(la), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
           "ava_delta_chunk")
     return y, F

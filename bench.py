@@ -209,6 +209,67 @@ class Gemm:
                 "sample": f"oracle W8A32 product (int8.rs:301-331 fma chain), {rows} rows, {dt:.2f} s"}
 
 
+class Delta:
+    """config[2]: the plain delta rule W += beta (v - W k) k^T, y = W q, chunks of 64: B=32, H=8, T=4096,
+    d_k = d_v = 64; keys and queries N(0,1) then unit length, values N(0,1), beta = sigmoid(N(0,1)) per
+    token and head, W_0 = 0."""
+
+    name = "delta"
+    kernel = "delta_chunk_kernel"
+
+    def __init__(self, B=32, H=8, T=4096):
+        import torch
+        from ava_amd import _lib
+
+        self.L = _lib.lib()
+        BH = B * H
+        self.BH, self.T = BH, T
+        g = torch.Generator(device="cuda").manual_seed(5)
+        n = lambda: torch.randn((BH, T, 64), device="cuda", generator=g)
+        self.q, self.k, self.v = n(), n(), n()
+        self.q /= self.q.norm(dim=2, keepdim=True)
+        self.k /= self.k.norm(dim=2, keepdim=True)
+        self.beta = torch.sigmoid(torch.randn((BH, T), device="cuda", generator=g))
+        self.F = torch.zeros((BH, 64, 64), device="cuda")
+        self.y = torch.empty_like(self.q)
+        self.tokens = B * T
+        # read q, k, v, beta; write y and the final state
+        self.bytes = 3 * BH * T * 64 * 4 + BH * T * 4 + BH * T * 64 * 4 + BH * 64 * 64 * 4
+        self.config = {"workload": "delta rule chunked config[2]", "B": B, "H": H, "T": T, "d": 64, "chunk": 64}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        import ctypes as C
+        from ava_amd._lib import check
+
+        p = lambda t: C.c_void_p(t.data_ptr())
+        self.F.zero_()
+        if ev: ev[0].record()
+        check(self.L.ava_delta_chunk(p(self.q), p(self.k), p(self.v), None, p(self.beta), self.BH, self.T, 64,
+                                     p(self.F), p(self.y), stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.bytes / kernel_s / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        BH, T = 8, 4096
+        rng = np.random.default_rng(5)
+        q, k, v = (rng.standard_normal((BH, T, 64)).astype(np.float32) for _ in range(3))
+        q /= np.linalg.norm(q, axis=2, keepdims=True)
+        k /= np.linalg.norm(k, axis=2, keepdims=True)
+        beta = (1.0 / (1.0 + np.exp(-rng.standard_normal((BH, T, 1))))).astype(np.float32)
+        t0 = time.perf_counter()
+        O.mem_rec(q, k, k, v, np.zeros_like(beta), beta)
+        dt = time.perf_counter() - t0
+        return {"value": BH * T / dt / 8, "unit": "tokens/s (B x T per second, 8 heads per token)", "cores": 1,
+                "kind": "port", "sample": f"oracle recurrence (mem_gen.rs:220-273 loop), {BH} of 256 heads, T={T}, "
+                                          f"{dt:.2f} s"}
+
+
 class Copy:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the FETCH/WRITE_SIZE counters."""
 
@@ -322,7 +383,7 @@ class Stack:
                           f"config[3]'s model, B=1, T={T}, {th} threads for the products, {dt:.2f} s"}
 
 
-WORKLOADS = {"stack": Stack, "lif": Lif, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
+WORKLOADS = {"stack": Stack, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
 DEFAULT = "stack"
 
 

@@ -120,12 +120,13 @@ int ava_mem_scan(const float *q, const float *k, const float *e, const float *v,
                  const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,
                  float *y, ava_stream stream);
 
-/* The plain delta rule W += beta (v - W k) k^T, y = W q, in its chunked (WY/UT) form, chunks of
- * 64: q, k, v [BH][T][64], beta [BH][T], F [BH][64][64] (F = W^T) carried in and out, y [BH][T][64].
- * T a multiple of 64. Replaces model::delta_rule_from (model.rs:700-799) for per-head gates at
- * alpha = 1. */
-int ava_delta_chunk(const float *q, const float *k, const float *v, const float *beta, int BH, int T,
-                    int hs, float *F, float *y, ava_stream stream);
+/* The gated delta rule F_t = alpha_t (I - beta_t k_t k_t^T) F_{t-1} + beta_t k_t v_t^T, y_t = F_t^T q_t
+ * (F = W^T: with alpha = 1 this is W += beta (v - W k) k^T, y = W q) in its chunked (WY/UT) form,
+ * chunks of 64 tokens: q, k, v [BH][T][64]; la = log alpha per token and head [BH][T] (NULL: alpha = 1);
+ * beta [BH][T]; F [BH][64][64] carried in and out; y [BH][T][64]. T a multiple of 64.
+ * Replaces model::delta_rule_from (model.rs:744-799) for per-head gates. */
+int ava_delta_chunk(const float *q, const float *k, const float *v, const float *la, const float *beta, int BH,
+                    int T, int hs, float *F, float *y, ava_stream stream);
 
 /* ------------------------------------------------------------------ model */
 

@@ -86,3 +86,54 @@ def test_mem_scan_rejects_bad_shapes():
     la = torch.zeros((2, 8, 1), device="cuda")
     with pytest.raises(AvaError):
         ops.mem_gen(q, q, q, q, la, la)
+
+
+# ----------------------------------------------------------------------------- the chunked delta rule
+
+
+def delta_inputs(BH, T, seed, gated):
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal((BH, T, 64)).astype(np.float32) for _ in range(3))
+    q /= np.linalg.norm(q, axis=2, keepdims=True)
+    k /= np.linalg.norm(k, axis=2, keepdims=True)
+    beta = (1.0 / (1.0 + np.exp(-rng.standard_normal((BH, T))))).astype(np.float32)  # config[2]: sigmoid(N(0,1))
+    la = (-np.exp(rng.standard_normal((BH, T)) - 3.0)).astype(np.float32) if gated else np.zeros((BH, T), np.float32)
+    return q, k, v, beta, la
+
+
+@pytest.mark.parametrize("gated,T", [(False, 64), (False, 256), (True, 192)])
+def test_delta_chunk_matches_recurrence(gated, T):
+    """model.rs:744-799 vs the token loop (arch/tests.rs:704-750: chunked = recurrence within 1e-4), with a
+    carried initial state; config[2]'s rule (alpha = 1, e = k, one beta per token and head, no momentum)."""
+    BH = 6
+    print(f"delta_chunk gated={gated} T={T}", flush=True)
+    q, k, v, beta, la = delta_inputs(BH, T, 3 + T, gated)
+    F0 = (np.random.default_rng(2).standard_normal((BH, 64, 64)) * 0.1).astype(np.float32)
+    from ava_amd import ops
+    y, F = ops.delta_rule_from(cuda(q), cuda(k), cuda(v), cuda(beta), cuda(la) if gated else None, f0=cuda(F0))
+    y, F = host(y), host(F)
+    g3 = lambda a: a[:, :, None]
+    y64, F64, _ = O.mem_rec_f64(q, k, k, v, g3(la), g3(beta), F=F0)
+    assert rel(y, y64) < 1e-4 and rel(F, F64) < 1e-4
+    yo, Fo, _ = O.mem_rec(q, k, k, v, g3(la), g3(beta), F=F0)
+    assert rel(y, yo) < 1e-4 and rel(F, Fo) < 1e-4
+
+
+def test_delta_chunk_repeated_keys_read_back():
+    """tests/smoke.rs:373-397: two chunks, the second one key repeated; with beta 1 every read right after a
+    write returns the written value (unit keys), where a power-series inverse would cancel catastrophically."""
+    BH, T = 3, 128
+    q, k, v, beta, la = delta_inputs(BH, T, 9, False)
+    k[:, 64:] = k[:, 64:65]
+    beta[:] = 1.0
+    from ava_amd import ops
+    y, _ = ops.delta_rule_from(cuda(k), cuda(k), cuda(v), cuda(beta))
+    assert np.max(np.abs(host(y) - v)) < 1e-4
+
+
+def test_delta_chunk_rejects_ragged_length():
+    from ava_amd import ops
+    from ava_amd._lib import AvaError
+    q = torch.zeros((2, 100, 64), device="cuda")
+    with pytest.raises(AvaError):
+        ops.delta_rule_from(q, q, q, torch.zeros((2, 100), device="cuda"))
