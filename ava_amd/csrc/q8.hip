@@ -107,12 +107,14 @@ struct EpiArgs {
 };
 
 // LDS position of 16-byte chunk c of tile row r: the chunk index XOR a function of the row, so that
-// the fragment reads (32 consecutive rows, one chunk) and the staging writes (whole rows) touch
-// distinct banks with either 32 or 64 four-byte banks. CPR = chunks per row (4 or 8).
+// the fragment reads (32 consecutive rows, one chunk) and the staging writes (whole rows) do not
+// collide in banks. For 64-byte rows, c ^ ((r >> 2) & 3) measured conflict-free on gfx950 (207 of
+// about 210 B/clk/CU for ds_read_b128, against 61 unswizzled and 117 for c ^ (((r>>1)^(r>>3)) & 3)).
+// CPR = chunks per row (4 or 8).
 template <int CPR>
 __device__ __forceinline__ int swz(int r, int c) {
-    if (CPR == 4) return c ^ (((r >> 1) ^ (r >> 3)) & 3);
-    return c ^ ((r ^ (r >> 3)) & 7);
+    if (CPR == 4) return c ^ ((r >> 2) & 3);
+    return c ^ ((r >> 1) & 7);
 }
 
 // The product over one BM x BN output tile: 256 threads = 4 waves in WM x (4 / WM); wave tile
@@ -297,12 +299,420 @@ __global__ __launch_bounds__(256, 2) void q8_gemm_kernel(const int8_t *__restric
     }
 }
 
-// Tile shapes (BM, BN, WM); AVA_Q8_TILE=<index> overrides the choice per plane count (tuning).
+// ------------------------------------------------------------------ the product, direct-to-LDS form
+//
+// The same product with the operands brought into LDS by global_load_lds_dwordx4 (gfx950): each
+// load instruction writes 64 lanes x 16 bytes = 16 rows of 64 bytes contiguously, lane l taking
+// row r0 + l/4 and the 16-byte chunk that lands in slot l%4 under the row's swizzle, so no register
+// holds staged data. S LDS stages form a ring: at step kt a wave waits for its own loads of step kt,
+// one barrier makes every wave's loads visible (and frees the stage of step kt-1), the loads of step
+// kt+S-1 are issued into that freed stage, and step kt is multiplied. NW waves = WM x WN.
+
+// ds_read_b128 of an LDS pointer, issued as inline assembly so the compiler's wait insertion, which
+// cannot tell the stages apart and would wait for every direct-to-LDS load in flight, does not see it.
+// The caller waits with lgkm_wait<N>() and passes every fragment through tie() before using it.
+__device__ __forceinline__ i32x4 lds_read128(const int8_t *p) {
+    i32x4 v;
+#if defined(__HIP_DEVICE_COMPILE__)
+    const unsigned a = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) int8_t *)p;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+#else
+    v = *reinterpret_cast<const i32x4 *>(p);
+#endif
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt");
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+#endif
+}
+// An empty asm that "rewrites" v after the wait above it, so no use of v can move before the wait.
+__device__ __forceinline__ void tie(i32x4 &v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(v));
+#endif
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] in [15:14]
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// global_load_lds_dwordx4: 16 bytes per lane from `g` to LDS at `l` + 16 x lane (l wave-uniform). The
+// address-space cast exists only in the device pass (the host pass never sees the body).
+__device__ __forceinline__ void dma16(const void *g, void *l) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
+#endif
+}
+
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_dma_kernel(const int8_t *__restrict__ xq,
+                                                                     const int32_t *__restrict__ xexp, int m, int n,
+                                                                     int ldk, const int8_t *__restrict__ qt,
+                                                                     const float *__restrict__ scale, EpiArgs ep) {
+    constexpr int NT = 64 * WM * WN, BK = 64, CPR = 4, LDS_ROW = BK;
+    constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
+    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
+    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;  // bytes per stage
+    constexpr int A_INS = A_ROWS / 16, B_INS = BN / 16;              // 1 KB load instructions per stage
+    constexpr int NWAVE = WM * WN;
+    static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
+    constexpr int LPW = (A_INS + B_INS) / NWAVE;  // load instructions per wave per stage
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
+    const int total = tiles_m * tiles_n;
+    int tile = blockIdx.x;
+    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    // this lane's source for each of the wave's load instructions (instruction ins covers stage rows
+    // 16 ins .. 16 ins + 15; A rows first (plane-major), then B rows)
+    const int8_t *src[LPW];
+    int dst_off[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int ins = wave * LPW + i;
+        const int srow = ins * 16 + (lane >> 2);  // stage row
+        if (srow < A_ROWS) {
+            const int p = srow / BM, rr = srow % BM;
+            const int c = swz<CPR>(rr, lane & 3);  // the logical chunk whose swizzled slot is lane & 3
+            const int row = min(m0 + rr, m - 1);
+            src[i] = xq + ((size_t)p * m + row) * ldk + c * 16;
+        } else {
+            const int rr = srow - A_ROWS;
+            const int c = swz<CPR>(rr, lane & 3);
+            const int col = min(n0 + rr, n - 1);
+            src[i] = qt + (size_t)col * ldk + c * 16;
+        }
+        dst_off[i] = ins * 1024;
+    }
+    auto issue = [&](int kt, int stage) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < LPW; i++) dma16(src[i] + k0, smem + stage * STAGE + dst_off[i]);
+    };
+
+    i32x16 acc[P][FM][FN];
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
+
+    const int KT = ldk / BK;
+#pragma unroll
+    for (int s0 = 0; s0 < S - 1; s0++) issue(min(s0, KT - 1), s0);
+
+    const int frow = lane & 31, fc = lane >> 5;
+    for (int kt = 0; kt < KT; kt++) {
+        const int stage = kt % S;
+        wait_vm<(S - 2) * LPW>();  // this wave's loads of step kt are in LDS
+        __syncthreads();            // ... and every wave's; the stage of step kt-1 is free
+        issue(min(kt + S - 1, KT - 1), (kt + S - 1) % S);
+        const int8_t *la = smem + stage * STAGE;
+        const int8_t *lb = la + A_ROWS * LDS_ROW;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ks++) {
+            i32x4 bf[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int r = wn * NW + j * 32 + frow;
+                bf[j] = *reinterpret_cast<const i32x4 *>(lb + r * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
+            }
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                i32x4 af[FM];
+#pragma unroll
+                for (int i = 0; i < FM; i++) {
+                    const int r = wm * MW + i * 32 + frow;
+                    af[i] = *reinterpret_cast<const i32x4 *>(la + (p * BM + r) * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
+                }
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[p][i][j], 0, 0, 0);
+            }
+        }
+    }
+    wait_vm<0>();
+    __syncthreads();
+
+    // epilogue (as q8_gemm_kernel's)
+    int *s_exp = reinterpret_cast<int *>(smem);
+    if (EPI != EPI_ACC) {
+        for (int i = tid; i < BM; i += NT) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        __syncthreads();
+    }
+    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + wn * NW + j * 32 + ccol;
+        const bool col_ok = col < n;
+        const int colc = col_ok ? col : n - 1;
+        const float sc = scale[colc];
+        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int rbase = wm * MW + i * 32 + rsub;
+            if (EPI == EPI_ACC) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
+                    if (row < m && col_ok)
+#pragma unroll
+                        for (int p = 0; p < P; p++)
+                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
+                }
+                continue;
+            }
+            float *ybase = reinterpret_cast<float *>(ep.y);
+            float prev[16];
+            if (EPI == EPI_ADD) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
+                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
+                float v;
+                if (P == 1) {
+                    v = (float)acc[0][i][j][r];
+                } else {
+                    double A = (double)acc[0][i][j][r];
+#pragma unroll
+                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
+                    v = (float)A;
+                }
+                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
+                v = v * sc;
+                if (EPI == EPI_MUL) v = v * cv;
+                if (EPI == EPI_ADD) v = prev[r] + v;
+                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ the product, software-pipelined form
+//
+// One wave per SIMD (4 waves, up to 512 registers each: the P x FM x FN accumulators in AGPRs) and an
+// explicit pipeline in every wave: during step kt's MFMAs the fragments of step kt+1 are already being
+// read from LDS (inline-assembly reads, explicit lgkmcnt waits), and the direct-to-LDS loads of step
+// kt+S run S-1 steps ahead in an S-stage ring. At the single barrier of step kt, stage kt+1 has landed
+// (each wave waited for its own loads of it) and every wave has finished reading stage kt, which the
+// loads of step kt+S then overwrite.
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_pipe_kernel(const int8_t *__restrict__ xq,
+                                                                      const int32_t *__restrict__ xexp, int m, int n,
+                                                                      int ldk, const int8_t *__restrict__ qt,
+                                                                      const float *__restrict__ scale, EpiArgs ep) {
+    constexpr int NT = 64 * WM * WN, BK = 64, CPR = 4, LDS_ROW = BK;
+    constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
+    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
+    static_assert(S >= 2 && S <= 4, "stages");
+    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;
+    constexpr int A_INS = A_ROWS / 16, B_INS = BN / 16, NWAVE = WM * WN;
+    static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
+    constexpr int LPW = (A_INS + B_INS) / NWAVE;
+    constexpr int NF = FN + P * FM;  // fragments per K substep: B then A (plane-major)
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
+    const int total = tiles_m * tiles_n;
+    int tile = blockIdx.x;
+    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    const int8_t *src[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int ins = wave * LPW + i;
+        const int srow = ins * 16 + (lane >> 2);
+        if (srow < A_ROWS) {
+            const int p = srow / BM, rr = srow % BM;
+            const int row = min(m0 + rr, m - 1);
+            src[i] = xq + ((size_t)p * m + row) * ldk + swz<CPR>(rr, lane & 3) * 16;
+        } else {
+            const int rr = srow - A_ROWS;
+            const int col = min(n0 + rr, n - 1);
+            src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane & 3) * 16;
+        }
+    }
+    const int KT = ldk / BK;
+    auto issue = [&](int kt) {
+        const int k0 = min(kt, KT - 1) * BK;  // past the end: the last step again, never read
+        int8_t *base = smem + (kt % S) * STAGE + wave * LPW * 1024;
+#pragma unroll
+        for (int i = 0; i < LPW; i++) dma16(src[i] + k0, base + i * 1024);
+    };
+    // byte offsets (within a stage) of this lane's fragments for K substep 0; substep 1 is offset ^ 32
+    int foff[NF];
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int r = A_ROWS + wn * NW + j * 32 + (lane & 31);
+        foff[j] = r * LDS_ROW + swz<CPR>(r - A_ROWS, lane >> 5) * 16;
+    }
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int r = wm * MW + i * 32 + (lane & 31);
+            foff[FN + p * FM + i] = (p * BM + r) * LDS_ROW + swz<CPR>(r, lane >> 5) * 16;
+        }
+    auto read_frags = [&](int kt, i32x4 (&f)[2][NF]) {
+        const int8_t *base = smem + (kt % S) * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int x = 0; x < NF; x++) f[ks][x] = lds_read128(base + (foff[x] ^ (ks * 32)));
+    };
+
+    i32x16 acc[P][FM][FN];
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
+
+    // prologue: stages 0 .. S-1 in flight; step 0's fragments read
+#pragma unroll
+    for (int s0 = 0; s0 < S; s0++) issue(s0);
+    wait_vm<(S - 1) * LPW>();
+    __syncthreads();
+    i32x4 fc[2][NF], fn[2][NF];
+    read_frags(0, fc);
+
+    for (int kt = 0; kt < KT; kt++) {
+        // stage kt+1 landed (own loads, then everyone's), and every wave is done reading stage kt
+        lgkm_wait<0>();
+        wait_vm<(S - 2) * LPW>();
+        __syncthreads();
+        issue(kt + S);
+        if (kt + 1 < KT) read_frags(kt + 1, fn);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+            for (int x = 0; x < NF; x++) tie(fc[ks][x]);
+#pragma unroll
+            for (int p = 0; p < P; p++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fc[ks][FN + p * FM + i], fc[ks][j],
+                                                                             acc[p][i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int x = 0; x < NF; x++) fc[ks][x] = fn[ks][x];
+    }
+    lgkm_wait<0>();
+    wait_vm<0>();
+    __syncthreads();
+
+    int *s_exp = reinterpret_cast<int *>(smem);
+    if (EPI != EPI_ACC) {
+        for (int i = tid; i < BM; i += NT) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        __syncthreads();
+    }
+    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + wn * NW + j * 32 + ccol;
+        const bool col_ok = col < n;
+        const int colc = col_ok ? col : n - 1;
+        const float sc = scale[colc];
+        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int rbase = wm * MW + i * 32 + rsub;
+            if (EPI == EPI_ACC) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
+                    if (row < m && col_ok)
+#pragma unroll
+                        for (int p = 0; p < P; p++)
+                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
+                }
+                continue;
+            }
+            float *ybase = reinterpret_cast<float *>(ep.y);
+            float prev[16];
+            if (EPI == EPI_ADD) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
+                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
+                float v;
+                if (P == 1) {
+                    v = (float)acc[0][i][j][r];
+                } else {
+                    double A = (double)acc[0][i][j][r];
+#pragma unroll
+                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
+                    v = (float)A;
+                }
+                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
+                v = v * sc;
+                if (EPI == EPI_MUL) v = v * cv;
+                if (EPI == EPI_ADD) v = prev[r] + v;
+                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
+            }
+        }
+    }
+}
+
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+int launch_pipe(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                EpiArgs ep, hipStream_t st) {
+    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    size_t lds = (size_t)S * (P * BM + BN) * 64;
+    static bool attr = false;
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_pipe_kernel<P, EPI, BM, BN, WM, WN, S>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    q8_gemm_pipe_kernel<P, EPI, BM, BN, WM, WN, S><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(xq, xexp, m, n, ldk,
+                                                                                                 qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
+}
+
+// Tile shapes. kind 0: the register-staged kernel (BM, BN, WM, BK); kind 1: the direct-to-LDS kernel
+// (BM, BN, WM, WN, S). AVA_Q8_TILE=<index> overrides the choice per plane count (tuning).
 struct TileCfg {
-    int bm, bn, wm, bk;
+    int kind, bm, bn, wm, wn, bk_or_s;
 };
-constexpr TileCfg TILES[] = {{128, 128, 2, 64}, {64, 128, 2, 64},  {128, 64, 2, 64}, {64, 256, 1, 64},
-                             {64, 64, 2, 64},   {128, 128, 2, 128}, {64, 128, 2, 128}, {64, 64, 2, 128}};
+constexpr TileCfg TILES[] = {
+    {0, 128, 128, 2, 2, 64}, {0, 64, 128, 2, 2, 64}, {1, 128, 128, 2, 2, 2}, {1, 128, 256, 2, 4, 2},
+    {1, 256, 128, 4, 2, 2},  {2, 128, 128, 2, 2, 3}, {2, 128, 128, 2, 2, 4}, {2, 64, 256, 1, 4, 3},
+    {2, 128, 64, 2, 2, 3},   {2, 256, 128, 2, 2, 2}, {2, 128, 256, 2, 2, 2}, {2, 64, 128, 2, 2, 4}};
 constexpr int NTILES = sizeof(TILES) / sizeof(TILES[0]);
 
 int tile_override() {
@@ -331,17 +741,44 @@ int launch_tile(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
     return AVA_OK;
 }
 
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+int launch_dma(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+               EpiArgs ep, hipStream_t st) {
+    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    size_t lds = (size_t)S * (P * BM + BN) * 64;
+    if (lds < (size_t)BM * 4) lds = (size_t)BM * 4;
+    static bool attr = false;
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(xq, xexp, m, n, ldk,
+                                                                                                qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
+}
+
 template <int P, int EPI>
 int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                 EpiArgs ep, hipStream_t st) {
     int t = tile_override();
-    if (t < 0) t = P == 1 ? 0 : 1;  // defaults
-    if (ldk % (2 * TILES[t].bk)) t = P == 1 ? 0 : 1;  // an even number of K steps
-#define AVA_T(I)                                                                                              \
-    if (t == I)                                                                                               \
-        return launch_tile<P, EPI, TILES[I].bm, TILES[I].bn, TILES[I].wm, TILES[I].bk>(xq, xexp, m, n, ldk, qt, \
-                                                                                      scale, ep, st);
-    AVA_T(0) AVA_T(1) AVA_T(2) AVA_T(3) AVA_T(4) AVA_T(5) AVA_T(6) AVA_T(7)
+    if (t < 0) t = 3;  // the direct-to-LDS 128 x 256 tile, 8 waves (measured best for every shape here)
+#define AVA_T(I)                                                                                                   \
+    if (t == I) {                                                                                                  \
+        constexpr TileCfg c = TILES[I];                                                                            \
+        if constexpr (c.kind == 0)                                                                                 \
+            return launch_tile<P, EPI, c.bm, c.bn, c.wm, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st);       \
+        else if constexpr (c.kind == 1 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
+                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0)                                          \
+            return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
+        else if constexpr (c.kind == 2 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
+                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0 && P * c.bm / c.wm * c.bn / c.wn <= 16384) \
+            return launch_pipe<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
+        else                                                                                                       \
+            return ava::fail(AVA_ERR_UNSUPPORTED, "q8 product: tile %d does not fit %d planes", I, P);             \
+    }
+    AVA_T(0) AVA_T(1) AVA_T(2) AVA_T(3) AVA_T(4) AVA_T(5) AVA_T(6) AVA_T(7) AVA_T(8) AVA_T(9) AVA_T(10) AVA_T(11)
 #undef AVA_T
     return ava::fail(AVA_ERR_ARG, "q8 product: tile %d", t);
 }
