@@ -103,14 +103,15 @@ int mem_scan_strided(const float *q, const float *k, const float *e, const float
                      int B, int T, int nh, int ld, int g, int ldg, float m, float cap, float *F, float *S, float *y,
                      int ldy, hipStream_t st);
 
+int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const float *ba, const float *bb,
+              const float *off, const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out,
+              float m, float cap, float *F, float *S, float *y, hipStream_t st);
+
 // glue.hip
 int embed(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, hipStream_t st);
 int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
                float *hout, hipStream_t st);
 int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st);
-int mem_prep(float *P, const float *G, int n, int d, int nh, int r, const float *ba, const float *bb, const float *off,
-             const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out, float *la, float *b,
-             hipStream_t st);
 int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, int8_t *xq, int32_t *xexp, int ldq,
              hipStream_t st);
 int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,

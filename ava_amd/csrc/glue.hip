@@ -1,7 +1,7 @@
 // The per-row kernels between the products of one Ava-0.4 block (gfx950): the token embedding,
-// RMSNorm fused with the split-plane int8 quantizer, the memory's key/value/gate preparation and its
-// read-out (head norm times silu(g)), the f32 gate projections, the engram's causal read, and the
-// dense (DenseFormer) mix.
+// RMSNorm fused with the split-plane int8 quantizer, the memory's read-out (head norm times silu(g)),
+// the f32 gate projections, the engram's causal read, and the dense (DenseFormer) mix. (The memory's
+// key/value/gate preparation is fused into its scan, mem.hip.)
 //
 // Row kernels run one wavefront per row with the row in registers (d <= 2048: NV float4 per lane),
 // so a row is read once from HBM and every reduction is a wave reduction (no LDS, no barrier).
@@ -16,12 +16,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float NORM_EPS = 1e-5f;  // gpu/model.rs:36
 
-__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }
-__device__ __forceinline__ float log_sigmoid_ref(float x) {
-    const float soft = logf(expf(-fabsf(x)) * 1.0f + 1.0f);
-    const float r = -x > 0.0f ? -x : 0.0f;
-    return -(r + soft);
-}
 
 // Write one row's P planes (the row's values in registers, NV float4 chunks per lane at columns
 // 4 (i*64 + lane)), its exponent, and zero the K padding [k, ldq).
@@ -122,129 +116,56 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
 // ------------------------------------------------------------------ f32 gate projections
 
 // G [n][nc] = h [n][d] . W [d][nc] in f32 (the reference keeps the gate projections f32:
-// gpu/arch.rs:1914-1936). 64 rows x nc (<= 128) columns per block; K in steps of 32 through LDS.
-constexpr int GR = 64, GK = 32;
-__global__ __launch_bounds__(256) void gate_gemm_kernel(const float *__restrict__ h, int n, int d,
+// gpu/arch.rs:1914-1936), on the fp32 MFMA (v_mfma_f32_32x32x2_f32). Block = 128 rows x NC columns
+// (NC = nc rounded up to 32, <= 128); wave w owns rows 32w..32w+31; K in steps of 32 through LDS
+// (h tile row-major, W tile row-major, both padded), each step 16 MFMA k-substeps per column block.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int GR = 128, GK = 32;
+template <int NCB>  // column blocks of 32
+__global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict__ h, int n, int d,
                                                         const float *__restrict__ w, int nc, float *__restrict__ g) {
     __shared__ float sh[GR][GK + 1];
-    __shared__ float sw[GK][128];
-    const int tid = threadIdx.x;
-    const int r0 = blockIdx.x * GR;
-    // thread -> rows (tid / 16) * 4 .. +3, columns (tid % 16) + 16 c, c < nc/16
-    const int tr = (tid >> 4) * 4, tc = tid & 15;
-    float acc[4][8];
-#pragma unroll
-    for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int b = 0; b < 8; b++) acc[a][b] = 0.0f;
-    for (int k0 = 0; k0 < d; k0 += GK) {
-        for (int i = tid; i < GR * GK; i += 256) {
-            const int rr = i / GK, kk = i % GK;
-            const int row = r0 + rr;
-            sh[rr][kk] = (row < n && k0 + kk < d) ? h[(size_t)row * d + k0 + kk] : 0.0f;
-        }
-        for (int i = tid; i < GK * 128; i += 256) {
-            const int kk = i / 128, cc = i % 128;
-            sw[kk][cc] = (cc < nc && k0 + kk < d) ? w[(size_t)(k0 + kk) * nc + cc] : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll 4
-        for (int kk = 0; kk < GK; kk++) {
-            float hv[4], wv[8];
-#pragma unroll
-            for (int a = 0; a < 4; a++) hv[a] = sh[tr + a][kk];
-#pragma unroll
-            for (int b = 0; b < 8; b++) wv[b] = sw[kk][tc + 16 * b];
-#pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int b = 0; b < 8; b++) acc[a][b] = fmaf(hv[a], wv[b], acc[a][b]);
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const int row = r0 + tr + a;
-        if (row >= n) continue;
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const int c = tc + 16 * b;
-            if (c < nc) g[(size_t)row * nc + c] = acc[a][b];
-        }
-    }
-}
-
-// ------------------------------------------------------------------ memory preparation
-
-// Per (row, head), one wave, lane = channel c of the head (gpu/arch.rs:1873-1941, gpu/lif.cu's
-// wprepc semantics): from P = [q | k | v | we | g] (raw projections, [n][5d]) and G = [za | zb |
-// z1a | z1b] ([n][2 nh + 2 r]):
-//   q <- q / |q|, k <- k / |k|, e = (k_raw + we) / |k_raw + we|   (|x| = (sum x^2 + 1e-6)^1/2)
-//   v <- v (1 + p0) + v0 p1 (value residual, blocks after the first; v0 = the first block's v)
-//   la_c = logsig(((za_h + ba_h) + off_c) + (z1a . Wa2)_c),  b_c = 2 sigmoid((zb_h + bb_h) + (z1b . Wb2)_c)
-// written in place (q, k, v; e over the we columns) and into la, b [n][d]. With vfirst_out the raw
-// v is saved for later blocks.
-struct PrepArgs {
-    float *P;  // [n][5d]
-    const float *G;
-    int n, d, nh, r;
-    const float *ba, *bb, *off, *wa2, *wb2;  // [nh], [nh], [d], [r][d], [r][d]
-    const float *vres;                        // [2] or NULL
-    const float *v0;                          // [n][d] or NULL
-    float *v0_out;                            // [n][d] or NULL
-    float *la, *b;                            // [n][d]
-};
-
-__global__ __launch_bounds__(256) void mem_prep_kernel(PrepArgs p) {
-    extern __shared__ float smem[];  // wa2, wb2 slices of this head: [2][r][64]
-    const int hh = blockIdx.y;
+    __shared__ float sw[GK][NCB * 32 + 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float *swa = smem, *swb = smem + p.r * 64;
-    for (int i = tid; i < p.r * 64; i += 256) {
-        const int rr = i >> 6, c = i & 63;
-        swa[i] = p.wa2[(size_t)rr * p.d + hh * 64 + c];
-        swb[i] = p.wb2[(size_t)rr * p.d + hh * 64 + c];
-    }
-    __syncthreads();
-    const int d = p.d, ldp = 5 * d, ldg = 2 * p.nh + 2 * p.r;
-    const int c = hh * 64 + lane;
-    const float offc = p.off[c], bah = p.ba[hh], bbh = p.bb[hh];
-    float p0 = 0.0f, p1 = 0.0f;
-    if (p.vres) {
-        p0 = p.vres[0] * 1.0f + 1.0f;
-        p1 = p.vres[1];
-    }
-    // 16 rows per block: 4 waves x 4 rows
-    for (int rr = 0; rr < 4; rr++) {
-        const int row = blockIdx.x * 16 + wave * 4 + rr;
-        if (row >= p.n) break;
-        float *Pr = p.P + (size_t)row * ldp;
-        const float *Gr = p.G + (size_t)row * ldg;
-        const float q = Pr[c], kr = Pr[d + c], v = Pr[2 * d + c], we = Pr[3 * d + c];
-        const float ek = kr + we;
-        const float sq = ava::wave_sum(q * q), sk = ava::wave_sum(kr * kr), se = ava::wave_sum(ek * ek);
-        Pr[c] = q * (1.0f / sqrtf(sq * 1.0f + 1e-6f));
-        Pr[d + c] = kr * (1.0f / sqrtf(sk * 1.0f + 1e-6f));
-        Pr[3 * d + c] = ek * (1.0f / sqrtf(se * 1.0f + 1e-6f));
-        if (p.v0_out) p.v0_out[(size_t)row * d + c] = v;
-        if (p.v0) Pr[2 * d + c] = v * p0 + p.v0[(size_t)row * d + c] * p1;
-        const float za = Gr[hh] + bah, zb = Gr[p.nh + hh] + bbh;
-        // lanes 0..r-1 hold z1a, lanes 32..32+r-1 hold z1b; each is broadcast with readlane
-        const int zl_i = lane < 32 ? lane : lane - 32 + p.r;
-        const float zl = (lane & 31) < p.r ? Gr[2 * p.nh + zl_i] : 0.0f;
-        const int zbits = __float_as_int(zl);
-        float lra = 0.0f, lrb = 0.0f;
+    const int r0 = blockIdx.x * GR;
+    f32x16 acc[NCB];
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
-            if (j < p.r) {
-                const float za_j = __int_as_float(__builtin_amdgcn_readlane(zbits, j));
-                const float zb_j = __int_as_float(__builtin_amdgcn_readlane(zbits, 32 + j));
-                lra = fmaf(za_j, swa[j * 64 + lane], lra);
-                lrb = fmaf(zb_j, swb[j * 64 + lane], lrb);
+    for (int cb = 0; cb < NCB; cb++) acc[cb] = f32x16{};
+    for (int k0 = 0; k0 < d; k0 += GK) {
+        // h tile: 128 rows x 32 floats, 8 threads per row, float4 each
+        for (int i = tid; i < GR * GK / 4; i += 256) {
+            const int rr = i >> 3, kk = (i & 7) * 4;
+            const int row = min(r0 + rr, n - 1);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(h + (size_t)row * d + k0 + kk);
+#pragma unroll
+            for (int z = 0; z < 4; z++) sh[rr][kk + z] = v[z];
+        }
+        for (int i = tid; i < GK * NCB * 32; i += 256) {
+            const int kk = i / (NCB * 32), cc = i % (NCB * 32);
+            sw[kk][cc] = cc < nc ? w[(size_t)(k0 + kk) * nc + cc] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < GK; ks += 2) {
+            const float a = sh[wave * 32 + (lane & 31)][ks + (lane >> 5)];
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                const float b = sw[ks + (lane >> 5)][cb * 32 + (lane & 31)];
+                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[cb], 0, 0, 0);
             }
         }
-        p.la[(size_t)row * d + c] = log_sigmoid_ref((za + offc) + lra);
-        p.b[(size_t)row * d + c] = sigmoid_ref(zb + lrb) * 2.0f + 0.0f;
+        __syncthreads();
+    }
+    // lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32 of each 32 x 32 block
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+        const int col = cb * 32 + (lane & 31);
+        if (col >= nc) continue;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = r0 + wave * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (row < n) g[(size_t)row * nc + col] = acc[cb][r];
+        }
     }
 }
 
@@ -459,20 +380,15 @@ int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8
 }
 
 int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st) {
-    AVA_REQUIRE(nc <= 128, AVA_ERR_SHAPE, "gate_gemm: %d columns (<= 128)", nc);
-    gate_gemm_kernel<<<ceil_div(n, GR), 256, 0, st>>>(h, n, d, w, nc, g);
+    AVA_REQUIRE(nc > 0 && nc <= 128 && d % GK == 0, AVA_ERR_SHAPE, "gate_gemm: %d columns (<= 128), d=%d", nc, d);
+    const int blocks = ceil_div(n, GR);
+    switch ((nc + 31) / 32) {
+    case 1: gate_mfma_kernel<1><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    case 2: gate_mfma_kernel<2><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    case 3: gate_mfma_kernel<3><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    default: gate_mfma_kernel<4><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    }
     AVA_LAUNCHED("gate_gemm");
-    return AVA_OK;
-}
-
-int mem_prep(float *P, const float *G, int n, int d, int nh, int r, const float *ba, const float *bb, const float *off,
-             const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out, float *la, float *b,
-             hipStream_t st) {
-    AVA_REQUIRE(d == nh * 64 && r > 0 && r <= 32, AVA_ERR_SHAPE, "mem_prep: d=%d nh=%d r=%d", d, nh, r);
-    PrepArgs a{P, G, n, d, nh, r, ba, bb, off, wa2, wb2, vres, v0, v0_out, la, b};
-    dim3 grid(ceil_div(n, 16), nh), block(256);
-    mem_prep_kernel<<<grid, block, sizeof(float) * 2 * r * 64, st>>>(a);
-    AVA_LAUNCHED("mem_prep");
     return AVA_OK;
 }
 

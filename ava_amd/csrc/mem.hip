@@ -17,6 +17,8 @@
 // columns 64h..64h+63 (ld = 64, nh = 1 is the [BH][T][64] layout of the C ABI; ld = d, nh = d / 64 is
 // the block stack's [B T][d] projection output, read in place). Per-head gates (G1) are one value
 // per (row, head) at column h of a [B T][ldg] matrix.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace {
@@ -167,6 +169,190 @@ __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ the block's memory, prep fused
+
+// The memory of one Ava-0.4 block in one kernel: the preparation of gpu/arch.rs:1873-1941 (unit q, k
+// and erase key, value residual, per-channel log alpha and write strength from the f32 gate
+// projections) is computed while each 16-step chunk is staged, then the same register-resident scan
+// as mem_scan_kernel runs on it. Staging: wave w prepares steps t0 + 4w .. t0 + 4w + 3 with lane =
+// channel, so every norm is a wave reduction and the rank-r gate read-outs are r FMAs per lane with
+// the row's z1 values broadcast by readlane. Nothing of the preparation goes through HBM.
+struct FusedArgs {
+    const float *P;    // [B T][5d]: q | k | v | we | g (raw projections)
+    const float *G;    // [B T][2 nh + 2 r]: za | zb | z1a | z1b
+    const float *ba, *bb, *off, *wa2, *wb2;  // [nh], [nh], [d], [r][d], [r][d]
+    const float *vres;                       // [2] (value residual, blocks after the first) or NULL
+    const float *v0;                         // [B T][d]: the first block's raw v (read) or NULL
+    float *v0_out;                           // [B T][d]: write the raw v (first block) or NULL
+    int T, nh, r;
+    float m, cap;
+    float *F, *S, *y;  // F, S [B nh][64][64]; y [B T][d]
+};
+
+__device__ __forceinline__ float fsig(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }
+__device__ __forceinline__ float flogsig(float x) {
+    const float soft = logf(expf(-fabsf(x)) * 1.0f + 1.0f);
+    const float r = -x > 0.0f ? -x : 0.0f;
+    return -(r + soft);
+}
+__device__ __forceinline__ float wsum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <bool MOM, bool PF>
+__global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
+    // 40 KB of LDS and at most 128 VGPRs, so all four heads' blocks of a CU are resident at once
+    // (1024 heads of config[3] on 256 CUs run as one round, not two)
+    __shared__ __attribute__((aligned(16))) float s_q[TS][HS], s_e[TS][HS], s_v[TS][HS];
+    __shared__ __attribute__((aligned(16))) float s_a[TS][HS], s_bk[TS][HS], s_abe[TS][HS];
+    __shared__ float s_wa2[32][HS], s_wb2[32][HS];
+
+    const int bh = blockIdx.x;
+    const int d = p.nh * HS, ldp = 5 * d, ldg = 2 * p.nh + 2 * p.r;
+    const int bi = bh / p.nh, hh = bh - bi * p.nh;
+    const size_t row0 = (size_t)bi * p.T;  // the stream's first row
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform, so per-step rows are scalar
+    const int j = wave * 16 + (lane & 15), i0 = (lane >> 4) * 16;  // scan: column, first row
+    const int c = hh * HS + lane;                                   // staging: this lane's channel
+
+    for (int x = tid; x < p.r * HS; x += 256) {
+        const int rr = x >> 6, cc = x & 63;
+        s_wa2[rr][cc] = p.wa2[(size_t)rr * d + hh * HS + cc];
+        s_wb2[rr][cc] = p.wb2[(size_t)rr * d + hh * HS + cc];
+    }
+    const float offc = p.off[c], bah = p.ba[hh], bbh = p.bb[hh];
+    float p0 = 0.0f, p1 = 0.0f;
+    if (p.vres) {
+        p0 = p.vres[0] * 1.0f + 1.0f;
+        p1 = p.vres[1];
+    }
+
+    float Fr[16], Sr[16];
+    float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+        Fr[m] = Fh[(i0 + m) * HS + j];
+        Sr[m] = MOM ? Sh[(i0 + m) * HS + j] : 0.0f;
+    }
+
+    // the raw inputs of this wave's 4 steps of a chunk, prefetched one chunk ahead
+    float rq[4], rk[4], rv[4], rw[4], rv0[4], rz[4], rza[4], rzb[4];
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int t = min(t0 + wave * 4 + s, p.T - 1);  // past the end: the last step, never used
+            const size_t rw_ = row0 + t;
+            const float *Pr = p.P + rw_ * ldp, *Gr = p.G + rw_ * ldg;
+            rq[s] = Pr[c];
+            rk[s] = Pr[d + c];
+            rv[s] = Pr[2 * d + c];
+            rw[s] = Pr[3 * d + c];
+            rv0[s] = p.v0 ? p.v0[rw_ * d + c] : 0.0f;
+            rz[s] = (lane & 31) < p.r ? Gr[2 * p.nh + (lane < 32 ? lane : lane - 32 + p.r)] : 0.0f;
+            rza[s] = Gr[hh];
+            rzb[s] = Gr[p.nh + hh];
+        }
+    };
+    auto stage = [&](int t0) {
+        float lra[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lrb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int jj = 0; jj < p.r; jj++) {
+            const float wa = s_wa2[jj][lane], wb = s_wb2[jj][lane];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int zi = __float_as_int(rz[s]);
+                lra[s] = fmaf(__int_as_float(__builtin_amdgcn_readlane(zi, jj)), wa, lra[s]);
+                lrb[s] = fmaf(__int_as_float(__builtin_amdgcn_readlane(zi, 32 + jj)), wb, lrb[s]);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int st = wave * 4 + s, t = t0 + st;
+            const float ek = rk[s] + rw[s];
+            const float sq = wsum(rq[s] * rq[s]), sk = wsum(rk[s] * rk[s]), se = wsum(ek * ek);
+            const float qn = rq[s] * (1.0f / sqrtf(sq * 1.0f + 1e-6f));
+            const float kn = rk[s] * (1.0f / sqrtf(sk * 1.0f + 1e-6f));
+            const float en = ek * (1.0f / sqrtf(se * 1.0f + 1e-6f));
+            float v = rv[s];
+            if (p.v0_out && t < p.T) p.v0_out[(row0 + t) * d + c] = v;
+            if (p.v0) v = v * p0 + rv0[s] * p1;
+            // alpha = exp(logsig(z)) is sigmoid(z); formed directly (equal up to rounding)
+            const float a = fsig(((rza[s] + bah) + offc) + lra[s]);
+            const float bw = fsig((rzb[s] + bbh) + lrb[s]) * 2.0f + 0.0f;
+            s_q[st][lane] = qn;
+            s_e[st][lane] = en;
+            s_v[st][lane] = v;
+            s_a[st][lane] = a;
+            s_bk[st][lane] = bw * kn;
+            s_abe[st][lane] = (a * bw) * en;
+        }
+    };
+
+    const float M = p.m, cap = p.cap;
+    float *yb = p.y + row0 * d + hh * HS + j;
+    if (PF) load(0);
+    for (int t0 = 0; t0 < p.T; t0 += TS) {
+        if (!PF) load(t0);
+        __syncthreads();  // the previous chunk's LDS reads are done
+        stage(t0);
+        __syncthreads();
+        if (PF && t0 + TS < p.T) load(t0 + TS);  // in flight during this chunk's scan
+        const int n = min(TS, p.T - t0);
+        for (int s = 0; s < n; s++) {
+            // r_j = sum_i e_i F_ij over this lane's 16 rows, then the column's four row groups
+            float r0 = 0.0f, r1 = 0.0f;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&s_e[s][i0 + 4 * cc]);
+                r0 = fmaf(e4[0], Fr[4 * cc], r0);
+                r1 = fmaf(e4[1], Fr[4 * cc + 1], r1);
+                r0 = fmaf(e4[2], Fr[4 * cc + 2], r0);
+                r1 = fmaf(e4[3], Fr[4 * cc + 3], r1);
+            }
+            float r = r0 + r1;
+            r += __shfl_xor(r, 16, 64);
+            r += __shfl_xor(r, 32, 64);
+            const float vj = s_v[s][j];
+            float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&s_q[s][i0 + 4 * cc]);
+                const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&s_a[s][i0 + 4 * cc]);
+                const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&s_bk[s][i0 + 4 * cc]);
+                const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&s_abe[s][i0 + 4 * cc]);
+#pragma unroll
+                for (int z = 0; z < 4; z++) {
+                    const int mm = 4 * cc + z;
+                    const float u = k4[z] * vj - x4[z] * r;
+                    float f;
+                    if (MOM) {
+                        Sr[mm] = fmaf(M, Sr[mm], u);
+                        f = fmaf(a4[z], Fr[mm], Sr[mm]);
+                    } else {
+                        f = fmaf(a4[z], Fr[mm], u);
+                    }
+                    f = fminf(fmaxf(f, -cap), cap);
+                    Fr[mm] = f;
+                    if (z & 1) y1 = fmaf(q4[z], f, y1);
+                    else y0 = fmaf(q4[z], f, y0);
+                }
+            }
+            float yy = y0 + y1;
+            yy += __shfl_xor(yy, 16, 64);
+            yy += __shfl_xor(yy, 32, 64);
+            if (lane < 16) yb[(size_t)(t0 + s) * d] = yy;
+        }
+    }
+
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+        Fh[(i0 + m) * HS + j] = Fr[m];
+        if (MOM) Sh[(i0 + m) * HS + j] = Sr[m];
+    }
+}
+
 }  // namespace
 
 namespace ava {
@@ -191,6 +377,31 @@ int mem_scan_strided(const float *q, const float *k, const float *e, const float
         else mem_scan_kernel<false, false><<<grid, block, 0, st>>>(a);
     }
     AVA_LAUNCHED("mem_scan");
+    return AVA_OK;
+}
+
+// The block's memory from the raw projections P and gate projections G (see mem_fused_kernel).
+int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const float *ba, const float *bb,
+              const float *off, const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out,
+              float m, float cap, float *F, float *S, float *y, hipStream_t st) {
+    AVA_REQUIRE(P && G && ba && bb && off && wa2 && wb2 && F && y, AVA_ERR_ARG, "mem_block: NULL buffer");
+    AVA_REQUIRE(m == 0.0f || S, AVA_ERR_ARG, "mem_block: momentum needs S");
+    AVA_REQUIRE(B > 0 && T > 0 && nh > 0 && r > 0 && r <= 32, AVA_ERR_SHAPE, "mem_block: B=%d T=%d nh=%d r=%d", B, T,
+                nh, r);
+    FusedArgs a{P, G, ba, bb, off, wa2, wb2, vres, v0, v0_out, T, nh, r, m, cap, F, S, y};
+    static int pf = -1;  // AVA_MEM_PF=0/1 overrides the prefetch choice (tuning)
+    if (pf < 0) {
+        const char *e = getenv("AVA_MEM_PF");
+        pf = e ? atoi(e) != 0 : 0;
+    }
+    if (m != 0.0f) {
+        if (pf) mem_fused_kernel<true, true><<<B * nh, 256, 0, st>>>(a);
+        else mem_fused_kernel<true, false><<<B * nh, 256, 0, st>>>(a);
+    } else {
+        if (pf) mem_fused_kernel<false, true><<<B * nh, 256, 0, st>>>(a);
+        else mem_fused_kernel<false, false><<<B * nh, 256, 0, st>>>(a);
+    }
+    AVA_LAUNCHED("mem_block");
     return AVA_OK;
 }
 

@@ -5,8 +5,8 @@
 // gpu/state.rs:870-1071 (block_state):
 //   spiking layer   h = rms(x) -> planes -> cur = (h.Win) (1 - beta) -> LIF scan -> x += s.Wout
 //   memory          h = rms(x) -> P = h.[Wq|Wk|Wv|We|Wg] (one product), G = h.[Wa|Wb|Wa1|Wb1] (f32)
-//                   -> prep (unit q, k, e; value residual; log alpha, b) -> scan -> head norm * silu(g)
-//                   -> x += o.Wo
+//                   -> one kernel: prep (unit q, k, e; value residual; log alpha, b) + scan
+//                   -> head norm * silu(g) -> x += o.Wo
 //   engram (one block)  h = rms(x) -> [q|k|v] -> append k, v to the store -> causal read -> x += o.Wo
 //   sparse MLP      h = rms(x) -> u = h.W1 -> kWTA, relu^2 -> planes -> x += a.W2
 //   dense mix       stream_{i+1} = x; x += sum_j w_j stream_j
@@ -69,7 +69,7 @@ struct ava_model {
     // scratch for up to `rows` rows
     size_t rows = 0, scratch_bytes = 0;
     std::vector<void *> scratch;
-    float *x = nullptr, *h = nullptr, *cur = nullptr, *P = nullptr, *G = nullptr, *la = nullptr, *bw = nullptr;
+    float *x = nullptr, *h = nullptr, *cur = nullptr, *P = nullptr, *G = nullptr;
     float *y = nullptr, *v0 = nullptr, *u = nullptr, *qkv = nullptr, *eo = nullptr;
     int8_t *xq = nullptr, *spk = nullptr;
     int32_t *xexp = nullptr;
@@ -224,8 +224,6 @@ int ensure_scratch(ava_model *m, size_t rows) {
     A((void **)&m->cur, rows * d * 4);
     A((void **)&m->P, rows * 5 * d * 4);
     A((void **)&m->G, rows * nc * 4);
-    A((void **)&m->la, rows * d * 4);
-    A((void **)&m->bw, rows * d * 4);
     A((void **)&m->y, rows * d * 4);
     if (c.value_residual) A((void **)&m->v0, rows * d * 4);
     A((void **)&m->u, rows * H * 4);
@@ -327,13 +325,11 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
         AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, st));
         const bool vr = c.value_residual != 0;
-        AVA_RUN("mem_prep", ava::mem_prep(m->P, m->G, N, d, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,
-                                          vr && i > 0 ? b.vres : nullptr, vr && i > 0 ? m->v0 : nullptr,
-                                          vr && i == 0 ? m->v0 : nullptr, m->la, m->bw, st));
         const size_t sm = (size_t)i * B * nh * 64 * 64;
-        AVA_RUN("mem_scan", ava::mem_scan_strided(m->P, m->P + d, m->P + 3 * d, m->P + 2 * d, m->la, m->bw, B, T, nh,
-                                                  5 * d, 64, d, c.momentum, c.cap, s->mem_f + sm,
-                                                  c.momentum != 0.0f ? s->mem_s + sm : nullptr, m->y, d, st));
+        AVA_RUN("mem_scan", ava::mem_block(m->P, m->G, B, T, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,
+                                           vr && i > 0 ? b.vres : nullptr, vr && i > 0 ? m->v0 : nullptr,
+                                           vr && i == 0 ? m->v0 : nullptr, c.momentum, c.cap, s->mem_f + sm,
+                                           c.momentum != 0.0f ? s->mem_s + sm : nullptr, m->y, st));
         AVA_RUN("mem_post", ava::mem_post(m->y, N, d, m->P + 4 * d, 5 * d, P, m->xq, m->xexp, ldd, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         // the engram read

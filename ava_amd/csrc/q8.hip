@@ -507,6 +507,203 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_dma_kernel(const int8
     }
 }
 
+// ------------------------------------------------------------------ the product, deep-ring form
+//
+// As q8_gemm_dma_kernel, with the direct-to-LDS loads and the fragment reads both issued as inline
+// assembly, so the compiler's wait insertion (which cannot tell LDS stages apart and would wait for
+// every load in flight before any LDS read) sees neither: the waits are explicit. An S-stage ring
+// keeps S-1 K steps of loads in flight; at step kt a wave waits until only the loads of steps kt+1 ..
+// kt+S-2 are outstanding, one barrier publishes the stage, the stage freed at step kt-1 is refilled
+// with step kt+S-1, and the fragments pass through tie() after their lgkmcnt wait.
+__device__ __forceinline__ void dma16_asm(const void *g, unsigned lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+#endif
+}
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+#else
+    return 0;
+#endif
+}
+
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_ring_kernel(const int8_t *__restrict__ xq,
+                                                                      const int32_t *__restrict__ xexp, int m, int n,
+                                                                      int ldk, const int8_t *__restrict__ qt,
+                                                                      const float *__restrict__ scale, EpiArgs ep) {
+    constexpr int NT = 64 * WM * WN, BK = 64, CPR = 4, LDS_ROW = BK;
+    constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
+    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
+    static_assert(S >= 2 && S <= 8, "stages");
+    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;
+    constexpr int A_INS = A_ROWS / 16, B_INS = BN / 16, NWAVE = WM * WN;
+    static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
+    constexpr int LPW = (A_INS + B_INS) / NWAVE;
+    static_assert((S - 2) * LPW < 64, "vmcnt range");
+    constexpr int NF = FN + P * FM;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
+    const int total = tiles_m * tiles_n;
+    int tile = blockIdx.x;
+    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    const int8_t *src[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int ins = wave * LPW + i;
+        const int srow = ins * 16 + (lane >> 2);
+        if (srow < A_ROWS) {
+            const int p = srow / BM, rr = srow % BM;
+            const int row = min(m0 + rr, m - 1);
+            src[i] = xq + ((size_t)p * m + row) * ldk + swz<CPR>(rr, lane & 3) * 16;
+        } else {
+            const int rr = srow - A_ROWS;
+            const int col = min(n0 + rr, n - 1);
+            src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane & 3) * 16;
+        }
+    }
+    const unsigned lds0 = lds_addr(smem);
+    const int KT = ldk / BK;
+    auto issue = [&](int kt) {
+        const int k0 = min(kt, KT - 1) * BK;  // past the end: the last step again, never read
+        const unsigned base = lds0 + (unsigned)((kt % S) * STAGE + wave * LPW * 1024);
+#pragma unroll
+        for (int i = 0; i < LPW; i++) dma16_asm(src[i] + k0, base + i * 1024);
+    };
+    int foff[NF];
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int r = A_ROWS + wn * NW + j * 32 + (lane & 31);
+        foff[j] = r * LDS_ROW + swz<CPR>(r - A_ROWS, lane >> 5) * 16;
+    }
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int r = wm * MW + i * 32 + (lane & 31);
+            foff[FN + p * FM + i] = (p * BM + r) * LDS_ROW + swz<CPR>(r, lane >> 5) * 16;
+        }
+
+    i32x16 acc[P][FM][FN];
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
+
+#pragma unroll
+    for (int s0 = 0; s0 < S - 1; s0++) issue(s0);
+
+    for (int kt = 0; kt < KT; kt++) {
+        wait_vm<(S - 2) * LPW>();  // this wave's loads of step kt have landed
+        __builtin_amdgcn_s_barrier();  // ... and every wave's; every wave is done reading step kt-1's stage
+        issue(kt + S - 1);
+        const int8_t *base = smem + (kt % S) * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            i32x4 f[NF];
+#pragma unroll
+            for (int x = 0; x < NF; x++) f[x] = lds_read128(base + (foff[x] ^ (ks * 32)));
+            lgkm_wait<0>();
+#pragma unroll
+            for (int x = 0; x < NF; x++) tie(f[x]);
+#pragma unroll
+            for (int p = 0; p < P; p++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[FN + p * FM + i], f[j], acc[p][i][j], 0,
+                                                                             0, 0);
+        }
+    }
+    wait_vm<0>();
+    __syncthreads();
+
+    int *s_exp = reinterpret_cast<int *>(smem);
+    if (EPI != EPI_ACC) {
+        for (int i = tid; i < BM; i += NT) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        __syncthreads();
+    }
+    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + wn * NW + j * 32 + ccol;
+        const bool col_ok = col < n;
+        const int colc = col_ok ? col : n - 1;
+        const float sc = scale[colc];
+        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int rbase = wm * MW + i * 32 + rsub;
+            if (EPI == EPI_ACC) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
+                    if (row < m && col_ok)
+#pragma unroll
+                        for (int p = 0; p < P; p++)
+                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
+                }
+                continue;
+            }
+            float *ybase = reinterpret_cast<float *>(ep.y);
+            float prev[16];
+            if (EPI == EPI_ADD) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
+                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
+                float v;
+                if (P == 1) {
+                    v = (float)acc[0][i][j][r];
+                } else {
+                    double A = (double)acc[0][i][j][r];
+#pragma unroll
+                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
+                    v = (float)A;
+                }
+                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
+                v = v * sc;
+                if (EPI == EPI_MUL) v = v * cv;
+                if (EPI == EPI_ADD) v = prev[r] + v;
+                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
+            }
+        }
+    }
+}
+
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+int launch_ring(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                EpiArgs ep, hipStream_t st) {
+    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    size_t lds = (size_t)S * (P * BM + BN) * 64;
+    static bool attr = false;
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_ring_kernel<P, EPI, BM, BN, WM, WN, S>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    q8_gemm_ring_kernel<P, EPI, BM, BN, WM, WN, S><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(xq, xexp, m, n, ldk,
+                                                                                                 qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
+}
+
 // ------------------------------------------------------------------ the product, software-pipelined form
 //
 // One wave per SIMD (4 waves, up to 512 registers each: the P x FM x FN accumulators in AGPRs) and an
@@ -711,8 +908,8 @@ struct TileCfg {
 };
 constexpr TileCfg TILES[] = {
     {0, 128, 128, 2, 2, 64}, {0, 64, 128, 2, 2, 64}, {1, 128, 128, 2, 2, 2}, {1, 128, 256, 2, 4, 2},
-    {1, 256, 128, 4, 2, 2},  {2, 128, 128, 2, 2, 3}, {2, 128, 128, 2, 2, 4}, {2, 64, 256, 1, 4, 3},
-    {2, 128, 64, 2, 2, 3},   {2, 256, 128, 2, 2, 2}, {2, 128, 256, 2, 2, 2}, {2, 64, 128, 2, 2, 4}};
+    {1, 256, 128, 4, 2, 2},  {2, 128, 128, 2, 2, 3}, {3, 128, 256, 2, 4, 3}, {3, 128, 256, 2, 4, 4},
+    {3, 128, 128, 2, 2, 4},  {3, 256, 128, 4, 2, 3}, {3, 128, 128, 2, 4, 4}, {3, 64, 256, 1, 4, 4}};
 constexpr int NTILES = sizeof(TILES) / sizeof(TILES[0]);
 
 int tile_override() {
@@ -772,6 +969,10 @@ int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
         else if constexpr (c.kind == 1 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
                            ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0)                                          \
             return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
+        else if constexpr (c.kind == 3 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
+                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0 && (c.bm / c.wm) % 32 == 0 &&            \
+                           (c.bn / c.wn) % 32 == 0)                                                                \
+            return launch_ring<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
         else if constexpr (c.kind == 2 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
                            ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0 && P * c.bm / c.wm * c.bn / c.wn <= 16384) \
             return launch_pipe<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
