@@ -34,6 +34,63 @@ struct MemArgs {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// v[l] + v[l ^ 16] and v[l] + v[l ^ 32] in every lane l, through the VALU lane swaps of gfx950
+// (v_permlane16_swap / v_permlane32_swap: no LDS round trip). With both operands v, the swap leaves
+// v[l] in one result and v[l ^ 16] (v[l ^ 32]) in the other.
+__device__ __forceinline__ float xsum16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xsum32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// One step of the recurrence on this lane's 16 rows (i0..i0+15) of column j, with the step's staged
+// inputs e, q, a, bk = b k, abe = a b e at rows i0.. and the value v_j: F (and S) updated in place;
+// returns y_j = sum_i q_i F_ij over the whole column (the read after the write).
+template <bool MOM>
+__device__ __forceinline__ float scan_step(float (&Fr)[16], float (&Sr)[16], const float *e, const float *q,
+                                           const float *a, const float *bk, const float *abe, float vj, float M,
+                                           float cap) {
+    // r_j = sum_i e_i F_ij: two partial chains over the lane's rows, then the column's four row groups
+    float r0 = 0.0f, r1 = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+        const f32x4 e4 = *reinterpret_cast<const f32x4 *>(e + 4 * cc);
+        r0 = fmaf(e4[0], Fr[4 * cc], r0);
+        r1 = fmaf(e4[1], Fr[4 * cc + 1], r1);
+        r0 = fmaf(e4[2], Fr[4 * cc + 2], r0);
+        r1 = fmaf(e4[3], Fr[4 * cc + 3], r1);
+    }
+    const float r = xsum32(xsum16(r0 + r1));
+    float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+        const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q + 4 * cc);
+        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(a + 4 * cc);
+        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(bk + 4 * cc);
+        const f32x4 x4 = *reinterpret_cast<const f32x4 *>(abe + 4 * cc);
+#pragma unroll
+        for (int z = 0; z < 4; z++) {
+            const int mm = 4 * cc + z;
+            const float u = fmaf(-x4[z], r, k4[z] * vj);  // b_i k_i v_j - a_i b_i e_i r_j
+            float f;
+            if (MOM) {
+                Sr[mm] = fmaf(M, Sr[mm], u);
+                f = fmaf(a4[z], Fr[mm], Sr[mm]);
+            } else {
+                f = fmaf(a4[z], Fr[mm], u);
+            }
+            f = __builtin_amdgcn_fmed3f(f, -cap, cap);  // clamp to +-cap
+            Fr[mm] = f;
+            if (z & 1) y1 = fmaf(q4[z], f, y1);
+            else y0 = fmaf(q4[z], f, y0);
+        }
+    }
+    return xsum32(xsum16(y0 + y1));
+}
+
 template <bool G1, bool MOM>
 __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
     __shared__ __attribute__((aligned(16))) float s_q[TS][HS], s_e[TS][HS], s_v[TS][HS];
@@ -107,53 +164,8 @@ __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
         if (t0 + TS < p.T) load(t0 + TS);  // in flight during this chunk's scan
         const int n = min(TS, p.T - t0);
         for (int s = 0; s < n; s++) {
-            float ev[16], qv[16], av[16], bkv[16], abev[16];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&s_e[s][i0 + 4 * c]);
-                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&s_q[s][i0 + 4 * c]);
-                const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&s_a[s][i0 + 4 * c]);
-                const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&s_bk[s][i0 + 4 * c]);
-                const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&s_abe[s][i0 + 4 * c]);
-#pragma unroll
-                for (int z = 0; z < 4; z++) {
-                    ev[4 * c + z] = e4[z];
-                    qv[4 * c + z] = q4[z];
-                    av[4 * c + z] = a4[z];
-                    bkv[4 * c + z] = k4[z];
-                    abev[4 * c + z] = x4[z];
-                }
-            }
-            const float vj = s_v[s][j];
-            // r_j = sum_i e_i F_ij: two partial chains, then the four row groups of this column
-            float r0 = 0.0f, r1 = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 16; m += 2) {
-                r0 = fmaf(ev[m], Fr[m], r0);
-                r1 = fmaf(ev[m + 1], Fr[m + 1], r1);
-            }
-            float r = r0 + r1;
-            r += __shfl_xor(r, 16, 64);
-            r += __shfl_xor(r, 32, 64);
-            float y0 = 0.0f, y1 = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 16; m++) {
-                const float u = bkv[m] * vj - abev[m] * r;
-                float f;
-                if (MOM) {
-                    Sr[m] = fmaf(M, Sr[m], u);
-                    f = fmaf(av[m], Fr[m], Sr[m]);
-                } else {
-                    f = fmaf(av[m], Fr[m], u);
-                }
-                f = fminf(fmaxf(f, -cap), cap);
-                Fr[m] = f;
-                if (m & 1) y1 = fmaf(qv[m], f, y1);
-                else y0 = fmaf(qv[m], f, y0);
-            }
-            float y = y0 + y1;
-            y += __shfl_xor(y, 16, 64);
-            y += __shfl_xor(y, 32, 64);
+            const float y = scan_step<MOM>(Fr, Sr, &s_e[s][i0], &s_q[s][i0], &s_a[s][i0], &s_bk[s][i0], &s_abe[s][i0],
+                                           s_v[s][j], M, cap);
             if (lane < 16) s_y[s][j] = y;
         }
         __syncthreads();
@@ -189,16 +201,22 @@ struct FusedArgs {
     float *F, *S, *y;  // F, S [B nh][64][64]; y [B T][d]
 };
 
-__device__ __forceinline__ float fsig(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }
-__device__ __forceinline__ float flogsig(float x) {
-    const float soft = logf(expf(-fabsf(x)) * 1.0f + 1.0f);
-    const float r = -x > 0.0f ? -x : 0.0f;
-    return -(r + soft);
+// sigmoid(x) = 1 / (exp(-x) + 1) with the hardware exp2 and reciprocal (a few ulp of the f32 form)
+__device__ __forceinline__ float fsig(float x) { return __builtin_amdgcn_rcpf(__expf(-x) + 1.0f); }
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+// The sum of v over the wave, in every lane: DPP within each row of 16 lanes (quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror), then the lane swaps across rows. Each stage adds the same
+// two partial sums in every lane, so all lanes hold the same bits.
 __device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    v += dppf<0x141>(v);
+    v += dppf<0x140>(v);
+    return xsum32(xsum16(v));
 }
 
 template <bool MOM, bool PF>
@@ -257,30 +275,33 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
         }
     };
     auto stage = [&](int t0) {
-        float lra[4] = {0.0f, 0.0f, 0.0f, 0.0f}, lrb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int jj = 0; jj < p.r; jj++) {
-            const float wa = s_wa2[jj][lane], wb = s_wb2[jj][lane];
+        // the rank-r gate read-outs of the wave's 4 steps on the matrix cores (v_mfma_f32_4x4x1, 16
+        // blocks): lane l gives A = z(step l & 3, jj) and B = w2(jj, channel l), and register s of the
+        // accumulator then holds sum_jj z(s, jj) w2(jj, l). The z rows pass through LDS rows of s_abe
+        // that only this wave uses and rewrites below.
+        float *zs = &s_abe[wave * 4][0];
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                const int zi = __float_as_int(rz[s]);
-                lra[s] = fmaf(__int_as_float(__builtin_amdgcn_readlane(zi, jj)), wa, lra[s]);
-                lrb[s] = fmaf(__int_as_float(__builtin_amdgcn_readlane(zi, 32 + jj)), wb, lrb[s]);
-            }
+        for (int s = 0; s < 4; s++) zs[s * HS + lane] = rz[s];
+        f32x4 lra = {0.0f, 0.0f, 0.0f, 0.0f}, lrb = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float *za = zs + (lane & 3) * HS;
+        for (int jj = 0; jj < p.r; jj++) {
+            lra = __builtin_amdgcn_mfma_f32_4x4x1f32(za[jj], s_wa2[jj][lane], lra, 0, 0, 0);
+            lrb = __builtin_amdgcn_mfma_f32_4x4x1f32(za[32 + jj], s_wb2[jj][lane], lrb, 0, 0, 0);
         }
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const int st = wave * 4 + s, t = t0 + st;
             const float ek = rk[s] + rw[s];
             const float sq = wsum(rq[s] * rq[s]), sk = wsum(rk[s] * rk[s]), se = wsum(ek * ek);
-            const float qn = rq[s] * (1.0f / sqrtf(sq * 1.0f + 1e-6f));
-            const float kn = rk[s] * (1.0f / sqrtf(sk * 1.0f + 1e-6f));
-            const float en = ek * (1.0f / sqrtf(se * 1.0f + 1e-6f));
+            const float qn = rq[s] * rsqrtf(sq + 1e-6f);
+            const float kn = rk[s] * rsqrtf(sk + 1e-6f);
+            const float en = ek * rsqrtf(se + 1e-6f);
             float v = rv[s];
             if (p.v0_out && t < p.T) p.v0_out[(row0 + t) * d + c] = v;
             if (p.v0) v = v * p0 + rv0[s] * p1;
             // alpha = exp(logsig(z)) is sigmoid(z); formed directly (equal up to rounding)
             const float a = fsig(((rza[s] + bah) + offc) + lra[s]);
-            const float bw = fsig((rzb[s] + bbh) + lrb[s]) * 2.0f + 0.0f;
+            const float bw = fsig((rzb[s] + bbh) + lrb[s]) * 2.0f;
             s_q[st][lane] = qn;
             s_e[st][lane] = en;
             s_v[st][lane] = v;
@@ -301,47 +322,8 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
         if (PF && t0 + TS < p.T) load(t0 + TS);  // in flight during this chunk's scan
         const int n = min(TS, p.T - t0);
         for (int s = 0; s < n; s++) {
-            // r_j = sum_i e_i F_ij over this lane's 16 rows, then the column's four row groups
-            float r0 = 0.0f, r1 = 0.0f;
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&s_e[s][i0 + 4 * cc]);
-                r0 = fmaf(e4[0], Fr[4 * cc], r0);
-                r1 = fmaf(e4[1], Fr[4 * cc + 1], r1);
-                r0 = fmaf(e4[2], Fr[4 * cc + 2], r0);
-                r1 = fmaf(e4[3], Fr[4 * cc + 3], r1);
-            }
-            float r = r0 + r1;
-            r += __shfl_xor(r, 16, 64);
-            r += __shfl_xor(r, 32, 64);
-            const float vj = s_v[s][j];
-            float y0 = 0.0f, y1 = 0.0f;
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&s_q[s][i0 + 4 * cc]);
-                const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&s_a[s][i0 + 4 * cc]);
-                const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&s_bk[s][i0 + 4 * cc]);
-                const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&s_abe[s][i0 + 4 * cc]);
-#pragma unroll
-                for (int z = 0; z < 4; z++) {
-                    const int mm = 4 * cc + z;
-                    const float u = k4[z] * vj - x4[z] * r;
-                    float f;
-                    if (MOM) {
-                        Sr[mm] = fmaf(M, Sr[mm], u);
-                        f = fmaf(a4[z], Fr[mm], Sr[mm]);
-                    } else {
-                        f = fmaf(a4[z], Fr[mm], u);
-                    }
-                    f = fminf(fmaxf(f, -cap), cap);
-                    Fr[mm] = f;
-                    if (z & 1) y1 = fmaf(q4[z], f, y1);
-                    else y0 = fmaf(q4[z], f, y0);
-                }
-            }
-            float yy = y0 + y1;
-            yy += __shfl_xor(yy, 16, 64);
-            yy += __shfl_xor(yy, 32, 64);
+            const float yy = scan_step<MOM>(Fr, Sr, &s_e[s][i0], &s_q[s][i0], &s_a[s][i0], &s_bk[s][i0],
+                                            &s_abe[s][i0], s_v[s][j], M, cap);
             if (lane < 16) yb[(size_t)(t0 + s) * d] = yy;
         }
     }

@@ -104,7 +104,28 @@ struct EpiArgs {
     void *y;
     int ldy;
     const float *colv;
+    int group;  // row blocks per tile group (tile_origin)
 };
+
+// The output tile of this workgroup. Workgroups are dealt round-robin to the 8 XCDs, each with its
+// own L2, so XCD x is given the x-th contiguous eighth of the tiles. The tiles go in groups of
+// `group` row blocks, rows fastest: a weight column tile is then fetched from beyond L2 once per
+// group, not once per row block, while the group's activation rows stay in L2 as the group sweeps
+// the columns. group <= 1 is plain row-major order.
+__device__ __forceinline__ void tile_origin(int tiles_m, int tiles_n, int group, int &mt, int &nt) {
+    const int total = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if (total % 8 == 0) t = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    if (group <= 1) {
+        mt = t / tiles_n;
+        nt = t - mt * tiles_n;
+        return;
+    }
+    const int span = group * tiles_n, g = t / span, r = t - g * span;
+    const int rows = min(group, tiles_m - g * group);  // the last group may be short
+    mt = g * group + r % rows;
+    nt = r / rows;
+}
 
 // LDS position of 16-byte chunk c of tile row r: the chunk index XOR a function of the row, so that
 // the fragment reads (32 consecutive rows, one chunk) and the staging writes (whole rows) do not
@@ -131,10 +152,9 @@ __global__ __launch_bounds__(256, 2) void q8_gemm_kernel(const int8_t *__restric
     int8_t *lds_b = smem + 2 * P * BM * LDS_ROW;       // [2][BN][LDS_ROW]
 
     const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    const int total = tiles_m * tiles_n;
-    int tile = blockIdx.x;
-    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    int mt, nt;
+    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -366,10 +386,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_dma_kernel(const int8
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    const int total = tiles_m * tiles_n;
-    int tile = blockIdx.x;
-    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    int mt, nt;
+    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -546,10 +565,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_ring_kernel(const int
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    const int total = tiles_m * tiles_n;
-    int tile = blockIdx.x;
-    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    int mt, nt;
+    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -729,10 +747,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_pipe_kernel(const int
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    const int total = tiles_m * tiles_n;
-    int tile = blockIdx.x;
-    if (total % 8 == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    int mt, nt;
+    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -922,6 +939,17 @@ int tile_override() {
     return v;
 }
 
+// Row blocks per tile group (tile_origin); AVA_Q8_GROUP overrides it (tuning).
+int tile_group() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_Q8_GROUP");
+        v = e ? atoi(e) : 8;
+        if (v < 1) v = 1;
+    }
+    return v;
+}
+
 template <int P, int EPI, int BM, int BN, int WM, int BK>
 int launch_tile(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                 EpiArgs ep, hipStream_t st) {
@@ -1022,7 +1050,7 @@ int q8_gemm(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_
     if (int r = check_qw(w)) return r;
     AVA_REQUIRE(xq && y, AVA_ERR_ARG, "q8 product: NULL buffer");
     if (m == 0) return AVA_OK;
-    EpiArgs ep{y, ldy, colv};
+    EpiArgs ep{y, ldy, colv, tile_group()};
     if (kind == EPI_STORE) return gemm_planes<EPI_STORE>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     if (kind == EPI_MUL) return gemm_planes<EPI_MUL>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     if (kind == EPI_ADD) return gemm_planes<EPI_ADD>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
@@ -1058,7 +1086,7 @@ extern "C" int ava_q8_gemm_acc(const int8_t *xq, int planes, int m, const ava_qw
     if (int r = check_qw(w)) return r;
     AVA_REQUIRE(xq && acc, AVA_ERR_ARG, "q8_gemm_acc: NULL buffer");
     if (m == 0) return AVA_OK;
-    EpiArgs ep{acc, w->dout, nullptr};
+    EpiArgs ep{acc, w->dout, nullptr, tile_group()};
     return gemm_planes<EPI_ACC>(planes, xq, nullptr, m, w->dout, w->ldk, w->qt, w->scale, ep, (hipStream_t)stream);
 }
 
