@@ -7,6 +7,28 @@
 
 #include "../../include/ava.h"
 
+// A raw buffer resource over [base, base + bytes): a load or store through it takes a 32-bit lane
+// offset and a wave-uniform offset, so no 64-bit address is held per lane (dword 3 = 0x00020000:
+// the gfx9-family raw 32-bit format). Accesses past `bytes` in the lane offset are dropped (loads
+// return 0) by the hardware range check; the uniform offset is not range checked.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t BufRes;
+__device__ __forceinline__ BufRes buf_res(float *base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void store_f32(BufRes r, unsigned voff, unsigned soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ float load_f32(BufRes r, unsigned voff, unsigned soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+#else
+typedef float *BufRes;  // the host pass compiles no kernel bodies
+__device__ inline BufRes buf_res(float *base, unsigned) { return base; }
+__device__ inline void store_f32(BufRes, unsigned, unsigned, float) {}
+__device__ inline float load_f32(BufRes, unsigned, unsigned) { return 0.0f; }
+#endif
+
 namespace ava {
 
 // Per-thread last error (ava_last_error).

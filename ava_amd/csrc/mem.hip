@@ -34,6 +34,18 @@ struct MemArgs {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// The sum of v over the 8 lanes l & ~7 .. l | 7, in each of them: DPP quad_perm [1,0,3,2] and
+// [2,3,0,1], then row_half_mirror (lane i <-> 7 - i of each 8). Each stage adds the same two partial
+// sums in every lane (in either order), so the 8 lanes hold the same bits.
+__device__ __forceinline__ float sum8(float v) {
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    return v + dppf<0x141>(v);
+}
 // v[l] + v[l ^ 16] and v[l] + v[l ^ 32] in every lane l, through the VALU lane swaps of gfx950
 // (v_permlane16_swap / v_permlane32_swap: no LDS round trip). With both operands v, the swap leaves
 // v[l] in one result and v[l ^ 16] (v[l ^ 32]) in the other.
@@ -45,50 +57,71 @@ __device__ __forceinline__ float xsum32(float v) {
     const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
+// The sum of v over the wave, in every lane: DPP within each row of 16 lanes (sum8, then
+// row_mirror, lane i <-> 15 - i), then the lane swaps across rows.
+__device__ __forceinline__ float wsum(float v) {
+    v = sum8(v);
+    v += dppf<0x140>(v);
+    return xsum32(xsum16(v));
+}
 
-// One step of the recurrence on this lane's 16 rows (i0..i0+15) of column j, with the step's staged
-// inputs e, q, a, bk = b k, abe = a b e at rows i0.. and the value v_j: F (and S) updated in place;
-// returns y_j = sum_i q_i F_ij over the whole column (the read after the write).
+// State layout per head: 4 waves, wave w holds columns 16w..16w+15; lane l holds rows
+// i0 = 8 (l & 7) .. i0 + 7 of the two columns j0 = 16 w + 2 (l >> 3), j0 + 1, as Fr[2 r + c] (S alike).
+// A column's 64 rows are then 8 lanes: a column sum is 8 FMAs per lane and 3 DPP adds, and a step
+// reads 10 + 1 16-byte LDS vectors per lane (the row group's e, q, a, bk, abe and the two v_j).
+__device__ __forceinline__ void lane_origin(int lane, int wave, int &i0, int &j0) {
+    i0 = (lane & 7) * 8;
+    j0 = wave * 16 + (lane >> 3) * 2;
+}
+
+// One step of the recurrence on this lane's 8 x 2 block, with the step's staged inputs e, q, a,
+// bk = b k, abe = a b e at rows i0.. and v at column j0: F (and S) updated in place; y0, y1 get
+// y_j = sum_i q_i F_ij of the two columns over all 64 rows (the read after the write).
 template <bool MOM>
-__device__ __forceinline__ float scan_step(float (&Fr)[16], float (&Sr)[16], const float *e, const float *q,
-                                           const float *a, const float *bk, const float *abe, float vj, float M,
-                                           float cap) {
-    // r_j = sum_i e_i F_ij: two partial chains over the lane's rows, then the column's four row groups
+__device__ __forceinline__ void scan_step(float (&Fr)[16], float (&Sr)[16], const float *e, const float *q,
+                                          const float *a, const float *bk, const float *abe, const float *v,
+                                          float M, float cap, float &y0, float &y1) {
+    // r_j = sum_i e_i F_ij
+    const f32x4 e0 = *reinterpret_cast<const f32x4 *>(e), e1 = *reinterpret_cast<const f32x4 *>(e + 4);
     float r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) {
-        const f32x4 e4 = *reinterpret_cast<const f32x4 *>(e + 4 * cc);
-        r0 = fmaf(e4[0], Fr[4 * cc], r0);
-        r1 = fmaf(e4[1], Fr[4 * cc + 1], r1);
-        r0 = fmaf(e4[2], Fr[4 * cc + 2], r0);
-        r1 = fmaf(e4[3], Fr[4 * cc + 3], r1);
+    for (int rr = 0; rr < 8; rr++) {
+        const float er = rr < 4 ? e0[rr] : e1[rr - 4];
+        r0 = fmaf(er, Fr[2 * rr], r0);
+        r1 = fmaf(er, Fr[2 * rr + 1], r1);
     }
-    const float r = xsum32(xsum16(r0 + r1));
-    float y0 = 0.0f, y1 = 0.0f;
+    r0 = sum8(r0);
+    r1 = sum8(r1);
+    const float v0 = v[0], v1 = v[1];
+    float ya = 0.0f, yb = 0.0f;
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) {
-        const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q + 4 * cc);
-        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(a + 4 * cc);
-        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(bk + 4 * cc);
-        const f32x4 x4 = *reinterpret_cast<const f32x4 *>(abe + 4 * cc);
+    for (int h = 0; h < 2; h++) {
+        const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q + 4 * h);
+        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(a + 4 * h);
+        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(bk + 4 * h);
+        const f32x4 x4 = *reinterpret_cast<const f32x4 *>(abe + 4 * h);
 #pragma unroll
         for (int z = 0; z < 4; z++) {
-            const int mm = 4 * cc + z;
-            const float u = fmaf(-x4[z], r, k4[z] * vj);  // b_i k_i v_j - a_i b_i e_i r_j
-            float f;
-            if (MOM) {
-                Sr[mm] = fmaf(M, Sr[mm], u);
-                f = fmaf(a4[z], Fr[mm], Sr[mm]);
-            } else {
-                f = fmaf(a4[z], Fr[mm], u);
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int mm = 2 * (4 * h + z) + c;
+                const float u = fmaf(-x4[z], c ? r1 : r0, k4[z] * (c ? v1 : v0));  // b_i k_i v_j - a_i b_i e_i r_j
+                float f;
+                if (MOM) {
+                    Sr[mm] = fmaf(M, Sr[mm], u);
+                    f = fmaf(a4[z], Fr[mm], Sr[mm]);
+                } else {
+                    f = fmaf(a4[z], Fr[mm], u);
+                }
+                f = __builtin_amdgcn_fmed3f(f, -cap, cap);  // clamp to +-cap
+                Fr[mm] = f;
+                if (c) yb = fmaf(q4[z], f, yb);
+                else ya = fmaf(q4[z], f, ya);
             }
-            f = __builtin_amdgcn_fmed3f(f, -cap, cap);  // clamp to +-cap
-            Fr[mm] = f;
-            if (z & 1) y1 = fmaf(q4[z], f, y1);
-            else y0 = fmaf(q4[z], f, y0);
         }
     }
-    return xsum32(xsum16(y0 + y1));
+    y0 = sum8(ya);
+    y1 = sum8(yb);
 }
 
 template <bool G1, bool MOM>
@@ -104,15 +137,16 @@ __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
     const size_t ybase = (size_t)bi * p.T * p.ldy + (size_t)hh * HS;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int j = wave * 16 + (lane & 15);  // this lane's column
-    const int i0 = (lane >> 4) * 16;        // this lane's first row
+    int i0, j0;
+    lane_origin(lane, wave, i0, j0);
 
     float Fr[16], Sr[16];
     float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
 #pragma unroll
     for (int m = 0; m < 16; m++) {
-        Fr[m] = Fh[(i0 + m) * HS + j];
-        Sr[m] = MOM ? Sh[(i0 + m) * HS + j] : 0.0f;
+        const int o = (i0 + (m >> 1)) * HS + j0 + (m & 1);
+        Fr[m] = Fh[o];
+        Sr[m] = MOM ? Sh[o] : 0.0f;
     }
 
     // staging: thread -> (step st, rows si..si+3)
@@ -164,9 +198,10 @@ __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
         if (t0 + TS < p.T) load(t0 + TS);  // in flight during this chunk's scan
         const int n = min(TS, p.T - t0);
         for (int s = 0; s < n; s++) {
-            const float y = scan_step<MOM>(Fr, Sr, &s_e[s][i0], &s_q[s][i0], &s_a[s][i0], &s_bk[s][i0], &s_abe[s][i0],
-                                           s_v[s][j], M, cap);
-            if (lane < 16) s_y[s][j] = y;
+            float y0, y1;
+            scan_step<MOM>(Fr, Sr, &s_e[s][i0], &s_q[s][i0], &s_a[s][i0], &s_bk[s][i0], &s_abe[s][i0], &s_v[s][j0], M,
+                           cap, y0, y1);
+            if ((lane & 7) < 2) s_y[s][j0 + (lane & 1)] = (lane & 1) ? y1 : y0;
         }
         __syncthreads();
         // write the chunk's read-outs: thread -> (step st, columns si..si+3)
@@ -176,8 +211,9 @@ __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
 
 #pragma unroll
     for (int m = 0; m < 16; m++) {
-        Fh[(i0 + m) * HS + j] = Fr[m];
-        if (MOM) Sh[(i0 + m) * HS + j] = Sr[m];
+        const int o = (i0 + (m >> 1)) * HS + j0 + (m & 1);
+        Fh[o] = Fr[m];
+        if (MOM) Sh[o] = Sr[m];
     }
 }
 
@@ -204,20 +240,6 @@ struct FusedArgs {
 // sigmoid(x) = 1 / (exp(-x) + 1) with the hardware exp2 and reciprocal (a few ulp of the f32 form)
 __device__ __forceinline__ float fsig(float x) { return __builtin_amdgcn_rcpf(__expf(-x) + 1.0f); }
 
-template <int CTRL>
-__device__ __forceinline__ float dppf(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-// The sum of v over the wave, in every lane: DPP within each row of 16 lanes (quad_perm [1,0,3,2],
-// [2,3,0,1], row_half_mirror, row_mirror), then the lane swaps across rows. Each stage adds the same
-// two partial sums in every lane, so all lanes hold the same bits.
-__device__ __forceinline__ float wsum(float v) {
-    v += dppf<0xB1>(v);
-    v += dppf<0x4E>(v);
-    v += dppf<0x141>(v);
-    v += dppf<0x140>(v);
-    return xsum32(xsum16(v));
-}
 
 template <bool MOM, bool PF>
 __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
@@ -233,7 +255,8 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
     const size_t row0 = (size_t)bi * p.T;  // the stream's first row
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform, so per-step rows are scalar
-    const int j = wave * 16 + (lane & 15), i0 = (lane >> 4) * 16;  // scan: column, first row
+    int i0, j0;  // scan: this lane's first row and column
+    lane_origin(lane, wave, i0, j0);
     const int c = hh * HS + lane;                                   // staging: this lane's channel
 
     for (int x = tid; x < p.r * HS; x += 256) {
@@ -252,8 +275,9 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
     float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
 #pragma unroll
     for (int m = 0; m < 16; m++) {
-        Fr[m] = Fh[(i0 + m) * HS + j];
-        Sr[m] = MOM ? Sh[(i0 + m) * HS + j] : 0.0f;
+        const int o = (i0 + (m >> 1)) * HS + j0 + (m & 1);
+        Fr[m] = Fh[o];
+        Sr[m] = MOM ? Sh[o] : 0.0f;
     }
 
     // the raw inputs of this wave's 4 steps of a chunk, prefetched one chunk ahead
@@ -312,7 +336,9 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
     };
 
     const float M = p.m, cap = p.cap;
-    float *yb = p.y + row0 * d + hh * HS + j;
+    // y_j is stored by lanes 8g and 8g + 1 (columns j0, j0 + 1); the step's row offset is wave-uniform
+    const unsigned ycol = hh * HS + j0 + (lane & 1);
+    const BufRes yres = buf_res(p.y + row0 * d, (unsigned)(p.T * d) * 4u);  // this stream's rows of y
     if (PF) load(0);
     for (int t0 = 0; t0 < p.T; t0 += TS) {
         if (!PF) load(t0);
@@ -321,17 +347,26 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
         __syncthreads();
         if (PF && t0 + TS < p.T) load(t0 + TS);  // in flight during this chunk's scan
         const int n = min(TS, p.T - t0);
-        for (int s = 0; s < n; s++) {
-            const float yy = scan_step<MOM>(Fr, Sr, &s_e[s][i0], &s_q[s][i0], &s_a[s][i0], &s_bk[s][i0],
-                                            &s_abe[s][i0], s_v[s][j], M, cap);
-            if (lane < 16) yb[(size_t)(t0 + s) * d] = yy;
+        auto step = [&](int s) {
+            float y0, y1;
+            scan_step<MOM>(Fr, Sr, &s_e[s][i0], &s_q[s][i0], &s_a[s][i0], &s_bk[s][i0], &s_abe[s][i0], &s_v[s][j0],
+                           M, cap, y0, y1);
+            if ((lane & 7) < 2) store_f32(yres, ycol * 4u, (unsigned)((t0 + s) * d) * 4u, (lane & 1) ? y1 : y0);
+        };
+        if (n == TS) {
+            // a whole chunk unrolled: F and S stay in fixed registers (a rolled loop rotates them)
+#pragma unroll
+            for (int s = 0; s < TS; s++) step(s);
+        } else {
+            for (int s = 0; s < n; s++) step(s);
         }
     }
 
 #pragma unroll
     for (int m = 0; m < 16; m++) {
-        Fh[(i0 + m) * HS + j] = Fr[m];
-        if (MOM) Sh[(i0 + m) * HS + j] = Sr[m];
+        const int o = (i0 + (m >> 1)) * HS + j0 + (m & 1);
+        Fh[o] = Fr[m];
+        if (MOM) Sh[o] = Sr[m];
     }
 }
 

@@ -138,6 +138,110 @@ __device__ __forceinline__ int swz(int r, int c) {
     return c ^ ((r >> 1) & 7);
 }
 
+// The product's epilogue for one wave's FM x FN blocks of 32 x 32 outputs at tile rows rw0..,
+// columns cw0..: in block (i, j) the lane holds, in register r, plane p's int32 sum for tile row
+// rw0 + 32 i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3) and column cw0 + 32 j + (lane & 31).
+// s_exp [BM] holds each tile row's exponent less 7 (P - 1). The planes combine exactly in double
+// (sum_p acc_p 2^(7(P-1-p)): integers below 2^53, so the fma is exact) and round once to f32.
+// An interior tile stores (and, for EPI_ADD, loads) through a buffer resource based at its first
+// row: the lane's offset is one VGPR and each register's row offset a wave-uniform SGPR, so no
+// element forms a 64-bit address or tests a bound. Edge tiles and the int32 planes take the
+// checked path.
+template <int P, int EPI, int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const int *s_exp, int m, int n, int m0,
+                                         int n0, int rw0, int cw0, const float *__restrict__ scale, const EpiArgs &ep,
+                                         int lane) {
+    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
+    auto value = [&](int i, int j, int r) {
+        if (P == 1) return (float)acc[0][i][j][r];
+        double A = (double)acc[0][i][j][r];
+#pragma unroll
+        for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][i][j][r]);
+        return (float)A;
+    };
+    if (EPI == EPI_ACC) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + cw0 + j * 32 + ccol;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + rw0 + i * 32 + rsub + (r >> 2) * 8 + (r & 3);
+                    if (row < m && col < n)
+#pragma unroll
+                        for (int p = 0; p < P; p++)
+                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
+                }
+        }
+        return;
+    }
+    float *ybase = reinterpret_cast<float *>(ep.y);
+    if (m0 + BM <= m && n0 + BN <= n) {
+        const BufRes yr = buf_res(ybase + (size_t)m0 * ep.ldy, (unsigned)(BM * ep.ldy) * 4u);
+        const unsigned ld4 = (unsigned)ep.ldy * 4u;
+        const unsigned voff = ((unsigned)(rw0 + rsub) * (unsigned)ep.ldy + (unsigned)(n0 + cw0 + ccol)) * 4u;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + cw0 + j * 32 + ccol;
+            const float sc = scale[col];
+            const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                int ex[16];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const i32x4 e4 = *reinterpret_cast<const i32x4 *>(s_exp + rw0 + i * 32 + g * 8 + rsub);
+#pragma unroll
+                    for (int z = 0; z < 4; z++) ex[g * 4 + z] = e4[z];
+                }
+                float prev[16];
+                if (EPI == EPI_ADD) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        prev[r] = load_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    float v = ldexpf(value(i, j, r), ex[r]) * sc;
+                    if (EPI == EPI_MUL) v = v * cv;
+                    if (EPI == EPI_ADD) v = prev[r] + v;
+                    store_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4, v);
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + cw0 + j * 32 + ccol;
+        const bool col_ok = col < n;
+        const int colc = col_ok ? col : n - 1;
+        const float sc = scale[colc];
+        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int rbase = rw0 + i * 32 + rsub;  // tile row of r = 0
+            float prev[16];
+            if (EPI == EPI_ADD) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
+                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
+                float v = ldexpf(value(i, j, r), s_exp[tr]) * sc;
+                if (EPI == EPI_MUL) v = v * cv;
+                if (EPI == EPI_ADD) v = prev[r] + v;
+                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
+            }
+        }
+    }
+}
+
 // The product over one BM x BN output tile: 256 threads = 4 waves in WM x (4 / WM); wave tile
 // MW x NW = (BM / WM) x (BN * WM / 4), FM x FN blocks of 32 x 32 per plane.
 template <int P, int EPI, int BM, int BN, int WM, int BK>
@@ -257,66 +361,13 @@ __global__ __launch_bounds__(256, 2) void q8_gemm_kernel(const int8_t *__restric
         step(kt + 1, std::integral_constant<int, 1>{});
     }
 
-    // epilogue. The tile's row exponents are staged in LDS (free after the K loop) so no element waits
-    // on a global load of its own; per 32 x 32 block, the lane holds rows (r/4)*8 + (lane/32)*4 + r%4
-    // of column lane%32, and all 16 of its loads (the accumulated output, EPI_ADD) are issued before use.
+    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
     int *s_exp = reinterpret_cast<int *>(smem);
     if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += 256) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        for (int i = tid; i < BM; i += 256) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
         __syncthreads();
     }
-    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int col = n0 + wn * NW + j * 32 + ccol;
-        const bool col_ok = col < n;
-        const int colc = col_ok ? col : n - 1;
-        const float sc = scale[colc];
-        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int rbase = wm * MW + i * 32 + rsub;  // tile row of r = 0
-            if (EPI == EPI_ACC) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
-                    if (row < m && col_ok)
-#pragma unroll
-                        for (int p = 0; p < P; p++)
-                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
-                }
-                continue;
-            }
-            float *ybase = reinterpret_cast<float *>(ep.y);
-            float prev[16];
-            if (EPI == EPI_ADD) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
-                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
-                float v;
-                if (P == 1) {
-                    v = (float)acc[0][i][j][r];  // one rounding, as (float)(double) of the exact sum
-                } else {
-                    // sum_p acc_p 2^(7(P-1-p)) is exact in double (|acc_p| < 2^31, the sum < 2^46)
-                    double A = (double)acc[0][i][j][r];
-#pragma unroll
-                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
-                    v = (float)A;
-                }
-                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
-                v = v * sc;
-                if (EPI == EPI_MUL) v = v * cv;
-                if (EPI == EPI_ADD) v = prev[r] + v;
-                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
-            }
-        }
-    }
+    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
 // ------------------------------------------------------------------ the product, direct-to-LDS form
@@ -467,63 +518,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_dma_kernel(const int8
     wait_vm<0>();
     __syncthreads();
 
-    // epilogue (as q8_gemm_kernel's)
+    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
     int *s_exp = reinterpret_cast<int *>(smem);
     if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += NT) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        for (int i = tid; i < BM; i += NT) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
         __syncthreads();
     }
-    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int col = n0 + wn * NW + j * 32 + ccol;
-        const bool col_ok = col < n;
-        const int colc = col_ok ? col : n - 1;
-        const float sc = scale[colc];
-        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int rbase = wm * MW + i * 32 + rsub;
-            if (EPI == EPI_ACC) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
-                    if (row < m && col_ok)
-#pragma unroll
-                        for (int p = 0; p < P; p++)
-                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
-                }
-                continue;
-            }
-            float *ybase = reinterpret_cast<float *>(ep.y);
-            float prev[16];
-            if (EPI == EPI_ADD) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
-                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
-                float v;
-                if (P == 1) {
-                    v = (float)acc[0][i][j][r];
-                } else {
-                    double A = (double)acc[0][i][j][r];
-#pragma unroll
-                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
-                    v = (float)A;
-                }
-                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
-                v = v * sc;
-                if (EPI == EPI_MUL) v = v * cv;
-                if (EPI == EPI_ADD) v = prev[r] + v;
-                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
-            }
-        }
-    }
+    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
 // ------------------------------------------------------------------ the product, deep-ring form
@@ -647,62 +648,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_ring_kernel(const int
     wait_vm<0>();
     __syncthreads();
 
+    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
     int *s_exp = reinterpret_cast<int *>(smem);
     if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += NT) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        for (int i = tid; i < BM; i += NT) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
         __syncthreads();
     }
-    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int col = n0 + wn * NW + j * 32 + ccol;
-        const bool col_ok = col < n;
-        const int colc = col_ok ? col : n - 1;
-        const float sc = scale[colc];
-        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int rbase = wm * MW + i * 32 + rsub;
-            if (EPI == EPI_ACC) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
-                    if (row < m && col_ok)
-#pragma unroll
-                        for (int p = 0; p < P; p++)
-                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
-                }
-                continue;
-            }
-            float *ybase = reinterpret_cast<float *>(ep.y);
-            float prev[16];
-            if (EPI == EPI_ADD) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
-                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
-                float v;
-                if (P == 1) {
-                    v = (float)acc[0][i][j][r];
-                } else {
-                    double A = (double)acc[0][i][j][r];
-#pragma unroll
-                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
-                    v = (float)A;
-                }
-                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
-                v = v * sc;
-                if (EPI == EPI_MUL) v = v * cv;
-                if (EPI == EPI_ADD) v = prev[r] + v;
-                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
-            }
-        }
-    }
+    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
 template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
@@ -843,62 +795,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_pipe_kernel(const int
     wait_vm<0>();
     __syncthreads();
 
+    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
     int *s_exp = reinterpret_cast<int *>(smem);
     if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += NT) s_exp[i] = xexp ? xexp[min(m0 + i, m - 1)] : 0;
+        for (int i = tid; i < BM; i += NT) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
         __syncthreads();
     }
-    const int ccol = lane & 31, rsub = (lane >> 5) * 4;
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int col = n0 + wn * NW + j * 32 + ccol;
-        const bool col_ok = col < n;
-        const int colc = col_ok ? col : n - 1;
-        const float sc = scale[colc];
-        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int rbase = wm * MW + i * 32 + rsub;
-            if (EPI == EPI_ACC) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + rbase + (r >> 2) * 8 + (r & 3);
-                    if (row < m && col_ok)
-#pragma unroll
-                        for (int p = 0; p < P; p++)
-                            reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = acc[p][i][j][r];
-                }
-                continue;
-            }
-            float *ybase = reinterpret_cast<float *>(ep.y);
-            float prev[16];
-            if (EPI == EPI_ADD) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
-                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
-                float v;
-                if (P == 1) {
-                    v = (float)acc[0][i][j][r];
-                } else {
-                    double A = (double)acc[0][i][j][r];
-#pragma unroll
-                    for (int p = 1; p < P; p++) A = A * 128.0 + (double)acc[p][i][j][r];
-                    v = (float)A;
-                }
-                v = ldexpf(v, s_exp[tr] - 7 * (P - 1));
-                v = v * sc;
-                if (EPI == EPI_MUL) v = v * cv;
-                if (EPI == EPI_ADD) v = prev[r] + v;
-                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
-            }
-        }
-    }
+    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
 template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
