@@ -334,6 +334,14 @@ class Stack:
                        "engram_block": c["eng_block"], "momentum": c["momentum"], "act_planes": planes}
         self.dtype = "i8"
         self.breakdown = None
+        # MFMA work actually executed: the dense products run their activations as `planes` int8
+        # planes (one i8 pass each), the spike product (Wout) one pass
+        P = planes
+        self.exec_ops = 2.0 * self.tokens * (L * (P * 15 + 1) * d * d + P * 4 * d * c["eng_dim"] + P * d * V)
+        # HBM bytes per q8 product launch, the mean over one forward's 51 launches, measured with
+        # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this workload (2.0 x FETCH_SIZE + WRITE_SIZE,
+        # KiB; the factor from the 1 GiB copy kernel of --workload copy)
+        self.traffic = 2.856e9
 
     def _reset(self):
         st = self.st
@@ -360,7 +368,9 @@ class Stack:
     def roofline(self, kernel_s):
         per_fwd = kernel_s / self.nsteps
         a = self.ops / per_fwd / 1e12
+        x = self.exec_ops / per_fwd / 1e12
         return {"bound": "mfma", "achieved": a, "peak": I8_PEAK_TOPS, "unit": "TOP/s", "frac": a / I8_PEAK_TOPS,
+                "executed": x, "executed_frac": x / I8_PEAK_TOPS, "executed_ops_per_forward": self.exec_ops,
                 "algorithmic_ops_per_forward": self.ops, "gemm_ms_per_forward": per_fwd * 1e3,
                 "kernel_calls_per_forward": self.gemm_calls // self.nsteps,
                 "kernel_avg_us": self.gemm_ms_total * 1e3 / self.gemm_calls}
@@ -371,16 +381,16 @@ class Stack:
     def cpu_baseline(self):
         from oracle import oracle as O
 
-        T = 128
+        B, T = 2, 2048  # 4096 tokens: about 10-15 s of CPU work
         th = cpu_threads()
         om = O.OracleModel(self.cfg, self.params)
-        ids = np.random.default_rng(4).integers(0, self.cfg["vocab"], (1, T)).astype(np.int32)
+        ids = np.random.default_rng(4).integers(0, self.cfg["vocab"], (B, T)).astype(np.int32)
         t0 = time.perf_counter()
-        om.forward(ids, state=om.new_state(1, eng_cap=T), planes=0, threads=th)
+        om.forward(ids, state=om.new_state(B, eng_cap=T), planes=0, threads=th)
         dt = time.perf_counter() - t0
-        return {"value": T / dt, "unit": "tokens/s", "cores": th, "kind": "port",
+        return {"value": B * T / dt, "unit": "tokens/s", "cores": th, "kind": "port",
                 "sample": f"oracle block-stack forward with the reference's W8A32 products (int8.rs:301-331) on "
-                          f"config[3]'s model, B=1, T={T}, {th} threads for the products, {dt:.2f} s"}
+                          f"config[3]'s model, B={B}, T={T}, {th} threads for the products, {dt:.2f} s"}
 
 
 WORKLOADS = {"stack": Stack, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
