@@ -1,11 +1,13 @@
 // k-winners-take-all for gfx950: one wavefront per row, the row held in registers.
 //
-// The k-th largest value of a row is found exactly by a bisection over the order-preserving uint32
-// image of the floats (larger float <=> larger key): at each step the candidate key prefix|bit is
-// kept when at least k keys are >= it, which ends at the largest key with k keys at or above it,
-// i.e. the k-th largest (duplicates counted). As soon as a candidate has exactly k keys at or above
-// it, the answer is the smallest of those keys (one wave min), which ends the search early. Each count is a wave
-// ballot per register and a popcount: no LDS, no atomics, no barriers, so a SIMD interleaves
+// The k-th largest value of a row is exact. As soon as some threshold t has exactly k values at or
+// above it, the answer is the smallest of those values (one wave min). Such a t is searched in value
+// space first: the count of values >= t is monotone in t, so t is interpolated (alternating with
+// midpoints) inside a bracket whose counts straddle k; a continuous row needs a handful of counts.
+// When ties make the count skip k, an exact bisection over the order-preserving uint32 image of
+// the floats (larger float <=> larger key) takes over: the candidate key prefix|bit is kept when at
+// least k keys are >= it, which ends at the k-th largest key (duplicates counted). Each count is a
+// wave ballot per register and a popcount: no LDS, no atomics, no barriers, so a SIMD interleaves
 // several rows' waves while their loads are in flight. HBM traffic is one read of u and one
 // write of the output per element.
 //
@@ -29,7 +31,7 @@ __device__ __forceinline__ float float_of_key(uint32_t k) {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // NV float4 chunks per lane: h <= 256 NV. OUT: 0 = f32 a, P>0 = P int8 planes + row exponent.
-template <int NV, int P>
+template <int NV, int P, bool FULL>
 __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, int n, int h, int k, int relu2,
                                                    float *__restrict__ a, float *__restrict__ kth_out,
                                                    int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq) {
@@ -43,44 +45,136 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int c = i * 64 + lane;
-        if (c < nq) x[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(ur) + c);
+        if (FULL || c < nq) x[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(ur) + c);
         else x[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // never counted: see below
     }
 
     float kth = -INFINITY;
     const bool all = k >= h;
-    if (!all) {
-        uint32_t keys[NV][4];
+    constexpr bool full = FULL;  // h == 256 NV: every chunk real, no padding lanes
+    // count of the row's values >= t (padding chunks are -inf and never counted for finite t)
+    auto count_ge = [&](float t) {
+        int c = 0;
 #pragma unroll
         for (int i = 0; i < NV; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) keys[i][j] = (i * 64 + lane < nq) ? key_of(x[i][j]) : 0u;
-        // padding keys are 0, below every real key except -NaN patterns (inputs are NaN-free), and
-        // the candidates are >= 1 after the first step, so padding never counts.
-        uint32_t prefix = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t cand = prefix | (1u << bit);
-            int cnt = 0;
+            for (int j = 0; j < 4; j++) c += __popcll(__ballot(x[i][j] >= t));
+        return c;
+    };
+    // the k-th largest once exactly k values are >= t: the smallest of them. A zero result is
+    // -0 when a -0 is among them (in the order of the keys, -0 < +0), else +0.
+    auto smallest_at_or_above = [&](float t) {
+        float mn = INFINITY;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) mn = x[i][j] >= t ? fminf(mn, x[i][j]) : mn;
+        mn = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ava::wave_min(mn))));
+        if (mn == 0.0f) {
+            bool neg = false;
 #pragma unroll
             for (int i = 0; i < NV; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) cnt += __popcll(__ballot(keys[i][j] >= cand));
-            if (cnt >= k) prefix = cand;
-            if (cnt == k) {
-                // exactly k keys are >= cand: the k-th largest is the smallest of them (typically after
-                // about log2(h) of the 32 steps)
-                uint32_t mn = 0xffffffffu;
+                for (int j = 0; j < 4; j++) neg |= x[i][j] >= t && __float_as_uint(x[i][j]) == 0x80000000u;
+            mn = __ballot(neg) ? -0.0f : 0.0f;
+        }
+        return mn;
+    };
+    if (!all) {
+        // 1. search in value space: count(>= t) is monotone; interpolate t between a bracket
+        //    lo (count > k) and hi (count < k) until exactly k values are >= t, which for
+        //    continuous rows takes a handful of counts. Ties can make the count skip k: then
+        //    (or on non-finite values) fall through to the exact bisection.
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool real = full || i * 64 + lane < nq;
+                if (real) {
+                    lo = fminf(lo, x[i][j]);
+                    hi = fmaxf(hi, x[i][j]);
+                }
+            }
+        // wave-uniform (readfirstlane), so the search's control flow is scalar
+        lo = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ava::wave_min(lo))));
+        hi = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ava::wave_max(hi))));
+        bool done = false, found = false;
+        float tk = 0.0f;  // a threshold with exactly k values at or above it
+        if (isfinite(lo) && isfinite(hi)) {
+            int clo = h, chi = count_ge(hi);
+            if (chi >= k) {  // the maximum is the k-th largest (ties at the top)
+                kth = hi;
+                done = true;
+            }
+            for (int it = 0; it < 24 && !done && !found; it++) {
+                // interpolation on even steps, midpoint on odd ones (guards slow one-sided convergence)
+                float t = (it & 1) ? lo * 0.5f + hi * 0.5f
+                                   : lo + (hi - lo) * ((float)(clo - k) / (float)(clo - chi));
+                if (!(t > lo && t < hi)) t = lo * 0.5f + hi * 0.5f;
+                if (!(t > lo && t < hi)) break;  // lo, hi adjacent floats: ties
+                const int c = count_ge(t);
+                if (c == k) {
+                    tk = t;
+                    found = true;
+                } else if (c > k) {
+                    lo = t;
+                    clo = c;
+                } else {
+                    hi = t;
+                    chi = c;
+                }
+            }
+        }
+        if (found) {  // outside the search loop, so the keys are not hoisted into registers of their own
+            kth = smallest_at_or_above(tk);
+            done = true;
+        }
+        if (!done) {
+            // 2. exact bisection over the order-preserving key image (any input, ties included). The
+            //    keys replace the values in place (padding: key 0, below every real key) and the
+            //    values come back after, so the row stays in one set of registers.
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool real = full || i * 64 + lane < nq;
+                    x[i][j] = __uint_as_float(real ? key_of(x[i][j]) : 0u);
+                }
+            uint32_t prefix = 0;
+            for (int bit = 31; bit >= 0; bit--) {
+                const uint32_t cand = prefix | (1u << bit);
+                int cnt = 0;
 #pragma unroll
                 for (int i = 0; i < NV; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) mn = keys[i][j] >= cand ? min(mn, keys[i][j]) : mn;
+                    for (int j = 0; j < 4; j++) cnt += __popcll(__ballot(__float_as_uint(x[i][j]) >= cand));
+                if (cnt >= k) prefix = cand;
+                if (cnt == k) {
+                    // exactly k keys are >= cand: the k-th largest is the smallest of them
+                    uint32_t mn = 0xffffffffu;
 #pragma unroll
-                for (int o = 32; o > 0; o >>= 1) mn = min(mn, (uint32_t)__shfl_xor((int)mn, o, 64));
-                prefix = mn;
-                break;
+                    for (int i = 0; i < NV; i++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const uint32_t kk = __float_as_uint(x[i][j]);
+                            mn = kk >= cand ? min(mn, kk) : mn;
+                        }
+#pragma unroll
+                    for (int o = 32; o > 0; o >>= 1) mn = min(mn, (uint32_t)__shfl_xor((int)mn, o, 64));
+                    prefix = mn;
+                    break;
+                }
             }
+            kth = float_of_key(prefix);
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool real = full || i * 64 + lane < nq;
+                    x[i][j] = real ? float_of_key(__float_as_uint(x[i][j])) : -INFINITY;
+                }
         }
-        kth = float_of_key(prefix);
     }
     if (kth_out && lane == 0) kth_out[row] = kth;
 
@@ -104,7 +198,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int c = i * 64 + lane;
-            if (c < nq) __builtin_nontemporal_store(x[i], reinterpret_cast<f32x4 *>(ar) + c);
+            if (full || c < nq) __builtin_nontemporal_store(x[i], reinterpret_cast<f32x4 *>(ar) + c);
         }
     } else {
         amax = ava::wave_max(amax);
@@ -113,7 +207,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int c = i * 64 + lane;
-            if (c < nq) {
+            if (full || c < nq) {
                 int q0[P], q1[P], q2[P], q3[P];
                 ava::to_planes<P>(x[i][0], e, q0);
                 ava::to_planes<P>(x[i][1], e, q1);
@@ -140,7 +234,10 @@ int launch(const float *u, int n, int h, int k, int relu2, float *a, float *kth,
     dim3 grid(ava::ceil_div(n, 4)), block(256);
 #define AVA_KW(NV_)                                                                                      \
     if (nv <= NV_) {                                                                                     \
-        kwta_kernel<NV_, P><<<grid, block, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);           \
+        if (h == NV_ * 256)                                                                              \
+            kwta_kernel<NV_, P, true><<<grid, block, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);  \
+        else                                                                                             \
+            kwta_kernel<NV_, P, false><<<grid, block, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq); \
         AVA_LAUNCHED("kwta");                                                                            \
         return AVA_OK;                                                                                   \
     }
