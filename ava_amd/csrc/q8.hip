@@ -421,16 +421,19 @@ __device__ __forceinline__ void dma16(const void *g, void *l) {
 #endif
 }
 
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
-__global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_dma_kernel(const int8_t *__restrict__ xq,
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S, int MINB, int BKB>
+__global__ __launch_bounds__(64 * WM * WN, MINB) void q8_gemm_dma_kernel(const int8_t *__restrict__ xq,
                                                                      const int32_t *__restrict__ xexp, int m, int n,
                                                                      int ldk, const int8_t *__restrict__ qt,
                                                                      const float *__restrict__ scale, EpiArgs ep) {
-    constexpr int NT = 64 * WM * WN, BK = 64, CPR = 4, LDS_ROW = BK;
+    // K step of BK = 64 or 128 bytes per row: a 1 KB load instruction covers RPI = 1024 / BK rows,
+    // CPR = BK / 16 lanes per row (at 128 bytes every request is one whole cache line)
+    constexpr int NT = 64 * WM * WN, BK = BKB, CPR = BK / 16, RPI = 1024 / BK, LDS_ROW = BK;
+    static_assert(BK == 64 || BK == 128, "K step");
     constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
     static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
     constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;  // bytes per stage
-    constexpr int A_INS = A_ROWS / 16, B_INS = BN / 16;              // 1 KB load instructions per stage
+    constexpr int A_INS = A_ROWS / RPI, B_INS = BN / RPI;            // 1 KB load instructions per stage
     constexpr int NWAVE = WM * WN;
     static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
     constexpr int LPW = (A_INS + B_INS) / NWAVE;  // load instructions per wave per stage
@@ -451,15 +454,15 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_dma_kernel(const int8
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const int ins = wave * LPW + i;
-        const int srow = ins * 16 + (lane >> 2);  // stage row
+        const int srow = ins * RPI + lane / CPR;  // stage row
         if (srow < A_ROWS) {
             const int p = srow / BM, rr = srow % BM;
-            const int c = swz<CPR>(rr, lane & 3);  // the logical chunk whose swizzled slot is lane & 3
+            const int c = swz<CPR>(rr, lane % CPR);  // the logical chunk whose swizzled slot is lane % CPR
             const int row = min(m0 + rr, m - 1);
             src[i] = xq + ((size_t)p * m + row) * ldk + c * 16;
         } else {
             const int rr = srow - A_ROWS;
-            const int c = swz<CPR>(rr, lane & 3);
+            const int c = swz<CPR>(rr, lane % CPR);
             const int col = min(n0 + rr, n - 1);
             src[i] = qt + (size_t)col * ldk + c * 16;
         }
@@ -822,14 +825,18 @@ int launch_pipe(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
 }
 
 // Tile shapes. kind 0: the register-staged kernel (BM, BN, WM, BK); kind 1: the direct-to-LDS kernel
-// (BM, BN, WM, WN, S). AVA_Q8_TILE=<index> overrides the choice per plane count (tuning).
+// (BM, BN, WM, WN, S) with 64-byte K steps; kind 5: the same with 128-byte K steps; kind 4: kind 1
+// at two workgroups per CU; kind 2: the software-pipelined form; kind 3: the deep-ring form.
+// AVA_Q8_TILE=<index> overrides the choice (tuning).
 struct TileCfg {
     int kind, bm, bn, wm, wn, bk_or_s;
 };
 constexpr TileCfg TILES[] = {
     {0, 128, 128, 2, 2, 64}, {0, 64, 128, 2, 2, 64}, {1, 128, 128, 2, 2, 2}, {1, 128, 256, 2, 4, 2},
     {1, 256, 128, 4, 2, 2},  {2, 128, 128, 2, 2, 3}, {3, 128, 256, 2, 4, 3}, {3, 128, 256, 2, 4, 4},
-    {3, 128, 128, 2, 2, 4},  {3, 256, 128, 4, 2, 3}, {3, 128, 128, 2, 4, 4}, {3, 64, 256, 1, 4, 4}};
+    {3, 128, 128, 2, 2, 4},  {3, 256, 128, 4, 2, 3}, {3, 128, 128, 2, 4, 4}, {3, 64, 256, 1, 4, 4},
+    {4, 128, 128, 2, 2, 2},  {4, 64, 256, 1, 4, 2},  {5, 128, 256, 2, 4, 2},  {5, 128, 128, 2, 2, 2},
+    {5, 64, 256, 1, 4, 2}};
 constexpr int NTILES = sizeof(TILES) / sizeof(TILES[0]);
 
 int tile_override() {
@@ -869,20 +876,20 @@ int launch_tile(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
     return AVA_OK;
 }
 
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
+template <int P, int EPI, int BM, int BN, int WM, int WN, int S, int MINB = 1, int BKB = 64>
 int launch_dma(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                EpiArgs ep, hipStream_t st) {
     const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    size_t lds = (size_t)S * (P * BM + BN) * 64;
+    size_t lds = (size_t)S * (P * BM + BN) * BKB;
     if (lds < (size_t)BM * 4) lds = (size_t)BM * 4;
     static bool attr = false;
     if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S>,
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
-    q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(xq, xexp, m, n, ldk,
-                                                                                                qt, scale, ep);
+    q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(
+        xq, xexp, m, n, ldk, qt, scale, ep);
     AVA_LAUNCHED("q8_gemm");
     return AVA_OK;
 }
@@ -891,7 +898,9 @@ template <int P, int EPI>
 int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                 EpiArgs ep, hipStream_t st) {
     int t = tile_override();
-    if (t < 0) t = 3;  // the direct-to-LDS 128 x 256 tile, 8 waves (measured best for every shape here)
+    // the direct-to-LDS 128 x 256 tile, 8 waves: 128-byte K steps for split-plane inputs, 64-byte
+    // ones for the single spike plane (measured best on every config[3] shape)
+    if (t < 0) t = P == 1 ? 3 : 14;
 #define AVA_T(I)                                                                                                   \
     if (t == I) {                                                                                                  \
         constexpr TileCfg c = TILES[I];                                                                            \
@@ -900,6 +909,13 @@ int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
         else if constexpr (c.kind == 1 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
                            ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0)                                          \
             return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
+        else if constexpr (c.kind == 4 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 80 * 1024 &&                      \
+                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0)                                          \
+            return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
+        else if constexpr (c.kind == 5 && (P * c.bm + c.bn) * 128 * c.bk_or_s <= 160 * 1024 &&                    \
+                           ((P * c.bm + c.bn) / 8) % (c.wm * c.wn) == 0)                                           \
+            return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s, 1, 128>(xq, xexp, m, n, ldk, qt, scale, ep, \
+                                                                               st);                             \
         else if constexpr (c.kind == 3 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
                            ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0 && (c.bm / c.wm) % 32 == 0 &&            \
                            (c.bn / c.wn) % 32 == 0)                                                                \
@@ -910,7 +926,7 @@ int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
         else                                                                                                       \
             return ava::fail(AVA_ERR_UNSUPPORTED, "q8 product: tile %d does not fit %d planes", I, P);             \
     }
-    AVA_T(0) AVA_T(1) AVA_T(2) AVA_T(3) AVA_T(4) AVA_T(5) AVA_T(6) AVA_T(7) AVA_T(8) AVA_T(9) AVA_T(10) AVA_T(11)
+    AVA_T(0) AVA_T(1) AVA_T(2) AVA_T(3) AVA_T(4) AVA_T(5) AVA_T(6) AVA_T(7) AVA_T(8) AVA_T(9) AVA_T(10) AVA_T(11) AVA_T(12) AVA_T(13) AVA_T(14) AVA_T(15) AVA_T(16)
 #undef AVA_T
     return ava::fail(AVA_ERR_ARG, "q8 product: tile %d", t);
 }
