@@ -25,7 +25,7 @@ class Config(C.Structure):
     _fields_ = [(n, i32) for n in ("vocab", "d", "layers", "hidden", "kwta_k", "head_size", "gate_rank",
                                    "eng_block", "eng_dim", "levels", "alif", "lif_scale", "value_residual",
                                    "dense", "relu2")] + \
-               [("momentum", f32), ("cap", f32), ("planes", i32)]
+               [("momentum", f32), ("cap", f32), ("planes", i32), ("cb_units", i32), ("cb_lr", f32), ("cb_half", f32)]
 
 
 BLOCK_FIELDS = ["lif_norm", "win", "beta_p", "theta", "arho", "again", "wout",
@@ -40,12 +40,13 @@ class BlockParams(C.Structure):
 
 
 class Params(C.Structure):
-    _fields_ = [("tok_emb", vp), ("final_norm", vp), ("blocks", C.POINTER(BlockParams))]
+    _fields_ = [("tok_emb", vp), ("final_norm", vp), ("blocks", C.POINTER(BlockParams)), ("cb_w", vp)]
 
 
 class State(C.Structure):
     _fields_ = [("lif_v", vp), ("lif_s", vp), ("lif_a", vp), ("mem_f", vp), ("mem_s", vp),
-                ("eng_k", vp), ("eng_v", vp), ("eng_cap", i32), ("eng_len", i32)]
+                ("eng_k", vp), ("eng_v", vp), ("eng_cap", i32), ("eng_len", i32),
+                ("cb_tab", vp), ("cb_scale", vp), ("cb_code", vp)]
 
 
 _lib = None
@@ -75,6 +76,7 @@ def lib():
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
+        "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],
     }
     for name, args in sig.items():
         fn = getattr(L, name, None)

@@ -1,0 +1,504 @@
+// The cerebellum head (CB) and its online table (CB2) for gfx950: the granule code, the read-out with
+// the table's share (emitting the head product's split planes), and the online learning step.
+//
+// Reference: gpu/v51b.rs:18-32 (the part), :242-265 (wiring), :327-337 (cb_code), :373-389
+// (CbOnline::add); gpu/model/fstep/arch_f3.rs:225-299 (the one-row forward); gpu/fast4/cb.rs:25-84
+// (the learning step). The wiring is built on the host (model.cpp) from the same seed.
+//
+// Per row the code is:
+//   u = [xf, rmsnorm(E[id], 1)] (2d); h_j = sum over the unit's 4 inputs of u[idx] * sgn, from 0 in order;
+//   kth = the k-th largest of h (k = G / 32); a_j = relu(h_j) where h_j - kth >= 0, else 0;
+//   c = a / (sqrt(sum a^2) + 1e-6).
+// One workgroup per row holds h in registers (G / 256 units per thread). The k-th largest is exact:
+// a threshold t is interpolated (alternating with midpoints) inside a bracket whose block-wide counts
+// straddle k until exactly k values are >= t, the answer then being the smallest of them; ties that
+// make the count skip k fall back to an exact bisection over the order-preserving key image.
+#include "common.h"
+
+namespace {
+
+constexpr int NT = 256;
+constexpr float NORM_EPS = 1e-5f;  // gpu/model.rs:36
+
+__device__ __forceinline__ uint32_t key_of(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float float_of_key(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Block-wide reductions for 256 threads (4 waves); every thread gets the result, made wave-uniform
+// (readfirstlane) so control flow on it stays scalar. `red` holds 4 slots; the leading barrier
+// protects it from the previous reduction's reads.
+__device__ __forceinline__ float uni(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = ava::wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return uni((red[0] + red[1]) + (red[2] + red[3]));
+}
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = ava::wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return uni(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+__device__ __forceinline__ float block_min(float v, float *red) {
+    v = ava::wave_min(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return uni(fminf(fminf(red[0], red[1]), fminf(red[2], red[3])));
+}
+__device__ __forceinline__ int block_isum(int v, int *red) {
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;  // v is wave-uniform (ballot counts)
+    __syncthreads();
+    return uni((red[0] + red[1]) + (red[2] + red[3]));
+}
+__device__ __forceinline__ uint32_t block_umin(uint32_t v, uint32_t *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (uint32_t)uni((int)min(min(red[0], red[1]), min(red[2], red[3])));
+}
+
+// The granule code of rows n: code [n][g]. With keep != NULL, each stream's last position (row
+// b T + T - 1) is also written to keep [b][g] (the code the learning step uses).
+template <int GPT>
+__global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ xf, const int32_t *__restrict__ ids,
+                                                     const float *__restrict__ emb, int d, int vocab,
+                                                     const uint32_t *__restrict__ widx,
+                                                     const float *__restrict__ wsgn, int g, int k, int T,
+                                                     float *__restrict__ code, float *__restrict__ keep) {
+    __shared__ float su[2048];
+    __shared__ float fred[4];
+    __shared__ int ired[4];
+    __shared__ uint32_t ured[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    int id = ids[row];
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // an id outside [0, vocab) reads the nearest row
+    const float *xr = xf + (size_t)row * d, *er = emb + (size_t)id * d;
+
+    // u = [xf, rmsnorm(emb row, 1)]
+    float ss = 0.0f;
+    for (int c = tid; c < d; c += NT) {
+        su[c] = xr[c];
+        const float e = er[c];
+        ss += e * e;
+    }
+    ss = block_sum(ss, fred);
+    const float inv = 1.0f / sqrtf((ss * (1.0f / (float)d) + 0.0f) * 1.0f + NORM_EPS);
+    for (int c = tid; c < d; c += NT) su[d + c] = (er[c] * inv) * 1.0f;
+    __syncthreads();
+
+    // h: unit j = tid + 256 i (padding units are -inf: never counted, never kept)
+    float h[GPT];
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        const int j = tid + i * NT;
+        if (j < g) {
+            const uint4 ix = reinterpret_cast<const uint4 *>(widx)[j];
+            const float4 sv = reinterpret_cast<const float4 *>(wsgn)[j];
+            float acc = 0.0f;
+            acc += su[ix.x] * sv.x;
+            acc += su[ix.y] * sv.y;
+            acc += su[ix.z] * sv.z;
+            acc += su[ix.w] * sv.w;
+            h[i] = acc;
+        } else {
+            h[i] = -INFINITY;
+        }
+    }
+    auto count_ge = [&](float t) {
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < GPT; i++) c += __popcll(__ballot(h[i] >= t));
+        return block_isum(c, ired);
+    };
+
+    float kth = -INFINITY;
+    if (k < g) {
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < GPT; i++)
+            if (tid + i * NT < g) {
+                lo = fminf(lo, h[i]);
+                hi = fmaxf(hi, h[i]);
+            }
+        lo = block_min(lo, fred);
+        hi = block_max(hi, fred);
+        bool done = false, found = false;
+        float tk = 0.0f;
+        if (isfinite(lo) && isfinite(hi)) {
+            int clo = g, chi = count_ge(hi);
+            if (chi >= k) {
+                kth = hi;
+                done = true;
+            }
+            for (int it = 0; it < 40 && !done && !found; it++) {
+                float t = (it & 1) ? lo * 0.5f + hi * 0.5f : lo + (hi - lo) * ((float)(clo - k) / (float)(clo - chi));
+                if (!(t > lo && t < hi)) t = lo * 0.5f + hi * 0.5f;
+                if (!(t > lo && t < hi)) break;
+                const int c = count_ge(t);
+                if (c == k) {
+                    tk = t;
+                    found = true;
+                } else if (c > k) {
+                    lo = t;
+                    clo = c;
+                } else {
+                    hi = t;
+                    chi = c;
+                }
+            }
+        }
+        if (found) {
+            // the smallest value >= tk; a zero is -0 when a -0 is among them (key order -0 < +0)
+            float mn = INFINITY;
+#pragma unroll
+            for (int i = 0; i < GPT; i++) mn = h[i] >= tk ? fminf(mn, h[i]) : mn;
+            mn = block_min(mn, fred);
+            if (mn == 0.0f) {
+                int neg = 0;
+#pragma unroll
+                for (int i = 0; i < GPT; i++)
+                    neg += __popcll(__ballot(h[i] >= tk && __float_as_uint(h[i]) == 0x80000000u));
+                mn = block_isum(neg, ired) ? -0.0f : 0.0f;
+            }
+            kth = mn;
+            done = true;
+        }
+        if (!done) {
+            // exact bisection over the keys (padding: key 0, below every real key)
+            uint32_t prefix = 0;
+            for (int bit = 31; bit >= 0; bit--) {
+                const uint32_t cand = prefix | (1u << bit);
+                int c = 0;
+#pragma unroll
+                for (int i = 0; i < GPT; i++)
+                    c += __popcll(__ballot(tid + i * NT < g && key_of(h[i]) >= cand));
+                const int cnt = block_isum(c, ired);
+                if (cnt >= k) prefix = cand;
+                if (cnt == k) {
+                    uint32_t mn = 0xffffffffu;
+#pragma unroll
+                    for (int i = 0; i < GPT; i++) {
+                        const uint32_t kk = key_of(h[i]);
+                        mn = (tid + i * NT < g && kk >= cand) ? min(mn, kk) : mn;
+                    }
+                    prefix = block_umin(mn, ured);
+                    break;
+                }
+            }
+            kth = float_of_key(prefix);
+        }
+    }
+
+    // relu on the winners, then unit length
+    float s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        const float v = h[i];
+        float a = v * ((k >= g || v - kth >= 0.0f) ? 1.0f : 0.0f);
+        a = a > 0.0f ? a : 0.0f;
+        h[i] = tid + i * NT < g ? a : 0.0f;
+        s2 += h[i] * h[i];
+    }
+    s2 = block_sum(s2, fred);
+    const float len = sqrtf(s2) * 1.0f + (float)1e-6;
+    float *cr = code + (size_t)row * g;
+    float *kr = (keep && row % T == T - 1) ? keep + (size_t)(row / T) * g : nullptr;
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+        const int j = tid + i * NT;
+        if (j < g) {
+            const float c = h[i] / len;
+            cr[j] = c;
+            if (kr) kr[j] = c;
+        }
+    }
+}
+
+// out = xf + sum over the non-zero units j in order of W[j] c_j (W NULL: nothing), then + the table's
+// share sum x_j tab[b][j] with x_j = c_j or (float)((double)c_j * scale[b]); the row's split planes
+// for the head product (and out itself when hout). One workgroup per row; the non-zero units are
+// compacted into LDS in unit order first (dynamic LDS: 8 bytes per unit).
+template <int P>
+__global__ __launch_bounds__(NT) void cb_apply_kernel(const float *__restrict__ xf, const float *__restrict__ code,
+                                                      int g, int d, const float *__restrict__ w,
+                                                      const float *__restrict__ tab, const double *__restrict__ scale,
+                                                      int T, int n, int8_t *__restrict__ xq,
+                                                      int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
+    extern __shared__ __attribute__((aligned(16))) char dyn[];
+    int *s_j = reinterpret_cast<int *>(dyn);
+    float *s_c = reinterpret_cast<float *>(dyn + sizeof(int) * (size_t)g);
+    __shared__ int s_cnt[NT + 1];
+    __shared__ float fred[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *cr = code + (size_t)row * g;
+
+    // compaction: thread tid scans units [tid * per, (tid + 1) * per)
+    const int per = (g + NT - 1) / NT, j0 = tid * per, j1 = min(g, j0 + per);
+    int cnt = 0;
+    for (int j = j0; j < j1; j++) cnt += cr[j] != 0.0f;
+    s_cnt[tid + 1] = cnt;
+    if (tid == 0) s_cnt[0] = 0;
+    __syncthreads();
+    if (tid == 0)
+        for (int t = 1; t <= NT; t++) s_cnt[t] += s_cnt[t - 1];
+    __syncthreads();
+    int o = s_cnt[tid];
+    for (int j = j0; j < j1; j++) {
+        const float c = cr[j];
+        if (c != 0.0f) {
+            s_j[o] = j;
+            s_c[o] = c;
+            o++;
+        }
+    }
+    __syncthreads();
+    const int nz = s_cnt[NT];
+
+    const int b = row / T;
+    const double sc = scale ? scale[b] : 1.0;
+    const float *xr = xf + (size_t)row * d;
+    const float *tb = tab ? tab + (size_t)b * g * d : nullptr;
+    float amax = 0.0f;
+    float outv[4];
+    const int cbase = tid * 4;  // this thread's 4 columns (d <= 1024)
+#pragma unroll
+    for (int z = 0; z < 4; z++) {
+        const int c = cbase + z;
+        float acc = 0.0f;
+        if (c < d) {
+            if (w)
+                for (int q = 0; q < nz; q++) acc += w[(size_t)s_j[q] * d + c] * s_c[q];
+            float o2 = xr[c] + acc;
+            if (tb) {
+                float acc2 = 0.0f;
+                for (int q = 0; q < nz; q++) {
+                    const float x = sc == 1.0 ? s_c[q] : (float)((double)s_c[q] * sc);
+                    acc2 += x * tb[(size_t)s_j[q] * d + c];
+                }
+                o2 = o2 + acc2;
+            }
+            outv[z] = o2;
+            amax = fmaxf(amax, fabsf(o2));
+            if (hout) hout[(size_t)row * d + c] = o2;
+        } else {
+            outv[z] = 0.0f;
+        }
+    }
+    amax = block_max(amax, fred);
+    const int e = ava::plane_exp(amax);
+    if (tid == 0) xexp[row] = e;
+    for (int c0 = cbase; c0 < ldq; c0 += NT * 4) {
+        int q[4][P];
+#pragma unroll
+        for (int z = 0; z < 4; z++) ava::to_planes<P>(c0 == cbase && c0 + z < d ? outv[z] : 0.0f, e, q[z]);
+#pragma unroll
+        for (int p = 0; p < P; p++)
+            *reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq + c0) = ava::pack4(q[0][p], q[1][p], q[2][p], q[3][p]);
+    }
+}
+
+// ------------------------------------------------------------------ the learning step
+
+// err [B][V] = softmax(logits row) - onehot(next) (max, exp(z - max), the sum, p / sum); nats [B]
+// (nullable) = -ln max(p_next, 1e-30). Rows whose next is outside [0, V) are skipped (err zeroed,
+// nats NaN): the reference's IGNORE.
+__global__ __launch_bounds__(NT) void cb_err_kernel(const float *__restrict__ logits, int ldl, int V,
+                                                    const int32_t *__restrict__ next, float *__restrict__ err,
+                                                    double *__restrict__ nats) {
+    __shared__ float fred[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float *z = logits + (size_t)b * ldl;
+    float *er = err + (size_t)b * V;
+    const int y = next[b];
+    if (y < 0 || y >= V) {
+        for (int j = tid; j < V; j += NT) er[j] = 0.0f;
+        if (nats && tid == 0) nats[b] = __longlong_as_double(0x7ff8000000000000ll);
+        return;
+    }
+    float mx = -INFINITY;
+    for (int j = tid; j < V; j += NT) mx = fmaxf(mx, z[j]);
+    mx = block_max(mx, fred);
+    float den = 0.0f;
+    for (int j = tid; j < V; j += NT) den += expf(z[j] - mx);
+    den = block_sum(den, fred);
+    for (int j = tid; j < V; j += NT) {
+        const float p = expf(z[j] - mx) / den;
+        er[j] = p - (j == y ? 1.0f : 0.0f);
+        if (nats && j == y) nats[b] = -log((double)(p > 1e-30f ? p : 1e-30f));
+    }
+}
+
+// part [ks][B][d] = err [B][V] slice ks . E [V][d] slice ks, fp32 MFMA (v_mfma_f32_32x32x2_f32): block
+// = 64 rows x 64 columns, 4 waves of 32 x 32, K in steps of 32 through LDS.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__global__ __launch_bounds__(NT) void cb_delta_kernel(const float *__restrict__ err, int B, int V,
+                                                      const float *__restrict__ E, int d, int kslice,
+                                                      float *__restrict__ part) {
+    __shared__ float sa[64][33];
+    __shared__ float sb[32][64 + 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64, ks = blockIdx.z;
+    const int kb = ks * kslice, ke = min(V, kb + kslice);
+    const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+    f32x16 acc = {};
+    for (int k0 = kb; k0 < ke; k0 += 32) {
+        __syncthreads();
+        for (int i = tid; i < 64 * 32; i += NT) {
+            const int r = i >> 5, kk = i & 31;
+            sa[r][kk] = (r0 + r < B && k0 + kk < ke) ? err[(size_t)(r0 + r) * V + k0 + kk] : 0.0f;
+        }
+        for (int i = tid; i < 32 * 64; i += NT) {
+            const int kk = i >> 6, c = i & 63;
+            sb[kk][c] = (k0 + kk < ke && c0 + c < d) ? E[(size_t)(k0 + kk) * d + c0 + c] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 32; s += 2) {
+            const float a = sa[wr + (lane & 31)][s + (lane >> 5)];
+            const float bb = sb[s + (lane >> 5)][wc + (lane & 31)];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
+        }
+    }
+    // accumulator layout: register r -> row (r / 4) * 8 + (lane / 32) * 4 + r % 4, column lane % 32
+    float *pr = part + (size_t)ks * B * d;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int row = r0 + wr + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), col = c0 + wc + (lane & 31);
+        if (row < B && col < d) pr[(size_t)row * d + col] = acc[r];
+    }
+}
+
+// delta [B][d] = sum over ks in order of part [ks]
+__global__ void cb_delta_sum_kernel(const float *__restrict__ part, int nks, int total, float *__restrict__ delta) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    float s = part[i];
+    for (int k = 1; k < nks; k++) s += part[(size_t)k * total + i];
+    delta[i] = s;
+}
+
+// The table's scale: rows with a valid next fade by `fade` (2^(-1/half), host-computed; 1 = no fading);
+// below 1e-18 the row is marked for folding (fold[b] = the old scale) and its scale returns to 1.
+__global__ void cb_scale_kernel(const int32_t *__restrict__ next, int B, int V, double fade, double *__restrict__ scale,
+                                double *__restrict__ fold) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const int y = next[b];
+    double f = 0.0;
+    if (y >= 0 && y < V && fade != 1.0) {
+        double s = scale[b] * fade;
+        if (s < 1e-18) {
+            f = s;
+            s = 1.0;
+        }
+        scale[b] = s;
+    }
+    fold[b] = f;
+}
+
+// Fold marked rows: tab[b] = (float)((double)tab[b] * fold[b]) (a rare event; one workgroup per row).
+__global__ __launch_bounds__(1024) void cb_fold_kernel(const double *__restrict__ fold, size_t per,
+                                                       float *__restrict__ tab) {
+    const double f = fold[blockIdx.x];
+    if (f == 0.0) return;
+    float *t = tab + (size_t)blockIdx.x * per;
+    for (size_t i = threadIdx.x; i < per; i += 1024) t[i] = (float)((double)t[i] * f);
+}
+
+// tab[b][u] -= s_u delta[b] for the non-zero units u of the kept code, s_u = lr * c_u (divided by
+// the scale in double when it is not 1). Block (b, 64-unit range); threads over the d columns.
+__global__ __launch_bounds__(NT) void cb_table_kernel(const float *__restrict__ keep, int g, int d,
+                                                      const float *__restrict__ delta, const int32_t *__restrict__ next,
+                                                      int V, float lr, const double *__restrict__ scale,
+                                                      float *__restrict__ tab) {
+    const int b = blockIdx.x, u0 = blockIdx.y * 64, tid = threadIdx.x;
+    const int y = next[b];
+    if (y < 0 || y >= V) return;
+    const double sc = scale[b];
+    const float *kc = keep + (size_t)b * g;
+    const float *dr = delta + (size_t)b * d;
+    float *tb = tab + (size_t)b * g * d;
+    for (int u = u0; u < min(g, u0 + 64); u++) {
+        const float c = kc[u];
+        if (c == 0.0f) continue;
+        float s = lr * c;
+        if (sc != 1.0) s = (float)((double)s / sc);
+        float *tr = tb + (size_t)u * d;
+        for (int i = tid; i < d; i += NT) tr[i] -= s * dr[i];
+    }
+}
+
+}  // namespace
+
+namespace ava {
+
+int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
+            const float *wsgn, int g, int k, int T, float *code, float *keep, hipStream_t st) {
+    AVA_REQUIRE(d <= 1024 && d % 4 == 0 && g > 0 && g <= 16384 && T > 0, AVA_ERR_SHAPE, "cb_code: d=%d g=%d", d, g);
+    const int gpt = (g + NT - 1) / NT;
+#define AVA_CBC(G_) cb_code_kernel<G_><<<n, NT, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep)
+    if (gpt <= 2) AVA_CBC(2);
+    else if (gpt <= 8) AVA_CBC(8);
+    else if (gpt <= 16) AVA_CBC(16);
+    else if (gpt <= 32) AVA_CBC(32);
+    else if (gpt <= 48) AVA_CBC(48);
+    else AVA_CBC(64);
+#undef AVA_CBC
+    AVA_LAUNCHED("cb_code");
+    return AVA_OK;
+}
+
+int cb_apply(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
+             const double *scale, int T, int planes, int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st) {
+    AVA_REQUIRE(d <= 1024 && d % 4 == 0 && ldq % 4 == 0 && ldq <= 1024 && g <= 16384, AVA_ERR_SHAPE,
+                "cb_apply: d=%d ldq=%d g=%d", d, ldq, g);
+    const size_t lds = (size_t)g * 8;
+    static bool attr[4] = {false, false, false, false};
+#define AVA_CBA(P_)                                                                                          \
+    if (planes == P_) {                                                                                      \
+        if (!attr[P_]) {                                                                                     \
+            AVA_HIP(hipFuncSetAttribute((const void *)cb_apply_kernel<P_>,                                   \
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 8));             \
+            attr[P_] = true;                                                                                 \
+        }                                                                                                    \
+        cb_apply_kernel<P_><<<n, NT, lds, st>>>(xf, code, g, d, w, tab, scale, T, n, xq, xexp, ldq, hout);   \
+    }
+    AVA_CBA(1) else AVA_CBA(2) else AVA_CBA(3) else return fail(AVA_ERR_ARG, "cb_apply: planes %d", planes);
+#undef AVA_CBA
+    AVA_LAUNCHED("cb_apply");
+    return AVA_OK;
+}
+
+int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, const float *emb, int d,
+             const float *keep, int g, float lr, double fade, double *scale, float *tab, float *err, float *part,
+             int nks, float *delta, double *fold, double *nats, hipStream_t st) {
+    AVA_REQUIRE(B > 0 && V > 0 && d > 0 && nks > 0, AVA_ERR_SHAPE, "cb_learn: B=%d V=%d d=%d", B, V, d);
+    cb_err_kernel<<<B, NT, 0, st>>>(logits, ldl, V, next, err, nats);
+    AVA_LAUNCHED("cb_err");
+    const int kslice = ((V + nks - 1) / nks + 31) / 32 * 32;
+    cb_delta_kernel<<<dim3(ceil_div(B, 64), ceil_div(d, 64), nks), NT, 0, st>>>(err, B, V, emb, d, kslice, part);
+    AVA_LAUNCHED("cb_delta");
+    cb_delta_sum_kernel<<<ceil_div(B * d, 256), 256, 0, st>>>(part, nks, B * d, delta);
+    AVA_LAUNCHED("cb_delta_sum");
+    cb_scale_kernel<<<ceil_div(B, 256), 256, 0, st>>>(next, B, V, fade, scale, fold);
+    AVA_LAUNCHED("cb_scale");
+    cb_fold_kernel<<<B, 1024, 0, st>>>(fold, (size_t)g * d, tab);
+    AVA_LAUNCHED("cb_fold");
+    cb_table_kernel<<<dim3(B, ceil_div(g, 64)), NT, 0, st>>>(keep, g, d, delta, next, V, lr, scale, tab);
+    AVA_LAUNCHED("cb_table");
+    return AVA_OK;
+}
+
+}  // namespace ava

@@ -143,6 +143,14 @@ int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, 
              hipStream_t st);
 int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,
                 hipStream_t st);
+// cb.hip: the cerebellum head (code, read-out with the online table to the head's planes, learning)
+int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
+            const float *wsgn, int g, int k, int T, float *code, float *keep, hipStream_t st);
+int cb_apply(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
+             const double *scale, int T, int planes, int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st);
+int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, const float *emb, int d,
+             const float *keep, int g, float lr, double fade, double *scale, float *tab, float *err, float *part,
+             int nks, float *delta, double *fold, double *nats, hipStream_t st);
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st);
 
 }  // namespace ava

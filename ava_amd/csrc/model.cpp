@@ -75,6 +75,17 @@ struct ava_model {
     int32_t *xexp = nullptr;
     std::vector<float *> streams;
 
+    // the cerebellum head (cfg.cb_units > 0): the fixed wiring, the read-out (NULL: zero), the fade
+    uint32_t *cb_idx = nullptr;
+    float *cb_sgn = nullptr, *cb_w = nullptr;
+    int cb_k = 0;
+    double cb_fade = 1.0;
+    float *cb_codes = nullptr;  // scratch [rows][cb_units]
+    // the learning step's scratch for up to cb_rows streams
+    int cb_rows = 0;
+    float *cb_err = nullptr, *cb_part = nullptr, *cb_delta = nullptr;
+    double *cb_fold = nullptr;
+
     bool timing = false;
     Timer timer;
     hipStream_t last_stream = nullptr;
@@ -130,6 +141,36 @@ int quantize(ava_model *m, DevQW *q, int din, const std::vector<std::pair<const 
     return AVA_OK;
 }
 
+// The cerebellum's fixed granule wiring (gpu/v51b.rs:242-265): xorshift64 from seed | 1; per unit,
+// `fan` distinct inputs of `inputs` drawn as next() % inputs, then one sign per input from next() & 1,
+// amplitude 1/sqrt(fan). The seed is the reference's CB_SEED (gpu/v51b.rs:49).
+void cb_wiring(int inputs, int g, int fan, std::vector<uint32_t> &idx, std::vector<float> &sgn) {
+    uint64_t s = 0x51B0CE7EULL | 1ULL;
+    auto next = [&]() {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        return s;
+    };
+    const float amp = 1.0f / sqrtf((float)fan);
+    idx.assign((size_t)g * fan, 0);
+    sgn.assign((size_t)g * fan, 0.0f);
+    for (int j = 0; j < g; j++) {
+        uint32_t picked[8];
+        int np = 0;
+        while (np < std::min(fan, inputs)) {
+            const uint32_t r = (uint32_t)(next() % (uint64_t)inputs);
+            bool seen = false;
+            for (int a = 0; a < np; a++) seen = seen || picked[a] == r;
+            if (!seen) picked[np++] = r;
+        }
+        for (int a = 0; a < np; a++) {
+            idx[(size_t)j * fan + a] = picked[a];
+            sgn[(size_t)j * fan + a] = (next() & 1) == 0 ? amp : -amp;
+        }
+    }
+}
+
 int build(ava_model *m, const ava_params *prm) {
     const ava_config &c = m->cfg;
     const int d = c.d, nh = d / c.head_size, r = c.gate_rank, de = c.eng_dim, H = c.hidden;
@@ -141,6 +182,18 @@ int build(ava_model *m, const ava_params *prm) {
         for (int v = 0; v < c.vocab; v++)
             for (int j = 0; j < d; j++) et[(size_t)j * c.vocab + v] = prm->tok_emb[(size_t)v * d + j];
         if (int e = quantize(m, &m->head, d, {{et.data(), c.vocab}})) return e;
+    }
+    if (c.cb_units > 0) {
+        std::vector<uint32_t> idx;
+        std::vector<float> sgn;
+        cb_wiring(2 * d, c.cb_units, 4, idx, sgn);
+        if (int e = dev_alloc(m, (void **)&m->cb_idx, idx.size() * sizeof(uint32_t))) return e;
+        AVA_HIP(hipMemcpy(m->cb_idx, idx.data(), idx.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+        if (int e = upload(m, &m->cb_sgn, sgn.data(), sgn.size())) return e;
+        if (prm->cb_w)
+            if (int e = upload(m, &m->cb_w, prm->cb_w, (size_t)c.cb_units * d)) return e;
+        m->cb_k = c.cb_units / 32;  // gpu/v51b.rs:47 (CB_SPARSITY)
+        m->cb_fade = c.cb_half > 0.0f ? exp2(-1.0 / (double)c.cb_half) : 1.0;
     }
     m->blocks.resize(c.layers);
     for (int i = 0; i < c.layers; i++) {
@@ -238,6 +291,7 @@ int ensure_scratch(ava_model *m, size_t rows) {
         m->streams.resize(c.layers + 1);
         for (auto &s : m->streams) A((void **)&s, rows * d * 4);
     }
+    if (c.cb_units > 0) A((void **)&m->cb_codes, rows * c.cb_units * 4);
     if (e) return e;
     m->rows = rows;
     return AVA_OK;
@@ -350,7 +404,15 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     }
     if (c.eng_block >= 0) s->eng_len += T;
     if (logits) {
-        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+        const bool cb = c.cb_units > 0 && s->cb_code;
+        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, cb ? m->h : nullptr, st));
+        if (cb) {
+            // the cerebellum's correction between the final norm and the head (gpu/model/fstep/arch.rs:1045-1047)
+            AVA_RUN("cb_code", ava::cb_code(m->h, ids, m->tok_emb, N, d, c.vocab, m->cb_idx, m->cb_sgn, c.cb_units, m->cb_k,
+                                            T, m->cb_codes, s->cb_code, st));
+            AVA_RUN("cb_apply", ava::cb_apply(m->h, m->cb_codes, N, c.cb_units, d, m->cb_w, s->cb_tab, s->cb_scale, T, P,
+                                              m->xq, m->xexp, ldd, nullptr, st));
+        }
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &m->head.w, ava::Q8_STORE, logits, c.vocab, nullptr, st));
     }
     return AVA_OK;
@@ -373,6 +435,8 @@ extern "C" int ava_model_new(const ava_config *cfg, const ava_params *params, av
                 "model_new: engram block %d, dim %d (64)", c.eng_block, c.eng_dim);
     AVA_REQUIRE(c.levels == 1 || c.levels == 2, AVA_ERR_ARG, "model_new: levels %d", c.levels);
     AVA_REQUIRE(c.planes >= 1 && c.planes <= 3, AVA_ERR_ARG, "model_new: planes %d (1..3)", c.planes);
+    AVA_REQUIRE(c.cb_units == 0 || (c.cb_units > 0 && c.cb_units % 32 == 0 && c.cb_units <= 16384), AVA_ERR_SHAPE,
+                "model_new: cb_units %d (0, or a multiple of 32 up to 16384)", c.cb_units);
     ava_model *m = new ava_model();
     m->cfg = c;
     (void)hipGetDevice(&m->device);
@@ -390,6 +454,7 @@ extern "C" void ava_model_free(ava_model *m) {
     for (void *p : m->allocs) (void)hipFree(p);
     for (void *p : m->scratch) (void)hipFree(p);
     for (hipEvent_t e : m->timer.pool) (void)hipEventDestroy(e);
+    for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
     delete m;
 }
 
@@ -398,6 +463,28 @@ extern "C" int ava_model_forward(ava_model *m, ava_state *st, const int32_t *ids
     AVA_REQUIRE(m && st && ids, AVA_ERR_ARG, "model_forward: NULL argument");
     AVA_REQUIRE(B > 0 && T > 0 && (long)B * T <= (1L << 24), AVA_ERR_SHAPE, "model_forward: B=%d T=%d", B, T);
     return forward(m, st, ids, B, T, logits, (hipStream_t)stream);
+}
+
+extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logits, int ld_logits,
+                                  const int32_t *next, int B, double *nats, ava_stream stream) {
+    AVA_REQUIRE(m && st && logits && next, AVA_ERR_ARG, "cb_learn: NULL argument");
+    const ava_config &c = m->cfg;
+    AVA_REQUIRE(c.cb_units > 0 && st->cb_tab && st->cb_scale && st->cb_code, AVA_ERR_ARG,
+                "cb_learn: the model has no cerebellum head or the state no online table");
+    AVA_REQUIRE(B > 0 && ld_logits >= c.vocab, AVA_ERR_SHAPE, "cb_learn: B=%d ld=%d", B, ld_logits);
+    const int nks = 8;  // the delta product's K slices (vocab / 8 each)
+    if (B > m->cb_rows) {
+        for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
+        m->cb_rows = 0;
+        AVA_HIP(hipMalloc(&m->cb_err, (size_t)B * c.vocab * sizeof(float)));
+        AVA_HIP(hipMalloc(&m->cb_part, (size_t)nks * B * c.d * sizeof(float)));
+        AVA_HIP(hipMalloc(&m->cb_delta, (size_t)B * c.d * sizeof(float)));
+        AVA_HIP(hipMalloc(&m->cb_fold, (size_t)B * sizeof(double)));
+        m->cb_rows = B;
+    }
+    return ava::cb_learn(logits, ld_logits, c.vocab, next, B, m->tok_emb, c.d, st->cb_code, c.cb_units, c.cb_lr,
+                         m->cb_fade, st->cb_scale, st->cb_tab, m->cb_err, m->cb_part, nks, m->cb_delta, m->cb_fold, nats,
+                         (hipStream_t)stream);
 }
 
 extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }

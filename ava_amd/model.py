@@ -5,6 +5,7 @@ gpu/state.rs), over ava_model_* of include/ava.h.
     st = m.state(B, eng_cap)            Model::state (state.rs:593)
     logits = m.forward_with_state(ids, st)   state.rs:684-865 (ids [B, T] int32 on the GPU)
     logits = m.forward(ids)             model.rs:1171: a fresh state per call
+    nats = m.cb_learn(logits, next, st) Model::cb_learn (gpu/v51b.rs:600-604, gpu/fast4/cb.rs:25-84)
 
 `params` is a dict of float32 numpy arrays keyed as ava_amd.synth (the reference's VarMap names).
 The library raises AvaError on any failure; nothing falls back to another path.
@@ -39,12 +40,18 @@ class State:
         cap = max(eng_cap, 1)
         self.eng_k, self.eng_v = z(B, cap, de), z(B, cap, de)
         self.eng_cap, self.eng_len = eng_cap, 0
+        g = cfg.get("cb_units", 0)
+        # the cerebellum's online table (CbOnline, gpu/v51b.rs:340-367): delta, scale 1, last code
+        self.cb_tab = z(B, g, d) if g else None
+        self.cb_scale = torch.ones(B, dtype=torch.float64, device=device) if g else None
+        self.cb_code = z(B, g) if g else None
 
     def c(self):
-        p = lambda t: t.data_ptr()
+        p = lambda t: t.data_ptr() if t is not None else None
         return _CState(lif_v=p(self.lif_v), lif_s=p(self.lif_s), lif_a=p(self.lif_a), mem_f=p(self.mem_f),
                        mem_s=p(self.mem_s), eng_k=p(self.eng_k), eng_v=p(self.eng_v), eng_cap=self.eng_cap,
-                       eng_len=self.eng_len)
+                       eng_len=self.eng_len, cb_tab=p(self.cb_tab), cb_scale=p(self.cb_scale),
+                       cb_code=p(self.cb_code))
 
 
 class Model:
@@ -59,13 +66,21 @@ class Model:
                 if bp.get(name) is not None:
                     setattr(blocks[i], name, _ptr(bp[name], keep))
         prm = Params(tok_emb=_ptr(params["tok_emb"], keep), final_norm=_ptr(params["final_norm"], keep),
-                     blocks=C.cast(blocks, C.POINTER(BlockParams)))
+                     blocks=C.cast(blocks, C.POINTER(BlockParams)),
+                     cb_w=_ptr(params["cb_w"], keep) if params.get("cb_w") is not None else None)
         c = self.cfg
+        cb_lr = 0.0
+        if c.get("cb_units", 0):
+            # the online rate: eta / mean |E_v|^2 (Model::cb_rate, gpu/v51b.rs:606-611) unless given
+            from .synth import cb_rate
+            cb_lr = c["cb_lr"] if c.get("cb_lr") is not None else cb_rate(params["tok_emb"], c["cb_eta"])
+        self.cb_lr = cb_lr
         ccfg = Config(vocab=c["vocab"], d=c["d"], layers=L, hidden=c["hidden"], kwta_k=c["kwta_k"],
                       head_size=c["head_size"], gate_rank=c["gate_rank"], eng_block=c["eng_block"],
                       eng_dim=c["eng_dim"], levels=c["levels"], alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
                       value_residual=int(c["value_residual"]), dense=int(c["dense"]), relu2=int(c["relu2"]),
-                      momentum=c["momentum"], cap=c["cap"], planes=planes)
+                      momentum=c["momentum"], cap=c["cap"], planes=planes, cb_units=c.get("cb_units", 0),
+                      cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0))
         torch.cuda.init()
         h = C.c_void_p()
         check(lib().ava_model_new(C.byref(ccfg), C.byref(prm), C.byref(h)), "ava_model_new")
@@ -92,6 +107,25 @@ class Model:
               "ava_model_forward")
         st.eng_len = cst.eng_len
         return logits
+
+    def cb_learn(self, logits: torch.Tensor, nxt: torch.Tensor, st: State) -> torch.Tensor:
+        """One online step of every stream's table (Model::cb_learn): logits [B, >= vocab] f32 GPU rows of
+        each stream's last position, nxt [B] int32 GPU (outside [0, vocab): no step). Returns nats [B] f64."""
+        if st.cb_tab is None:
+            raise ValueError("cb_learn: the state has no cerebellum table (cb_units == 0)")
+        B = st.B
+        if not (nxt.is_cuda and nxt.dtype == torch.int32 and nxt.is_contiguous() and nxt.numel() == B):
+            raise ValueError("nxt: a contiguous [B] int32 GPU tensor is required")
+        if not (logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2 and logits.shape[0] == B
+                and logits.stride(1) == 1):
+            raise ValueError("logits: [B, vocab] f32 GPU rows with unit column stride are required")
+        nats = torch.empty(B, dtype=torch.float64, device=logits.device)
+        cst = st.c()
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check(lib().ava_model_cb_learn(self.h, C.byref(cst), C.c_void_p(logits.data_ptr()), logits.stride(0),
+                                       C.c_void_p(nxt.data_ptr()), B, C.c_void_p(nats.data_ptr()), stream),
+              "ava_model_cb_learn")
+        return nats
 
     def forward(self, ids: torch.Tensor):
         B, T = ids.shape

@@ -23,7 +23,10 @@ FIXED_TS = (5.0, 8.0)  # gpu/arch.rs:91
 
 
 def config(name: str) -> dict:
-    """Named configurations: "ava04_d512" (config[0]), "ava04_d1024" (config[3]), "tiny" (tests)."""
+    """Named configurations: "ava04_d512" (config[0]), "ava04_d1024" (config[3]), "ava04_d1024_decode"
+    (config[4]), "tiny", "small" and "tiny_cb" (tests). cb_units > 0 adds the cerebellum head
+    (gpu/v51b.rs:18-32) with its online table: cb_eta sets the rate as cb_rate, cb_half the
+    table's half-life in tokens (<= 0: it never fades)."""
     base = dict(levels=2, alif=True, lif_scale=True, value_residual=True, dense=True, relu2=True,
                 momentum=0.5, cap=MEM_CAP, head_size=64, gate_rank=GATE_RANK, eng_dim=64)
     if name == "ava04_d512":
@@ -34,6 +37,14 @@ def config(name: str) -> dict:
         base.update(vocab=256, d=128, layers=2, hidden=512, kwta_k=128, eng_block=1)
     elif name == "small":
         base.update(vocab=512, d=256, layers=3, hidden=1024, kwta_k=256, eng_block=1)
+    elif name == "tiny_cb":
+        base.update(vocab=256, d=128, layers=2, hidden=512, kwta_k=128, eng_block=1)
+        base.update(cb_units=512, cb_eta=0.5, cb_half=256.0)
+    elif name == "ava04_d1024_decode":
+        # config[4]: config[3]'s shapes with the cerebellum head's online table as Ava 0.4 talks with it
+        # (gpu/bin/ava_live.rs:61-64: 12,288 granule units, rate 0.3 / mean |E_v|^2, half-life 256 tokens)
+        base.update(vocab=8192, d=1024, layers=8, hidden=4096, kwta_k=1024, eng_block=4)
+        base.update(cb_units=12288, cb_eta=0.3, cb_half=256.0)
     else:
         raise ValueError(f"unknown config {name!r}")
     return base
@@ -91,3 +102,14 @@ def params(cfg: dict, seed: int = 0) -> dict:
             b.update(eng_norm=const(d, 1.0), ewq=n(d, de), ewk=n(d, de), ewv=n(d, de), ewo=n(de, d))
         blocks.append(b)
     return {"tok_emb": n(V, d), "final_norm": const(d, 1.0), "blocks": blocks}
+
+
+CB_FAN_IN = 4  # gpu/v51b.rs:46-48
+CB_SPARSITY = 32
+CB_SEED = 0x51B0CE7E
+
+
+def cb_rate(tok_emb: np.ndarray, eta: float) -> float:
+    """gpu/v51b.rs:606-611 (Model::cb_rate): eta / mean |E_v|^2 = eta * V / sum(E^2), the sum in f32."""
+    e2 = np.float32(np.sum(np.asarray(tok_emb, np.float32) ** 2, dtype=np.float32))
+    return float(np.float32(eta * tok_emb.shape[0] / float(e2)))

@@ -139,6 +139,12 @@ typedef struct {
     int alif, lif_scale, value_residual, dense, relu2;
     float momentum, cap;
     int planes;     /* activation planes of the dense int8 products (3 = accurate) */
+    /* The cerebellum head (gpu/v51b.rs:18-32): cb_units granule units (0 = off; a multiple of 32,
+     * <= 16384), the top cb_units/32 kept. cb_lr is the online table's rate (Model::cb_rate,
+     * gpu/v51b.rs:606-611, gives eta / mean |E_v|^2), cb_half its half-life in tokens (<= 0: it
+     * never fades; gpu/v51b.rs:352-367). */
+    int cb_units;
+    float cb_lr, cb_half;
 } ava_config;
 
 /* f32 HOST weights, named as the reference's VarMap (arch.rs:806-860). W [din][dout] as applied x·W. */
@@ -154,6 +160,7 @@ typedef struct {
     const float *tok_emb;    /* [vocab][d]; the head is its transpose in int8 */
     const float *final_norm; /* [d] */
     const ava_block_params *blocks;
+    const float *cb_w;       /* [cb_units][d] the cerebellum's read-out cbh.wo (NULL: zero, as at init) */
 } ava_params;
 
 /* The carried state of B streams (caller-owned device buffers). Replaces State's LIF, memory and
@@ -165,6 +172,13 @@ typedef struct {
     float *mem_f, *mem_s;         /* [layers][B][d/hs][hs][hs] */
     float *eng_k, *eng_v;         /* [B][eng_cap][eng_dim] */
     int eng_cap, eng_len;         /* eng_len advances by T per forward */
+    /* The cerebellum's online table per stream (gpu/v51b.rs:340-367, CbOnline): cb_tab
+     * [B][cb_units][d] (its `delta`; NULL: no table), cb_scale [B] f64 (its `scale`, 1 at the start),
+     * and cb_code [B][cb_units], the granule code of each stream's last position, which
+     * ava_model_cb_learn uses (CbOnline::last). All NULL when cb_units == 0. */
+    float *cb_tab;
+    double *cb_scale;
+    float *cb_code;
 } ava_state;
 
 typedef struct ava_model ava_model;
@@ -179,6 +193,15 @@ void ava_model_free(ava_model *m);
  * Scratch memory is allocated on first use per (B, T) and kept by the model. */
 int ava_model_forward(ava_model *m, ava_state *st, const int32_t *ids, int B, int T, float *logits,
                       ava_stream stream);
+
+/* One online learning step of every stream's cerebellum table (gpu/fast4/cb.rs:25-84, Model::cb_learn):
+ * logits [B] rows of ld_logits floats (device; the rows of each stream's last position of the last
+ * forward), next [B] the words that followed (device int32; outside [0, vocab): no step for that
+ * stream, the reference's IGNORE). Per stream: p = softmax(logits), delta = (p - onehot(next)) . E,
+ * the scale fades by 2^(-1/cb_half) (folded into the table below 1e-18), and each unit u of the kept
+ * code moves: tab[u] -= (cb_lr c_u / scale) delta. nats [B] (device f64, nullable) = -ln p_next. */
+int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logits, int ld_logits, const int32_t *next, int B,
+                       double *nats, ava_stream stream);
 
 /* Bytes of scratch the model holds after forwards of up to B*T rows. */
 size_t ava_model_scratch_bytes(const ava_model *m);

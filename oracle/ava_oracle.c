@@ -600,3 +600,135 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------ cerebellum head (CB) */
+
+/* gpu/v51b.rs:242-265 (cb_wiring): xorshift64 from seed | 1; per unit, fan_in distinct inputs
+ * next() % inputs, then one sign per input from next() & 1, amplitude 1/sqrt(fan_in). */
+void orc_cb_wiring(int inputs, int g, int fan_in, uint64_t seed, uint32_t *idx, float *sgn) {
+    uint64_t s = seed | 1u;
+    const float amp = 1.0f / sqrtf((float)fan_in);
+    const int want = fan_in < inputs ? fan_in : inputs;
+    for (int j = 0; j < g; j++) {
+        uint32_t picked[64];
+        int np = 0;
+        while (np < want) {
+            s ^= s << 13;
+            s ^= s >> 7;
+            s ^= s << 17;
+            uint32_t r = (uint32_t)(s % (uint64_t)inputs);
+            int seen = 0;
+            for (int a = 0; a < np; a++) seen |= picked[a] == r;
+            if (!seen) picked[np++] = r;
+        }
+        for (int a = 0; a < np; a++) {
+            s ^= s << 13;
+            s ^= s >> 7;
+            s ^= s << 17;
+            idx[(size_t)j * fan_in + a] = picked[a];
+            sgn[(size_t)j * fan_in + a] = (s & 1u) == 0 ? amp : -amp;
+        }
+    }
+}
+
+/* gpu/model/fstep/arch_f3.rs:225-262 (cb_parts, the code) = gpu/v51b.rs:329-337 (cb_code):
+ * u = [xf, rmsnorm(emb_row, 1)] (2d); h_j = sum over the unit's fan-in of u[idx] * sgn, from 0 in
+ * order; the k-th largest of h kept (v - kth >= 0, ties kept), relu; c = a / (sqrt(sum a^2) + 1e-6),
+ * the sum from 0 in unit order. c [g]. */
+void orc_cb_code(const float *xf, const float *emb_row, int d, const uint32_t *idx, const float *sgn, int g,
+                 int fan_in, int k, float *c) {
+    float *u = (float *)malloc(sizeof(float) * 2 * (size_t)d);
+    float *ones = (float *)malloc(sizeof(float) * (size_t)d);
+    for (int i = 0; i < d; i++) ones[i] = 1.0f;
+    memcpy(u, xf, sizeof(float) * (size_t)d);
+    orc_rmsnorm(emb_row, 1, d, ones, u + d);
+    float *h = (float *)malloc(sizeof(float) * (size_t)g);
+    for (int j = 0; j < g; j++) {
+        float acc = 0.0f;
+        for (int a = 0; a < fan_in; a++) acc += u[idx[(size_t)j * fan_in + a]] * sgn[(size_t)j * fan_in + a];
+        h[j] = acc;
+    }
+    orc_kwta(h, 1, g, k, 0, c, NULL);
+    float s2 = 0.0f;
+    for (int j = 0; j < g; j++) s2 += c[j] * c[j];
+    const float len = sqrtf(s2) * 1.0f + (float)1e-6;
+    for (int j = 0; j < g; j++) c[j] = c[j] / len;
+    free(u);
+    free(ones);
+    free(h);
+}
+
+/* gpu/model/fstep/arch_f3.rs:262-299 (cb_parts, the read-out and the online table's share) with
+ * gpu/v51b.rs:373-389 (CbOnline::add): corr = sum over the non-zero units j in order of W[j] * c_j
+ * (W NULL: a zero read-out, corr = 0); out = xf + corr; with a table, out += sum over the same units
+ * of x_j * tab[j] where x_j = c_j, or (float)((double)c_j * scale) when scale != 1. */
+void orc_cb_apply(const float *xf, const float *c, int g, int d, const float *w, const float *tab, double scale,
+                  float *out) {
+    float *acc = (float *)calloc((size_t)d, sizeof(float));
+    if (w)
+        for (int j = 0; j < g; j++) {
+            if (c[j] == 0.0f) continue;
+            const float *wr = w + (size_t)j * d;
+            for (int i = 0; i < d; i++) acc[i] += wr[i] * c[j];
+        }
+    for (int i = 0; i < d; i++) out[i] = xf[i] + acc[i];
+    if (tab) {
+        memset(acc, 0, sizeof(float) * (size_t)d);
+        for (int j = 0; j < g; j++) {
+            if (c[j] == 0.0f) continue;
+            const float x = scale == 1.0 ? c[j] : (float)((double)c[j] * scale);
+            const float *tr = tab + (size_t)j * d;
+            for (int i = 0; i < d; i++) acc[i] += x * tr[i];
+        }
+        for (int i = 0; i < d; i++) out[i] = out[i] + acc[i];
+    }
+    free(acc);
+}
+
+/* gpu/fast4/cb.rs:25-84 (fast4_cb_learn_sized): p = softmax(logits) (max, exp(z - max), the sum
+ * from 0 in order, p / sum); err = p - onehot(next); delta = err . E (E [V][d], each output summed
+ * over v in order); the scale fades by 2^(-1/half) when half is finite (> 0 here) and the table
+ * folds (tab * scale in double, scale back to 1) below 1e-18; then for each non-zero unit u of the
+ * kept code c: s = lr * c_u, divided by the scale in double when it is not 1, tab[u] -= s * delta.
+ * Returns -ln max(p_next, 1e-30); a next outside [0, V) (the reference's IGNORE) changes nothing
+ * and returns NaN. */
+double orc_cb_learn(const float *logits, int V, int next, const float *E, int d, const float *c, int g, float lr,
+                    double half, double *scale, float *tab) {
+    if (V <= 0 || next < 0 || next >= V) return NAN; /* IGNORE (u32::MAX): no step, fast4/cb.rs:45-47 */
+    float *p = (float *)malloc(sizeof(float) * (size_t)V);
+    float mx = logits[0];
+    for (int j = 0; j < V; j++)
+        if (mx < logits[j]) mx = logits[j];
+    float den = 0.0f;
+    for (int j = 0; j < V; j++) {
+        p[j] = expf(logits[j] - mx);
+        den += p[j];
+    }
+    for (int j = 0; j < V; j++) p[j] = p[j] / den;
+    const double ce = -log((double)(p[next] > 1e-30f ? p[next] : 1e-30f));
+    for (int j = 0; j < V; j++) p[j] = p[j] - (j == next ? 1.0f : 0.0f);
+    float *delta = (float *)calloc((size_t)d, sizeof(float));
+    for (int i = 0; i < d; i++) {
+        float acc = 0.0f;
+        for (int j = 0; j < V; j++) acc = fmaf(p[j], E[(size_t)j * d + i], acc);
+        delta[i] = acc;
+    }
+    if (half > 0.0 && isfinite(half)) {
+        *scale *= exp2(-1.0 / half);
+        if (*scale < 1e-18) {
+            for (size_t z = 0; z < (size_t)g * d; z++) tab[z] = (float)((double)tab[z] * *scale);
+            *scale = 1.0;
+        }
+    }
+    const double sc = *scale;
+    for (int u = 0; u < g; u++) {
+        if (c[u] == 0.0f) continue;
+        float s = lr * c[u];
+        if (sc != 1.0) s = (float)((double)s / sc);
+        float *wr = tab + (size_t)u * d;
+        for (int i = 0; i < d; i++) wr[i] -= s * delta[i];
+    }
+    free(p);
+    free(delta);
+    return ce;
+}

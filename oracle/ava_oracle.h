@@ -159,6 +159,20 @@ typedef struct {
 int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *ids, int B, int T,
                       orc_state *st, float *logits, int gemm_planes, int threads, orc_trace *tr);
 
+/* ---------------------------------------------------------------- cerebellum head (CB, CB2) */
+
+/* gpu/v51b.rs:242-265: the fixed granule wiring (idx [g][fan_in] in [0, inputs), sgn +-1/sqrt(fan_in)). */
+void orc_cb_wiring(int inputs, int g, int fan_in, uint64_t seed, uint32_t *idx, float *sgn);
+/* gpu/model/fstep/arch_f3.rs:225-262: the granule code c [g] of xf [d] and the token's embedding row. */
+void orc_cb_code(const float *xf, const float *emb_row, int d, const uint32_t *idx, const float *sgn, int g,
+                 int fan_in, int k, float *c);
+/* gpu/model/fstep/arch_f3.rs:262-299, gpu/v51b.rs:373-389: out = xf + c.W (+ the online table's share). */
+void orc_cb_apply(const float *xf, const float *c, int g, int d, const float *w, const float *tab, double scale,
+                  float *out);
+/* gpu/fast4/cb.rs:25-84: one online learning step of a stream's table; returns the token's nats. */
+double orc_cb_learn(const float *logits, int V, int next, const float *E, int d, const float *c, int g, float lr,
+                    double half, double *scale, float *tab);
+
 /* The same building blocks exposed for tests. */
 void orc_rmsnorm(const float *x, int n, int d, const float *gain, float *out);
 float orc_sigmoid(float x);

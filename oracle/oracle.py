@@ -50,6 +50,12 @@ def lib():
         L.orc_sigmoid.restype = C.c_float
         L.orc_log_sigmoid.argtypes = [C.c_float]
         L.orc_log_sigmoid.restype = C.c_float
+        L.orc_cb_wiring.argtypes = [C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_void_p, C.c_void_p]
+        L.orc_cb_code.argtypes = [f32p, f32p, C.c_int, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int, f32p]
+        L.orc_cb_apply.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_double, f32p]
+        L.orc_cb_learn.restype = C.c_double
+        L.orc_cb_learn.argtypes = [f32p, C.c_int, C.c_int, f32p, C.c_int, f32p, C.c_int, C.c_float, C.c_double,
+                                   C.POINTER(C.c_double), f32p]
         L.orc_model_forward.restype = C.c_int
         L.orc_model_forward.argtypes = [C.POINTER(_Cfg), C.POINTER(_Model), C.c_void_p, C.c_int, C.c_int,
                                         C.POINTER(_State), C.c_void_p, C.c_int, C.c_int, C.POINTER(_Trace)]
@@ -185,6 +191,49 @@ def log_sigmoid(x):
     return np.float32(lib().orc_log_sigmoid(float(x)))
 
 
+# --------------------------------------------------------------------------- cerebellum head
+
+
+def cb_wiring(inputs, g, fan_in, seed):
+    """gpu/v51b.rs:242-265: idx [g, fan_in] uint32, sgn [g, fan_in] f32."""
+    idx = np.empty((g, fan_in), np.uint32)
+    sgn = np.empty((g, fan_in), np.float32)
+    lib().orc_cb_wiring(inputs, g, fan_in, C.c_uint64(seed), idx.ctypes.data, sgn.ctypes.data)
+    return idx, sgn
+
+
+def cb_code(xf, emb_row, idx, sgn, k):
+    """gpu/model/fstep/arch_f3.rs:225-262: the unit-length granule code c [g] of one row."""
+    xf, emb_row = _c(xf, np.float32), _c(emb_row, np.float32)
+    idx, sgn = _c(idx, np.uint32), _c(sgn, np.float32)
+    g, fan_in = sgn.shape
+    c = np.empty(g, np.float32)
+    lib().orc_cb_code(xf, emb_row, xf.shape[0], idx.ctypes.data, sgn, g, fan_in, k, c)
+    return c
+
+
+def cb_apply(xf, c, w=None, tab=None, scale=1.0):
+    """gpu/model/fstep/arch_f3.rs:262-299 + gpu/v51b.rs:373-389: xf + c.W (+ the table's share)."""
+    xf, c = _c(xf, np.float32), _c(c, np.float32)
+    w = None if w is None else _c(w, np.float32)
+    tab = None if tab is None else _c(tab, np.float32)
+    out = np.empty_like(xf)
+    lib().orc_cb_apply(xf, c, c.shape[0], xf.shape[0], None if w is None else w.ctypes.data,
+                       None if tab is None else tab.ctypes.data, C.c_double(scale), out)
+    return out
+
+
+def cb_learn(logits, nxt, E, c, lr, half, scale, tab):
+    """gpu/fast4/cb.rs:25-84: one online step of a stream's table tab [g, d] (updated in place).
+    Returns (nats, new scale)."""
+    logits, E, c = _c(logits, np.float32), _c(E, np.float32), _c(c, np.float32)
+    assert tab.dtype == np.float32 and tab.flags.c_contiguous
+    sc = C.c_double(scale)
+    nats = lib().orc_cb_learn(logits, logits.shape[0], int(nxt), E, E.shape[1], c, c.shape[0], C.c_float(lr),
+                              C.c_double(half if half and half > 0 else 0.0), C.byref(sc), tab)
+    return nats, sc.value
+
+
 # --------------------------------------------------------------------------- model
 
 class _QW(C.Structure):
@@ -249,8 +298,10 @@ class OracleModel:
                 if name in bp and bp[name] is not None:
                     setattr(blk, name, self._qw(bp[name]))
         self.blocks = blocks
+        head_w = np.ascontiguousarray(params["tok_emb"].T)
+        self._keep.append(head_w)
         self.model = _Model(tok_emb=self._ptr(params["tok_emb"]),
-                            head=self._qw(np.ascontiguousarray(params["tok_emb"].T)),
+                            head=self._qw(head_w),
                             final_norm=self._ptr(params["final_norm"]),
                             blocks=C.cast(blocks, C.POINTER(_Block)))
         c = self.cfg
@@ -260,6 +311,18 @@ class OracleModel:
                          alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
                          value_residual=int(c["value_residual"]), dense=int(c["dense"]),
                          relu2=int(c["relu2"]), momentum=c["momentum"], cap=c["cap"])
+        self.head_q, self.head_s = self.q8[id(head_w)]
+        # the cerebellum head (gpu/v51b.rs:18-32, 282-293): wiring from the fixed seed, the read-out W
+        # (cbh.wo, zero at init: None), the online rate and half-life
+        self.cb = int(c.get("cb_units", 0) or 0)
+        if self.cb:
+            from ava_amd import synth
+            d = c["d"]
+            self.cb_idx, self.cb_sgn = cb_wiring(2 * d, self.cb, synth.CB_FAN_IN, synth.CB_SEED)
+            self.cb_k = self.cb // synth.CB_SPARSITY
+            self.cb_w = params.get("cb_w")
+            self.cb_lr = synth.cb_rate(params["tok_emb"], c["cb_eta"])
+            self.cb_half = float(c.get("cb_half", 0.0) or 0.0)
 
     def _ptr(self, a):
         a = _c(a, np.float32)
@@ -285,6 +348,11 @@ class OracleModel:
             "eng_v": np.zeros((B, max(eng_cap, 1), de), np.float32),
             "eng_cap": eng_cap, "eng_len": 0,
         }
+        if self.cb:
+            # the online table per stream (gpu/v51b.rs:340-367: delta, scale) and the last position's code
+            st["cb_tab"] = np.zeros((B, self.cb, d), np.float32)
+            st["cb_scale"] = np.ones(B, np.float64)
+            st["cb_code"] = np.zeros((B, self.cb), np.float32)
         return st
 
     def forward(self, ids, state=None, planes=0, threads=1, trace=False, logits=True):
@@ -298,9 +366,13 @@ class OracleModel:
                                                          "eng_k", "eng_v")},
                      eng_cap=state["eng_cap"], eng_len=state["eng_len"])
         N = B * T
-        out = np.empty((N, c["vocab"]), np.float32) if logits else None
+        cb = self.cb and logits
+        out = np.empty((N, c["vocab"]), np.float32) if logits and not cb else None
         tr = None
         trd = {}
+        if cb and not trace:
+            trd = {"hf": np.empty((N, c["d"]), np.float32)}
+            tr = _Trace(hf=trd["hf"].ctypes.data)
         if trace:
             L, d, H = c["layers"], c["d"], c["hidden"]
             trd = {"spikes": np.empty((L, N, d), np.int8), "cur": np.empty((L, N, d), np.float32),
@@ -314,4 +386,31 @@ class OracleModel:
         if rc != 0:
             raise RuntimeError(f"orc_model_forward failed ({rc})")
         state["eng_len"] = cst.eng_len
+        if cb:
+            # gpu/model/fstep/arch.rs:1045-1047: the final normed state, the cerebellum's correction, the head
+            E = self.params["tok_emb"]
+            hf = trd["hf"]
+            xo = np.empty_like(hf)
+            for n in range(N):
+                bi = n // T
+                code = cb_code(hf[n], E[ids.reshape(-1)[n]], self.cb_idx, self.cb_sgn, self.cb_k)
+                xo[n] = cb_apply(hf[n], code, self.cb_w, state["cb_tab"][bi], float(state["cb_scale"][bi]))
+                if n % T == T - 1:
+                    state["cb_code"][bi] = code
+            if planes <= 0:
+                out = q8_matmul_ref(xo, self.head_q, self.head_s, threads)
+            else:
+                out = q8_matmul_planes(xo, planes, self.head_q, self.head_s, threads)
         return out, state, trd
+
+    def cb_learn(self, logits, nxt, state):
+        """gpu/fast4/cb.rs:25-84 per stream: logits [B, V] of each stream's last position, nxt [B]
+        (a negative id: no step). Returns the nats per stream."""
+        E = self.params["tok_emb"]
+        nats = []
+        for bi in range(len(nxt)):
+            n, sc = cb_learn(logits[bi], int(nxt[bi]), E, state["cb_code"][bi], self.cb_lr, self.cb_half,
+                             float(state["cb_scale"][bi]), state["cb_tab"][bi])
+            state["cb_scale"][bi] = sc
+            nats.append(n)
+        return np.array(nats)
