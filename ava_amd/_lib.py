@@ -74,6 +74,7 @@ def lib():
         "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
+        "ava_attend": [vp, i32, vp, vp, i32, i32, i32, i32, vp, vp, sz, vp],
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
         "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],
@@ -84,6 +85,8 @@ def lib():
             continue
         fn.argtypes = args
         fn.restype = i32
+    L.ava_attend_part_floats.argtypes = [i32, i32, i32]
+    L.ava_attend_part_floats.restype = sz
     L.ava_q8_workspace.argtypes = [i32, i32, i32]
     L.ava_q8_workspace.restype = sz
     if hasattr(L, "ava_model_free"):

@@ -138,11 +138,20 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
 int embed(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, hipStream_t st);
 int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
                float *hout, hipStream_t st);
-int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st);
+// G = h . W in f32; with few rows the K dimension is split over part (gate_part_floats of scratch).
+size_t gate_part_floats(int n, int d, int nc);
+int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, float *part, size_t part_floats,
+              hipStream_t st);
 int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, int8_t *xq, int32_t *xexp, int ldq,
              hipStream_t st);
+// The engram read: the tiled causal form for T > ENGRAM_SPLIT_T, the chunk-split decode form (with
+// part, engram_split_floats of scratch) for T <= ENGRAM_SPLIT_T.
+constexpr int ENGRAM_SPLIT_T = 4;
+size_t engram_split_floats(int B, int T, int n0);
+int attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T, float *out,
+           float *part, size_t part_floats, hipStream_t st);
 int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,
-                hipStream_t st);
+                float *part, size_t part_floats, hipStream_t st);
 // cb.hip: the cerebellum head (code, read-out with the online table to the head's planes, learning)
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
             const float *wsgn, int g, int k, int T, float *code, float *keep, hipStream_t st);

@@ -8,6 +8,8 @@
 // Element-wise arithmetic follows the reference's operation order (gpu/model.rs:458-622,
 // gpu/arch.rs:1873-2020, gpu/model/fstep.rs:207-292); the reductions sum in a tree, not in the
 // reference's sequential order, which moves results by float rounding only.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -121,17 +123,22 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
 // (h tile row-major, W tile row-major, both padded), each step 16 MFMA k-substeps per column block.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int GR = 128, GK = 32;
+// With few rows the K dimension is split: block (x, y) sums K range [y kslice, (y + 1) kslice) into
+// g + y n nc (partials, added in slice order by gate_sum_kernel).
 template <int NCB>  // column blocks of 32
 __global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict__ h, int n, int d,
-                                                        const float *__restrict__ w, int nc, float *__restrict__ g) {
+                                                        const float *__restrict__ w, int nc, int kslice,
+                                                        float *__restrict__ g) {
     __shared__ float sh[GR][GK + 1];
     __shared__ float sw[GK][NCB * 32 + 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * GR;
+    const int kb = blockIdx.y * kslice, ke = min(d, kb + kslice);
+    g += (size_t)blockIdx.y * n * nc;
     f32x16 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[cb] = f32x16{};
-    for (int k0 = 0; k0 < d; k0 += GK) {
+    for (int k0 = kb; k0 < ke; k0 += GK) {
         // h tile: 128 rows x 32 floats, 8 threads per row, float4 each
         for (int i = tid; i < GR * GK / 4; i += 256) {
             const int rr = i >> 3, kk = (i & 7) * 4;
@@ -309,6 +316,128 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
     }
 }
 
+// The decode form of the same read (flash-decoding), for a few queries per stream: query row
+// (b, t) at store position n0 + t reads keys 0..n0 + t. Its keys are cut into chunks of ACH; workgroup
+// (s, row) reads chunk s, each wave a quarter of it, 32 keys per iteration: lane l holds dims
+// 4 (l & 15)..+3 of the query, and lane group l >> 4 takes keys 4 j + (l >> 4) (a wave reads 4 whole
+// 256-byte rows per load, coalesced). The 16 lanes of a group add their partial dot products by DPP;
+// each group keeps its own running max, sum and 4 output dims. The 16 groups of a workgroup merge in
+// LDS into one partial (max, sum, o[64]) per (row, chunk): part [row][nsplit][66]; attend_combine
+// merges the chunks.
+constexpr int ACH = 1024;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// The sum over the 16 lanes of each DPP row, in every lane (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror).
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v + dpp_f<0x140>(v);
+}
+
+__global__ __launch_bounds__(256) void attend_split_kernel(const float *__restrict__ q, int ldq,
+                                                           const float *__restrict__ ks, const float *__restrict__ vs,
+                                                           int cap, int n0, int T, float scale, int nsplit,
+                                                           float *__restrict__ part) {
+    __shared__ float sm[16], sl[16];
+    __shared__ float so[16][64];
+    const int s = blockIdx.x, row = blockIdx.y;
+    const int b = row / T, t = row - b * T;
+    const int klen = n0 + t + 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, c4 = (lane & 15) * 4;
+    const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q + (size_t)row * ldq + c4);
+    const int kb = s * ACH + wave * (ACH / 4), ke = min(kb + ACH / 4, klen);
+    const float *kbase = ks + (size_t)b * cap * 64 + c4, *vbase = vs + (size_t)b * cap * 64 + c4;
+    float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = kb; k0 < ke; k0 += 32) {
+        f32x4 kv[8], vv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int kk = k0 + 4 * j + grp;
+            const bool ok = kk < ke;
+            kv[j] = ok ? *reinterpret_cast<const f32x4 *>(kbase + (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            vv[j] = ok ? *reinterpret_cast<const f32x4 *>(vbase + (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        float sc[8], bm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float a = kv[j][0] * q4[0];
+            a = fmaf(kv[j][1], q4[1], a);
+            a = fmaf(kv[j][2], q4[2], a);
+            a = fmaf(kv[j][3], q4[3], a);
+            a = row_sum16(a) * scale;
+            sc[j] = (k0 + 4 * j + grp < ke) ? a : -INFINITY;
+            bm = fmaxf(bm, sc[j]);
+        }
+        const float nm = fmaxf(m, bm);
+        if (nm == -INFINITY) continue;  // no key of this group yet
+        const float corr = expf(m - nm);  // m = -inf: 0
+        l *= corr;
+#pragma unroll
+        for (int z = 0; z < 4; z++) o[z] *= corr;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float p = expf(sc[j] - nm);  // -inf: 0
+            l += p;
+#pragma unroll
+            for (int z = 0; z < 4; z++) o[z] = fmaf(p, vv[j][z], o[z]);
+        }
+        m = nm;
+    }
+    const int gi = wave * 4 + grp;
+    if ((lane & 15) == 0) {
+        sm[gi] = m;
+        sl[gi] = l;
+    }
+#pragma unroll
+    for (int z = 0; z < 4; z++) so[gi][c4 + z] = o[z];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int c = threadIdx.x;
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) M = fmaxf(M, sm[i]);
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float w = sm[i] == -INFINITY ? 0.0f : expf(sm[i] - M);
+                L = fmaf(sl[i], w, L);
+                O = fmaf(so[i][c], w, O);
+            }
+        }
+        float *pr = part + ((size_t)row * nsplit + s) * 66;
+        if (c == 0) {
+            pr[0] = M;
+            pr[1] = L;
+        }
+        pr[2 + c] = O;
+    }
+}
+
+// out [row][64] = the merge of the row's chunk partials: M = max m_s, L = sum l_s e^(m_s - M),
+// o = sum o_s e^(m_s - M) / L.
+__global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int nsplit,
+                                                            float *__restrict__ out) {
+    const int row = blockIdx.x, c = threadIdx.x;
+    const float *pr = part + (size_t)row * nsplit * 66;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pr[(size_t)s * 66]);
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < nsplit; s++) {
+        const float ms = pr[(size_t)s * 66];
+        if (ms == -INFINITY) continue;
+        const float w = expf(ms - M);
+        L = fmaf(pr[(size_t)s * 66 + 1], w, L);
+        O = fmaf(pr[(size_t)s * 66 + 2 + c], w, O);
+    }
+    out[(size_t)row * 64 + c] = O / L;
+}
+
 // Append this forward's keys and values to the store: store[b][n0 + t] = kv[b T + t].
 __global__ void store_append_kernel(const float *__restrict__ kv, int ldkv, int T, int B, int cap, int n0,
                                     float *__restrict__ ks, float *__restrict__ vs) {
@@ -379,16 +508,49 @@ int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8
     return AVA_OK;
 }
 
-int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st) {
+// K slices of the gate product for n rows: enough workgroups for the chip when the row blocks are
+// few (decode), slices of at least 64.
+static int gate_slices(int n, int d) {
+    const int blocks = ceil_div(n, GR);
+    if (blocks >= 64) return 1;
+    return std::max(1, std::min(d / 64, ceil_div(128, blocks)));
+}
+
+size_t gate_part_floats(int n, int d, int nc) {
+    const int s = gate_slices(n, d);
+    return s > 1 ? (size_t)s * n * nc : 0;
+}
+
+__global__ void gate_sum_kernel(const float *__restrict__ part, int ns, size_t total, float *__restrict__ g) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    float v = part[i];
+    for (int s = 1; s < ns; s++) v += part[(size_t)s * total + i];
+    g[i] = v;
+}
+
+int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, float *part, size_t part_floats,
+              hipStream_t st) {
     AVA_REQUIRE(nc > 0 && nc <= 128 && d % GK == 0, AVA_ERR_SHAPE, "gate_gemm: %d columns (<= 128), d=%d", nc, d);
     const int blocks = ceil_div(n, GR);
+    int ns = gate_slices(n, d);
+    if (ns > 1 && (!part || part_floats < gate_part_floats(n, d, nc))) ns = 1;  // no scratch: one pass
+    const int kslice = ceil_div(ceil_div(d, ns), GK) * GK;
+    ns = ceil_div(d, kslice);
+    float *out = ns > 1 ? part : g;
+    const dim3 grid(blocks, ns);
     switch ((nc + 31) / 32) {
-    case 1: gate_mfma_kernel<1><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
-    case 2: gate_mfma_kernel<2><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
-    case 3: gate_mfma_kernel<3><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
-    default: gate_mfma_kernel<4><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    case 1: gate_mfma_kernel<1><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
+    case 2: gate_mfma_kernel<2><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
+    case 3: gate_mfma_kernel<3><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
+    default: gate_mfma_kernel<4><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
     }
     AVA_LAUNCHED("gate_gemm");
+    if (ns > 1) {
+        const size_t total = (size_t)n * nc;
+        gate_sum_kernel<<<ceil_div((long)total, 256), 256, 0, st>>>(part, ns, total, g);
+        AVA_LAUNCHED("gate_sum");
+    }
     return AVA_OK;
 }
 
@@ -403,16 +565,39 @@ int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, 
     return AVA_OK;
 }
 
+size_t engram_split_floats(int B, int T, int n0) {
+    return T <= ENGRAM_SPLIT_T ? (size_t)B * T * ceil_div(n0 + T, ACH) * 66 : 0;
+}
+
+int attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T, float *out,
+           float *part, size_t part_floats, hipStream_t st) {
+    AVA_REQUIRE(B > 0 && T > 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
+                "attend: B=%d T=%d, a store of %d entries holds %d + %d", B, T, cap, n0, T);
+    AVA_REQUIRE(ldq >= 64 && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d", ldq);
+    const float scale = (float)(1.0 / sqrt(64.0));
+    if (T <= ENGRAM_SPLIT_T) {
+        const int nsplit = ceil_div(n0 + T, ACH);
+        AVA_REQUIRE(part && part_floats >= engram_split_floats(B, T, n0), AVA_ERR_ARG,
+                    "attend: the decode read needs %zu floats of partials", engram_split_floats(B, T, n0));
+        attend_split_kernel<<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, nsplit, part);
+        AVA_LAUNCHED("attend_split");
+        attend_combine_kernel<<<B * T, 64, 0, st>>>(part, nsplit, out);
+        AVA_LAUNCHED("attend_combine");
+        return AVA_OK;
+    }
+    dim3 grid(ceil_div(T, 64), B);
+    attend_kernel<<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, out);
+    AVA_LAUNCHED("attend");
+    return AVA_OK;
+}
+
 int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,
-                hipStream_t st) {
+                float *part, size_t part_floats, hipStream_t st) {
     AVA_REQUIRE(n0 + T <= cap, AVA_ERR_SHAPE, "engram: store of %d entries holds %d + %d", cap, n0, T);
     const int total = B * T * 64;
     store_append_kernel<<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, ks, vs);
     AVA_LAUNCHED("store_append");
-    dim3 grid(ceil_div(T, 64), B);
-    attend_kernel<<<grid, 256, 0, st>>>(qkv, ldqkv, ks, vs, cap, n0, T, (float)(1.0 / sqrt(64.0)), out);
-    AVA_LAUNCHED("attend");
-    return AVA_OK;
+    return attend(qkv, ldqkv, ks, vs, cap, n0, B, T, out, part, part_floats, st);
 }
 
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st) {
@@ -431,3 +616,11 @@ int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n,
 }
 
 }  // namespace ava
+
+extern "C" size_t ava_attend_part_floats(int B, int T, int n0) { return ava::engram_split_floats(B, T, n0); }
+
+extern "C" int ava_attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T,
+                          float *out, float *part, size_t part_floats, ava_stream stream) {
+    AVA_REQUIRE(q && ks && vs && out, AVA_ERR_ARG, "attend: NULL argument");
+    return ava::attend(q, ldq, ks, vs, cap, n0, B, T, out, part, part_floats, (hipStream_t)stream);
+}

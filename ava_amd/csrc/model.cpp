@@ -85,6 +85,12 @@ struct ava_model {
     int cb_rows = 0;
     float *cb_err = nullptr, *cb_part = nullptr, *cb_delta = nullptr;
     double *cb_fold = nullptr;
+    // the gate product's K-slice partials for few rows
+    float *gate_part = nullptr;
+    size_t gate_part_floats = 0;
+    // the decode engram read's chunk partials (grow-only)
+    float *att_part = nullptr;
+    size_t att_part_floats = 0;
 
     bool timing = false;
     Timer timer;
@@ -292,6 +298,16 @@ int ensure_scratch(ava_model *m, size_t rows) {
         for (auto &s : m->streams) A((void **)&s, rows * d * 4);
     }
     if (c.cb_units > 0) A((void **)&m->cb_codes, rows * c.cb_units * 4);
+    // the gate product's K-slice partials: the most any row count up to `rows` asks for
+    size_t gp = 0;
+    for (size_t nn = 128; nn < rows + 128 && nn <= 64 * 128; nn += 128)
+        gp = std::max(gp, ava::gate_part_floats((int)std::min(nn, rows), (int)d, (int)nc));
+    m->gate_part = nullptr;
+    m->gate_part_floats = 0;
+    if (gp) {
+        A((void **)&m->gate_part, gp * 4);
+        if (!e) m->gate_part_floats = gp;
+    }
     if (e) return e;
     m->rows = rows;
     return AVA_OK;
@@ -358,6 +374,17 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
                 AVA_ERR_SHAPE, "forward: the engram store holds %d of %d entries, %d more do not fit", s->eng_len,
                 s->eng_cap, T);
     if (int e = ensure_scratch(m, (size_t)N)) return e;
+    if (c.eng_block >= 0) {
+        // sized for the fullest store this state can reach, so a decode loop allocates once
+        const size_t need = ava::engram_split_floats(B, T, s->eng_cap - T);
+        if (need > m->att_part_floats) {
+            (void)hipFree(m->att_part);
+            m->att_part = nullptr;
+            m->att_part_floats = 0;
+            AVA_HIP(hipMalloc(&m->att_part, need * sizeof(float)));
+            m->att_part_floats = need;
+        }
+    }
     if (m->timing && m->last_stream != st) {
         if (int e = collect(m)) return e;
     }
@@ -377,7 +404,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         // the fast-weight memory
         AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
-        AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, st));
+        AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, m->gate_part,
+                                            m->gate_part_floats, st));
         const bool vr = c.value_residual != 0;
         const size_t sm = (size_t)i * B * nh * 64 * 64;
         AVA_RUN("mem_scan", ava::mem_block(m->P, m->G, B, T, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,
@@ -390,7 +418,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         if (b.eng) {
             AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.eng_norm, P, m->xq, m->xexp, ldd, nullptr, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.eqkv.w, ava::Q8_STORE, m->qkv, 3 * de, nullptr, st));
-            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, s->eng_cap, s->eng_len, m->eo, st));
+            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, s->eng_cap, s->eng_len, m->eo,
+                                                   m->att_part, m->att_part_floats, st));
             AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         }
@@ -455,6 +484,7 @@ extern "C" void ava_model_free(ava_model *m) {
     for (void *p : m->scratch) (void)hipFree(p);
     for (hipEvent_t e : m->timer.pool) (void)hipEventDestroy(e);
     for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
+    (void)hipFree(m->att_part);
     delete m;
 }
 

@@ -530,6 +530,146 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void q8_gemm_dma_kernel(const i
     epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
+// ------------------------------------------------------------------ the product for few rows
+//
+// Decode shapes (m <= 512 rows) leave the tiled kernels with a few dozen workgroups. Here a workgroup
+// owns a 32 x 32 output block and all of K; its 4 waves take the 128-byte K steps kt = w, w + 4, ...
+// each on its own: a wave stages its step (P planes x 32 rows and 32 weight columns, 128 bytes each)
+// in its own double-buffered LDS with direct-to-LDS loads and waits for its own loads only, so the K
+// loop has no barrier. At the end wave w forms its exact plane combination A_w = sum_p acc_p
+// 2^(7(P-1-p)) in double (an integer below 2^47); the four are added in LDS (still exact) and rounded
+// once as the tiled kernels' epilogue does: the same bits as they give, for any m.
+template <int P, int EPI>
+__global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
+                                                       int m, int n, int ldk, const int8_t *__restrict__ qt,
+                                                       const float *__restrict__ scale, EpiArgs ep) {
+    constexpr int BM = 32, BN = 32, BK = 128, CPR = 8, RPI = 8;  // a 1 KB load covers 8 rows of 128 bytes
+    constexpr int ROWS = P * BM + BN, LPS = ROWS / RPI, BUF = ROWS * BK;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];  // 4 waves x 2 buffers of BUF bytes
+    const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+    int mt, nt;
+    tile_origin(tiles_m, tiles_n, tiles_m, mt, nt);  // a weight block's row blocks on one XCD
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int8_t *wbuf = smem + wave * 2 * BUF;
+
+    const int8_t *src[LPS];
+#pragma unroll
+    for (int i = 0; i < LPS; i++) {
+        const int srow = i * RPI + lane / CPR;
+        if (srow < P * BM) {
+            const int p = srow / BM, rr = srow % BM;
+            const int row = min(m0 + rr, m - 1);
+            src[i] = xq + ((size_t)p * m + row) * ldk + swz<CPR>(rr, lane % CPR) * 16;
+        } else {
+            const int rr = srow - P * BM;
+            const int col = min(n0 + rr, n - 1);
+            src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane % CPR) * 16;
+        }
+    }
+    auto issue = [&](int kt, int b) {
+#pragma unroll
+        for (int i = 0; i < LPS; i++) dma16(src[i] + kt * BK, wbuf + b * BUF + i * 1024);
+    };
+
+    i32x16 acc[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) acc[p] = i32x16{};
+    const int KT = ldk / BK, frow = lane & 31, fc = lane >> 5;
+    int b = 0;
+    if (wave < KT) issue(wave, 0);
+    for (int kt = wave; kt < KT; kt += 4) {
+        if (kt + 4 < KT) {
+            issue(kt + 4, b ^ 1);
+            wait_vm<LPS>();  // this step's loads are in LDS; the next step's are in flight
+        } else {
+            wait_vm<0>();
+        }
+        const int8_t *la = wbuf + b * BUF, *lb = la + P * BM * BK;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ks++) {
+            const int c = swz<CPR>(frow, ks * 2 + fc) * 16;
+            const i32x4 bf = *reinterpret_cast<const i32x4 *>(lb + frow * BK + c);
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                const i32x4 af = *reinterpret_cast<const i32x4 *>(la + (p * BM + frow) * BK + c);
+                acc[p] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, acc[p], 0, 0, 0);
+            }
+        }
+        // the buffer is refilled two steps on: its fragment reads must have completed
+#if defined(__HIP_DEVICE_COMPILE__)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+        b ^= 1;
+    }
+    __syncthreads();  // every wave is done with its buffers
+
+    const int rsub = (lane >> 5) * 4, col = n0 + (lane & 31);
+    if (EPI == EPI_ACC) {
+        int *si = reinterpret_cast<int *>(smem);  // [wave][p][16][64]
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) si[((wave * P + p) * 16 + r) * 64 + lane] = acc[p][r];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+            if (row < m && col < n)
+#pragma unroll
+                for (int p = 0; p < P; p++) {
+                    int v = 0;
+#pragma unroll
+                    for (int w = 0; w < 4; w++) v += si[((w * P + p) * 16 + r) * 64 + lane];
+                    reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = v;
+                }
+        }
+        return;
+    }
+    double *sd = reinterpret_cast<double *>(smem);  // [wave][16][64]
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        double A = (double)acc[0][r];
+#pragma unroll
+        for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][r]);
+        sd[(wave * 16 + r) * 64 + lane] = A;
+    }
+    __syncthreads();
+    if (col >= n) return;
+    const float sc = scale[col];
+    const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+    float *ybase = reinterpret_cast<float *>(ep.y);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+        if (row >= m) continue;
+        const double A = ((sd[r * 64 + lane] + sd[(16 + r) * 64 + lane]) + sd[(32 + r) * 64 + lane]) +
+                         sd[(48 + r) * 64 + lane];
+        const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
+        float v = ldexpf((float)A, ex) * sc;
+        if (EPI == EPI_MUL) v = v * cv;
+        float *yp = ybase + (size_t)row * ep.ldy + col;
+        if (EPI == EPI_ADD) v = *yp + v;
+        *yp = v;
+    }
+}
+
+template <int P, int EPI>
+int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                 EpiArgs ep, hipStream_t st) {
+    const int total = ((m + 31) / 32) * ((n + 31) / 32);
+    const size_t lds = (size_t)8 * (P * 32 + 32) * 128;
+    static bool attr = false;
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds));
+        attr = true;
+    }
+    q8_small_kernel<P, EPI><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
+}
+
 // ------------------------------------------------------------------ the product, deep-ring form
 //
 // As q8_gemm_dma_kernel, with the direct-to-LDS loads and the fragment reads both issued as inline
@@ -844,7 +984,18 @@ int tile_override() {
     if (v == -2) {
         const char *e = getenv("AVA_Q8_TILE");
         v = e ? atoi(e) : -1;
-        if (v >= NTILES) v = -1;
+        if (v > NTILES) v = -1;  // NTILES: the few-rows kernel
+    }
+    return v;
+}
+
+// Products of at most this many rows take the few-rows kernel; AVA_Q8_SMALL_ROWS overrides it (tuning).
+int small_rows() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_Q8_SMALL_ROWS");
+        v = e ? atoi(e) : 512;
+        if (v < 0) v = 0;
     }
     return v;
 }
@@ -898,6 +1049,9 @@ template <int P, int EPI>
 int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                 EpiArgs ep, hipStream_t st) {
     int t = tile_override();
+    // few rows (decode): 32 x 32 blocks with the K steps spread over the waves
+    if (t < 0 && m <= small_rows()) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    if (t == NTILES) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
     // the direct-to-LDS 128 x 256 tile, 8 waves: 128-byte K steps for split-plane inputs, 64-byte
     // ones for the single spike plane (measured best on every config[3] shape)
     if (t < 0) t = P == 1 ? 3 : 14;

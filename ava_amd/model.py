@@ -108,7 +108,7 @@ class Model:
         st.eng_len = cst.eng_len
         return logits
 
-    def cb_learn(self, logits: torch.Tensor, nxt: torch.Tensor, st: State) -> torch.Tensor:
+    def cb_learn(self, logits: torch.Tensor, nxt: torch.Tensor, st: State, nats: torch.Tensor | None = None):
         """One online step of every stream's table (Model::cb_learn): logits [B, >= vocab] f32 GPU rows of
         each stream's last position, nxt [B] int32 GPU (outside [0, vocab): no step). Returns nats [B] f64."""
         if st.cb_tab is None:
@@ -119,7 +119,10 @@ class Model:
         if not (logits.is_cuda and logits.dtype == torch.float32 and logits.dim() == 2 and logits.shape[0] == B
                 and logits.stride(1) == 1):
             raise ValueError("logits: [B, vocab] f32 GPU rows with unit column stride are required")
-        nats = torch.empty(B, dtype=torch.float64, device=logits.device)
+        if nats is None:
+            nats = torch.empty(B, dtype=torch.float64, device=logits.device)
+        elif not (nats.is_cuda and nats.dtype == torch.float64 and nats.numel() >= B and nats.is_contiguous()):
+            raise ValueError("nats: a contiguous f64 GPU tensor of >= B entries is required")
         cst = st.c()
         stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
         check(lib().ava_model_cb_learn(self.h, C.byref(cst), C.c_void_p(logits.data_ptr()), logits.stride(0),

@@ -11,6 +11,7 @@ status (the reference bail!s on shape, dtype and contiguity errors).
     kwta_relu(u, k, relu2)       model.rs:504-528 + arch.rs:1820-1835
     mem_gen(q, k, e, v, la, b, m)   mem_gen.rs:127-137
     delta_rule_from(q, k, v, beta, la, f0)   model.rs:744-799 (chunked, per-head gates)
+    attend(q, ks, vs, n0)        model/fstep.rs:303-329 (one head of 64, causal, over a store)
 """
 from __future__ import annotations
 
@@ -176,3 +177,19 @@ def delta_rule_from(q, k, v, beta, la=None, f0=None):
     check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(la), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
           "ava_delta_chunk")
     return y, F
+
+
+def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int) -> torch.Tensor:
+    """model/fstep.rs:303-329 per stream and query: q [B, T, 64]; ks, vs [B, cap, 64] holding entries
+    0..n0+T-1; query t reads entries 0..n0+t. Returns out [B, T, 64]."""
+    for t, nm in ((q, "q"), (ks, "ks"), (vs, "vs")):
+        _need(t, torch.float32, f"attend {nm}")
+    B, T, de = q.shape
+    cap = ks.shape[1]
+    if de != 64 or ks.shape != vs.shape or ks.shape[0] != B or ks.shape[2] != 64:
+        raise ValueError("attend: q [B, T, 64], ks and vs [B, cap, 64] are required")
+    out = torch.empty_like(q)
+    n = lib().ava_attend_part_floats(B, T, n0)
+    part = torch.empty(max(n, 1), dtype=torch.float32, device=q.device)
+    check(lib().ava_attend(_p(q), 64, _p(ks), _p(vs), cap, n0, B, T, _p(out), _p(part), n, _stream()), "ava_attend")
+    return out

@@ -393,7 +393,113 @@ class Stack:
                           f"config[3]'s model, B={B}, T={T}, {th} threads for the products, {dt:.2f} s"}
 
 
-WORKLOADS = {"stack": Stack, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
+class Decode:
+    """config[4]: batched stateful decode. B=256 streams of config[3]'s model with the cerebellum head
+    (12,288 granule units, 384 kept, per-stream online table with a 256-token half-life). Each stream's
+    state (membranes, thresholds, fast weights and momentum, the engram store) comes from a
+    teacher-forced prefill of `prefill` random tokens (32,768 as config[4]; untimed, in pieces of
+    `piece` tokens). A step is one token per stream: the forward (T = 1) to logits [256, 8192], then
+    the online table's learning step on each stream's next token (random ids: a teacher-forced
+    continuation)."""
+
+    name = "decode"
+    kernel = "attend_split"
+    metric = "tokens/sec batched stateful int8 decode @B=256 streams, 32768-token state (config[4]), 1 GPU; % HBM roofline"
+    default_steps = 256
+
+    def __init__(self, B=256, prefill=32768, piece=512, steps_cap=1024, planes=3):
+        import torch
+        from ava_amd import synth
+        from ava_amd.model import Model
+
+        self.cfg = c = synth.config("ava04_d1024_decode")
+        self.prefill = prefill = int(os.environ.get("AVA_DECODE_PREFILL", prefill))
+        self.B, self.planes = B, planes
+        log("bench: building weights")
+        self.params = synth.params(c, seed=0)
+        self.model = Model(c, self.params, planes=planes)
+        self.st = self.model.state(B, eng_cap=prefill + steps_cap)
+        g = torch.Generator(device="cuda").manual_seed(5)
+        V = c["vocab"]
+        self.toks = torch.randint(0, V, (steps_cap + 1, B, 1), device="cuda", generator=g, dtype=torch.int32)
+        self.nexts = self.toks[1:, :, 0].contiguous()
+        self.logits = torch.empty((B, V), device="cuda")
+        self.nats = torch.empty(B, dtype=torch.float64, device="cuda")
+        self.t = 0
+        self.steps_cap = steps_cap
+        t0 = time.perf_counter()
+        done = 0
+        while done < prefill:
+            n = min(piece, prefill - done)
+            ids = torch.randint(0, V, (B, n), device="cuda", generator=g, dtype=torch.int32)
+            self.model.forward_with_state(ids, self.st, want_logits=False)
+            done += n
+        torch.cuda.synchronize()
+        log(f"bench: prefill of {prefill} tokens x {B} streams in {time.perf_counter() - t0:.1f} s")
+        self.tokens = B
+        d, H, L, de = c["d"], c["hidden"], c["layers"], c["eng_dim"]
+        nh = d // c["head_size"]
+        self.config = {"workload": "stateful decode config[4]", "streams": B, "prefill": prefill, "d": d,
+                       "blocks": L, "hidden": H, "kwta_k": c["kwta_k"], "heads": nh, "vocab": V,
+                       "engram_block": c["eng_block"], "engram_store": "f32", "cb_units": c["cb_units"],
+                       "cb_half": c["cb_half"], "momentum": c["momentum"], "act_planes": planes}
+        self.dtype = "i8"
+        self.breakdown = None
+
+    def step_bytes(self):
+        """Algorithmic HBM bytes of one step at the current store length: int8 weights, the carried
+        state read and written (LIF v, s, a; F and S), the engram keys and values read, the step's keys
+        and values written, the online table rows of the kept units read (apply) and read + written
+        (learn), the code, the logits, E read by the learning step."""
+        c, B = self.cfg, self.B
+        d, H, L, V, de, G = c["d"], c["hidden"], c["layers"], c["vocab"], c["eng_dim"], c["cb_units"]
+        w = L * 16 * d * d + 4 * d * de + d * V
+        lif = L * B * d * 4 * 3 * 2
+        fs = L * B * d * c["head_size"] * 4 * 2 * 2
+        n = self.st.eng_len
+        kv = B * (n + 1) * de * 4 * 2 + B * de * 4 * 2
+        kept = G // 32
+        cb = B * kept * d * 4 * 3 + B * G * 4 * 2
+        out = B * V * 4 * 2 + V * d * 4
+        return w + lif + fs + kv + cb + out
+
+    def step(self, stream, ev=None):
+        if self.t >= self.steps_cap:
+            raise RuntimeError("decode: more steps than the store was sized for")
+        self.model.forward_with_state(self.toks[self.t], self.st, self.logits)
+        self.model.cb_learn(self.logits, self.nexts[self.t], self.st, nats=self.nats)
+        self.t += 1
+
+    def start_timed(self):
+        self.bytes0 = self.step_bytes()
+        self.model.timing(reset=True)
+        self.model.set_timing(True)
+
+    def kernel_ms(self):
+        t = self.model.timing(reset=True)
+        self.model.set_timing(False)
+        self.breakdown = {k: {"calls": v[0], "ms": round(v[1], 3)} for k, v in sorted(t.items(), key=lambda kv: -kv[1][1])}
+        calls, ms = t.get("attend", (1, 0.0))
+        self.att_calls, self.att_ms = calls, ms
+        return [ms]
+
+    def roofline(self, kernel_s):
+        # the whole step is HBM-bound: algorithmic bytes per step over the measured step time
+        per = self.wall / self.nsteps
+        b = 0.5 * (self.bytes0 + self.step_bytes())
+        a = b / per / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
+                "algorithmic_bytes_per_step": b, "scope": "whole decode step",
+                "kernel_avg_us": self.att_ms * 1e3 / max(self.att_calls, 1)}
+
+    def extra(self):
+        return {"breakdown_ms_total": self.breakdown}
+
+    def cpu_baseline(self):
+        return None
+
+
+WORKLOADS = {"stack": Stack, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
 DEFAULT = "stack"
 
 
@@ -407,7 +513,7 @@ def extra_workloads():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 10; decode 256)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -427,6 +533,8 @@ def main():
     default = extra_workloads()
     wname = args.workload or default
     W = WORKLOADS[wname]()
+    if args.steps is None:
+        args.steps = getattr(W, "default_steps", 10)
     stream = torch.cuda.current_stream()
     sptr = __import__("ctypes").c_void_p(stream.cuda_stream)
 
@@ -445,6 +553,7 @@ def main():
         W.step(sptr, ev[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    W.wall = wall
     # the dominant kernel's launches: one event pair per step, or the workload's own launch timer
     kernel_ms = W.kernel_ms() if hasattr(W, "kernel_ms") else [a.elapsed_time(b) for a, b in ev]
     ms_per_step = wall * 1e3 / args.steps
@@ -461,7 +570,7 @@ def main():
         cpu = W.cpu_baseline()
 
     out = {
-        "metric": METRIC,
+        "metric": getattr(W, "metric", METRIC),
         "value": value,
         "unit": "tokens/s",
         "n_gpus": 1,

@@ -128,6 +128,19 @@ int ava_mem_scan(const float *q, const float *k, const float *e, const float *v,
 int ava_delta_chunk(const float *q, const float *k, const float *v, const float *la, const float *beta, int BH,
                     int T, int hs, float *F, float *y, ava_stream stream);
 
+/* ------------------------------------------------------------------ engram read */
+
+/* The engram's causal single-head read (head size 64) over a store that already holds entries
+ * 0..n0+T-1 of each stream: query (b, t), row b*T + t of q (ldq floats apart), reads entries
+ * 0..n0+t: softmax(q.k / sqrt(64)) . V, the softmax in its online (running max) form. ks, vs
+ * [B][cap][64]; out [B*T][64]. For T <= 4 (decode) the keys are cut into chunks of 1024 read by
+ * separate workgroups, whose partials need ava_attend_part_floats(B, T, n0) floats of device
+ * scratch in part; for T > 4 part may be NULL. Replaces fstep::attend (model/fstep.rs:303-329)
+ * and one head of attention_g (model.rs:543-562) / memory::read. */
+size_t ava_attend_part_floats(int B, int T, int n0);
+int ava_attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T,
+               float *out, float *part, size_t part_floats, ava_stream stream);
+
 /* ------------------------------------------------------------------ model */
 
 /* The block options of the path (Ava 0.4's recipe, release/ava-0.4/arch.txt:1). */

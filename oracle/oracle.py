@@ -140,6 +140,16 @@ def lif_scan(cur, ps, v0=None, s0=None, a0=None, levels=2, signed=True, alif=Tru
     return spk, v, s, a
 
 
+def lif_params(block, alif=True):
+    """The scan's per-channel parameters of one block as the oracle's forward forms them
+    (ava_oracle.c, after gpu/arch.rs:1632-1695): beta = sigmoid(beta_p) | theta | rho = sigmoid(arho)
+    | gain, in f32 with the oracle's own sigmoid."""
+    f = np.vectorize(lambda x: lib().orc_sigmoid(float(x)), otypes=[np.float32])
+    z = np.zeros_like(block["theta"], dtype=np.float32)
+    return np.concatenate([f(block["beta_p"]), np.asarray(block["theta"], np.float32),
+                           f(block["arho"]) if alif else z, np.asarray(block["again"], np.float32) if alif else z])
+
+
 def kwta(u, k, relu2=True):
     """gpu/model/fstep.rs:295-299 + fstep/arch.rs:976-989 -> (a [n, h], kth [n])."""
     u = _c(u, np.float32)

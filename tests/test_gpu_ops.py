@@ -126,7 +126,9 @@ def test_kwta_matches_oracle(relu2, dev):
 
 # ----------------------------------------------------------------------------- int8 products
 
-SHAPES = [(32, 32, 3), (128, 128, 1), (96, 200, 5), (64, 4112, 2), (1024, 1024, 300), (1024, 192, 129)]
+# m <= 512 takes the few-rows kernel (32 x 32 blocks, K steps over the waves), larger m the tiled ones
+SHAPES = [(32, 32, 3), (128, 128, 1), (96, 200, 5), (64, 4112, 2), (1024, 1024, 300), (1024, 192, 129),
+          (4096, 1024, 257), (1024, 1024, 700), (512, 4112, 530)]
 
 
 @pytest.mark.parametrize("din,dout,m", SHAPES)
