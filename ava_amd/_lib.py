@@ -25,7 +25,8 @@ class Config(C.Structure):
     _fields_ = [(n, i32) for n in ("vocab", "d", "layers", "hidden", "kwta_k", "head_size", "gate_rank",
                                    "eng_block", "eng_dim", "levels", "alif", "lif_scale", "value_residual",
                                    "dense", "relu2")] + \
-               [("momentum", f32), ("cap", f32), ("planes", i32), ("cb_units", i32), ("cb_lr", f32), ("cb_half", f32)]
+               [("momentum", f32), ("cap", f32), ("planes", i32), ("cb_units", i32), ("cb_lr", f32), ("cb_half", f32),
+                ("eng_half", i32)]
 
 
 BLOCK_FIELDS = ["lif_norm", "win", "beta_p", "theta", "arho", "again", "wout",
@@ -74,7 +75,7 @@ def lib():
         "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
-        "ava_attend": [vp, i32, vp, vp, i32, i32, i32, i32, vp, vp, sz, vp],
+        "ava_attend": [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, sz, vp],
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
         "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],

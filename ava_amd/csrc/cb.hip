@@ -1,5 +1,5 @@
 // The cerebellum head (CB) and its online table (CB2) for gfx950: the granule code, the read-out with
-// the table's share (emitting the head product's split planes), and the online learning step.
+// the table's share, and the online learning step.
 //
 // Reference: gpu/v51b.rs:18-32 (the part), :242-265 (wiring), :327-337 (cb_code), :373-389
 // (CbOnline::add); gpu/model/fstep/arch_f3.rs:225-299 (the one-row forward); gpu/fast4/cb.rs:25-84
@@ -71,16 +71,22 @@ __device__ __forceinline__ uint32_t block_umin(uint32_t v, uint32_t *red) {
 
 // The granule code of rows n: code [n][g]. With keep != NULL, each stream's last position (row
 // b T + T - 1) is also written to keep [b][g] (the code the learning step uses).
+// With lcnt != NULL the row's non-zero units are also listed in unit order: lidx/lval [n][lcap] (unit,
+// value) and lcnt [n] = their number (beyond lcap only the first lcap are listed; readers then use the
+// dense code).
 template <int GPT>
 __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ xf, const int32_t *__restrict__ ids,
                                                      const float *__restrict__ emb, int d, int vocab,
                                                      const uint32_t *__restrict__ widx,
                                                      const float *__restrict__ wsgn, int g, int k, int T,
-                                                     float *__restrict__ code, float *__restrict__ keep) {
+                                                     float *__restrict__ code, float *__restrict__ keep,
+                                                     int *__restrict__ lcnt, int *__restrict__ lidx,
+                                                     float *__restrict__ lval, int lcap) {
     __shared__ float su[2048];
     __shared__ float fred[4];
     __shared__ int ired[4];
     __shared__ uint32_t ured[4];
+    __shared__ int s_wc[4][GPT];
     const int row = blockIdx.x, tid = threadIdx.x;
     int id = ids[row];
     id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // an id outside [0, vocab) reads the nearest row
@@ -218,95 +224,95 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
 #pragma unroll
     for (int i = 0; i < GPT; i++) {
         const int j = tid + i * NT;
+        h[i] = j < g ? h[i] / len : 0.0f;
         if (j < g) {
-            const float c = h[i] / len;
-            cr[j] = c;
-            if (kr) kr[j] = c;
+            cr[j] = h[i];
+            if (kr) kr[j] = h[i];
         }
+    }
+    if (lcnt) {
+        // unit j = tid + 256 i: in unit order the i-th group of 256 comes after all earlier groups
+        const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+        for (int i = 0; i < GPT; i++) {
+            const int c = __popcll(__ballot(h[i] != 0.0f));
+            if (lane == 0) s_wc[wave][i] = c;
+        }
+        __syncthreads();
+        int base = 0;
+        int *li = lidx + (size_t)row * lcap;
+        float *lv = lval + (size_t)row * lcap;
+#pragma unroll
+        for (int i = 0; i < GPT; i++) {
+            const uint64_t bm = __ballot(h[i] != 0.0f);
+            int before = 0;
+            for (int w = 0; w < wave; w++) before += s_wc[w][i];
+            const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0));
+            const int pos = base + before + rank;
+            if (h[i] != 0.0f && pos < lcap) {
+                li[pos] = tid + i * NT;
+                lv[pos] = h[i];
+            }
+            base += (s_wc[0][i] + s_wc[1][i]) + (s_wc[2][i] + s_wc[3][i]);
+        }
+        if (tid == 0) lcnt[row] = base;
     }
 }
 
-// out = xf + sum over the non-zero units j in order of W[j] c_j (W NULL: nothing), then + the table's
-// share sum x_j tab[b][j] with x_j = c_j or (float)((double)c_j * scale[b]); the row's split planes
-// for the head product (and out itself when hout). One workgroup per row; the non-zero units are
-// compacted into LDS in unit order first (dynamic LDS: 8 bytes per unit).
-template <int P>
-__global__ __launch_bounds__(NT) void cb_apply_kernel(const float *__restrict__ xf, const float *__restrict__ code,
-                                                      int g, int d, const float *__restrict__ w,
-                                                      const float *__restrict__ tab, const double *__restrict__ scale,
-                                                      int T, int n, int8_t *__restrict__ xq,
-                                                      int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
-    extern __shared__ __attribute__((aligned(16))) char dyn[];
-    int *s_j = reinterpret_cast<int *>(dyn);
-    float *s_c = reinterpret_cast<float *>(dyn + sizeof(int) * (size_t)g);
-    __shared__ int s_cnt[NT + 1];
-    __shared__ float fred[4];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float *cr = code + (size_t)row * g;
-
-    // compaction: thread tid scans units [tid * per, (tid + 1) * per)
-    const int per = (g + NT - 1) / NT, j0 = tid * per, j1 = min(g, j0 + per);
-    int cnt = 0;
-    for (int j = j0; j < j1; j++) cnt += cr[j] != 0.0f;
-    s_cnt[tid + 1] = cnt;
-    if (tid == 0) s_cnt[0] = 0;
-    __syncthreads();
-    if (tid == 0)
-        for (int t = 1; t <= NT; t++) s_cnt[t] += s_cnt[t - 1];
-    __syncthreads();
-    int o = s_cnt[tid];
-    for (int j = j0; j < j1; j++) {
-        const float c = cr[j];
-        if (c != 0.0f) {
-            s_j[o] = j;
-            s_c[o] = c;
-            o++;
+// out [n][d] = xf + sum over the non-zero units j in order of W[j] c_j (W NULL: nothing), then + the
+// table's share sum x_j tab[b][j] with x_j = c_j or (float)((double)c_j * scale[b]), from the row's
+// unit list (cb_code's lidx/lval) or, when the list overflowed, the dense code. Block (row, 256
+// columns), one column per thread: the table rows are read 1 KB per wave, coalesced.
+constexpr int APPLY_LCAP = 1024;
+__global__ __launch_bounds__(NT) void cb_apply_cols_kernel(const float *__restrict__ xf, const float *__restrict__ code,
+                                                           int g, int d, const float *__restrict__ w,
+                                                           const float *__restrict__ tab,
+                                                           const double *__restrict__ scale, int T,
+                                                           const int *__restrict__ lcnt, const int *__restrict__ lidx,
+                                                           const float *__restrict__ lval, int lcap,
+                                                           float *__restrict__ out) {
+    __shared__ int s_j[APPLY_LCAP];
+    __shared__ float s_c[APPLY_LCAP];
+    const int row = blockIdx.x, tid = threadIdx.x, c = blockIdx.y * NT + tid;
+    const int cnt = lcnt[row];
+    const bool listed = cnt <= lcap && cnt <= APPLY_LCAP;
+    if (listed)
+        for (int q = tid; q < cnt; q += NT) {
+            s_j[q] = lidx[(size_t)row * lcap + q];
+            s_c[q] = lval[(size_t)row * lcap + q];
         }
-    }
     __syncthreads();
-    const int nz = s_cnt[NT];
-
+    if (c >= d) return;
     const int b = row / T;
     const double sc = scale ? scale[b] : 1.0;
-    const float *xr = xf + (size_t)row * d;
-    const float *tb = tab ? tab + (size_t)b * g * d : nullptr;
-    float amax = 0.0f;
-    float outv[4];
-    const int cbase = tid * 4;  // this thread's 4 columns (d <= 1024)
-#pragma unroll
-    for (int z = 0; z < 4; z++) {
-        const int c = cbase + z;
-        float acc = 0.0f;
-        if (c < d) {
-            if (w)
-                for (int q = 0; q < nz; q++) acc += w[(size_t)s_j[q] * d + c] * s_c[q];
-            float o2 = xr[c] + acc;
-            if (tb) {
-                float acc2 = 0.0f;
-                for (int q = 0; q < nz; q++) {
-                    const float x = sc == 1.0 ? s_c[q] : (float)((double)s_c[q] * sc);
-                    acc2 += x * tb[(size_t)s_j[q] * d + c];
-                }
-                o2 = o2 + acc2;
+    const float *tb = tab ? tab + (size_t)b * g * d + c : nullptr;
+    const float *cr = code + (size_t)row * g;
+    float acc = 0.0f, acc2 = 0.0f;
+    if (listed) {
+        if (w) {
+#pragma unroll 8
+            for (int q = 0; q < cnt; q++) acc += w[(size_t)s_j[q] * d + c] * s_c[q];
+        }
+        if (tb) {
+            if (sc == 1.0) {
+#pragma unroll 8
+                for (int q = 0; q < cnt; q++) acc2 += s_c[q] * tb[(size_t)s_j[q] * d];
+            } else {
+#pragma unroll 8
+                for (int q = 0; q < cnt; q++) acc2 += (float)((double)s_c[q] * sc) * tb[(size_t)s_j[q] * d];
             }
-            outv[z] = o2;
-            amax = fmaxf(amax, fabsf(o2));
-            if (hout) hout[(size_t)row * d + c] = o2;
-        } else {
-            outv[z] = 0.0f;
+        }
+    } else {
+        for (int j = 0; j < g; j++) {
+            const float cj = cr[j];
+            if (cj == 0.0f) continue;
+            if (w) acc += w[(size_t)j * d + c] * cj;
+            if (tb) acc2 += (sc == 1.0 ? cj : (float)((double)cj * sc)) * tb[(size_t)j * d];
         }
     }
-    amax = block_max(amax, fred);
-    const int e = ava::plane_exp(amax);
-    if (tid == 0) xexp[row] = e;
-    for (int c0 = cbase; c0 < ldq; c0 += NT * 4) {
-        int q[4][P];
-#pragma unroll
-        for (int z = 0; z < 4; z++) ava::to_planes<P>(c0 == cbase && c0 + z < d ? outv[z] : 0.0f, e, q[z]);
-#pragma unroll
-        for (int p = 0; p < P; p++)
-            *reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq + c0) = ava::pack4(q[0][p], q[1][p], q[2][p], q[3][p]);
-    }
+    float o = xf[(size_t)row * d + c] + acc;
+    if (tb) o = o + acc2;
+    out[(size_t)row * d + c] = o;
 }
 
 // ------------------------------------------------------------------ the learning step
@@ -418,25 +424,57 @@ __global__ __launch_bounds__(1024) void cb_fold_kernel(const double *__restrict_
 }
 
 // tab[b][u] -= s_u delta[b] for the non-zero units u of the kept code, s_u = lr * c_u (divided by
-// the scale in double when it is not 1). Block (b, 64-unit range); threads over the d columns.
+// the scale in double when it is not 1). Block (b, slice of g / TSPLIT units): the slice's code is read
+// 256 units at a time and its non-zero units gathered in LDS (wave ballots), then every thread updates
+// 4 columns of each gathered unit's row (float4; d a multiple of 4, d <= 1024).
+constexpr int TSPLIT = 4;
 __global__ __launch_bounds__(NT) void cb_table_kernel(const float *__restrict__ keep, int g, int d,
                                                       const float *__restrict__ delta, const int32_t *__restrict__ next,
                                                       int V, float lr, const double *__restrict__ scale,
                                                       float *__restrict__ tab) {
-    const int b = blockIdx.x, u0 = blockIdx.y * 64, tid = threadIdx.x;
+    __shared__ int s_u[NT];
+    __shared__ float s_s[NT];
+    __shared__ int s_wc[4];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int y = next[b];
     if (y < 0 || y >= V) return;
     const double sc = scale[b];
     const float *kc = keep + (size_t)b * g;
-    const float *dr = delta + (size_t)b * d;
     float *tb = tab + (size_t)b * g * d;
-    for (int u = u0; u < min(g, u0 + 64); u++) {
-        const float c = kc[u];
-        if (c == 0.0f) continue;
-        float s = lr * c;
-        if (sc != 1.0) s = (float)((double)s / sc);
-        float *tr = tb + (size_t)u * d;
-        for (int i = tid; i < d; i += NT) tr[i] -= s * dr[i];
+    const int per = (g + TSPLIT - 1) / TSPLIT, ub = blockIdx.y * per, ue = min(g, ub + per);
+    const int c4 = tid * 4;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (c4 < d) dv = *reinterpret_cast<const f4 *>(delta + (size_t)b * d + c4);
+    for (int u0 = ub; u0 < ue; u0 += NT) {
+        const int u = u0 + tid;
+        const float c = u < ue ? kc[u] : 0.0f;
+        const uint64_t bm = __ballot(c != 0.0f);
+        __syncthreads();  // the previous chunk's list is consumed
+        if (lane == 0) s_wc[wave] = __popcll(bm);
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < wave; w++) before += s_wc[w];
+        const int total = (s_wc[0] + s_wc[1]) + (s_wc[2] + s_wc[3]);
+        if (c != 0.0f) {
+            const int pos = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0));
+            float s = lr * c;
+            if (sc != 1.0) s = (float)((double)s / sc);
+            s_u[pos] = u;
+            s_s[pos] = s;
+        }
+        __syncthreads();
+        if (c4 < d) {
+#pragma unroll 4
+            for (int q = 0; q < total; q++) {
+                f4 *tr = reinterpret_cast<f4 *>(tb + (size_t)s_u[q] * d + c4);
+                const float s = s_s[q];
+                f4 t = *tr;
+#pragma unroll
+                for (int z = 0; z < 4; z++) t[z] -= s * dv[z];
+                *tr = t;
+            }
+        }
     }
 }
 
@@ -445,10 +483,14 @@ __global__ __launch_bounds__(NT) void cb_table_kernel(const float *__restrict__ 
 namespace ava {
 
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
-            const float *wsgn, int g, int k, int T, float *code, float *keep, hipStream_t st) {
+            const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,
+            int lcap, hipStream_t st) {
     AVA_REQUIRE(d <= 1024 && d % 4 == 0 && g > 0 && g <= 16384 && T > 0, AVA_ERR_SHAPE, "cb_code: d=%d g=%d", d, g);
+    AVA_REQUIRE(!lcnt || (lidx && lval && lcap > 0), AVA_ERR_ARG, "cb_code: unit list without storage");
     const int gpt = (g + NT - 1) / NT;
-#define AVA_CBC(G_) cb_code_kernel<G_><<<n, NT, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep)
+#define AVA_CBC(G_)                                                                                        \
+    cb_code_kernel<G_><<<n, NT, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep, lcnt, lidx, \
+                                         lval, lcap)
     if (gpt <= 2) AVA_CBC(2);
     else if (gpt <= 8) AVA_CBC(8);
     else if (gpt <= 16) AVA_CBC(16);
@@ -460,23 +502,12 @@ int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d,
     return AVA_OK;
 }
 
-int cb_apply(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
-             const double *scale, int T, int planes, int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st) {
-    AVA_REQUIRE(d <= 1024 && d % 4 == 0 && ldq % 4 == 0 && ldq <= 1024 && g <= 16384, AVA_ERR_SHAPE,
-                "cb_apply: d=%d ldq=%d g=%d", d, ldq, g);
-    const size_t lds = (size_t)g * 8;
-    static bool attr[4] = {false, false, false, false};
-#define AVA_CBA(P_)                                                                                          \
-    if (planes == P_) {                                                                                      \
-        if (!attr[P_]) {                                                                                     \
-            AVA_HIP(hipFuncSetAttribute((const void *)cb_apply_kernel<P_>,                                   \
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 8));             \
-            attr[P_] = true;                                                                                 \
-        }                                                                                                    \
-        cb_apply_kernel<P_><<<n, NT, lds, st>>>(xf, code, g, d, w, tab, scale, T, n, xq, xexp, ldq, hout);   \
-    }
-    AVA_CBA(1) else AVA_CBA(2) else AVA_CBA(3) else return fail(AVA_ERR_ARG, "cb_apply: planes %d", planes);
-#undef AVA_CBA
+int cb_apply_list(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
+                  const double *scale, int T, const int *lcnt, const int *lidx, const float *lval, int lcap, float *out,
+                  hipStream_t st) {
+    AVA_REQUIRE(d > 0 && g > 0 && lcnt && lidx && lval && lcap > 0, AVA_ERR_ARG, "cb_apply: d=%d g=%d", d, g);
+    cb_apply_cols_kernel<<<dim3(n, ceil_div(d, NT)), NT, 0, st>>>(xf, code, g, d, w, tab, scale, T, lcnt, lidx, lval,
+                                                                  lcap, out);
     AVA_LAUNCHED("cb_apply");
     return AVA_OK;
 }
@@ -496,7 +527,8 @@ int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, co
     AVA_LAUNCHED("cb_scale");
     cb_fold_kernel<<<B, 1024, 0, st>>>(fold, (size_t)g * d, tab);
     AVA_LAUNCHED("cb_fold");
-    cb_table_kernel<<<dim3(B, ceil_div(g, 64)), NT, 0, st>>>(keep, g, d, delta, next, V, lr, scale, tab);
+    AVA_REQUIRE(d % 4 == 0 && d <= 4 * NT, AVA_ERR_SHAPE, "cb_learn: d=%d (a multiple of 4, <= 1024)", d);
+    cb_table_kernel<<<dim3(B, TSPLIT), NT, 0, st>>>(keep, g, d, delta, next, V, lr, scale, tab);
     AVA_LAUNCHED("cb_table");
     return AVA_OK;
 }

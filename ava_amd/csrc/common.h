@@ -148,15 +148,17 @@ int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, 
 // part, engram_split_floats of scratch) for T <= ENGRAM_SPLIT_T.
 constexpr int ENGRAM_SPLIT_T = 4;
 size_t engram_split_floats(int B, int T, int n0);
-int attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T, float *out,
-           float *part, size_t part_floats, hipStream_t st);
-int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,
-                float *part, size_t part_floats, hipStream_t st);
-// cb.hip: the cerebellum head (code, read-out with the online table to the head's planes, learning)
+int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B, int T,
+           float *out, float *part, size_t part_floats, hipStream_t st);
+int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
+                float *out, float *part, size_t part_floats, hipStream_t st);
+// cb.hip: the cerebellum head (code with its unit lists, read-out with the online table, learning)
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
-            const float *wsgn, int g, int k, int T, float *code, float *keep, hipStream_t st);
-int cb_apply(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
-             const double *scale, int T, int planes, int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st);
+            const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,
+            int lcap, hipStream_t st);
+int cb_apply_list(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
+                  const double *scale, int T, const int *lcnt, const int *lidx, const float *lval, int lcap, float *out,
+                  hipStream_t st);
 int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, const float *emb, int d,
              const float *keep, int g, float lr, double fade, double *scale, float *tab, float *err, float *part,
              int nks, float *delta, double *fold, double *nats, hipStream_t st);

@@ -8,6 +8,8 @@
 // Element-wise arithmetic follows the reference's operation order (gpu/model.rs:458-622,
 // gpu/arch.rs:1873-2020, gpu/model/fstep.rs:207-292); the reductions sum in a tree, not in the
 // reference's sequential order, which moves results by float rounding only.
+#include <hip/hip_fp16.h>
+
 #include <algorithm>
 
 #include "common.h"
@@ -234,13 +236,28 @@ __global__ __launch_bounds__(256) void mem_post_kernel(const float *__restrict__
 
 // ------------------------------------------------------------------ engram read
 
+// The engram store's element: f32 (the reference's store) or fp16 (a KV cache at half the bytes).
+__device__ __forceinline__ float kv_get(const float *p, size_t i) { return p[i]; }
+__device__ __forceinline__ float kv_get(const __half *p, size_t i) { return __half2float(p[i]); }
+__device__ __forceinline__ void kv_put(float *p, size_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void kv_put(__half *p, size_t i, float v) { p[i] = __float2half_rn(v); }
+// Four consecutive elements (16-byte or 8-byte aligned).
+__device__ __forceinline__ f32x4 kv_get4(const float *p, size_t i) { return *reinterpret_cast<const f32x4 *>(p + i); }
+__device__ __forceinline__ f32x4 kv_get4(const __half *p, size_t i) {
+    const uint2 u = *reinterpret_cast<const uint2 *>(p + i);
+    const __half2 a = *reinterpret_cast<const __half2 *>(&u.x), b = *reinterpret_cast<const __half2 *>(&u.y);
+    const float2 fa = __half22float2(a), fb = __half22float2(b);
+    return f32x4{fa.x, fa.y, fb.x, fb.y};
+}
+
 // Causal single-head attention of one stream's T queries against its store: query t (store
 // position n0 + t) reads entries 0..n0 + t with softmax(q.k / sqrt(de)) (gpu/model.rs:543-562,
 // gpu/model/fstep.rs:303-329). de == 64. Block = 64 queries x 256 threads; keys and values in
 // tiles of 64 through LDS; the softmax is the online (running max) form, equal to the reference's
 // two-pass form up to rounding. out [B*T][64].
-__global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q, int ldq, const float *__restrict__ ks,
-                                                     const float *__restrict__ vs, int cap, int n0, int T, float scale,
+template <typename KV>
+__global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q, int ldq, const KV *__restrict__ ks,
+                                                     const KV *__restrict__ vs, int cap, int n0, int T, float scale,
                                                      float *__restrict__ out) {
     __shared__ float sk[64][65];
     __shared__ float sv[64][64];
@@ -248,7 +265,7 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
     const int bi = blockIdx.y, qb = blockIdx.x * 64;
     const int tid = threadIdx.x;
     const int r = tid >> 2, sub = tid & 3;  // query row, quarter (16 keys / 16 output dims)
-    const float *kb = ks + (size_t)bi * cap * 64, *vb = vs + (size_t)bi * cap * 64;
+    const KV *kb = ks + (size_t)bi * cap * 64, *vb = vs + (size_t)bi * cap * 64;
     float qr[64];
     {
         const bool ok = qb + r < T;
@@ -270,8 +287,8 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
         for (int i = tid; i < 64 * 64; i += 256) {
             const int rr = i >> 6, cc = i & 63;
             const bool ok = k0 + rr < kend;
-            sk[rr][cc] = ok ? kb[(size_t)(k0 + rr) * 64 + cc] : 0.0f;
-            sv[rr][cc] = ok ? vb[(size_t)(k0 + rr) * 64 + cc] : 0.0f;
+            sk[rr][cc] = ok ? kv_get(kb, (size_t)(k0 + rr) * 64 + cc) : 0.0f;
+            sv[rr][cc] = ok ? kv_get(vb, (size_t)(k0 + rr) * 64 + cc) : 0.0f;
         }
         __syncthreads();
         float s[16], tmax = -INFINITY;
@@ -339,8 +356,9 @@ __device__ __forceinline__ float row_sum16(float v) {
     return v + dpp_f<0x140>(v);
 }
 
+template <typename KV>
 __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restrict__ q, int ldq,
-                                                           const float *__restrict__ ks, const float *__restrict__ vs,
+                                                           const KV *__restrict__ ks, const KV *__restrict__ vs,
                                                            int cap, int n0, int T, float scale, int nsplit,
                                                            float *__restrict__ part) {
     __shared__ float sm[16], sl[16];
@@ -351,7 +369,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, c4 = (lane & 15) * 4;
     const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q + (size_t)row * ldq + c4);
     const int kb = s * ACH + wave * (ACH / 4), ke = min(kb + ACH / 4, klen);
-    const float *kbase = ks + (size_t)b * cap * 64 + c4, *vbase = vs + (size_t)b * cap * 64 + c4;
+    const KV *kbase = ks + (size_t)b * cap * 64 + c4, *vbase = vs + (size_t)b * cap * 64 + c4;
     float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = kb; k0 < ke; k0 += 32) {
         f32x4 kv[8], vv[8];
@@ -359,8 +377,8 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
         for (int j = 0; j < 8; j++) {
             const int kk = k0 + 4 * j + grp;
             const bool ok = kk < ke;
-            kv[j] = ok ? *reinterpret_cast<const f32x4 *>(kbase + (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            vv[j] = ok ? *reinterpret_cast<const f32x4 *>(vbase + (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            kv[j] = ok ? kv_get4(kbase, (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            vv[j] = ok ? kv_get4(vbase, (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         float sc[8], bm = -INFINITY;
 #pragma unroll
@@ -439,14 +457,15 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
 }
 
 // Append this forward's keys and values to the store: store[b][n0 + t] = kv[b T + t].
+template <typename KV>
 __global__ void store_append_kernel(const float *__restrict__ kv, int ldkv, int T, int B, int cap, int n0,
-                                    float *__restrict__ ks, float *__restrict__ vs) {
+                                    KV *__restrict__ ks, KV *__restrict__ vs) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over B*T*64
     if (i >= B * T * 64) return;
     const int c = i & 63, row = i >> 6, bi = row / T, t = row - bi * T;
     const size_t dst = ((size_t)bi * cap + n0 + t) * 64 + c;
-    ks[dst] = kv[(size_t)row * ldkv + c];
-    vs[dst] = kv[(size_t)row * ldkv + 64 + c];
+    kv_put(ks, dst, kv[(size_t)row * ldkv + c]);
+    kv_put(vs, dst, kv[(size_t)row * ldkv + 64 + c]);
 }
 
 // ------------------------------------------------------------------ dense mix
@@ -569,35 +588,48 @@ size_t engram_split_floats(int B, int T, int n0) {
     return T <= ENGRAM_SPLIT_T ? (size_t)B * T * ceil_div(n0 + T, ACH) * 66 : 0;
 }
 
-int attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T, float *out,
-           float *part, size_t part_floats, hipStream_t st) {
-    AVA_REQUIRE(B > 0 && T > 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
-                "attend: B=%d T=%d, a store of %d entries holds %d + %d", B, T, cap, n0, T);
-    AVA_REQUIRE(ldq >= 64 && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d", ldq);
+template <typename KV>
+int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n0, int B, int T, float *out,
+             float *part, size_t part_floats, hipStream_t st) {
     const float scale = (float)(1.0 / sqrt(64.0));
     if (T <= ENGRAM_SPLIT_T) {
         const int nsplit = ceil_div(n0 + T, ACH);
         AVA_REQUIRE(part && part_floats >= engram_split_floats(B, T, n0), AVA_ERR_ARG,
                     "attend: the decode read needs %zu floats of partials", engram_split_floats(B, T, n0));
-        attend_split_kernel<<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, nsplit, part);
+        attend_split_kernel<KV><<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, nsplit, part);
         AVA_LAUNCHED("attend_split");
         attend_combine_kernel<<<B * T, 64, 0, st>>>(part, nsplit, out);
         AVA_LAUNCHED("attend_combine");
         return AVA_OK;
     }
     dim3 grid(ceil_div(T, 64), B);
-    attend_kernel<<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, out);
+    attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, out);
     AVA_LAUNCHED("attend");
     return AVA_OK;
 }
 
-int engram_read(const float *qkv, int ldqkv, int B, int T, float *ks, float *vs, int cap, int n0, float *out,
-                float *part, size_t part_floats, hipStream_t st) {
+int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B, int T,
+           float *out, float *part, size_t part_floats, hipStream_t st) {
+    AVA_REQUIRE(B > 0 && T > 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
+                "attend: B=%d T=%d, a store of %d entries holds %d + %d", B, T, cap, n0, T);
+    AVA_REQUIRE(ldq >= 64 && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d", ldq);
+    if (kv_half)
+        return attend_t(q, ldq, (const __half *)ks, (const __half *)vs, cap, n0, B, T, out, part, part_floats, st);
+    return attend_t(q, ldq, (const float *)ks, (const float *)vs, cap, n0, B, T, out, part, part_floats, st);
+}
+
+int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
+                float *out, float *part, size_t part_floats, hipStream_t st) {
     AVA_REQUIRE(n0 + T <= cap, AVA_ERR_SHAPE, "engram: store of %d entries holds %d + %d", cap, n0, T);
     const int total = B * T * 64;
-    store_append_kernel<<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, ks, vs);
+    if (kv_half)
+        store_append_kernel<__half><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0,
+                                                                           (__half *)ks, (__half *)vs);
+    else
+        store_append_kernel<float><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0,
+                                                                          (float *)ks, (float *)vs);
     AVA_LAUNCHED("store_append");
-    return attend(qkv, ldqkv, ks, vs, cap, n0, B, T, out, part, part_floats, st);
+    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, B, T, out, part, part_floats, st);
 }
 
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st) {
@@ -619,8 +651,8 @@ int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n,
 
 extern "C" size_t ava_attend_part_floats(int B, int T, int n0) { return ava::engram_split_floats(B, T, n0); }
 
-extern "C" int ava_attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T,
-                          float *out, float *part, size_t part_floats, ava_stream stream) {
+extern "C" int ava_attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B,
+                          int T, float *out, float *part, size_t part_floats, ava_stream stream) {
     AVA_REQUIRE(q && ks && vs && out, AVA_ERR_ARG, "attend: NULL argument");
-    return ava::attend(q, ldq, ks, vs, cap, n0, B, T, out, part, part_floats, (hipStream_t)stream);
+    return ava::attend(q, ldq, ks, vs, kv_half, cap, n0, B, T, out, part, part_floats, (hipStream_t)stream);
 }

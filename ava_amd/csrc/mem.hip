@@ -370,6 +370,103 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
     }
 }
 
+// One token per stream (decode, T == 1): the same recurrence step as mem_fused_kernel, laid out for
+// streaming the state rather than for a long scan. Wave w holds rows 16w..16w+15 of F and S and lane
+// j column j, so each of the lane's 16 + 16 state loads and stores is one 256-byte row per wave
+// (coalesced). Wave 0 stages the step's factors (the same formulas as mem_fused_kernel's staging, the
+// rank-r gate read-outs as fma chains in jj order) while the other waves' state loads are in flight;
+// the column sums r_j and y_j add four per-wave partials in LDS.
+template <bool MOM>
+__global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
+    __shared__ float s_q[HS], s_e[HS], s_v[HS], s_a[HS], s_bk[HS], s_abe[HS];
+    __shared__ float s_part[4][HS], s_lr[2][4][HS];
+    const int bh = blockIdx.x;
+    const int d = p.nh * HS, ldp = 5 * d, ldg = 2 * p.nh + 2 * p.r;
+    const int bi = bh / p.nh, hh = bh - bi * p.nh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t row = (size_t)bi;  // T == 1: stream bi's only row
+    float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
+    const int i0 = wave * 16;
+    float Fr[16], Sr[16];
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+        Fr[m] = Fh[(i0 + m) * HS + lane];
+        Sr[m] = MOM ? Sh[(i0 + m) * HS + lane] : 0.0f;
+    }
+    const int c = hh * HS + lane;
+    const float *Gr = p.G + row * ldg;
+    {
+        // the rank-r gate read-outs, a quarter of the rank per wave (fma chains in jj order)
+        const int q = (p.r + 3) / 4, j0 = wave * q, j1 = min(p.r, j0 + q);
+        float la = 0.0f, lb = 0.0f;
+#pragma unroll 8
+        for (int jj = j0; jj < j1; jj++) {
+            la = fmaf(Gr[2 * p.nh + jj], p.wa2[(size_t)jj * d + c], la);
+            lb = fmaf(Gr[2 * p.nh + p.r + jj], p.wb2[(size_t)jj * d + c], lb);
+        }
+        s_lr[0][wave][lane] = la;
+        s_lr[1][wave][lane] = lb;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float *Pr = p.P + row * ldp;
+        const float rq = Pr[c], rk = Pr[d + c], rv = Pr[2 * d + c], rw = Pr[3 * d + c];
+        const float lra = ((s_lr[0][0][lane] + s_lr[0][1][lane]) + s_lr[0][2][lane]) + s_lr[0][3][lane];
+        const float lrb = ((s_lr[1][0][lane] + s_lr[1][1][lane]) + s_lr[1][2][lane]) + s_lr[1][3][lane];
+        const float ek = rk + rw;
+        const float sq = wsum(rq * rq), sk = wsum(rk * rk), se = wsum(ek * ek);
+        const float qn = rq * rsqrtf(sq + 1e-6f);
+        const float kn = rk * rsqrtf(sk + 1e-6f);
+        const float en = ek * rsqrtf(se + 1e-6f);
+        float v = rv;
+        if (p.v0_out) p.v0_out[row * d + c] = v;
+        if (p.v0) {
+            const float p0 = p.vres ? p.vres[0] * 1.0f + 1.0f : 0.0f, p1 = p.vres ? p.vres[1] : 0.0f;
+            v = v * p0 + p.v0[row * d + c] * p1;
+        }
+        const float a = fsig(((Gr[hh] + p.ba[hh]) + p.off[c]) + lra);
+        const float bw = fsig((Gr[p.nh + hh] + p.bb[hh]) + lrb) * 2.0f;
+        s_q[lane] = qn;
+        s_e[lane] = en;
+        s_v[lane] = v;
+        s_a[lane] = a;
+        s_bk[lane] = bw * kn;
+        s_abe[lane] = (a * bw) * en;
+    }
+    __syncthreads();
+    // r_j = sum_i e_i F_ij
+    float r = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 16; m++) r = fmaf(s_e[i0 + m], Fr[m], r);
+    s_part[wave][lane] = r;
+    __syncthreads();
+    r = ((s_part[0][lane] + s_part[1][lane]) + s_part[2][lane]) + s_part[3][lane];
+    const float vj = s_v[lane], M = p.m, cap = p.cap;
+    float y = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+        const int i = i0 + m;
+        const float u = fmaf(-s_abe[i], r, s_bk[i] * vj);
+        float f;
+        if (MOM) {
+            Sr[m] = fmaf(M, Sr[m], u);
+            f = fmaf(s_a[i], Fr[m], Sr[m]);
+        } else {
+            f = fmaf(s_a[i], Fr[m], u);
+        }
+        f = __builtin_amdgcn_fmed3f(f, -cap, cap);
+        Fr[m] = f;
+        y = fmaf(s_q[i], f, y);
+        Fh[i * HS + lane] = f;
+        if (MOM) Sh[i * HS + lane] = Sr[m];
+    }
+    __syncthreads();  // every wave has read s_part
+    s_part[wave][lane] = y;
+    __syncthreads();
+    if (wave == 0)
+        p.y[row * d + hh * HS + lane] = ((s_part[0][lane] + s_part[1][lane]) + s_part[2][lane]) + s_part[3][lane];
+}
+
 }  // namespace
 
 namespace ava {
@@ -410,6 +507,12 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
     if (pf < 0) {
         const char *e = getenv("AVA_MEM_PF");
         pf = e ? atoi(e) != 0 : 0;
+    }
+    if (T == 1) {
+        if (m != 0.0f) mem_step_kernel<true><<<B * nh, 256, 0, st>>>(a);
+        else mem_step_kernel<false><<<B * nh, 256, 0, st>>>(a);
+        AVA_LAUNCHED("mem_step");
+        return AVA_OK;
     }
     if (m != 0.0f) {
         if (pf) mem_fused_kernel<true, true><<<B * nh, 256, 0, st>>>(a);

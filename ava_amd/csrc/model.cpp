@@ -81,6 +81,9 @@ struct ava_model {
     int cb_k = 0;
     double cb_fade = 1.0;
     float *cb_codes = nullptr;  // scratch [rows][cb_units]
+    int *cb_lcnt = nullptr, *cb_lidx = nullptr;  // the codes' unit lists: [rows], [rows][cb_lcap]
+    float *cb_lval = nullptr;
+    int cb_lcap = 0;
     // the learning step's scratch for up to cb_rows streams
     int cb_rows = 0;
     float *cb_err = nullptr, *cb_part = nullptr, *cb_delta = nullptr;
@@ -297,7 +300,13 @@ int ensure_scratch(ava_model *m, size_t rows) {
         m->streams.resize(c.layers + 1);
         for (auto &s : m->streams) A((void **)&s, rows * d * 4);
     }
-    if (c.cb_units > 0) A((void **)&m->cb_codes, rows * c.cb_units * 4);
+    if (c.cb_units > 0) {
+        A((void **)&m->cb_codes, rows * c.cb_units * 4);
+        m->cb_lcap = std::min(1024, 2 * (c.cb_units / 32));  // room for ties beyond the k kept
+        A((void **)&m->cb_lcnt, rows * 4);
+        A((void **)&m->cb_lidx, rows * m->cb_lcap * 4);
+        A((void **)&m->cb_lval, rows * m->cb_lcap * 4);
+    }
     // the gate product's K-slice partials: the most any row count up to `rows` asks for
     size_t gp = 0;
     for (size_t nn = 128; nn < rows + 128 && nn <= 64 * 128; nn += 128)
@@ -418,8 +427,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         if (b.eng) {
             AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.eng_norm, P, m->xq, m->xexp, ldd, nullptr, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.eqkv.w, ava::Q8_STORE, m->qkv, 3 * de, nullptr, st));
-            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, s->eng_cap, s->eng_len, m->eo,
-                                                   m->att_part, m->att_part_floats, st));
+            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, c.eng_half, s->eng_cap, s->eng_len,
+                                                   m->eo, m->att_part, m->att_part_floats, st));
             AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         }
@@ -438,9 +447,11 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         if (cb) {
             // the cerebellum's correction between the final norm and the head (gpu/model/fstep/arch.rs:1045-1047)
             AVA_RUN("cb_code", ava::cb_code(m->h, ids, m->tok_emb, N, d, c.vocab, m->cb_idx, m->cb_sgn, c.cb_units, m->cb_k,
-                                            T, m->cb_codes, s->cb_code, st));
-            AVA_RUN("cb_apply", ava::cb_apply(m->h, m->cb_codes, N, c.cb_units, d, m->cb_w, s->cb_tab, s->cb_scale, T, P,
-                                              m->xq, m->xexp, ldd, nullptr, st));
+                                            T, m->cb_codes, s->cb_code, m->cb_lcnt, m->cb_lidx, m->cb_lval, m->cb_lcap,
+                                            st));
+            AVA_RUN("cb_apply", ava::cb_apply_list(m->h, m->cb_codes, N, c.cb_units, d, m->cb_w, s->cb_tab, s->cb_scale,
+                                                   T, m->cb_lcnt, m->cb_lidx, m->cb_lval, m->cb_lcap, m->y, st));
+            AVA_RUN("quant_rows", ava::launch_quant_rows(m->y, N, d, d, P, m->xq, m->xexp, st));
         }
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &m->head.w, ava::Q8_STORE, logits, c.vocab, nullptr, st));
     }
@@ -502,7 +513,7 @@ extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logi
     AVA_REQUIRE(c.cb_units > 0 && st->cb_tab && st->cb_scale && st->cb_code, AVA_ERR_ARG,
                 "cb_learn: the model has no cerebellum head or the state no online table");
     AVA_REQUIRE(B > 0 && ld_logits >= c.vocab, AVA_ERR_SHAPE, "cb_learn: B=%d ld=%d", B, ld_logits);
-    const int nks = 8;  // the delta product's K slices (vocab / 8 each)
+    const int nks = 32;  // the delta product's K slices (vocab / 32 each)
     if (B > m->cb_rows) {
         for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
         m->cb_rows = 0;
@@ -512,9 +523,19 @@ extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logi
         AVA_HIP(hipMalloc(&m->cb_fold, (size_t)B * sizeof(double)));
         m->cb_rows = B;
     }
-    return ava::cb_learn(logits, ld_logits, c.vocab, next, B, m->tok_emb, c.d, st->cb_code, c.cb_units, c.cb_lr,
-                         m->cb_fade, st->cb_scale, st->cb_tab, m->cb_err, m->cb_part, nks, m->cb_delta, m->cb_fold, nats,
-                         (hipStream_t)stream);
+    hipStream_t sst = (hipStream_t)stream;
+    if (m->timing && m->last_stream != sst) {
+        if (int e = collect(m)) return e;
+    }
+    m->last_stream = sst;
+    ava_state *as = st;
+    {
+        hipStream_t st = sst;  // the stream AVA_RUN times on
+        AVA_RUN("cb_learn", ava::cb_learn(logits, ld_logits, c.vocab, next, B, m->tok_emb, c.d, as->cb_code, c.cb_units,
+                                          c.cb_lr, m->cb_fade, as->cb_scale, as->cb_tab, m->cb_err, m->cb_part, nks,
+                                          m->cb_delta, m->cb_fold, nats, st));
+    }
+    return AVA_OK;
 }
 
 extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }

@@ -38,7 +38,9 @@ class State:
         self.mem_f = z(L, B, nh, hs, hs)
         self.mem_s = z(L, B, nh, hs, hs)
         cap = max(eng_cap, 1)
-        self.eng_k, self.eng_v = z(B, cap, de), z(B, cap, de)
+        kv = torch.float16 if cfg.get("eng_half") else torch.float32  # the store's element
+        self.eng_k = torch.zeros((B, cap, de), dtype=kv, device=device)
+        self.eng_v = torch.zeros((B, cap, de), dtype=kv, device=device)
         self.eng_cap, self.eng_len = eng_cap, 0
         g = cfg.get("cb_units", 0)
         # the cerebellum's online table (CbOnline, gpu/v51b.rs:340-367): delta, scale 1, last code
@@ -80,7 +82,8 @@ class Model:
                       eng_dim=c["eng_dim"], levels=c["levels"], alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
                       value_residual=int(c["value_residual"]), dense=int(c["dense"]), relu2=int(c["relu2"]),
                       momentum=c["momentum"], cap=c["cap"], planes=planes, cb_units=c.get("cb_units", 0),
-                      cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0))
+                      cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0),
+                      eng_half=int(bool(c.get("eng_half", False))))
         torch.cuda.init()
         h = C.c_void_p()
         check(lib().ava_model_new(C.byref(ccfg), C.byref(prm), C.byref(h)), "ava_model_new")

@@ -180,10 +180,13 @@ def delta_rule_from(q, k, v, beta, la=None, f0=None):
 
 
 def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int) -> torch.Tensor:
-    """model/fstep.rs:303-329 per stream and query: q [B, T, 64]; ks, vs [B, cap, 64] holding entries
-    0..n0+T-1; query t reads entries 0..n0+t. Returns out [B, T, 64]."""
-    for t, nm in ((q, "q"), (ks, "ks"), (vs, "vs")):
-        _need(t, torch.float32, f"attend {nm}")
+    """model/fstep.rs:303-329 per stream and query: q [B, T, 64]; ks, vs [B, cap, 64] (float32 or
+    float16) holding entries 0..n0+T-1; query t reads entries 0..n0+t. Returns out [B, T, 64]."""
+    _need(q, torch.float32, "attend q")
+    for t, nm in ((ks, "ks"), (vs, "vs")):
+        _need(t, ks.dtype, f"attend {nm}")
+    if ks.dtype not in (torch.float32, torch.float16):
+        raise ValueError("attend: the store is float32 or float16")
     B, T, de = q.shape
     cap = ks.shape[1]
     if de != 64 or ks.shape != vs.shape or ks.shape[0] != B or ks.shape[2] != 64:
@@ -191,5 +194,7 @@ def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int) -> torc
     out = torch.empty_like(q)
     n = lib().ava_attend_part_floats(B, T, n0)
     part = torch.empty(max(n, 1), dtype=torch.float32, device=q.device)
-    check(lib().ava_attend(_p(q), 64, _p(ks), _p(vs), cap, n0, B, T, _p(out), _p(part), n, _stream()), "ava_attend")
+    half = int(ks.dtype == torch.float16)
+    check(lib().ava_attend(_p(q), 64, _p(ks), _p(vs), half, cap, n0, B, T, _p(out), _p(part), n, _stream()),
+          "ava_attend")
     return out

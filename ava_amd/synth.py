@@ -45,6 +45,7 @@ def config(name: str) -> dict:
         # (gpu/bin/ava_live.rs:61-64: 12,288 granule units, rate 0.3 / mean |E_v|^2, half-life 256 tokens)
         base.update(vocab=8192, d=1024, layers=8, hidden=4096, kwta_k=1024, eng_block=4)
         base.update(cb_units=12288, cb_eta=0.3, cb_half=256.0)
+        base.update(eng_half=True)  # config[4]: an fp16 KV cache
     else:
         raise ValueError(f"unknown config {name!r}")
     return base

@@ -133,12 +133,13 @@ int ava_delta_chunk(const float *q, const float *k, const float *v, const float 
 /* The engram's causal single-head read (head size 64) over a store that already holds entries
  * 0..n0+T-1 of each stream: query (b, t), row b*T + t of q (ldq floats apart), reads entries
  * 0..n0+t: softmax(q.k / sqrt(64)) . V, the softmax in its online (running max) form. ks, vs
- * [B][cap][64]; out [B*T][64]. For T <= 4 (decode) the keys are cut into chunks of 1024 read by
- * separate workgroups, whose partials need ava_attend_part_floats(B, T, n0) floats of device
- * scratch in part; for T > 4 part may be NULL. Replaces fstep::attend (model/fstep.rs:303-329)
- * and one head of attention_g (model.rs:543-562) / memory::read. */
+ * [B][cap][64] of f32, or of fp16 (IEEE binary16) with kv_half; out [B*T][64]. For T <= 4 (decode)
+ * the keys are cut into chunks of 1024 read by separate workgroups, whose partials need
+ * ava_attend_part_floats(B, T, n0) floats of device scratch in part; for T > 4 part may be NULL.
+ * Replaces fstep::attend (model/fstep.rs:303-329) and one head of attention_g (model.rs:543-562) /
+ * memory::read. */
 size_t ava_attend_part_floats(int B, int T, int n0);
-int ava_attend(const float *q, int ldq, const float *ks, const float *vs, int cap, int n0, int B, int T,
+int ava_attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B, int T,
                float *out, float *part, size_t part_floats, ava_stream stream);
 
 /* ------------------------------------------------------------------ model */
@@ -158,6 +159,9 @@ typedef struct {
      * never fades; gpu/v51b.rs:352-367). */
     int cb_units;
     float cb_lr, cb_half;
+    /* The engram store's element: 0 = f32 (the reference's store), 1 = fp16, a KV cache of half the
+     * bytes (config[4]); the state's eng_k and eng_v then hold IEEE binary16 values. */
+    int eng_half;
 } ava_config;
 
 /* f32 HOST weights, named as the reference's VarMap (arch.rs:806-860). W [din][dout] as applied x·W. */
@@ -183,7 +187,7 @@ typedef struct {
 typedef struct {
     float *lif_v, *lif_s, *lif_a; /* [layers][B][d] */
     float *mem_f, *mem_s;         /* [layers][B][d/hs][hs][hs] */
-    float *eng_k, *eng_v;         /* [B][eng_cap][eng_dim] */
+    float *eng_k, *eng_v;         /* [B][eng_cap][eng_dim] (fp16 elements when the config's eng_half) */
     int eng_cap, eng_len;         /* eng_len advances by T per forward */
     /* The cerebellum's online table per stream (gpu/v51b.rs:340-367, CbOnline): cb_tab
      * [B][cb_units][d] (its `delta`; NULL: no table), cb_scale [B] f64 (its `scale`, 1 at the start),

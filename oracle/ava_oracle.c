@@ -23,6 +23,27 @@
 /* ------------------------------------------------------------------ scalar helpers */
 
 /* candle's sigmoid as gpu/model.rs:465-467 builds it: (exp(-x)·1 + 1)^-1 (gpu/model/fstep.rs:260-262). */
+/* IEEE binary16 round-to-nearest-even of x, returned as the float it stands for: the subnormal range
+ * (below 2^-14) in steps of 2^-24, normals to 10 fraction bits, from 65520 on infinity; NaN stays NaN. */
+float orc_round_half(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint32_t sign = u & 0x80000000u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x7f800000u) return x;
+    if (a < 0x38800000u) {
+        const float y = rintf(fabsf(x) * 16777216.0f) / 16777216.0f; /* exact: |x| 2^24 < 2^10 */
+        return sign ? -y : y;
+    }
+    a += 0xfffu + ((a >> 13) & 1u);
+    a &= ~0x1fffu;
+    if (a >= 0x47800000u) a = 0x7f800000u;
+    a |= sign;
+    float r;
+    memcpy(&r, &a, 4);
+    return r;
+}
+
 float orc_sigmoid(float x) { return 1.0f / (expf(-x) * 1.0f + 1.0f); }
 
 /* gpu/model.rs:618-622 / gpu/model/fstep.rs:265-268: -(relu(-x) + ln(exp(-|x|)·1 + 1)). */
@@ -548,6 +569,11 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
                     size_t dst = ((size_t)bi * st->eng_cap + n0 + t) * de;
                     memcpy(st->eng_k + dst, ekk + ((size_t)bi * T + t) * de, sizeof(float) * de);
                     memcpy(st->eng_v + dst, evv + ((size_t)bi * T + t) * de, sizeof(float) * de);
+                    if (cfg->eng_half)
+                        for (int c = 0; c < de; c++) {
+                            st->eng_k[dst + c] = orc_round_half(st->eng_k[dst + c]);
+                            st->eng_v[dst + c] = orc_round_half(st->eng_v[dst + c]);
+                        }
                 }
             float scale = (float)(1.0 / sqrt((double)de));
             for (int bi = 0; bi < B; bi++)

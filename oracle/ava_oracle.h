@@ -125,6 +125,7 @@ typedef struct {
     int levels;      /* spike levels each side (2 = int2) */
     int alif, lif_scale, value_residual, dense, relu2;
     float momentum, cap;
+    int eng_half;    /* the engram store keeps keys and values at fp16 precision (config[4]'s KV cache) */
 } orc_cfg;
 
 typedef struct {
@@ -173,7 +174,8 @@ void orc_cb_apply(const float *xf, const float *c, int g, int d, const float *w,
 double orc_cb_learn(const float *logits, int V, int next, const float *E, int d, const float *c, int g, float lr,
                     double half, double *scale, float *tab);
 
-/* The same building blocks exposed for tests. */
+/* The same building blocks exposed for tests. orc_round_half: IEEE binary16 round-to-nearest-even. */
+float orc_round_half(float x);
 void orc_rmsnorm(const float *x, int n, int d, const float *gain, float *out);
 float orc_sigmoid(float x);
 float orc_log_sigmoid(float x);

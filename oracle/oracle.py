@@ -46,6 +46,8 @@ def lib():
         L.orc_mem_rec.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_float, C.c_float, f32p, C.c_void_p, f32p]
         L.orc_mem_rec_f64.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_double, f64p, C.c_void_p, f64p]
         L.orc_rmsnorm.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p]
+        L.orc_round_half.argtypes = [C.c_float]
+        L.orc_round_half.restype = C.c_float
         L.orc_sigmoid.argtypes = [C.c_float]
         L.orc_sigmoid.restype = C.c_float
         L.orc_log_sigmoid.argtypes = [C.c_float]
@@ -138,6 +140,12 @@ def lif_scan(cur, ps, v0=None, s0=None, a0=None, levels=2, signed=True, alif=Tru
     spk = np.empty((B, T, D), np.int8)
     lib().orc_lif_scan(cur, B, T, D, _c(ps, np.float32), v, s, a, levels, int(signed), int(alif), spk)
     return spk, v, s, a
+
+
+def round_half(x):
+    """IEEE binary16 round-to-nearest-even of each element (the oracle's orc_round_half), as float32."""
+    f = np.vectorize(lambda v: lib().orc_round_half(float(v)), otypes=[np.float32])
+    return f(np.asarray(x, np.float32))
 
 
 def lif_params(block, alif=True):
@@ -270,7 +278,7 @@ class _Cfg(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab", "d", "layers", "hidden", "kwta_k", "heads", "head_size",
                                        "gate_rank", "eng_block", "eng_dim", "levels", "alif", "lif_scale",
                                        "value_residual", "dense", "relu2")] + \
-               [("momentum", C.c_float), ("cap", C.c_float)]
+               [("momentum", C.c_float), ("cap", C.c_float), ("eng_half", C.c_int)]
 
 
 class _Model(C.Structure):
@@ -320,7 +328,8 @@ class OracleModel:
                          eng_block=c["eng_block"], eng_dim=c["eng_dim"], levels=c["levels"],
                          alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
                          value_residual=int(c["value_residual"]), dense=int(c["dense"]),
-                         relu2=int(c["relu2"]), momentum=c["momentum"], cap=c["cap"])
+                         relu2=int(c["relu2"]), momentum=c["momentum"], cap=c["cap"],
+                         eng_half=int(c.get("eng_half", 0) or 0))
         self.head_q, self.head_s = self.q8[id(head_w)]
         # the cerebellum head (gpu/v51b.rs:18-32, 282-293): wiring from the fixed seed, the read-out W
         # (cbh.wo, zero at init: None), the online rate and half-life

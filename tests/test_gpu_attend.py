@@ -24,14 +24,17 @@ def attend_f64(q, ks, vs, n0):
     return out
 
 
+@pytest.mark.parametrize("kv", [np.float32, np.float16])
 @pytest.mark.parametrize("B,T,n0,cap", [(3, 1, 0, 8), (3, 1, 1023, 1100), (2, 1, 1024, 1100), (4, 1, 5000, 6000),
                                         (2, 3, 2047, 2100), (2, 4, 3100, 3200), (2, 70, 1500, 1600),
                                         (1, 200, 0, 200)])
-def test_attend_matches_f64(B, T, n0, cap):
-    print(f"attend B={B} T={T} n0={n0} cap={cap}", flush=True)
+def test_attend_matches_f64(B, T, n0, cap, kv):
+    """f32 store, and the fp16 store (config[4]'s KV cache): the f64 statement reads the same fp16
+    values, so the bar is the same."""
+    print(f"attend B={B} T={T} n0={n0} cap={cap} kv={kv.__name__}", flush=True)
     rng = np.random.default_rng(B * 7 + T + n0)
-    ks = rng.standard_normal((B, cap, 64)).astype(np.float32)
-    vs = rng.standard_normal((B, cap, 64)).astype(np.float32)
+    ks = rng.standard_normal((B, cap, 64)).astype(kv)
+    vs = rng.standard_normal((B, cap, 64)).astype(kv)
     q = (rng.standard_normal((B, T, 64)) * 2.0).astype(np.float32)
     want = attend_f64(q, ks, vs, n0)
     got = ops.attend(torch.from_numpy(q).cuda(), torch.from_numpy(ks).cuda(), torch.from_numpy(vs).cuda(), n0)

@@ -24,10 +24,11 @@ def rel(a, b):
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
 
 
-def run_both(name, B, T, seed, layers=None, pieces=None, threads=8, prefix=None):
+def run_both(name, B, T, seed, layers=None, pieces=None, threads=8, prefix=None, **over):
     """The oracle's and the GPU's forward of seeded ids [B, T] (with prefix: only its first `prefix`
-    tokens)."""
+    tokens); `over` overrides config entries."""
     cfg = synth.config(name)
+    cfg.update(over)
     if layers:
         cfg["layers"] = layers
         cfg["eng_block"] = min(cfg["eng_block"], layers - 1)
@@ -114,6 +115,21 @@ def test_tiny_stack_matches_oracle(B, T):
     assert rel(lg, lo) < 1e-3
     check_state(so, st)
     assert st.eng_len == T
+
+
+def test_fp16_engram_store_decode_matches_oracle():
+    """The fp16 engram store (config[4]'s KV cache) through a prefill and single-token steps: the oracle
+    rounds the stored keys and values to binary16 (round-to-nearest-even) the same way."""
+    cfg, lo, so, lg, st = run_both("tiny", 2, 40, seed=6, pieces=[(0, 30), (30, 31), (31, 32), (32, 40)],
+                                   eng_half=True)
+    assert st.eng_k.dtype == torch.float16
+    assert np.max(np.abs(lg - lo)) < 1e-2
+    check_state(so, st)
+    # the stored values: one binary16 step of the value (f32-level differences of the projections can
+    # straddle a rounding tie), or 1e-5 of the store's scale for values near zero, where a step is finer
+    for name in ("eng_k", "eng_v"):
+        g, o = host(getattr(st, name)).astype(np.float32), so[name]
+        assert np.all(np.abs(g - o) <= np.abs(o) * 2.0 ** -10 + 1e-5 * np.max(np.abs(o))), name
 
 
 def test_stack_in_pieces_matches_one_pass():

@@ -390,3 +390,20 @@ def test_model_planes_near_the_reference_products():
     ref, _, _ = mdl.forward(ids, planes=0)
     p3, _, _ = mdl.forward(ids, planes=3)
     assert np.max(np.abs(ref - p3)) < 1e-3 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_round_half_is_ieee_binary16():
+    """orc_round_half against numpy's float32 -> float16 conversion (IEEE round-to-nearest-even):
+    random values over the whole half range, ties, the subnormal range, overflow and specials."""
+    rng = np.random.default_rng(12)
+    x = np.concatenate([
+        (rng.standard_normal(20000) * 10.0 ** rng.integers(-8, 5, 20000)).astype(np.float32),
+        np.float32(1.0) + np.arange(-64, 64, dtype=np.float32) * np.float32(2.0 ** -11),  # ties at 1.0
+        (np.arange(0, 3000, dtype=np.float32) * np.float32(2.0 ** -25)),  # subnormals and their ties
+        np.array([65504.0, 65519.9, 65520.0, 70000.0, -65520.0, 6.1e-5, 6.2e-5, 0.0, -0.0, np.inf, -np.inf],
+                 np.float32),
+    ])
+    got = O.round_half(x)
+    want = x.astype(np.float16).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isnan(O.round_half(np.array([np.nan], np.float32)))[0]
