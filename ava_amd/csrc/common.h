@@ -138,10 +138,8 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
 int embed(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, hipStream_t st);
 int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
                float *hout, hipStream_t st);
-// G = h . W in f32; with few rows the K dimension is split over part (gate_part_floats of scratch).
-size_t gate_part_floats(int n, int d, int nc);
-int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, float *part, size_t part_floats,
-              hipStream_t st);
+// G = h . W in f32 (fp32 MFMA tiles; few rows: a VALU kernel over 4 rows per workgroup).
+int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st);
 int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, int8_t *xq, int32_t *xexp, int ldq,
              hipStream_t st);
 // The engram read: the tiled causal form for T > ENGRAM_SPLIT_T, the chunk-split decode form (with

@@ -125,22 +125,17 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
 // (h tile row-major, W tile row-major, both padded), each step 16 MFMA k-substeps per column block.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int GR = 128, GK = 32;
-// With few rows the K dimension is split: block (x, y) sums K range [y kslice, (y + 1) kslice) into
-// g + y n nc (partials, added in slice order by gate_sum_kernel).
 template <int NCB>  // column blocks of 32
 __global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict__ h, int n, int d,
-                                                        const float *__restrict__ w, int nc, int kslice,
-                                                        float *__restrict__ g) {
+                                                        const float *__restrict__ w, int nc, float *__restrict__ g) {
     __shared__ float sh[GR][GK + 1];
     __shared__ float sw[GK][NCB * 32 + 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * GR;
-    const int kb = blockIdx.y * kslice, ke = min(d, kb + kslice);
-    g += (size_t)blockIdx.y * n * nc;
     f32x16 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[cb] = f32x16{};
-    for (int k0 = kb; k0 < ke; k0 += GK) {
+    for (int k0 = 0; k0 < d; k0 += GK) {
         // h tile: 128 rows x 32 floats, 8 threads per row, float4 each
         for (int i = tid; i < GR * GK / 4; i += 256) {
             const int rr = i >> 3, kk = (i & 7) * 4;
@@ -241,14 +236,6 @@ __device__ __forceinline__ float kv_get(const float *p, size_t i) { return p[i];
 __device__ __forceinline__ float kv_get(const __half *p, size_t i) { return __half2float(p[i]); }
 __device__ __forceinline__ void kv_put(float *p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void kv_put(__half *p, size_t i, float v) { p[i] = __float2half_rn(v); }
-// Four consecutive elements (16-byte or 8-byte aligned).
-__device__ __forceinline__ f32x4 kv_get4(const float *p, size_t i) { return *reinterpret_cast<const f32x4 *>(p + i); }
-__device__ __forceinline__ f32x4 kv_get4(const __half *p, size_t i) {
-    const uint2 u = *reinterpret_cast<const uint2 *>(p + i);
-    const __half2 a = *reinterpret_cast<const __half2 *>(&u.x), b = *reinterpret_cast<const __half2 *>(&u.y);
-    const float2 fa = __half22float2(a), fb = __half22float2(b);
-    return f32x4{fa.x, fa.y, fb.x, fb.y};
-}
 
 // Causal single-head attention of one stream's T queries against its store: query t (store
 // position n0 + t) reads entries 0..n0 + t with softmax(q.k / sqrt(de)) (gpu/model.rs:543-562,
@@ -335,10 +322,9 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
 
 // The decode form of the same read (flash-decoding), for a few queries per stream: query row
 // (b, t) at store position n0 + t reads keys 0..n0 + t. Its keys are cut into chunks of ACH; workgroup
-// (s, row) reads chunk s, each wave a quarter of it, 32 keys per iteration: lane l holds dims
-// 4 (l & 15)..+3 of the query, and lane group l >> 4 takes keys 4 j + (l >> 4) (a wave reads 4 whole
-// 256-byte rows per load, coalesced). The 16 lanes of a group add their partial dot products by DPP;
-// each group keeps its own running max, sum and 4 output dims. The 16 groups of a workgroup merge in
+// (s, row) reads chunk s, each wave a quarter of it, 32 keys per iteration, 16 bytes per lane per
+// load (attend_split_kernel's lane layout); the lanes of a key add their partial dot products by DPP,
+// each lane group keeps its own running max, sum and output dims, and a workgroup's groups merge in
 // LDS into one partial (max, sum, o[64]) per (row, chunk): part [row][nsplit][66]; attend_combine
 // merges the chunks.
 constexpr int ACH = 1024;
@@ -356,39 +342,84 @@ __device__ __forceinline__ float row_sum16(float v) {
     return v + dpp_f<0x140>(v);
 }
 
+// The sum over each group of 8 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror), in every lane.
+__device__ __forceinline__ float row_sum8(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0x141>(v);
+}
+
+// 16-byte loads of the store: DPL elements per lane (4 f32 or 8 fp16), widened to f32.
+template <typename KV>
+struct KvLane;
+template <>
+struct KvLane<float> {
+    static constexpr int DPL = 4;
+    static __device__ __forceinline__ void load(const float *p, float (&x)[4]) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
+#pragma unroll
+        for (int z = 0; z < 4; z++) x[z] = v[z];
+    }
+};
+template <>
+struct KvLane<__half> {
+    static constexpr int DPL = 8;
+    static __device__ __forceinline__ void load(const __half *p, float (&x)[8]) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int z = 0; z < 4; z++) {
+            const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[z]));
+            x[2 * z] = f.x;
+            x[2 * z + 1] = f.y;
+        }
+    }
+};
+
+// Lane layout: a key's 64 dims are read by LPK = 64 / DPL lanes (16 for f32, 8 for fp16), so a wave
+// holds G = 64 / LPK key groups and reads G whole keys per 16-byte load instruction; each group takes
+// U = 32 / G keys of a 32-key iteration (keys G j + group).
 template <typename KV>
 __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restrict__ q, int ldq,
                                                            const KV *__restrict__ ks, const KV *__restrict__ vs,
                                                            int cap, int n0, int T, float scale, int nsplit,
                                                            float *__restrict__ part) {
-    __shared__ float sm[16], sl[16];
-    __shared__ float so[16][64];
+    constexpr int DPL = KvLane<KV>::DPL, LPK = 64 / DPL, G = 64 / LPK, U = 32 / G, NG = 4 * G;
+    __shared__ float sm[NG], sl[NG];
+    __shared__ float so[NG][64];
     const int s = blockIdx.x, row = blockIdx.y;
     const int b = row / T, t = row - b * T;
     const int klen = n0 + t + 1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, c4 = (lane & 15) * 4;
-    const f32x4 q4 = *reinterpret_cast<const f32x4 *>(q + (size_t)row * ldq + c4);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane / LPK, cl = (lane % LPK) * DPL;
+    float qv[DPL];
+#pragma unroll
+    for (int z = 0; z < DPL; z++) qv[z] = q[(size_t)row * ldq + cl + z];
     const int kb = s * ACH + wave * (ACH / 4), ke = min(kb + ACH / 4, klen);
-    const KV *kbase = ks + (size_t)b * cap * 64 + c4, *vbase = vs + (size_t)b * cap * 64 + c4;
-    float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const KV *kbase = ks + (size_t)b * cap * 64 + cl, *vbase = vs + (size_t)b * cap * 64 + cl;
+    float m = -INFINITY, l = 0.0f, o[DPL];
+#pragma unroll
+    for (int z = 0; z < DPL; z++) o[z] = 0.0f;
     for (int k0 = kb; k0 < ke; k0 += 32) {
-        f32x4 kv[8], vv[8];
+        float kv[U][DPL], vv[U][DPL];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int kk = k0 + 4 * j + grp;
-            const bool ok = kk < ke;
-            kv[j] = ok ? kv_get4(kbase, (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            vv[j] = ok ? kv_get4(vbase, (size_t)kk * 64) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < U; j++) {
+            const int kk = k0 + G * j + grp;
+            if (kk < ke) {
+                KvLane<KV>::load(kbase + (size_t)kk * 64, kv[j]);
+                KvLane<KV>::load(vbase + (size_t)kk * 64, vv[j]);
+            } else {
+#pragma unroll
+                for (int z = 0; z < DPL; z++) kv[j][z] = vv[j][z] = 0.0f;
+            }
         }
-        float sc[8], bm = -INFINITY;
+        float sc[U], bm = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            float a = kv[j][0] * q4[0];
-            a = fmaf(kv[j][1], q4[1], a);
-            a = fmaf(kv[j][2], q4[2], a);
-            a = fmaf(kv[j][3], q4[3], a);
-            a = row_sum16(a) * scale;
-            sc[j] = (k0 + 4 * j + grp < ke) ? a : -INFINITY;
+        for (int j = 0; j < U; j++) {
+            float a = kv[j][0] * qv[0];
+#pragma unroll
+            for (int z = 1; z < DPL; z++) a = fmaf(kv[j][z], qv[z], a);
+            a = (LPK == 16 ? row_sum16(a) : row_sum8(a)) * scale;
+            sc[j] = (k0 + G * j + grp < ke) ? a : -INFINITY;
             bm = fmaxf(bm, sc[j]);
         }
         const float nm = fmaxf(m, bm);
@@ -396,33 +427,33 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
         const float corr = expf(m - nm);  // m = -inf: 0
         l *= corr;
 #pragma unroll
-        for (int z = 0; z < 4; z++) o[z] *= corr;
+        for (int z = 0; z < DPL; z++) o[z] *= corr;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < U; j++) {
             const float p = expf(sc[j] - nm);  // -inf: 0
             l += p;
 #pragma unroll
-            for (int z = 0; z < 4; z++) o[z] = fmaf(p, vv[j][z], o[z]);
+            for (int z = 0; z < DPL; z++) o[z] = fmaf(p, vv[j][z], o[z]);
         }
         m = nm;
     }
-    const int gi = wave * 4 + grp;
-    if ((lane & 15) == 0) {
+    const int gi = wave * G + grp;
+    if (lane % LPK == 0) {
         sm[gi] = m;
         sl[gi] = l;
     }
 #pragma unroll
-    for (int z = 0; z < 4; z++) so[gi][c4 + z] = o[z];
+    for (int z = 0; z < DPL; z++) so[gi][cl + z] = o[z];
     __syncthreads();
     if (threadIdx.x < 64) {
         const int c = threadIdx.x;
         float M = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; i++) M = fmaxf(M, sm[i]);
+        for (int i = 0; i < NG; i++) M = fmaxf(M, sm[i]);
         float L = 0.0f, O = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
+            for (int i = 0; i < NG; i++) {
                 const float w = sm[i] == -INFINITY ? 0.0f : expf(sm[i] - M);
                 L = fmaf(sl[i], w, L);
                 O = fmaf(so[i][c], w, O);
@@ -527,49 +558,59 @@ int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8
     return AVA_OK;
 }
 
-// K slices of the gate product for n rows: enough workgroups for the chip when the row blocks are
-// few (decode), slices of at least 64.
-static int gate_slices(int n, int d) {
-    const int blocks = ceil_div(n, GR);
-    if (blocks >= 64) return 1;
-    return std::max(1, std::min(d / 64, ceil_div(128, blocks)));
+// Few rows (decode): 4 rows per workgroup on the VALU, 1024 threads. Thread t takes column t % 128
+// over the K eighth t / 128, with the rows' inputs staged in LDS and 32 weight loads in flight (an L2
+// round trip is ~0.5 us, so the loop is load-latency bound); the eighths add in order at the end.
+constexpr int GRR = 4, GKS = 8;
+__global__ __launch_bounds__(1024) void gate_rows_kernel(const float *__restrict__ h, int n, int d,
+                                                         const float *__restrict__ w, int nc, float *__restrict__ g) {
+    __shared__ float sh[GRR][1024];
+    __shared__ float sacc[GKS][GRR][128];
+    const int tid = threadIdx.x, c = tid & 127, ks = tid >> 7, r0 = blockIdx.x * GRR;
+    for (int i = tid; i < GRR * d; i += 1024) {
+        const int r = i / d, k = i - r * d;
+        sh[r][k] = r0 + r < n ? h[(size_t)(r0 + r) * d + k] : 0.0f;
+    }
+    __syncthreads();
+    float acc[GRR] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < nc) {
+        const int kb = ks * (d / GKS), ke = kb + d / GKS;
+#pragma unroll 32
+        for (int k = kb; k < ke; k++) {
+            const float wv = w[(size_t)k * nc + c];
+#pragma unroll
+            for (int r = 0; r < GRR; r++) acc[r] = fmaf(sh[r][k], wv, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GRR; r++) sacc[ks][r][c] = acc[r];
+    __syncthreads();
+    if (tid < GRR * 128) {
+        const int r = tid >> 7;
+        if (c < nc && r0 + r < n) {
+            float v = sacc[0][r][c];
+#pragma unroll
+            for (int q = 1; q < GKS; q++) v += sacc[q][r][c];
+            g[(size_t)(r0 + r) * nc + c] = v;
+        }
+    }
 }
 
-size_t gate_part_floats(int n, int d, int nc) {
-    const int s = gate_slices(n, d);
-    return s > 1 ? (size_t)s * n * nc : 0;
-}
-
-__global__ void gate_sum_kernel(const float *__restrict__ part, int ns, size_t total, float *__restrict__ g) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    float v = part[i];
-    for (int s = 1; s < ns; s++) v += part[(size_t)s * total + i];
-    g[i] = v;
-}
-
-int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, float *part, size_t part_floats,
-              hipStream_t st) {
+int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st) {
     AVA_REQUIRE(nc > 0 && nc <= 128 && d % GK == 0, AVA_ERR_SHAPE, "gate_gemm: %d columns (<= 128), d=%d", nc, d);
     const int blocks = ceil_div(n, GR);
-    int ns = gate_slices(n, d);
-    if (ns > 1 && (!part || part_floats < gate_part_floats(n, d, nc))) ns = 1;  // no scratch: one pass
-    const int kslice = ceil_div(ceil_div(d, ns), GK) * GK;
-    ns = ceil_div(d, kslice);
-    float *out = ns > 1 ? part : g;
-    const dim3 grid(blocks, ns);
+    if (blocks < 64 && d <= 1024 && d % GKS == 0) {
+        gate_rows_kernel<<<ceil_div(n, GRR), 1024, 0, st>>>(h, n, d, w, nc, g);
+        AVA_LAUNCHED("gate_gemm");
+        return AVA_OK;
+    }
     switch ((nc + 31) / 32) {
-    case 1: gate_mfma_kernel<1><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
-    case 2: gate_mfma_kernel<2><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
-    case 3: gate_mfma_kernel<3><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
-    default: gate_mfma_kernel<4><<<grid, 256, 0, st>>>(h, n, d, w, nc, kslice, out); break;
+    case 1: gate_mfma_kernel<1><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    case 2: gate_mfma_kernel<2><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    case 3: gate_mfma_kernel<3><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
+    default: gate_mfma_kernel<4><<<blocks, 256, 0, st>>>(h, n, d, w, nc, g); break;
     }
     AVA_LAUNCHED("gate_gemm");
-    if (ns > 1) {
-        const size_t total = (size_t)n * nc;
-        gate_sum_kernel<<<ceil_div((long)total, 256), 256, 0, st>>>(part, ns, total, g);
-        AVA_LAUNCHED("gate_sum");
-    }
     return AVA_OK;
 }
 

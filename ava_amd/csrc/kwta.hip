@@ -30,6 +30,18 @@ __device__ __forceinline__ float float_of_key(uint32_t k) {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+__device__ __forceinline__ float uni(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
+
+// z with P(N(0,1) >= z) = p, 0 < p < 1, to about 1e-3 (a search guess only): the rational
+// approximation of Abramowitz and Stegun 26.2.23 on the smaller tail.
+__device__ __forceinline__ float normal_upper_quantile(float p) {
+    const float q = p < 0.5f ? p : 1.0f - p;
+    const float w = sqrtf(-2.0f * __logf(fmaxf(q, 1e-30f)));
+    const float z = w - (2.515517f + w * (0.802853f + w * 0.010328f)) /
+                            (1.0f + w * (1.432788f + w * (0.189269f + w * 0.001308f)));
+    return p < 0.5f ? z : -z;
+}
+
 // NV float4 chunks per lane: h <= 256 NV. OUT: 0 = f32 a, P>0 = P int8 planes + row exponent.
 template <int NV, int P, bool FULL>
 __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, int n, int h, int k, int relu2,
@@ -106,6 +118,42 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
             if (chi >= k) {  // the maximum is the k-th largest (ties at the top)
                 kth = hi;
                 done = true;
+            }
+            // Two first guesses from the row's mean and deviation as if it were normal: the quantile
+            // of the kept fraction, then one Newton step on the count with the normal density. They
+            // only place the bracket (any guess gives the same exact answer); on wide-layer rows they
+            // land within a few per cent of k, so the interpolation below needs a few counts more.
+            if (!done) {
+                float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NV; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const bool real = full || i * 64 + lane < nq;
+                        s1 += real ? x[i][j] : 0.0f;
+                        s2 += real ? x[i][j] * x[i][j] : 0.0f;
+                    }
+                s1 = ava::wave_sum(s1);
+                s2 = ava::wave_sum(s2);
+                const float mu = s1 / (float)h, sd = sqrtf(fmaxf(s2 / (float)h - mu * mu, 0.0f));
+                const float z = normal_upper_quantile((float)k / (float)h);
+                const float dens = (float)h * 0.39894228f * __expf(-0.5f * z * z) / fmaxf(sd, 1e-30f);
+                float t = uni(mu + z * sd);
+                for (int g = 0; g < 2 && !found; g++) {
+                    if (!(t > lo && t < hi)) break;
+                    const int c = count_ge(t);
+                    if (c == k) {
+                        tk = t;
+                        found = true;
+                    } else if (c > k) {
+                        lo = t;
+                        clo = c;
+                    } else {
+                        hi = t;
+                        chi = c;
+                    }
+                    t = uni(t + (float)(c - k) / dens);
+                }
             }
             for (int it = 0; it < 24 && !done && !found; it++) {
                 // interpolation on even steps, midpoint on odd ones (guards slow one-sided convergence)

@@ -387,11 +387,12 @@ __global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
     const size_t row = (size_t)bi;  // T == 1: stream bi's only row
     float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
     const int i0 = wave * 16;
+    // the state is streamed once each way: non-temporal loads and stores
     float Fr[16], Sr[16];
 #pragma unroll
     for (int m = 0; m < 16; m++) {
-        Fr[m] = Fh[(i0 + m) * HS + lane];
-        Sr[m] = MOM ? Sh[(i0 + m) * HS + lane] : 0.0f;
+        Fr[m] = __builtin_nontemporal_load(Fh + (i0 + m) * HS + lane);
+        Sr[m] = MOM ? __builtin_nontemporal_load(Sh + (i0 + m) * HS + lane) : 0.0f;
     }
     const int c = hh * HS + lane;
     const float *Gr = p.G + row * ldg;
@@ -457,8 +458,8 @@ __global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
         f = __builtin_amdgcn_fmed3f(f, -cap, cap);
         Fr[m] = f;
         y = fmaf(s_q[i], f, y);
-        Fh[i * HS + lane] = f;
-        if (MOM) Sh[i * HS + lane] = Sr[m];
+        __builtin_nontemporal_store(f, Fh + i * HS + lane);
+        if (MOM) __builtin_nontemporal_store(Sr[m], Sh + i * HS + lane);
     }
     __syncthreads();  // every wave has read s_part
     s_part[wave][lane] = y;

@@ -88,9 +88,6 @@ struct ava_model {
     int cb_rows = 0;
     float *cb_err = nullptr, *cb_part = nullptr, *cb_delta = nullptr;
     double *cb_fold = nullptr;
-    // the gate product's K-slice partials for few rows
-    float *gate_part = nullptr;
-    size_t gate_part_floats = 0;
     // the decode engram read's chunk partials (grow-only)
     float *att_part = nullptr;
     size_t att_part_floats = 0;
@@ -307,16 +304,6 @@ int ensure_scratch(ava_model *m, size_t rows) {
         A((void **)&m->cb_lidx, rows * m->cb_lcap * 4);
         A((void **)&m->cb_lval, rows * m->cb_lcap * 4);
     }
-    // the gate product's K-slice partials: the most any row count up to `rows` asks for
-    size_t gp = 0;
-    for (size_t nn = 128; nn < rows + 128 && nn <= 64 * 128; nn += 128)
-        gp = std::max(gp, ava::gate_part_floats((int)std::min(nn, rows), (int)d, (int)nc));
-    m->gate_part = nullptr;
-    m->gate_part_floats = 0;
-    if (gp) {
-        A((void **)&m->gate_part, gp * 4);
-        if (!e) m->gate_part_floats = gp;
-    }
     if (e) return e;
     m->rows = rows;
     return AVA_OK;
@@ -413,8 +400,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         // the fast-weight memory
         AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
-        AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, m->gate_part,
-                                            m->gate_part_floats, st));
+        AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, st));
         const bool vr = c.value_residual != 0;
         const size_t sm = (size_t)i * B * nh * 64 * 64;
         AVA_RUN("mem_scan", ava::mem_block(m->P, m->G, B, T, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,

@@ -20,6 +20,8 @@
 
 #include <type_traits>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -530,22 +532,55 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void q8_gemm_dma_kernel(const i
     epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
+// Products of at most this many rows take the few-rows kernel; AVA_Q8_SMALL_ROWS overrides it (tuning).
+int small_rows() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_Q8_SMALL_ROWS");
+        v = e ? atoi(e) : 512;
+        if (v < 0) v = 0;
+    }
+    return v;
+}
+
+// Few-rows products of at least this many columns take 64-column blocks; AVA_Q8_WIDE_COLS overrides it.
+int small_wide_cols() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_Q8_WIDE_COLS");
+        v = e ? atoi(e) : 4096;
+        if (v < 0) v = 0;
+    }
+    return v;
+}
+
 // ------------------------------------------------------------------ the product for few rows
 //
 // Decode shapes (m <= 512 rows) leave the tiled kernels with a few dozen workgroups. Here a workgroup
-// owns a 32 x 32 output block and all of K; its 4 waves take the 128-byte K steps kt = w, w + 4, ...
-// each on its own: a wave stages its step (P planes x 32 rows and 32 weight columns, 128 bytes each)
-// in its own double-buffered LDS with direct-to-LDS loads and waits for its own loads only, so the K
-// loop has no barrier. At the end wave w forms its exact plane combination A_w = sum_p acc_p
-// 2^(7(P-1-p)) in double (an integer below 2^47); the four are added in LDS (still exact) and rounded
-// once as the tiled kernels' epilogue does: the same bits as they give, for any m.
-template <int P, int EPI>
+// owns a 32 x BN output block (BN = 32 FN) and all of K; its 4 waves take the 64-byte K steps
+// kt = w, w + 4, ... each on its own: a wave stages its step (P planes x 32 rows and BN weight columns,
+// 64 bytes each) in its own double-buffered LDS with direct-to-LDS loads and waits for its own loads
+// only, so the K loop has no barrier (80 KB or less per workgroup: two fit a CU). At the end wave w
+// forms its exact plane combination A_w = sum_p acc_p 2^(7(P-1-p)) in double (an integer below 2^47);
+// the four are added in LDS (still exact) and rounded once as the tiled kernels' epilogue does: the
+// same bits as they give, for any m.
+template <int P, int FN>
+struct SmallCfg {
+    static constexpr int BM = 32, BN = 32 * FN, BK = 64, CPR = 4, RPI = 16;  // a 1 KB load = 16 rows
+    static constexpr int ROWS = P * BM + BN, LPS = ROWS / RPI, BUF = ROWS * BK;
+    static constexpr size_t OPS = (size_t)8 * BUF;                            // 4 waves x 2 buffers
+    static constexpr size_t ACC = (size_t)4 * P * FN * 16 * 64 * 4;          // int32 planes, EPI_ACC
+    static constexpr size_t DBL = (size_t)4 * FN * 16 * 64 * 8;              // doubles, other epilogues
+};
+
+template <int P, int EPI, int FN>
 __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
                                                        int m, int n, int ldk, const int8_t *__restrict__ qt,
                                                        const float *__restrict__ scale, EpiArgs ep) {
-    constexpr int BM = 32, BN = 32, BK = 128, CPR = 8, RPI = 8;  // a 1 KB load covers 8 rows of 128 bytes
-    constexpr int ROWS = P * BM + BN, LPS = ROWS / RPI, BUF = ROWS * BK;
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];  // 4 waves x 2 buffers of BUF bytes
+    using C = SmallCfg<P, FN>;
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, CPR = C::CPR, RPI = C::RPI, LPS = C::LPS, BUF = C::BUF;
+    static_assert(C::ROWS % RPI == 0, "rows per load");
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
     int mt, nt;
     tile_origin(tiles_m, tiles_n, tiles_m, mt, nt);  // a weight block's row blocks on one XCD
@@ -572,9 +607,11 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
         for (int i = 0; i < LPS; i++) dma16(src[i] + kt * BK, wbuf + b * BUF + i * 1024);
     };
 
-    i32x16 acc[P];
+    i32x16 acc[P][FN];
 #pragma unroll
-    for (int p = 0; p < P; p++) acc[p] = i32x16{};
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[p][j] = i32x16{};
     const int KT = ldk / BK, frow = lane & 31, fc = lane >> 5;
     int b = 0;
     if (wave < KT) issue(wave, 0);
@@ -588,12 +625,18 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
         const int8_t *la = wbuf + b * BUF, *lb = la + P * BM * BK;
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ks++) {
-            const int c = swz<CPR>(frow, ks * 2 + fc) * 16;
-            const i32x4 bf = *reinterpret_cast<const i32x4 *>(lb + frow * BK + c);
+            i32x4 bf[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int r = j * 32 + frow;
+                bf[j] = *reinterpret_cast<const i32x4 *>(lb + r * BK + swz<CPR>(r, ks * 2 + fc) * 16);
+            }
 #pragma unroll
             for (int p = 0; p < P; p++) {
-                const i32x4 af = *reinterpret_cast<const i32x4 *>(la + (p * BM + frow) * BK + c);
-                acc[p] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, acc[p], 0, 0, 0);
+                const i32x4 af =
+                    *reinterpret_cast<const i32x4 *>(la + (p * BM + frow) * BK + swz<CPR>(frow, ks * 2 + fc) * 16);
+#pragma unroll
+                for (int j = 0; j < FN; j++) acc[p][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[p][j], 0, 0, 0);
             }
         }
         // the buffer is refilled two steps on: its fragment reads must have completed
@@ -604,70 +647,91 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
     }
     __syncthreads();  // every wave is done with its buffers
 
-    const int rsub = (lane >> 5) * 4, col = n0 + (lane & 31);
+    const int rsub = (lane >> 5) * 4;
     if (EPI == EPI_ACC) {
-        int *si = reinterpret_cast<int *>(smem);  // [wave][p][16][64]
+        int *si = reinterpret_cast<int *>(smem);  // [wave][p][j][16][64]
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) si[((wave * P + p) * 16 + r) * 64 + lane] = acc[p][r];
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) si[(((wave * P + p) * FN + j) * 16 + r) * 64 + lane] = acc[p][j][r];
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
-            if (row < m && col < n)
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + j * 32 + (lane & 31);
 #pragma unroll
-                for (int p = 0; p < P; p++) {
-                    int v = 0;
+            for (int q = 0; q < 4; q++) {
+                const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+                if (row < m && col < n)
 #pragma unroll
-                    for (int w = 0; w < 4; w++) v += si[((w * P + p) * 16 + r) * 64 + lane];
-                    reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = v;
-                }
+                    for (int p = 0; p < P; p++) {
+                        int v = 0;
+#pragma unroll
+                        for (int w = 0; w < 4; w++) v += si[(((w * P + p) * FN + j) * 16 + r) * 64 + lane];
+                        reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = v;
+                    }
+            }
         }
         return;
     }
-    double *sd = reinterpret_cast<double *>(smem);  // [wave][16][64]
+    double *sd = reinterpret_cast<double *>(smem);  // [wave][j][16][64]
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        double A = (double)acc[0][r];
+    for (int j = 0; j < FN; j++)
 #pragma unroll
-        for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][r]);
-        sd[(wave * 16 + r) * 64 + lane] = A;
-    }
+        for (int r = 0; r < 16; r++) {
+            double A = (double)acc[0][j][r];
+#pragma unroll
+            for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][j][r]);
+            sd[((wave * FN + j) * 16 + r) * 64 + lane] = A;
+        }
     __syncthreads();
-    if (col >= n) return;
-    const float sc = scale[col];
-    const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
     float *ybase = reinterpret_cast<float *>(ep.y);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
-        if (row >= m) continue;
-        const double A = ((sd[r * 64 + lane] + sd[(16 + r) * 64 + lane]) + sd[(32 + r) * 64 + lane]) +
-                         sd[(48 + r) * 64 + lane];
-        const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
-        float v = ldexpf((float)A, ex) * sc;
-        if (EPI == EPI_MUL) v = v * cv;
-        float *yp = ybase + (size_t)row * ep.ldy + col;
-        if (EPI == EPI_ADD) v = *yp + v;
-        *yp = v;
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + j * 32 + (lane & 31);
+        if (col >= n) continue;
+        const float sc = scale[col];
+        const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+            if (row >= m) continue;
+            const int e = (j * 16 + r) * 64 + lane, ws = FN * 16 * 64;
+            const double A = ((sd[e] + sd[ws + e]) + sd[2 * ws + e]) + sd[3 * ws + e];
+            const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
+            float v = ldexpf((float)A, ex) * sc;
+            if (EPI == EPI_MUL) v = v * cv;
+            float *yp = ybase + (size_t)row * ep.ldy + col;
+            if (EPI == EPI_ADD) v = *yp + v;
+            *yp = v;
+        }
     }
 }
 
+template <int P, int EPI, int FN>
+int launch_small_fn(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt,
+                    const float *scale, EpiArgs ep, hipStream_t st) {
+    using C = SmallCfg<P, FN>;
+    const int total = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
+    const size_t lds = std::max(C::OPS, EPI == EPI_ACC ? C::ACC : C::DBL);
+    static bool attr = false;
+    if (!attr) {
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI, FN>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    q8_small_kernel<P, EPI, FN><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+    AVA_LAUNCHED("q8_gemm");
+    return AVA_OK;
+}
+
+// 64-column blocks for wide products (half the activation re-reads), 32 otherwise (enough blocks).
 template <int P, int EPI>
 int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                  EpiArgs ep, hipStream_t st) {
-    const int total = ((m + 31) / 32) * ((n + 31) / 32);
-    const size_t lds = (size_t)8 * (P * 32 + 32) * 128;
-    static bool attr = false;
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds));
-        attr = true;
-    }
-    q8_small_kernel<P, EPI><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
-    AVA_LAUNCHED("q8_gemm");
-    return AVA_OK;
+    if (n >= small_wide_cols()) return launch_small_fn<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    return launch_small_fn<P, EPI, 1>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 // ------------------------------------------------------------------ the product, deep-ring form
@@ -989,16 +1053,7 @@ int tile_override() {
     return v;
 }
 
-// Products of at most this many rows take the few-rows kernel; AVA_Q8_SMALL_ROWS overrides it (tuning).
-int small_rows() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_Q8_SMALL_ROWS");
-        v = e ? atoi(e) : 512;
-        if (v < 0) v = 0;
-    }
-    return v;
-}
+
 
 // Row blocks per tile group (tile_origin); AVA_Q8_GROUP overrides it (tuning).
 int tile_group() {
