@@ -289,17 +289,31 @@ __global__ __launch_bounds__(NT) void cb_apply_cols_kernel(const float *__restri
     const float *cr = code + (size_t)row * g;
     float acc = 0.0f, acc2 = 0.0f;
     if (listed) {
+        // rows in batches of 16 whose loads are all issued before the adds (in unit order) use them
+        constexpr int QB = 16;
         if (w) {
-#pragma unroll 8
-            for (int q = 0; q < cnt; q++) acc += w[(size_t)s_j[q] * d + c] * s_c[q];
+            for (int q0 = 0; q0 < cnt; q0 += QB) {
+                float v[QB];
+#pragma unroll
+                for (int z = 0; z < QB; z++) v[z] = w[(size_t)s_j[min(q0 + z, cnt - 1)] * d + c];
+                AVA_ISSUE_FENCE();
+#pragma unroll
+                for (int z = 0; z < QB; z++)
+                    if (q0 + z < cnt) acc += v[z] * s_c[q0 + z];
+            }
         }
         if (tb) {
-            if (sc == 1.0) {
-#pragma unroll 8
-                for (int q = 0; q < cnt; q++) acc2 += s_c[q] * tb[(size_t)s_j[q] * d];
-            } else {
-#pragma unroll 8
-                for (int q = 0; q < cnt; q++) acc2 += (float)((double)s_c[q] * sc) * tb[(size_t)s_j[q] * d];
+            for (int q0 = 0; q0 < cnt; q0 += QB) {
+                float v[QB];
+#pragma unroll
+                for (int z = 0; z < QB; z++) v[z] = tb[(size_t)s_j[min(q0 + z, cnt - 1)] * d];
+                AVA_ISSUE_FENCE();
+#pragma unroll
+                for (int z = 0; z < QB; z++)
+                    if (q0 + z < cnt) {
+                        const float x = sc == 1.0 ? s_c[q0 + z] : (float)((double)s_c[q0 + z] * sc);
+                        acc2 += x * v[z];
+                    }
             }
         }
     } else {

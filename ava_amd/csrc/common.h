@@ -29,6 +29,11 @@ __device__ inline void store_f32(BufRes, unsigned, unsigned, float) {}
 __device__ inline float load_f32(BufRes, unsigned, unsigned) { return 0.0f; }
 #endif
 
+// A compiler-only barrier: memory operations are not moved across it. Placed after a batch of
+// independent loads it keeps the scheduler from spreading them between their uses, so the whole
+// batch is in flight at once (each use still waits only for its own load).
+#define AVA_ISSUE_FENCE() asm volatile("" ::: "memory")
+
 namespace ava {
 
 // Per-thread last error (ava_last_error).

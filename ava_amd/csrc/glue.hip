@@ -574,12 +574,16 @@ __global__ __launch_bounds__(1024) void gate_rows_kernel(const float *__restrict
     __syncthreads();
     float acc[GRR] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (c < nc) {
-        const int kb = ks * (d / GKS), ke = kb + d / GKS;
-#pragma unroll 32
-        for (int k = kb; k < ke; k++) {
-            const float wv = w[(size_t)k * nc + c];
+        const int kb = ks * (d / GKS), ke = kb + d / GKS;  // (ke - kb) % 32 == 0 (launcher)
+        for (int k0 = kb; k0 < ke; k0 += 32) {
+            float wv[32];  // the 32 loads are issued before any is used
 #pragma unroll
-            for (int r = 0; r < GRR; r++) acc[r] = fmaf(sh[r][k], wv, acc[r]);
+            for (int j = 0; j < 32; j++) wv[j] = w[(size_t)(k0 + j) * nc + c];
+            AVA_ISSUE_FENCE();
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+#pragma unroll
+                for (int r = 0; r < GRR; r++) acc[r] = fmaf(sh[r][k0 + j], wv[j], acc[r]);
         }
     }
 #pragma unroll
@@ -599,7 +603,7 @@ __global__ __launch_bounds__(1024) void gate_rows_kernel(const float *__restrict
 int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st) {
     AVA_REQUIRE(nc > 0 && nc <= 128 && d % GK == 0, AVA_ERR_SHAPE, "gate_gemm: %d columns (<= 128), d=%d", nc, d);
     const int blocks = ceil_div(n, GR);
-    if (blocks < 64 && d <= 1024 && d % GKS == 0) {
+    if (blocks < 64 && d <= 1024 && d % (GKS * 32) == 0) {
         gate_rows_kernel<<<ceil_div(n, GRR), 1024, 0, st>>>(h, n, d, w, nc, g);
         AVA_LAUNCHED("gate_gemm");
         return AVA_OK;
