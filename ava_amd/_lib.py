@@ -47,7 +47,7 @@ class Params(C.Structure):
 class State(C.Structure):
     _fields_ = [("lif_v", vp), ("lif_s", vp), ("lif_a", vp), ("mem_f", vp), ("mem_s", vp),
                 ("eng_k", vp), ("eng_v", vp), ("eng_cap", i32), ("eng_len", i32),
-                ("cb_tab", vp), ("cb_scale", vp), ("cb_code", vp)]
+                ("cb_tab", vp), ("cb_scale", vp), ("cb_code", vp), ("eng_len_dev", vp)]
 
 
 _lib = None
@@ -93,6 +93,9 @@ def lib():
     if hasattr(L, "ava_model_free"):
         L.ava_model_free.argtypes = [vp]
         L.ava_model_free.restype = None
+    if hasattr(L, "ava_model_freeze"):
+        L.ava_model_freeze.argtypes = [vp, i32]
+        L.ava_model_freeze.restype = i32
     if hasattr(L, "ava_model_scratch_bytes"):
         L.ava_model_scratch_bytes.argtypes = [vp]
         L.ava_model_scratch_bytes.restype = sz

@@ -151,10 +151,11 @@ int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, 
 // part, engram_split_floats of scratch) for T <= ENGRAM_SPLIT_T.
 constexpr int ENGRAM_SPLIT_T = 4;
 size_t engram_split_floats(int B, int T, int n0);
-int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B, int T,
-           float *out, float *part, size_t part_floats, hipStream_t st);
+int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, const int *n0p,
+           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st);
 int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
-                float *out, float *part, size_t part_floats, hipStream_t st);
+                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st);
+int engram_advance(int *n0p, int T, int cap, hipStream_t st);
 // cb.hip: the cerebellum head (code with its unit lists, read-out with the online table, learning)
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
             const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,

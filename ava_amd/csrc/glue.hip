@@ -244,8 +244,9 @@ __device__ __forceinline__ void kv_put(__half *p, size_t i, float v) { p[i] = __
 // two-pass form up to rounding. out [B*T][64].
 template <typename KV>
 __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q, int ldq, const KV *__restrict__ ks,
-                                                     const KV *__restrict__ vs, int cap, int n0, int T, float scale,
-                                                     float *__restrict__ out) {
+                                                     const KV *__restrict__ vs, int cap, int n0, const int *n0p,
+                                                     int T, float scale, float *__restrict__ out) {
+    if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device (a replayed graph)
     __shared__ float sk[64][65];
     __shared__ float sv[64][64];
     __shared__ float sp[64][65];
@@ -382,8 +383,9 @@ struct KvLane<__half> {
 template <typename KV>
 __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restrict__ q, int ldq,
                                                            const KV *__restrict__ ks, const KV *__restrict__ vs,
-                                                           int cap, int n0, int T, float scale, int nsplit,
-                                                           float *__restrict__ part) {
+                                                           int cap, int n0, const int *n0p, int T, float scale,
+                                                           int nsplit, float *__restrict__ part) {
+    if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device: chunks past it are empty
     constexpr int DPL = KvLane<KV>::DPL, LPK = 64 / DPL, G = 64 / LPK, U = 32 / G, NG = 4 * G;
     __shared__ float sm[NG], sl[NG];
     __shared__ float so[NG][64];
@@ -487,12 +489,20 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
     out[(size_t)row * 64 + c] = O / L;
 }
 
-// Append this forward's keys and values to the store: store[b][n0 + t] = kv[b T + t].
+// The device store length advances by T after a forward, saturating at the store's capacity (the
+// host refuses forwards that would not fit; a replayed graph cannot ask, so this keeps it in bounds).
+__global__ void store_advance_kernel(int *n0p, int T, int cap) {
+    if (threadIdx.x == 0) *n0p = min(*n0p + T, cap);
+}
+
+// Append this forward's keys and values to the store: store[b][n0 + t] = kv[b T + t] (n0 from the
+// device when n0p).
 template <typename KV>
 __global__ void store_append_kernel(const float *__restrict__ kv, int ldkv, int T, int B, int cap, int n0,
-                                    KV *__restrict__ ks, KV *__restrict__ vs) {
+                                    const int *n0p, KV *__restrict__ ks, KV *__restrict__ vs) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over B*T*64
     if (i >= B * T * 64) return;
+    if (n0p) n0 = min(*n0p, cap - T);
     const int c = i & 63, row = i >> 6, bi = row / T, t = row - bi * T;
     const size_t dst = ((size_t)bi * cap + n0 + t) * 64 + c;
     kv_put(ks, dst, kv[(size_t)row * ldkv + c]);
@@ -633,48 +643,59 @@ size_t engram_split_floats(int B, int T, int n0) {
     return T <= ENGRAM_SPLIT_T ? (size_t)B * T * ceil_div(n0 + T, ACH) * 66 : 0;
 }
 
+// With n0p (the store length on the device) the chunk grid covers the whole store, so a captured
+// launch serves every length; chunks past the length are empty and merge as nothing.
 template <typename KV>
-int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n0, int B, int T, float *out,
-             float *part, size_t part_floats, hipStream_t st) {
+int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n0, const int *n0p, int B, int T,
+             float *out, float *part, size_t part_floats, hipStream_t st) {
     const float scale = (float)(1.0 / sqrt(64.0));
     if (T <= ENGRAM_SPLIT_T) {
-        const int nsplit = ceil_div(n0 + T, ACH);
-        AVA_REQUIRE(part && part_floats >= engram_split_floats(B, T, n0), AVA_ERR_ARG,
-                    "attend: the decode read needs %zu floats of partials", engram_split_floats(B, T, n0));
-        attend_split_kernel<KV><<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, nsplit, part);
+        const int span = n0p ? cap - T : n0;
+        const int nsplit = ceil_div(span + T, ACH);
+        AVA_REQUIRE(part && part_floats >= engram_split_floats(B, T, span), AVA_ERR_ARG,
+                    "attend: the decode read needs %zu floats of partials", engram_split_floats(B, T, span));
+        attend_split_kernel<KV><<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, nsplit,
+                                                                     part);
         AVA_LAUNCHED("attend_split");
         attend_combine_kernel<<<B * T, 64, 0, st>>>(part, nsplit, out);
         AVA_LAUNCHED("attend_combine");
         return AVA_OK;
     }
     dim3 grid(ceil_div(T, 64), B);
-    attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, T, scale, out);
+    attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
     AVA_LAUNCHED("attend");
     return AVA_OK;
 }
 
-int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B, int T,
-           float *out, float *part, size_t part_floats, hipStream_t st) {
+int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, const int *n0p,
+           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st) {
     AVA_REQUIRE(B > 0 && T > 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
                 "attend: B=%d T=%d, a store of %d entries holds %d + %d", B, T, cap, n0, T);
     AVA_REQUIRE(ldq >= 64 && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d", ldq);
     if (kv_half)
-        return attend_t(q, ldq, (const __half *)ks, (const __half *)vs, cap, n0, B, T, out, part, part_floats, st);
-    return attend_t(q, ldq, (const float *)ks, (const float *)vs, cap, n0, B, T, out, part, part_floats, st);
+        return attend_t(q, ldq, (const __half *)ks, (const __half *)vs, cap, n0, n0p, B, T, out, part, part_floats,
+                        st);
+    return attend_t(q, ldq, (const float *)ks, (const float *)vs, cap, n0, n0p, B, T, out, part, part_floats, st);
 }
 
 int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
-                float *out, float *part, size_t part_floats, hipStream_t st) {
+                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st) {
     AVA_REQUIRE(n0 + T <= cap, AVA_ERR_SHAPE, "engram: store of %d entries holds %d + %d", cap, n0, T);
     const int total = B * T * 64;
     if (kv_half)
-        store_append_kernel<__half><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0,
+        store_append_kernel<__half><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, n0p,
                                                                            (__half *)ks, (__half *)vs);
     else
-        store_append_kernel<float><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0,
+        store_append_kernel<float><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, n0p,
                                                                           (float *)ks, (float *)vs);
     AVA_LAUNCHED("store_append");
-    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, B, T, out, part, part_floats, st);
+    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, n0p, B, T, out, part, part_floats, st);
+}
+
+int engram_advance(int *n0p, int T, int cap, hipStream_t st) {
+    store_advance_kernel<<<1, 64, 0, st>>>(n0p, T, cap);
+    AVA_LAUNCHED("store_advance");
+    return AVA_OK;
 }
 
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st) {
@@ -699,5 +720,5 @@ extern "C" size_t ava_attend_part_floats(int B, int T, int n0) { return ava::eng
 extern "C" int ava_attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B,
                           int T, float *out, float *part, size_t part_floats, ava_stream stream) {
     AVA_REQUIRE(q && ks && vs && out, AVA_ERR_ARG, "attend: NULL argument");
-    return ava::attend(q, ldq, ks, vs, kv_half, cap, n0, B, T, out, part, part_floats, (hipStream_t)stream);
+    return ava::attend(q, ldq, ks, vs, kv_half, cap, n0, nullptr, B, T, out, part, part_floats, (hipStream_t)stream);
 }

@@ -91,6 +91,8 @@ struct ava_model {
     // the decode engram read's chunk partials (grow-only)
     float *att_part = nullptr;
     size_t att_part_floats = 0;
+    // set while captured graphs hold the scratch's addresses: nothing is freed or reallocated
+    bool frozen = false;
 
     bool timing = false;
     Timer timer;
@@ -266,6 +268,8 @@ int build(ava_model *m, const ava_params *prm) {
 
 int ensure_scratch(ava_model *m, size_t rows) {
     if (rows <= m->rows) return AVA_OK;
+    AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "forward: %zu rows need more scratch, and the model's scratch is frozen "
+                "(a captured graph uses it)", rows);
     for (void *p : m->scratch) (void)hipFree(p);
     m->scratch.clear();
     m->streams.clear();
@@ -374,6 +378,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         // sized for the fullest store this state can reach, so a decode loop allocates once
         const size_t need = ava::engram_split_floats(B, T, s->eng_cap - T);
         if (need > m->att_part_floats) {
+            AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "forward: the engram read needs more scratch, and the model's "
+                        "scratch is frozen (a captured graph uses it)");
             (void)hipFree(m->att_part);
             m->att_part = nullptr;
             m->att_part_floats = 0;
@@ -414,7 +420,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.eng_norm, P, m->xq, m->xexp, ldd, nullptr, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.eqkv.w, ava::Q8_STORE, m->qkv, 3 * de, nullptr, st));
             AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, c.eng_half, s->eng_cap, s->eng_len,
-                                                   m->eo, m->att_part, m->att_part_floats, st));
+                                                   s->eng_len_dev, m->eo, m->att_part, m->att_part_floats, st));
             AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         }
@@ -426,7 +432,10 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         if (c.dense)
             AVA_RUN("dense_mix", ava::dense_mix(m->x, m->streams.data(), b.dense.data(), i + 2, (size_t)N * d, st));
     }
-    if (c.eng_block >= 0) s->eng_len += T;
+    if (c.eng_block >= 0) {
+        s->eng_len += T;
+        if (s->eng_len_dev) AVA_RUN("store_advance", ava::engram_advance(s->eng_len_dev, T, s->eng_cap, st));
+    }
     if (logits) {
         const bool cb = c.cb_units > 0 && s->cb_code;
         AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, cb ? m->h : nullptr, st));
@@ -501,6 +510,8 @@ extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logi
     AVA_REQUIRE(B > 0 && ld_logits >= c.vocab, AVA_ERR_SHAPE, "cb_learn: B=%d ld=%d", B, ld_logits);
     const int nks = 32;  // the delta product's K slices (vocab / 32 each)
     if (B > m->cb_rows) {
+        AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "cb_learn: %d streams need more scratch, and the model's scratch is "
+                    "frozen (a captured graph uses it)", B);
         for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
         m->cb_rows = 0;
         AVA_HIP(hipMalloc(&m->cb_err, (size_t)B * c.vocab * sizeof(float)));
@@ -525,6 +536,12 @@ extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logi
 }
 
 extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }
+
+extern "C" int ava_model_freeze(ava_model *m, int on) {
+    AVA_REQUIRE(m, AVA_ERR_ARG, "freeze: NULL model");
+    m->frozen = on != 0;
+    return AVA_OK;
+}
 
 extern "C" int ava_model_set_timing(ava_model *m, int on) {
     AVA_REQUIRE(m, AVA_ERR_ARG, "set_timing: NULL model");

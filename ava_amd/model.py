@@ -27,9 +27,10 @@ def _ptr(a, keep):
 
 
 class State:
-    """The carried state of B streams (state.rs:94-116), device tensors."""
+    """The carried state of B streams (state.rs:94-116), device tensors. device_len keeps the store
+    length on the device too (needed to replay a captured decode step, DecodeGraph)."""
 
-    def __init__(self, cfg: dict, B: int, eng_cap: int = 0, device="cuda"):
+    def __init__(self, cfg: dict, B: int, eng_cap: int = 0, device="cuda", device_len: bool = False):
         L, d, hs, de = cfg["layers"], cfg["d"], cfg["head_size"], cfg["eng_dim"]
         nh = d // hs
         z = lambda *s: torch.zeros(s, dtype=torch.float32, device=device)
@@ -47,13 +48,14 @@ class State:
         self.cb_tab = z(B, g, d) if g else None
         self.cb_scale = torch.ones(B, dtype=torch.float64, device=device) if g else None
         self.cb_code = z(B, g) if g else None
+        self.eng_len_dev = torch.zeros(1, dtype=torch.int32, device=device) if device_len else None
 
     def c(self):
         p = lambda t: t.data_ptr() if t is not None else None
         return _CState(lif_v=p(self.lif_v), lif_s=p(self.lif_s), lif_a=p(self.lif_a), mem_f=p(self.mem_f),
                        mem_s=p(self.mem_s), eng_k=p(self.eng_k), eng_v=p(self.eng_v), eng_cap=self.eng_cap,
                        eng_len=self.eng_len, cb_tab=p(self.cb_tab), cb_scale=p(self.cb_scale),
-                       cb_code=p(self.cb_code))
+                       cb_code=p(self.cb_code), eng_len_dev=p(self.eng_len_dev))
 
 
 class Model:
@@ -94,8 +96,26 @@ class Model:
             lib().ava_model_free(self.h)
             self.h = None
 
-    def state(self, B: int, eng_cap: int = 0) -> State:
-        return State(self.cfg, B, eng_cap)
+    def state(self, B: int, eng_cap: int = 0, device_len: bool = False) -> State:
+        return State(self.cfg, B, eng_cap, device_len=device_len)
+
+    def capture_decode(self, st: State, ids: torch.Tensor, logits: torch.Tensor, nxt: torch.Tensor | None = None,
+                       nats: torch.Tensor | None = None) -> "DecodeGraph":
+        """One decode step (the forward of ids [B, T] into logits, then, with nxt, the online table's
+        step) captured as a HIP graph over fixed buffers: fill ids (and nxt) in place, then replay().
+        The state needs device_len; call the step eagerly once before capturing (scratch is allocated
+        on first use, and a capture must not allocate)."""
+        if st.eng_len_dev is None:
+            raise ValueError("capture_decode: the state needs device_len=True")
+        check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")  # the graph keeps the scratch's addresses
+        g = torch.cuda.CUDAGraph()
+        n0 = st.eng_len
+        with torch.cuda.graph(g):
+            self.forward_with_state(ids, st, logits)
+            if nxt is not None:
+                self.cb_learn(logits, nxt, st, nats=nats)
+        st.eng_len = n0  # the capture ran nothing: the store did not advance
+        return DecodeGraph(g, st, ids.shape[1])
 
     def forward_with_state(self, ids: torch.Tensor, st: State, logits: torch.Tensor | None = None, want_logits=True):
         if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
@@ -154,3 +174,18 @@ class Model:
 
     def scratch_bytes(self) -> int:
         return lib().ava_model_scratch_bytes(self.h)
+
+
+class DecodeGraph:
+    """A captured decode step (Model.capture_decode). replay() runs it once on the current stream and
+    advances the host's store length as the captured forward advances the device's."""
+
+    def __init__(self, graph, st: State, T: int):
+        self.graph, self.st, self.T = graph, st, T
+
+    def replay(self):
+        st = self.st
+        if st.eng_cap and st.eng_len + self.T > st.eng_cap:
+            raise ValueError(f"decode graph: the engram store holds {st.eng_len} of {st.eng_cap} entries")
+        self.graph.replay()
+        st.eng_len += self.T

@@ -418,13 +418,18 @@ class Decode:
         log("bench: building weights")
         self.params = synth.params(c, seed=0)
         self.model = Model(c, self.params, planes=planes)
-        self.st = self.model.state(B, eng_cap=prefill + steps_cap)
+        self.st = self.model.state(B, eng_cap=prefill + steps_cap, device_len=True)
         g = torch.Generator(device="cuda").manual_seed(5)
         V = c["vocab"]
         self.toks = torch.randint(0, V, (steps_cap + 1, B, 1), device="cuda", generator=g, dtype=torch.int32)
         self.nexts = self.toks[1:, :, 0].contiguous()
         self.logits = torch.empty((B, V), device="cuda")
         self.nats = torch.empty(B, dtype=torch.float64, device="cuda")
+        # the step's inputs live in fixed buffers so that it can be captured once and replayed
+        self.ids_buf = torch.empty((B, 1), dtype=torch.int32, device="cuda")
+        self.nxt_buf = torch.empty(B, dtype=torch.int32, device="cuda")
+        self.use_graph = os.environ.get("AVA_DECODE_GRAPH", "1") != "0"
+        self.graph = None
         self.t = 0
         self.steps_cap = steps_cap
         t0 = time.perf_counter()
@@ -442,7 +447,8 @@ class Decode:
         self.config = {"workload": "stateful decode config[4]", "streams": B, "prefill": prefill, "d": d,
                        "blocks": L, "hidden": H, "kwta_k": c["kwta_k"], "heads": nh, "vocab": V,
                        "engram_block": c["eng_block"], "engram_store": "f32", "cb_units": c["cb_units"],
-                       "cb_half": c["cb_half"], "momentum": c["momentum"], "act_planes": planes}
+                       "cb_half": c["cb_half"], "momentum": c["momentum"], "act_planes": planes,
+                       "hip_graph": self.use_graph}
         self.dtype = "i8"
         self.breakdown = None
 
@@ -463,11 +469,19 @@ class Decode:
         out = B * V * 4 * 2 + V * d * 4
         return w + lif + fs + kv + cb + out
 
-    def step(self, stream, ev=None):
+    def step(self, stream, ev=None, eager=False):
         if self.t >= self.steps_cap:
             raise RuntimeError("decode: more steps than the store was sized for")
-        self.model.forward_with_state(self.toks[self.t], self.st, self.logits)
-        self.model.cb_learn(self.logits, self.nexts[self.t], self.st, nats=self.nats)
+        self.ids_buf.copy_(self.toks[self.t])
+        self.nxt_buf.copy_(self.nexts[self.t])
+        if self.graph is not None and not eager:
+            self.graph.replay()
+        else:
+            self.model.forward_with_state(self.ids_buf, self.st, self.logits)
+            self.model.cb_learn(self.logits, self.nxt_buf, self.st, nats=self.nats)
+            if self.use_graph and self.graph is None:
+                # captured after the first eager step (scratch allocated): every later step replays it
+                self.graph = self.model.capture_decode(self.st, self.ids_buf, self.logits, self.nxt_buf, self.nats)
         self.t += 1
 
     prof_steps = 8
@@ -483,7 +497,7 @@ class Decode:
         self.model.timing(reset=True)
         self.model.set_timing(True)
         for _ in range(self.prof_steps):
-            self.step(None)
+            self.step(None, eager=True)
         torch.cuda.synchronize()
         t = self.model.timing(reset=True)
         self.model.set_timing(False)

@@ -196,6 +196,11 @@ typedef struct {
     float *cb_tab;
     double *cb_scale;
     float *cb_code;
+    /* Optional (NULL: unused): the store length on the device, one int32 kept equal to eng_len. With
+     * it the engram kernels read the length from the device and each forward advances it there, so a
+     * forward captured in a HIP graph stays correct on replay (the host's eng_len only advances on
+     * real calls; the caller keeps replays within eng_cap, and the device length saturates there). */
+    int32_t *eng_len_dev;
 } ava_state;
 
 typedef struct ava_model ava_model;
@@ -222,6 +227,11 @@ int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logits, int ld_
 
 /* Bytes of scratch the model holds after forwards of up to B*T rows. */
 size_t ava_model_scratch_bytes(const ava_model *m);
+
+/* While frozen (on != 0) the model never frees or reallocates its scratch: a forward or learning
+ * step that would need more fails with AVA_ERR_ARG instead. For callers that capture forwards in HIP
+ * graphs, which keep the scratch's addresses (no reference counterpart: the reference has no graphs). */
+int ava_model_freeze(ava_model *m, int on);
 
 /* Launch timing by kernel class (the counterpart of int8::set_mm_prof, int8.rs:628-669): with `on`,
  * every launch of ava_model_forward is bracketed by HIP events on its stream. ava_model_timing
