@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = "tokens/sec int8 block-stack forward @B=64,T=2048, 1 GPU; % HBM / MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 I8_PEAK_TOPS = 5000.0  # dense int8 MFMA, TOP/s
+F32_MFMA_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 FP32_PEAK_TFLOPS = 157.3
 
 
@@ -250,8 +251,14 @@ class Delta:
         if ev: ev[1].record()
 
     def roofline(self, kernel_s):
-        a = self.bytes / kernel_s / 1e9
-        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS}
+        # fp32-MFMA bound: the chunked form's work, 6 hs^2 + (5 c - 1) hs FLOPs per token and head
+        # (c = 64), against the dense fp32 MFMA peak; the HBM rate of the same launch beside it
+        hs, c = 64, 64
+        flops = (6 * hs * hs + (5 * c - 1) * hs) * self.BH * self.T
+        a = flops / kernel_s / 1e12
+        return {"bound": "mfma", "achieved": a, "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": a / F32_MFMA_PEAK_TFLOPS, "flops_per_launch": flops, "hbm_bytes_per_launch": self.bytes,
+                "hbm_gbs": self.bytes / kernel_s / 1e9}
 
     def cpu_baseline(self):
         from oracle import oracle as O
