@@ -126,6 +126,30 @@ enum { Q8_STORE = 1, Q8_MUL = 2, Q8_ADD = 3 };
 int q8_gemm(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w, int kind, float *y, int ldy,
             const float *colv, hipStream_t st);
 
+// One LIF step (T = 1) fused into a few-rows product's epilogue: row b = stream b, column c = channel c.
+struct LifEpi {
+    const float *ps;       // [4][n]: beta | theta | rho | gain
+    float *v, *s, *a;      // [m][n] state, updated in place
+    int8_t *spikes;        // [m][ldspk] out
+    int ldspk, levels, is_signed, alif;
+};
+// y-less product: cur = planes . W (times colv when colv), then the step; m <= the few-rows limit.
+int q8_gemm_lif(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w, const float *colv,
+                const LifEpi &lif, hipStream_t st);
+int q8_small_rows();
+
+// The reference's LIF step (gpu/lif_gen.rs:171-180), every operation rounded on its own (the library
+// is compiled with -ffp-contract=off): the spike of membrane v at threshold th, levels each side.
+__device__ __forceinline__ float lif_spike(float v, float th, int levels, int is_signed) {
+    if (!is_signed) return (v - th >= 0.0f) ? 1.0f : 0.0f;
+    float h = 0.0f;
+    for (int k = 1; k <= levels; k++) {
+        const float kth = th * (float)k;
+        h += ((v - kth >= 0.0f) ? 1.0f : 0.0f) - ((-v - kth >= 0.0f) ? 1.0f : 0.0f);
+    }
+    return h;
+}
+
 // lif.hip / kwta.hip / mem.hip
 int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
                    int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf, hipStream_t st);
@@ -167,5 +191,11 @@ int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, co
              const float *keep, int g, float lr, double fade, double *scale, float *tab, float *err, float *part,
              int nks, float *delta, double *fold, double *nats, hipStream_t st);
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st);
+// The dense mix of [n][d] rows, then the planes of rmsnorm(row) * gain (and the normed row when hout);
+// the embedding rows, then the first norm's planes. d <= 1024.
+int dense_rms(float *x, float *const *streams, const float *w, int ns, int n, int d, const float *gain, int planes,
+              int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st);
+int embed_rms(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, const float *gain,
+              int planes, int8_t *xq, int32_t *xexp, int ldq, hipStream_t st);
 
 }  // namespace ava

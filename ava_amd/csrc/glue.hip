@@ -82,25 +82,18 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t *__restrict__ 
 
 // ------------------------------------------------------------------ RMSNorm -> planes
 
-// h = x (mean(x^2) + eps)^-1/2 * gain (gpu/model.rs:458-462); its planes, and h itself when hout.
+// h = x (mean(x^2) + eps)^-1/2 * gain (gpu/model.rs:458-462) of one row held in a wave's registers
+// (NV float4 chunks per lane, zero past d); its planes, and h itself when hout.
 template <int P, int NV>
-__global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict__ x, int n, int d,
-                                                         const float *__restrict__ gain, int8_t *__restrict__ xq,
-                                                         int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= n) return;
+__device__ __forceinline__ void row_rms_planes(f32x4 (&v)[NV], int lane, int d, const float *__restrict__ gain,
+                                               size_t n, size_t row, int8_t *__restrict__ xq,
+                                               int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
     const int nq = d >> 2;
-    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)row * d);
-    f32x4 v[NV];
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int c = i * 64 + lane;
-        v[i] = c < nq ? xr[c] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < NV; i++)
 #pragma unroll
         for (int z = 0; z < 4; z++) ss += v[i][z] * v[i][z];
-    }
     ss = ava::wave_sum(ss);
     const float ms = ss * (1.0f / (float)d) + 0.0f;
     const float inv = 1.0f / sqrtf(ms * 1.0f + NORM_EPS);
@@ -111,10 +104,28 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
             const f32x4 g = reinterpret_cast<const f32x4 *>(gain)[c];
 #pragma unroll
             for (int z = 0; z < 4; z++) v[i][z] = (v[i][z] * inv) * g[z];
-            if (hout) reinterpret_cast<f32x4 *>(hout + (size_t)row * d)[c] = v[i];
+            if (hout) reinterpret_cast<f32x4 *>(hout + row * d)[c] = v[i];
         }
     }
-    put_planes<P, NV>(v, lane, d, ldq, (size_t)n, (size_t)row, xq, xexp);
+    put_planes<P, NV>(v, lane, d, ldq, n, row, xq, xexp);
+}
+
+template <int P, int NV>
+__global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict__ x, int n, int d,
+                                                         const float *__restrict__ gain, int8_t *__restrict__ xq,
+                                                         int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    const int nq = d >> 2;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)row * d);
+    f32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = i * 64 + lane;
+        v[i] = c < nq ? xr[c] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    row_rms_planes<P, NV>(v, lane, d, gain, (size_t)n, (size_t)row, xq, xexp, ldq, hout);
 }
 
 // ------------------------------------------------------------------ f32 gate projections
@@ -536,6 +547,69 @@ __global__ __launch_bounds__(256) void dense_mix_kernel(DenseArgs a) {
     reinterpret_cast<f32x4 *>(a.x)[i] = mix;
 }
 
+// The dense mix of whole rows (the same terms in the same order as dense_mix_kernel) followed by the
+// next norm's planes of the mixed row (row_rms_planes): one wave per row, so the row is read once.
+template <int P, int NV>
+__global__ __launch_bounds__(256) void dense_rms_kernel(DenseArgs a, int n, int d, const float *__restrict__ gain,
+                                                        int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq,
+                                                        float *__restrict__ hout) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    const int nq = d >> 2;
+    const size_t base = (size_t)row * nq;
+    f32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = i * 64 + lane;
+        if (c < nq) {
+            const f32x4 x = reinterpret_cast<const f32x4 *>(a.x)[base + c];
+            reinterpret_cast<f32x4 *>(a.streams[a.ns - 1])[base + c] = x;
+            f32x4 mix = x;
+            for (int j = 0; j < a.ns; j++) {
+                const f32x4 s = j == a.ns - 1 ? x : reinterpret_cast<const f32x4 *>(a.streams[j])[base + c];
+                const float w = a.w[j];
+#pragma unroll
+                for (int z = 0; z < 4; z++) mix[z] = mix[z] + s[z] * w;
+            }
+            reinterpret_cast<f32x4 *>(a.x)[base + c] = mix;
+            v[i] = mix;
+        } else {
+            v[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    row_rms_planes<P, NV>(v, lane, d, gain, (size_t)n, (size_t)row, xq, xexp, ldq, hout);
+}
+
+// The embedding rows (as embed_kernel) followed by the first block's norm planes.
+template <int P, int NV>
+__global__ __launch_bounds__(256) void embed_rms_kernel(const int32_t *__restrict__ ids, const float *__restrict__ emb,
+                                                        int n, int d, int vocab, float *__restrict__ x,
+                                                        float *__restrict__ x0, const float *__restrict__ gain,
+                                                        int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    int id = ids[row];
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(emb + (size_t)id * d);
+    f32x4 *dst = reinterpret_cast<f32x4 *>(x + (size_t)row * d);
+    f32x4 *dst0 = x0 ? reinterpret_cast<f32x4 *>(x0 + (size_t)row * d) : nullptr;
+    f32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = i * 64 + lane;
+        if (c < (d >> 2)) {
+            v[i] = src[c];
+            dst[c] = v[i];
+            if (dst0) dst0[c] = v[i];
+        } else {
+            v[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    row_rms_planes<P, NV>(v, lane, d, gain, (size_t)n, (size_t)row, xq, xexp, ldq, nullptr);
+}
+
 }  // namespace
 
 namespace ava {
@@ -695,6 +769,37 @@ int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, i
 int engram_advance(int *n0p, int T, int cap, hipStream_t st) {
     store_advance_kernel<<<1, 64, 0, st>>>(n0p, T, cap);
     AVA_LAUNCHED("store_advance");
+    return AVA_OK;
+}
+
+int dense_rms(float *x, float *const *streams, const float *w, int ns, int n, int d, const float *gain, int planes,
+              int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st) {
+    AVA_REQUIRE(ns >= 2 && ns <= 17 && d % 4 == 0 && d <= 1024 && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE,
+                "dense_rms: %d streams, d=%d", ns, d);
+    DenseArgs a;
+    a.x = x;
+    for (int j = 0; j < ns; j++) {
+        a.streams[j] = streams[j];
+        a.w[j] = w[j];
+    }
+    a.ns = ns;
+    a.n4 = (size_t)n * d / 4;
+    const dim3 grid(ceil_div(n, 4)), block(256);
+    if (planes == 1) dense_rms_kernel<1, 4><<<grid, block, 0, st>>>(a, n, d, gain, xq, xexp, ldq, hout);
+    else if (planes == 2) dense_rms_kernel<2, 4><<<grid, block, 0, st>>>(a, n, d, gain, xq, xexp, ldq, hout);
+    else dense_rms_kernel<3, 4><<<grid, block, 0, st>>>(a, n, d, gain, xq, xexp, ldq, hout);
+    AVA_LAUNCHED("dense_rms");
+    return AVA_OK;
+}
+
+int embed_rms(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, const float *gain,
+              int planes, int8_t *xq, int32_t *xexp, int ldq, hipStream_t st) {
+    AVA_REQUIRE(d % 4 == 0 && d <= 1024 && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE, "embed_rms: d=%d", d);
+    const dim3 grid(ceil_div(n, 4)), block(256);
+    if (planes == 1) embed_rms_kernel<1, 4><<<grid, block, 0, st>>>(ids, emb, n, d, vocab, x, x0, gain, xq, xexp, ldq);
+    else if (planes == 2) embed_rms_kernel<2, 4><<<grid, block, 0, st>>>(ids, emb, n, d, vocab, x, x0, gain, xq, xexp, ldq);
+    else embed_rms_kernel<3, 4><<<grid, block, 0, st>>>(ids, emb, n, d, vocab, x, x0, gain, xq, xexp, ldq);
+    AVA_LAUNCHED("embed_rms");
     return AVA_OK;
 }
 

@@ -392,16 +392,29 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     }
     m->last_stream = st;
 
-    AVA_RUN("embed", ava::embed(ids, m->tok_emb, N, d, c.vocab, m->x, c.dense ? m->streams[0] : nullptr, st));
+    const bool cb = logits && c.cb_units > 0 && s->cb_code;
+    // the embedding and the first block's norm planes in one pass; after each block the dense mix and
+    // the next norm's planes in one pass (ready: the planes of the next norm are already in xq)
+    AVA_RUN("embed", ava::embed_rms(ids, m->tok_emb, N, d, c.vocab, m->x, c.dense ? m->streams[0] : nullptr,
+                                    m->blocks[0].lif_norm, P, m->xq, m->xexp, ldd, st));
+    bool ready = true, final_ready = false;
     for (int i = 0; i < L; i++) {
         const Block &b = m->blocks[i];
         const size_t sbd = (size_t)i * B * d;
         // the spiking layer
-        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.lif_norm, P, m->xq, m->xexp, ldd, nullptr, st));
-        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.win.w, c.lif_scale ? ava::Q8_MUL : ava::Q8_STORE,
-                                        m->cur, d, b.omb, st));
-        AVA_RUN("lif_scan", ava::lif_scan_tuned(m->cur, B, T, d, b.ps, s->lif_v + sbd, s->lif_s + sbd, s->lif_a + sbd,
-                                                c.levels, 1, c.alif, m->spk, nullptr, 0, 0, st));
+        if (!ready) AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.lif_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+        ready = false;
+        if (T == 1 && N <= ava::q8_small_rows()) {
+            // one token per stream: the LIF step runs in the Win product's epilogue
+            const ava::LifEpi lif{b.ps, s->lif_v + sbd, s->lif_s + sbd, s->lif_a + sbd, m->spk, ava::q8_ldk(d),
+                                  c.levels, 1, c.alif};
+            AVA_RUN("q8_gemm", ava::q8_gemm_lif(m->xq, m->xexp, P, N, &b.win.w, c.lif_scale ? b.omb : nullptr, lif, st));
+        } else {
+            AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.win.w, c.lif_scale ? ava::Q8_MUL : ava::Q8_STORE,
+                                            m->cur, d, b.omb, st));
+            AVA_RUN("lif_scan", ava::lif_scan_tuned(m->cur, B, T, d, b.ps, s->lif_v + sbd, s->lif_s + sbd,
+                                                    s->lif_a + sbd, c.levels, 1, c.alif, m->spk, nullptr, 0, 0, st));
+        }
         AVA_RUN("q8_gemm", ava::q8_gemm(m->spk, nullptr, 1, N, &b.wout.w, ava::Q8_ADD, m->x, d, nullptr, st));
         // the fast-weight memory
         AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
@@ -429,16 +442,28 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w1.w, ava::Q8_STORE, m->u, H, nullptr, st));
         AVA_RUN("kwta", ava::kwta_planes(m->u, N, H, c.kwta_k, c.relu2, P, m->xq, m->xexp, ldh, nullptr, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w2.w, ava::Q8_ADD, m->x, d, nullptr, st));
-        if (c.dense)
-            AVA_RUN("dense_mix", ava::dense_mix(m->x, m->streams.data(), b.dense.data(), i + 2, (size_t)N * d, st));
+        if (c.dense) {
+            if (i + 1 < L) {
+                AVA_RUN("dense_mix", ava::dense_rms(m->x, m->streams.data(), b.dense.data(), i + 2, N, d,
+                                                    m->blocks[i + 1].lif_norm, P, m->xq, m->xexp, ldd, nullptr, st));
+                ready = true;
+            } else if (logits) {
+                AVA_RUN("dense_mix", ava::dense_rms(m->x, m->streams.data(), b.dense.data(), i + 2, N, d, m->final_norm,
+                                                    P, m->xq, m->xexp, ldd, cb ? m->h : nullptr, st));
+                final_ready = true;
+            } else {
+                AVA_RUN("dense_mix", ava::dense_mix(m->x, m->streams.data(), b.dense.data(), i + 2, (size_t)N * d, st));
+            }
+        }
     }
     if (c.eng_block >= 0) {
         s->eng_len += T;
         if (s->eng_len_dev) AVA_RUN("store_advance", ava::engram_advance(s->eng_len_dev, T, s->eng_cap, st));
     }
     if (logits) {
-        const bool cb = c.cb_units > 0 && s->cb_code;
-        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, cb ? m->h : nullptr, st));
+        if (!final_ready)
+            AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, cb ? m->h : nullptr,
+                                                  st));
         if (cb) {
             // the cerebellum's correction between the final norm and the head (gpu/model/fstep/arch.rs:1045-1047)
             AVA_RUN("cb_code", ava::cb_code(m->h, ids, m->tok_emb, N, d, c.vocab, m->cb_idx, m->cb_sgn, c.cb_units, m->cb_k,

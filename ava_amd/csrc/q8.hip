@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
 
 // ------------------------------------------------------------------ the product
 
-enum Epi { EPI_ACC = 0, EPI_STORE = ava::Q8_STORE, EPI_MUL = ava::Q8_MUL, EPI_ADD = ava::Q8_ADD };
+enum Epi { EPI_ACC = 0, EPI_STORE = ava::Q8_STORE, EPI_MUL = ava::Q8_MUL, EPI_ADD = ava::Q8_ADD, EPI_LIF = 4 };
 
 
 
@@ -107,6 +107,7 @@ struct EpiArgs {
     int ldy;
     const float *colv;
     int group;  // row blocks per tile group (tile_origin)
+    ava::LifEpi lif;  // EPI_LIF (few-rows kernel only): the LIF step on the product
 };
 
 // The output tile of this workgroup. Workgroups are dealt round-robin to the 8 XCDs, each with its
@@ -573,6 +574,97 @@ struct SmallCfg {
     static constexpr size_t DBL = (size_t)4 * FN * 16 * 64 * 8;              // doubles, other epilogues
 };
 
+// The few-rows products' epilogue: wave w's P-plane accumulators of the 32 x 32 FN block combine
+// exactly in double; the four waves' partials add in LDS (smem, 32 FN KB; int32 planes for EPI_ACC);
+// then one rounding and the epilogue kind, as the tiled kernels' epilogue.
+template <int P, int EPI, int FN>
+__device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_t *smem, int m, int n, int m0, int n0,
+                                               const int32_t *__restrict__ xexp, const float *__restrict__ scale,
+                                               const EpiArgs &ep, int lane, int wave) {
+    const int rsub = (lane >> 5) * 4;
+    if (EPI == EPI_ACC) {
+        int *si = reinterpret_cast<int *>(smem);  // [wave][p][j][16][64]
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) si[(((wave * P + p) * FN + j) * 16 + r) * 64 + lane] = acc[p][j][r];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+                if (row < m && col < n)
+#pragma unroll
+                    for (int p = 0; p < P; p++) {
+                        int v = 0;
+#pragma unroll
+                        for (int w = 0; w < 4; w++) v += si[(((w * P + p) * FN + j) * 16 + r) * 64 + lane];
+                        reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = v;
+                    }
+            }
+        }
+        return;
+    }
+    double *sd = reinterpret_cast<double *>(smem);  // [wave][j][16][64]
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            double A = (double)acc[0][j][r];
+#pragma unroll
+            for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][j][r]);
+            sd[((wave * FN + j) * 16 + r) * 64 + lane] = A;
+        }
+    __syncthreads();
+    float *ybase = reinterpret_cast<float *>(ep.y);
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int col = n0 + j * 32 + (lane & 31);
+        if (col >= n) continue;
+        const float sc = scale[col];
+        const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+            if (row >= m) continue;
+            const int e = (j * 16 + r) * 64 + lane, ws = FN * 16 * 64;
+            const double A = ((sd[e] + sd[ws + e]) + sd[2 * ws + e]) + sd[3 * ws + e];
+            const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
+            float v = ldexpf((float)A, ex) * sc;
+            if (EPI == EPI_MUL) v = v * cv;
+            if (EPI == EPI_LIF) {
+                // cur (times colv: the lif-scale factor) into one step of the channel's scan, as
+                // lif_scan_kernel's loop body
+                const ava::LifEpi &L = ep.lif;
+                if (ep.colv) v = v * ep.colv[col];
+                const float bt = L.ps[col], th0 = L.ps[n + col], rho = L.ps[2 * n + col], gain = L.ps[3 * n + col];
+                const size_t o = (size_t)row * n + col;
+                float vv = L.v[o], sp = L.s[o], aa = L.a[o];
+                const float thp = L.alif ? th0 + aa * gain : th0;
+                float tht = th0;
+                if (L.alif) {
+                    aa = aa * rho + fabsf(sp) * (1.0f - rho);
+                    tht = th0 + aa * gain;
+                }
+                vv = (vv * bt + v) - sp * thp;
+                sp = ava::lif_spike(vv, tht, L.levels, L.is_signed);
+                L.v[o] = vv;
+                L.s[o] = sp;
+                L.a[o] = aa;
+                L.spikes[(size_t)row * L.ldspk + col] = (int8_t)sp;
+                continue;
+            }
+            float *yp = ybase + (size_t)row * ep.ldy + col;
+            if (EPI == EPI_ADD) v = *yp + v;
+            *yp = v;
+        }
+    }
+}
+
 template <int P, int EPI, int FN>
 __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
                                                        int m, int n, int ldk, const int8_t *__restrict__ qt,
@@ -646,67 +738,7 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
         b ^= 1;
     }
     __syncthreads();  // every wave is done with its buffers
-
-    const int rsub = (lane >> 5) * 4;
-    if (EPI == EPI_ACC) {
-        int *si = reinterpret_cast<int *>(smem);  // [wave][p][j][16][64]
-#pragma unroll
-        for (int p = 0; p < P; p++)
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) si[(((wave * P + p) * FN + j) * 16 + r) * 64 + lane] = acc[p][j][r];
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int col = n0 + j * 32 + (lane & 31);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
-                if (row < m && col < n)
-#pragma unroll
-                    for (int p = 0; p < P; p++) {
-                        int v = 0;
-#pragma unroll
-                        for (int w = 0; w < 4; w++) v += si[(((w * P + p) * FN + j) * 16 + r) * 64 + lane];
-                        reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = v;
-                    }
-            }
-        }
-        return;
-    }
-    double *sd = reinterpret_cast<double *>(smem);  // [wave][j][16][64]
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            double A = (double)acc[0][j][r];
-#pragma unroll
-            for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][j][r]);
-            sd[((wave * FN + j) * 16 + r) * 64 + lane] = A;
-        }
-    __syncthreads();
-    float *ybase = reinterpret_cast<float *>(ep.y);
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int col = n0 + j * 32 + (lane & 31);
-        if (col >= n) continue;
-        const float sc = scale[col];
-        const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
-            if (row >= m) continue;
-            const int e = (j * 16 + r) * 64 + lane, ws = FN * 16 * 64;
-            const double A = ((sd[e] + sd[ws + e]) + sd[2 * ws + e]) + sd[3 * ws + e];
-            const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
-            float v = ldexpf((float)A, ex) * sc;
-            if (EPI == EPI_MUL) v = v * cv;
-            float *yp = ybase + (size_t)row * ep.ldy + col;
-            if (EPI == EPI_ADD) v = *yp + v;
-            *yp = v;
-        }
-    }
+    small_epilogue<P, EPI, FN>(acc, smem, m, n, m0, n0, xexp, scale, ep, lane, wave);
 }
 
 template <int P, int EPI, int FN>
@@ -1183,6 +1215,21 @@ int q8_gemm(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_
     if (kind == EPI_MUL) return gemm_planes<EPI_MUL>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     if (kind == EPI_ADD) return gemm_planes<EPI_ADD>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     return fail(AVA_ERR_ARG, "q8 product: epilogue %d", kind);
+}
+
+int q8_small_rows() { return small_rows(); }
+
+int q8_gemm_lif(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w, const float *colv,
+                const LifEpi &lif, hipStream_t st) {
+    if (int r = check_qw(w)) return r;
+    AVA_REQUIRE(xq && lif.ps && lif.v && lif.s && lif.a && lif.spikes, AVA_ERR_ARG, "q8 lif product: NULL buffer");
+    AVA_REQUIRE(m > 0 && m <= small_rows(), AVA_ERR_SHAPE, "q8 lif product: %d rows (the few-rows form only)", m);
+    AVA_REQUIRE(lif.levels == 1 || lif.levels == 2, AVA_ERR_ARG, "q8 lif product: levels %d", lif.levels);
+    EpiArgs ep{nullptr, 0, colv, 1, lif};
+    if (planes == 1) return launch_small<1, EPI_LIF>(xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
+    if (planes == 2) return launch_small<2, EPI_LIF>(xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
+    if (planes == 3) return launch_small<3, EPI_LIF>(xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
+    return fail(AVA_ERR_ARG, "q8 lif product: planes %d", planes);
 }
 
 }  // namespace ava

@@ -470,7 +470,8 @@ class Decode:
         lif = L * B * d * 4 * 3 * 2
         fs = L * B * d * c["head_size"] * 4 * 2 * 2
         n = self.st.eng_len
-        kv = B * (n + 1) * de * 4 * 2 + B * de * 4 * 2
+        ek = 2 if c.get("eng_half") else 4  # the store's element (fp16 for config[4])
+        kv = B * (n + 1) * de * ek * 2 + B * de * ek * 2
         kept = G // 32
         cb = B * kept * d * 4 * 3 + B * G * 4 * 2
         out = B * V * 4 * 2 + V * d * 4
