@@ -148,6 +148,38 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
                 kth = hi;
                 done = true;
             }
+            // two first guesses from the units' mean and deviation as if normal (the quantile of the kept
+            // fraction, then a Newton step on the count): they only place the bracket
+            if (!done) {
+                float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < GPT; i++)
+                    if (tid + i * NT < g) {
+                        s1 += h[i];
+                        s2 += h[i] * h[i];
+                    }
+                s1 = block_sum(s1, fred);
+                s2 = block_sum(s2, fred);
+                const float mu = s1 / (float)g, sd = sqrtf(fmaxf(s2 / (float)g - mu * mu, 0.0f));
+                const float z = ava::normal_upper_quantile((float)k / (float)g);
+                const float dens = (float)g * 0.39894228f * __expf(-0.5f * z * z) / fmaxf(sd, 1e-30f);
+                float t = uni(mu + z * sd);
+                for (int gi = 0; gi < 2 && !found; gi++) {
+                    if (!(t > lo && t < hi)) break;
+                    const int c = count_ge(t);
+                    if (c == k) {
+                        tk = t;
+                        found = true;
+                    } else if (c > k) {
+                        lo = t;
+                        clo = c;
+                    } else {
+                        hi = t;
+                        chi = c;
+                    }
+                    t = uni(t + (float)(c - k) / dens);
+                }
+            }
             for (int it = 0; it < 40 && !done && !found; it++) {
                 float t = (it & 1) ? lo * 0.5f + hi * 0.5f : lo + (hi - lo) * ((float)(clo - k) / (float)(clo - chi));
                 if (!(t > lo && t < hi)) t = lo * 0.5f + hi * 0.5f;
@@ -373,17 +405,29 @@ __global__ __launch_bounds__(NT) void cb_delta_kernel(const float *__restrict__ 
     const int kb = ks * kslice, ke = min(V, kb + kslice);
     const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
     f32x16 acc = {};
+    // the next K tile is loaded into registers while the current one is multiplied
+    float ra[8], rb[8];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int z = 0; z < 8; z++) {
+            const int i = tid + z * NT;
+            const int r = i >> 5, kk = i & 31;
+            ra[z] = (r0 + r < B && k0 + kk < ke) ? err[(size_t)(r0 + r) * V + k0 + kk] : 0.0f;
+            const int kb2 = i >> 6, c = i & 63;
+            rb[z] = (k0 + kb2 < ke && c0 + c < d) ? E[(size_t)(k0 + kb2) * d + c0 + c] : 0.0f;
+        }
+    };
+    if (kb < ke) fetch(kb);
     for (int k0 = kb; k0 < ke; k0 += 32) {
         __syncthreads();
-        for (int i = tid; i < 64 * 32; i += NT) {
-            const int r = i >> 5, kk = i & 31;
-            sa[r][kk] = (r0 + r < B && k0 + kk < ke) ? err[(size_t)(r0 + r) * V + k0 + kk] : 0.0f;
-        }
-        for (int i = tid; i < 32 * 64; i += NT) {
-            const int kk = i >> 6, c = i & 63;
-            sb[kk][c] = (k0 + kk < ke && c0 + c < d) ? E[(size_t)(k0 + kk) * d + c0 + c] : 0.0f;
+#pragma unroll
+        for (int z = 0; z < 8; z++) {
+            const int i = tid + z * NT;
+            sa[i >> 5][i & 31] = ra[z];
+            sb[i >> 6][i & 63] = rb[z];
         }
         __syncthreads();
+        if (k0 + 32 < ke) fetch(k0 + 32);
 #pragma unroll
         for (int s = 0; s < 32; s += 2) {
             const float a = sa[wr + (lane & 31)][s + (lane >> 5)];

@@ -100,6 +100,16 @@ static inline __device__ uint32_t pack4(int a, int b, int c, int d) {
            ((uint32_t)(uint8_t)(int8_t)c << 16) | ((uint32_t)(uint8_t)(int8_t)d << 24);
 }
 
+// z with P(N(0,1) >= z) = p, 0 < p < 1, to about 1e-3 (a search guess only): the rational
+// approximation of Abramowitz and Stegun 26.2.23 on the smaller tail.
+__device__ __forceinline__ float normal_upper_quantile(float p) {
+    const float q = p < 0.5f ? p : 1.0f - p;
+    const float w = sqrtf(-2.0f * __logf(fmaxf(q, 1e-30f)));
+    const float z = w - (2.515517f + w * (0.802853f + w * 0.010328f)) /
+                            (1.0f + w * (1.432788f + w * (0.189269f + w * 0.001308f)));
+    return p < 0.5f ? z : -z;
+}
+
 // Wave64 reductions.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -169,6 +179,10 @@ int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8
                float *hout, hipStream_t st);
 // G = h . W in f32 (fp32 MFMA tiles; few rows: a VALU kernel over 4 rows per workgroup).
 int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st);
+// For few rows: the norm's planes and the gate projections of the normed rows in one launch.
+bool rms_gate_fits(int n, int d, int nc);
+int rms_gate(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
+             const float *w, int nc, float *g, hipStream_t st);
 int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, int8_t *xq, int32_t *xexp, int ldq,
              hipStream_t st);
 // The engram read: the tiled causal form for T > ENGRAM_SPLIT_T, the chunk-split decode form (with

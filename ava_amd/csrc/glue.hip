@@ -684,6 +684,84 @@ __global__ __launch_bounds__(1024) void gate_rows_kernel(const float *__restrict
     }
 }
 
+// The norm of 4 rows (waves 0..3, one row each, as rms_planes_kernel: planes to xq) and then, from
+// the normed rows kept in LDS, their gate projections (all 16 waves, as gate_rows_kernel): for few
+// rows, one launch instead of two and no round trip of h.
+template <int P>
+__global__ __launch_bounds__(1024) void rms_gate_kernel(const float *__restrict__ x, int n, int d,
+                                                        const float *__restrict__ gain, int8_t *__restrict__ xq,
+                                                        int32_t *__restrict__ xexp, int ldq,
+                                                        const float *__restrict__ w, int nc, float *__restrict__ g) {
+    __shared__ __attribute__((aligned(16))) float sh[GRR][1024];
+    __shared__ float sacc[GKS][GRR][128];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r0 = blockIdx.x * GRR;
+    if (wave < GRR) {
+        const int row = r0 + wave, nq = d >> 2;
+        f32x4 v[4];
+        if (row < n) {
+            const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)row * d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = i * 64 + lane;
+                v[i] = c < nq ? xr[c] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            row_rms_planes<P, 4>(v, lane, d, gain, (size_t)n, (size_t)row, xq, xexp, ldq, nullptr);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = i * 64 + lane;
+            if (c < nq) *reinterpret_cast<f32x4 *>(&sh[wave][4 * c]) = v[i];
+        }
+    }
+    __syncthreads();
+    const int c = tid & 127, ks = tid >> 7;
+    float acc[GRR] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < nc) {
+        const int kb = ks * (d / GKS), ke = kb + d / GKS;
+        for (int k0 = kb; k0 < ke; k0 += 32) {
+            float wv[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++) wv[j] = w[(size_t)(k0 + j) * nc + c];
+            AVA_ISSUE_FENCE();
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+#pragma unroll
+                for (int r = 0; r < GRR; r++) acc[r] = fmaf(sh[r][k0 + j], wv[j], acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GRR; r++) sacc[ks][r][c] = acc[r];
+    __syncthreads();
+    if (tid < GRR * 128) {
+        const int r = tid >> 7;
+        if (c < nc && r0 + r < n) {
+            float v = sacc[0][r][c];
+#pragma unroll
+            for (int q = 1; q < GKS; q++) v += sacc[q][r][c];
+            g[(size_t)(r0 + r) * nc + c] = v;
+        }
+    }
+}
+
+bool rms_gate_fits(int n, int d, int nc) {
+    return ceil_div(n, GR) < 64 && d <= 1024 && d % (GKS * 32) == 0 && nc <= 128;
+}
+
+int rms_gate(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
+             const float *w, int nc, float *g, hipStream_t st) {
+    AVA_REQUIRE(rms_gate_fits(n, d, nc) && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE, "rms_gate: n=%d d=%d nc=%d", n,
+                d, nc);
+    const dim3 grid(ceil_div(n, GRR)), block(1024);
+    if (planes == 1) rms_gate_kernel<1><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);
+    else if (planes == 2) rms_gate_kernel<2><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);
+    else rms_gate_kernel<3><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);
+    AVA_LAUNCHED("rms_gate");
+    return AVA_OK;
+}
+
 int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st) {
     AVA_REQUIRE(nc > 0 && nc <= 128 && d % GK == 0, AVA_ERR_SHAPE, "gate_gemm: %d columns (<= 128), d=%d", nc, d);
     const int blocks = ceil_div(n, GR);

@@ -32,38 +32,95 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float uni(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
 
-// z with P(N(0,1) >= z) = p, 0 < p < 1, to about 1e-3 (a search guess only): the rational
-// approximation of Abramowitz and Stegun 26.2.23 on the smaller tail.
-__device__ __forceinline__ float normal_upper_quantile(float p) {
-    const float q = p < 0.5f ? p : 1.0f - p;
-    const float w = sqrtf(-2.0f * __logf(fmaxf(q, 1e-30f)));
-    const float z = w - (2.515517f + w * (0.802853f + w * 0.010328f)) /
-                            (1.0f + w * (1.432788f + w * (0.189269f + w * 0.001308f)));
-    return p < 0.5f ? z : -z;
-}
 
-// NV float4 chunks per lane: h <= 256 NV. OUT: 0 = f32 a, P>0 = P int8 planes + row exponent.
-template <int NV, int P, bool FULL>
+
+// Row reductions: over the wave (a wave per row), or over the 4 waves through LDS (WG: a workgroup
+// per row, for few rows). Results are wave-uniform (readfirstlane) either way; the leading barrier
+// keeps a reduction from overwriting slots the previous one is still reading.
+template <bool WG>
+struct RowRed {
+    float *fs;
+    int *is;
+    __device__ __forceinline__ float fsum(float v) {
+        v = ava::wave_sum(v);
+        if (WG) {
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) fs[threadIdx.x >> 6] = v;
+            __syncthreads();
+            v = (fs[0] + fs[1]) + (fs[2] + fs[3]);
+        }
+        return uni(v);
+    }
+    __device__ __forceinline__ float fmin(float v) {
+        v = ava::wave_min(v);
+        if (WG) {
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) fs[threadIdx.x >> 6] = v;
+            __syncthreads();
+            v = fminf(fminf(fs[0], fs[1]), fminf(fs[2], fs[3]));
+        }
+        return uni(v);
+    }
+    __device__ __forceinline__ float fmax(float v) {
+        v = ava::wave_max(v);
+        if (WG) {
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) fs[threadIdx.x >> 6] = v;
+            __syncthreads();
+            v = fmaxf(fmaxf(fs[0], fs[1]), fmaxf(fs[2], fs[3]));
+        }
+        return uni(v);
+    }
+    __device__ __forceinline__ int isum(int v) {  // v wave-uniform
+        if (WG) {
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) is[threadIdx.x >> 6] = v;
+            __syncthreads();
+            v = (is[0] + is[1]) + (is[2] + is[3]);
+        }
+        return __builtin_amdgcn_readfirstlane(v);
+    }
+    __device__ __forceinline__ uint32_t umin(uint32_t v) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+        if (WG) {
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) is[threadIdx.x >> 6] = (int)v;
+            __syncthreads();
+            v = min(min((uint32_t)is[0], (uint32_t)is[1]), min((uint32_t)is[2], (uint32_t)is[3]));
+        }
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+    }
+};
+
+// NV float4 chunks per lane. A wave per row (WG false): h <= 256 NV, chunk c = 64 i + lane; a
+// workgroup per row (WG true): h <= 1024 NV, chunk c = 256 i + thread. OUT: 0 = f32 a, P>0 = P int8
+// planes + row exponent.
+template <int NV, int P, bool FULL, bool WG = false>
 __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, int n, int h, int k, int relu2,
                                                    float *__restrict__ a, float *__restrict__ kth_out,
                                                    int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= n) return;
+    __shared__ float s_f[4];
+    __shared__ int s_i[4];
+    RowRed<WG> red{s_f, s_i};
+    constexpr int LANES = WG ? 256 : 64;  // threads of a row
+    const int lane = WG ? (int)threadIdx.x : (int)(threadIdx.x & 63);
+    const int row = WG ? (int)blockIdx.x : (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    if (row >= n) return;  // uniform over the row's threads
     const float *ur = u + (size_t)row * h;
     const int nq = h >> 2;  // float4 chunks in the row
 
     f32x4 x[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int c = i * 64 + lane;
+        const int c = i * LANES + lane;
         if (FULL || c < nq) x[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(ur) + c);
         else x[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // never counted: see below
     }
 
     float kth = -INFINITY;
     const bool all = k >= h;
-    constexpr bool full = FULL;  // h == 256 NV: every chunk real, no padding lanes
+    constexpr bool full = FULL;  // h == LANES NV * 4: every chunk real, no padding lanes
     // count of the row's values >= t (padding chunks are -inf and never counted for finite t)
     auto count_ge = [&](float t) {
         int c = 0;
@@ -71,7 +128,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
         for (int i = 0; i < NV; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) c += __popcll(__ballot(x[i][j] >= t));
-        return c;
+        return red.isum(c);
     };
     // the k-th largest once exactly k values are >= t: the smallest of them. A zero result is
     // -0 when a -0 is among them (in the order of the keys, -0 < +0), else +0.
@@ -81,14 +138,14 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
         for (int i = 0; i < NV; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) mn = x[i][j] >= t ? fminf(mn, x[i][j]) : mn;
-        mn = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ava::wave_min(mn))));
+        mn = red.fmin(mn);
         if (mn == 0.0f) {
             bool neg = false;
 #pragma unroll
             for (int i = 0; i < NV; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) neg |= x[i][j] >= t && __float_as_uint(x[i][j]) == 0x80000000u;
-            mn = __ballot(neg) ? -0.0f : 0.0f;
+            mn = red.isum(__ballot(neg) ? 1 : 0) ? -0.0f : 0.0f;
         }
         return mn;
     };
@@ -102,15 +159,15 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
         for (int i = 0; i < NV; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const bool real = full || i * 64 + lane < nq;
+                const bool real = full || i * LANES + lane < nq;
                 if (real) {
                     lo = fminf(lo, x[i][j]);
                     hi = fmaxf(hi, x[i][j]);
                 }
             }
         // wave-uniform (readfirstlane), so the search's control flow is scalar
-        lo = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ava::wave_min(lo))));
-        hi = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ava::wave_max(hi))));
+        lo = red.fmin(lo);
+        hi = red.fmax(hi);
         bool done = false, found = false;
         float tk = 0.0f;  // a threshold with exactly k values at or above it
         if (isfinite(lo) && isfinite(hi)) {
@@ -129,14 +186,14 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
                 for (int i = 0; i < NV; i++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        const bool real = full || i * 64 + lane < nq;
+                        const bool real = full || i * LANES + lane < nq;
                         s1 += real ? x[i][j] : 0.0f;
                         s2 += real ? x[i][j] * x[i][j] : 0.0f;
                     }
-                s1 = ava::wave_sum(s1);
-                s2 = ava::wave_sum(s2);
+                s1 = red.fsum(s1);
+                s2 = red.fsum(s2);
                 const float mu = s1 / (float)h, sd = sqrtf(fmaxf(s2 / (float)h - mu * mu, 0.0f));
-                const float z = normal_upper_quantile((float)k / (float)h);
+                const float z = ava::normal_upper_quantile((float)k / (float)h);
                 const float dens = (float)h * 0.39894228f * __expf(-0.5f * z * z) / fmaxf(sd, 1e-30f);
                 float t = uni(mu + z * sd);
                 for (int g = 0; g < 2 && !found; g++) {
@@ -186,7 +243,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
             for (int i = 0; i < NV; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const bool real = full || i * 64 + lane < nq;
+                    const bool real = full || i * LANES + lane < nq;
                     x[i][j] = __uint_as_float(real ? key_of(x[i][j]) : 0u);
                 }
             uint32_t prefix = 0;
@@ -197,6 +254,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
                 for (int i = 0; i < NV; i++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) cnt += __popcll(__ballot(__float_as_uint(x[i][j]) >= cand));
+                cnt = red.isum(cnt);
                 if (cnt >= k) prefix = cand;
                 if (cnt == k) {
                     // exactly k keys are >= cand: the k-th largest is the smallest of them
@@ -208,9 +266,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
                             const uint32_t kk = __float_as_uint(x[i][j]);
                             mn = kk >= cand ? min(mn, kk) : mn;
                         }
-#pragma unroll
-                    for (int o = 32; o > 0; o >>= 1) mn = min(mn, (uint32_t)__shfl_xor((int)mn, o, 64));
-                    prefix = mn;
+                    prefix = red.umin(mn);
                     break;
                 }
             }
@@ -219,7 +275,7 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
             for (int i = 0; i < NV; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const bool real = full || i * 64 + lane < nq;
+                    const bool real = full || i * LANES + lane < nq;
                     x[i][j] = real ? float_of_key(__float_as_uint(x[i][j])) : -INFINITY;
                 }
         }
@@ -245,16 +301,16 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
         float *ar = a + (size_t)row * h;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            const int c = i * 64 + lane;
+            const int c = i * LANES + lane;
             if (full || c < nq) __builtin_nontemporal_store(x[i], reinterpret_cast<f32x4 *>(ar) + c);
         }
     } else {
-        amax = ava::wave_max(amax);
+        amax = red.fmax(amax);
         const int e = ava::plane_exp(amax);
         if (lane == 0) xexp[row] = e;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            const int c = i * 64 + lane;
+            const int c = i * LANES + lane;
             if (full || c < nq) {
                 int q0[P], q1[P], q2[P], q3[P];
                 ava::to_planes<P>(x[i][0], e, q0);
@@ -268,16 +324,42 @@ __global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, 
             }
         }
         // zero the K padding of the planes (ldq > h)
-        for (int c = h + lane * 4; c < ldq; c += 256)
+        for (int c = h + lane * 4; c < ldq; c += 4 * LANES)
 #pragma unroll
             for (int p = 0; p < P; p++)
                 *reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq + c) = 0u;
     }
 }
 
+// Rows at most this many take a workgroup each (AVA_KWTA_WG_ROWS overrides it; tuning): with few rows
+// a wave per row leaves most of the chip idle and each row's search is a chain of counts.
+int wg_rows() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_KWTA_WG_ROWS");
+        v = e ? atoi(e) : 2048;
+        if (v < 0) v = 0;
+    }
+    return v;
+}
+
 template <int P>
 int launch(const float *u, int n, int h, int k, int relu2, float *a, float *kth, int8_t *xq, int32_t *xexp,
            int ldq, hipStream_t st) {
+    if (n <= wg_rows() && h <= 4096) {
+        const int nv4 = (h + 1023) / 1024;
+#define AVA_KWG(NV_)                                                                                           \
+    if (nv4 <= NV_) {                                                                                          \
+        if (h == NV_ * 1024)                                                                                   \
+            kwta_kernel<NV_, P, true, true><<<n, 256, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);       \
+        else                                                                                                   \
+            kwta_kernel<NV_, P, false, true><<<n, 256, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);      \
+        AVA_LAUNCHED("kwta");                                                                                  \
+        return AVA_OK;                                                                                         \
+    }
+        AVA_KWG(1) AVA_KWG(2) AVA_KWG(4)
+#undef AVA_KWG
+    }
     const int nv = (h + 255) / 256;
     dim3 grid(ava::ceil_div(n, 4)), block(256);
 #define AVA_KW(NV_)                                                                                      \

@@ -417,9 +417,15 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         }
         AVA_RUN("q8_gemm", ava::q8_gemm(m->spk, nullptr, 1, N, &b.wout.w, ava::Q8_ADD, m->x, d, nullptr, st));
         // the fast-weight memory
-        AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
-        AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
-        AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, st));
+        if (ava::rms_gate_fits(N, d, 2 * nh + 2 * r)) {
+            AVA_RUN("rms_planes", ava::rms_gate(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, b.wgate, 2 * nh + 2 * r,
+                                                m->G, st));
+            AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
+        } else {
+            AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
+            AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
+            AVA_RUN("gate_gemm", ava::gate_gemm(m->h, N, d, b.wgate, 2 * nh + 2 * r, m->G, st));
+        }
         const bool vr = c.value_residual != 0;
         const size_t sm = (size_t)i * B * nh * 64 * 64;
         AVA_RUN("mem_scan", ava::mem_block(m->P, m->G, B, T, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,
