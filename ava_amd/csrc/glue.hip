@@ -566,12 +566,24 @@ __global__ __launch_bounds__(256) void dense_rms_kernel(DenseArgs a, int n, int 
             const f32x4 x = reinterpret_cast<const f32x4 *>(a.x)[base + c];
             reinterpret_cast<f32x4 *>(a.streams[a.ns - 1])[base + c] = x;
             f32x4 mix = x;
-            for (int j = 0; j < a.ns; j++) {
-                const f32x4 s = j == a.ns - 1 ? x : reinterpret_cast<const f32x4 *>(a.streams[j])[base + c];
-                const float w = a.w[j];
+            // the earlier streams in batches of 4 whose loads are all in flight before the adds (in j order)
+            for (int j0 = 0; j0 < a.ns - 1; j0 += 4) {
+                f32x4 sv[4];
 #pragma unroll
-                for (int z = 0; z < 4; z++) mix[z] = mix[z] + s[z] * w;
+                for (int q = 0; q < 4; q++)
+                    sv[q] = reinterpret_cast<const f32x4 *>(a.streams[min(j0 + q, a.ns - 2)])[base + c];
+                AVA_ISSUE_FENCE();
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (j0 + q < a.ns - 1) {
+                        const float w = a.w[j0 + q];
+#pragma unroll
+                        for (int z = 0; z < 4; z++) mix[z] = mix[z] + sv[q][z] * w;
+                    }
             }
+            const float wl = a.w[a.ns - 1];
+#pragma unroll
+            for (int z = 0; z < 4; z++) mix[z] = mix[z] + x[z] * wl;
             reinterpret_cast<f32x4 *>(a.x)[base + c] = mix;
             v[i] = mix;
         } else {
@@ -687,15 +699,15 @@ __global__ __launch_bounds__(1024) void gate_rows_kernel(const float *__restrict
 // The norm of 4 rows (waves 0..3, one row each, as rms_planes_kernel: planes to xq) and then, from
 // the normed rows kept in LDS, their gate projections (all 16 waves, as gate_rows_kernel): for few
 // rows, one launch instead of two and no round trip of h.
-template <int P>
+template <int P, int RR>  // RR rows per workgroup (1: the most workgroups, for the fewest rows)
 __global__ __launch_bounds__(1024) void rms_gate_kernel(const float *__restrict__ x, int n, int d,
                                                         const float *__restrict__ gain, int8_t *__restrict__ xq,
                                                         int32_t *__restrict__ xexp, int ldq,
                                                         const float *__restrict__ w, int nc, float *__restrict__ g) {
-    __shared__ __attribute__((aligned(16))) float sh[GRR][1024];
-    __shared__ float sacc[GKS][GRR][128];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r0 = blockIdx.x * GRR;
-    if (wave < GRR) {
+    __shared__ __attribute__((aligned(16))) float sh[RR][1024];
+    __shared__ float sacc[GKS][RR][128];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r0 = blockIdx.x * RR;
+    if (wave < RR) {
         const int row = r0 + wave, nq = d >> 2;
         f32x4 v[4];
         if (row < n) {
@@ -718,7 +730,9 @@ __global__ __launch_bounds__(1024) void rms_gate_kernel(const float *__restrict_
     }
     __syncthreads();
     const int c = tid & 127, ks = tid >> 7;
-    float acc[GRR] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[RR];
+#pragma unroll
+    for (int r = 0; r < RR; r++) acc[r] = 0.0f;
     if (c < nc) {
         const int kb = ks * (d / GKS), ke = kb + d / GKS;
         for (int k0 = kb; k0 < ke; k0 += 32) {
@@ -729,13 +743,13 @@ __global__ __launch_bounds__(1024) void rms_gate_kernel(const float *__restrict_
 #pragma unroll
             for (int j = 0; j < 32; j++)
 #pragma unroll
-                for (int r = 0; r < GRR; r++) acc[r] = fmaf(sh[r][k0 + j], wv[j], acc[r]);
+                for (int r = 0; r < RR; r++) acc[r] = fmaf(sh[r][k0 + j], wv[j], acc[r]);
         }
     }
 #pragma unroll
-    for (int r = 0; r < GRR; r++) sacc[ks][r][c] = acc[r];
+    for (int r = 0; r < RR; r++) sacc[ks][r][c] = acc[r];
     __syncthreads();
-    if (tid < GRR * 128) {
+    if (tid < RR * 128) {
         const int r = tid >> 7;
         if (c < nc && r0 + r < n) {
             float v = sacc[0][r][c];
@@ -754,10 +768,16 @@ int rms_gate(const float *x, int n, int d, const float *gain, int planes, int8_t
              const float *w, int nc, float *g, hipStream_t st) {
     AVA_REQUIRE(rms_gate_fits(n, d, nc) && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE, "rms_gate: n=%d d=%d nc=%d", n,
                 d, nc);
-    const dim3 grid(ceil_div(n, GRR)), block(1024);
-    if (planes == 1) rms_gate_kernel<1><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);
-    else if (planes == 2) rms_gate_kernel<2><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);
-    else rms_gate_kernel<3><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);
+    // one row per workgroup while that still fills the chip with a few rounds, else four
+    const bool one = n <= 1024;
+    const dim3 grid(ceil_div(n, one ? 1 : GRR)), block(1024);
+#define AVA_RG(P_)                                                                                            \
+    if (one) rms_gate_kernel<P_, 1><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);          \
+    else rms_gate_kernel<P_, GRR><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g)
+    if (planes == 1) AVA_RG(1);
+    else if (planes == 2) AVA_RG(2);
+    else AVA_RG(3);
+#undef AVA_RG
     AVA_LAUNCHED("rms_gate");
     return AVA_OK;
 }

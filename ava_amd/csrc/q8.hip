@@ -627,6 +627,57 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
         if (col >= n) continue;
         const float sc = scale[col];
         const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+        if constexpr (EPI == EPI_LIF) {
+            // cur (times colv: the lif-scale factor) into one step of the channel's scan, as
+            // lif_scan_kernel's loop body; the 4 rows' state loads are all issued before any use
+            const ava::LifEpi &L = ep.lif;
+            const float bt = L.ps[col], th0 = L.ps[n + col], rho = L.ps[2 * n + col], gain = L.ps[3 * n + col];
+            const float cf = ep.colv ? ep.colv[col] : 1.0f;
+            float sv[4], ss[4], sa[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int r = wave + 4 * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
+                const size_t o = (size_t)row * n + col;
+                sv[q] = L.v[o];
+                ss[q] = L.s[o];
+                sa[q] = L.a[o];
+            }
+            AVA_ISSUE_FENCE();
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+                if (row >= m) continue;
+                const int e = (j * 16 + r) * 64 + lane, ws = FN * 16 * 64;
+                const double A = ((sd[e] + sd[ws + e]) + sd[2 * ws + e]) + sd[3 * ws + e];
+                const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
+                float v = ldexpf((float)A, ex) * sc;
+                if (ep.colv) v = v * cf;
+                float vv = sv[q], sp = ss[q], aa = sa[q];
+                const float thp = L.alif ? th0 + aa * gain : th0;
+                float tht = th0;
+                if (L.alif) {
+                    aa = aa * rho + fabsf(sp) * (1.0f - rho);
+                    tht = th0 + aa * gain;
+                }
+                vv = (vv * bt + v) - sp * thp;
+                sp = ava::lif_spike(vv, tht, L.levels, L.is_signed);
+                const size_t o = (size_t)row * n + col;
+                L.v[o] = vv;
+                L.s[o] = sp;
+                L.a[o] = aa;
+                L.spikes[(size_t)row * L.ldspk + col] = (int8_t)sp;
+            }
+            continue;
+        }
+        float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (EPI == EPI_ADD) {  // the 4 rows' loads all in flight before any add
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int r = wave + 4 * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
+                prev[q] = ybase[(size_t)row * ep.ldy + col];
+            }
+            AVA_ISSUE_FENCE();
+        }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
@@ -636,31 +687,8 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
             const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
             float v = ldexpf((float)A, ex) * sc;
             if (EPI == EPI_MUL) v = v * cv;
-            if (EPI == EPI_LIF) {
-                // cur (times colv: the lif-scale factor) into one step of the channel's scan, as
-                // lif_scan_kernel's loop body
-                const ava::LifEpi &L = ep.lif;
-                if (ep.colv) v = v * ep.colv[col];
-                const float bt = L.ps[col], th0 = L.ps[n + col], rho = L.ps[2 * n + col], gain = L.ps[3 * n + col];
-                const size_t o = (size_t)row * n + col;
-                float vv = L.v[o], sp = L.s[o], aa = L.a[o];
-                const float thp = L.alif ? th0 + aa * gain : th0;
-                float tht = th0;
-                if (L.alif) {
-                    aa = aa * rho + fabsf(sp) * (1.0f - rho);
-                    tht = th0 + aa * gain;
-                }
-                vv = (vv * bt + v) - sp * thp;
-                sp = ava::lif_spike(vv, tht, L.levels, L.is_signed);
-                L.v[o] = vv;
-                L.s[o] = sp;
-                L.a[o] = aa;
-                L.spikes[(size_t)row * L.ldspk + col] = (int8_t)sp;
-                continue;
-            }
-            float *yp = ybase + (size_t)row * ep.ldy + col;
-            if (EPI == EPI_ADD) v = *yp + v;
-            *yp = v;
+            if (EPI == EPI_ADD) v = prev[q] + v;
+            ybase[(size_t)row * ep.ldy + col] = v;
         }
     }
 }
