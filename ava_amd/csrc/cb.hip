@@ -366,29 +366,78 @@ __global__ __launch_bounds__(NT) void cb_apply_cols_kernel(const float *__restri
 // err [B][V] = softmax(logits row) - onehot(next) (max, exp(z - max), the sum, p / sum); nats [B]
 // (nullable) = -ln max(p_next, 1e-30). Rows whose next is outside [0, V) are skipped (err zeroed,
 // nats NaN): the reference's IGNORE.
+// err[b] = softmax(logits[b]) - onehot(next[b]) and nats[b] = -ln p(next), one workgroup per row;
+// rows with next outside [0, V) get err = 0 and nats = NaN. KV > 0: the row (V <= KV NT) is read once
+// into registers, all loads in flight together; KV = 0: any V, three passes over the row. Both add
+// the same terms in the same order. Thread 0 also steps the row's table scale: rows with a valid next
+// fade by `fade` (2^(-1/half), host-computed; 1 = no fading); below 1e-18 the row is marked for
+// folding (fold[b] = the old scale) and its scale returns to 1.
+template <int KV>
 __global__ __launch_bounds__(NT) void cb_err_kernel(const float *__restrict__ logits, int ldl, int V,
                                                     const int32_t *__restrict__ next, float *__restrict__ err,
-                                                    double *__restrict__ nats) {
+                                                    double *__restrict__ nats, double fade, double *__restrict__ scale,
+                                                    double *__restrict__ fold) {
     __shared__ float fred[4];
     const int b = blockIdx.x, tid = threadIdx.x;
     const float *z = logits + (size_t)b * ldl;
     float *er = err + (size_t)b * V;
     const int y = next[b];
-    if (y < 0 || y >= V) {
+    const bool live = y >= 0 && y < V;
+    if (tid == 0) {
+        double f = 0.0;
+        if (live && fade != 1.0) {
+            double sc = scale[b] * fade;
+            if (sc < 1e-18) {
+                f = sc;
+                sc = 1.0;
+            }
+            scale[b] = sc;
+        }
+        fold[b] = f;
+    }
+    if (!live) {
         for (int j = tid; j < V; j += NT) er[j] = 0.0f;
         if (nats && tid == 0) nats[b] = __longlong_as_double(0x7ff8000000000000ll);
         return;
     }
-    float mx = -INFINITY;
-    for (int j = tid; j < V; j += NT) mx = fmaxf(mx, z[j]);
-    mx = block_max(mx, fred);
-    float den = 0.0f;
-    for (int j = tid; j < V; j += NT) den += expf(z[j] - mx);
-    den = block_sum(den, fred);
-    for (int j = tid; j < V; j += NT) {
-        const float p = expf(z[j] - mx) / den;
-        er[j] = p - (j == y ? 1.0f : 0.0f);
-        if (nats && j == y) nats[b] = -log((double)(p > 1e-30f ? p : 1e-30f));
+    if constexpr (KV > 0) {
+        float zv[KV];
+#pragma unroll
+        for (int i = 0; i < KV; i++) {
+            const int j = tid + i * NT;
+            zv[i] = j < V ? z[j] : 0.0f;
+        }
+        AVA_ISSUE_FENCE();
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < KV; i++)
+            if (tid + i * NT < V) mx = fmaxf(mx, zv[i]);
+        mx = block_max(mx, fred);
+        float den = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KV; i++)
+            if (tid + i * NT < V) den += expf(zv[i] - mx);
+        den = block_sum(den, fred);
+#pragma unroll
+        for (int i = 0; i < KV; i++) {
+            const int j = tid + i * NT;
+            if (j >= V) continue;
+            const float p = expf(zv[i] - mx) / den;
+            er[j] = p - (j == y ? 1.0f : 0.0f);
+            if (nats && j == y) nats[b] = -log((double)(p > 1e-30f ? p : 1e-30f));
+        }
+    } else {
+        float mx = -INFINITY;
+        for (int j = tid; j < V; j += NT) mx = fmaxf(mx, z[j]);
+        mx = block_max(mx, fred);
+        float den = 0.0f;
+        for (int j = tid; j < V; j += NT) den += expf(z[j] - mx);
+        den = block_sum(den, fred);
+        for (int j = tid; j < V; j += NT) {
+            const float p = expf(z[j] - mx) / den;
+            er[j] = p - (j == y ? 1.0f : 0.0f);
+            if (nats && j == y) nats[b] = -log((double)(p > 1e-30f ? p : 1e-30f));
+        }
     }
 }
 
@@ -453,43 +502,17 @@ __global__ void cb_delta_sum_kernel(const float *__restrict__ part, int nks, int
     delta[i] = s;
 }
 
-// The table's scale: rows with a valid next fade by `fade` (2^(-1/half), host-computed; 1 = no fading);
-// below 1e-18 the row is marked for folding (fold[b] = the old scale) and its scale returns to 1.
-__global__ void cb_scale_kernel(const int32_t *__restrict__ next, int B, int V, double fade, double *__restrict__ scale,
-                                double *__restrict__ fold) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) return;
-    const int y = next[b];
-    double f = 0.0;
-    if (y >= 0 && y < V && fade != 1.0) {
-        double s = scale[b] * fade;
-        if (s < 1e-18) {
-            f = s;
-            s = 1.0;
-        }
-        scale[b] = s;
-    }
-    fold[b] = f;
-}
-
-// Fold marked rows: tab[b] = (float)((double)tab[b] * fold[b]) (a rare event; one workgroup per row).
-__global__ __launch_bounds__(1024) void cb_fold_kernel(const double *__restrict__ fold, size_t per,
-                                                       float *__restrict__ tab) {
-    const double f = fold[blockIdx.x];
-    if (f == 0.0) return;
-    float *t = tab + (size_t)blockIdx.x * per;
-    for (size_t i = threadIdx.x; i < per; i += 1024) t[i] = (float)((double)t[i] * f);
-}
-
 // tab[b][u] -= s_u delta[b] for the non-zero units u of the kept code, s_u = lr * c_u (divided by
 // the scale in double when it is not 1). Block (b, slice of g / TSPLIT units): the slice's code is read
 // 256 units at a time and its non-zero units gathered in LDS (wave ballots), then every thread updates
-// 4 columns of each gathered unit's row (float4; d a multiple of 4, d <= 1024).
+// 4 columns of each gathered unit's row (float4; d a multiple of 4, d <= 1024). A row marked for
+// folding (fold[b] != 0, a rare event) first has every unit of the slice scaled,
+// tab = (float)((double)tab * fold[b]), by the same threads and columns that then update it.
 constexpr int TSPLIT = 4;
 __global__ __launch_bounds__(NT) void cb_table_kernel(const float *__restrict__ keep, int g, int d,
                                                       const float *__restrict__ delta, const int32_t *__restrict__ next,
                                                       int V, float lr, const double *__restrict__ scale,
-                                                      float *__restrict__ tab) {
+                                                      const double *__restrict__ fold, float *__restrict__ tab) {
     __shared__ int s_u[NT];
     __shared__ float s_s[NT];
     __shared__ int s_wc[4];
@@ -502,6 +525,15 @@ __global__ __launch_bounds__(NT) void cb_table_kernel(const float *__restrict__ 
     const int per = (g + TSPLIT - 1) / TSPLIT, ub = blockIdx.y * per, ue = min(g, ub + per);
     const int c4 = tid * 4;
     typedef float f4 __attribute__((ext_vector_type(4)));
+    const double fo = fold[b];
+    if (fo != 0.0 && c4 < d)
+        for (int u = ub; u < ue; u++) {
+            f4 *tr = reinterpret_cast<f4 *>(tb + (size_t)u * d + c4);
+            f4 t = *tr;
+#pragma unroll
+            for (int z = 0; z < 4; z++) t[z] = (float)((double)t[z] * fo);
+            *tr = t;
+        }
     f4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (c4 < d) dv = *reinterpret_cast<const f4 *>(delta + (size_t)b * d + c4);
     for (int u0 = ub; u0 < ue; u0 += NT) {
@@ -574,19 +606,16 @@ int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, co
              const float *keep, int g, float lr, double fade, double *scale, float *tab, float *err, float *part,
              int nks, float *delta, double *fold, double *nats, hipStream_t st) {
     AVA_REQUIRE(B > 0 && V > 0 && d > 0 && nks > 0, AVA_ERR_SHAPE, "cb_learn: B=%d V=%d d=%d", B, V, d);
-    cb_err_kernel<<<B, NT, 0, st>>>(logits, ldl, V, next, err, nats);
+    if (V <= 32 * NT) cb_err_kernel<32><<<B, NT, 0, st>>>(logits, ldl, V, next, err, nats, fade, scale, fold);
+    else cb_err_kernel<0><<<B, NT, 0, st>>>(logits, ldl, V, next, err, nats, fade, scale, fold);
     AVA_LAUNCHED("cb_err");
     const int kslice = ((V + nks - 1) / nks + 31) / 32 * 32;
     cb_delta_kernel<<<dim3(ceil_div(B, 64), ceil_div(d, 64), nks), NT, 0, st>>>(err, B, V, emb, d, kslice, part);
     AVA_LAUNCHED("cb_delta");
     cb_delta_sum_kernel<<<ceil_div(B * d, 256), 256, 0, st>>>(part, nks, B * d, delta);
     AVA_LAUNCHED("cb_delta_sum");
-    cb_scale_kernel<<<ceil_div(B, 256), 256, 0, st>>>(next, B, V, fade, scale, fold);
-    AVA_LAUNCHED("cb_scale");
-    cb_fold_kernel<<<B, 1024, 0, st>>>(fold, (size_t)g * d, tab);
-    AVA_LAUNCHED("cb_fold");
     AVA_REQUIRE(d % 4 == 0 && d <= 4 * NT, AVA_ERR_SHAPE, "cb_learn: d=%d (a multiple of 4, <= 1024)", d);
-    cb_table_kernel<<<dim3(B, TSPLIT), NT, 0, st>>>(keep, g, d, delta, next, V, lr, scale, tab);
+    cb_table_kernel<<<dim3(B, TSPLIT), NT, 0, st>>>(keep, g, d, delta, next, V, lr, scale, fold, tab);
     AVA_LAUNCHED("cb_table");
     return AVA_OK;
 }

@@ -482,20 +482,40 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
 }
 
 // out [row][64] = the merge of the row's chunk partials: M = max m_s, L = sum l_s e^(m_s - M),
-// o = sum o_s e^(m_s - M) / L.
+// o = sum o_s e^(m_s - M) / L, the terms added in chunk order. Lane s takes chunk s's (m, l) and
+// weight; every lane's o_s loads for 16 chunks are in flight together.
 __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int nsplit,
                                                             float *__restrict__ out) {
     const int row = blockIdx.x, c = threadIdx.x;
     const float *pr = part + (size_t)row * nsplit * 66;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pr[(size_t)s * 66]);
+    for (int s0 = 0; s0 < nsplit; s0 += 64)
+        if (s0 + c < nsplit) M = fmaxf(M, pr[(size_t)(s0 + c) * 66]);
+    M = ava::wave_max(M);
     float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < nsplit; s++) {
-        const float ms = pr[(size_t)s * 66];
-        if (ms == -INFINITY) continue;
-        const float w = expf(ms - M);
-        L = fmaf(pr[(size_t)s * 66 + 1], w, L);
-        O = fmaf(pr[(size_t)s * 66 + 2 + c], w, O);
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+        const int cnt = min(64, nsplit - s0);
+        float ms = -INFINITY, ls = 0.0f;
+        if (c < cnt) {
+            ms = pr[(size_t)(s0 + c) * 66];
+            ls = pr[(size_t)(s0 + c) * 66 + 1];
+        }
+        const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
+        for (int j0 = 0; j0 < cnt; j0 += 16) {
+            float ov[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) ov[j] = j0 + j < cnt ? pr[(size_t)(s0 + j0 + j) * 66 + 2 + c] : 0.0f;
+            AVA_ISSUE_FENCE();
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int sj = j0 + j;
+                if (sj >= cnt) break;
+                if (__shfl(ms, sj) == -INFINITY) continue;
+                const float wj = __shfl(w, sj);
+                L = fmaf(__shfl(ls, sj), wj, L);
+                O = fmaf(ov[j], wj, O);
+            }
+        }
     }
     out[(size_t)row * 64 + c] = O / L;
 }

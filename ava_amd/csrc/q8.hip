@@ -559,17 +559,19 @@ int small_wide_cols() {
 //
 // Decode shapes (m <= 512 rows) leave the tiled kernels with a few dozen workgroups. Here a workgroup
 // owns a 32 x BN output block (BN = 32 FN) and all of K; its 4 waves take the 64-byte K steps
-// kt = w, w + 4, ... each on its own: a wave stages its step (P planes x 32 rows and BN weight columns,
-// 64 bytes each) in its own double-buffered LDS with direct-to-LDS loads and waits for its own loads
-// only, so the K loop has no barrier (80 KB or less per workgroup: two fit a CU). At the end wave w
-// forms its exact plane combination A_w = sum_p acc_p 2^(7(P-1-p)) in double (an integer below 2^47);
-// the four are added in LDS (still exact) and rounded once as the tiled kernels' epilogue does: the
-// same bits as they give, for any m.
-template <int P, int FN>
+// kt = w, w + 4, ... each on its own: a wave stages its steps (P planes x 32 rows and BN weight
+// columns, 64 bytes each) in its own ring of D LDS buffers with direct-to-LDS loads, D - 1 steps ahead
+// of the one it multiplies, and waits for its own loads only, so the K loop has no barrier. At the end
+// wave w forms its exact plane combination A_w = sum_p acc_p 2^(7(P-1-p)) in double (an integer below
+// 2^47); the four are added in LDS (still exact) and rounded once as the tiled kernels' epilogue does:
+// the same bits as they give, for any m. The work is latency-bound, so the ring depth (the bytes a
+// CU keeps in flight) sets the time more than the arithmetic does.
+template <int P, int FN, int D = 2>
 struct SmallCfg {
     static constexpr int BM = 32, BN = 32 * FN, BK = 64, CPR = 4, RPI = 16;  // a 1 KB load = 16 rows
     static constexpr int ROWS = P * BM + BN, LPS = ROWS / RPI, BUF = ROWS * BK;
-    static constexpr size_t OPS = (size_t)8 * BUF;                            // 4 waves x 2 buffers
+    static_assert(D >= 2 && (D - 1) * LPS < 64, "ring depth: the loads in flight must fit vmcnt");
+    static constexpr size_t OPS = (size_t)4 * D * BUF;                        // 4 waves x D buffers
     static constexpr size_t ACC = (size_t)4 * P * FN * 16 * 64 * 4;          // int32 planes, EPI_ACC
     static constexpr size_t DBL = (size_t)4 * FN * 16 * 64 * 8;              // doubles, other epilogues
 };
@@ -693,11 +695,25 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
     }
 }
 
-template <int P, int EPI, int FN>
+// Waits until at most `ahead` steps of LPS loads each are still in flight (ahead < D, wave-uniform).
+template <int LPS, int D>
+__device__ __forceinline__ void wait_steps(int ahead) {
+    if constexpr (D > 1) {
+        if (ahead >= D - 1) {
+            wait_vm<(D - 1) * LPS>();
+            return;
+        }
+        wait_steps<LPS, D - 1>(ahead);
+    } else {
+        wait_vm<0>();
+    }
+}
+
+template <int P, int EPI, int FN, int D>
 __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
                                                        int m, int n, int ldk, const int8_t *__restrict__ qt,
                                                        const float *__restrict__ scale, EpiArgs ep) {
-    using C = SmallCfg<P, FN>;
+    using C = SmallCfg<P, FN, D>;
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, CPR = C::CPR, RPI = C::RPI, LPS = C::LPS, BUF = C::BUF;
     static_assert(C::ROWS % RPI == 0, "rows per load");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -706,7 +722,7 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
     tile_origin(tiles_m, tiles_n, tiles_m, mt, nt);  // a weight block's row blocks on one XCD
     const int m0 = mt * BM, n0 = nt * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int8_t *wbuf = smem + wave * 2 * BUF;
+    int8_t *wbuf = smem + wave * D * BUF;
 
     const int8_t *src[LPS];
 #pragma unroll
@@ -722,9 +738,12 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
             src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane % CPR) * 16;
         }
     }
-    auto issue = [&](int kt, int b) {
+    // step s of this wave is K step kt = wave + 4 s, staged in buffer s % D
+    auto issue = [&](int s) {
+        int8_t *dst = wbuf + (s % D) * BUF;
+        const int off = (wave + 4 * s) * BK;
 #pragma unroll
-        for (int i = 0; i < LPS; i++) dma16(src[i] + kt * BK, wbuf + b * BUF + i * 1024);
+        for (int i = 0; i < LPS; i++) dma16(src[i] + off, dst + i * 1024);
     };
 
     i32x16 acc[P][FN];
@@ -733,16 +752,15 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[p][j] = i32x16{};
     const int KT = ldk / BK, frow = lane & 31, fc = lane >> 5;
-    int b = 0;
-    if (wave < KT) issue(wave, 0);
-    for (int kt = wave; kt < KT; kt += 4) {
-        if (kt + 4 < KT) {
-            issue(kt + 4, b ^ 1);
-            wait_vm<LPS>();  // this step's loads are in LDS; the next step's are in flight
-        } else {
-            wait_vm<0>();
-        }
-        const int8_t *la = wbuf + b * BUF, *lb = la + P * BM * BK;
+    const int ns = wave < KT ? (KT - wave + 3) / 4 : 0;  // this wave's steps
+#pragma unroll
+    for (int s = 0; s < D - 1; s++)
+        if (s < ns) issue(s);
+    for (int s = 0; s < ns; s++) {
+        // the buffer of step s + D - 1 held step s - 1, whose fragment reads completed last iteration
+        if (s + D - 1 < ns) issue(s + D - 1);
+        wait_steps<LPS, D>(min(D - 1, ns - 1 - s));  // step s is in LDS; the later ones may be in flight
+        const int8_t *la = wbuf + (s % D) * BUF, *lb = la + P * BM * BK;
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ks++) {
             i32x4 bf[FN];
@@ -759,39 +777,65 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
                 for (int j = 0; j < FN; j++) acc[p][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[p][j], 0, 0, 0);
             }
         }
-        // the buffer is refilled two steps on: its fragment reads must have completed
+        // the buffer is refilled D - 1 steps on: its fragment reads must have completed
 #if defined(__HIP_DEVICE_COMPILE__)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #endif
-        b ^= 1;
     }
     __syncthreads();  // every wave is done with its buffers
     small_epilogue<P, EPI, FN>(acc, smem, m, n, m0, n0, xexp, scale, ep, lane, wave);
 }
 
-template <int P, int EPI, int FN>
+template <int P, int EPI, int FN, int D>
 int launch_small_fn(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt,
                     const float *scale, EpiArgs ep, hipStream_t st) {
-    using C = SmallCfg<P, FN>;
+    using C = SmallCfg<P, FN, D>;
     const int total = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
     const size_t lds = std::max(C::OPS, EPI == EPI_ACC ? C::ACC : C::DBL);
     static bool attr = false;
     if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI, FN>,
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI, FN, D>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
-    q8_small_kernel<P, EPI, FN><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+    q8_small_kernel<P, EPI, FN, D><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
     AVA_LAUNCHED("q8_gemm");
     return AVA_OK;
+}
+
+// Ring depth override (AVA_Q8_SMALL_DEPTH, tuning): 0 = by shape.
+int small_depth() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_Q8_SMALL_DEPTH");
+        v = e ? atoi(e) : 0;
+        if (v < 0) v = 0;
+    }
+    return v;
+}
+
+template <int P, int EPI, int FN>
+int launch_small_d(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                   EpiArgs ep, hipStream_t st) {
+    int d = small_depth();
+    if (d == 0) d = 2;
+    // 4 waves x d buffers within the CU's 160 KB of LDS
+    while (d > 2 && (size_t)4 * d * SmallCfg<P, FN>::BUF > 163840) d--;
+    switch (d) {
+        case 3: return launch_small_fn<P, EPI, FN, 3>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+        case 4: return launch_small_fn<P, EPI, FN, 4>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+        case 5: return launch_small_fn<P, EPI, FN, 5>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+        case 6: return launch_small_fn<P, EPI, FN, 6>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+        default: return launch_small_fn<P, EPI, FN, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    }
 }
 
 // 64-column blocks for wide products (half the activation re-reads), 32 otherwise (enough blocks).
 template <int P, int EPI>
 int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                  EpiArgs ep, hipStream_t st) {
-    if (n >= small_wide_cols()) return launch_small_fn<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    return launch_small_fn<P, EPI, 1>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    if (n >= small_wide_cols()) return launch_small_d<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    return launch_small_d<P, EPI, 1>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 // ------------------------------------------------------------------ the product, deep-ring form
