@@ -79,6 +79,7 @@ def lib():
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
         "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],
+        "ava_model_decode_step": [vp, C.POINTER(State), vp, i32, i32, vp, vp, i32, vp, vp, vp],
     }
     for name, args in sig.items():
         fn = getattr(L, name, None)

@@ -26,6 +26,7 @@ constexpr float NORM_EPS = 1e-5f;  // gpu/model.rs:36
 template <int P, int NV>
 __device__ __forceinline__ void put_planes(const f32x4 (&x)[NV], int lane, int k, int ldq, size_t m, size_t row,
                                            int8_t *__restrict__ xq, int32_t *__restrict__ xexp) {
+    if (!xq) return;  // the row's planes are written elsewhere
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; i++)
@@ -780,6 +781,89 @@ __global__ __launch_bounds__(1024) void rms_gate_kernel(const float *__restrict_
     }
 }
 
+// Few rows: workgroup (8 rows, 16 gate columns), so a workgroup reads 64 KB of W instead of all of it.
+// Every workgroup norms its 8 rows (two per wave, as rms_planes_kernel) into LDS; those of column group
+// 0 also write the planes. Thread (row half, K eighth, column) then forms 4 rows' partial sums over its
+// eighth with all its weight loads in flight, and the eighths add in order: the same operations in the
+// same order as rms_gate_kernel, so the same bits.
+constexpr int GCR = 8, GCC = 16;
+template <int P>
+__global__ __launch_bounds__(256) void rms_gate_cols_kernel(const float *__restrict__ x, int n, int d,
+                                                            const float *__restrict__ gain, int8_t *__restrict__ xq,
+                                                            int32_t *__restrict__ xexp, int ldq,
+                                                            const float *__restrict__ w, int nc, float *__restrict__ g) {
+    // the K eighths of a row sit 4 floats apart in banks, so a wave's four eighths read without conflict
+    __shared__ __attribute__((aligned(16))) float sh[GCR][1024 + 4 * GKS];
+    auto at = [](int k) { return k + (k >> 7) * 4; };
+    __shared__ float sacc[GKS][GCR][GCC];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * GCR, c0 = blockIdx.y * GCC, nq = d >> 2;
+    {
+        f32x4 v[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int row = r0 + 2 * wave + h;
+            const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)min(row, n - 1) * d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = i * 64 + lane;
+                v[h][i] = c < nq && row < n ? xr[c] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+        AVA_ISSUE_FENCE();
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int rl = 2 * wave + h, row = r0 + rl;
+            if (row < n)
+                row_rms_planes<P, 4>(v[h], lane, d, gain, (size_t)n, (size_t)row, blockIdx.y == 0 ? xq : nullptr,
+                                     xexp, ldq, nullptr);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = i * 64 + lane;
+                if (c < nq) *reinterpret_cast<f32x4 *>(&sh[rl][at(4 * c)]) = v[h][i];
+            }
+        }
+    }
+    __syncthreads();
+    const int cl = tid & (GCC - 1), ks = (tid >> 4) & (GKS - 1), rh = tid >> 7, c = c0 + cl;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < nc) {
+        const int kb = ks * (d / GKS), ke = kb + d / GKS;  // (ke - kb) % 32 == 0 (rms_gate_fits)
+        for (int k0 = kb; k0 < ke; k0 += 32) {
+            float wv[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++) wv[j] = w[(size_t)(k0 + j) * nc + c];
+            AVA_ISSUE_FENCE();
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                // the 4 rows' 16 inputs as float4 LDS reads, all issued before the first fma
+                f32x4 hv[4][4];
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        hv[r][q] = *reinterpret_cast<const f32x4 *>(&sh[rh * 4 + r][at(k0 + 16 * h + 4 * q)]);
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[r] = fmaf(hv[r][j >> 2][j & 3], wv[16 * h + j], acc[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) sacc[ks][rh * 4 + r][cl] = acc[r];
+    __syncthreads();
+    if (tid < GCR * GCC) {
+        const int r = tid / GCC, cc = tid % GCC, row = r0 + r;
+        if (c0 + cc < nc && row < n) {
+            float v = sacc[0][r][cc];
+#pragma unroll
+            for (int q = 1; q < GKS; q++) v += sacc[q][r][cc];
+            g[(size_t)row * nc + c0 + cc] = v;
+        }
+    }
+}
+
 bool rms_gate_fits(int n, int d, int nc) {
     return ceil_div(n, GR) < 64 && d <= 1024 && d % (GKS * 32) == 0 && nc <= 128;
 }
@@ -788,11 +872,12 @@ int rms_gate(const float *x, int n, int d, const float *gain, int planes, int8_t
              const float *w, int nc, float *g, hipStream_t st) {
     AVA_REQUIRE(rms_gate_fits(n, d, nc) && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE, "rms_gate: n=%d d=%d nc=%d", n,
                 d, nc);
-    // one row per workgroup while that still fills the chip with a few rounds, else four
-    const bool one = n <= 1024;
-    const dim3 grid(ceil_div(n, one ? 1 : GRR)), block(1024);
+    // (8 rows, 16 columns) per workgroup while that still fills the chip with a few rounds, else four
+    // rows and all columns
+    const bool cols = n <= 1024;
+    const dim3 grid(ceil_div(n, GRR)), block(1024), cgrid(ceil_div(n, GCR), ceil_div(nc, GCC));
 #define AVA_RG(P_)                                                                                            \
-    if (one) rms_gate_kernel<P_, 1><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);          \
+    if (cols) rms_gate_cols_kernel<P_><<<cgrid, 256, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g);        \
     else rms_gate_kernel<P_, GRR><<<grid, block, 0, st>>>(x, n, d, gain, xq, xexp, ldq, w, nc, g)
     if (planes == 1) AVA_RG(1);
     else if (planes == 2) AVA_RG(2);

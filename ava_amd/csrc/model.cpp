@@ -97,6 +97,10 @@ struct ava_model {
     bool timing = false;
     Timer timer;
     hipStream_t last_stream = nullptr;
+    // ava_model_decode_step: the stream the previous token's table step runs on, and the events that
+    // fork it from and join it back to the caller's stream (made at build when the model has a table)
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -202,6 +206,9 @@ int build(ava_model *m, const ava_params *prm) {
             if (int e = upload(m, &m->cb_w, prm->cb_w, (size_t)c.cb_units * d)) return e;
         m->cb_k = c.cb_units / 32;  // gpu/v51b.rs:47 (CB_SPARSITY)
         m->cb_fade = c.cb_half > 0.0f ? exp2(-1.0 / (double)c.cb_half) : 1.0;
+        AVA_HIP(hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking));  // default priority
+        AVA_HIP(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
+        AVA_HIP(hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming));
     }
     m->blocks.resize(c.layers);
     for (int i = 0; i < c.layers; i++) {
@@ -364,7 +371,10 @@ int collect(ava_model *m) {
     return AVA_OK;
 }
 
-int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float *logits, hipStream_t st) {
+// join (nullable): an event the forward waits for before the final norm and the cerebellum (which
+// read and overwrite the code, the table and its scale).
+int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float *logits, hipStream_t st,
+            hipEvent_t join = nullptr) {
     const ava_config &c = m->cfg;
     const int d = c.d, nh = d / c.head_size, r = c.gate_rank, H = c.hidden, de = c.eng_dim, L = c.layers;
     const int P = c.planes, N = B * T, ldd = ava::q8_ldk(d), ldh = ava::q8_ldk(H);
@@ -466,6 +476,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         s->eng_len += T;
         if (s->eng_len_dev) AVA_RUN("store_advance", ava::engram_advance(s->eng_len_dev, T, s->eng_cap, st));
     }
+    if (join) AVA_HIP(hipStreamWaitEvent(st, join, 0));
     if (logits) {
         if (!final_ready)
             AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, m->final_norm, P, m->xq, m->xexp, ldd, cb ? m->h : nullptr,
@@ -481,6 +492,26 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         }
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &m->head.w, ava::Q8_STORE, logits, c.vocab, nullptr, st));
     }
+    return AVA_OK;
+}
+
+constexpr int CB_NKS = 32;  // the learning step's delta product: K slices of vocab / 32 each
+
+// The learning step's scratch for B streams (kept; regrown only while the scratch is not frozen).
+int ensure_cb(ava_model *m, int B) {
+    const ava_config &c = m->cfg;
+    if (B <= m->cb_rows) return AVA_OK;
+    AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "cb_learn: %d streams need more scratch, and the model's scratch is "
+                "frozen (a captured graph uses it)", B);
+    for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
+    m->cb_err = m->cb_part = m->cb_delta = nullptr;
+    m->cb_fold = nullptr;
+    m->cb_rows = 0;
+    AVA_HIP(hipMalloc(&m->cb_err, (size_t)B * c.vocab * sizeof(float)));
+    AVA_HIP(hipMalloc(&m->cb_part, (size_t)CB_NKS * B * c.d * sizeof(float)));
+    AVA_HIP(hipMalloc(&m->cb_delta, (size_t)B * c.d * sizeof(float)));
+    AVA_HIP(hipMalloc(&m->cb_fold, (size_t)B * sizeof(double)));
+    m->cb_rows = B;
     return AVA_OK;
 }
 
@@ -522,6 +553,9 @@ extern "C" void ava_model_free(ava_model *m) {
     for (hipEvent_t e : m->timer.pool) (void)hipEventDestroy(e);
     for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
     (void)hipFree(m->att_part);
+    if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
+    if (m->ev_join) (void)hipEventDestroy(m->ev_join);
+    if (m->side) (void)hipStreamDestroy(m->side);
     delete m;
 }
 
@@ -539,18 +573,7 @@ extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logi
     AVA_REQUIRE(c.cb_units > 0 && st->cb_tab && st->cb_scale && st->cb_code, AVA_ERR_ARG,
                 "cb_learn: the model has no cerebellum head or the state no online table");
     AVA_REQUIRE(B > 0 && ld_logits >= c.vocab, AVA_ERR_SHAPE, "cb_learn: B=%d ld=%d", B, ld_logits);
-    const int nks = 32;  // the delta product's K slices (vocab / 32 each)
-    if (B > m->cb_rows) {
-        AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "cb_learn: %d streams need more scratch, and the model's scratch is "
-                    "frozen (a captured graph uses it)", B);
-        for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
-        m->cb_rows = 0;
-        AVA_HIP(hipMalloc(&m->cb_err, (size_t)B * c.vocab * sizeof(float)));
-        AVA_HIP(hipMalloc(&m->cb_part, (size_t)nks * B * c.d * sizeof(float)));
-        AVA_HIP(hipMalloc(&m->cb_delta, (size_t)B * c.d * sizeof(float)));
-        AVA_HIP(hipMalloc(&m->cb_fold, (size_t)B * sizeof(double)));
-        m->cb_rows = B;
-    }
+    if (int e = ensure_cb(m, B)) return e;
     hipStream_t sst = (hipStream_t)stream;
     if (m->timing && m->last_stream != sst) {
         if (int e = collect(m)) return e;
@@ -560,10 +583,41 @@ extern "C" int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logi
     {
         hipStream_t st = sst;  // the stream AVA_RUN times on
         AVA_RUN("cb_learn", ava::cb_learn(logits, ld_logits, c.vocab, next, B, m->tok_emb, c.d, as->cb_code, c.cb_units,
-                                          c.cb_lr, m->cb_fade, as->cb_scale, as->cb_tab, m->cb_err, m->cb_part, nks,
+                                          c.cb_lr, m->cb_fade, as->cb_scale, as->cb_tab, m->cb_err, m->cb_part, CB_NKS,
                                           m->cb_delta, m->cb_fold, nats, st));
     }
     return AVA_OK;
+}
+
+extern "C" int ava_model_decode_step(ava_model *m, ava_state *st, const int32_t *ids, int B, int T, float *logits,
+                                     const float *prev_logits, int ld_prev, const int32_t *prev_next, double *prev_nats,
+                                     ava_stream stream) {
+    AVA_REQUIRE(m && st && ids, AVA_ERR_ARG, "decode_step: NULL argument");
+    AVA_REQUIRE(B > 0 && T > 0 && (long)B * T <= (1L << 24), AVA_ERR_SHAPE, "decode_step: B=%d T=%d", B, T);
+    hipStream_t sst = (hipStream_t)stream;
+    if (!prev_logits) return forward(m, st, ids, B, T, logits, sst);
+    const ava_config &c = m->cfg;
+    AVA_REQUIRE(prev_next && c.cb_units > 0 && st->cb_tab && st->cb_scale && st->cb_code && m->side, AVA_ERR_ARG,
+                "decode_step: a table step needs the model's cerebellum head, the state's table and prev_next");
+    AVA_REQUIRE(ld_prev >= c.vocab, AVA_ERR_SHAPE, "decode_step: ld_prev=%d", ld_prev);
+    AVA_REQUIRE(!logits || logits != prev_logits, AVA_ERR_ARG, "decode_step: logits and prev_logits are one buffer");
+    if (m->timing) {
+        // the launch timer follows one stream: the two parts run one after the other
+        if (int e = ava_model_cb_learn(m, st, prev_logits, ld_prev, prev_next, B, prev_nats, stream)) return e;
+        return ava_model_forward(m, st, ids, B, T, logits, stream);
+    }
+    if (int e = ensure_cb(m, B)) return e;
+    m->last_stream = sst;
+    // fork: the table step of the previous token on the side stream, after everything before it on sst
+    AVA_HIP(hipEventRecord(m->ev_fork, sst));
+    AVA_HIP(hipStreamWaitEvent(m->side, m->ev_fork, 0));
+    if (int e = ava::cb_learn(prev_logits, ld_prev, c.vocab, prev_next, B, m->tok_emb, c.d, st->cb_code, c.cb_units,
+                              c.cb_lr, m->cb_fade, st->cb_scale, st->cb_tab, m->cb_err, m->cb_part, CB_NKS, m->cb_delta,
+                              m->cb_fold, prev_nats, m->side))
+        return e;
+    AVA_HIP(hipEventRecord(m->ev_join, m->side));
+    // the blocks run meanwhile; the join comes before the final norm and the cerebellum
+    return forward(m, st, ids, B, T, logits, sst, m->ev_join);
 }
 
 extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }

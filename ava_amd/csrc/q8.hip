@@ -558,28 +558,31 @@ int small_wide_cols() {
 // ------------------------------------------------------------------ the product for few rows
 //
 // Decode shapes (m <= 512 rows) leave the tiled kernels with a few dozen workgroups. Here a workgroup
-// owns a 32 x BN output block (BN = 32 FN) and all of K; its 4 waves take the 64-byte K steps
-// kt = w, w + 4, ... each on its own: a wave stages its steps (P planes x 32 rows and BN weight
+// owns a 32 x BN output block (BN = 32 FN) and all of K; its NW waves take the 64-byte K steps
+// kt = w, w + NW, ... each on its own: a wave stages its steps (P planes x 32 rows and BN weight
 // columns, 64 bytes each) in its own ring of D LDS buffers with direct-to-LDS loads, D - 1 steps ahead
 // of the one it multiplies, and waits for its own loads only, so the K loop has no barrier. At the end
 // wave w forms its exact plane combination A_w = sum_p acc_p 2^(7(P-1-p)) in double (an integer below
-// 2^47); the four are added in LDS (still exact) and rounded once as the tiled kernels' epilogue does:
-// the same bits as they give, for any m. The work is latency-bound, so the ring depth (the bytes a
-// CU keeps in flight) sets the time more than the arithmetic does.
-template <int P, int FN, int D = 2>
+// 2^47); the NW partials are added in LDS (still exact, so in any order) and rounded once as the tiled
+// kernels' epilogue does: the same bits as they give, for any m. The staging rate per CU bounds the
+// time, so a CU wants 8 waves loading: two 4-wave workgroups when the grid has enough blocks, else
+// one of 8 waves (5-7% faster than 4 there).
+template <int P, int FN, int D = 2, int NW = 4>
 struct SmallCfg {
     static constexpr int BM = 32, BN = 32 * FN, BK = 64, CPR = 4, RPI = 16;  // a 1 KB load = 16 rows
     static constexpr int ROWS = P * BM + BN, LPS = ROWS / RPI, BUF = ROWS * BK;
     static_assert(D >= 2 && (D - 1) * LPS < 64, "ring depth: the loads in flight must fit vmcnt");
-    static constexpr size_t OPS = (size_t)4 * D * BUF;                        // 4 waves x D buffers
-    static constexpr size_t ACC = (size_t)4 * P * FN * 16 * 64 * 4;          // int32 planes, EPI_ACC
-    static constexpr size_t DBL = (size_t)4 * FN * 16 * 64 * 8;              // doubles, other epilogues
+    static_assert(NW == 4 || NW == 8, "waves per workgroup");
+    static constexpr size_t OPS = (size_t)NW * D * BUF;                       // NW waves x D buffers
+    static constexpr size_t ACC = (size_t)NW * P * FN * 16 * 64 * 4;         // int32 planes, EPI_ACC
+    static constexpr size_t DBL = (size_t)NW * FN * 16 * 64 * 8;             // doubles, other epilogues
 };
 
 // The few-rows products' epilogue: wave w's P-plane accumulators of the 32 x 32 FN block combine
-// exactly in double; the four waves' partials add in LDS (smem, 32 FN KB; int32 planes for EPI_ACC);
-// then one rounding and the epilogue kind, as the tiled kernels' epilogue.
-template <int P, int EPI, int FN>
+// exactly in double; the NW waves' partials add in LDS (smem, 8 NW FN KB; int32 planes for EPI_ACC);
+// then one rounding and the epilogue kind, as the tiled kernels' epilogue. Wave w finishes the
+// accumulator rows r = w + NW q.
+template <int P, int EPI, int FN, int NW>
 __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_t *smem, int m, int n, int m0, int n0,
                                                const int32_t *__restrict__ xexp, const float *__restrict__ scale,
                                                const EpiArgs &ep, int lane, int wave) {
@@ -597,14 +600,14 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
         for (int j = 0; j < FN; j++) {
             const int col = n0 + j * 32 + (lane & 31);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+            for (int q = 0; q < 16 / NW; q++) {
+                const int r = wave + NW * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
                 if (row < m && col < n)
 #pragma unroll
                     for (int p = 0; p < P; p++) {
                         int v = 0;
 #pragma unroll
-                        for (int w = 0; w < 4; w++) v += si[(((w * P + p) * FN + j) * 16 + r) * 64 + lane];
+                        for (int w = 0; w < NW; w++) v += si[(((w * P + p) * FN + j) * 16 + r) * 64 + lane];
                         reinterpret_cast<int32_t *>(ep.y)[((size_t)p * m + row) * n + col] = v;
                     }
             }
@@ -635,10 +638,10 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
             const ava::LifEpi &L = ep.lif;
             const float bt = L.ps[col], th0 = L.ps[n + col], rho = L.ps[2 * n + col], gain = L.ps[3 * n + col];
             const float cf = ep.colv ? ep.colv[col] : 1.0f;
-            float sv[4], ss[4], sa[4];
+            float sv[16 / NW], ss[16 / NW], sa[16 / NW];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = wave + 4 * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
+            for (int q = 0; q < 16 / NW; q++) {
+                const int r = wave + NW * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
                 const size_t o = (size_t)row * n + col;
                 sv[q] = L.v[o];
                 ss[q] = L.s[o];
@@ -646,11 +649,13 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
             }
             AVA_ISSUE_FENCE();
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+            for (int q = 0; q < 16 / NW; q++) {
+                const int r = wave + NW * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
                 if (row >= m) continue;
                 const int e = (j * 16 + r) * 64 + lane, ws = FN * 16 * 64;
-                const double A = ((sd[e] + sd[ws + e]) + sd[2 * ws + e]) + sd[3 * ws + e];
+                double A = sd[e];
+#pragma unroll
+                for (int w = 1; w < NW; w++) A += sd[w * ws + e];
                 const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
                 float v = ldexpf((float)A, ex) * sc;
                 if (ep.colv) v = v * cf;
@@ -671,21 +676,23 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
             }
             continue;
         }
-        float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (EPI == EPI_ADD) {  // the 4 rows' loads all in flight before any add
+        float prev[16 / NW] = {};
+        if (EPI == EPI_ADD) {  // the rows' loads all in flight before any add
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = wave + 4 * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
+            for (int q = 0; q < 16 / NW; q++) {
+                const int r = wave + NW * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
                 prev[q] = ybase[(size_t)row * ep.ldy + col];
             }
             AVA_ISSUE_FENCE();
         }
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int r = wave + 4 * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
+        for (int q = 0; q < 16 / NW; q++) {
+            const int r = wave + NW * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
             if (row >= m) continue;
             const int e = (j * 16 + r) * 64 + lane, ws = FN * 16 * 64;
-            const double A = ((sd[e] + sd[ws + e]) + sd[2 * ws + e]) + sd[3 * ws + e];
+            double A = sd[e];
+#pragma unroll
+            for (int w = 1; w < NW; w++) A += sd[w * ws + e];
             const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
             float v = ldexpf((float)A, ex) * sc;
             if (EPI == EPI_MUL) v = v * cv;
@@ -709,11 +716,11 @@ __device__ __forceinline__ void wait_steps(int ahead) {
     }
 }
 
-template <int P, int EPI, int FN, int D>
-__global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
+template <int P, int EPI, int FN, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void q8_small_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
                                                        int m, int n, int ldk, const int8_t *__restrict__ qt,
                                                        const float *__restrict__ scale, EpiArgs ep) {
-    using C = SmallCfg<P, FN, D>;
+    using C = SmallCfg<P, FN, D, NW>;
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, CPR = C::CPR, RPI = C::RPI, LPS = C::LPS, BUF = C::BUF;
     static_assert(C::ROWS % RPI == 0, "rows per load");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -738,10 +745,10 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
             src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane % CPR) * 16;
         }
     }
-    // step s of this wave is K step kt = wave + 4 s, staged in buffer s % D
+    // step s of this wave is K step kt = wave + NW s, staged in buffer s % D
     auto issue = [&](int s) {
         int8_t *dst = wbuf + (s % D) * BUF;
-        const int off = (wave + 4 * s) * BK;
+        const int off = (wave + NW * s) * BK;
 #pragma unroll
         for (int i = 0; i < LPS; i++) dma16(src[i] + off, dst + i * 1024);
     };
@@ -752,7 +759,7 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[p][j] = i32x16{};
     const int KT = ldk / BK, frow = lane & 31, fc = lane >> 5;
-    const int ns = wave < KT ? (KT - wave + 3) / 4 : 0;  // this wave's steps
+    const int ns = wave < KT ? (KT - wave + NW - 1) / NW : 0;  // this wave's steps
 #pragma unroll
     for (int s = 0; s < D - 1; s++)
         if (s < ns) issue(s);
@@ -783,59 +790,58 @@ __global__ __launch_bounds__(256) void q8_small_kernel(const int8_t *__restrict_
 #endif
     }
     __syncthreads();  // every wave is done with its buffers
-    small_epilogue<P, EPI, FN>(acc, smem, m, n, m0, n0, xexp, scale, ep, lane, wave);
+    small_epilogue<P, EPI, FN, NW>(acc, smem, m, n, m0, n0, xexp, scale, ep, lane, wave);
 }
 
-template <int P, int EPI, int FN, int D>
+template <int P, int EPI, int FN, int D, int NW>
 int launch_small_fn(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt,
                     const float *scale, EpiArgs ep, hipStream_t st) {
-    using C = SmallCfg<P, FN, D>;
+    using C = SmallCfg<P, FN, D, NW>;
     const int total = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
     const size_t lds = std::max(C::OPS, EPI == EPI_ACC ? C::ACC : C::DBL);
     static bool attr = false;
     if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI, FN, D>,
+        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI, FN, D, NW>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
-    q8_small_kernel<P, EPI, FN, D><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+    q8_small_kernel<P, EPI, FN, D, NW><<<dim3(total), dim3(64 * NW), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
     AVA_LAUNCHED("q8_gemm");
     return AVA_OK;
 }
 
-// Ring depth override (AVA_Q8_SMALL_DEPTH, tuning): 0 = by shape.
-int small_depth() {
+// Waves per workgroup override (AVA_Q8_SMALL_WAVES = 4 or 8, tuning): 0 = by grid size.
+int small_waves() {
     static int v = -1;
     if (v < 0) {
-        const char *e = getenv("AVA_Q8_SMALL_DEPTH");
+        const char *e = getenv("AVA_Q8_SMALL_WAVES");
         v = e ? atoi(e) : 0;
-        if (v < 0) v = 0;
+        if (v != 4 && v != 8) v = 0;
     }
     return v;
 }
 
+// 8 waves per workgroup when the grid gives a CU one workgroup or fewer, else 4 (two per CU); single
+// planes (spikes) stage so little per step that 4 waves do better.
 template <int P, int EPI, int FN>
-int launch_small_d(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+int launch_small_w(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                    EpiArgs ep, hipStream_t st) {
-    int d = small_depth();
-    if (d == 0) d = 2;
-    // 4 waves x d buffers within the CU's 160 KB of LDS
-    while (d > 2 && (size_t)4 * d * SmallCfg<P, FN>::BUF > 163840) d--;
-    switch (d) {
-        case 3: return launch_small_fn<P, EPI, FN, 3>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-        case 4: return launch_small_fn<P, EPI, FN, 4>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-        case 5: return launch_small_fn<P, EPI, FN, 5>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-        case 6: return launch_small_fn<P, EPI, FN, 6>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-        default: return launch_small_fn<P, EPI, FN, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    }
+    using C8 = SmallCfg<P, FN, 2, 8>;
+    constexpr bool fits8 = P > 1 && std::max(C8::OPS, EPI == EPI_ACC ? C8::ACC : C8::DBL) <= 163840;  // LDS per CU
+    int nw = small_waves();
+    if (nw == 0) nw = ((m + 31) / 32) * ((n + 32 * FN - 1) / (32 * FN)) <= 256 ? 8 : 4;
+    if constexpr (fits8)
+        if (nw == 8) return launch_small_fn<P, EPI, FN, 2, 8>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    return launch_small_fn<P, EPI, FN, 2, 4>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 // 64-column blocks for wide products (half the activation re-reads), 32 otherwise (enough blocks).
+// Wider blocks (128, 160 columns: one workgroup per CU) and deeper rings measured no faster.
 template <int P, int EPI>
 int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                  EpiArgs ep, hipStream_t st) {
-    if (n >= small_wide_cols()) return launch_small_d<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    return launch_small_d<P, EPI, 1>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    if (n >= small_wide_cols()) return launch_small_w<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    return launch_small_w<P, EPI, 1>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 // ------------------------------------------------------------------ the product, deep-ring form

@@ -6,6 +6,7 @@ gpu/state.rs), over ava_model_* of include/ava.h.
     logits = m.forward_with_state(ids, st)   state.rs:684-865 (ids [B, T] int32 on the GPU)
     logits = m.forward(ids)             model.rs:1171: a fresh state per call
     nats = m.cb_learn(logits, next, st) Model::cb_learn (gpu/v51b.rs:600-604, gpu/fast4/cb.rs:25-84)
+    m.decode_step(ids, st, logits, prev_logits, prev_next)   cb_learn(prev) then forward, overlapped
 
 `params` is a dict of float32 numpy arrays keyed as ava_amd.synth (the reference's VarMap names).
 The library raises AvaError on any failure; nothing falls back to another path.
@@ -130,6 +131,58 @@ class Model:
               "ava_model_forward")
         st.eng_len = cst.eng_len
         return logits
+
+    def decode_step(self, ids: torch.Tensor, st: State, logits: torch.Tensor, prev_logits: torch.Tensor | None = None,
+                    prev_next: torch.Tensor | None = None, prev_nats: torch.Tensor | None = None):
+        """One decode step with the previous token's table step overlapped (ava_model_decode_step): the
+        same results as cb_learn(prev_logits, prev_next) then forward_with_state(ids). Alternate two
+        logits and two next buffers between steps; prev_* None: no table step (the first token)."""
+        if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
+            raise ValueError("ids: a contiguous [B, T] int32 GPU tensor is required")
+        B, T = ids.shape
+        V = self.cfg["vocab"]
+        if not (logits.is_cuda and logits.dtype == torch.float32 and logits.is_contiguous()
+                and logits.numel() >= B * T * V):
+            raise ValueError("logits: a contiguous f32 GPU tensor of B*T*vocab entries is required")
+        pl = pn = pz = None
+        ld = 0
+        if prev_logits is not None:
+            if prev_next is None or st.cb_tab is None:
+                raise ValueError("decode_step: a table step needs prev_next and a state with a table")
+            if not (prev_logits.is_cuda and prev_logits.dtype == torch.float32 and prev_logits.dim() == 2
+                    and prev_logits.shape[0] == B and prev_logits.stride(1) == 1):
+                raise ValueError("prev_logits: [B, vocab] f32 GPU rows with unit column stride are required")
+            if prev_logits.data_ptr() == logits.data_ptr():
+                raise ValueError("decode_step: logits and prev_logits must be different buffers")
+            if not (prev_next.is_cuda and prev_next.dtype == torch.int32 and prev_next.is_contiguous()
+                    and prev_next.numel() == B):
+                raise ValueError("prev_next: a contiguous [B] int32 GPU tensor is required")
+            if prev_nats is not None and not (prev_nats.is_cuda and prev_nats.dtype == torch.float64
+                                              and prev_nats.numel() >= B and prev_nats.is_contiguous()):
+                raise ValueError("prev_nats: a contiguous f64 GPU tensor of >= B entries is required")
+            pl, pn = C.c_void_p(prev_logits.data_ptr()), C.c_void_p(prev_next.data_ptr())
+            pz = C.c_void_p(prev_nats.data_ptr()) if prev_nats is not None else None
+            ld = prev_logits.stride(0)
+        cst = st.c()
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check(lib().ava_model_decode_step(self.h, C.byref(cst), C.c_void_p(ids.data_ptr()), B, T,
+                                          C.c_void_p(logits.data_ptr()), pl, ld, pn, pz, stream),
+              "ava_model_decode_step")
+        st.eng_len = cst.eng_len
+        return logits
+
+    def capture_decode_step(self, st: State, ids: torch.Tensor, logits: torch.Tensor, prev_logits: torch.Tensor,
+                            prev_next: torch.Tensor, prev_nats: torch.Tensor | None = None) -> "DecodeGraph":
+        """decode_step over fixed buffers as a HIP graph (both streams' work; see capture_decode)."""
+        if st.eng_len_dev is None:
+            raise ValueError("capture_decode_step: the state needs device_len=True")
+        check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")
+        g = torch.cuda.CUDAGraph()
+        n0 = st.eng_len
+        with torch.cuda.graph(g):
+            self.decode_step(ids, st, logits, prev_logits, prev_next, prev_nats)
+        st.eng_len = n0
+        return DecodeGraph(g, st, ids.shape[1])
 
     def cb_learn(self, logits: torch.Tensor, nxt: torch.Tensor, st: State, nats: torch.Tensor | None = None):
         """One online step of every stream's table (Model::cb_learn): logits [B, >= vocab] f32 GPU rows of

@@ -405,9 +405,8 @@ class Decode:
     (12,288 granule units, 384 kept, per-stream online table with a 256-token half-life). Each stream's
     state (membranes, thresholds, fast weights and momentum, the engram store) comes from a
     teacher-forced prefill of `prefill` random tokens (32,768 as config[4]; untimed, in pieces of
-    `piece` tokens). A step is one token per stream: the forward (T = 1) to logits [256, 8192], then
-    the online table's learning step on each stream's next token (random ids: a teacher-forced
-    continuation)."""
+    `piece` tokens). A step is one token per stream: the forward (T = 1) to logits [256, 8192] and
+    one online table step on each stream's next token (random ids: a teacher-forced continuation)."""
 
     name = "decode"
     kernel = "attend_split"
@@ -430,13 +429,21 @@ class Decode:
         V = c["vocab"]
         self.toks = torch.randint(0, V, (steps_cap + 1, B, 1), device="cuda", generator=g, dtype=torch.int32)
         self.nexts = self.toks[1:, :, 0].contiguous()
-        self.logits = torch.empty((B, V), device="cuda")
+        # the step's inputs live in fixed buffers so that it can be captured and replayed; the logits
+        # and next buffers alternate between steps, as the overlapped step learns from the previous
+        # step's pair while this step's forward writes the other
+        self.logits2 = [torch.empty((B, V), device="cuda") for _ in range(2)]
+        self.nxt2 = [torch.empty(B, dtype=torch.int32, device="cuda") for _ in range(2)]
+        self.logits, self.nxt_buf = self.logits2[0], self.nxt2[0]
         self.nats = torch.empty(B, dtype=torch.float64, device="cuda")
-        # the step's inputs live in fixed buffers so that it can be captured once and replayed
         self.ids_buf = torch.empty((B, 1), dtype=torch.int32, device="cuda")
-        self.nxt_buf = torch.empty(B, dtype=torch.int32, device="cuda")
         self.use_graph = os.environ.get("AVA_DECODE_GRAPH", "1") != "0"
+        # AVA_DECODE_OVERLAP=1: overlapped steps (Model.decode_step), step t running the table step of
+        # token t - 1 beside the forward of token t. Off by default: on this box the two streams'
+        # kernels land on one hardware queue and run in turn (measured 1% slower than in order).
+        self.overlap = os.environ.get("AVA_DECODE_OVERLAP", "0") != "0"
         self.graph = None
+        self.graphs = None
         self.t = 0
         self.steps_cap = steps_cap
         t0 = time.perf_counter()
@@ -453,9 +460,9 @@ class Decode:
         nh = d // c["head_size"]
         self.config = {"workload": "stateful decode config[4]", "streams": B, "prefill": prefill, "d": d,
                        "blocks": L, "hidden": H, "kwta_k": c["kwta_k"], "heads": nh, "vocab": V,
-                       "engram_block": c["eng_block"], "engram_store": "f32", "cb_units": c["cb_units"],
-                       "cb_half": c["cb_half"], "momentum": c["momentum"], "act_planes": planes,
-                       "hip_graph": self.use_graph}
+                       "engram_block": c["eng_block"], "engram_store": "fp16" if c.get("eng_half") else "f32",
+                       "cb_units": c["cb_units"], "cb_half": c["cb_half"], "momentum": c["momentum"],
+                       "act_planes": planes, "hip_graph": self.use_graph, "overlapped_table_step": self.overlap}
         self.dtype = "i8"
         self.breakdown = None
 
@@ -480,6 +487,8 @@ class Decode:
     def step(self, stream, ev=None, eager=False):
         if self.t >= self.steps_cap:
             raise RuntimeError("decode: more steps than the store was sized for")
+        if self.overlap:
+            return self.step_overlapped(eager)
         self.ids_buf.copy_(self.toks[self.t])
         self.nxt_buf.copy_(self.nexts[self.t])
         if self.graph is not None and not eager:
@@ -490,6 +499,24 @@ class Decode:
             if self.use_graph and self.graph is None:
                 # captured after the first eager step (scratch allocated): every later step replays it
                 self.graph = self.model.capture_decode(self.st, self.ids_buf, self.logits, self.nxt_buf, self.nats)
+        self.t += 1
+
+    def step_overlapped(self, eager):
+        """Token t's forward with token t - 1's table step beside it (none at t = 0). Both graphs are
+        captured after two eager steps (the second allocates the table step's scratch)."""
+        t, m = self.t, self.model
+        cur, prev = t % 2, (t - 1) % 2
+        self.ids_buf.copy_(self.toks[t])
+        self.nxt2[cur].copy_(self.nexts[t])
+        if self.graphs is not None and not eager:
+            self.graphs[prev].replay()  # graph p learns from buffer p and writes buffer 1 - p
+        elif t == 0:
+            m.decode_step(self.ids_buf, self.st, self.logits2[cur])
+        else:
+            m.decode_step(self.ids_buf, self.st, self.logits2[cur], self.logits2[prev], self.nxt2[prev], self.nats)
+            if self.use_graph and self.graphs is None:
+                self.graphs = [m.capture_decode_step(self.st, self.ids_buf, self.logits2[1 - p], self.logits2[p],
+                                                     self.nxt2[p], self.nats) for p in (0, 1)]
         self.t += 1
 
     prof_steps = 8

@@ -225,6 +225,19 @@ int ava_model_forward(ava_model *m, ava_state *st, const int32_t *ids, int B, in
 int ava_model_cb_learn(ava_model *m, ava_state *st, const float *logits, int ld_logits, const int32_t *next, int B,
                        double *nats, ava_stream stream);
 
+/* One decode step with the previous token's table step overlapped (no counterpart in the reference,
+ * whose talking loop runs Model::cb_learn after each forward: gpu/v51b.rs:590-611). With prev_logits
+ * NULL this is ava_model_forward. Otherwise the learning step of ava_model_cb_learn for
+ * (prev_logits [B] rows of ld_prev floats, prev_next [B], prev_nats nullable) runs on a second stream
+ * of the model's while this step's blocks run on `stream`, and the forward waits for it before its
+ * final norm and cerebellum, which read and overwrite the code, the table and its scale. The results
+ * are those of ava_model_cb_learn(prev) followed by ava_model_forward(ids), bit for bit. The caller
+ * keeps prev_logits and prev_next unchanged until the step completes on `stream` (alternate two
+ * buffers for logits and next), and logits may not be prev_logits. Capturable in a HIP graph. */
+int ava_model_decode_step(ava_model *m, ava_state *st, const int32_t *ids, int B, int T, float *logits,
+                          const float *prev_logits, int ld_prev, const int32_t *prev_next, double *prev_nats,
+                          ava_stream stream);
+
 /* Bytes of scratch the model holds after forwards of up to B*T rows. */
 size_t ava_model_scratch_bytes(const ava_model *m);
 
