@@ -28,45 +28,57 @@ __device__ __forceinline__ float float_of_key(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Block-wide reductions for 256 threads (4 waves); every thread gets the result, made wave-uniform
+// Block-wide reductions; every thread gets the result, made wave-uniform
 // (readfirstlane) so control flow on it stays scalar. `red` holds 4 slots; the leading barrier
 // protects it from the previous reduction's reads.
 __device__ __forceinline__ float uni(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Block reductions over NWV waves (4 by default: 256 threads) in a fixed pairwise order (for 4 waves
+// (r0 + r1) + (r2 + r3)); red holds NWV slots.
+template <int NWV, class T, class F>
+__device__ __forceinline__ T tree(const T *red, F op) {
+    if constexpr (NWV == 1) return red[0];
+    else return op(tree<NWV / 2>(red, op), tree<NWV / 2>(red + NWV / 2, op));
+}
+template <int NWV = 4>
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = ava::wave_sum(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return uni((red[0] + red[1]) + (red[2] + red[3]));
+    return uni(tree<NWV>(red, [](float a, float b) { return a + b; }));
 }
+template <int NWV = 4>
 __device__ __forceinline__ float block_max(float v, float *red) {
     v = ava::wave_max(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return uni(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    return uni(tree<NWV>(red, [](float a, float b) { return fmaxf(a, b); }));
 }
+template <int NWV = 4>
 __device__ __forceinline__ float block_min(float v, float *red) {
     v = ava::wave_min(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return uni(fminf(fminf(red[0], red[1]), fminf(red[2], red[3])));
+    return uni(tree<NWV>(red, [](float a, float b) { return fminf(a, b); }));
 }
+template <int NWV = 4>
 __device__ __forceinline__ int block_isum(int v, int *red) {
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;  // v is wave-uniform (ballot counts)
     __syncthreads();
-    return uni((red[0] + red[1]) + (red[2] + red[3]));
+    return uni(tree<NWV>(red, [](int a, int b) { return a + b; }));
 }
+template <int NWV = 4>
 __device__ __forceinline__ uint32_t block_umin(uint32_t v, uint32_t *red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return (uint32_t)uni((int)min(min(red[0], red[1]), min(red[2], red[3])));
+    return (uint32_t)uni((int)tree<NWV>(red, [](uint32_t a, uint32_t b) { return min(a, b); }));
 }
 
 // The granule code of rows n: code [n][g]. With keep != NULL, each stream's last position (row
@@ -74,8 +86,8 @@ __device__ __forceinline__ uint32_t block_umin(uint32_t v, uint32_t *red) {
 // With lcnt != NULL the row's non-zero units are also listed in unit order: lidx/lval [n][lcap] (unit,
 // value) and lcnt [n] = their number (beyond lcap only the first lcap are listed; readers then use the
 // dense code).
-template <int GPT>
-__global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ xf, const int32_t *__restrict__ ids,
+template <int GPT, int NTH>
+__global__ __launch_bounds__(NTH) void cb_code_kernel(const float *__restrict__ xf, const int32_t *__restrict__ ids,
                                                      const float *__restrict__ emb, int d, int vocab,
                                                      const uint32_t *__restrict__ widx,
                                                      const float *__restrict__ wsgn, int g, int k, int T,
@@ -83,10 +95,11 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
                                                      int *__restrict__ lcnt, int *__restrict__ lidx,
                                                      float *__restrict__ lval, int lcap) {
     __shared__ float su[2048];
-    __shared__ float fred[4];
-    __shared__ int ired[4];
-    __shared__ uint32_t ured[4];
-    __shared__ int s_wc[4][GPT];
+    constexpr int NWV = NTH / 64;
+    __shared__ float fred[NWV];
+    __shared__ int ired[NWV];
+    __shared__ uint32_t ured[NWV];
+    __shared__ int s_wc[NWV][GPT];
     const int row = blockIdx.x, tid = threadIdx.x;
     int id = ids[row];
     id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // an id outside [0, vocab) reads the nearest row
@@ -94,21 +107,21 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
 
     // u = [xf, rmsnorm(emb row, 1)]
     float ss = 0.0f;
-    for (int c = tid; c < d; c += NT) {
+    for (int c = tid; c < d; c += NTH) {
         su[c] = xr[c];
         const float e = er[c];
         ss += e * e;
     }
-    ss = block_sum(ss, fred);
+    ss = block_sum<NWV>(ss, fred);
     const float inv = 1.0f / sqrtf((ss * (1.0f / (float)d) + 0.0f) * 1.0f + NORM_EPS);
-    for (int c = tid; c < d; c += NT) su[d + c] = (er[c] * inv) * 1.0f;
+    for (int c = tid; c < d; c += NTH) su[d + c] = (er[c] * inv) * 1.0f;
     __syncthreads();
 
-    // h: unit j = tid + 256 i (padding units are -inf: never counted, never kept)
+    // h: unit j = tid + NTH i (padding units are -inf: never counted, never kept)
     float h[GPT];
 #pragma unroll
     for (int i = 0; i < GPT; i++) {
-        const int j = tid + i * NT;
+        const int j = tid + i * NTH;
         if (j < g) {
             const uint4 ix = reinterpret_cast<const uint4 *>(widx)[j];
             const float4 sv = reinterpret_cast<const float4 *>(wsgn)[j];
@@ -126,7 +139,7 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
         int c = 0;
 #pragma unroll
         for (int i = 0; i < GPT; i++) c += __popcll(__ballot(h[i] >= t));
-        return block_isum(c, ired);
+        return block_isum<NWV>(c, ired);
     };
 
     float kth = -INFINITY;
@@ -134,12 +147,12 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
         float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
         for (int i = 0; i < GPT; i++)
-            if (tid + i * NT < g) {
+            if (tid + i * NTH < g) {
                 lo = fminf(lo, h[i]);
                 hi = fmaxf(hi, h[i]);
             }
-        lo = block_min(lo, fred);
-        hi = block_max(hi, fred);
+        lo = block_min<NWV>(lo, fred);
+        hi = block_max<NWV>(hi, fred);
         bool done = false, found = false;
         float tk = 0.0f;
         if (isfinite(lo) && isfinite(hi)) {
@@ -154,12 +167,12 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
                 float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
                 for (int i = 0; i < GPT; i++)
-                    if (tid + i * NT < g) {
+                    if (tid + i * NTH < g) {
                         s1 += h[i];
                         s2 += h[i] * h[i];
                     }
-                s1 = block_sum(s1, fred);
-                s2 = block_sum(s2, fred);
+                s1 = block_sum<NWV>(s1, fred);
+                s2 = block_sum<NWV>(s2, fred);
                 const float mu = s1 / (float)g, sd = sqrtf(fmaxf(s2 / (float)g - mu * mu, 0.0f));
                 const float z = ava::normal_upper_quantile((float)k / (float)g);
                 const float dens = (float)g * 0.39894228f * __expf(-0.5f * z * z) / fmaxf(sd, 1e-30f);
@@ -202,13 +215,13 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
             float mn = INFINITY;
 #pragma unroll
             for (int i = 0; i < GPT; i++) mn = h[i] >= tk ? fminf(mn, h[i]) : mn;
-            mn = block_min(mn, fred);
+            mn = block_min<NWV>(mn, fred);
             if (mn == 0.0f) {
                 int neg = 0;
 #pragma unroll
                 for (int i = 0; i < GPT; i++)
                     neg += __popcll(__ballot(h[i] >= tk && __float_as_uint(h[i]) == 0x80000000u));
-                mn = block_isum(neg, ired) ? -0.0f : 0.0f;
+                mn = block_isum<NWV>(neg, ired) ? -0.0f : 0.0f;
             }
             kth = mn;
             done = true;
@@ -221,17 +234,17 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
                 int c = 0;
 #pragma unroll
                 for (int i = 0; i < GPT; i++)
-                    c += __popcll(__ballot(tid + i * NT < g && key_of(h[i]) >= cand));
-                const int cnt = block_isum(c, ired);
+                    c += __popcll(__ballot(tid + i * NTH < g && key_of(h[i]) >= cand));
+                const int cnt = block_isum<NWV>(c, ired);
                 if (cnt >= k) prefix = cand;
                 if (cnt == k) {
                     uint32_t mn = 0xffffffffu;
 #pragma unroll
                     for (int i = 0; i < GPT; i++) {
                         const uint32_t kk = key_of(h[i]);
-                        mn = (tid + i * NT < g && kk >= cand) ? min(mn, kk) : mn;
+                        mn = (tid + i * NTH < g && kk >= cand) ? min(mn, kk) : mn;
                     }
-                    prefix = block_umin(mn, ured);
+                    prefix = block_umin<NWV>(mn, ured);
                     break;
                 }
             }
@@ -246,16 +259,16 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
         const float v = h[i];
         float a = v * ((k >= g || v - kth >= 0.0f) ? 1.0f : 0.0f);
         a = a > 0.0f ? a : 0.0f;
-        h[i] = tid + i * NT < g ? a : 0.0f;
+        h[i] = tid + i * NTH < g ? a : 0.0f;
         s2 += h[i] * h[i];
     }
-    s2 = block_sum(s2, fred);
+    s2 = block_sum<NWV>(s2, fred);
     const float len = sqrtf(s2) * 1.0f + (float)1e-6;
     float *cr = code + (size_t)row * g;
     float *kr = (keep && row % T == T - 1) ? keep + (size_t)(row / T) * g : nullptr;
 #pragma unroll
     for (int i = 0; i < GPT; i++) {
-        const int j = tid + i * NT;
+        const int j = tid + i * NTH;
         h[i] = j < g ? h[i] / len : 0.0f;
         if (j < g) {
             cr[j] = h[i];
@@ -263,7 +276,7 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
         }
     }
     if (lcnt) {
-        // unit j = tid + 256 i: in unit order the i-th group of 256 comes after all earlier groups
+        // unit j = tid + NTH i: in unit order the i-th group of NTH comes after all earlier groups
         const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
         for (int i = 0; i < GPT; i++) {
@@ -282,10 +295,11 @@ __global__ __launch_bounds__(NT) void cb_code_kernel(const float *__restrict__ x
             const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0));
             const int pos = base + before + rank;
             if (h[i] != 0.0f && pos < lcap) {
-                li[pos] = tid + i * NT;
+                li[pos] = tid + i * NTH;
                 lv[pos] = h[i];
             }
-            base += (s_wc[0][i] + s_wc[1][i]) + (s_wc[2][i] + s_wc[3][i]);
+#pragma unroll
+            for (int w = 0; w < NWV; w++) base += s_wc[w][i];
         }
         if (tid == 0) lcnt[row] = base;
     }
@@ -577,16 +591,27 @@ int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d,
             int lcap, hipStream_t st) {
     AVA_REQUIRE(d <= 1024 && d % 4 == 0 && g > 0 && g <= 16384 && T > 0, AVA_ERR_SHAPE, "cb_code: d=%d g=%d", d, g);
     AVA_REQUIRE(!lcnt || (lidx && lval && lcap > 0), AVA_ERR_ARG, "cb_code: unit list without storage");
-    const int gpt = (g + NT - 1) / NT;
-#define AVA_CBC(G_)                                                                                        \
-    cb_code_kernel<G_><<<n, NT, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep, lcnt, lidx, \
-                                         lval, lcap)
-    if (gpt <= 2) AVA_CBC(2);
-    else if (gpt <= 8) AVA_CBC(8);
-    else if (gpt <= 16) AVA_CBC(16);
-    else if (gpt <= 32) AVA_CBC(32);
-    else if (gpt <= 48) AVA_CBC(48);
-    else AVA_CBC(64);
+    // few rows (a decode step): 1024 threads per row, so each wave's share of the search is short;
+    // many rows: 256
+#define AVA_CBC(G_, N_)                                                                                        \
+    cb_code_kernel<G_, N_><<<n, N_, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep, lcnt, lidx, \
+                                             lval, lcap)
+    if (n <= 1024) {
+        const int gpt = (g + 1023) / 1024;
+        if (gpt <= 2) AVA_CBC(2, 1024);
+        else if (gpt <= 4) AVA_CBC(4, 1024);
+        else if (gpt <= 8) AVA_CBC(8, 1024);
+        else if (gpt <= 12) AVA_CBC(12, 1024);
+        else AVA_CBC(16, 1024);
+    } else {
+        const int gpt = (g + NT - 1) / NT;
+        if (gpt <= 2) AVA_CBC(2, NT);
+        else if (gpt <= 8) AVA_CBC(8, NT);
+        else if (gpt <= 16) AVA_CBC(16, NT);
+        else if (gpt <= 32) AVA_CBC(32, NT);
+        else if (gpt <= 48) AVA_CBC(48, NT);
+        else AVA_CBC(64, NT);
+    }
 #undef AVA_CBC
     AVA_LAUNCHED("cb_code");
     return AVA_OK;
