@@ -34,76 +34,63 @@ __device__ __forceinline__ float uni(float v) { return __int_as_float(__builtin_
 
 
 
-// Row reductions: over the wave (a wave per row), or over the 4 waves through LDS (WG: a workgroup
-// per row, for few rows). Results are wave-uniform (readfirstlane) either way; the leading barrier
-// keeps a reduction from overwriting slots the previous one is still reading.
-template <bool WG>
+// Row reductions: over the wave (a wave per row), or over the row's RW waves through LDS (a
+// workgroup per row, for few rows), combined pairwise in a fixed order. Results are wave-uniform
+// (readfirstlane) either way; the leading barrier keeps a reduction from overwriting slots the
+// previous one is still reading.
+template <int N, class T, class F>
+__device__ __forceinline__ T tree(const T *r, F op) {
+    if constexpr (N == 1) return r[0];
+    else return op(tree<N / 2>(r, op), tree<N / 2>(r + N / 2, op));
+}
+template <int RW>
 struct RowRed {
     float *fs;
     int *is;
-    __device__ __forceinline__ float fsum(float v) {
-        v = ava::wave_sum(v);
-        if (WG) {
+    template <class T, class F>
+    __device__ __forceinline__ T across(T v, T *slots, F op) {
+        if constexpr (RW > 1) {
             __syncthreads();
-            if ((threadIdx.x & 63) == 0) fs[threadIdx.x >> 6] = v;
+            if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
             __syncthreads();
-            v = (fs[0] + fs[1]) + (fs[2] + fs[3]);
+            v = tree<RW>(slots, op);
         }
-        return uni(v);
+        return v;
+    }
+    __device__ __forceinline__ float fsum(float v) {
+        return uni(across(ava::wave_sum(v), fs, [](float a, float b) { return a + b; }));
     }
     __device__ __forceinline__ float fmin(float v) {
-        v = ava::wave_min(v);
-        if (WG) {
-            __syncthreads();
-            if ((threadIdx.x & 63) == 0) fs[threadIdx.x >> 6] = v;
-            __syncthreads();
-            v = fminf(fminf(fs[0], fs[1]), fminf(fs[2], fs[3]));
-        }
-        return uni(v);
+        return uni(across(ava::wave_min(v), fs, [](float a, float b) { return fminf(a, b); }));
     }
     __device__ __forceinline__ float fmax(float v) {
-        v = ava::wave_max(v);
-        if (WG) {
-            __syncthreads();
-            if ((threadIdx.x & 63) == 0) fs[threadIdx.x >> 6] = v;
-            __syncthreads();
-            v = fmaxf(fmaxf(fs[0], fs[1]), fmaxf(fs[2], fs[3]));
-        }
-        return uni(v);
+        return uni(across(ava::wave_max(v), fs, [](float a, float b) { return fmaxf(a, b); }));
     }
     __device__ __forceinline__ int isum(int v) {  // v wave-uniform
-        if (WG) {
-            __syncthreads();
-            if ((threadIdx.x & 63) == 0) is[threadIdx.x >> 6] = v;
-            __syncthreads();
-            v = (is[0] + is[1]) + (is[2] + is[3]);
-        }
-        return __builtin_amdgcn_readfirstlane(v);
+        return __builtin_amdgcn_readfirstlane(across(v, is, [](int a, int b) { return a + b; }));
     }
     __device__ __forceinline__ uint32_t umin(uint32_t v) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
-        if (WG) {
-            __syncthreads();
-            if ((threadIdx.x & 63) == 0) is[threadIdx.x >> 6] = (int)v;
-            __syncthreads();
-            v = min(min((uint32_t)is[0], (uint32_t)is[1]), min((uint32_t)is[2], (uint32_t)is[3]));
-        }
-        return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+        int r = across((int)v, is, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
+        return (uint32_t)__builtin_amdgcn_readfirstlane(r);
     }
 };
 
-// NV float4 chunks per lane. A wave per row (WG false): h <= 256 NV, chunk c = 64 i + lane; a
-// workgroup per row (WG true): h <= 1024 NV, chunk c = 256 i + thread. OUT: 0 = f32 a, P>0 = P int8
-// planes + row exponent.
-template <int NV, int P, bool FULL, bool WG = false>
-__global__ __launch_bounds__(256) void kwta_kernel(const float *__restrict__ u, int n, int h, int k, int relu2,
-                                                   float *__restrict__ a, float *__restrict__ kth_out,
-                                                   int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq) {
-    __shared__ float s_f[4];
-    __shared__ int s_i[4];
-    RowRed<WG> red{s_f, s_i};
-    constexpr int LANES = WG ? 256 : 64;  // threads of a row
+// NV float4 chunks per lane. A wave per row (RW = 1): h <= 256 NV, chunk c = 64 i + lane; a
+// workgroup of RW waves per row (RW = 4): h <= 256 RW NV, chunk c = 64 RW i + thread (8 and 16 waves
+// per row measured slower on the decode rows). OUT: 0 = f32 a, P>0 = P int8 planes + row exponent.
+template <int NV, int P, bool FULL, int RW = 1>
+__global__ __launch_bounds__(RW > 4 ? 64 * RW : 256) void kwta_kernel(const float *__restrict__ u, int n, int h, int k,
+                                                                      int relu2, float *__restrict__ a,
+                                                                      float *__restrict__ kth_out,
+                                                                      int8_t *__restrict__ xq,
+                                                                      int32_t *__restrict__ xexp, int ldq) {
+    constexpr bool WG = RW > 1;
+    __shared__ float s_f[RW > 4 ? RW : 4];
+    __shared__ int s_i[RW > 4 ? RW : 4];
+    RowRed<RW> red{s_f, s_i};
+    constexpr int LANES = 64 * RW;  // threads of a row
     const int lane = WG ? (int)threadIdx.x : (int)(threadIdx.x & 63);
     const int row = WG ? (int)blockIdx.x : (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     if (row >= n) return;  // uniform over the row's threads
@@ -351,9 +338,9 @@ int launch(const float *u, int n, int h, int k, int relu2, float *a, float *kth,
 #define AVA_KWG(NV_)                                                                                           \
     if (nv4 <= NV_) {                                                                                          \
         if (h == NV_ * 1024)                                                                                   \
-            kwta_kernel<NV_, P, true, true><<<n, 256, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);       \
+            kwta_kernel<NV_, P, true, 4><<<n, 256, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);          \
         else                                                                                                   \
-            kwta_kernel<NV_, P, false, true><<<n, 256, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);      \
+            kwta_kernel<NV_, P, false, 4><<<n, 256, 0, st>>>(u, n, h, k, relu2, a, kth, xq, xexp, ldq);         \
         AVA_LAUNCHED("kwta");                                                                                  \
         return AVA_OK;                                                                                         \
     }
