@@ -249,6 +249,53 @@ __device__ __forceinline__ float kv_get(const __half *p, size_t i) { return __ha
 __device__ __forceinline__ void kv_put(float *p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void kv_put(__half *p, size_t i, float v) { p[i] = __float2half_rn(v); }
 
+// 16-byte loads of the store: DPL elements per lane (4 f32 or 8 fp16), widened to f32; load16: 16
+// consecutive elements.
+template <typename KV>
+struct KvLane;
+template <>
+struct KvLane<float> {
+    static constexpr int DPL = 4;
+    static __device__ __forceinline__ void load(const float *p, float (&x)[4]) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
+#pragma unroll
+        for (int z = 0; z < 4; z++) x[z] = v[z];
+    }
+    static __device__ __forceinline__ void load16(const float *p, float (&x)[16]) {
+        f32x4 v[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = reinterpret_cast<const f32x4 *>(p)[c];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int z = 0; z < 4; z++) x[4 * c + z] = v[c][z];
+    }
+};
+template <>
+struct KvLane<__half> {
+    static constexpr int DPL = 8;
+    static __device__ __forceinline__ void load(const __half *p, float (&x)[8]) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int z = 0; z < 4; z++) {
+            const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[z]));
+            x[2 * z] = f.x;
+            x[2 * z + 1] = f.y;
+        }
+    }
+    static __device__ __forceinline__ void load16(const __half *p, float (&x)[16]) {
+        const uint4 u0 = reinterpret_cast<const uint4 *>(p)[0], u1 = reinterpret_cast<const uint4 *>(p)[1];
+        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int z = 0; z < 8; z++) {
+            const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[z]));
+            x[2 * z] = f.x;
+            x[2 * z + 1] = f.y;
+        }
+    }
+};
+
 // Causal single-head attention of one stream's T queries against its store: query t (store
 // position n0 + t) reads entries 0..n0 + t with softmax(q.k / sqrt(de)) (gpu/model.rs:543-562,
 // gpu/model/fstep.rs:303-329). de == 64. Block = 64 queries x 256 threads; keys and values in
@@ -333,6 +380,116 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
     }
 }
 
+// The same read on the fp32 MFMA (v_mfma_f32_32x32x2_f32), for query blocks of 64: per 64-key tile,
+// S = Q K^T (wave w: a 32 x 32 quadrant), scaled and masked into LDS; the online softmax by row as
+// attend_kernel (4 threads per row, 16 scores each: the running max, the rescale factor of the
+// previous tiles, exp); then O = O corr + P V (wave w: its quadrant of the 64 x 64 output, kept in
+// the MFMA accumulator across tiles); O / den at the end. Equal to attend_kernel up to the products'
+// summation order.
+template <typename KV>
+__global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restrict__ q, int ldq,
+                                                          const KV *__restrict__ ks, const KV *__restrict__ vs,
+                                                          int cap, int n0, const int *n0p, int T, float scale,
+                                                          float *__restrict__ out) {
+    if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device (a replayed graph)
+    constexpr int L = 65;               // LDS row stride (odd: a column read hits 32 banks)
+    __shared__ float sQ[64 * L], sK[64 * L], sV[64 * L], sP[64 * L];
+    __shared__ float s_corr[64], s_den[64];
+    const int bi = blockIdx.y, qb = blockIdx.x * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lc = lane & 31;
+    const int row0 = (wave >> 1) * 32, col0 = (wave & 1) * 32;
+    const int r = tid >> 2, sub = tid & 3;  // the softmax's row and quarter
+    const KV *kb = ks + (size_t)bi * cap * 64, *vb = vs + (size_t)bi * cap * 64;
+    for (int i = tid; i < 64 * 64; i += 256) {
+        const int rr = i >> 6, cc = i & 63;
+        sQ[rr * L + cc] = qb + rr < T ? q[((size_t)bi * T + qb + rr) * ldq + cc] : 0.0f;
+    }
+    auto qrow = [&](int i) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); };
+    float mx = -INFINITY, den = 0.0f;
+    f32x16 o = {};
+    const int qpos = n0 + qb + r;                // the softmax row's store position
+    const int kend = min(n0 + qb + 64, n0 + T);  // keys the block's last row reads
+    // thread (r, sub) stages key/value row r, dims 16 sub .. 16 sub + 15; the next tile's are loaded
+    // into registers while this tile is computed
+    float kr[16], vr[16];
+    auto fetch = [&](int k0) {
+        const bool ok = k0 + r < kend;
+        const size_t o16 = (size_t)(k0 + (ok ? r : 0)) * 64 + sub * 16;
+        KvLane<KV>::load16(kb + o16, kr);
+        KvLane<KV>::load16(vb + o16, vr);
+        if (!ok)
+#pragma unroll
+            for (int z = 0; z < 16; z++) kr[z] = vr[z] = 0.0f;
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < kend; k0 += 64) {
+        __syncthreads();  // the previous tile's K, V and P are read
+#pragma unroll
+        for (int z = 0; z < 16; z++) {
+            sK[r * L + sub * 16 + z] = kr[z];
+            sV[r * L + sub * 16 + z] = vr[z];
+        }
+        if (k0 + 64 < kend) fetch(k0 + 64);
+        __syncthreads();
+        {
+            f32x16 sa = {};
+            const int fr = lane & 31, h = lane >> 5;
+#pragma unroll 8
+            for (int x = 0; x < 64; x += 2)
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[(row0 + fr) * L + x + h], sK[(col0 + fr) * L + x + h], sa,
+                                                          0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int rr = row0 + qrow(i), cc = col0 + lc;
+                const float a = sa[i] * scale + 0.0f;
+                sP[rr * L + cc] = (k0 + cc <= n0 + qb + rr) ? a : -INFINITY;
+            }
+        }
+        __syncthreads();
+        {
+            float sc[16], tmax = -INFINITY;
+#pragma unroll
+            for (int z = 0; z < 16; z++) {
+                sc[z] = sP[r * L + sub * 16 + z];
+                tmax = fmaxf(tmax, sc[z]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+            const float nmx = fmaxf(mx, tmax);
+            const float corr = (mx == -INFINITY) ? 0.0f : expf(mx - nmx);
+            float psum = 0.0f;
+#pragma unroll
+            for (int z = 0; z < 16; z++) {
+                const float e = (sc[z] == -INFINITY) ? 0.0f : expf(sc[z] - nmx);
+                sP[r * L + sub * 16 + z] = e;
+                psum += e;
+            }
+            psum += __shfl_xor(psum, 1, 64);
+            psum += __shfl_xor(psum, 2, 64);
+            den = den * corr + psum;
+            mx = nmx;
+            if (sub == 0) s_corr[r] = corr;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[i] *= s_corr[row0 + qrow(i)];
+        {
+            const int fr = lane & 31, h = lane >> 5;
+#pragma unroll 8
+            for (int x = 0; x < 64; x += 2)
+                o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + x + h], sV[(x + h) * L + col0 + fr], o, 0,
+                                                         0, 0);
+        }
+    }
+    if (sub == 0) s_den[r] = den;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int rr = row0 + qrow(i);
+        if (qb + rr < T) out[((size_t)bi * T + qb + rr) * 64 + col0 + lc] = o[i] / s_den[rr];
+    }
+}
+
 // The decode form of the same read (flash-decoding), for a few queries per stream: query row
 // (b, t) at store position n0 + t reads keys 0..n0 + t. Its keys are cut into chunks of ACH; workgroup
 // (s, row) reads chunk s, each wave a quarter of it, 32 keys per iteration, 16 bytes per lane per
@@ -361,33 +518,6 @@ __device__ __forceinline__ float row_sum8(float v) {
     v += dpp_f<0x4E>(v);
     return v + dpp_f<0x141>(v);
 }
-
-// 16-byte loads of the store: DPL elements per lane (4 f32 or 8 fp16), widened to f32.
-template <typename KV>
-struct KvLane;
-template <>
-struct KvLane<float> {
-    static constexpr int DPL = 4;
-    static __device__ __forceinline__ void load(const float *p, float (&x)[4]) {
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
-#pragma unroll
-        for (int z = 0; z < 4; z++) x[z] = v[z];
-    }
-};
-template <>
-struct KvLane<__half> {
-    static constexpr int DPL = 8;
-    static __device__ __forceinline__ void load(const __half *p, float (&x)[8]) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(p);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int z = 0; z < 4; z++) {
-            const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[z]));
-            x[2 * z] = f.x;
-            x[2 * z + 1] = f.y;
-        }
-    }
-};
 
 // Lane layout: a key's 64 dims are read by LPK = 64 / DPL lanes (16 for f32, 8 for fp16), so a wave
 // holds G = 64 / LPK key groups and reads G whole keys per 16-byte load instruction; each group takes
@@ -920,6 +1050,16 @@ size_t engram_split_floats(int B, int T, int n0) {
     return T <= ENGRAM_SPLIT_T ? (size_t)B * T * ceil_div(n0 + T, ACH) * 66 : 0;
 }
 
+// The query-block read on the fp32 MFMA (AVA_ATTEND_MFMA=0: the VALU form; tuning).
+bool attend_mfma() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("AVA_ATTEND_MFMA");
+        v = e ? (atoi(e) != 0) : 1;
+    }
+    return v != 0;
+}
+
 // With n0p (the store length on the device) the chunk grid covers the whole store, so a captured
 // launch serves every length; chunks past the length are empty and merge as nothing.
 template <typename KV>
@@ -939,7 +1079,8 @@ int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n
         return AVA_OK;
     }
     dim3 grid(ceil_div(T, 64), B);
-    attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
+    if (attend_mfma()) attend_mfma_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
+    else attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
     AVA_LAUNCHED("attend");
     return AVA_OK;
 }
