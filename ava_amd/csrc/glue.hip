@@ -134,7 +134,8 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
 // G [n][nc] = h [n][d] . W [d][nc] in f32 (the reference keeps the gate projections f32:
 // gpu/arch.rs:1914-1936), on the fp32 MFMA (v_mfma_f32_32x32x2_f32). Block = 128 rows x NC columns
 // (NC = nc rounded up to 32, <= 128); wave w owns rows 32w..32w+31; K in steps of 32 through LDS
-// (h tile row-major, W tile row-major, both padded), each step 16 MFMA k-substeps per column block.
+// (h tile row-major, W tile row-major, both padded), each step 16 MFMA k-substeps per column block,
+// the next step's tiles in flight meanwhile.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int GR = 128, GK = 32;
 template <int NCB>  // column blocks of 32
@@ -147,19 +148,38 @@ __global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict_
     f32x16 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[cb] = f32x16{};
-    for (int k0 = 0; k0 < d; k0 += GK) {
-        // h tile: 128 rows x 32 floats, 8 threads per row, float4 each
-        for (int i = tid; i < GR * GK / 4; i += 256) {
-            const int rr = i >> 3, kk = (i & 7) * 4;
-            const int row = min(r0 + rr, n - 1);
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(h + (size_t)row * d + k0 + kk);
+    // the next K step's tiles are loaded into registers while this one is multiplied: h 128 rows x 32
+    // floats (8 threads per row, a float4 each, HR per thread), W 32 x 32 NCB (WR floats per thread)
+    constexpr int HR = GR * GK / 4 / 256, WR = GK * NCB * 32 / 256;
+    f32x4 hr[HR];
+    float wr[WR];
+    auto fetch = [&](int k0) {
 #pragma unroll
-            for (int z = 0; z < 4; z++) sh[rr][kk + z] = v[z];
+        for (int j = 0; j < HR; j++) {
+            const int i = tid + j * 256, rr = i >> 3, kk = (i & 7) * 4;
+            hr[j] = *reinterpret_cast<const f32x4 *>(h + (size_t)min(r0 + rr, n - 1) * d + k0 + kk);
         }
-        for (int i = tid; i < GK * NCB * 32; i += 256) {
-            const int kk = i / (NCB * 32), cc = i % (NCB * 32);
-            sw[kk][cc] = cc < nc ? w[(size_t)(k0 + kk) * nc + cc] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < WR; j++) {
+            const int i = tid + j * 256, kk = i / (NCB * 32), cc = i % (NCB * 32);
+            wr[j] = cc < nc ? w[(size_t)(k0 + kk) * nc + cc] : 0.0f;
         }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < d; k0 += GK) {
+        __syncthreads();  // the previous step's tiles are read
+#pragma unroll
+        for (int j = 0; j < HR; j++) {
+            const int i = tid + j * 256, rr = i >> 3, kk = (i & 7) * 4;
+#pragma unroll
+            for (int z = 0; z < 4; z++) sh[rr][kk + z] = hr[j][z];
+        }
+#pragma unroll
+        for (int j = 0; j < WR; j++) {
+            const int i = tid + j * 256, kk = i / (NCB * 32), cc = i % (NCB * 32);
+            sw[kk][cc] = wr[j];
+        }
+        if (k0 + GK < d) fetch(k0 + GK);
         __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < GK; ks += 2) {
@@ -170,7 +190,6 @@ __global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict_
                 acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[cb], 0, 0, 0);
             }
         }
-        __syncthreads();
     }
     // lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32 of each 32 x 32 block
 #pragma unroll
