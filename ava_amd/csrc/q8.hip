@@ -184,34 +184,42 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
         const BufRes yr = buf_res(ybase + (size_t)m0 * ep.ldy, (unsigned)(BM * ep.ldy) * 4u);
         const unsigned ld4 = (unsigned)ep.ldy * 4u;
         const unsigned voff = ((unsigned)(rw0 + rsub) * (unsigned)ep.ldy + (unsigned)(n0 + cw0 + ccol)) * 4u;
+        float sc[FN], cv[FN];
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int col = n0 + cw0 + j * 32 + ccol;
-            const float sc = scale[col];
-            const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+            sc[j] = scale[col];
+            cv[j] = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+        }
+        // row block i of every column block at a time: its FN x 16 prior values (EPI_ADD) are all in
+        // flight before the first add
 #pragma unroll
-            for (int i = 0; i < FM; i++) {
-                int ex[16];
+        for (int i = 0; i < FM; i++) {
+            int ex[16];
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const i32x4 e4 = *reinterpret_cast<const i32x4 *>(s_exp + rw0 + i * 32 + g * 8 + rsub);
+            for (int g = 0; g < 4; g++) {
+                const i32x4 e4 = *reinterpret_cast<const i32x4 *>(s_exp + rw0 + i * 32 + g * 8 + rsub);
 #pragma unroll
-                    for (int z = 0; z < 4; z++) ex[g * 4 + z] = e4[z];
-                }
-                float prev[16];
-                if (EPI == EPI_ADD) {
+                for (int z = 0; z < 4; z++) ex[g * 4 + z] = e4[z];
+            }
+            float prev[FN][16];
+            if (EPI == EPI_ADD) {
+#pragma unroll
+                for (int j = 0; j < FN; j++)
 #pragma unroll
                     for (int r = 0; r < 16; r++)
-                        prev[r] = load_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
-                }
+                        prev[j][r] = load_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
+                AVA_ISSUE_FENCE();
+            }
+#pragma unroll
+            for (int j = 0; j < FN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    float v = ldexpf(value(i, j, r), ex[r]) * sc;
-                    if (EPI == EPI_MUL) v = v * cv;
-                    if (EPI == EPI_ADD) v = prev[r] + v;
+                    float v = ldexpf(value(i, j, r), ex[r]) * sc[j];
+                    if (EPI == EPI_MUL) v = v * cv[j];
+                    if (EPI == EPI_ADD) v = prev[j][r] + v;
                     store_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4, v);
                 }
-            }
         }
         return;
     }
