@@ -189,10 +189,18 @@ int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, 
 // part, engram_split_floats of scratch) for T <= ENGRAM_SPLIT_T.
 constexpr int ENGRAM_SPLIT_T = 4;
 size_t engram_split_floats(int B, int T, int n0);
+// Optional work after the decode form's merge: the read's planes for the next product (xq [planes][rows]
+// [ldq], xexp [rows]; xq NULL: none), and the device store length advanced by T (adv NULL: none).
+struct PostRead {
+    int8_t *xq = nullptr;
+    int32_t *xexp = nullptr;
+    int ldq = 0, planes = 0;
+    int *adv = nullptr;
+};
 int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, const int *n0p,
-           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st);
+           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post = {});
 int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
-                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st);
+                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post = {});
 int engram_advance(int *n0p, int T, int cap, hipStream_t st);
 // cb.hip: the cerebellum head (code with its unit lists, read-out with the online table, learning)
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,

@@ -634,8 +634,14 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
 // out [row][64] = the merge of the row's chunk partials: M = max m_s, L = sum l_s e^(m_s - M),
 // o = sum o_s e^(m_s - M) / L, the terms added in chunk order. Lane s takes chunk s's (m, l) and
 // weight; every lane's o_s loads for 16 chunks are in flight together.
+// With P > 0 the row's planes (quant_rows_kernel's, the next product's input) are written too, and with
+// adv the store length on the device advances by T (store_advance_kernel's step: every reader of it
+// in this forward, the store append and the chunk reads, ran before this kernel).
+template <int P>
 __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int nsplit,
-                                                            float *__restrict__ out) {
+                                                            float *__restrict__ out, int8_t *__restrict__ xq,
+                                                            int32_t *__restrict__ xexp, int ldq, int *adv, int T,
+                                                            int cap) {
     const int row = blockIdx.x, c = threadIdx.x;
     const float *pr = part + (size_t)row * nsplit * 66;
     float M = -INFINITY;
@@ -667,7 +673,22 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
             }
         }
     }
-    out[(size_t)row * 64 + c] = O / L;
+    const float o = O / L;
+    out[(size_t)row * 64 + c] = o;
+    if constexpr (P > 0) {
+        const int e = ava::plane_exp(ava::wave_max(fabsf(o)));
+        if (c == 0) xexp[row] = e;
+        int qv[P];
+        ava::to_planes<P>(o, e, qv);
+        const int nrows = gridDim.x;
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            int8_t *qr = xq + ((size_t)p * nrows + row) * ldq;
+            qr[c] = (int8_t)qv[p];
+            for (int z = 64 + c; z < ldq; z += 64) qr[z] = 0;
+        }
+    }
+    if (adv && row == 0 && c == 0) *adv = min(*adv + T, cap);
 }
 
 // The device store length advances by T after a forward, saturating at the store's capacity (the
@@ -1083,7 +1104,7 @@ bool attend_mfma() {
 // launch serves every length; chunks past the length are empty and merge as nothing.
 template <typename KV>
 int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n0, const int *n0p, int B, int T,
-             float *out, float *part, size_t part_floats, hipStream_t st) {
+             float *out, float *part, size_t part_floats, const PostRead &post, hipStream_t st) {
     const float scale = (float)(1.0 / sqrt(64.0));
     if (T <= ENGRAM_SPLIT_T) {
         const int span = n0p ? cap - T : n0;
@@ -1093,7 +1114,13 @@ int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n
         attend_split_kernel<KV><<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, nsplit,
                                                                      part);
         AVA_LAUNCHED("attend_split");
-        attend_combine_kernel<<<B * T, 64, 0, st>>>(part, nsplit, out);
+#define AVA_AC(P_) \
+    attend_combine_kernel<P_><<<B * T, 64, 0, st>>>(part, nsplit, out, post.xq, post.xexp, post.ldq, post.adv, T, cap)
+        if (!post.xq) AVA_AC(0);
+        else if (post.planes == 1) AVA_AC(1);
+        else if (post.planes == 2) AVA_AC(2);
+        else AVA_AC(3);
+#undef AVA_AC
         AVA_LAUNCHED("attend_combine");
         return AVA_OK;
     }
@@ -1105,18 +1132,21 @@ int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n
 }
 
 int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, const int *n0p,
-           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st) {
+           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post) {
     AVA_REQUIRE(B > 0 && T > 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
                 "attend: B=%d T=%d, a store of %d entries holds %d + %d", B, T, cap, n0, T);
     AVA_REQUIRE(ldq >= 64 && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d", ldq);
+    AVA_REQUIRE(!post.xq || (post.planes >= 1 && post.planes <= 3 && post.ldq >= 64 && post.ldq % 64 == 0),
+                AVA_ERR_ARG, "attend: planes %d, ldq %d", post.planes, post.ldq);
     if (kv_half)
         return attend_t(q, ldq, (const __half *)ks, (const __half *)vs, cap, n0, n0p, B, T, out, part, part_floats,
-                        st);
-    return attend_t(q, ldq, (const float *)ks, (const float *)vs, cap, n0, n0p, B, T, out, part, part_floats, st);
+                        post, st);
+    return attend_t(q, ldq, (const float *)ks, (const float *)vs, cap, n0, n0p, B, T, out, part, part_floats, post,
+                    st);
 }
 
 int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
-                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st) {
+                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post) {
     AVA_REQUIRE(n0 + T <= cap, AVA_ERR_SHAPE, "engram: store of %d entries holds %d + %d", cap, n0, T);
     const int total = B * T * 64;
     if (kv_half)
@@ -1126,7 +1156,7 @@ int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, i
         store_append_kernel<float><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, n0p,
                                                                           (float *)ks, (float *)vs);
     AVA_LAUNCHED("store_append");
-    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, n0p, B, T, out, part, part_floats, st);
+    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, n0p, B, T, out, part, part_floats, st, post);
 }
 
 int engram_advance(int *n0p, int T, int cap, hipStream_t st) {

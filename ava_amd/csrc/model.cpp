@@ -407,7 +407,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     // the next norm's planes in one pass (ready: the planes of the next norm are already in xq)
     AVA_RUN("embed", ava::embed_rms(ids, m->tok_emb, N, d, c.vocab, m->x, c.dense ? m->streams[0] : nullptr,
                                     m->blocks[0].lif_norm, P, m->xq, m->xexp, ldd, st));
-    bool ready = true, final_ready = false;
+    bool ready = true, final_ready = false, advanced = false;
     for (int i = 0; i < L; i++) {
         const Block &b = m->blocks[i];
         const size_t sbd = (size_t)i * B * d;
@@ -448,9 +448,19 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         if (b.eng) {
             AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.eng_norm, P, m->xq, m->xexp, ldd, nullptr, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.eqkv.w, ava::Q8_STORE, m->qkv, 3 * de, nullptr, st));
+            // the decode form's merge also writes the read's planes and advances the device store length
+            ava::PostRead post;
+            if (T <= ava::ENGRAM_SPLIT_T) {
+                post.xq = m->xq;
+                post.xexp = m->xexp;
+                post.ldq = ava::q8_ldk(de);
+                post.planes = P;
+                post.adv = s->eng_len_dev;
+                advanced = s->eng_len_dev != nullptr;
+            }
             AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, c.eng_half, s->eng_cap, s->eng_len,
-                                                   s->eng_len_dev, m->eo, m->att_part, m->att_part_floats, st));
-            AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
+                                                   s->eng_len_dev, m->eo, m->att_part, m->att_part_floats, st, post));
+            if (!post.xq) AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         }
         // the sparse MLP
@@ -474,7 +484,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     }
     if (c.eng_block >= 0) {
         s->eng_len += T;
-        if (s->eng_len_dev) AVA_RUN("store_advance", ava::engram_advance(s->eng_len_dev, T, s->eng_cap, st));
+        if (s->eng_len_dev && !advanced)
+            AVA_RUN("store_advance", ava::engram_advance(s->eng_len_dev, T, s->eng_cap, st));
     }
     if (join) AVA_HIP(hipStreamWaitEvent(st, join, 0));
     if (logits) {
