@@ -86,15 +86,31 @@ __device__ __forceinline__ uint32_t block_umin(uint32_t v, uint32_t *red) {
 // With lcnt != NULL the row's non-zero units are also listed in unit order: lidx/lval [n][lcap] (unit,
 // value) and lcnt [n] = their number (beyond lcap only the first lcap are listed; readers then use the
 // dense code).
-template <int GPT, int NTH>
+constexpr int APPLY_LCAP = 1024;  // unit lists the read-out takes through LDS
+
+// With AP > 0 (a row per workgroup of NTH >= d threads, the unit lists on) the kernel goes on to the
+// read-out and its planes: thread c forms out[row][c] with cb_apply_cols_kernel's sums in its order
+// (the list kept in LDS as it is written), then the row's AP planes for the head as
+// quant_rows_kernel writes them (xq [AP][n][ldq], xexp [n]): one launch instead of three.
+struct ApplyArgs {
+    const float *w, *tab;
+    const double *scale;
+    float *out;
+    int8_t *xq;
+    int32_t *xexp;
+    int ldq;
+};
+template <int GPT, int NTH, int AP = 0>
 __global__ __launch_bounds__(NTH) void cb_code_kernel(const float *__restrict__ xf, const int32_t *__restrict__ ids,
                                                      const float *__restrict__ emb, int d, int vocab,
                                                      const uint32_t *__restrict__ widx,
                                                      const float *__restrict__ wsgn, int g, int k, int T,
                                                      float *__restrict__ code, float *__restrict__ keep,
                                                      int *__restrict__ lcnt, int *__restrict__ lidx,
-                                                     float *__restrict__ lval, int lcap) {
+                                                     float *__restrict__ lval, int lcap, ApplyArgs ap) {
     __shared__ float su[2048];
+    __shared__ int s_lu[AP > 0 ? APPLY_LCAP : 1];
+    __shared__ float s_lv[AP > 0 ? APPLY_LCAP : 1];
     constexpr int NWV = NTH / 64;
     __shared__ float fred[NWV];
     __shared__ int ired[NWV];
@@ -298,10 +314,72 @@ __global__ __launch_bounds__(NTH) void cb_code_kernel(const float *__restrict__ 
                 li[pos] = tid + i * NTH;
                 lv[pos] = h[i];
             }
+            if constexpr (AP > 0)
+                if (h[i] != 0.0f && pos < APPLY_LCAP) {
+                    s_lu[pos] = tid + i * NTH;
+                    s_lv[pos] = h[i];
+                }
 #pragma unroll
             for (int w = 0; w < NWV; w++) base += s_wc[w][i];
         }
         if (tid == 0) lcnt[row] = base;
+        if constexpr (AP > 0) {
+            __syncthreads();  // the LDS list (and this row's code in memory) are complete
+            const int cnt = base, c = tid, b = row / T;
+            const bool listed = cnt <= lcap && cnt <= APPLY_LCAP;
+            float o = 0.0f;
+            if (c < d) {
+                const double sc = ap.scale ? ap.scale[b] : 1.0;
+                const float *tb = ap.tab ? ap.tab + (size_t)b * g * d + c : nullptr;
+                float acc = 0.0f, acc2 = 0.0f;
+                if (listed) {
+                    constexpr int QB = 16;
+                    if (ap.w) {
+                        for (int q0 = 0; q0 < cnt; q0 += QB) {
+                            float v[QB];
+#pragma unroll
+                            for (int z = 0; z < QB; z++) v[z] = ap.w[(size_t)s_lu[min(q0 + z, cnt - 1)] * d + c];
+                            AVA_ISSUE_FENCE();
+#pragma unroll
+                            for (int z = 0; z < QB; z++)
+                                if (q0 + z < cnt) acc += v[z] * s_lv[q0 + z];
+                        }
+                    }
+                    if (tb) {
+                        for (int q0 = 0; q0 < cnt; q0 += QB) {
+                            float v[QB];
+#pragma unroll
+                            for (int z = 0; z < QB; z++) v[z] = tb[(size_t)s_lu[min(q0 + z, cnt - 1)] * d];
+                            AVA_ISSUE_FENCE();
+#pragma unroll
+                            for (int z = 0; z < QB; z++)
+                                if (q0 + z < cnt) {
+                                    const float x = sc == 1.0 ? s_lv[q0 + z] : (float)((double)s_lv[q0 + z] * sc);
+                                    acc2 += x * v[z];
+                                }
+                        }
+                    }
+                } else {
+                    for (int j = 0; j < g; j++) {
+                        const float cj = cr[j];
+                        if (cj == 0.0f) continue;
+                        if (ap.w) acc += ap.w[(size_t)j * d + c] * cj;
+                        if (tb) acc2 += (sc == 1.0 ? cj : (float)((double)cj * sc)) * tb[(size_t)j * d];
+                    }
+                }
+                o = xr[c] + acc;
+                if (tb) o = o + acc2;
+                ap.out[(size_t)row * d + c] = o;
+            }
+            const int e = ava::plane_exp(block_max<NWV>(c < d ? fabsf(o) : 0.0f, fred));
+            if (tid == 0) ap.xexp[row] = e;
+            for (int cc = tid; cc < ap.ldq; cc += NTH) {
+                int qv[AP];
+                ava::to_planes<AP>(cc < d ? o : 0.0f, e, qv);
+#pragma unroll
+                for (int p = 0; p < AP; p++) ap.xq[((size_t)p * gridDim.x + row) * ap.ldq + cc] = (int8_t)qv[p];
+            }
+        }
     }
 }
 
@@ -309,7 +387,6 @@ __global__ __launch_bounds__(NTH) void cb_code_kernel(const float *__restrict__ 
 // table's share sum x_j tab[b][j] with x_j = c_j or (float)((double)c_j * scale[b]), from the row's
 // unit list (cb_code's lidx/lval) or, when the list overflowed, the dense code. Block (row, 256
 // columns), one column per thread: the table rows are read 1 KB per wave, coalesced.
-constexpr int APPLY_LCAP = 1024;
 __global__ __launch_bounds__(NT) void cb_apply_cols_kernel(const float *__restrict__ xf, const float *__restrict__ code,
                                                            int g, int d, const float *__restrict__ w,
                                                            const float *__restrict__ tab,
@@ -595,7 +672,7 @@ int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d,
     // many rows: 256
 #define AVA_CBC(G_, N_)                                                                                        \
     cb_code_kernel<G_, N_><<<n, N_, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep, lcnt, lidx, \
-                                             lval, lcap)
+                                             lval, lcap, ApplyArgs{})
     if (n <= 1024) {
         const int gpt = (g + 1023) / 1024;
         if (gpt <= 2) AVA_CBC(2, 1024);
@@ -613,6 +690,29 @@ int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d,
         else AVA_CBC(64, NT);
     }
 #undef AVA_CBC
+    AVA_LAUNCHED("cb_code");
+    return AVA_OK;
+}
+
+bool cb_head_fits(int n, int d, int g, int planes) { return n <= 1024 && d <= 1024 && g <= 16384 && planes == 3; }
+
+int cb_head(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
+            const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,
+            int lcap, const float *w, const float *tab, const double *scale, float *out, int planes, int8_t *xq,
+            int32_t *xexp, hipStream_t st) {
+    AVA_REQUIRE(cb_head_fits(n, d, g, planes) && d % 4 == 0 && lcnt && lidx && lval && lcap > 0 && T > 0,
+                AVA_ERR_SHAPE, "cb_head: n=%d d=%d g=%d planes=%d", n, d, g, planes);
+    const ApplyArgs ap{w, tab, scale, out, xq, xexp, q8_ldk(d)};
+    const int gpt = (g + 1023) / 1024;
+#define AVA_CBH(G_)                                                                                            \
+    cb_code_kernel<G_, 1024, 3><<<n, 1024, 0, st>>>(xf, ids, emb, d, vocab, widx, wsgn, g, k, T, code, keep, lcnt, \
+                                                    lidx, lval, lcap, ap)
+    if (gpt <= 2) AVA_CBH(2);
+    else if (gpt <= 4) AVA_CBH(4);
+    else if (gpt <= 8) AVA_CBH(8);
+    else if (gpt <= 12) AVA_CBH(12);
+    else AVA_CBH(16);
+#undef AVA_CBH
     AVA_LAUNCHED("cb_code");
     return AVA_OK;
 }

@@ -206,6 +206,12 @@ int engram_advance(int *n0p, int T, int cap, hipStream_t st);
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
             const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,
             int lcap, hipStream_t st);
+// cb_code, cb_apply_list and the planes of its output in one launch, for few rows (cb_head_fits)
+bool cb_head_fits(int n, int d, int g, int planes);
+int cb_head(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
+            const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,
+            int lcap, const float *w, const float *tab, const double *scale, float *out, int planes, int8_t *xq,
+            int32_t *xexp, hipStream_t st);
 int cb_apply_list(const float *xf, const float *code, int n, int g, int d, const float *w, const float *tab,
                   const double *scale, int T, const int *lcnt, const int *lidx, const float *lval, int lcap, float *out,
                   hipStream_t st);

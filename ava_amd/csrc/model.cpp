@@ -494,12 +494,21 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
                                                   st));
         if (cb) {
             // the cerebellum's correction between the final norm and the head (gpu/model/fstep/arch.rs:1045-1047)
-            AVA_RUN("cb_code", ava::cb_code(m->h, ids, m->tok_emb, N, d, c.vocab, m->cb_idx, m->cb_sgn, c.cb_units, m->cb_k,
-                                            T, m->cb_codes, s->cb_code, m->cb_lcnt, m->cb_lidx, m->cb_lval, m->cb_lcap,
-                                            st));
-            AVA_RUN("cb_apply", ava::cb_apply_list(m->h, m->cb_codes, N, c.cb_units, d, m->cb_w, s->cb_tab, s->cb_scale,
-                                                   T, m->cb_lcnt, m->cb_lidx, m->cb_lval, m->cb_lcap, m->y, st));
-            AVA_RUN("quant_rows", ava::launch_quant_rows(m->y, N, d, d, P, m->xq, m->xexp, st));
+            if (ava::cb_head_fits(N, d, c.cb_units, P)) {
+                // few rows: the code, the read-out and its planes in one launch
+                AVA_RUN("cb_code", ava::cb_head(m->h, ids, m->tok_emb, N, d, c.vocab, m->cb_idx, m->cb_sgn, c.cb_units,
+                                                m->cb_k, T, m->cb_codes, s->cb_code, m->cb_lcnt, m->cb_lidx,
+                                                m->cb_lval, m->cb_lcap, m->cb_w, s->cb_tab, s->cb_scale, m->y, P,
+                                                m->xq, m->xexp, st));
+            } else {
+                AVA_RUN("cb_code", ava::cb_code(m->h, ids, m->tok_emb, N, d, c.vocab, m->cb_idx, m->cb_sgn, c.cb_units,
+                                                m->cb_k, T, m->cb_codes, s->cb_code, m->cb_lcnt, m->cb_lidx,
+                                                m->cb_lval, m->cb_lcap, st));
+                AVA_RUN("cb_apply", ava::cb_apply_list(m->h, m->cb_codes, N, c.cb_units, d, m->cb_w, s->cb_tab,
+                                                       s->cb_scale, T, m->cb_lcnt, m->cb_lidx, m->cb_lval, m->cb_lcap,
+                                                       m->y, st));
+                AVA_RUN("quant_rows", ava::launch_quant_rows(m->y, N, d, d, P, m->xq, m->xexp, st));
+            }
         }
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &m->head.w, ava::Q8_STORE, logits, c.vocab, nullptr, st));
     }
