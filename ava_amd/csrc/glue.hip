@@ -740,43 +740,54 @@ __global__ __launch_bounds__(256) void dense_mix_kernel(DenseArgs a) {
 
 // The dense mix of whole rows (the same terms in the same order as dense_mix_kernel) followed by the
 // next norm's planes of the mixed row (row_rms_planes): one wave per row, so the row is read once.
+// The earlier streams go in batches of 4 with the loads of all the lane's chunks in flight together
+// (a batch is one memory round trip, not one per chunk).
 template <int P, int NV>
 __global__ __launch_bounds__(256) void dense_rms_kernel(DenseArgs a, int n, int d, const float *__restrict__ gain,
                                                         int8_t *__restrict__ xq, int32_t *__restrict__ xexp, int ldq,
                                                         float *__restrict__ hout) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= n) return;
     const int nq = d >> 2;
     const size_t base = (size_t)row * nq;
-    f32x4 v[NV];
+    f32x4 x[NV], v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = min(i * 64 + lane, nq - 1);
+        x[i] = reinterpret_cast<const f32x4 *>(a.x)[base + c];
+        v[i] = x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        if (i * 64 + lane < nq) reinterpret_cast<f32x4 *>(a.streams[a.ns - 1])[base + i * 64 + lane] = x[i];
+    for (int j0 = 0; j0 < a.ns - 1; j0 += 4) {
+        f32x4 sv[4][NV];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const f32x4 *sp = reinterpret_cast<const f32x4 *>(a.streams[min(j0 + q, a.ns - 2)]) + base;
+#pragma unroll
+            for (int i = 0; i < NV; i++) sv[q][i] = sp[min(i * 64 + lane, nq - 1)];
+        }
+        AVA_ISSUE_FENCE();
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (j0 + q < a.ns - 1) {
+                const float w = a.w[j0 + q];
+#pragma unroll
+                for (int i = 0; i < NV; i++)
+#pragma unroll
+                    for (int z = 0; z < 4; z++) v[i][z] = v[i][z] + sv[q][i][z] * w;
+            }
+    }
+    const float wl = a.w[a.ns - 1];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int c = i * 64 + lane;
         if (c < nq) {
-            const f32x4 x = reinterpret_cast<const f32x4 *>(a.x)[base + c];
-            reinterpret_cast<f32x4 *>(a.streams[a.ns - 1])[base + c] = x;
-            f32x4 mix = x;
-            // the earlier streams in batches of 4 whose loads are all in flight before the adds (in j order)
-            for (int j0 = 0; j0 < a.ns - 1; j0 += 4) {
-                f32x4 sv[4];
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    sv[q] = reinterpret_cast<const f32x4 *>(a.streams[min(j0 + q, a.ns - 2)])[base + c];
-                AVA_ISSUE_FENCE();
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    if (j0 + q < a.ns - 1) {
-                        const float w = a.w[j0 + q];
-#pragma unroll
-                        for (int z = 0; z < 4; z++) mix[z] = mix[z] + sv[q][z] * w;
-                    }
-            }
-            const float wl = a.w[a.ns - 1];
-#pragma unroll
-            for (int z = 0; z < 4; z++) mix[z] = mix[z] + x[z] * wl;
-            reinterpret_cast<f32x4 *>(a.x)[base + c] = mix;
-            v[i] = mix;
+            for (int z = 0; z < 4; z++) v[i][z] = v[i][z] + x[i][z] * wl;
+            reinterpret_cast<f32x4 *>(a.x)[base + c] = v[i];
         } else {
             v[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -1177,7 +1188,9 @@ int dense_rms(float *x, float *const *streams, const float *w, int ns, int n, in
     }
     a.ns = ns;
     a.n4 = (size_t)n * d / 4;
-    const dim3 grid(ceil_div(n, 4)), block(256);
+    // few rows: one wave per workgroup, so the rows spread over more CUs
+    const int rpb = n <= 1024 ? 1 : 4;
+    const dim3 grid(ceil_div(n, rpb)), block(64 * rpb);
     if (planes == 1) dense_rms_kernel<1, 4><<<grid, block, 0, st>>>(a, n, d, gain, xq, xexp, ldq, hout);
     else if (planes == 2) dense_rms_kernel<2, 4><<<grid, block, 0, st>>>(a, n, d, gain, xq, xexp, ldq, hout);
     else dense_rms_kernel<3, 4><<<grid, block, 0, st>>>(a, n, d, gain, xq, xexp, ldq, hout);
