@@ -1010,10 +1010,15 @@ __global__ __launch_bounds__(256) void rms_gate_cols_kernel(const float *__restr
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (c < nc) {
         const int kb = ks * (d / GKS), ke = kb + d / GKS;  // (ke - kb) % 32 == 0 (rms_gate_fits)
-        for (int k0 = kb; k0 < ke; k0 += 32) {
-            float wv[32];
+        // 32 weights per step; the next step's 32 are in flight while this step's are used
+        float wv[32], wn[32];
 #pragma unroll
-            for (int j = 0; j < 32; j++) wv[j] = w[(size_t)(k0 + j) * nc + c];
+        for (int j = 0; j < 32; j++) wv[j] = w[(size_t)(kb + j) * nc + c];
+        for (int k0 = kb; k0 < ke; k0 += 32) {
+            if (k0 + 32 < ke) {
+#pragma unroll
+                for (int j = 0; j < 32; j++) wn[j] = w[(size_t)(k0 + 32 + j) * nc + c];
+            }
             AVA_ISSUE_FENCE();
 #pragma unroll
             for (int h = 0; h < 2; h++) {
@@ -1029,6 +1034,8 @@ __global__ __launch_bounds__(256) void rms_gate_cols_kernel(const float *__restr
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[r] = fmaf(hv[r][j >> 2][j & 3], wv[16 * h + j], acc[r]);
             }
+#pragma unroll
+            for (int j = 0; j < 32; j++) wv[j] = wn[j];
         }
     }
 #pragma unroll
