@@ -218,21 +218,26 @@ __global__ __launch_bounds__(256) void mem_post_kernel(const float *__restrict__
     constexpr int NV = 4;  // d = 1024: 16 channels per lane (d < 1024 leaves lanes idle)
     const int c0 = lane * 16;
     const bool on = c0 < d;
-    f32x4 v[NV];
-    float ss = 0.0f;
+    f32x4 v[NV], gvs[NV];
+    // the row's y and g loads all in flight before the first use
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         v[i] = on ? reinterpret_cast<const f32x4 *>(y + (size_t)row * d + c0)[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        gvs[i] = on ? reinterpret_cast<const f32x4 *>(g + (size_t)row * ldg + c0)[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    AVA_ISSUE_FENCE();
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
 #pragma unroll
         for (int z = 0; z < 4; z++) ss += v[i][z] * v[i][z];
-    }
     ss += __shfl_xor(ss, 1, 64);
     ss += __shfl_xor(ss, 2, 64);
     const float inv = 1.0f / sqrtf(ss * (1.0f / 64.0f) + 0.0f + NORM_EPS);
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const f32x4 gv = on ? reinterpret_cast<const f32x4 *>(g + (size_t)row * ldg + c0)[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4 gv = gvs[i];
 #pragma unroll
         for (int z = 0; z < 4; z++) {
             const float gz = gv[z];
