@@ -6,6 +6,7 @@ gpu/state.rs), over ava_model_* of include/ava.h.
     logits = m.forward_with_state(ids, st)   state.rs:684-865 (ids [B, T] int32 on the GPU)
     logits = m.forward(ids)             model.rs:1171: a fresh state per call
     nats = m.cb_learn(logits, next, st) Model::cb_learn (gpu/v51b.rs:600-604, gpu/fast4/cb.rs:25-84)
+    m = Model.from_safetensors(path, arch)   a model file in the reference's names (ckpt.rs, model.rs:805-905)
     m.decode_step(ids, st, logits, prev_logits, prev_next)   cb_learn(prev) then forward, overlapped
 
 `params` is a dict of float32 numpy arrays keyed as ava_amd.synth (the reference's VarMap names).
@@ -91,6 +92,13 @@ class Model:
         h = C.c_void_p()
         check(lib().ava_model_new(C.byref(ccfg), C.byref(prm), C.byref(h)), "ava_model_new")
         self.h = h
+
+    @classmethod
+    def from_safetensors(cls, path: str, arch: str, strict: bool = True, planes: int = 3, **overrides) -> "Model":
+        """A model file in the reference's naming with its arch string (ava_amd.checkpoint)."""
+        from .checkpoint import load_safetensors
+        cfg, params = load_safetensors(path, arch, strict=strict, **overrides)
+        return cls(cfg, params, planes=planes)
 
     def __del__(self):
         if getattr(self, "h", None):
