@@ -62,6 +62,8 @@ def lib():
     L = C.CDLL(LIB_PATH)
     L.ava_last_error.restype = C.c_char_p
     L.ava_version.restype = C.c_char_p
+    L.ava_fnv1a64.argtypes = [vp, sz, C.c_uint64]
+    L.ava_fnv1a64.restype = C.c_uint64
     sig = {
         "ava_q8_ldk": [i32],
         "ava_q8_pack": [vp, i32, i32, vp, vp, vp],

@@ -30,3 +30,13 @@ int fail(int code, const char *fmt, ...) {
 extern "C" const char *ava_last_error(void) { return g_err; }
 
 extern "C" const char *ava_version(void) { return "ava_amd 0.1 (gfx950)"; }
+
+// FNV-1a over n bytes, continuing from h (the reference's model fingerprint, gpu/state.rs:1095-1107).
+extern "C" uint64_t ava_fnv1a64(const void *p, size_t n, uint64_t h) {
+    const unsigned char *b = static_cast<const unsigned char *>(p);
+    for (size_t i = 0; i < n; ++i) {
+        h ^= b[i];
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}

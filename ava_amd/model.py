@@ -51,6 +51,7 @@ class State:
         self.cb_scale = torch.ones(B, dtype=torch.float64, device=device) if g else None
         self.cb_code = z(B, g) if g else None
         self.eng_len_dev = torch.zeros(1, dtype=torch.int32, device=device) if device_len else None
+        self.seen = 0  # tokens each stream has consumed (State::seen, state.rs:94-116)
 
     def c(self):
         p = lambda t: t.data_ptr() if t is not None else None
@@ -88,6 +89,8 @@ class Model:
                       momentum=c["momentum"], cap=c["cap"], planes=planes, cb_units=c.get("cb_units", 0),
                       cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0),
                       eng_half=int(bool(c.get("eng_half", False))))
+        from .state_io import fingerprint
+        self.fingerprint = fingerprint(self.cfg, params)  # keys saved states (Model::fingerprint)
         torch.cuda.init()
         h = C.c_void_p()
         check(lib().ava_model_new(C.byref(ccfg), C.byref(prm), C.byref(h)), "ava_model_new")
@@ -108,6 +111,18 @@ class Model:
     def state(self, B: int, eng_cap: int = 0, device_len: bool = False) -> State:
         return State(self.cfg, B, eng_cap, device_len=device_len)
 
+    def save_state(self, st: State, path: str) -> None:
+        """Write st to path (safetensors, whole or absent), keyed by this model's fingerprint
+        (State::save, gpu/state.rs:1225-1232). Call it between steps: it synchronizes on the copies."""
+        from .state_io import save_state
+        save_state(path, st, self.cfg, self.fingerprint)
+
+    def load_state(self, path: str, device_len: bool = False) -> State:
+        """The state save_state wrote; ValueError when another model wrote it (State::load,
+        gpu/state.rs:1236-1246)."""
+        from .state_io import load_state
+        return load_state(path, self.cfg, self.fingerprint, device="cuda", device_len=device_len)
+
     def capture_decode(self, st: State, ids: torch.Tensor, logits: torch.Tensor, nxt: torch.Tensor | None = None,
                        nats: torch.Tensor | None = None) -> "DecodeGraph":
         """One decode step (the forward of ids [B, T] into logits, then, with nxt, the online table's
@@ -118,12 +133,12 @@ class Model:
             raise ValueError("capture_decode: the state needs device_len=True")
         check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")  # the graph keeps the scratch's addresses
         g = torch.cuda.CUDAGraph()
-        n0 = st.eng_len
+        n0, s0 = st.eng_len, st.seen
         with torch.cuda.graph(g):
             self.forward_with_state(ids, st, logits)
             if nxt is not None:
                 self.cb_learn(logits, nxt, st, nats=nats)
-        st.eng_len = n0  # the capture ran nothing: the store did not advance
+        st.eng_len, st.seen = n0, s0  # the capture ran nothing: the store did not advance
         return DecodeGraph(g, st, ids.shape[1])
 
     def forward_with_state(self, ids: torch.Tensor, st: State, logits: torch.Tensor | None = None, want_logits=True):
@@ -138,6 +153,7 @@ class Model:
                                       C.c_void_p(logits.data_ptr()) if want_logits else None, stream),
               "ava_model_forward")
         st.eng_len = cst.eng_len
+        st.seen += T
         return logits
 
     def decode_step(self, ids: torch.Tensor, st: State, logits: torch.Tensor, prev_logits: torch.Tensor | None = None,
@@ -177,6 +193,7 @@ class Model:
                                           C.c_void_p(logits.data_ptr()), pl, ld, pn, pz, stream),
               "ava_model_decode_step")
         st.eng_len = cst.eng_len
+        st.seen += T
         return logits
 
     def capture_decode_step(self, st: State, ids: torch.Tensor, logits: torch.Tensor, prev_logits: torch.Tensor,
@@ -186,10 +203,10 @@ class Model:
             raise ValueError("capture_decode_step: the state needs device_len=True")
         check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")
         g = torch.cuda.CUDAGraph()
-        n0 = st.eng_len
+        n0, s0 = st.eng_len, st.seen
         with torch.cuda.graph(g):
             self.decode_step(ids, st, logits, prev_logits, prev_next, prev_nats)
-        st.eng_len = n0
+        st.eng_len, st.seen = n0, s0
         return DecodeGraph(g, st, ids.shape[1])
 
     def cb_learn(self, logits: torch.Tensor, nxt: torch.Tensor, st: State, nats: torch.Tensor | None = None):
@@ -250,3 +267,4 @@ class DecodeGraph:
             raise ValueError(f"decode graph: the engram store holds {st.eng_len} of {st.eng_cap} entries")
         self.graph.replay()
         st.eng_len += self.T
+        st.seen += self.T

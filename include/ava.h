@@ -37,6 +37,11 @@ enum {
 const char *ava_last_error(void);
 const char *ava_version(void);
 
+/* FNV-1a 64 over n host bytes, continuing from h (start: 0xcbf29ce484222325). The model fingerprint a
+ * saved state is keyed by hashes the configuration text and sampled weights with it; replaces the
+ * Fnv of gpu/state.rs:1095-1107 (Model::fingerprint, gpu/state.rs:1075-1092). */
+uint64_t ava_fnv1a64(const void *p, size_t n, uint64_t h);
+
 /* ------------------------------------------------------------------ int8 weights and products */
 
 /* One weight matrix in int8: W [din][dout] (applied x·W), stored transposed as qt [dout][din]
