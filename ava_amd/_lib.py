@@ -26,7 +26,7 @@ class Config(C.Structure):
                                    "eng_block", "eng_dim", "levels", "alif", "lif_scale", "value_residual",
                                    "dense", "relu2")] + \
                [("momentum", f32), ("cap", f32), ("planes", i32), ("cb_units", i32), ("cb_lr", f32), ("cb_half", f32),
-                ("eng_half", i32)]
+                ("eng_half", i32), ("eng_heads", i32)]
 
 
 BLOCK_FIELDS = ["lif_norm", "win", "beta_p", "theta", "arho", "again", "wout",
@@ -78,6 +78,7 @@ def lib():
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
         "ava_attend": [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, sz, vp],
+        "ava_attend_heads": [vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, sz, vp],
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
         "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],
@@ -91,6 +92,8 @@ def lib():
         fn.restype = i32
     L.ava_attend_part_floats.argtypes = [i32, i32, i32]
     L.ava_attend_part_floats.restype = sz
+    L.ava_attend_heads_part_floats.argtypes = [i32, i32, i32, i32, i32]
+    L.ava_attend_heads_part_floats.restype = sz
     L.ava_q8_workspace.argtypes = [i32, i32, i32]
     L.ava_q8_workspace.restype = sz
     if hasattr(L, "ava_model_free"):

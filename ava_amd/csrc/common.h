@@ -186,9 +186,10 @@ int rms_gate(const float *x, int n, int d, const float *gain, int planes, int8_t
 int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, int8_t *xq, int32_t *xexp, int ldq,
              hipStream_t st);
 // The engram read: the tiled causal form for T > ENGRAM_SPLIT_T, the chunk-split decode form (with
-// part, engram_split_floats of scratch) for T <= ENGRAM_SPLIT_T.
+// part, engram_split_floats of scratch) for T <= ENGRAM_SPLIT_T. A store row holds de dims in nh heads
+// of 32 or 64 (one head of 64: the single-head read; de / 32 heads: the reference's).
 constexpr int ENGRAM_SPLIT_T = 4;
-size_t engram_split_floats(int B, int T, int n0);
+size_t engram_split_floats(int B, int T, int n0, int de = 64, int nh = 1);
 // Optional work after the decode form's merge: the read's planes for the next product (xq [planes][rows]
 // [ldq], xexp [rows]; xq NULL: none), and the device store length advanced by T (adv NULL: none).
 struct PostRead {
@@ -198,9 +199,11 @@ struct PostRead {
     int *adv = nullptr;
 };
 int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, const int *n0p,
-           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post = {});
-int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
-                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post = {});
+           int B, int T, int de, int nh, float *out, float *part, size_t part_floats, hipStream_t st,
+           const PostRead &post = {});
+int engram_read(const float *qkv, int ldqkv, int B, int T, int de, int nh, void *ks, void *vs, int kv_half, int cap,
+                int n0, int *n0p, float *out, float *part, size_t part_floats, hipStream_t st,
+                const PostRead &post = {});
 int engram_advance(int *n0p, int T, int cap, hipStream_t st);
 // cb.hip: the cerebellum head (code with its unit lists, read-out with the online table, learning)
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,

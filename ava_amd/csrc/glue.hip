@@ -410,23 +410,28 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
 // previous tiles, exp); then O = O corr + P V (wave w: its quadrant of the 64 x 64 output, kept in
 // the MFMA accumulator across tiles); O / den at the end. Equal to attend_kernel up to the products'
 // summation order.
-template <typename KV>
+// Heads: the store's rows hold nh heads of HD dims (de = nh HD, the reference's heads of 32,
+// gpu/memory.rs:610-700); workgroup (query block, b nh + h) reads head h: its query, key and value
+// dims h HD .. h HD + HD - 1. For HD = 32 the tiles' dims 32..63 stay zero and the waves of output
+// columns 32..63 skip the P V products.
+template <typename KV, int HD>
 __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restrict__ q, int ldq,
                                                           const KV *__restrict__ ks, const KV *__restrict__ vs,
                                                           int cap, int n0, const int *n0p, int T, float scale,
-                                                          float *__restrict__ out) {
+                                                          int de, int nh, float *__restrict__ out) {
+    static_assert(HD == 32 || HD == 64, "head size 32 or 64");
     if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device (a replayed graph)
     constexpr int L = 65;               // LDS row stride (odd: a column read hits 32 banks)
     __shared__ float sQ[64 * L], sK[64 * L], sV[64 * L], sP[64 * L];
     __shared__ float s_corr[64], s_den[64];
-    const int bi = blockIdx.y, qb = blockIdx.x * 64;
+    const int bi = blockIdx.y / nh, hh = blockIdx.y - bi * nh, qb = blockIdx.x * 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lc = lane & 31;
     const int row0 = (wave >> 1) * 32, col0 = (wave & 1) * 32;
     const int r = tid >> 2, sub = tid & 3;  // the softmax's row and quarter
-    const KV *kb = ks + (size_t)bi * cap * 64, *vb = vs + (size_t)bi * cap * 64;
+    const KV *kb = ks + (size_t)bi * cap * de + hh * HD, *vb = vs + (size_t)bi * cap * de + hh * HD;
     for (int i = tid; i < 64 * 64; i += 256) {
         const int rr = i >> 6, cc = i & 63;
-        sQ[rr * L + cc] = qb + rr < T ? q[((size_t)bi * T + qb + rr) * ldq + cc] : 0.0f;
+        sQ[rr * L + cc] = qb + rr < T && cc < HD ? q[((size_t)bi * T + qb + rr) * ldq + hh * HD + cc] : 0.0f;
     }
     auto qrow = [&](int i) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); };
     float mx = -INFINITY, den = 0.0f;
@@ -437,8 +442,8 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     // into registers while this tile is computed
     float kr[16], vr[16];
     auto fetch = [&](int k0) {
-        const bool ok = k0 + r < kend;
-        const size_t o16 = (size_t)(k0 + (ok ? r : 0)) * 64 + sub * 16;
+        const bool ok = k0 + r < kend && sub * 16 < HD;
+        const size_t o16 = (size_t)(k0 + (ok ? r : 0)) * de + (ok ? sub * 16 : 0);
         KvLane<KV>::load16(kb + o16, kr);
         KvLane<KV>::load16(vb + o16, vr);
         if (!ok)
@@ -459,7 +464,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
             f32x16 sa = {};
             const int fr = lane & 31, h = lane >> 5;
 #pragma unroll 8
-            for (int x = 0; x < 64; x += 2)
+            for (int x = 0; x < HD; x += 2)
                 sa = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[(row0 + fr) * L + x + h], sK[(col0 + fr) * L + x + h], sa,
                                                           0, 0, 0);
 #pragma unroll
@@ -497,7 +502,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 16; i++) o[i] *= s_corr[row0 + qrow(i)];
-        {
+        if (col0 < HD) {
             const int fr = lane & 31, h = lane >> 5;
 #pragma unroll 8
             for (int x = 0; x < 64; x += 2)
@@ -510,7 +515,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int rr = row0 + qrow(i);
-        if (qb + rr < T) out[((size_t)bi * T + qb + rr) * 64 + col0 + lc] = o[i] / s_den[rr];
+        if (qb + rr < T && col0 < HD) out[((size_t)bi * T + qb + rr) * de + hh * HD + col0 + lc] = o[i] / s_den[rr];
     }
 }
 
@@ -543,27 +548,36 @@ __device__ __forceinline__ float row_sum8(float v) {
     return v + dpp_f<0x141>(v);
 }
 
-// Lane layout: a key's 64 dims are read by LPK = 64 / DPL lanes (16 for f32, 8 for fp16), so a wave
-// holds G = 64 / LPK key groups and reads G whole keys per 16-byte load instruction; each group takes
-// U = 32 / G keys of a 32-key iteration (keys G j + group).
-template <typename KV>
+// The sum over each group of 4 lanes (quad_perm [1,0,3,2], [2,3,0,1]), in every lane.
+__device__ __forceinline__ float row_sum4(float v) {
+    v += dpp_f<0xB1>(v);
+    return v + dpp_f<0x4E>(v);
+}
+
+// Lane layout: a key's HD dims are read by LPK = HD / DPL lanes (HD 64: 16 for f32, 8 for fp16; HD 32:
+// 8 and 4), so a wave holds G = 64 / LPK key groups and reads G whole keys per 16-byte load
+// instruction; each group takes U = 32 / G keys of a 32-key iteration (keys G j + group). Heads: the
+// store's rows hold nh heads of HD dims; workgroup (s, row nh + h) reads head h of the row's query.
+// part [row nh + h][nsplit][HD + 2].
+template <typename KV, int HD>
 __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restrict__ q, int ldq,
                                                            const KV *__restrict__ ks, const KV *__restrict__ vs,
                                                            int cap, int n0, const int *n0p, int T, float scale,
-                                                           int nsplit, float *__restrict__ part) {
+                                                           int de, int nh, int nsplit, float *__restrict__ part) {
     if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device: chunks past it are empty
-    constexpr int DPL = KvLane<KV>::DPL, LPK = 64 / DPL, G = 64 / LPK, U = 32 / G, NG = 4 * G;
+    constexpr int DPL = KvLane<KV>::DPL, LPK = HD / DPL, G = 64 / LPK, U = 32 / G, NG = 4 * G;
+    static_assert(LPK == 4 || LPK == 8 || LPK == 16, "lanes per key");
     __shared__ float sm[NG], sl[NG];
-    __shared__ float so[NG][64];
-    const int s = blockIdx.x, row = blockIdx.y;
+    __shared__ float so[NG][HD];
+    const int s = blockIdx.x, rh = blockIdx.y, row = rh / nh, hh = rh - row * nh;
     const int b = row / T, t = row - b * T;
     const int klen = n0 + t + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane / LPK, cl = (lane % LPK) * DPL;
     float qv[DPL];
 #pragma unroll
-    for (int z = 0; z < DPL; z++) qv[z] = q[(size_t)row * ldq + cl + z];
+    for (int z = 0; z < DPL; z++) qv[z] = q[(size_t)row * ldq + hh * HD + cl + z];
     const int kb = s * ACH + wave * (ACH / 4), ke = min(kb + ACH / 4, klen);
-    const KV *kbase = ks + (size_t)b * cap * 64 + cl, *vbase = vs + (size_t)b * cap * 64 + cl;
+    const KV *kbase = ks + (size_t)b * cap * de + hh * HD + cl, *vbase = vs + (size_t)b * cap * de + hh * HD + cl;
     float m = -INFINITY, l = 0.0f, o[DPL];
 #pragma unroll
     for (int z = 0; z < DPL; z++) o[z] = 0.0f;
@@ -573,8 +587,8 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
         for (int j = 0; j < U; j++) {
             const int kk = k0 + G * j + grp;
             if (kk < ke) {
-                KvLane<KV>::load(kbase + (size_t)kk * 64, kv[j]);
-                KvLane<KV>::load(vbase + (size_t)kk * 64, vv[j]);
+                KvLane<KV>::load(kbase + (size_t)kk * de, kv[j]);
+                KvLane<KV>::load(vbase + (size_t)kk * de, vv[j]);
             } else {
 #pragma unroll
                 for (int z = 0; z < DPL; z++) kv[j][z] = vv[j][z] = 0.0f;
@@ -586,7 +600,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
             float a = kv[j][0] * qv[0];
 #pragma unroll
             for (int z = 1; z < DPL; z++) a = fmaf(kv[j][z], qv[z], a);
-            a = (LPK == 16 ? row_sum16(a) : row_sum8(a)) * scale;
+            a = (LPK == 16 ? row_sum16(a) : LPK == 8 ? row_sum8(a) : row_sum4(a)) * scale;
             sc[j] = (k0 + G * j + grp < ke) ? a : -INFINITY;
             bm = fmaxf(bm, sc[j]);
         }
@@ -613,7 +627,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
 #pragma unroll
     for (int z = 0; z < DPL; z++) so[gi][cl + z] = o[z];
     __syncthreads();
-    if (threadIdx.x < 64) {
+    if (threadIdx.x < HD) {
         const int c = threadIdx.x;
         float M = -INFINITY;
 #pragma unroll
@@ -627,7 +641,7 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
                 O = fmaf(so[i][c], w, O);
             }
         }
-        float *pr = part + ((size_t)row * nsplit + s) * 66;
+        float *pr = part + ((size_t)rh * nsplit + s) * (HD + 2);
         if (c == 0) {
             pr[0] = M;
             pr[1] = L;
@@ -636,36 +650,40 @@ __global__ __launch_bounds__(256) void attend_split_kernel(const float *__restri
     }
 }
 
-// out [row][64] = the merge of the row's chunk partials: M = max m_s, L = sum l_s e^(m_s - M),
+// out [row][h HD + c] = the merge of head h's chunk partials: M = max m_s, L = sum l_s e^(m_s - M),
 // o = sum o_s e^(m_s - M) / L, the terms added in chunk order. Lane s takes chunk s's (m, l) and
-// weight; every lane's o_s loads for 16 chunks are in flight together.
-// With P > 0 the row's planes (quant_rows_kernel's, the next product's input) are written too, and with
-// adv the store length on the device advances by T (store_advance_kernel's step: every reader of it
-// in this forward, the store append and the chunk reads, ran before this kernel).
-template <int P>
+// weight; every lane's o_s loads for 16 chunks are in flight together. Workgroup row nh + h.
+// With P > 0 (one head of 64) the row's planes (quant_rows_kernel's, the next product's input) are
+// written too, and with adv the store length on the device advances by T (store_advance_kernel's
+// step: every reader of it in this forward, the store append and the chunk reads, ran before this
+// kernel).
+template <int P, int HD>
 __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int nsplit,
                                                             float *__restrict__ out, int8_t *__restrict__ xq,
                                                             int32_t *__restrict__ xexp, int ldq, int *adv, int T,
-                                                            int cap) {
-    const int row = blockIdx.x, c = threadIdx.x;
-    const float *pr = part + (size_t)row * nsplit * 66;
+                                                            int cap, int de, int nh) {
+    static_assert(P == 0 || HD == 64, "planes need one head of 64");
+    constexpr int PS = HD + 2;
+    const int rh = blockIdx.x, row = rh / nh, hh = rh - row * nh, c = threadIdx.x;
+    const float *pr = part + (size_t)rh * nsplit * PS;
     float M = -INFINITY;
     for (int s0 = 0; s0 < nsplit; s0 += 64)
-        if (s0 + c < nsplit) M = fmaxf(M, pr[(size_t)(s0 + c) * 66]);
+        if (s0 + c < nsplit) M = fmaxf(M, pr[(size_t)(s0 + c) * PS]);
     M = ava::wave_max(M);
     float L = 0.0f, O = 0.0f;
     for (int s0 = 0; s0 < nsplit; s0 += 64) {
         const int cnt = min(64, nsplit - s0);
         float ms = -INFINITY, ls = 0.0f;
         if (c < cnt) {
-            ms = pr[(size_t)(s0 + c) * 66];
-            ls = pr[(size_t)(s0 + c) * 66 + 1];
+            ms = pr[(size_t)(s0 + c) * PS];
+            ls = pr[(size_t)(s0 + c) * PS + 1];
         }
         const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
         for (int j0 = 0; j0 < cnt; j0 += 16) {
             float ov[16];
 #pragma unroll
-            for (int j = 0; j < 16; j++) ov[j] = j0 + j < cnt ? pr[(size_t)(s0 + j0 + j) * 66 + 2 + c] : 0.0f;
+            for (int j = 0; j < 16; j++)
+                ov[j] = j0 + j < cnt && c < HD ? pr[(size_t)(s0 + j0 + j) * PS + 2 + c] : 0.0f;
             AVA_ISSUE_FENCE();
 #pragma unroll
             for (int j = 0; j < 16; j++) {
@@ -679,7 +697,7 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
         }
     }
     const float o = O / L;
-    out[(size_t)row * 64 + c] = o;
+    if (c < HD) out[(size_t)row * de + hh * HD + c] = o;
     if constexpr (P > 0) {
         const int e = ava::plane_exp(ava::wave_max(fabsf(o)));
         if (c == 0) xexp[row] = e;
@@ -693,7 +711,7 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
             for (int z = 64 + c; z < ldq; z += 64) qr[z] = 0;
         }
     }
-    if (adv && row == 0 && c == 0) *adv = min(*adv + T, cap);
+    if (adv && rh == 0 && c == 0) *adv = min(*adv + T, cap);
 }
 
 // The device store length advances by T after a forward, saturating at the store's capacity (the
@@ -702,18 +720,18 @@ __global__ void store_advance_kernel(int *n0p, int T, int cap) {
     if (threadIdx.x == 0) *n0p = min(*n0p + T, cap);
 }
 
-// Append this forward's keys and values to the store: store[b][n0 + t] = kv[b T + t] (n0 from the
-// device when n0p).
+// Append this forward's keys and values to the store: store[b][n0 + t] = kv[b T + t], de values each
+// (keys at kv's columns 0..de-1, values at de..2de-1; n0 from the device when n0p).
 template <typename KV>
 __global__ void store_append_kernel(const float *__restrict__ kv, int ldkv, int T, int B, int cap, int n0,
-                                    const int *n0p, KV *__restrict__ ks, KV *__restrict__ vs) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over B*T*64
-    if (i >= B * T * 64) return;
+                                    const int *n0p, int de, KV *__restrict__ ks, KV *__restrict__ vs) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over B*T*de
+    if (i >= B * T * de) return;
     if (n0p) n0 = min(*n0p, cap - T);
-    const int c = i & 63, row = i >> 6, bi = row / T, t = row - bi * T;
-    const size_t dst = ((size_t)bi * cap + n0 + t) * 64 + c;
+    const int row = i / de, c = i - row * de, bi = row / T, t = row - bi * T;
+    const size_t dst = ((size_t)bi * cap + n0 + t) * de + c;
     kv_put(ks, dst, kv[(size_t)row * ldkv + c]);
-    kv_put(vs, dst, kv[(size_t)row * ldkv + 64 + c]);
+    kv_put(vs, dst, kv[(size_t)row * ldkv + de + c]);
 }
 
 // ------------------------------------------------------------------ dense mix
@@ -1109,8 +1127,9 @@ int mem_post(const float *y, int n, int d, const float *g, int ldg, int planes, 
     return AVA_OK;
 }
 
-size_t engram_split_floats(int B, int T, int n0) {
-    return T <= ENGRAM_SPLIT_T ? (size_t)B * T * ceil_div(n0 + T, ACH) * 66 : 0;
+size_t engram_split_floats(int B, int T, int n0, int de, int nh) {
+    const int hd = de / (nh > 0 ? nh : 1);
+    return T <= ENGRAM_SPLIT_T ? (size_t)B * T * nh * ceil_div(n0 + T, ACH) * (hd + 2) : 0;
 }
 
 // The query-block read on the fp32 MFMA (AVA_ATTEND_MFMA=0: the VALU form; tuning).
@@ -1125,61 +1144,78 @@ bool attend_mfma() {
 
 // With n0p (the store length on the device) the chunk grid covers the whole store, so a captured
 // launch serves every length; chunks past the length are empty and merge as nothing.
-template <typename KV>
+template <typename KV, int HD>
 int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n0, const int *n0p, int B, int T,
-             float *out, float *part, size_t part_floats, const PostRead &post, hipStream_t st) {
-    const float scale = (float)(1.0 / sqrt(64.0));
+             int de, int nh, float *out, float *part, size_t part_floats, const PostRead &post, hipStream_t st) {
+    const float scale = (float)(1.0 / sqrt((double)HD));
     if (T <= ENGRAM_SPLIT_T) {
         const int span = n0p ? cap - T : n0;
         const int nsplit = ceil_div(span + T, ACH);
-        AVA_REQUIRE(part && part_floats >= engram_split_floats(B, T, span), AVA_ERR_ARG,
-                    "attend: the decode read needs %zu floats of partials", engram_split_floats(B, T, span));
-        attend_split_kernel<KV><<<dim3(nsplit, B * T), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, nsplit,
-                                                                     part);
+        const size_t need = engram_split_floats(B, T, span, de, nh);
+        AVA_REQUIRE(part && part_floats >= need, AVA_ERR_ARG, "attend: the decode read needs %zu floats of partials",
+                    need);
+        attend_split_kernel<KV, HD><<<dim3(nsplit, B * T * nh), 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale,
+                                                                              de, nh, nsplit, part);
         AVA_LAUNCHED("attend_split");
-#define AVA_AC(P_) \
-    attend_combine_kernel<P_><<<B * T, 64, 0, st>>>(part, nsplit, out, post.xq, post.xexp, post.ldq, post.adv, T, cap)
-        if (!post.xq) AVA_AC(0);
-        else if (post.planes == 1) AVA_AC(1);
-        else if (post.planes == 2) AVA_AC(2);
-        else AVA_AC(3);
+        if constexpr (HD == 64) {
+#define AVA_AC(P_)                                                                                                 \
+    attend_combine_kernel<P_, 64><<<B * T * nh, 64, 0, st>>>(part, nsplit, out, post.xq, post.xexp, post.ldq, post.adv, \
+                                                             T, cap, de, nh)
+            if (!post.xq) AVA_AC(0);
+            else if (post.planes == 1) AVA_AC(1);
+            else if (post.planes == 2) AVA_AC(2);
+            else AVA_AC(3);
 #undef AVA_AC
+        } else {
+            attend_combine_kernel<0, HD><<<B * T * nh, 64, 0, st>>>(part, nsplit, out, nullptr, nullptr, 0, post.adv, T,
+                                                                     cap, de, nh);
+        }
         AVA_LAUNCHED("attend_combine");
         return AVA_OK;
     }
-    dim3 grid(ceil_div(T, 64), B);
-    if (attend_mfma()) attend_mfma_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
+    dim3 grid(ceil_div(T, 64), B * nh);
+    if (attend_mfma() || HD != 64 || nh != 1)
+        attend_mfma_kernel<KV, HD><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, de, nh, out);
     else attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
     AVA_LAUNCHED("attend");
     return AVA_OK;
 }
 
 int attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, const int *n0p,
-           int B, int T, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post) {
+           int B, int T, int de, int nh, float *out, float *part, size_t part_floats, hipStream_t st,
+           const PostRead &post) {
     AVA_REQUIRE(B > 0 && T > 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
                 "attend: B=%d T=%d, a store of %d entries holds %d + %d", B, T, cap, n0, T);
-    AVA_REQUIRE(ldq >= 64 && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d", ldq);
-    AVA_REQUIRE(!post.xq || (post.planes >= 1 && post.planes <= 3 && post.ldq >= 64 && post.ldq % 64 == 0),
-                AVA_ERR_ARG, "attend: planes %d, ldq %d", post.planes, post.ldq);
-    if (kv_half)
-        return attend_t(q, ldq, (const __half *)ks, (const __half *)vs, cap, n0, n0p, B, T, out, part, part_floats,
-                        post, st);
-    return attend_t(q, ldq, (const float *)ks, (const float *)vs, cap, n0, n0p, B, T, out, part, part_floats, post,
-                    st);
+    AVA_REQUIRE(nh >= 1 && de % nh == 0 && (de / nh == 32 || de / nh == 64) && de % 64 == 0 && de <= 4096,
+                AVA_ERR_SHAPE, "attend: %d dims in %d heads (heads of 32 or 64, a multiple of 64 dims)", de, nh);
+    AVA_REQUIRE(ldq >= de && ldq % 4 == 0, AVA_ERR_SHAPE, "attend: ldq %d for %d dims", ldq, de);
+    AVA_REQUIRE(!post.xq || (nh == 1 && de == 64 && post.planes >= 1 && post.planes <= 3 && post.ldq >= 64 &&
+                             post.ldq % 64 == 0),
+                AVA_ERR_ARG, "attend: planes %d, ldq %d (planes: one head of 64)", post.planes, post.ldq);
+    const bool h32 = de / nh == 32;
+    if (kv_half) {
+        const __half *k = (const __half *)ks, *v = (const __half *)vs;
+        return h32 ? attend_t<__half, 32>(q, ldq, k, v, cap, n0, n0p, B, T, de, nh, out, part, part_floats, post, st)
+                   : attend_t<__half, 64>(q, ldq, k, v, cap, n0, n0p, B, T, de, nh, out, part, part_floats, post, st);
+    }
+    const float *k = (const float *)ks, *v = (const float *)vs;
+    return h32 ? attend_t<float, 32>(q, ldq, k, v, cap, n0, n0p, B, T, de, nh, out, part, part_floats, post, st)
+               : attend_t<float, 64>(q, ldq, k, v, cap, n0, n0p, B, T, de, nh, out, part, part_floats, post, st);
 }
 
-int engram_read(const float *qkv, int ldqkv, int B, int T, void *ks, void *vs, int kv_half, int cap, int n0,
-                int *n0p, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post) {
+int engram_read(const float *qkv, int ldqkv, int B, int T, int de, int nh, void *ks, void *vs, int kv_half, int cap,
+                int n0, int *n0p, float *out, float *part, size_t part_floats, hipStream_t st, const PostRead &post) {
     AVA_REQUIRE(n0 + T <= cap, AVA_ERR_SHAPE, "engram: store of %d entries holds %d + %d", cap, n0, T);
-    const int total = B * T * 64;
+    AVA_REQUIRE(ldqkv >= 3 * de, AVA_ERR_SHAPE, "engram: ldqkv %d for %d dims", ldqkv, de);
+    const int total = B * T * de;
     if (kv_half)
-        store_append_kernel<__half><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, n0p,
+        store_append_kernel<__half><<<ceil_div(total, 256), 256, 0, st>>>(qkv + de, ldqkv, T, B, cap, n0, n0p, de,
                                                                            (__half *)ks, (__half *)vs);
     else
-        store_append_kernel<float><<<ceil_div(total, 256), 256, 0, st>>>(qkv + 64, ldqkv, T, B, cap, n0, n0p,
+        store_append_kernel<float><<<ceil_div(total, 256), 256, 0, st>>>(qkv + de, ldqkv, T, B, cap, n0, n0p, de,
                                                                           (float *)ks, (float *)vs);
     AVA_LAUNCHED("store_append");
-    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, n0p, B, T, out, part, part_floats, st, post);
+    return attend(qkv, ldqkv, ks, vs, kv_half, cap, n0, n0p, B, T, de, nh, out, part, part_floats, st, post);
 }
 
 int engram_advance(int *n0p, int T, int cap, hipStream_t st) {
@@ -1243,5 +1279,18 @@ extern "C" size_t ava_attend_part_floats(int B, int T, int n0) { return ava::eng
 extern "C" int ava_attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B,
                           int T, float *out, float *part, size_t part_floats, ava_stream stream) {
     AVA_REQUIRE(q && ks && vs && out, AVA_ERR_ARG, "attend: NULL argument");
-    return ava::attend(q, ldq, ks, vs, kv_half, cap, n0, nullptr, B, T, out, part, part_floats, (hipStream_t)stream);
+    return ava::attend(q, ldq, ks, vs, kv_half, cap, n0, nullptr, B, T, 64, 1, out, part, part_floats,
+                       (hipStream_t)stream);
+}
+
+extern "C" size_t ava_attend_heads_part_floats(int B, int T, int n0, int de, int heads) {
+    return heads >= 1 ? ava::engram_split_floats(B, T, n0, de, heads) : 0;
+}
+
+extern "C" int ava_attend_heads(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0,
+                                int B, int T, int de, int heads, float *out, float *part, size_t part_floats,
+                                ava_stream stream) {
+    AVA_REQUIRE(q && ks && vs && out, AVA_ERR_ARG, "attend_heads: NULL argument");
+    return ava::attend(q, ldq, ks, vs, kv_half, cap, n0, nullptr, B, T, de, heads, out, part, part_floats,
+                       (hipStream_t)stream);
 }

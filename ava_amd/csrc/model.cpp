@@ -24,6 +24,9 @@
 
 namespace {
 
+// The engram's heads: eng_heads <= 1 is one head of eng_dim.
+int eng_nh(const ava_config &c) { return c.eng_heads > 1 ? c.eng_heads : 1; }
+
 struct DevQW {
     ava_qw w{};
 };
@@ -386,7 +389,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     if (int e = ensure_scratch(m, (size_t)N)) return e;
     if (c.eng_block >= 0) {
         // sized for the fullest store this state can reach, so a decode loop allocates once
-        const size_t need = ava::engram_split_floats(B, T, s->eng_cap - T);
+        const size_t need = ava::engram_split_floats(B, T, s->eng_cap - T, c.eng_dim, eng_nh(c));
         if (need > m->att_part_floats) {
             AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "forward: the engram read needs more scratch, and the model's "
                         "scratch is frozen (a captured graph uses it)");
@@ -450,7 +453,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.eqkv.w, ava::Q8_STORE, m->qkv, 3 * de, nullptr, st));
             // the decode form's merge also writes the read's planes and advances the device store length
             ava::PostRead post;
-            if (T <= ava::ENGRAM_SPLIT_T) {
+            if (T <= ava::ENGRAM_SPLIT_T && eng_nh(c) == 1) {
                 post.xq = m->xq;
                 post.xexp = m->xexp;
                 post.ldq = ava::q8_ldk(de);
@@ -458,7 +461,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
                 post.adv = s->eng_len_dev;
                 advanced = s->eng_len_dev != nullptr;
             }
-            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, s->eng_k, s->eng_v, c.eng_half, s->eng_cap, s->eng_len,
+            AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, de, eng_nh(c), s->eng_k, s->eng_v, c.eng_half, s->eng_cap, s->eng_len,
                                                    s->eng_len_dev, m->eo, m->att_part, m->att_part_floats, st, post));
             if (!post.xq) AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
@@ -548,8 +551,11 @@ extern "C" int ava_model_new(const ava_config *cfg, const ava_params *params, av
     AVA_REQUIRE(c.layers > 0 && c.layers <= 16, AVA_ERR_SHAPE, "model_new: %d layers (1..16)", c.layers);
     AVA_REQUIRE(c.vocab > 0 && c.gate_rank > 0 && c.gate_rank <= 32, AVA_ERR_SHAPE, "model_new: vocab=%d gate_rank=%d",
                 c.vocab, c.gate_rank);
-    AVA_REQUIRE(c.eng_block < c.layers && (c.eng_block < 0 || c.eng_dim == 64), AVA_ERR_UNSUPPORTED,
-                "model_new: engram block %d, dim %d (64)", c.eng_block, c.eng_dim);
+    AVA_REQUIRE(c.eng_block < c.layers &&
+                    (c.eng_block < 0 || (c.eng_dim == 64 && eng_nh(c) == 1) ||
+                     (c.eng_dim % 64 == 0 && c.eng_dim <= 1024 && c.eng_dim == 32 * eng_nh(c))),
+                AVA_ERR_UNSUPPORTED, "model_new: engram block %d, %d dims in %d heads (one head of 64, or heads of 32)",
+                c.eng_block, c.eng_dim, eng_nh(c));
     AVA_REQUIRE(c.levels == 1 || c.levels == 2, AVA_ERR_ARG, "model_new: levels %d", c.levels);
     AVA_REQUIRE(c.planes >= 1 && c.planes <= 3, AVA_ERR_ARG, "model_new: planes %d (1..3)", c.planes);
     AVA_REQUIRE(c.cb_units == 0 || (c.cb_units > 0 && c.cb_units % 32 == 0 && c.cb_units <= 16384), AVA_ERR_SHAPE,

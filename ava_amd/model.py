@@ -88,7 +88,7 @@ class Model:
                       value_residual=int(c["value_residual"]), dense=int(c["dense"]), relu2=int(c["relu2"]),
                       momentum=c["momentum"], cap=c["cap"], planes=planes, cb_units=c.get("cb_units", 0),
                       cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0),
-                      eng_half=int(bool(c.get("eng_half", False))))
+                      eng_half=int(bool(c.get("eng_half", False))), eng_heads=int(c.get("eng_heads", 1) or 1))
         from .state_io import fingerprint
         self.fingerprint = fingerprint(self.cfg, params)  # keys saved states (Model::fingerprint)
         torch.cuda.init()

@@ -179,9 +179,11 @@ def delta_rule_from(q, k, v, beta, la=None, f0=None):
     return y, F
 
 
-def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int) -> torch.Tensor:
-    """model/fstep.rs:303-329 per stream and query: q [B, T, 64]; ks, vs [B, cap, 64] (float32 or
-    float16) holding entries 0..n0+T-1; query t reads entries 0..n0+t. Returns out [B, T, 64]."""
+def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int, heads: int = 1) -> torch.Tensor:
+    """model/fstep.rs:303-329 per stream and query: q [B, T, de]; ks, vs [B, cap, de] (float32 or
+    float16) holding entries 0..n0+T-1; query t reads entries 0..n0+t. heads = 1: one head of 64;
+    heads > 1: heads of de / heads (32 or 64) side by side in each row, as memory::read
+    (gpu/memory.rs:610-700). Returns out [B, T, de]."""
     _need(q, torch.float32, "attend q")
     for t, nm in ((ks, "ks"), (vs, "vs")):
         _need(t, ks.dtype, f"attend {nm}")
@@ -189,12 +191,20 @@ def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int) -> torc
         raise ValueError("attend: the store is float32 or float16")
     B, T, de = q.shape
     cap = ks.shape[1]
-    if de != 64 or ks.shape != vs.shape or ks.shape[0] != B or ks.shape[2] != 64:
-        raise ValueError("attend: q [B, T, 64], ks and vs [B, cap, 64] are required")
+    if ks.shape != vs.shape or ks.shape[0] != B or ks.shape[2] != de:
+        raise ValueError("attend: q [B, T, de], ks and vs [B, cap, de] are required")
     out = torch.empty_like(q)
-    n = lib().ava_attend_part_floats(B, T, n0)
-    part = torch.empty(max(n, 1), dtype=torch.float32, device=q.device)
     half = int(ks.dtype == torch.float16)
-    check(lib().ava_attend(_p(q), 64, _p(ks), _p(vs), half, cap, n0, B, T, _p(out), _p(part), n, _stream()),
-          "ava_attend")
+    if heads == 1:
+        if de != 64:
+            raise ValueError("attend: one head of 64 dims (heads > 1 for wider rows)")
+        n = lib().ava_attend_part_floats(B, T, n0)
+        part = torch.empty(max(n, 1), dtype=torch.float32, device=q.device)
+        check(lib().ava_attend(_p(q), 64, _p(ks), _p(vs), half, cap, n0, B, T, _p(out), _p(part), n, _stream()),
+              "ava_attend")
+        return out
+    n = lib().ava_attend_heads_part_floats(B, T, n0, de, heads)
+    part = torch.empty(max(n, 1), dtype=torch.float32, device=q.device)
+    check(lib().ava_attend_heads(_p(q), de, _p(ks), _p(vs), half, cap, n0, B, T, de, heads, _p(out), _p(part), n,
+                                 _stream()), "ava_attend_heads")
     return out

@@ -14,7 +14,7 @@ Tensor names, where the reference has the same quantity (state.rs:1113-1197):
     meta.seen [B] u32       tokens each stream has consumed
     lif.{i}.v / .s / .a     [B, d] membrane, last spikes, adaptation (.a with ALIF)
     mem.{i}.f / .s          [B, nh, hs, hs] the fast weights F and the momentum S (.s with momentum)
-    eng.k / eng.v           [B, 1, len, eng_dim] the engram store's filled entries (one head), its dtype
+    eng.k / eng.v           [B, heads, len, eng_dim / heads] the engram store's filled entries, its dtype
     eng.valid [B] u32       the filled entries of each stream
 Names of this package only (the reference keeps the online table on the model, gpu/v51b.rs:189-217,
 and its store has no fixed capacity):
@@ -64,6 +64,13 @@ def _u32(v) -> torch.Tensor:
     return torch.from_numpy(np.array(list(v), dtype=np.uint32))
 
 
+def _heads(cfg: dict, t: torch.Tensor) -> torch.Tensor:
+    """Store rows [B, n, de] as the reference's [B, heads, n, hd] (a view)."""
+    nh = max(int(cfg.get("eng_heads", 1) or 1), 1)
+    B, n, de = t.shape
+    return t.view(B, n, nh, de // nh).permute(0, 2, 1, 3)
+
+
 def _ints(t: torch.Tensor) -> list:
     if t.dtype != torch.uint32:
         raise ValueError(f"a u32 tensor was expected, not {t.dtype}")
@@ -85,8 +92,8 @@ def state_tensors(st, cfg: dict, fp: int) -> dict:
         if cfg["momentum"] != 0.0:
             m[f"mem.{i}.s"] = cpu(st.mem_s[i])
     if st.eng_cap:
-        m["eng.k"] = cpu(st.eng_k[:, :n].unsqueeze(1))
-        m["eng.v"] = cpu(st.eng_v[:, :n].unsqueeze(1))
+        m["eng.k"] = cpu(_heads(cfg, st.eng_k[:, :n]))
+        m["eng.v"] = cpu(_heads(cfg, st.eng_v[:, :n]))
         m["eng.valid"] = _u32([n] * st.B)
     if st.cb_tab is not None:
         m["cb.tab"], m["cb.scale"], m["cb.code"] = cpu(st.cb_tab), cpu(st.cb_scale), cpu(st.cb_code)
@@ -143,8 +150,8 @@ def load_state(path: str, cfg: dict, fp: int, device="cuda", device_len: bool = 
     if cap:
         if n > cap:
             raise ValueError(f"{path}: {n} stored entries exceed the capacity {cap}")
-        put(st.eng_k[:, :n].unsqueeze(1), "eng.k")
-        put(st.eng_v[:, :n].unsqueeze(1), "eng.v")
+        put(_heads(cfg, st.eng_k[:, :n]), "eng.k")
+        put(_heads(cfg, st.eng_v[:, :n]), "eng.v")
         if _ints(get("eng.valid")) != [n] * B:
             raise ValueError(f"{path}: eng.valid does not match the store length {n}")
     st.eng_len = n

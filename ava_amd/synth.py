@@ -24,7 +24,8 @@ FIXED_TS = (5.0, 8.0)  # gpu/arch.rs:91
 
 def config(name: str) -> dict:
     """Named configurations: "ava04_d512" (config[0]), "ava04_d1024" (config[3]), "ava04_d1024_decode"
-    (config[4]), "tiny", "small" and "tiny_cb" (tests). cb_units > 0 adds the cerebellum head
+    (config[4]), "ava04_d1024_heads" (config[3] with the engram's reference geometry: 32 heads of 32),
+    "tiny", "small", "tiny_heads" and "tiny_cb" (tests). cb_units > 0 adds the cerebellum head
     (gpu/v51b.rs:18-32) with its online table: cb_eta sets the rate as cb_rate, cb_half the
     table's half-life in tokens (<= 0: it never fades)."""
     base = dict(levels=2, alif=True, lif_scale=True, value_residual=True, dense=True, relu2=True,
@@ -37,6 +38,12 @@ def config(name: str) -> dict:
         base.update(vocab=256, d=128, layers=2, hidden=512, kwta_k=128, eng_block=1)
     elif name == "small":
         base.update(vocab=512, d=256, layers=3, hidden=1024, kwta_k=256, eng_block=1)
+    elif name == "tiny_heads":
+        # the engram at the reference's geometry: d / 32 heads of 32 over the whole width (gpu/memory.rs:610-700)
+        base.update(vocab=256, d=128, layers=2, hidden=512, kwta_k=128, eng_block=1, eng_dim=128, eng_heads=4)
+    elif name == "ava04_d1024_heads":
+        # config[3]'s shapes with the engram at the reference's geometry: 32 heads of 32, f32 store
+        base.update(vocab=8192, d=1024, layers=8, hidden=4096, kwta_k=1024, eng_block=4, eng_dim=1024, eng_heads=32)
     elif name == "tiny_cb":
         base.update(vocab=256, d=128, layers=2, hidden=512, kwta_k=128, eng_block=1)
         base.update(cb_units=512, cb_eta=0.5, cb_half=256.0)

@@ -4,6 +4,8 @@
 
 Workloads:
     stack   config[3]: the Ava-0.4-shaped int8 block stack, teacher-forced, B=64, T=2048, d=1024
+    stack_heads  config[3] with the engram at the reference's geometry (32 heads of 32, f32 store)
+    decode  config[4]: batched stateful decode, B=256 streams, 32768-token state
     lif     config[1]: the standalone LIF scan, B=64, T=2048, C=2048
     delta   config[2]: the plain delta rule, chunked, B=32, H=8, T=4096, d=64
     kwta    the kWTA + relu2 of config[3]'s wide layer (131072 rows of 4096, k=1024)
@@ -400,6 +402,20 @@ class Stack:
                           f"config[3]'s model, B={B}, T={T}, {th} threads for the products, {dt:.2f} s"}
 
 
+class StackHeads(Stack):
+    """config[3] with the engram read at the reference's geometry (gpu/memory.rs:610-700): 32 heads of
+    32 over the whole width (Wq, Wk, Wv, Wo 1024 x 1024) and an f32 store, instead of BASELINE's one
+    head of 64. Not the headline line: it shows what the reference's own engram costs on this path."""
+
+    name = "stack_heads"
+
+    def __init__(self, B=64, T=2048, planes=3):
+        super().__init__(B=B, T=T, cfg_name="ava04_d1024_heads", planes=planes)
+        self.config.update(workload="int8 block stack config[3], engram of 32 heads of 32",
+                           engram_heads=self.cfg["eng_heads"], engram_dim=self.cfg["eng_dim"])
+        self.traffic = None  # the counter runs cover the headline workload
+
+
 class Decode:
     """config[4]: batched stateful decode. B=256 streams of config[3]'s model with the cerebellum head
     (12,288 granule units, 384 kept, per-stream online table with a 256-token half-life). Each stream's
@@ -561,7 +577,7 @@ class Decode:
         return None
 
 
-WORKLOADS = {"stack": Stack, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
+WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
 DEFAULT = "stack"
 
 

@@ -147,13 +147,22 @@ size_t ava_attend_part_floats(int B, int T, int n0);
 int ava_attend(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B, int T,
                float *out, float *part, size_t part_floats, ava_stream stream);
 
+/* The same read with heads (memory::read, gpu/memory.rs:610-700: heads of 32, scores scaled by
+ * 1/sqrt(32)): a row of q, of the store and of out holds de dims, heads h*hd .. h*hd + hd - 1 side
+ * by side, hd = de / heads (32 or 64; de a multiple of 64, <= 4096). Each head reads its own slice of
+ * the keys and values. ks, vs [B][cap][de]; out [B*T][de]; decode partials as ava_attend's, sized
+ * by ava_attend_heads_part_floats. */
+size_t ava_attend_heads_part_floats(int B, int T, int n0, int de, int heads);
+int ava_attend_heads(const float *q, int ldq, const void *ks, const void *vs, int kv_half, int cap, int n0, int B,
+                     int T, int de, int heads, float *out, float *part, size_t part_floats, ava_stream stream);
+
 /* ------------------------------------------------------------------ model */
 
 /* The block options of the path (Ava 0.4's recipe, release/ava-0.4/arch.txt:1). */
 typedef struct {
     int vocab, d, layers, hidden, kwta_k, head_size, gate_rank;
     int eng_block;  /* the block with the engram read, -1 for none */
-    int eng_dim;    /* the engram's single head size (64) */
+    int eng_dim;    /* the engram's dims: its single head (64), or eng_heads heads of 32 */
     int levels;     /* spike levels each side (2 = int2) */
     int alif, lif_scale, value_residual, dense, relu2;
     float momentum, cap;
@@ -167,6 +176,10 @@ typedef struct {
     /* The engram store's element: 0 = f32 (the reference's store), 1 = fp16, a KV cache of half the
      * bytes (config[4]); the state's eng_k and eng_v then hold IEEE binary16 values. */
     int eng_half;
+    /* The engram's heads: 0 or 1 = one head of eng_dim (64); eng_dim / 32 = the reference's heads of
+     * 32 (gpu/memory.rs:610-700, HEAD_SIZE 32; eng_dim a multiple of 64 up to 1024, normally d).
+     * The store row [eng_dim] holds the heads side by side. */
+    int eng_heads;
 } ava_config;
 
 /* f32 HOST weights, named as the reference's VarMap (arch.rs:806-860). W [din][dout] as applied x·W. */

@@ -91,22 +91,25 @@ static void head_norm(float *y, int n, int hs) {
 
 /* gpu/model/fstep.rs:223-257: one-row product out[c] = sum_j x[j] w[j][c] in gemm's order
  * (k >= 3: w[0][c]·x[0], then fma over j = 1, 2, ...). */
-static void gemv(const float *x, int k, const float *w, int n, float *out) {
+/* gemv over the first n columns of a matrix whose rows are ld floats apart */
+static void gemv_ld(const float *x, int k, const float *w, int ld, int n, float *out) {
     if (k == 0) {
         for (int c = 0; c < n; c++) out[c] = 0.0f;
     } else if (k == 1) {
         for (int c = 0; c < n; c++) out[c] = w[c] * x[0];
     } else if (k == 2) {
-        for (int c = 0; c < n; c++) out[c] = w[n + c] * x[1] + w[c] * x[0];
+        for (int c = 0; c < n; c++) out[c] = w[ld + c] * x[1] + w[c] * x[0];
     } else {
         for (int c = 0; c < n; c++) out[c] = w[c] * x[0];
         for (int j = 1; j < k; j++) {
-            const float *wr = w + (size_t)j * n;
+            const float *wr = w + (size_t)j * ld;
             float xj = x[j];
             for (int c = 0; c < n; c++) out[c] = fmaf(wr[c], xj, out[c]);
         }
     }
 }
+
+static void gemv(const float *x, int k, const float *w, int n, float *out) { gemv_ld(x, k, w, n, n, out); }
 
 /* ------------------------------------------------------------------ int8 weights */
 
@@ -409,11 +412,12 @@ static void mm_int(const int8_t *s, int m, const orc_qw *w, float *y, int thread
     free(acc);
 }
 
-/* One head's causal read (gpu/model/fstep.rs:303-329: scores in gemm's order, softmax, p·V). */
-static void attend(const float *q, const float *kc, const float *vc, int n, int hs, float scale,
+/* One head's causal read (gpu/model/fstep.rs:303-329: scores in gemm's order, softmax, p·V). The
+ * head's hs key and value dims sit in store rows ld floats apart (ld = hs for one head). */
+static void attend(const float *q, const float *kc, const float *vc, int n, int hs, int ld, float scale,
                    float *sc, float *out) {
     for (int j = 0; j < n; j++) {
-        const float *kr = kc + (size_t)j * hs;
+        const float *kr = kc + (size_t)j * ld;
         float s = kr[0] * q[0];
         for (int a = 1; a < hs; a++) s = fmaf(kr[a], q[a], s);
         sc[j] = s * scale + 0.0f;
@@ -427,7 +431,7 @@ static void attend(const float *q, const float *kc, const float *vc, int n, int 
         den += sc[j];
     }
     for (int j = 0; j < n; j++) sc[j] = sc[j] / den;
-    gemv(sc, n, vc, hs, out);
+    gemv_ld(sc, n, vc, ld, hs, out);
 }
 
 #define ALLOC(T_, n) ((T_ *)malloc(sizeof(T_) * (size_t)(n)))
@@ -555,7 +559,8 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
         mm(y, (int)N, &bk->wo, h, planes, threads);
         for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];
 
-        /* ---- the engram read (gpu/arch.rs:1706-1738; gpu/model/fstep/arch.rs:898-974), one head */
+        /* ---- the engram read (gpu/arch.rs:1706-1738; gpu/model/fstep/arch.rs:898-974): one head of
+         * eng_dim, or eng_heads heads side by side in each row (memory::read, gpu/memory.rs:610-700) */
         if (i == cfg->eng_block) {
             float *eq = ALLOC(float, N * de), *ekk = ALLOC(float, N * de), *evv = ALLOC(float, N * de);
             float *eo = ALLOC(float, N * de), *sc = ALLOC(float, st->eng_len + T);
@@ -575,13 +580,15 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
                             st->eng_v[dst + c] = orc_round_half(st->eng_v[dst + c]);
                         }
                 }
-            float scale = (float)(1.0 / sqrt((double)de));
+            const int enh = cfg->eng_heads > 1 ? cfg->eng_heads : 1, hd = de / enh;
+            float scale = (float)(1.0 / sqrt((double)hd));
             for (int bi = 0; bi < B; bi++)
-                for (int t = 0; t < T; t++) {
-                    size_t base = (size_t)bi * st->eng_cap * de;
-                    attend(eq + ((size_t)bi * T + t) * de, st->eng_k + base, st->eng_v + base,
-                           n0 + t + 1, de, scale, sc, eo + ((size_t)bi * T + t) * de);
-                }
+                for (int t = 0; t < T; t++)
+                    for (int hh = 0; hh < enh; hh++) {
+                        size_t base = (size_t)bi * st->eng_cap * de + (size_t)hh * hd;
+                        size_t row = ((size_t)bi * T + t) * de + (size_t)hh * hd;
+                        attend(eq + row, st->eng_k + base, st->eng_v + base, n0 + t + 1, hd, de, scale, sc, eo + row);
+                    }
             st->eng_len = n0 + T;
             mm(eo, (int)N, &bk->ewo, h, planes, threads);
             for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];

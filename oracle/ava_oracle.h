@@ -126,6 +126,7 @@ typedef struct {
     int alif, lif_scale, value_residual, dense, relu2;
     float momentum, cap;
     int eng_half;    /* the engram store keeps keys and values at fp16 precision (config[4]'s KV cache) */
+    int eng_heads;   /* 0 or 1: one head of eng_dim; else heads of eng_dim / eng_heads side by side */
 } orc_cfg;
 
 typedef struct {

@@ -278,7 +278,7 @@ class _Cfg(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab", "d", "layers", "hidden", "kwta_k", "heads", "head_size",
                                        "gate_rank", "eng_block", "eng_dim", "levels", "alif", "lif_scale",
                                        "value_residual", "dense", "relu2")] + \
-               [("momentum", C.c_float), ("cap", C.c_float), ("eng_half", C.c_int)]
+               [("momentum", C.c_float), ("cap", C.c_float), ("eng_half", C.c_int), ("eng_heads", C.c_int)]
 
 
 class _Model(C.Structure):
@@ -329,7 +329,7 @@ class OracleModel:
                          alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
                          value_residual=int(c["value_residual"]), dense=int(c["dense"]),
                          relu2=int(c["relu2"]), momentum=c["momentum"], cap=c["cap"],
-                         eng_half=int(c.get("eng_half", 0) or 0))
+                         eng_half=int(c.get("eng_half", 0) or 0), eng_heads=int(c.get("eng_heads", 1) or 1))
         self.head_q, self.head_s = self.q8[id(head_w)]
         # the cerebellum head (gpu/v51b.rs:18-32, 282-293): wiring from the fixed seed, the read-out W
         # (cbh.wo, zero at init: None), the online rate and half-life

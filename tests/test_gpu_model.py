@@ -202,3 +202,17 @@ def test_long_sequence_against_oracle():
     it the token's logits move by up to ~0.2 and the fast weights carry the difference, fading with the
     gates. Bars: check_long."""
     check_long("tiny", 2, 1105, seed=4)
+
+
+@pytest.mark.parametrize("half", [False, True])
+def test_engram_heads_match_oracle(half):
+    """The engram at the reference's geometry (d / 32 heads of 32, gpu/memory.rs:610-700) through a
+    prefill and single-token steps (the tiled read, then the chunked decode read of every head)."""
+    cfg, lo, so, lg, st = run_both("tiny_heads", 2, 40, seed=8, pieces=[(0, 30), (30, 31), (31, 32), (32, 40)],
+                                   eng_half=half)
+    assert np.max(np.abs(lg - lo)) < 1e-2
+    assert rel(lg, lo) < 1e-3
+    check_state(so, st)
+    assert st.eng_len == 40
+    if not half:
+        assert rel(host(st.eng_k), so["eng_k"]) < 1e-4

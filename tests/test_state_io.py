@@ -62,7 +62,7 @@ def _filled(cfg, B, cap, n, seed):
     return st
 
 
-@pytest.mark.parametrize("name,half", [("tiny", False), ("tiny_cb", False), ("small", True)])
+@pytest.mark.parametrize("name,half", [("tiny", False), ("tiny_cb", False), ("small", True), ("tiny_heads", False)])
 def test_round_trip(name, half, tmp_path):
     cfg = dict(synth.config(name), eng_half=half)
     B, cap, n = 3, 40, 17
@@ -81,6 +81,10 @@ def test_round_trip(name, half, tmp_path):
     if cfg.get("cb_units"):
         for f in ("cb_tab", "cb_scale", "cb_code"):
             assert torch.equal(getattr(r, f), getattr(st, f)), f
+    nh = cfg.get("eng_heads", 1)
+    ek = sio.state_tensors(st, cfg, fp)["eng.k"]
+    assert tuple(ek.shape) == (B, nh, n, cfg["eng_dim"] // nh)  # the reference's [B, heads, S, hd]
+    assert torch.equal(ek[:, -1], st.eng_k[:, :n, -(cfg["eng_dim"] // nh):])
     names = set(sio.state_tensors(st, cfg, fp))
     assert {"meta.model", "meta.blocks", "meta.seen", "lif.0.v", "lif.0.s", "lif.0.a", "mem.0.f", "mem.0.s",
             "eng.k", "eng.v", "eng.valid"} <= names
