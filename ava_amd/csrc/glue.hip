@@ -412,8 +412,8 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
 // summation order.
 // Heads: the store's rows hold nh heads of HD dims (de = nh HD, the reference's heads of 32,
 // gpu/memory.rs:610-700); workgroup (query block, b nh + h) reads head h: its query, key and value
-// dims h HD .. h HD + HD - 1. For HD = 32 the tiles' dims 32..63 stay zero and the waves of output
-// columns 32..63 skip the P V products.
+// dims h HD .. h HD + HD - 1. For HD = 32 the tiles' dims 32..63 stay zero (S runs over 32 dims) and
+// P V has one 32-column output: the two waves of a row half each take half of the tile's keys.
 template <typename KV, int HD>
 __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restrict__ q, int ldq,
                                                           const KV *__restrict__ ks, const KV *__restrict__ vs,
@@ -502,20 +502,42 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 16; i++) o[i] *= s_corr[row0 + qrow(i)];
-        if (col0 < HD) {
+        {
             const int fr = lane & 31, h = lane >> 5;
+            if constexpr (HD == 64) {
 #pragma unroll 8
-            for (int x = 0; x < 64; x += 2)
-                o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + x + h], sV[(x + h) * L + col0 + fr], o, 0,
-                                                         0, 0);
+                for (int x = 0; x < 64; x += 2)
+                    o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + x + h], sV[(x + h) * L + col0 + fr],
+                                                             o, 0, 0, 0);
+            } else {
+                // one 32-column output: the wave pair of a row half splits the tile's keys, each
+                // keeping its partial sum (both scale by the same corrections); added at the end
+                const int kh = col0;
+#pragma unroll 8
+                for (int x = 0; x < 32; x += 2)
+                    o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + kh + x + h],
+                                                             sV[(kh + x + h) * L + fr], o, 0, 0, 0);
+            }
         }
+    }
+    if constexpr (HD == 32) {
+        // the second key half's partials through sQ (no wave reads sQ after its last S product,
+        // which every wave passed before the last tile's softmax barrier)
+        if (col0)
+#pragma unroll
+            for (int i = 0; i < 16; i++) sQ[(row0 + qrow(i)) * L + lc] = o[i];
     }
     if (sub == 0) s_den[r] = den;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int rr = row0 + qrow(i);
-        if (qb + rr < T && col0 < HD) out[((size_t)bi * T + qb + rr) * de + hh * HD + col0 + lc] = o[i] / s_den[rr];
+        if constexpr (HD == 64) {
+            if (qb + rr < T) out[((size_t)bi * T + qb + rr) * de + hh * HD + col0 + lc] = o[i] / s_den[rr];
+        } else {
+            if (qb + rr < T && col0 == 0)
+                out[((size_t)bi * T + qb + rr) * de + hh * HD + lc] = (o[i] + sQ[rr * L + lc]) / s_den[rr];
+        }
     }
 }
 
