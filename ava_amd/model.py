@@ -52,6 +52,22 @@ class State:
         self.cb_code = z(B, g) if g else None
         self.eng_len_dev = torch.zeros(1, dtype=torch.int32, device=device) if device_len else None
         self.seen = 0  # tokens each stream has consumed (State::seen, state.rs:94-116)
+        # the store's cap (EngramCap with the oldest-first rule, state.rs:37-69): after a forward the
+        # store keeps its last eng_max entries (0: no cap); the capacity must hold eng_max + T
+        self.eng_max = 0
+
+    def evict(self):
+        """Keep the store's last eng_max entries (evict with Evict::Oldest, state.rs:518-540), on the
+        store's device, in order. Called by the model after each forward of a capped state."""
+        n, mx = self.eng_len, self.eng_max
+        if not mx or n <= mx:
+            return
+        drop = n - mx
+        for t in (self.eng_k, self.eng_v):
+            t[:, :mx].copy_(t[:, drop:n].clone())  # the ranges overlap when drop < mx
+        self.eng_len = mx
+        if self.eng_len_dev is not None:
+            self.eng_len_dev.fill_(mx)
 
     def c(self):
         p = lambda t: t.data_ptr() if t is not None else None
@@ -108,8 +124,15 @@ class Model:
             lib().ava_model_free(self.h)
             self.h = None
 
-    def state(self, B: int, eng_cap: int = 0, device_len: bool = False) -> State:
-        return State(self.cfg, B, eng_cap, device_len=device_len)
+    def state(self, B: int, eng_cap: int = 0, device_len: bool = False, eng_max: int = 0) -> State:
+        """A fresh state of B streams. eng_cap: the store's capacity in entries; eng_max > 0 caps the
+        store (oldest entries evicted after each forward; eng_cap must hold eng_max + the tokens of
+        the longest forward)."""
+        st = State(self.cfg, B, eng_cap, device_len=device_len)
+        if eng_max < 0 or (eng_max and eng_max >= max(eng_cap, 1)):
+            raise ValueError(f"eng_max {eng_max}: 0 (no cap) or below the capacity {eng_cap}")
+        st.eng_max = eng_max
+        return st
 
     def save_state(self, st: State, path: str) -> None:
         """Write st to path (safetensors, whole or absent), keyed by this model's fingerprint
@@ -131,6 +154,8 @@ class Model:
         on first use, and a capture must not allocate)."""
         if st.eng_len_dev is None:
             raise ValueError("capture_decode: the state needs device_len=True")
+        if st.eng_max:
+            raise ValueError("capture_decode: a capped store (eng_max) evicts on the host between steps")
         check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")  # the graph keeps the scratch's addresses
         g = torch.cuda.CUDAGraph()
         n0, s0 = st.eng_len, st.seen
@@ -154,6 +179,7 @@ class Model:
               "ava_model_forward")
         st.eng_len = cst.eng_len
         st.seen += T
+        st.evict()
         return logits
 
     def decode_step(self, ids: torch.Tensor, st: State, logits: torch.Tensor, prev_logits: torch.Tensor | None = None,
@@ -194,6 +220,7 @@ class Model:
               "ava_model_decode_step")
         st.eng_len = cst.eng_len
         st.seen += T
+        st.evict()
         return logits
 
     def capture_decode_step(self, st: State, ids: torch.Tensor, logits: torch.Tensor, prev_logits: torch.Tensor,
@@ -201,6 +228,8 @@ class Model:
         """decode_step over fixed buffers as a HIP graph (both streams' work; see capture_decode)."""
         if st.eng_len_dev is None:
             raise ValueError("capture_decode_step: the state needs device_len=True")
+        if st.eng_max:
+            raise ValueError("capture_decode_step: a capped store (eng_max) evicts on the host between steps")
         check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")
         g = torch.cuda.CUDAGraph()
         n0, s0 = st.eng_len, st.seen

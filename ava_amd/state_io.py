@@ -12,6 +12,7 @@ Tensor names, where the reference has the same quantity (state.rs:1113-1197):
     meta.model [2] u32      the fingerprint, high word first
     meta.blocks [1] u32     the layer count
     meta.seen [B] u32       tokens each stream has consumed
+    meta.cap [2] u32        the store's cap and rule: [0, 0] none, [max, 0] oldest first
     lif.{i}.v / .s / .a     [B, d] membrane, last spikes, adaptation (.a with ALIF)
     mem.{i}.f / .s          [B, nh, hs, hs] the fast weights F and the momentum S (.s with momentum)
     eng.k / eng.v           [B, heads, len, eng_dim / heads] the engram store's filled entries, its dtype
@@ -82,7 +83,8 @@ def state_tensors(st, cfg: dict, fp: int) -> dict:
     L = cfg["layers"]
     n = st.eng_len
     m = {"meta.model": _u32([fp >> 32, fp & 0xFFFFFFFF]), "meta.blocks": _u32([L]),
-         "meta.seen": _u32([st.seen] * st.B), "meta.store": _u32([st.eng_cap, n])}
+         "meta.seen": _u32([st.seen] * st.B), "meta.store": _u32([st.eng_cap, n]),
+         "meta.cap": _u32([getattr(st, "eng_max", 0), 0])}
     cpu = lambda t: t.detach().to("cpu").contiguous()
     for i in range(L):
         m[f"lif.{i}.v"], m[f"lif.{i}.s"] = cpu(st.lif_v[i]), cpu(st.lif_s[i])
@@ -131,6 +133,10 @@ def load_state(path: str, cfg: dict, fp: int, device="cuda", device_len: bool = 
     B = len(seen)
     cap, n = _ints(get("meta.store"))
     st = State(cfg, B, cap, device=device, device_len=device_len)
+    emax, rule = _ints(get("meta.cap"))
+    if rule != 0:
+        raise ValueError(f"{path}: eviction rule {rule} (this build evicts oldest first only)")
+    st.eng_max = emax
 
     def put(dst, k):
         src = get(k)

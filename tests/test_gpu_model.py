@@ -216,3 +216,35 @@ def test_engram_heads_match_oracle(half):
     assert st.eng_len == 40
     if not half:
         assert rel(host(st.eng_k), so["eng_k"]) < 1e-4
+
+
+def test_capped_store_matches_oracle_with_the_same_eviction():
+    """A store capped at 24 entries (EngramCap, oldest first: state.rs:518-540) through a prefill of
+    20 and single-token steps: after every forward both sides keep the last 24 entries (the oracle's
+    store trimmed the same way, by slicing), and the logits of every step agree."""
+    cfg = synth.config("tiny")
+    prm = synth.params(cfg, seed=12)
+    B, T0, steps, mx = 2, 20, 12, 24
+    ids = np.random.default_rng(13).integers(0, cfg["vocab"], (B, T0 + steps)).astype(np.int32)
+    print(f"capped store B={B} prefill={T0} steps={steps} max={mx}", flush=True)
+    om = O.OracleModel(cfg, prm)
+    so = om.new_state(B, eng_cap=mx + T0)
+    from ava_amd.model import Model
+    m = Model(cfg, prm)
+    st = m.state(B, eng_cap=mx + T0, eng_max=mx)
+    pieces = [(0, T0)] + [(t, t + 1) for t in range(T0, T0 + steps)]
+    uncapped = m.state(B, eng_cap=T0 + steps)
+    for a, b in pieces:
+        x = np.ascontiguousarray(ids[:, a:b])
+        lo, so, _ = om.forward(x, state=so, planes=3, threads=8)
+        n = so["eng_len"]
+        if n > mx:
+            for k in ("eng_k", "eng_v"):
+                so[k][:, :mx] = so[k][:, n - mx:n].copy()
+            so["eng_len"] = mx
+        lg = host(m.forward_with_state(torch.from_numpy(x).cuda(), st))
+        lu = host(m.forward_with_state(torch.from_numpy(x).cuda(), uncapped))
+        assert np.max(np.abs(lg - lo)) < 1e-2, (a, b)
+        assert st.eng_len == min(b, mx)
+    assert rel(host(st.eng_k)[:, :mx], so["eng_k"][:, :mx]) < 1e-4
+    assert np.max(np.abs(lu - lg)) > 1e-4  # the cap changed what the last steps read

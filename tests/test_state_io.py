@@ -106,3 +106,32 @@ def test_refusals(tmp_path):
     sio.save_state(path, st, cfg0, 7)
     assert "mem.0.s" not in sio.state_tensors(st, cfg0, 7)
     assert not sio.load_state(path, cfg0, 7, device="cpu").mem_s.any()
+
+
+def test_evict_keeps_the_last_entries_in_order():
+    """Evict::Oldest (state.rs:518-540): the store keeps its last eng_max entries, oldest first."""
+    cfg = synth.config("tiny")
+    st = _filled(cfg, 2, 20, 13, seed=8)
+    k0, v0 = st.eng_k.clone(), st.eng_v.clone()
+    st.eng_max = 5
+    st.evict()
+    assert st.eng_len == 5
+    assert torch.equal(st.eng_k[:, :5], k0[:, 8:13]) and torch.equal(st.eng_v[:, :5], v0[:, 8:13])
+    st.eng_max = 16
+    st.evict()  # under the cap: nothing moves
+    assert st.eng_len == 5 and torch.equal(st.eng_k[:, :5], k0[:, 8:13])
+
+
+def test_cap_saved_and_refused_rules(tmp_path):
+    cfg = synth.config("tiny")
+    st = _filled(cfg, 2, 20, 5, seed=9)
+    st.eng_max = 12
+    path = str(tmp_path / "s.safetensors")
+    sio.save_state(path, st, cfg, 3)
+    assert sio.load_state(path, cfg, 3, device="cpu").eng_max == 12
+    t = sio.state_tensors(st, cfg, 3)
+    t["meta.cap"] = sio._u32([12, 1])  # least-read: not built
+    from safetensors.torch import save_file
+    save_file(t, path)
+    with pytest.raises(ValueError, match="eviction rule"):
+        sio.load_state(path, cfg, 3, device="cpu")
