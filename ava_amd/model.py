@@ -56,6 +56,21 @@ class State:
         # store keeps its last eng_max entries (0: no cap); the capacity must hold eng_max + T
         self.eng_max = 0
 
+    def select(self, rows) -> "State":
+        """A state of the given streams only, in that order (State::select): every tensor's stream axis
+        indexed; the store's length, cap and token count are shared."""
+        idx = torch.as_tensor(list(rows), dtype=torch.long, device=self.lif_v.device)
+        out = object.__new__(State)
+        out.__dict__.update(self.__dict__)
+        out.B = len(rows)
+        for f in ("lif_v", "lif_s", "lif_a", "mem_f", "mem_s"):
+            setattr(out, f, getattr(self, f).index_select(1, idx).contiguous())
+        for f in ("eng_k", "eng_v", "cb_tab", "cb_scale", "cb_code"):
+            t = getattr(self, f)
+            setattr(out, f, t.index_select(0, idx).contiguous() if t is not None else None)
+        out.eng_len_dev = self.eng_len_dev.clone() if self.eng_len_dev is not None else None
+        return out
+
     def evict(self):
         """Keep the store's last eng_max entries (evict with Evict::Oldest, state.rs:518-540), on the
         store's device, in order. Called by the model after each forward of a capped state."""
@@ -259,6 +274,52 @@ class Model:
                                        C.c_void_p(nxt.data_ptr()), B, C.c_void_p(nats.data_ptr()), stream),
               "ava_model_cb_learn")
         return nats
+
+    def generate(self, prompts, max_new: int, pick=None, stop=None, eos: int | None = None,
+                 batch_rows: int = 256) -> list:
+        """Continuations of every prompt with carried state (generate, gpu/state.rs:1392-1458): the
+        prompts are read in batched passes, then the rows step together, one token per pass; a row
+        leaves at eos (not included) or when stop(tokens) is true. pick(row, logits [vocab]) chooses
+        a token (default: greedy, the lowest id on ties). Rows of one pass share a prompt length
+        (this state keeps one store length for all its streams); rows are independent, so the
+        grouping does not change any row's tokens. Returns each prompt's tokens."""
+        if any(len(p) == 0 for p in prompts):
+            raise ValueError("generate: an empty prompt")
+        out = [[] for _ in prompts]
+        order = sorted(range(len(prompts)), key=lambda r: (len(prompts[r]), r))
+        br = max(batch_rows, 1)
+        eng = self.cfg["eng_block"] >= 0
+        i = 0
+        while i < len(order):
+            n0 = len(prompts[order[i]])
+            group = [r for r in order[i:i + br] if len(prompts[r]) == n0]
+            i += len(group)
+            st = self.state(len(group), eng_cap=n0 + max_new if eng else 0)
+            ids = torch.tensor([prompts[r] for r in group], dtype=torch.int32, device="cuda")
+            last = self.forward_with_state(ids, st).view(len(group), n0, -1)[:, -1]
+            live = list(group)
+            for step in range(max_new):
+                if pick is None:
+                    toks = torch.argmax(last, dim=1).tolist()  # the first (lowest) id of the maximum
+                else:
+                    toks = [int(pick(r, last[k])) for k, r in enumerate(live)]
+                keep, nxt = [], []
+                for k, (r, tok) in enumerate(zip(live, toks)):
+                    if eos is not None and tok == eos:
+                        continue
+                    out[r].append(tok)
+                    if stop is not None and stop(out[r]):
+                        continue
+                    keep.append(k)
+                    nxt.append(tok)
+                if not keep or step + 1 == max_new:
+                    break
+                if len(keep) != len(live):
+                    st = st.select(keep)
+                    live = [live[k] for k in keep]
+                x = torch.tensor(nxt, dtype=torch.int32, device="cuda").view(-1, 1)
+                last = self.forward_with_state(x, st)
+        return out
 
     def forward(self, ids: torch.Tensor):
         B, T = ids.shape
