@@ -5,6 +5,7 @@
 Workloads:
     stack   config[3]: the Ava-0.4-shaped int8 block stack, teacher-forced, B=64, T=2048, d=1024
     stack_heads  config[3] with the engram at the reference's geometry (32 heads of 32, f32 store)
+    greedy  config[0]: one stream, a 512-token prompt and 128 greedy steps, d=512
     decode  config[4]: batched stateful decode, B=256 streams, 32768-token state
     lif     config[1]: the standalone LIF scan, B=64, T=2048, C=2048
     delta   config[2]: the plain delta rule, chunked, B=32, H=8, T=4096, d=64
@@ -402,6 +403,76 @@ class Stack:
                           f"config[3]'s model, B={B}, T={T}, {th} threads for the products, {dt:.2f} s"}
 
 
+class Greedy:
+    """config[0]: the reference's own CPU-runnable case. Ava-0.4-shaped int8 model with d=512 (8 blocks,
+    wide 2048 with kWTA 512, 8 memory heads of 64, the single-head engram read in block 4), vocab 8192,
+    random-init weights; one stream: a prompt of 512 ids, then 128 greedy steps (argmax, the lowest id
+    on ties) with carried state (Model.generate, generate in gpu/state.rs:1392-1458). A step is the
+    whole generation; value = generated tokens per second. Latency-bound: one token's int8 weights
+    and state are ~46 MB, under 6 µs of HBM time, against ~110 launches per token."""
+
+    name = "greedy"
+    kernel = "whole_step"
+    metric = "tokens/sec greedy decode @B=1, 512-token prompt + 128 steps (config[0]), 1 GPU; % HBM roofline"
+    default_steps = 3
+
+    def __init__(self, prompt=512, new=128, planes=3):
+        from ava_amd import synth
+        from ava_amd.model import Model
+
+        self.cfg = c = synth.config("ava04_d512")
+        self.prompt_len, self.new = prompt, new
+        log("bench: building weights")
+        self.params = synth.params(c, seed=0)
+        self.model = Model(c, self.params, planes=planes)
+        self.prompt = np.random.default_rng(7).integers(0, c["vocab"], prompt).tolist()
+        self.tokens = new
+        d, H, V, L, nh = c["d"], c["hidden"], c["vocab"], c["layers"], c["d"] // c["head_size"]
+        # bytes per generated token: the int8 weights (16 d^2 per block, the engram's 4 d 64, the head
+        # d V, each with 4-byte column scales), LIF state r/w (3 [d] f32), F and S r/w ([nh][64][64] f32
+        # each), the engram's keys and values read (prompt + half the steps on average, 64 f32 each),
+        # the logits row written
+        w = L * 16 * d * d + 4 * d * c["eng_dim"] + d * V
+        self.bytes_per_token = (w + 4 * (L * 16 * d + 4 * c["eng_dim"] + V) + L * 3 * d * 4 * 2
+                                + L * nh * 64 * 64 * 4 * 2 * 2 + (prompt + new // 2) * 64 * 4 * 2 + V * 4)
+        self.config = {"workload": "greedy generation config[0]", "B": 1, "prompt": prompt, "steps": new, "d": d,
+                       "blocks": L, "hidden": H, "kwta_k": c["kwta_k"], "vocab": V, "act_planes": planes}
+        self.dtype = "i8"
+        self.out = None
+
+    def step(self, stream, ev=None):
+        self.out = self.model.generate([self.prompt], self.new)[0]
+
+    def kernel_ms(self):
+        return [self.wall * 1e3 / self.nsteps]  # the whole generation, per step
+
+    def roofline(self, kernel_s):
+        per_token = kernel_s / self.new
+        a = self.bytes_per_token / per_token / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
+                "bytes_per_token": self.bytes_per_token, "ms_per_token": per_token * 1e3,
+                "note": "whole generation (prefill included) over its wall time; latency-bound"}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        new = self.new  # the same generation: the prompt's pass and 128 greedy steps
+        th = cpu_threads()
+        om = O.OracleModel(self.cfg, self.params)
+        t0 = time.perf_counter()
+        st = om.new_state(1, eng_cap=self.prompt_len + new)
+        lg, st, _ = om.forward(np.asarray([self.prompt], np.int32), state=st, planes=0, threads=th)
+        last = lg[-1]
+        for _ in range(new - 1):
+            lg, st, _ = om.forward(np.asarray([[int(np.argmax(last))]], np.int32), state=st, planes=0, threads=th)
+            last = lg[-1]
+        dt = time.perf_counter() - t0
+        return {"value": new / dt, "unit": "tokens/s", "cores": th, "kind": "port",
+                "sample": f"oracle greedy loop with the reference's W8A32 products (int8.rs:301-331) on config[0]'s "
+                          f"model: the {self.prompt_len}-token prompt and {new} steps, {th} threads, {dt:.2f} s "
+                          f"(prefill included, as in the GPU figure; the same tokens are not checked here)"}
+
+
 class StackHeads(Stack):
     """config[3] with the engram read at the reference's geometry (gpu/memory.rs:610-700): 32 heads of
     32 over the whole width (Wq, Wk, Wv, Wo 1024 x 1024) and an f32 store, instead of BASELINE's one
@@ -577,7 +648,7 @@ class Decode:
         return None
 
 
-WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
+WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "greedy": Greedy, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
 DEFAULT = "stack"
 
 
