@@ -422,6 +422,10 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     static_assert(HD == 32 || HD == 64, "head size 32 or 64");
     if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device (a replayed graph)
     constexpr int L = 65;               // LDS row stride (odd: a column read hits 32 banks)
+    // scores in base-2 units (s log2 e), so the softmax's exponentials are the hardware 2^x
+    // (v_exp_f32): with m the running max in those units, 2^(s log2 e - m) = e^(s - m ln 2), and
+    // the normalized weights are the softmax's up to rounding
+    const float scale2 = scale * 1.44269504088896341f;
     __shared__ float sQ[64 * L], sK[64 * L], sV[64 * L], sP[64 * L];
     __shared__ float s_corr[64], s_den[64];
     const int bi = blockIdx.y / nh, hh = blockIdx.y - bi * nh, qb = blockIdx.x * 64;
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int rr = row0 + qrow(i), cc = col0 + lc;
-                const float a = sa[i] * scale + 0.0f;
+                const float a = sa[i] * scale2;
                 sP[rr * L + cc] = (k0 + cc <= n0 + qb + rr) ? a : -INFINITY;
             }
         }
@@ -485,11 +489,11 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
             tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
             tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
             const float nmx = fmaxf(mx, tmax);
-            const float corr = (mx == -INFINITY) ? 0.0f : expf(mx - nmx);
+            const float corr = (mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mx - nmx);
             float psum = 0.0f;
 #pragma unroll
             for (int z = 0; z < 16; z++) {
-                const float e = (sc[z] == -INFINITY) ? 0.0f : expf(sc[z] - nmx);
+                const float e = (sc[z] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc[z] - nmx);
                 sP[r * L + sub * 16 + z] = e;
                 psum += e;
             }
