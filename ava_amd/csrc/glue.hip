@@ -412,8 +412,8 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
 // summation order.
 // Heads: the store's rows hold nh heads of HD dims (de = nh HD, the reference's heads of 32,
 // gpu/memory.rs:610-700); workgroup (query block, b nh + h) reads head h: its query, key and value
-// dims h HD .. h HD + HD - 1. For HD = 32 the tiles' dims 32..63 stay zero (S runs over 32 dims) and
-// P V has one 32-column output: the two waves of a row half each take half of the tile's keys.
+// dims h HD .. h HD + HD - 1. The Q, K and V tiles are HD wide; for HD = 32, P V has one 32-column
+// output: the two waves of a row half each take half of the tile's keys.
 template <typename KV, int HD>
 __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restrict__ q, int ldq,
                                                           const KV *__restrict__ ks, const KV *__restrict__ vs,
@@ -422,20 +422,21 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     static_assert(HD == 32 || HD == 64, "head size 32 or 64");
     if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device (a replayed graph)
     constexpr int L = 65;               // LDS row stride (odd: a column read hits 32 banks)
+    constexpr int LK = HD + 1;          // the same for the head's Q, K and V tiles (HD 32: 3 workgroups per CU)
     // scores in base-2 units (s log2 e), so the softmax's exponentials are the hardware 2^x
     // (v_exp_f32): with m the running max in those units, 2^(s log2 e - m) = e^(s - m ln 2), and
     // the normalized weights are the softmax's up to rounding
     const float scale2 = scale * 1.44269504088896341f;
-    __shared__ float sQ[64 * L], sK[64 * L], sV[64 * L], sP[64 * L];
+    __shared__ float sQ[64 * LK], sK[64 * LK], sV[64 * LK], sP[64 * L];
     __shared__ float s_corr[64], s_den[64];
     const int bi = blockIdx.y / nh, hh = blockIdx.y - bi * nh, qb = blockIdx.x * 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lc = lane & 31;
     const int row0 = (wave >> 1) * 32, col0 = (wave & 1) * 32;
     const int r = tid >> 2, sub = tid & 3;  // the softmax's row and quarter
     const KV *kb = ks + (size_t)bi * cap * de + hh * HD, *vb = vs + (size_t)bi * cap * de + hh * HD;
-    for (int i = tid; i < 64 * 64; i += 256) {
-        const int rr = i >> 6, cc = i & 63;
-        sQ[rr * L + cc] = qb + rr < T && cc < HD ? q[((size_t)bi * T + qb + rr) * ldq + hh * HD + cc] : 0.0f;
+    for (int i = tid; i < 64 * HD; i += 256) {
+        const int rr = i / HD, cc = i % HD;
+        sQ[rr * LK + cc] = qb + rr < T ? q[((size_t)bi * T + qb + rr) * ldq + hh * HD + cc] : 0.0f;
     }
     auto qrow = [&](int i) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); };
     float mx = -INFINITY, den = 0.0f;
@@ -459,8 +460,10 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
         __syncthreads();  // the previous tile's K, V and P are read
 #pragma unroll
         for (int z = 0; z < 16; z++) {
-            sK[r * L + sub * 16 + z] = kr[z];
-            sV[r * L + sub * 16 + z] = vr[z];
+            if (sub * 16 < HD) {
+                sK[r * LK + sub * 16 + z] = kr[z];
+                sV[r * LK + sub * 16 + z] = vr[z];
+            }
         }
         if (k0 + 64 < kend) fetch(k0 + 64);
         __syncthreads();
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
             const int fr = lane & 31, h = lane >> 5;
 #pragma unroll 8
             for (int x = 0; x < HD; x += 2)
-                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[(row0 + fr) * L + x + h], sK[(col0 + fr) * L + x + h], sa,
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[(row0 + fr) * LK + x + h], sK[(col0 + fr) * LK + x + h], sa,
                                                           0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
             if constexpr (HD == 64) {
 #pragma unroll 8
                 for (int x = 0; x < 64; x += 2)
-                    o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + x + h], sV[(x + h) * L + col0 + fr],
+                    o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + x + h], sV[(x + h) * LK + col0 + fr],
                                                              o, 0, 0, 0);
             } else {
                 // one 32-column output: the wave pair of a row half splits the tile's keys, each
@@ -520,7 +523,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
 #pragma unroll 8
                 for (int x = 0; x < 32; x += 2)
                     o = __builtin_amdgcn_mfma_f32_32x32x2f32(sP[(row0 + fr) * L + kh + x + h],
-                                                             sV[(kh + x + h) * L + fr], o, 0, 0, 0);
+                                                             sV[(kh + x + h) * LK + fr], o, 0, 0, 0);
             }
         }
     }
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
         // which every wave passed before the last tile's softmax barrier)
         if (col0)
 #pragma unroll
-            for (int i = 0; i < 16; i++) sQ[(row0 + qrow(i)) * L + lc] = o[i];
+            for (int i = 0; i < 16; i++) sQ[(row0 + qrow(i)) * LK + lc] = o[i];
     }
     if (sub == 0) s_den[r] = den;
     __syncthreads();
@@ -540,7 +543,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
             if (qb + rr < T) out[((size_t)bi * T + qb + rr) * de + hh * HD + col0 + lc] = o[i] / s_den[rr];
         } else {
             if (qb + rr < T && col0 == 0)
-                out[((size_t)bi * T + qb + rr) * de + hh * HD + lc] = (o[i] + sQ[rr * L + lc]) / s_den[rr];
+                out[((size_t)bi * T + qb + rr) * de + hh * HD + lc] = (o[i] + sQ[rr * LK + lc]) / s_den[rr];
         }
     }
 }
