@@ -50,3 +50,19 @@ def test_ops_refuse_host_tensors():
         ops.kwta_relu(torch.zeros((2, 8)), 2)
     with pytest.raises(ValueError):
         ops.lif_gen(torch.zeros((1, 2, 8)), torch.zeros(8))
+
+
+def test_attend_heads_argument_errors():
+    """The heads read refuses NULL buffers and head geometries it does not run before touching the GPU;
+    its partials size follows (heads x (hd + 2)) floats per row and chunk."""
+    L = lib()
+    vp = C.c_void_p
+    rc = L.ava_attend_heads(None, 128, None, None, 0, 8, 0, 1, 1, 128, 4, None, None, 0, None)
+    assert rc == 1 and b"NULL" in L.ava_last_error()
+    dummy = vp(64)  # never dereferenced: the shape checks come first
+    for de, heads in ((96, 3), (128, 3), (256, 2), (128, 0)):
+        rc = L.ava_attend_heads(dummy, de, dummy, dummy, 0, 8, 0, 1, 1, de, heads, dummy, dummy, 0, None)
+        assert rc == 2 and b"heads" in L.ava_last_error(), (de, heads)
+    assert L.ava_attend_heads_part_floats(2, 1, 1500, 1024, 32) == 2 * 1 * 32 * 2 * 34
+    assert L.ava_attend_heads_part_floats(2, 1, 1500, 64, 1) == L.ava_attend_part_floats(2, 1, 1500) == 2 * 2 * 66
+    assert L.ava_attend_heads_part_floats(2, 8, 1500, 1024, 32) == 0  # the tiled form needs none
