@@ -427,7 +427,8 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     // (v_exp_f32): with m the running max in those units, 2^(s log2 e - m) = e^(s - m ln 2), and
     // the normalized weights are the softmax's up to rounding
     const float scale2 = scale * 1.44269504088896341f;
-    __shared__ float sQ[64 * LK], sK[64 * LK], sV[64 * LK], sP[64 * L];
+    // Q lives in registers (each wave's MFMA operand column of its 32 query rows); sK stages it first
+    __shared__ float sK[64 * LK], sV[64 * LK], sP[64 * L];
     __shared__ float s_corr[64], s_den[64];
     const int bi = blockIdx.y / nh, hh = blockIdx.y - bi * nh, qb = blockIdx.x * 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lc = lane & 31;
@@ -436,8 +437,12 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     const KV *kb = ks + (size_t)bi * cap * de + hh * HD, *vb = vs + (size_t)bi * cap * de + hh * HD;
     for (int i = tid; i < 64 * HD; i += 256) {
         const int rr = i / HD, cc = i % HD;
-        sQ[rr * LK + cc] = qb + rr < T ? q[((size_t)bi * T + qb + rr) * ldq + hh * HD + cc] : 0.0f;
+        sK[rr * LK + cc] = qb + rr < T ? q[((size_t)bi * T + qb + rr) * ldq + hh * HD + cc] : 0.0f;
     }
+    __syncthreads();
+    float qf[HD / 2];  // lane (fr, h): Q[row0 + fr][x + h] for x = 0, 2, ..
+#pragma unroll
+    for (int x = 0; x < HD; x += 2) qf[x >> 1] = sK[(row0 + (lane & 31)) * LK + x + (lane >> 5)];
     auto qrow = [&](int i) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); };
     float mx = -INFINITY, den = 0.0f;
     f32x16 o = {};
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     };
     fetch(0);
     for (int k0 = 0; k0 < kend; k0 += 64) {
-        __syncthreads();  // the previous tile's K, V and P are read
+        __syncthreads();  // the previous tile's K, V and P (the first time: Q) are read
 #pragma unroll
         for (int z = 0; z < 16; z++) {
             if (sub * 16 < HD) {
@@ -470,10 +475,9 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
         {
             f32x16 sa = {};
             const int fr = lane & 31, h = lane >> 5;
-#pragma unroll 8
+#pragma unroll
             for (int x = 0; x < HD; x += 2)
-                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[(row0 + fr) * LK + x + h], sK[(col0 + fr) * LK + x + h], sa,
-                                                          0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(qf[x >> 1], sK[(col0 + fr) * LK + x + h], sa, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int rr = row0 + qrow(i), cc = col0 + lc;
@@ -528,11 +532,11 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
         }
     }
     if constexpr (HD == 32) {
-        // the second key half's partials through sQ (no wave reads sQ after its last S product,
+        // the second key half's partials through sK (no wave reads sK after its last S product,
         // which every wave passed before the last tile's softmax barrier)
         if (col0)
 #pragma unroll
-            for (int i = 0; i < 16; i++) sQ[(row0 + qrow(i)) * LK + lc] = o[i];
+            for (int i = 0; i < 16; i++) sK[(row0 + qrow(i)) * LK + lc] = o[i];
     }
     if (sub == 0) s_den[r] = den;
     __syncthreads();
@@ -543,7 +547,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
             if (qb + rr < T) out[((size_t)bi * T + qb + rr) * de + hh * HD + col0 + lc] = o[i] / s_den[rr];
         } else {
             if (qb + rr < T && col0 == 0)
-                out[((size_t)bi * T + qb + rr) * de + hh * HD + lc] = (o[i] + sQ[rr * LK + lc]) / s_den[rr];
+                out[((size_t)bi * T + qb + rr) * de + hh * HD + lc] = (o[i] + sK[rr * LK + lc]) / s_den[rr];
         }
     }
 }
