@@ -20,6 +20,8 @@ those parts are left out of the forward.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 from . import synth
@@ -125,15 +127,64 @@ def parse_arch(text: str):
     return cfg, unsupported
 
 
+# The engram's head size in the reference (gpu/model.rs:43 HEAD_SIZE, read by memory::read,
+# gpu/memory.rs:610-700). A file this package writes records its own head count in the safetensors
+# metadata under this key (BASELINE's single head of 64 is not the reference's geometry).
+ENGRAM_HEAD = 32
+META_ENG_HEADS = "ava.eng_heads"
+
+
 def _tensors(path):
     from safetensors.numpy import load_file
     return load_file(path)
 
 
-def load_safetensors(path: str, arch: str, strict: bool = True, **overrides):
-    """(cfg, params) of a model file in the reference's naming and its arch string. Dimensions come
-    from the tensors (d and vocab from tok_emb, layers from b{i}.mem.win, hidden from b0.mlp.w1, the
-    engram block and width from b{i}.eng.wq); overrides set the rest (cap, cb_eta, cb_half, eng_half)."""
+def _metadata(path):
+    from safetensors import safe_open
+    with safe_open(path, framework="np") as f:
+        return f.metadata() or {}
+
+
+def arch_name(path: str) -> str:
+    """NAME.arch.txt for the model file NAME.safetensors (gpu/ckpt.rs:92-95: the last extension
+    replaced by arch.txt)."""
+    root, ext = os.path.splitext(path)
+    return (root if ext else path) + ".arch.txt"
+
+
+def arch_beside(path: str):
+    """The block options a model file was made with and the file they came from (gpu/ckpt.rs:97-112):
+    NAME.arch.txt beside the model file, else arch.txt in its folder; None when neither exists."""
+    for p in (arch_name(path), os.path.join(os.path.dirname(os.path.abspath(path)), "arch.txt")):
+        if os.path.isfile(p):
+            with open(p) as f:
+                return f.read().strip(), p
+    return None
+
+
+def write_arch_beside(path: str, cfg: dict) -> str:
+    """Write cfg's block options as NAME.arch.txt beside the model file (gpu/ckpt.rs:114-124), so the
+    file loads without an arch argument. Returns the path written."""
+    p = arch_name(path)
+    with open(p, "w") as f:
+        f.write(arch_of(cfg) + "\n")
+    return p
+
+
+def load_safetensors(path: str, arch: str | None = None, strict: bool = True, **overrides):
+    """(cfg, params) of a model file in the reference's naming. The block options come from `arch`, or
+    when it is None from the arch.txt found beside the file (arch_beside; ValueError if there is none:
+    this build runs only models with block options). Dimensions come from the tensors (d and vocab from
+    tok_emb, layers from b{i}.mem.win, hidden from b0.mlp.w1, the engram block and width from
+    b{i}.eng.wq); the engram's heads are the reference's heads of 32 (eng_dim / 32) unless the file's
+    metadata records another count. overrides set the rest (cap, cb_eta, cb_half, eng_half,
+    eng_heads)."""
+    if arch is None:
+        found = arch_beside(path)
+        if found is None:
+            raise ValueError(f"{path}: no block options given and none beside the file "
+                             f"({arch_name(path)} or arch.txt in its folder)")
+        arch = found[0]
     rec, unsupported = parse_arch(arch)
     if unsupported and strict:
         raise ValueError("arch: parts this build does not run: " + ", ".join(unsupported))
@@ -153,8 +204,11 @@ def load_safetensors(path: str, arch: str, strict: bool = True, **overrides):
         raise ValueError(f"{path}: engram reads in blocks {eng} (this build runs one)")
     eng_block = eng[0] if eng else -1
     eng_dim = t[f"b{eng_block}.eng.wq"].shape[1] if eng else 64
+    meta = _metadata(path)
+    eng_heads = int(meta[META_ENG_HEADS]) if META_ENG_HEADS in meta else max(1, eng_dim // ENGRAM_HEAD)
     cfg = dict(vocab=V, d=d, layers=layers, hidden=hidden, kwta_k=hidden // rec.pop("kwta_div"),
-               eng_block=eng_block, eng_dim=eng_dim, cap=synth.MEM_CAP, cb_units=rec.pop("cb_units", 0))
+               eng_block=eng_block, eng_dim=eng_dim, eng_heads=eng_heads if eng else 1, cap=synth.MEM_CAP,
+               cb_units=rec.pop("cb_units", 0))
     cfg.update(rec)
     if cfg["cb_units"]:
         cfg.update(cb_eta=0.3, cb_half=256.0)
@@ -189,9 +243,10 @@ def load_safetensors(path: str, arch: str, strict: bool = True, **overrides):
     return cfg, params
 
 
-def save_safetensors(path: str, cfg: dict, params: dict):
+def save_safetensors(path: str, cfg: dict, params: dict, write_arch: bool = False):
     """Write params in the reference's naming (the inverse of load_safetensors: `off` is not stored,
-    `vres` only for blocks after the first, the engram only in its block)."""
+    `vres` only for blocks after the first, the engram only in its block). The engram's head count goes
+    into the file's metadata. With write_arch, NAME.arch.txt is written beside it (write_arch_beside)."""
     from safetensors.numpy import save_file
     out = {TOP_NAMES[k]: np.ascontiguousarray(params[k], dtype=np.float32) for k in ("tok_emb", "final_norm")}
     if params.get("cb_w") is not None:
@@ -201,7 +256,12 @@ def save_safetensors(path: str, cfg: dict, params: dict):
             if f not in b or (f == "vres" and i == 0) or (f in ENGRAM and i != cfg["eng_block"]):
                 continue
             out[pat.format(i=i)] = np.ascontiguousarray(b[f], dtype=np.float32)
-    save_file(out, path)
+    meta = {}
+    if cfg.get("eng_block", -1) >= 0:
+        meta[META_ENG_HEADS] = str(max(1, int(cfg.get("eng_heads", 1) or 1)))
+    save_file(out, path, metadata=meta or None)
+    if write_arch:
+        write_arch_beside(path, cfg)
 
 
 def arch_of(cfg: dict) -> str:

@@ -450,9 +450,10 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     const int kend = min(n0 + qb + 64, n0 + T);  // keys the block's last row reads
     // thread (r, sub) stages key/value row r, dims 16 sub .. 16 sub + 15; the next tile's are loaded
     // into registers while this tile is computed
-    float kr[16], vr[16];
+    float kr[16] = {}, vr[16] = {};
     auto fetch = [&](int k0) {
-        const bool ok = k0 + r < kend && sub * 16 < HD;
+        if (sub * 16 >= HD) return;  // HD = 32: the threads of dims 32..63 stage nothing
+        const bool ok = k0 + r < kend;
         const size_t o16 = (size_t)(k0 + (ok ? r : 0)) * de + (ok ? sub * 16 : 0);
         KvLane<KV>::load16(kb + o16, kr);
         KvLane<KV>::load16(vb + o16, vr);

@@ -195,7 +195,7 @@ extern "C" int ava_lif_scan(const float *cur, int B, int T, int D, const float *
                                (hipStream_t)stream);
 }
 
-// Tuning entry (not part of ava.h): explicit lanes-per-channel-group and prefetch depth.
+// ava_lif_scan with the kernel variant named (channels per lane, steps in flight).
 extern "C" int ava_lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v,
                                   float *s, float *a, int levels, int is_signed, int alif, int8_t *spikes,
                                   float *th_out, int vec, int pf, ava_stream stream) {

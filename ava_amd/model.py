@@ -21,6 +21,10 @@ import torch
 
 from ._lib import BLOCK_FIELDS, BlockParams, Config, Params, State as _CState, check, lib
 
+# The end-of-text id of the reference's byte-pair vocabulary (ava_data::bpe::EOS, data/src/bpe.rs:57),
+# at which its generate ends a row (gpu/state.rs:1402, 1436).
+EOS = 256
+
 
 def _ptr(a, keep):
     a = np.ascontiguousarray(a, dtype=np.float32)
@@ -128,8 +132,10 @@ class Model:
         self.h = h
 
     @classmethod
-    def from_safetensors(cls, path: str, arch: str, strict: bool = True, planes: int = 3, **overrides) -> "Model":
-        """A model file in the reference's naming with its arch string (ava_amd.checkpoint)."""
+    def from_safetensors(cls, path: str, arch: str | None = None, strict: bool = True, planes: int = 3,
+                         **overrides) -> "Model":
+        """A model file in the reference's naming (ckpt::load_auto, gpu/ckpt.rs:51-72) with its arch
+        string, or with the arch.txt found beside it when arch is None (ava_amd.checkpoint)."""
         from .checkpoint import load_safetensors
         cfg, params = load_safetensors(path, arch, strict=strict, **overrides)
         return cls(cfg, params, planes=planes)
@@ -275,11 +281,13 @@ class Model:
               "ava_model_cb_learn")
         return nats
 
-    def generate(self, prompts, max_new: int, pick=None, stop=None, eos: int | None = None,
+    def generate(self, prompts, max_new: int, pick=None, stop=None, eos: int | None = EOS,
                  batch_rows: int = 256) -> list:
         """Continuations of every prompt with carried state (generate, gpu/state.rs:1392-1458): the
         prompts are read in batched passes, then the rows step together, one token per pass; a row
-        leaves at eos (not included) or when stop(tokens) is true. pick(row, logits [vocab]) chooses
+        leaves at eos (not included; the reference's ava_data::bpe::EOS = 256 by default, as its
+        generate always ends a row there; None: rows never stop at a token, as for synthetic
+        vocabularies) or when stop(tokens) is true. pick(row, logits [vocab]) chooses
         a token (default: greedy, the lowest id on ties). Rows of one pass share a prompt length
         (this state keeps one store length for all its streams); rows are independent, so the
         grouping does not change any row's tokens. Returns each prompt's tokens."""

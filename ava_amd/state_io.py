@@ -40,9 +40,39 @@ def fnv1a64(data: bytes, h: int = FNV_OFFSET) -> int:
     return int(lib().ava_fnv1a64(C.cast(buf, C.c_void_p), len(data), C.c_uint64(h)))
 
 
+# The configuration as hashed: a fixed list of the fields that change the forward or the state's
+# layout, each with its default, normalised to int or float (the reference hashes the Debug text of
+# its Config, gpu/state.rs:1075-1092, which is likewise one canonical print per configuration).
+_CANON = (("vocab", int, None), ("d", int, None), ("layers", int, None), ("hidden", int, None),
+          ("kwta_k", int, None), ("head_size", int, 64), ("gate_rank", int, None), ("eng_block", int, -1),
+          ("eng_dim", int, 64), ("eng_heads", int, 1), ("eng_half", int, 0), ("levels", int, 2), ("alif", int, 0),
+          ("lif_scale", int, 0), ("value_residual", int, 0), ("dense", int, 0), ("relu2", int, 0),
+          ("momentum", float, 0.0), ("cap", float, None), ("cb_units", int, 0))
+_CANON_CB = (("cb_eta", float, None), ("cb_lr", float, None), ("cb_half", float, 0.0))
+
+
 def cfg_text(cfg: dict) -> str:
-    """The configuration as hashed: its items sorted by name, repr'd."""
-    return repr(sorted((str(k), v) for k, v in cfg.items()))
+    """The configuration as hashed: the canonical fields in a fixed order, with their defaults filled in
+    and their types normalised, so the same model built from arrays or from its file hashes the same.
+    The engram's fields count only with an engram, the cerebellum's only with a cerebellum."""
+    def val(k, ty, dflt):
+        v = cfg.get(k, dflt)
+        if v is None:
+            return None
+        return ty(bool(v)) if ty is int and isinstance(v, bool) else ty(v)
+
+    items = []
+    eng = int(cfg.get("eng_block", -1)) >= 0
+    for k, ty, dflt in _CANON:
+        v = val(k, ty, dflt)
+        if k in ("eng_dim", "eng_heads", "eng_half") and not eng:
+            continue
+        if k == "eng_heads":
+            v = max(1, v or 1)
+        items.append((k, v))
+    if int(cfg.get("cb_units", 0) or 0) > 0:
+        items += [(k, val(k, ty, dflt)) for k, ty, dflt in _CANON_CB]
+    return repr(items)
 
 
 def _sample(t, stride: int) -> bytes:

@@ -441,7 +441,7 @@ class Greedy:
         self.out = None
 
     def step(self, stream, ev=None):
-        self.out = self.model.generate([self.prompt], self.new)[0]
+        self.out = self.model.generate([self.prompt], self.new, eos=None)[0]  # config[0]: 128 steps
 
     def kernel_ms(self):
         return [self.wall * 1e3 / self.nsteps]  # the whole generation, per step

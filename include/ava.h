@@ -104,6 +104,13 @@ int ava_q8_matmul_i8(const int8_t *s, int m, const ava_qw *w, float *y, ava_stre
 int ava_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
                  int levels, int is_signed, int alif, int8_t *spikes, float *th_out, ava_stream stream);
 
+/* ava_lif_scan with the kernel variant named: vec channels per lane (1, 2 or 4) and pf time steps
+ * in flight per lane (8 .. 64); 0 = the default ava_lif_scan picks. Every variant gives the same bits
+ * (the GPU tests check each one); AVA_ERR_ARG for a pair that has no kernel. Same reference op. */
+int ava_lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
+                       int levels, int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf,
+                       ava_stream stream);
+
 /* ------------------------------------------------------------------ kWTA */
 
 /* Per row of u [n][h]: kth = the k-th largest value (duplicates counted); keep u_i when

@@ -250,10 +250,14 @@ static float spike_of(float v, float th, int levels, int is_signed) {
     return h;
 }
 
+/* Each (b, c) is its own sequential scan, so the units run in parallel with the same bits at any
+ * thread count. */
 void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
                   float *a, int levels, int is_signed, int alif, int8_t *spikes) {
-    for (int bi = 0; bi < B; bi++)
-        for (int c = 0; c < D; c++) {
+#pragma omp parallel for schedule(static)
+    for (long i_ = 0; i_ < (long)B * D; i_++) {
+        {
+            const int bi = (int)(i_ / D), c = (int)(i_ % D);
             int i = bi * D + c;
             float bt = ps[c], th0 = ps[D + c], rho = ps[2 * D + c], gain = ps[3 * D + c];
             float omr = 1.0f - rho;
@@ -275,6 +279,7 @@ void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float 
             s[i] = sp;
             a[i] = aa;
         }
+    }
 }
 
 /* ------------------------------------------------------------------ kWTA */
@@ -285,7 +290,10 @@ static int cmp_desc(const void *pa, const void *pb) {
 }
 
 void orc_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *kth_out) {
+#pragma omp parallel
+    {
     float *buf = (float *)malloc(sizeof(float) * (size_t)h);
+#pragma omp for schedule(static)
     for (int r = 0; r < n; r++) {
         const float *ur = u + (size_t)r * h;
         float *ar = a + (size_t)r * h;
@@ -306,6 +314,7 @@ void orc_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *k
         }
     }
     free(buf);
+    }
 }
 
 /* ------------------------------------------------------------------ fast-weight memory */
@@ -313,9 +322,12 @@ void orc_kwta(const float *u, int n, int h, int k, int relu2, float *a, float *k
 void orc_mem_rec(const float *q, const float *k, const float *e, const float *v, const float *la,
                  const float *b, int BH, int T, int hs, int g, float m, float cap, float *F,
                  float *S, float *y) {
+#pragma omp parallel
+    {
     float *r = (float *)malloc(sizeof(float) * (size_t)hs);
     float *al = (float *)malloc(sizeof(float) * (size_t)hs);
     float *bb = (float *)malloc(sizeof(float) * (size_t)hs);
+#pragma omp for schedule(dynamic)
     for (int bh = 0; bh < BH; bh++) {
         float *f = F + (size_t)bh * hs * hs;
         float *sm = S ? S + (size_t)bh * hs * hs : NULL;
@@ -355,12 +367,16 @@ void orc_mem_rec(const float *q, const float *k, const float *e, const float *v,
     free(r);
     free(al);
     free(bb);
+    }
 }
 
 void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float *v,
                      const float *la, const float *b, int BH, int T, int hs, int g, double m,
                      double *F, double *S, double *y) {
+#pragma omp parallel
+    {
     double *r = (double *)malloc(sizeof(double) * (size_t)hs);
+#pragma omp for schedule(dynamic)
     for (int bh = 0; bh < BH; bh++) {
         double *f = F + (size_t)bh * hs * hs;
         double *sm = S ? S + (size_t)bh * hs * hs : NULL;
@@ -392,6 +408,7 @@ void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float
         }
     }
     free(r);
+    }
 }
 
 /* ------------------------------------------------------------------ model */

@@ -66,3 +66,112 @@ def test_attend_heads_argument_errors():
     assert L.ava_attend_heads_part_floats(2, 1, 1500, 1024, 32) == 2 * 1 * 32 * 2 * 34
     assert L.ava_attend_heads_part_floats(2, 1, 1500, 64, 1) == L.ava_attend_part_floats(2, 1, 1500) == 2 * 2 * 66
     assert L.ava_attend_heads_part_floats(2, 8, 1500, 1024, 32) == 0  # the tiled form needs none
+
+
+# ----------------------------------------------------------------------------- the binding guide vs the header
+
+_C_WIDTH = {"int": "i32", "float": "f32", "double": "f64", "size_t": "usize", "uint64_t": "u64"}
+_RS_WIDTH = {"c_int": "i32", "i32": "i32", "c_float": "f32", "f32": "f32", "c_double": "f64", "f64": "f64",
+             "usize": "usize", "u64": "u64"}
+
+
+def header_structs():
+    """{struct name: [(field, width)]} of include/ava.h's typedef structs; pointers are 'ptr'."""
+    hdr = open(os.path.join(ROOT, "include", "ava.h")).read()
+    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+    out = {}
+    for body, name in re.findall(r"typedef struct\s*\{(.*?)\}\s*(\w+)\s*;", hdr, flags=re.S):
+        fields = []
+        for decl in body.split(";"):
+            decl = " ".join(decl.split())
+            if not decl:
+                continue
+            m = re.match(r"((?:const\s+)?\w+)\s+(.*)", decl)
+            base, rest = m.group(1).replace("const ", ""), m.group(2)
+            for dcl in rest.split(","):
+                dcl = dcl.strip()
+                ptr = dcl.startswith("*")
+                fields.append((dcl.lstrip("*").strip(), "ptr" if ptr else _C_WIDTH[base]))
+        out[name] = fields
+    return out
+
+
+def header_functions():
+    """{function name: number of parameters} of include/ava.h."""
+    hdr = open(os.path.join(ROOT, "include", "ava.h")).read()
+    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(ava_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", hdr):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else len(args.split(","))
+    return out
+
+
+def guide_rust():
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    return text[text.index("```rust"):text.index("```", text.index("```rust") + 7)]
+
+
+def guide_structs():
+    out = {}
+    for name, body in re.findall(r"#\[repr\(C\)\]\s*pub struct (\w+)\s*\{(.*?)\n?\}", guide_rust(), flags=re.S):
+        body = re.sub(r"//[^\n]*", "", body)
+        fields = []
+        for name_, ty in re.findall(r"pub (\w+):\s*([^,]+?)\s*(?:,|$)", body.strip()):
+            ty = ty.strip()
+            fields.append((name_, "ptr" if ty.startswith("*") else _RS_WIDTH[ty]))
+        if fields:
+            out[name] = fields
+    return out
+
+
+def guide_functions():
+    block = guide_rust()
+    block = block[block.index('extern "C"'):]
+    out = {}
+    for name, args in re.findall(r"pub fn (ava_\w+)\s*\(([^)]*)\)", block, flags=re.S):
+        args = args.strip().rstrip(",")
+        out[name] = 0 if not args else len(args.split(","))
+    return out
+
+
+def test_binding_guide_structs_match_the_header():
+    """INTEGRATION.md's #[repr(C)] structs have the header's fields in the header's order and widths,
+    so a binding written from the guide passes structs of the right size and layout."""
+    hs, gs = header_structs(), guide_structs()
+    for name in ("ava_qw", "ava_config", "ava_block_params", "ava_params", "ava_state"):
+        assert name in hs and name in gs, name
+        assert gs[name] == hs[name], (name, [a for a, b in zip(gs[name], hs[name]) if a != b] or
+                                      (len(gs[name]), len(hs[name])))
+
+
+def test_binding_guide_declares_every_entry_point():
+    """Every function of include/ava.h is in the guide's extern block with the same number of arguments."""
+    hf, gf = header_functions(), guide_functions()
+    assert set(hf) == set(declared())
+    missing = sorted(set(hf) - set(gf))
+    assert not missing, missing
+    wrong = {n: (gf[n], hf[n]) for n in hf if gf[n] != hf[n]}
+    assert not wrong, wrong
+
+
+def test_ctypes_structs_match_the_header():
+    """ava_amd/_lib.py's ctypes structs have the header's field order and widths."""
+    from ava_amd import _lib
+    width = {C.c_int: "i32", C.c_float: "f32", C.c_double: "f64", C.c_size_t: "usize", C.c_uint64: "u64"}
+
+    def fields(cls):
+        out = []
+        for name, ty in cls._fields_:
+            if ty in width:
+                out.append((name, width[ty]))
+            else:
+                assert ty is C.c_void_p or issubclass(ty, C._Pointer), (cls, name, ty)
+                out.append((name, "ptr"))
+        return out
+
+    hs = header_structs()
+    pairs = {"ava_qw": _lib.QW, "ava_config": _lib.Config, "ava_block_params": _lib.BlockParams,
+             "ava_params": _lib.Params, "ava_state": _lib.State}
+    for name, cls in pairs.items():
+        assert fields(cls) == hs[name], name

@@ -37,7 +37,7 @@ def test_generate_matches_oracle_greedy():
     stop = lambda toks: len(toks) >= 3 and toks[-1] % 7 == 0  # a row may leave early
     print(f"generate prompts={[len(p) for p in prompts]}", flush=True)
     m = Model(cfg, prm)
-    got = m.generate(prompts, 10, stop=stop, batch_rows=8)
+    got = m.generate(prompts, 10, stop=stop, batch_rows=8, eos=None)
     om = O.OracleModel(cfg, prm)
     for r, p in enumerate(prompts):
         want, gaps = oracle_greedy(om, p, 10, stop)
@@ -54,5 +54,5 @@ def test_generate_refuses_empty_prompt_and_honours_eos():
     m = Model(cfg, synth.params(cfg, seed=19))
     with pytest.raises(ValueError):
         m.generate([[1, 2], []], 4)
-    first = m.generate([[3, 4, 5]], 1)[0][0]
+    first = m.generate([[3, 4, 5]], 1, eos=None)[0][0]
     assert m.generate([[3, 4, 5]], 6, eos=first) == [[]]  # eos is not included, and ends the row

@@ -135,3 +135,20 @@ def test_cap_saved_and_refused_rules(tmp_path):
     save_file(t, path)
     with pytest.raises(ValueError, match="eviction rule"):
         sio.load_state(path, cfg, 3, device="cpu")
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_heads", "tiny_cb"])
+def test_array_and_file_models_share_a_fingerprint(name, tmp_path):
+    """The same weights built from arrays and read back from their model file key the same states:
+    the configuration is hashed in one canonical form (fixed fields, defaults filled, types normalised)."""
+    from ava_amd import checkpoint as ck
+    cfg = synth.config(name)
+    prm = synth.params(cfg, seed=7)
+    path = str(tmp_path / "m.safetensors")
+    ck.save_safetensors(path, cfg, prm)
+    over = dict(cb_eta=cfg["cb_eta"], cb_half=cfg["cb_half"]) if cfg.get("cb_units") else {}
+    cfg2, prm2 = ck.load_safetensors(path, ck.arch_of(cfg), **over)
+    assert sio.cfg_text(cfg2) == sio.cfg_text(cfg)
+    assert sio.fingerprint(cfg2, prm2) == sio.fingerprint(cfg, prm)
+    other = dict(cfg, momentum=0.25)
+    assert sio.fingerprint(other, prm) != sio.fingerprint(cfg, prm)
