@@ -71,6 +71,7 @@ def lib():
         "ava_q8_gemm_acc": [vp, i32, i32, C.POINTER(QW), vp, vp],
         "ava_q8_matmul": [vp, i32, C.POINTER(QW), i32, vp, vp, sz, vp],
         "ava_q8_matmul_i8": [vp, i32, C.POINTER(QW), vp, vp],
+        "ava_q8_matmul_noalloc": [vp, i32, C.POINTER(QW), i32, vp, vp],
         "ava_q8_matmul_planes": [vp, vp, i32, i32, C.POINTER(QW), vp, vp],
         "ava_lif_scan": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
         "ava_lif_scan_tuned": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, vp],

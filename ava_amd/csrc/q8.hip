@@ -21,6 +21,7 @@
 #include <type_traits>
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -1380,4 +1381,58 @@ extern "C" int ava_q8_matmul_planes(const int8_t *xq, const int32_t *xexp, int p
     AVA_REQUIRE(xexp, AVA_ERR_ARG, "q8_matmul_planes: NULL row exponents");
     AVA_REQUIRE(m >= 0, AVA_ERR_SHAPE, "q8_matmul_planes: m=%d", m);
     return ava::q8_gemm(xq, xexp, planes, m, w, EPI_STORE, y, w ? w->dout : 0, nullptr, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ the product without allocation
+
+namespace {
+
+// The split planes and row exponents of ava_q8_matmul_noalloc: a file-scope device array, one copy
+// per GPU the library runs on, held until the process ends. In host code `scratch` names a host-side
+// stand-in, not device memory: its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is passed to kernels.
+constexpr size_t Q8_SCRATCH_BYTES = (size_t)32 << 20;
+__device__ __align__(256) unsigned char scratch[Q8_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device (looked up on the first call there).
+int scratch_ptr(void **out) {
+    int dev = 0;
+    AVA_HIP(hipGetDevice(&dev));
+    AVA_REQUIRE(dev >= 0 && dev < MAX_DEVICES, AVA_ERR_UNSUPPORTED, "q8_matmul_noalloc: device %d (0..%d)", dev,
+                MAX_DEVICES - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        AVA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        AVA_REQUIRE(p, AVA_ERR_HIP, "q8_matmul_noalloc: no device address for the scratch array");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return AVA_OK;
+}
+
+}  // namespace
+
+extern "C" int ava_q8_matmul_noalloc(const float *x, int m, const ava_qw *w, int planes, float *y,
+                                     ava_stream stream) {
+    if (int r = check_qw(w)) return r;
+    AVA_REQUIRE(x && y, AVA_ERR_ARG, "q8_matmul_noalloc: NULL buffer");
+    AVA_REQUIRE(planes >= 1 && planes <= 3, AVA_ERR_ARG, "q8_matmul_noalloc: planes %d (1..3)", planes);
+    AVA_REQUIRE(m >= 0, AVA_ERR_SHAPE, "q8_matmul_noalloc: m=%d", m);
+    const size_t need = ava_q8_workspace(m, w->din, planes);
+    AVA_REQUIRE(need <= Q8_SCRATCH_BYTES, AVA_ERR_SHAPE,
+                "q8_matmul_noalloc: %d rows of %d inputs in %d planes need %zu bytes of scratch; the library's "
+                "scratch holds %zu (use ava_q8_matmul with a workspace)", m, w->din, planes, need, Q8_SCRATCH_BYTES);
+    if (m == 0) return AVA_OK;
+    void *ws = nullptr;
+    if (int r = scratch_ptr(&ws)) return r;
+    hipStream_t st = (hipStream_t)stream;
+    int8_t *xq = (int8_t *)ws;
+    int32_t *xe = (int32_t *)(((uintptr_t)(xq + (size_t)planes * m * w->ldk) + 255) & ~(uintptr_t)255);
+    if (int r = ava::launch_quant_rows(x, m, w->din, w->din, planes, xq, xe, st)) return r;
+    return ava::q8_gemm(xq, xe, planes, m, w, EPI_STORE, y, w->dout, nullptr, st);
 }

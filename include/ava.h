@@ -81,6 +81,15 @@ size_t ava_q8_workspace(int m, int k, int planes);
 int ava_q8_matmul(const float *x, int m, const ava_qw *w, int planes, float *y, void *ws,
                   size_t ws_bytes, ava_stream stream);
 
+/* ava_q8_matmul without a workspace argument and without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The planes live in a static device array of the library, 32 MiB
+ * per GPU, held until the process ends: ava_q8_workspace(m, din, planes) must be at most 32 MiB
+ * (AVA_ERR_SHAPE otherwise). Every call on one GPU shares that array, so calls that overlap on one
+ * GPU (on different streams, or from different threads) race; calls on one stream are ordered.
+ * Nothing in the array needs clearing: each call writes all it reads. Same results as ava_q8_matmul. */
+int ava_q8_matmul_noalloc(const float *x, int m, const ava_qw *w, int planes, float *y, ava_stream stream);
+
 /* y [m][dout] from activations already in split-plane form (xq [planes][m][ldk], xexp [m], as
  * ava_q8_quant_rows writes them): the product and combine of ava_q8_matmul without the quantizer.
  * Replaces int8::mm (int8.rs:672-683) where the producer of x writes planes directly. */
