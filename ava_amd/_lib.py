@@ -106,6 +106,8 @@ def lib():
     if hasattr(L, "ava_model_scratch_bytes"):
         L.ava_model_scratch_bytes.argtypes = [vp]
         L.ava_model_scratch_bytes.restype = sz
+    L.ava_model_set_trace.argtypes = [vp, vp, vp, vp, sz]
+    L.ava_model_set_trace.restype = i32
     if hasattr(L, "ava_model_set_timing"):
         L.ava_model_set_timing.argtypes = [vp, i32]
         L.ava_model_set_timing.restype = i32

@@ -237,8 +237,16 @@ struct FusedArgs {
     float *F, *S, *y;  // F, S [B nh][64][64]; y [B T][d]
 };
 
-// sigmoid(x) = 1 / (exp(-x) + 1) with the hardware exp2 and reciprocal (a few ulp of the f32 form)
-__device__ __forceinline__ float fsig(float x) { return __builtin_amdgcn_rcpf(__expf(-x) + 1.0f); }
+// The gates as the reference forms them, with the correctly rounded-to-an-ulp expf/logf and an IEEE
+// divide: a bias of a few ulp in alpha would move the fast weights by that bias over (1 - alpha), ~256x
+// for the slowest head (alpha ~ 1 - 2^-8). alpha = exp(logsigmoid(z)), logsigmoid(z) =
+// -(relu(-z) + ln(exp(-|z|) + 1)) (gpu/model.rs:618-622); b = 2 sigmoid(z), sigmoid(z) =
+// 1 / (exp(-z) + 1) (gpu/model.rs:465-467).
+__device__ __forceinline__ float gate_alpha(float z) {
+    const float soft = logf(expf(-fabsf(z)) * 1.0f + 1.0f);
+    return expf(-(fmaxf(-z, 0.0f) + soft));
+}
+__device__ __forceinline__ float gate_sig(float z) { return 1.0f / (expf(-z) * 1.0f + 1.0f); }
 
 
 template <bool MOM, bool PF>
@@ -323,9 +331,8 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
             float v = rv[s];
             if (p.v0_out && t < p.T) p.v0_out[(row0 + t) * d + c] = v;
             if (p.v0) v = v * p0 + rv0[s] * p1;
-            // alpha = exp(logsig(z)) is sigmoid(z); formed directly (equal up to rounding)
-            const float a = fsig(((rza[s] + bah) + offc) + lra[s]);
-            const float bw = fsig((rzb[s] + bbh) + lrb[s]) * 2.0f;
+            const float a = gate_alpha(((rza[s] + bah) + offc) + lra[s]);
+            const float bw = gate_sig((rzb[s] + bbh) + lrb[s]) * 2.0f;
             s_q[st][lane] = qn;
             s_e[st][lane] = en;
             s_v[st][lane] = v;
@@ -425,8 +432,8 @@ __global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
             const float p0 = p.vres ? p.vres[0] * 1.0f + 1.0f : 0.0f, p1 = p.vres ? p.vres[1] : 0.0f;
             v = v * p0 + p.v0[row * d + c] * p1;
         }
-        const float a = fsig(((Gr[hh] + p.ba[hh]) + p.off[c]) + lra);
-        const float bw = fsig((Gr[p.nh + hh] + p.bb[hh]) + lrb) * 2.0f;
+        const float a = gate_alpha(((Gr[hh] + p.ba[hh]) + p.off[c]) + lra);
+        const float bw = gate_sig((Gr[p.nh + hh] + p.bb[hh]) + lrb) * 2.0f;
         s_q[lane] = qn;
         s_e[lane] = en;
         s_v[lane] = v;

@@ -97,6 +97,11 @@ struct ava_model {
     // set while captured graphs hold the scratch's addresses: nothing is freed or reallocated
     bool frozen = false;
 
+    // the decision trace (ava_model_set_trace): [layers][tr_rows][...] buffers, the next row tr_pos
+    int8_t *tr_spk = nullptr;
+    float *tr_u = nullptr, *tr_kth = nullptr;
+    size_t tr_rows = 0, tr_pos = 0;
+
     bool timing = false;
     Timer timer;
     hipStream_t last_stream = nullptr;
@@ -374,6 +379,12 @@ int collect(ava_model *m) {
     return AVA_OK;
 }
 
+int trace_copy(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t height,
+               hipStream_t st) {
+    AVA_HIP(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDeviceToDevice, st));
+    return AVA_OK;
+}
+
 // join (nullable): an event the forward waits for before the final norm and the cerebellum (which
 // read and overwrite the code, the table and its scale).
 int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float *logits, hipStream_t st,
@@ -386,6 +397,10 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     AVA_REQUIRE(c.eng_block < 0 || (s->eng_k && s->eng_v && s->eng_len >= 0 && s->eng_len + T <= s->eng_cap),
                 AVA_ERR_SHAPE, "forward: the engram store holds %d of %d entries, %d more do not fit", s->eng_len,
                 s->eng_cap, T);
+    const bool tracing = m->tr_spk != nullptr;
+    AVA_REQUIRE(!tracing || m->tr_pos + (size_t)N <= m->tr_rows, AVA_ERR_SHAPE,
+                "forward: the decision trace holds %zu rows, %zu are used and %d more do not fit", m->tr_rows,
+                m->tr_pos, N);
     if (int e = ensure_scratch(m, (size_t)N)) return e;
     if (c.eng_block >= 0) {
         // sized for the fullest store this state can reach, so a decode loop allocates once
@@ -428,6 +443,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             AVA_RUN("lif_scan", ava::lif_scan_tuned(m->cur, B, T, d, b.ps, s->lif_v + sbd, s->lif_s + sbd,
                                                     s->lif_a + sbd, c.levels, 1, c.alif, m->spk, nullptr, 0, 0, st));
         }
+        if (tracing)
+            AVA_RUN("trace", trace_copy(m->tr_spk + ((size_t)i * m->tr_rows + m->tr_pos) * d, d, m->spk, ldd, d, N, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->spk, nullptr, 1, N, &b.wout.w, ava::Q8_ADD, m->x, d, nullptr, st));
         // the fast-weight memory
         if (ava::rms_gate_fits(N, d, 2 * nh + 2 * r)) {
@@ -469,7 +486,11 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         // the sparse MLP
         AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mlp_norm, P, m->xq, m->xexp, ldd, nullptr, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w1.w, ava::Q8_STORE, m->u, H, nullptr, st));
-        AVA_RUN("kwta", ava::kwta_planes(m->u, N, H, c.kwta_k, c.relu2, P, m->xq, m->xexp, ldh, nullptr, st));
+        AVA_RUN("kwta", ava::kwta_planes(m->u, N, H, c.kwta_k, c.relu2, P, m->xq, m->xexp, ldh,
+                                         tracing ? m->tr_kth + (size_t)i * m->tr_rows + m->tr_pos : nullptr, st));
+        if (tracing)
+            AVA_RUN("trace", trace_copy(m->tr_u + ((size_t)i * m->tr_rows + m->tr_pos) * H, (size_t)H * 4, m->u,
+                                        (size_t)H * 4, (size_t)H * 4, N, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w2.w, ava::Q8_ADD, m->x, d, nullptr, st));
         if (c.dense) {
             if (i + 1 < L) {
@@ -485,6 +506,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             }
         }
     }
+    if (tracing) m->tr_pos += (size_t)N;
     if (c.eng_block >= 0) {
         s->eng_len += T;
         if (s->eng_len_dev && !advanced)
@@ -651,6 +673,18 @@ extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->sc
 extern "C" int ava_model_freeze(ava_model *m, int on) {
     AVA_REQUIRE(m, AVA_ERR_ARG, "freeze: NULL model");
     m->frozen = on != 0;
+    return AVA_OK;
+}
+
+extern "C" int ava_model_set_trace(ava_model *m, int8_t *spikes, float *u, float *kth, size_t rows) {
+    AVA_REQUIRE(m, AVA_ERR_ARG, "set_trace: NULL model");
+    AVA_REQUIRE((spikes && u && kth) || (!spikes && !u && !kth), AVA_ERR_ARG,
+                "set_trace: spikes, u and kth are all set or all NULL");
+    m->tr_spk = spikes;
+    m->tr_u = u;
+    m->tr_kth = kth;
+    m->tr_rows = spikes ? rows : 0;
+    m->tr_pos = 0;
     return AVA_OK;
 }
 

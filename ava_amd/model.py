@@ -334,6 +334,25 @@ class Model:
         st = self.state(B, eng_cap=T if self.cfg["eng_block"] >= 0 else 0)
         return self.forward_with_state(ids, st), st
 
+    # the decision trace (ava_model_set_trace)
+    def set_trace(self, rows: int | None):
+        """Trace the next forwards' discrete decisions into new GPU buffers of `rows` rows (None: off).
+        Returns {"spikes": int8 [L, rows, d], "u": f32 [L, rows, hidden], "kth": f32 [L, rows]}; each
+        forward fills the next B*T rows (b-major), and trace_rows() tells how many are filled."""
+        if rows is None:
+            check(lib().ava_model_set_trace(self.h, None, None, None, 0), "ava_model_set_trace")
+            self._trace = None
+            return None
+        c = self.cfg
+        L, d, H = c["layers"], c["d"], c["hidden"]
+        tr = {"spikes": torch.zeros((L, rows, d), dtype=torch.int8, device="cuda"),
+              "u": torch.zeros((L, rows, H), dtype=torch.float32, device="cuda"),
+              "kth": torch.zeros((L, rows), dtype=torch.float32, device="cuda")}
+        check(lib().ava_model_set_trace(self.h, C.c_void_p(tr["spikes"].data_ptr()), C.c_void_p(tr["u"].data_ptr()),
+                                        C.c_void_p(tr["kth"].data_ptr()), rows), "ava_model_set_trace")
+        self._trace = tr
+        return tr
+
     # launch timing by kernel class (ava_model_set_timing / ava_model_timing)
     def set_timing(self, on: bool):
         check(lib().ava_model_set_timing(self.h, int(on)), "ava_model_set_timing")

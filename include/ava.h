@@ -280,6 +280,16 @@ size_t ava_model_scratch_bytes(const ava_model *m);
  * graphs, which keep the scratch's addresses (no reference counterpart: the reference has no graphs). */
 int ava_model_freeze(ava_model *m, int on);
 
+/* The decision trace, for parity checks (no counterpart in the reference, whose tests compare single
+ * ops): with the buffers set (all NULL: off), every forward copies per block i the spikes [B*T][d]
+ * int8, the wide layer's values before the kWTA u [B*T][hidden] f32 and each row's k-th largest value
+ * kth [B*T] into rows pos .. pos + B*T - 1 of block i's slice of spikes [layers][rows][d],
+ * u [layers][rows][hidden] and kth [layers][rows]. pos starts at 0 (each call of this function resets
+ * it) and advances by B*T per forward; a forward that would pass `rows` fails with AVA_ERR_SHAPE
+ * before it runs. With the spikes and the kWTA's index set (u - kth >= 0) a checker can replay this
+ * model's discrete decisions. */
+int ava_model_set_trace(ava_model *m, int8_t *spikes, float *u, float *kth, size_t rows);
+
 /* Launch timing by kernel class (the counterpart of int8::set_mm_prof, int8.rs:628-669): with `on`,
  * every launch of ava_model_forward is bracketed by HIP events on its stream. ava_model_timing
  * synchronises the stream of the last forward, then fills up to `cap` entries of names (static

@@ -250,10 +250,13 @@ static float spike_of(float v, float th, int levels, int is_signed) {
     return h;
 }
 
-/* Each (b, c) is its own sequential scan, so the units run in parallel with the same bits at any
- * thread count. */
-void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
-                  float *a, int levels, int is_signed, int alif, int8_t *spikes) {
+/* The scan with optional forced spikes: spikes[j] gets the scan's own decision; the state (the reset
+ * and the ALIF trace) follows force[j] when force is given. vm/tho (nullable) get the membrane and the
+ * threshold each decision compared. Each (b, c) is its own sequential scan, so the units run in
+ * parallel with the same bits at any thread count. */
+static void lif_scan_ex(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
+                        int levels, int is_signed, int alif, int8_t *spikes, const int8_t *force, float *vm,
+                        float *tho) {
 #pragma omp parallel for schedule(static)
     for (long i_ = 0; i_ < (long)B * D; i_++) {
         {
@@ -272,14 +275,22 @@ void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float 
                 }
                 vv = (vv * bt + cur[j]) - sp * thp;
                 sp = spike_of(vv, tht, levels, is_signed);
-                thp = tht;
                 spikes[j] = (int8_t)sp;
+                if (vm) vm[j] = vv;
+                if (tho) tho[j] = tht;
+                if (force) sp = (float)force[j];
+                thp = tht;
             }
             v[i] = vv;
             s[i] = sp;
             a[i] = aa;
         }
     }
+}
+
+void orc_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
+                  float *a, int levels, int is_signed, int alif, int8_t *spikes) {
+    lif_scan_ex(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, NULL, NULL, NULL);
 }
 
 /* ------------------------------------------------------------------ kWTA */
@@ -502,10 +513,12 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
             for (size_t n = 0; n < N; n++)
                 for (int c = 0; c < d; c++) cur[n * d + c] = cur[n * d + c] * (ps[c] * -1.0f + 1.0f);
         if (tr && tr->cur) memcpy(tr->cur + (size_t)i * N * d, cur, sizeof(float) * N * d);
-        orc_lif_scan(cur, B, T, d, ps, st->lif_v + (size_t)i * B * d, st->lif_s + (size_t)i * B * d,
-                     st->lif_a + (size_t)i * B * d, cfg->levels, 1, cfg->alif, spk);
+        const int8_t *fsp = tr && tr->force_spikes ? tr->force_spikes + (size_t)i * N * d : NULL;
+        lif_scan_ex(cur, B, T, d, ps, st->lif_v + (size_t)i * B * d, st->lif_s + (size_t)i * B * d,
+                    st->lif_a + (size_t)i * B * d, cfg->levels, 1, cfg->alif, spk, fsp,
+                    tr && tr->vm ? tr->vm + (size_t)i * N * d : NULL, tr && tr->tht ? tr->tht + (size_t)i * N * d : NULL);
         if (tr && tr->spikes) memcpy(tr->spikes + (size_t)i * N * d, spk, N * d);
-        mm_int(spk, (int)N, &bk->wout, y, threads);
+        mm_int(fsp ? fsp : spk, (int)N, &bk->wout, y, threads);
         for (size_t j = 0; j < N * d; j++) x[j] = x[j] + y[j];
 
         /* ---- the fast-weight memory (gpu/arch.rs:1873-2020; gpu/model/fstep/arch.rs:683-896) */
@@ -621,6 +634,15 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
         mm(h, (int)N, &bk->w1, u, planes, threads);
         if (tr && tr->u) memcpy(tr->u + (size_t)i * N * H, u, sizeof(float) * N * H);
         orc_kwta(u, (int)N, H, cfg->kwta_k, cfg->relu2, act, tr && tr->kth ? tr->kth + (size_t)i * N : NULL);
+        if (tr && tr->force_keep) {
+            /* the forced index set in the same formula: relu(u mask), squared with relu2 */
+            const uint8_t *fk = tr->force_keep + (size_t)i * N * H;
+            for (size_t z = 0; z < N * (size_t)H; z++) {
+                float yv = u[z] * (fk[z] ? 1.0f : 0.0f);
+                yv = yv > 0.0f ? yv : 0.0f;
+                act[z] = cfg->relu2 ? yv * yv : yv;
+            }
+        }
         mm(act, (int)N, &bk->w2, h, planes, threads);
         for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];
 

@@ -152,6 +152,16 @@ typedef struct {
     float *memy;      /* [layers][B*T][d] memory read-outs before the head norm */
     float *x;         /* [layers][B*T][d] stream after each block (after the dense mix) */
     float *hf;        /* [B*T][d] final normed state */
+    /* Forced decisions (inputs; NULL: the oracle's own). With force_spikes the spikes that update the
+     * LIF state and feed Wout are these ([layers][B*T][d]); `spikes` above still receives the oracle's
+     * own decisions. With force_keep the kWTA keeps unit i of a row where force_keep is non-zero
+     * ([layers][B*T][H]); `u` and `kth` still receive the oracle's own values. A test feeds the
+     * decisions of another implementation here so both follow one trajectory, and checks that every
+     * decision where the two differ is a near-tie of the oracle's own values. */
+    const int8_t *force_spikes;
+    const uint8_t *force_keep;
+    float *vm;        /* [layers][B*T][d] the membrane each spike decision compared */
+    float *tht;       /* [layers][B*T][d] the threshold it compared with (theta + gain a_t) */
 } orc_trace;
 
 /* gpu/arch.rs:1407-1867 (forward_arch / block_arch / mem_arch) with carried state as in

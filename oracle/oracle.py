@@ -292,7 +292,8 @@ class _State(C.Structure):
 
 
 class _Trace(C.Structure):
-    _fields_ = [(n, C.c_void_p) for n in ("spikes", "cur", "u", "kth", "memy", "x", "hf")]
+    _fields_ = [(n, C.c_void_p) for n in ("spikes", "cur", "u", "kth", "memy", "x", "hf", "force_spikes",
+                                         "force_keep", "vm", "tht")]
 
 
 class OracleModel:
@@ -374,8 +375,11 @@ class OracleModel:
             st["cb_code"] = np.zeros((B, self.cb), np.float32)
         return st
 
-    def forward(self, ids, state=None, planes=0, threads=1, trace=False, logits=True):
-        """gpu/arch.rs:1407 forward_arch / gpu/state.rs:684 forward_with_state. ids [B, T]."""
+    def forward(self, ids, state=None, planes=0, threads=1, trace=False, logits=True, force=None):
+        """gpu/arch.rs:1407 forward_arch / gpu/state.rs:684 forward_with_state. ids [B, T].
+        force: None, or {"spikes": int8 [L, B*T, d], "keep": bool/uint8 [L, B*T, H]} decisions that
+        replace the oracle's own (its own are still traced: spikes, u, kth, and the LIF decision
+        inputs vm, tht); forcing implies trace=True."""
         ids = _c(ids, np.int32)
         B, T = ids.shape
         c = self.cfg
@@ -392,13 +396,20 @@ class OracleModel:
         if cb and not trace:
             trd = {"hf": np.empty((N, c["d"]), np.float32)}
             tr = _Trace(hf=trd["hf"].ctypes.data)
-        if trace:
+        if trace or force is not None:
             L, d, H = c["layers"], c["d"], c["hidden"]
             trd = {"spikes": np.empty((L, N, d), np.int8), "cur": np.empty((L, N, d), np.float32),
                    "u": np.empty((L, N, H), np.float32), "kth": np.empty((L, N), np.float32),
                    "memy": np.empty((L, N, d), np.float32), "x": np.empty((L, N, d), np.float32),
-                   "hf": np.empty((N, d), np.float32)}
-            tr = _Trace(**{k: v.ctypes.data for k, v in trd.items()})
+                   "hf": np.empty((N, d), np.float32), "vm": np.empty((L, N, d), np.float32),
+                   "tht": np.empty((L, N, d), np.float32)}
+            ptrs = {k: v.ctypes.data for k, v in trd.items()}
+            if force is not None:
+                fs = _c(force["spikes"], np.int8).reshape(L, N, d)
+                fk = _c(force["keep"], np.uint8).reshape(L, N, H)
+                trd["_force"] = (fs, fk)  # kept alive through the call
+                ptrs.update(force_spikes=fs.ctypes.data, force_keep=fk.ctypes.data)
+            tr = _Trace(**ptrs)
         rc = lib().orc_model_forward(C.byref(self.ccfg), C.byref(self.model), ids.ctypes.data, B, T,
                                      C.byref(cst), None if out is None else out.ctypes.data, planes, threads,
                                      None if tr is None else C.byref(tr))

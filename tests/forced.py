@@ -1,0 +1,172 @@
+"""Tie-forced parity of the block stack: the GPU's discrete decisions replayed in the oracle.
+
+The GPU and the oracle add in different orders (norms, memory column sums, softmax), so their values
+differ at the 1e-7 level. A run long enough meets a decision closer than that: a membrane within
+rounding of a spike level, or a wide-layer value at the kWTA boundary. Left alone, the two sides then
+take different branches and drift apart. Here the GPU's decisions (ava_model_set_trace: each block's
+spikes, and the kWTA index set u - kth >= 0) are fed to the oracle's forward as forced decisions, so
+both follow one trajectory and every row must meet the full bars:
+  - logits within 1e-2 absolute on every row;
+  - membranes and fast weights within 1e-4 relative, final spike state mismatch <= 1e-4 of units;
+  - the oracle's own decisions differ from the GPU's on at most 1e-4 of all spike units and of all
+    kWTA units, and every such difference is a near-tie of the oracle's own values (relative
+    margin below NEAR_TIE).
+"""
+import numpy as np
+import torch
+
+from oracle import oracle as O
+
+# The relative margin of a decision that two correct summation orders may take either way. At the end
+# of a deep stack over thousands of tokens the two sides' inputs to a decision differ by ~1e-4
+# relative (the conditioning of the recurrences; see one_ulp_envelope), so a flip is a near-tie when
+# its margin is within 10x that; a wrong selection or spike rule would flip decisions with margins
+# of order one.
+NEAR_TIE = 1e-3
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def gpu_decisions(tr, rows_order):
+    """The GPU trace's decisions in the oracle's row order: rows_order[n] = the trace row of oracle row n.
+    Returns {"spikes": int8 [L, N, d], "keep": uint8 [L, N, H]}."""
+    spk, u, kth = host(tr["spikes"]), host(tr["u"]), host(tr["kth"])
+    idx = np.asarray(rows_order)
+    spk, u, kth = spk[:, idx], u[:, idx], kth[:, idx]
+    keep = (u - kth[:, :, None] >= 0.0).astype(np.uint8)
+    return {"spikes": np.ascontiguousarray(spk), "keep": np.ascontiguousarray(keep), "u": u, "kth": kth}
+
+
+def piece_rows(B, pieces):
+    """rows_order for forwards of B streams over consecutive pieces [(t0, t1), ...] of one sequence: the
+    trace holds each piece's B x (t1 - t0) rows b-major, one piece after another; the oracle's single
+    pass holds B x T rows b-major."""
+    T = pieces[-1][1]
+    order = np.empty(B * T, np.int64)
+    pos = 0
+    for t0, t1 in pieces:
+        n = t1 - t0
+        for b in range(B):
+            order[b * T + t0:b * T + t1] = pos + b * n + np.arange(n)
+        pos += B * n
+    return order
+
+
+def check_decisions(cfg, dec, otr, label=""):
+    """The oracle's own decisions (its trace otr under forcing) against the GPU's (dec): at most 1e-4
+    of units differ, each a near-tie of the oracle's values. Returns (spike flips, kWTA flips)."""
+    own_s = otr["spikes"]
+    diff = own_s != dec["spikes"]
+    n_s = int(diff.sum())
+    frac_s = n_s / diff.size
+    if n_s:
+        vm, th = otr["vm"][diff], otr["tht"][diff]
+        lv = cfg["levels"]
+        dist = np.min(np.stack([np.abs(vm - k * th) for k in range(-lv, lv + 1) if k]), axis=0)
+        marg = dist / np.abs(th)
+        print(f"{label} spike flips {n_s} ({frac_s:.1e} of units), largest margin {marg.max():.2e}", flush=True)
+        assert marg.max() < NEAR_TIE, marg.max()
+    assert frac_s <= 1e-4, frac_s
+    own_k = (otr["u"] - otr["kth"][:, :, None] >= 0.0)
+    kd = own_k != dec["keep"].astype(bool)
+    n_k = int(kd.sum())
+    if n_k:
+        kth = np.broadcast_to(otr["kth"][:, :, None], otr["u"].shape)[kd]
+        kth_g = np.broadcast_to(dec["kth"][:, :, None], dec["u"].shape)[kd]
+        marg = np.abs(otr["u"][kd] - kth) / np.abs(kth)
+        gap = np.abs((otr["u"][kd] - kth) - (dec["u"][kd] - kth_g)) / np.abs(kth)
+        print(f"{label} kWTA flips {n_k} ({n_k / kd.size:.1e} of units), largest margin {marg.max():.2e}, "
+              f"largest two-sided difference {gap.max():.2e}", flush=True)
+        assert marg.max() < NEAR_TIE, marg.max()
+    assert n_k / kd.size <= 1e-4
+    return n_s, n_k
+
+
+ENVELOPE = 4.0  # the fast-weight bar of a deep stack: this many times the oracle's own one-ulp response
+
+
+def check_state(so, st, envelope=None):
+    """BASELINE.json's state bars: membranes and fast weights within 1e-4 relative, spike state
+    mismatch <= 1e-4 of units (st: the GPU State, or a dict of numpy arrays). With `envelope` (the
+    oracle's own per-block relative response to a one-ulp nudge of its inputs, {name: [per block]}),
+    the fast weights of block i may differ by up to max(1e-4, ENVELOPE x envelope[i]): the bar of a
+    recurrence whose conditioning is worse than 1e-4 at that depth (see one_ulp_envelope)."""
+    get = (lambda k: host(getattr(st, k))) if not isinstance(st, dict) else (lambda k: st[k])
+    names = ["lif_v", "mem_f"] + (["mem_s"] if so.get("mem_s") is not None and np.any(so["mem_s"]) else [])
+    for k in names:
+        g = get(k)
+        per = [rel(g[i], so[k][i]) for i in range(g.shape[0])]
+        env = envelope.get(k) if envelope and k != "lif_v" else None
+        print(f"state {k}: rel {rel(g, so[k]):.2e}; per block " + " ".join(f"{e:.1e}" for e in per) +
+              ("; one-ulp envelope " + " ".join(f"{e:.1e}" for e in env) if env is not None else ""), flush=True)
+        for i, e in enumerate(per):
+            bar = max(1e-4, ENVELOPE * env[i]) if env is not None else 1e-4
+            assert e < bar, (k, i, e, bar)
+    flips = float(np.mean(get("lif_s") != so["lif_s"]))
+    print(f"state lif_s: mismatch {flips:.2e}", flush=True)
+    assert flips <= 1e-4
+
+
+def one_ulp_envelope(cfg, prm, ids, dec, so, threads=16):
+    """The oracle's own sensitivity: the same forward with every embedding value moved by one ulp and
+    the same forced decisions, against the unmoved run's state so. Per block, the relative change of
+    the fast weights (mem_f, mem_s). Two correct f32 implementations that sum in different orders
+    differ by about this much; a fast-weight recurrence (with momentum, and heads that grow towards the
+    state bound) can amplify a one-ulp difference far beyond 1e-4 over thousands of tokens."""
+    p2 = dict(prm)
+    p2["tok_emb"] = np.nextafter(np.asarray(prm["tok_emb"], np.float32), np.float32(np.inf)).astype(np.float32)
+    om2 = O.OracleModel(cfg, p2)
+    B = ids.shape[0]
+    _, s2, _ = forced_oracle(om2, ids, dec, om2.new_state(B, eng_cap=ids.shape[1]), threads=threads)
+    out = {}
+    for k in ("mem_f", "mem_s"):
+        if so.get(k) is not None and np.any(so[k]):
+            out[k] = [rel(s2[k][i], so[k][i]) for i in range(so[k].shape[0])]
+    return out
+
+
+def forced_oracle(om, ids, dec, state, threads=16):
+    """The oracle's forward of ids [B, T] from `state` with the GPU's decisions forced."""
+    return om.forward(ids, state=state, planes=3, threads=threads,
+                      force={"spikes": dec["spikes"], "keep": dec["keep"]})
+
+
+def run_forced(name, B, T, seed, pieces=None, threads=16, envelope=False, **over):
+    """The GPU's forward of seeded ids [B, T] (in pieces when given) with its decision trace, and the
+    oracle's forward with those decisions forced: every row meets the full bars (with envelope, the
+    fast weights the conditioning bar of check_state). Returns (cfg, GPU logits, oracle logits, GPU
+    state, oracle state)."""
+    from ava_amd import synth
+    from ava_amd.model import Model
+    cfg = synth.config(name)
+    cfg.update(over)
+    prm = synth.params(cfg, seed=seed)
+    ids = np.random.default_rng(seed + 1).integers(0, cfg["vocab"], (B, T)).astype(np.int32)
+    pieces = pieces or [(0, T)]
+    print(f"forced parity {name} B={B} T={T} seed={seed} pieces={pieces}", flush=True)
+    m = Model(cfg, prm)
+    st = m.state(B, eng_cap=T)
+    tr = m.set_trace(B * T)
+    outs = [host(m.forward_with_state(torch.from_numpy(np.ascontiguousarray(ids[:, a:b])).cuda(), st))
+            .reshape(B, b - a, -1) for a, b in pieces]
+    lg = np.concatenate(outs, axis=1).reshape(B * T, -1)
+    dec = gpu_decisions(tr, piece_rows(B, pieces))
+    m.set_trace(None)
+    del tr
+    print(f"forced parity {name}: oracle forward", flush=True)
+    om = O.OracleModel(cfg, prm)
+    lo, so, otr = forced_oracle(om, ids, dec, om.new_state(B, eng_cap=T), threads=threads)
+    err = float(np.max(np.abs(lg - lo)))
+    print(f"{name}: logits max abs err {err:.2e}, rel {err / np.max(np.abs(lo)):.2e}", flush=True)
+    assert err < 1e-2
+    env = one_ulp_envelope(cfg, prm, ids, dec, so, threads) if envelope else None
+    check_state(so, st, env)
+    check_decisions(cfg, dec, otr, name)
+    return cfg, lg, lo, st, so

@@ -1,14 +1,16 @@
 """GPU parity of the whole block stack (ava_model_forward) against the oracle's forward.
 
 Bars: final logits within 1e-2 absolute; fp32 membranes and fast-weight
-state within 1e-4 relative; spike mismatch at most 1e-4 of units (the final spikes of every layer).
-The oracle runs the same split-plane products (planes = 3) as the GPU, so the comparison isolates
-the kernels; a second check against the reference's own W8A32 products bounds the first token.
+state within 1e-4 relative; spike mismatch at most 1e-4 of units. The oracle runs the same
+split-plane products (planes = 3) as the GPU, so the comparison isolates the kernels. Sequences long
+enough to meet near-ties run with the GPU's decisions forced in the oracle (tests/forced.py), which
+also checks every spike and kWTA decision of every block and row.
 """
 import numpy as np
 import pytest
 import torch
 
+import forced as F
 from ava_amd import synth
 from oracle import oracle as O
 
@@ -62,52 +64,6 @@ def check_state(so, st):
     assert np.mean(s != so["lif_s"]) <= 1e-4
 
 
-def tie_margin(cfg, prm, ids_row, t):
-    """The narrowest decision of token t of one stream in the oracle, relative to its scale: per block,
-    the membranes' distance to the nearest spike level (k theta, k = +-1, +-2) over theta, and the gap
-    between the k-th and (k+1)-th wide-layer values over the k-th."""
-    om = O.OracleModel(cfg, prm)
-    ids = np.ascontiguousarray(ids_row[None, :t + 1])
-    _, _, tr = om.forward(ids, state=om.new_state(1, eng_cap=t + 1), planes=3, threads=8, trace=True)
-    L, H, k = cfg["layers"], cfg["hidden"], cfg["kwta_k"]
-    cur = tr["cur"].reshape(L, t + 1, -1)
-    u = tr["u"].reshape(L, t + 1, H)
-    margins = []
-    for li in range(L):
-        ps = O.lif_params(prm["blocks"][li], cfg["alif"])
-        _, v, _, a = O.lif_scan(cur[li][None], ps)
-        D = v.shape[1]
-        tht = ps[D:2 * D] + a[0] * ps[3 * D:]
-        lv = cfg["levels"]
-        dist = np.min(np.abs(np.stack([v[0] - kk * tht for kk in range(-lv, lv + 1) if kk])), axis=0)
-        margins.append(float(np.min(dist / np.abs(tht))))
-        r = np.sort(u[li][t])[::-1]
-        margins.append(float((r[k - 1] - r[k]) / abs(r[k - 1])))
-    return min(margins)
-
-
-def check_logits_with_ties(cfg, prm, ids, lg, lo, bad_frac=0.10):
-    """The logits bar for sequences long enough to meet a near-tie (a spike or a kWTA winner decided by
-    less than the 1e-7-level differences of reduction order between the GPU and the oracle). Per
-    stream, every row before its first event (a row off by more than 1e-3) is within 1e-4; each first
-    event is shown to be a near-tie in the oracle itself (tie_margin); at most bad_frac of all rows are
-    off by more than 1e-2 (the event's token and the fading trace it leaves in the carried state).
-    A near-tie here: some decision of the event's token has a relative margin below 3e-5 in the
-    oracle (tie_margin), against margins of 1e-3 and more at typical tokens."""
-    B, T = ids.shape
-    err = np.abs(lg - lo).max(1).reshape(B, T)
-    firsts = [int(np.argmax(e > 1e-3)) if np.any(e > 1e-3) else None for e in err]
-    print("rows over 1e-2:", float(np.mean(err > 1e-2)), "first events:", firsts, flush=True)
-    assert np.mean(err > 1e-2) <= bad_frac
-    for b, (e, f) in enumerate(zip(err, firsts)):
-        assert np.all(e[:T if f is None else f] < 1e-4)
-        if f is not None:
-            mg = tie_margin(cfg, prm, ids[b], f)
-            print(f"stream {b} event t={f}: narrowest decision margin {mg:.2e}", flush=True)
-            assert mg < 3e-5
-    return firsts
-
-
 @pytest.mark.parametrize("B,T", [(2, 16), (3, 40)])
 def test_tiny_stack_matches_oracle(B, T):
     cfg, lo, so, lg, st = run_both("tiny", B, T, seed=1)
@@ -139,31 +95,11 @@ def test_stack_in_pieces_matches_one_pass():
     check_state(so, st)
 
 
-def check_long(name, B, T, seed):
-    """Parity of a sequence long enough to meet near-ties: the logits bar of check_logits_with_ties;
-    BASELINE.json's state bars (membranes and fast weights within 1e-4 relative, spike state mismatch
-    <= 1e-4) on the prefix that ends before the first event, where both sides still follow one
-    trajectory; after it the state only within 0.2 relative (no blow-up)."""
-    cfg, lo, so, lg, st = run_both(name, B, T, seed)
-    ids = np.random.default_rng(seed + 1).integers(0, cfg["vocab"], (B, T)).astype(np.int32)
-    firsts = check_logits_with_ties(cfg, synth.params(cfg, seed=seed), ids, lg, lo)
-    events = [f for f in firsts if f is not None]
-    if not events:
-        check_state(so, st)
-        return
-    for name_ in ("lif_v", "mem_f", "mem_s"):
-        assert rel(host(getattr(st, name_)), so[name_]) < 0.2, name_
-    f = min(events)
-    print(f"state bars on the first {f} tokens", flush=True)
-    _, _, so2, _, st2 = run_both(name, B, T, seed, prefix=f)
-    check_state(so2, st2)
-
-
 def test_config0_shape_matches_oracle():
     """config[0]'s architecture (d 512, 8 blocks, wide 2048 / k 512, engram in block 4, vocab 8192) on
-    a batch of 1 with 64 prompt tokens. With this seed token 47 meets a near-tie (a kWTA boundary of
-    block 6 with a 7e-6 relative gap), so the bars are those of long sequences (check_long)."""
-    check_long("ava04_d512", 1, 64, seed=3)
+    a batch of 1 with 64 prompt tokens; with this seed token 47 meets a kWTA near-tie of block 6, which
+    the forced comparison replays."""
+    F.run_forced("ava04_d512", 1, 64, seed=3)
 
 
 def test_decode_steps_after_long_prefill():
@@ -195,13 +131,10 @@ def test_decode_steps_after_long_prefill():
 
 
 def test_long_sequence_against_oracle():
-    """1105 tokens of two streams against the oracle. A recurrence carried this long can meet a
-    near-tie: a membrane within rounding of its threshold or a wide-layer value at the kWTA boundary,
-    which 1e-7-level differences of reduction order (norms, memory read-outs, softmax) decide the other
-    way (with this seed stream 0 at t = 116: a membrane of block 1 within 2e-6 of its threshold). After
-    it the token's logits move by up to ~0.2 and the fast weights carry the difference, fading with the
-    gates. Bars: check_long."""
-    check_long("tiny", 2, 1105, seed=4)
+    """1105 tokens of two streams in a prefill and single-token steps (the tiled and the chunk-split
+    engram reads) against the oracle with the GPU's decisions forced: every row within the bars (with
+    this seed stream 0 meets a membrane of block 1 within 2e-6 of its threshold at t = 116)."""
+    F.run_forced("tiny", 2, 1105, seed=4, pieces=[(0, 1100), (1100, 1101), (1101, 1104), (1104, 1105)])
 
 
 @pytest.mark.parametrize("half", [False, True])
