@@ -40,6 +40,10 @@ namespace ava {
 void set_error(const char *fmt, ...);
 int fail(int code, const char *fmt, ...);
 
+// Kernels above 64 KiB of dynamic LDS opt in with a function attribute: set once per (device, kernel),
+// under a lock (launches may come from several host threads).
+int lds_opt_in(const void *fn, size_t bytes);
+
 }  // namespace ava
 
 #define AVA_REQUIRE(cond, code, ...)                     \

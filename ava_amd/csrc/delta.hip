@@ -377,14 +377,8 @@ extern "C" int ava_delta_chunk(const float *q, const float *k, const float *v, c
     AVA_REQUIRE(BH >= 0 && T >= 0 && T % C == 0, AVA_ERR_SHAPE, "delta_chunk: BH=%d T=%d (T a multiple of 64)", BH, T);
     if (BH == 0 || T == 0) return AVA_OK;
     const size_t lds = sizeof(float) * (9 * C * LD + 2 * C);
-    static bool attr = false;
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)delta_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds));
-        AVA_HIP(hipFuncSetAttribute((const void *)delta_plain_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds));
-        attr = true;
-    }
+    if (int r = ava::lds_opt_in((const void *)delta_chunk_kernel, lds)) return r;
+    if (int r = ava::lds_opt_in((const void *)delta_plain_kernel, lds)) return r;
     DeltaArgs a{q, k, v, la, beta, T, F, y};
     if (la) delta_chunk_kernel<<<BH, 256, lds, (hipStream_t)stream>>>(a);
     else delta_plain_kernel<<<BH, 256, lds, (hipStream_t)stream>>>(a);

@@ -320,96 +320,14 @@ struct KvLane<__half> {
     }
 };
 
-// Causal single-head attention of one stream's T queries against its store: query t (store
-// position n0 + t) reads entries 0..n0 + t with softmax(q.k / sqrt(de)) (gpu/model.rs:543-562,
-// gpu/model/fstep.rs:303-329). de == 64. Block = 64 queries x 256 threads; keys and values in
-// tiles of 64 through LDS; the softmax is the online (running max) form, equal to the reference's
-// two-pass form up to rounding. out [B*T][64].
-template <typename KV>
-__global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q, int ldq, const KV *__restrict__ ks,
-                                                     const KV *__restrict__ vs, int cap, int n0, const int *n0p,
-                                                     int T, float scale, float *__restrict__ out) {
-    if (n0p) n0 = min(*n0p, cap - T);  // the store length on the device (a replayed graph)
-    __shared__ float sk[64][65];
-    __shared__ float sv[64][64];
-    __shared__ float sp[64][65];
-    const int bi = blockIdx.y, qb = blockIdx.x * 64;
-    const int tid = threadIdx.x;
-    const int r = tid >> 2, sub = tid & 3;  // query row, quarter (16 keys / 16 output dims)
-    const KV *kb = ks + (size_t)bi * cap * 64, *vb = vs + (size_t)bi * cap * 64;
-    float qr[64];
-    {
-        const bool ok = qb + r < T;
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(q + ((size_t)bi * T + qb + r) * ldq);
-#pragma unroll
-        for (int c = 0; c < 16; c++) {
-            const f32x4 v = ok ? src[c] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int z = 0; z < 4; z++) qr[4 * c + z] = v[z];
-        }
-    }
-    float mx = -INFINITY, den = 0.0f, o[16];
-#pragma unroll
-    for (int z = 0; z < 16; z++) o[z] = 0.0f;
-    const int qpos = n0 + qb + r;                  // this row's store position
-    const int kend = min(n0 + qb + 64, n0 + T);    // keys the block's last row reads
-    for (int k0 = 0; k0 < kend; k0 += 64) {
-        __syncthreads();
-        for (int i = tid; i < 64 * 64; i += 256) {
-            const int rr = i >> 6, cc = i & 63;
-            const bool ok = k0 + rr < kend;
-            sk[rr][cc] = ok ? kv_get(kb, (size_t)(k0 + rr) * 64 + cc) : 0.0f;
-            sv[rr][cc] = ok ? kv_get(vb, (size_t)(k0 + rr) * 64 + cc) : 0.0f;
-        }
-        __syncthreads();
-        float s[16], tmax = -INFINITY;
-#pragma unroll
-        for (int z = 0; z < 16; z++) {
-            const int kk = sub * 16 + z;
-            float a = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 64; c++) a = fmaf(sk[kk][c], qr[c], a);
-            a = a * scale + 0.0f;
-            s[z] = (k0 + kk <= qpos) ? a : -INFINITY;
-            tmax = fmaxf(tmax, s[z]);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
-        const float nmx = fmaxf(mx, tmax);
-        const float corr = (mx == -INFINITY) ? 0.0f : expf(mx - nmx);
-        float psum = 0.0f;
-#pragma unroll
-        for (int z = 0; z < 16; z++) {
-            const float e = (s[z] == -INFINITY) ? 0.0f : expf(s[z] - nmx);
-            sp[r][sub * 16 + z] = e;
-            psum += e;
-        }
-        psum += __shfl_xor(psum, 1, 64);
-        psum += __shfl_xor(psum, 2, 64);
-        den = den * corr + psum;
-        mx = nmx;
-        __syncthreads();
-#pragma unroll
-        for (int z = 0; z < 16; z++) o[z] *= corr;
-        for (int kk = 0; kk < 64; kk++) {
-            const float pk = sp[r][kk];
-#pragma unroll
-            for (int z = 0; z < 16; z++) o[z] = fmaf(pk, sv[kk][sub * 16 + z], o[z]);
-        }
-    }
-    if (qb + r < T) {
-        float *orow = out + ((size_t)bi * T + qb + r) * 64 + sub * 16;
-#pragma unroll
-        for (int z = 0; z < 16; z++) orow[z] = o[z] / den;
-    }
-}
-
-// The same read on the fp32 MFMA (v_mfma_f32_32x32x2_f32), for query blocks of 64: per 64-key tile,
-// S = Q K^T (wave w: a 32 x 32 quadrant), scaled and masked into LDS; the online softmax by row as
-// attend_kernel (4 threads per row, 16 scores each: the running max, the rescale factor of the
-// previous tiles, exp); then O = O corr + P V (wave w: its quadrant of the 64 x 64 output, kept in
-// the MFMA accumulator across tiles); O / den at the end. Equal to attend_kernel up to the products'
-// summation order.
+// Causal attention of one stream's T queries against its store (gpu/model.rs:543-562,
+// gpu/model/fstep.rs:303-329): query t (store position n0 + t) reads entries 0..n0 + t with
+// softmax(q.k / sqrt(head size)). On the fp32 MFMA (v_mfma_f32_32x32x2_f32), for query blocks of 64:
+// per 64-key tile, S = Q K^T (wave w: a 32 x 32 quadrant), scaled and masked into LDS; the online
+// (running max) softmax by row, 4 threads per row with 16 scores each (the running max, the rescale
+// factor of the previous tiles, exp); then O = O corr + P V (wave w: its quadrant of the 64 x 64
+// output, kept in the MFMA accumulator across tiles); O / den at the end. Equal to the reference's
+// two-pass softmax up to rounding.
 // Heads: the store's rows hold nh heads of HD dims (de = nh HD, the reference's heads of 32,
 // gpu/memory.rs:610-700); workgroup (query block, b nh + h) reads head h: its query, key and value
 // dims h HD .. h HD + HD - 1. The Q, K and V tiles are HD wide; for HD = 32, P V has one 32-column
@@ -1166,16 +1084,6 @@ size_t engram_split_floats(int B, int T, int n0, int de, int nh) {
     return T <= ENGRAM_SPLIT_T ? (size_t)B * T * nh * ceil_div(n0 + T, ACH) * (hd + 2) : 0;
 }
 
-// The query-block read on the fp32 MFMA (AVA_ATTEND_MFMA=0: the VALU form; tuning).
-bool attend_mfma() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_ATTEND_MFMA");
-        v = e ? (atoi(e) != 0) : 1;
-    }
-    return v != 0;
-}
-
 // With n0p (the store length on the device) the chunk grid covers the whole store, so a captured
 // launch serves every length; chunks past the length are empty and merge as nothing.
 template <typename KV, int HD>
@@ -1208,9 +1116,7 @@ int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n
         return AVA_OK;
     }
     dim3 grid(ceil_div(T, 64), B * nh);
-    if (attend_mfma() || HD != 64 || nh != 1)
-        attend_mfma_kernel<KV, HD><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, de, nh, out);
-    else attend_kernel<KV><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, out);
+    attend_mfma_kernel<KV, HD><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, de, nh, out);
     AVA_LAUNCHED("attend");
     return AVA_OK;
 }

@@ -318,22 +318,14 @@ __global__ __launch_bounds__(RW > 4 ? 64 * RW : 256) void kwta_kernel(const floa
     }
 }
 
-// Rows at most this many take a workgroup each (AVA_KWTA_WG_ROWS overrides it; tuning): with few rows
-// a wave per row leaves most of the chip idle and each row's search is a chain of counts.
-int wg_rows() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_KWTA_WG_ROWS");
-        v = e ? atoi(e) : 2048;
-        if (v < 0) v = 0;
-    }
-    return v;
-}
+// Rows at most this many take a workgroup each: with few rows a wave per row leaves most of the chip
+// idle and each row's search is a chain of counts.
+constexpr int WG_ROWS = 2048;
 
 template <int P>
 int launch(const float *u, int n, int h, int k, int relu2, float *a, float *kth, int8_t *xq, int32_t *xexp,
            int ldq, hipStream_t st) {
-    if (n <= wg_rows() && h <= 4096) {
+    if (n <= WG_ROWS && h <= 4096) {
         const int nv4 = (h + 1023) / 1024;
 #define AVA_KWG(NV_)                                                                                           \
     if (nv4 <= NV_) {                                                                                          \

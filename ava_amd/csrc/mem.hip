@@ -511,24 +511,15 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
     AVA_REQUIRE(B > 0 && T > 0 && nh > 0 && r > 0 && r <= 32, AVA_ERR_SHAPE, "mem_block: B=%d T=%d nh=%d r=%d", B, T,
                 nh, r);
     FusedArgs a{P, G, ba, bb, off, wa2, wb2, vres, v0, v0_out, T, nh, r, m, cap, F, S, y};
-    static int pf = -1;  // AVA_MEM_PF=0/1 overrides the prefetch choice (tuning)
-    if (pf < 0) {
-        const char *e = getenv("AVA_MEM_PF");
-        pf = e ? atoi(e) != 0 : 0;
-    }
     if (T == 1) {
         if (m != 0.0f) mem_step_kernel<true><<<B * nh, 256, 0, st>>>(a);
         else mem_step_kernel<false><<<B * nh, 256, 0, st>>>(a);
         AVA_LAUNCHED("mem_step");
         return AVA_OK;
     }
-    if (m != 0.0f) {
-        if (pf) mem_fused_kernel<true, true><<<B * nh, 256, 0, st>>>(a);
-        else mem_fused_kernel<true, false><<<B * nh, 256, 0, st>>>(a);
-    } else {
-        if (pf) mem_fused_kernel<false, true><<<B * nh, 256, 0, st>>>(a);
-        else mem_fused_kernel<false, false><<<B * nh, 256, 0, st>>>(a);
-    }
+    // the chunk's inputs are staged by the scan's own waves (loading them a chunk ahead measured no faster)
+    if (m != 0.0f) mem_fused_kernel<true, false><<<B * nh, 256, 0, st>>>(a);
+    else mem_fused_kernel<false, false><<<B * nh, 256, 0, st>>>(a);
     AVA_LAUNCHED("mem_block");
     return AVA_OK;
 }

@@ -22,6 +22,8 @@
 
 #include <algorithm>
 #include <mutex>
+#include <set>
+#include <utility>
 
 #include "common.h"
 
@@ -254,134 +256,6 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
     }
 }
 
-// The product over one BM x BN output tile: 256 threads = 4 waves in WM x (4 / WM); wave tile
-// MW x NW = (BM / WM) x (BN * WM / 4), FM x FN blocks of 32 x 32 per plane.
-template <int P, int EPI, int BM, int BN, int WM, int BK>
-__global__ __launch_bounds__(256, 2) void q8_gemm_kernel(const int8_t *__restrict__ xq, const int32_t *__restrict__ xexp,
-                                                      int m, int n, int ldk, const int8_t *__restrict__ qt,
-                                                      const float *__restrict__ scale, EpiArgs ep) {
-    constexpr int WN = 4 / WM, MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
-    constexpr int LDS_ROW = BK;  // unpadded rows; the 16-byte chunks are XOR-swizzled per row (swz)
-    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    int8_t *lds_a = smem;                              // [2][P][BM][LDS_ROW]
-    int8_t *lds_b = smem + 2 * P * BM * LDS_ROW;       // [2][BN][LDS_ROW]
-
-    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    int mt, nt;
-    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-
-    // global -> register staging: A: P*BM rows x BK/16 chunks of 16 B; B: BN rows x BK/16 chunks.
-    // Rows past m and columns past n load the last valid row / column instead (their outputs are
-    // never stored), so every load is unconditional and the compiler can keep two K steps in flight.
-    constexpr int CPR = BK / 16;  // 16-byte chunks per row
-    constexpr int A_CH = P * BM * CPR, B_CH = BN * CPR;
-    static_assert(A_CH % 256 == 0 && B_CH % 256 == 0, "staging");
-    constexpr int A_CHUNKS = A_CH / 256, B_CHUNKS = B_CH / 256;  // per thread
-    i32x4 ra[2][A_CHUNKS], rb[2][B_CHUNKS];
-    const int8_t *a_src[A_CHUNKS];
-    const int8_t *b_src[B_CHUNKS];
-    int a_dst[A_CHUNKS], b_dst[B_CHUNKS];
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; i++) {
-        const int c = i * 256 + tid;
-        const int p = c / (BM * CPR), rr = (c / CPR) % BM, kc = c % CPR;
-        const int row = min(m0 + rr, m - 1);
-        a_src[i] = xq + ((size_t)p * m + row) * ldk + kc * 16;
-        a_dst[i] = (p * BM + rr) * LDS_ROW + swz<CPR>(rr, kc) * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; i++) {
-        const int c = i * 256 + tid;
-        const int rr = c / CPR, kc = c % CPR;
-        const int col = min(n0 + rr, n - 1);
-        b_src[i] = qt + (size_t)col * ldk + kc * 16;
-        b_dst[i] = rr * LDS_ROW + swz<CPR>(rr, kc) * 16;
-    }
-    auto load_tile = [&](int kt, int set) {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; i++) ra[set][i] = *reinterpret_cast<const i32x4 *>(a_src[i] + k0);
-#pragma unroll
-        for (int i = 0; i < B_CHUNKS; i++) rb[set][i] = *reinterpret_cast<const i32x4 *>(b_src[i] + k0);
-    };
-    auto store_tile = [&](int buf, int set) {
-        int8_t *la = lds_a + buf * P * BM * LDS_ROW;
-        int8_t *lb = lds_b + buf * BN * LDS_ROW;
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; i++) *reinterpret_cast<i32x4 *>(la + a_dst[i]) = ra[set][i];
-#pragma unroll
-        for (int i = 0; i < B_CHUNKS; i++) *reinterpret_cast<i32x4 *>(lb + b_dst[i]) = rb[set][i];
-    };
-
-    i32x16 acc[P][FM][FN];
-#pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
-
-    const int KT = ldk / BK;  // even: ldk is a multiple of 128, and BK is 64 or a multiple of ldk's factor
-    load_tile(0, 0);
-    load_tile(min(1, KT - 1), 1);
-    store_tile(0, 0);
-    __syncthreads();
-
-    const int frow = lane & 31, fc = lane >> 5;  // fragment row, 16-byte chunk within the 32-byte K substep
-    // One K step on LDS buffer / register set SET (= kt & 1, a constant so the staging registers are
-    // addressed statically): refill set SET with step kt+2, multiply step kt, store step kt+1. KT is
-    // even (K is padded to 128) and the loads past the end re-read the last step, so nothing here is
-    // conditional and the compiler waits only for the older register set.
-    auto step = [&](int kt, auto set_c) {
-        constexpr int SET = decltype(set_c)::value;
-        load_tile(min(kt + 2, KT - 1), SET);
-        const int8_t *la = lds_a + SET * P * BM * LDS_ROW;
-        const int8_t *lb = lds_b + SET * BN * LDS_ROW;
-#pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
-            i32x4 bf[FN];
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int r = wn * NW + j * 32 + frow;
-                bf[j] = *reinterpret_cast<const i32x4 *>(lb + r * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
-            }
-#pragma unroll
-            for (int p = 0; p < P; p++) {
-                i32x4 af[FM];
-#pragma unroll
-                for (int i = 0; i < FM; i++) {
-                    const int r = wm * MW + i * 32 + frow;  // swizzle by the row within the plane (BM % 16 == 0)
-                    af[i] = *reinterpret_cast<const i32x4 *>(la + (p * BM + r) * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
-                }
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[p][i][j], 0, 0, 0);
-            }
-        }
-        store_tile(SET ^ 1, SET ^ 1);
-        __syncthreads();
-    };
-    for (int kt = 0; kt < KT; kt += 2) {
-        step(kt, std::integral_constant<int, 0>{});
-        step(kt + 1, std::integral_constant<int, 1>{});
-    }
-
-    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
-    int *s_exp = reinterpret_cast<int *>(smem);
-    if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += 256) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
-        __syncthreads();
-    }
-    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
-}
-
 // ------------------------------------------------------------------ the product, direct-to-LDS form
 //
 // The same product with the operands brought into LDS by global_load_lds_dwordx4 (gfx950): each
@@ -542,27 +416,10 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void q8_gemm_dma_kernel(const i
     epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
 }
 
-// Products of at most this many rows take the few-rows kernel; AVA_Q8_SMALL_ROWS overrides it (tuning).
-int small_rows() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_Q8_SMALL_ROWS");
-        v = e ? atoi(e) : 512;
-        if (v < 0) v = 0;
-    }
-    return v;
-}
-
-// Few-rows products of at least this many columns take 64-column blocks; AVA_Q8_WIDE_COLS overrides it.
-int small_wide_cols() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_Q8_WIDE_COLS");
-        v = e ? atoi(e) : 4096;
-        if (v < 0) v = 0;
-    }
-    return v;
-}
+// Products of at most this many rows take the few-rows kernel.
+constexpr int SMALL_ROWS = 512;
+// Few-rows products of at least this many columns take 64-column blocks.
+constexpr int SMALL_WIDE_COLS = 4096;
 
 // ------------------------------------------------------------------ the product for few rows
 //
@@ -808,26 +665,10 @@ int launch_small_fn(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk
     using C = SmallCfg<P, FN, D, NW>;
     const int total = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
     const size_t lds = std::max(C::OPS, EPI == EPI_ACC ? C::ACC : C::DBL);
-    static bool attr = false;
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_small_kernel<P, EPI, FN, D, NW>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
+    if (int r = ava::lds_opt_in((const void *)q8_small_kernel<P, EPI, FN, D, NW>, lds)) return r;
     q8_small_kernel<P, EPI, FN, D, NW><<<dim3(total), dim3(64 * NW), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
     AVA_LAUNCHED("q8_gemm");
     return AVA_OK;
-}
-
-// Waves per workgroup override (AVA_Q8_SMALL_WAVES = 4 or 8, tuning): 0 = by grid size.
-int small_waves() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_Q8_SMALL_WAVES");
-        v = e ? atoi(e) : 0;
-        if (v != 4 && v != 8) v = 0;
-    }
-    return v;
 }
 
 // 8 waves per workgroup when the grid gives a CU one workgroup or fewer, else 4 (two per CU); single
@@ -837,8 +678,7 @@ int launch_small_w(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk,
                    EpiArgs ep, hipStream_t st) {
     using C8 = SmallCfg<P, FN, 2, 8>;
     constexpr bool fits8 = P > 1 && std::max(C8::OPS, EPI == EPI_ACC ? C8::ACC : C8::DBL) <= 163840;  // LDS per CU
-    int nw = small_waves();
-    if (nw == 0) nw = ((m + 31) / 32) * ((n + 32 * FN - 1) / (32 * FN)) <= 256 ? 8 : 4;
+    const int nw = ((m + 31) / 32) * ((n + 32 * FN - 1) / (32 * FN)) <= 256 ? 8 : 4;
     if constexpr (fits8)
         if (nw == 8) return launch_small_fn<P, EPI, FN, 2, 8>(xq, xexp, m, n, ldk, qt, scale, ep, st);
     return launch_small_fn<P, EPI, FN, 2, 4>(xq, xexp, m, n, ldk, qt, scale, ep, st);
@@ -849,357 +689,12 @@ int launch_small_w(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk,
 template <int P, int EPI>
 int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                  EpiArgs ep, hipStream_t st) {
-    if (n >= small_wide_cols()) return launch_small_w<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    if (n >= SMALL_WIDE_COLS) return launch_small_w<P, EPI, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st);
     return launch_small_w<P, EPI, 1>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
-// ------------------------------------------------------------------ the product, deep-ring form
-//
-// As q8_gemm_dma_kernel, with the direct-to-LDS loads and the fragment reads both issued as inline
-// assembly, so the compiler's wait insertion (which cannot tell LDS stages apart and would wait for
-// every load in flight before any LDS read) sees neither: the waits are explicit. An S-stage ring
-// keeps S-1 K steps of loads in flight; at step kt a wave waits until only the loads of steps kt+1 ..
-// kt+S-2 are outstanding, one barrier publishes the stage, the stage freed at step kt-1 is refilled
-// with step kt+S-1, and the fragments pass through tie() after their lgkmcnt wait.
-__device__ __forceinline__ void dma16_asm(const void *g, unsigned lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-#endif
-}
-__device__ __forceinline__ unsigned lds_addr(const void *p) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-#else
-    return 0;
-#endif
-}
-
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
-__global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_ring_kernel(const int8_t *__restrict__ xq,
-                                                                      const int32_t *__restrict__ xexp, int m, int n,
-                                                                      int ldk, const int8_t *__restrict__ qt,
-                                                                      const float *__restrict__ scale, EpiArgs ep) {
-    constexpr int NT = 64 * WM * WN, BK = 64, CPR = 4, LDS_ROW = BK;
-    constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
-    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
-    static_assert(S >= 2 && S <= 8, "stages");
-    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;
-    constexpr int A_INS = A_ROWS / 16, B_INS = BN / 16, NWAVE = WM * WN;
-    static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
-    constexpr int LPW = (A_INS + B_INS) / NWAVE;
-    static_assert((S - 2) * LPW < 64, "vmcnt range");
-    constexpr int NF = FN + P * FM;
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-
-    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    int mt, nt;
-    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-
-    const int8_t *src[LPW];
-#pragma unroll
-    for (int i = 0; i < LPW; i++) {
-        const int ins = wave * LPW + i;
-        const int srow = ins * 16 + (lane >> 2);
-        if (srow < A_ROWS) {
-            const int p = srow / BM, rr = srow % BM;
-            const int row = min(m0 + rr, m - 1);
-            src[i] = xq + ((size_t)p * m + row) * ldk + swz<CPR>(rr, lane & 3) * 16;
-        } else {
-            const int rr = srow - A_ROWS;
-            const int col = min(n0 + rr, n - 1);
-            src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane & 3) * 16;
-        }
-    }
-    const unsigned lds0 = lds_addr(smem);
-    const int KT = ldk / BK;
-    auto issue = [&](int kt) {
-        const int k0 = min(kt, KT - 1) * BK;  // past the end: the last step again, never read
-        const unsigned base = lds0 + (unsigned)((kt % S) * STAGE + wave * LPW * 1024);
-#pragma unroll
-        for (int i = 0; i < LPW; i++) dma16_asm(src[i] + k0, base + i * 1024);
-    };
-    int foff[NF];
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int r = A_ROWS + wn * NW + j * 32 + (lane & 31);
-        foff[j] = r * LDS_ROW + swz<CPR>(r - A_ROWS, lane >> 5) * 16;
-    }
-#pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int r = wm * MW + i * 32 + (lane & 31);
-            foff[FN + p * FM + i] = (p * BM + r) * LDS_ROW + swz<CPR>(r, lane >> 5) * 16;
-        }
-
-    i32x16 acc[P][FM][FN];
-#pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
-
-#pragma unroll
-    for (int s0 = 0; s0 < S - 1; s0++) issue(s0);
-
-    for (int kt = 0; kt < KT; kt++) {
-        wait_vm<(S - 2) * LPW>();  // this wave's loads of step kt have landed
-        __builtin_amdgcn_s_barrier();  // ... and every wave's; every wave is done reading step kt-1's stage
-        issue(kt + S - 1);
-        const int8_t *base = smem + (kt % S) * STAGE;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            i32x4 f[NF];
-#pragma unroll
-            for (int x = 0; x < NF; x++) f[x] = lds_read128(base + (foff[x] ^ (ks * 32)));
-            lgkm_wait<0>();
-#pragma unroll
-            for (int x = 0; x < NF; x++) tie(f[x]);
-#pragma unroll
-            for (int p = 0; p < P; p++)
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[FN + p * FM + i], f[j], acc[p][i][j], 0,
-                                                                             0, 0);
-        }
-    }
-    wait_vm<0>();
-    __syncthreads();
-
-    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
-    int *s_exp = reinterpret_cast<int *>(smem);
-    if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += NT) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
-        __syncthreads();
-    }
-    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
-}
-
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
-int launch_ring(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
-                EpiArgs ep, hipStream_t st) {
-    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    size_t lds = (size_t)S * (P * BM + BN) * 64;
-    static bool attr = false;
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_ring_kernel<P, EPI, BM, BN, WM, WN, S>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
-    q8_gemm_ring_kernel<P, EPI, BM, BN, WM, WN, S><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(xq, xexp, m, n, ldk,
-                                                                                                 qt, scale, ep);
-    AVA_LAUNCHED("q8_gemm");
-    return AVA_OK;
-}
-
-// ------------------------------------------------------------------ the product, software-pipelined form
-//
-// One wave per SIMD (4 waves, up to 512 registers each: the P x FM x FN accumulators in AGPRs) and an
-// explicit pipeline in every wave: during step kt's MFMAs the fragments of step kt+1 are already being
-// read from LDS (inline-assembly reads, explicit lgkmcnt waits), and the direct-to-LDS loads of step
-// kt+S run S-1 steps ahead in an S-stage ring. At the single barrier of step kt, stage kt+1 has landed
-// (each wave waited for its own loads of it) and every wave has finished reading stage kt, which the
-// loads of step kt+S then overwrite.
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
-__global__ __launch_bounds__(64 * WM * WN, 1) void q8_gemm_pipe_kernel(const int8_t *__restrict__ xq,
-                                                                      const int32_t *__restrict__ xexp, int m, int n,
-                                                                      int ldk, const int8_t *__restrict__ qt,
-                                                                      const float *__restrict__ scale, EpiArgs ep) {
-    constexpr int NT = 64 * WM * WN, BK = 64, CPR = 4, LDS_ROW = BK;
-    constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
-    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
-    static_assert(S >= 2 && S <= 4, "stages");
-    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;
-    constexpr int A_INS = A_ROWS / 16, B_INS = BN / 16, NWAVE = WM * WN;
-    static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
-    constexpr int LPW = (A_INS + B_INS) / NWAVE;
-    constexpr int NF = FN + P * FM;  // fragments per K substep: B then A (plane-major)
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-
-    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    int mt, nt;
-    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-
-    const int8_t *src[LPW];
-#pragma unroll
-    for (int i = 0; i < LPW; i++) {
-        const int ins = wave * LPW + i;
-        const int srow = ins * 16 + (lane >> 2);
-        if (srow < A_ROWS) {
-            const int p = srow / BM, rr = srow % BM;
-            const int row = min(m0 + rr, m - 1);
-            src[i] = xq + ((size_t)p * m + row) * ldk + swz<CPR>(rr, lane & 3) * 16;
-        } else {
-            const int rr = srow - A_ROWS;
-            const int col = min(n0 + rr, n - 1);
-            src[i] = qt + (size_t)col * ldk + swz<CPR>(rr, lane & 3) * 16;
-        }
-    }
-    const int KT = ldk / BK;
-    auto issue = [&](int kt) {
-        const int k0 = min(kt, KT - 1) * BK;  // past the end: the last step again, never read
-        int8_t *base = smem + (kt % S) * STAGE + wave * LPW * 1024;
-#pragma unroll
-        for (int i = 0; i < LPW; i++) dma16(src[i] + k0, base + i * 1024);
-    };
-    // byte offsets (within a stage) of this lane's fragments for K substep 0; substep 1 is offset ^ 32
-    int foff[NF];
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int r = A_ROWS + wn * NW + j * 32 + (lane & 31);
-        foff[j] = r * LDS_ROW + swz<CPR>(r - A_ROWS, lane >> 5) * 16;
-    }
-#pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int r = wm * MW + i * 32 + (lane & 31);
-            foff[FN + p * FM + i] = (p * BM + r) * LDS_ROW + swz<CPR>(r, lane >> 5) * 16;
-        }
-    auto read_frags = [&](int kt, i32x4 (&f)[2][NF]) {
-        const int8_t *base = smem + (kt % S) * STAGE;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int x = 0; x < NF; x++) f[ks][x] = lds_read128(base + (foff[x] ^ (ks * 32)));
-    };
-
-    i32x16 acc[P][FM][FN];
-#pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
-
-    // prologue: stages 0 .. S-1 in flight; step 0's fragments read
-#pragma unroll
-    for (int s0 = 0; s0 < S; s0++) issue(s0);
-    wait_vm<(S - 1) * LPW>();
-    __syncthreads();
-    i32x4 fc[2][NF], fn[2][NF];
-    read_frags(0, fc);
-
-    for (int kt = 0; kt < KT; kt++) {
-        // stage kt+1 landed (own loads, then everyone's), and every wave is done reading stage kt
-        lgkm_wait<0>();
-        wait_vm<(S - 2) * LPW>();
-        __syncthreads();
-        issue(kt + S);
-        if (kt + 1 < KT) read_frags(kt + 1, fn);
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-            for (int x = 0; x < NF; x++) tie(fc[ks][x]);
-#pragma unroll
-            for (int p = 0; p < P; p++)
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fc[ks][FN + p * FM + i], fc[ks][j],
-                                                                             acc[p][i][j], 0, 0, 0);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int x = 0; x < NF; x++) fc[ks][x] = fn[ks][x];
-    }
-    lgkm_wait<0>();
-    wait_vm<0>();
-    __syncthreads();
-
-    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
-    int *s_exp = reinterpret_cast<int *>(smem);
-    if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += NT) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
-        __syncthreads();
-    }
-    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
-}
-
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S>
-int launch_pipe(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
-                EpiArgs ep, hipStream_t st) {
-    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    size_t lds = (size_t)S * (P * BM + BN) * 64;
-    static bool attr = false;
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_pipe_kernel<P, EPI, BM, BN, WM, WN, S>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
-    q8_gemm_pipe_kernel<P, EPI, BM, BN, WM, WN, S><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(xq, xexp, m, n, ldk,
-                                                                                                 qt, scale, ep);
-    AVA_LAUNCHED("q8_gemm");
-    return AVA_OK;
-}
-
-// Tile shapes. kind 0: the register-staged kernel (BM, BN, WM, BK); kind 1: the direct-to-LDS kernel
-// (BM, BN, WM, WN, S) with 64-byte K steps; kind 5: the same with 128-byte K steps; kind 4: kind 1
-// at two workgroups per CU; kind 2: the software-pipelined form; kind 3: the deep-ring form.
-// AVA_Q8_TILE=<index> overrides the choice (tuning).
-struct TileCfg {
-    int kind, bm, bn, wm, wn, bk_or_s;
-};
-constexpr TileCfg TILES[] = {
-    {0, 128, 128, 2, 2, 64}, {0, 64, 128, 2, 2, 64}, {1, 128, 128, 2, 2, 2}, {1, 128, 256, 2, 4, 2},
-    {1, 256, 128, 4, 2, 2},  {2, 128, 128, 2, 2, 3}, {3, 128, 256, 2, 4, 3}, {3, 128, 256, 2, 4, 4},
-    {3, 128, 128, 2, 2, 4},  {3, 256, 128, 4, 2, 3}, {3, 128, 128, 2, 4, 4}, {3, 64, 256, 1, 4, 4},
-    {4, 128, 128, 2, 2, 2},  {4, 64, 256, 1, 4, 2},  {5, 128, 256, 2, 4, 2},  {5, 128, 128, 2, 2, 2},
-    {5, 64, 256, 1, 4, 2}};
-constexpr int NTILES = sizeof(TILES) / sizeof(TILES[0]);
-
-int tile_override() {
-    static int v = -2;
-    if (v == -2) {
-        const char *e = getenv("AVA_Q8_TILE");
-        v = e ? atoi(e) : -1;
-        if (v > NTILES) v = -1;  // NTILES: the few-rows kernel
-    }
-    return v;
-}
-
-
-
-// Row blocks per tile group (tile_origin); AVA_Q8_GROUP overrides it (tuning).
-int tile_group() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("AVA_Q8_GROUP");
-        v = e ? atoi(e) : 8;
-        if (v < 1) v = 1;
-    }
-    return v;
-}
-
-template <int P, int EPI, int BM, int BN, int WM, int BK>
-int launch_tile(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
-                EpiArgs ep, hipStream_t st) {
-    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    const size_t lds = (size_t)2 * (P * BM + BN) * BK;
-    static bool attr = false;  // above 64 KiB of dynamic LDS the kernel must opt in (gfx950: 160 KiB)
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_kernel<P, EPI, BM, BN, WM, BK>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
-    q8_gemm_kernel<P, EPI, BM, BN, WM, BK><<<dim3(total), dim3(256), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
-    AVA_LAUNCHED("q8_gemm");
-    return AVA_OK;
-}
+// Row blocks per tile group (tile_origin): a weight column tile is fetched past L2 once per 8 row blocks.
+constexpr int TILE_GROUP = 8;
 
 template <int P, int EPI, int BM, int BN, int WM, int WN, int S, int MINB = 1, int BKB = 64>
 int launch_dma(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
@@ -1207,12 +702,7 @@ int launch_dma(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, con
     const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     size_t lds = (size_t)S * (P * BM + BN) * BKB;
     if (lds < (size_t)BM * 4) lds = (size_t)BM * 4;
-    static bool attr = false;
-    if (!attr) {
-        AVA_HIP(hipFuncSetAttribute((const void *)q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
+    if (int r = ava::lds_opt_in((const void *)q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB>, lds)) return r;
     q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(
         xq, xexp, m, n, ldk, qt, scale, ep);
     AVA_LAUNCHED("q8_gemm");
@@ -1222,41 +712,14 @@ int launch_dma(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, con
 template <int P, int EPI>
 int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
                 EpiArgs ep, hipStream_t st) {
-    int t = tile_override();
-    // few rows (decode): 32 x 32 blocks with the K steps spread over the waves
-    if (t < 0 && m <= small_rows()) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    if (t == NTILES) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    // the direct-to-LDS 128 x 256 tile, 8 waves: 128-byte K steps for split-plane inputs, 64-byte
-    // ones for the single spike plane (measured best on every config[3] shape)
-    if (t < 0) t = P == 1 ? 3 : 14;
-#define AVA_T(I)                                                                                                   \
-    if (t == I) {                                                                                                  \
-        constexpr TileCfg c = TILES[I];                                                                            \
-        if constexpr (c.kind == 0)                                                                                 \
-            return launch_tile<P, EPI, c.bm, c.bn, c.wm, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st);       \
-        else if constexpr (c.kind == 1 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
-                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0)                                          \
-            return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
-        else if constexpr (c.kind == 4 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 80 * 1024 &&                      \
-                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0)                                          \
-            return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s, 2>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
-        else if constexpr (c.kind == 5 && (P * c.bm + c.bn) * 128 * c.bk_or_s <= 160 * 1024 &&                    \
-                           ((P * c.bm + c.bn) / 8) % (c.wm * c.wn) == 0)                                           \
-            return launch_dma<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s, 1, 128>(xq, xexp, m, n, ldk, qt, scale, ep, \
-                                                                               st);                             \
-        else if constexpr (c.kind == 3 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
-                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0 && (c.bm / c.wm) % 32 == 0 &&            \
-                           (c.bn / c.wn) % 32 == 0)                                                                \
-            return launch_ring<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
-        else if constexpr (c.kind == 2 && (P * c.bm + c.bn) * 64 * c.bk_or_s <= 160 * 1024 &&                     \
-                           ((P * c.bm + c.bn) / 16) % (c.wm * c.wn) == 0 && P * c.bm / c.wm * c.bn / c.wn <= 16384) \
-            return launch_pipe<P, EPI, c.bm, c.bn, c.wm, c.wn, c.bk_or_s>(xq, xexp, m, n, ldk, qt, scale, ep, st); \
-        else                                                                                                       \
-            return ava::fail(AVA_ERR_UNSUPPORTED, "q8 product: tile %d does not fit %d planes", I, P);             \
-    }
-    AVA_T(0) AVA_T(1) AVA_T(2) AVA_T(3) AVA_T(4) AVA_T(5) AVA_T(6) AVA_T(7) AVA_T(8) AVA_T(9) AVA_T(10) AVA_T(11) AVA_T(12) AVA_T(13) AVA_T(14) AVA_T(15) AVA_T(16)
-#undef AVA_T
-    return ava::fail(AVA_ERR_ARG, "q8 product: tile %d", t);
+    // few rows (decode): 32-row blocks with the K steps spread over the waves
+    if (m <= SMALL_ROWS) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    // the direct-to-LDS 128 x 256 tile, 8 waves, two stages: 128-byte K steps for split-plane inputs,
+    // 64-byte ones for the single spike plane (measured best on every config[3] shape)
+    if constexpr (P == 1)
+        return launch_dma<P, EPI, 128, 256, 2, 4, 2, 1, 64>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    else
+        return launch_dma<P, EPI, 128, 256, 2, 4, 2, 1, 128>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 template <int EPI>
@@ -1297,20 +760,20 @@ int q8_gemm(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_
     if (int r = check_qw(w)) return r;
     AVA_REQUIRE(xq && y, AVA_ERR_ARG, "q8 product: NULL buffer");
     if (m == 0) return AVA_OK;
-    EpiArgs ep{y, ldy, colv, tile_group()};
+    EpiArgs ep{y, ldy, colv, TILE_GROUP};
     if (kind == EPI_STORE) return gemm_planes<EPI_STORE>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     if (kind == EPI_MUL) return gemm_planes<EPI_MUL>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     if (kind == EPI_ADD) return gemm_planes<EPI_ADD>(planes, xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
     return fail(AVA_ERR_ARG, "q8 product: epilogue %d", kind);
 }
 
-int q8_small_rows() { return small_rows(); }
+int q8_small_rows() { return SMALL_ROWS; }
 
 int q8_gemm_lif(const int8_t *xq, const int32_t *xexp, int planes, int m, const ava_qw *w, const float *colv,
                 const LifEpi &lif, hipStream_t st) {
     if (int r = check_qw(w)) return r;
     AVA_REQUIRE(xq && lif.ps && lif.v && lif.s && lif.a && lif.spikes, AVA_ERR_ARG, "q8 lif product: NULL buffer");
-    AVA_REQUIRE(m > 0 && m <= small_rows(), AVA_ERR_SHAPE, "q8 lif product: %d rows (the few-rows form only)", m);
+    AVA_REQUIRE(m > 0 && m <= SMALL_ROWS, AVA_ERR_SHAPE, "q8 lif product: %d rows (the few-rows form only)", m);
     AVA_REQUIRE(lif.levels == 1 || lif.levels == 2, AVA_ERR_ARG, "q8 lif product: levels %d", lif.levels);
     EpiArgs ep{nullptr, 0, colv, 1, lif};
     if (planes == 1) return launch_small<1, EPI_LIF>(xq, xexp, m, w->dout, w->ldk, w->qt, w->scale, ep, st);
@@ -1348,7 +811,7 @@ extern "C" int ava_q8_gemm_acc(const int8_t *xq, int planes, int m, const ava_qw
     if (int r = check_qw(w)) return r;
     AVA_REQUIRE(xq && acc, AVA_ERR_ARG, "q8_gemm_acc: NULL buffer");
     if (m == 0) return AVA_OK;
-    EpiArgs ep{acc, w->dout, nullptr, tile_group()};
+    EpiArgs ep{acc, w->dout, nullptr, TILE_GROUP};
     return gemm_planes<EPI_ACC>(planes, xq, nullptr, m, w->dout, w->ldk, w->qt, w->scale, ep, (hipStream_t)stream);
 }
 
