@@ -78,6 +78,10 @@ def lib():
         "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
+        "ava_lif_scan_bwd": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, f32, i32] + [vp] * 10,
+        "ava_kwta_relu2_bwd": [vp, vp, i32, i32, vp, vp, vp],
+        "ava_mem_scan_bwd": [vp] * 6 + [i32] * 4 + [f32, f32] + [vp] * 14 + [sz, vp],
+        "ava_dense_back": [vp] * 6 + [i32] * 4 + [C.c_longlong, vp, sz, vp],
         "ava_attend": [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, sz, vp],
         "ava_attend_heads": [vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, sz, vp],
         "ava_model_new": [C.POINTER(Config), C.POINTER(Params), C.POINTER(vp)],
@@ -95,6 +99,10 @@ def lib():
     L.ava_attend_part_floats.restype = sz
     L.ava_attend_heads_part_floats.argtypes = [i32, i32, i32, i32, i32]
     L.ava_attend_heads_part_floats.restype = sz
+    L.ava_mem_scan_bwd_workspace.argtypes = [i32, i32, i32]
+    L.ava_mem_scan_bwd_workspace.restype = sz
+    L.ava_dense_back_part_floats.argtypes = [C.c_longlong, i32]
+    L.ava_dense_back_part_floats.restype = sz
     L.ava_q8_workspace.argtypes = [i32, i32, i32]
     L.ava_q8_workspace.restype = sz
     if hasattr(L, "ava_model_free"):

@@ -1,0 +1,263 @@
+// The backward of the general LIF scan for gfx950 (the surrogate gradient of the straight-through
+// spikes: gpu/arch.rs:964-1071 lif_ref's autograd; the CUDA form lifg_bwd, gpu/lif.cu:3228-3290).
+//
+// One lane per (b, c), channel-contiguous as the forward, walking T twice:
+//   1. the forward replayed from (v0, s0, a0), nothing kept but the state at the start of every
+//      segment of K steps (segments are cut from the end, so only the first may be short). That
+//      state (v, s, a) is parked in the segment's own first three rows of dI, which the reverse
+//      pass overwrites last: no workspace and 12 bytes per segment of traffic.
+//   2. segment by segment from the last: the K steps replayed from the parked state with v_t, a_t
+//      and s_t in registers, then walked back. The next (earlier) segment's currents, incoming
+//      gradients and parked state are loaded while this one is processed.
+// HBM per element: the currents twice, the incoming gradient once and dI once, 16 bytes (a
+// backward that stores the membrane and trace instead moves 28).
+//
+// Per step, backwards (G = dL/dv_t, carried: cv = beta G_{t+1}, ca = dL/da_{t+1} rho):
+//   ds/dv, ds/dth from the surrogate 1 / (1 + S |x|)^2 of each spike edge x = v - k th, -v - k th;
+//   gs = dL/ds_t (minus te G_{t+1} when the reset carries gradient, te = th_t or 2 beta / (ds/dv)
+//   where th_t ds/dv > 2 beta);  G = gs ds/dv + cv;  dbeta += G v_{t-1};
+//   ALIF: gth = gs ds/dth (- s_t G_{t+1}), ga = gth gain + ca, dgain += gth a_t,
+//   drho += ga (a_{t-1} - |s_{t-1}|), ca = rho ga.
+// Every operation is rounded on its own (-ffp-contract=off), in the order of the CPU statement.
+#include "common.h"
+
+namespace {
+
+template <int LEVELS, bool SIGNED>
+__device__ __forceinline__ float spike_of(float v, float th) {
+    if (!SIGNED) return (v - th >= 0.0f) ? 1.0f : 0.0f;
+    float h = 0.0f;
+#pragma unroll
+    for (int k = 1; k <= LEVELS; k++) {
+        const float kth = th * (float)k;
+        h += ((v - kth >= 0.0f) ? 1.0f : 0.0f) - ((-v - kth >= 0.0f) ? 1.0f : 0.0f);
+    }
+    return h;
+}
+
+__device__ __forceinline__ float surrogate(float x, float slope) {
+    const float a = 1.0f + slope * fabsf(x);
+    return 1.0f / (a * a);
+}
+
+// d s / d v and d s / d th of one step's surrogate spike.
+template <int LEVELS, bool SIGNED>
+__device__ __forceinline__ void dspike(float v, float th, float slope, float &dv, float &dth) {
+    if (!SIGNED) {
+        const float g = surrogate(v - th, slope);
+        dv = g;
+        dth = -g;
+        return;
+    }
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int k = 1; k <= LEVELS; k++) {
+        const float kth = th * (float)k;
+        const float gu = surrogate(v - kth, slope), gd = surrogate(-v - kth, slope);
+        a += gu + gd;
+        b += (float)k * (gd - gu);
+    }
+    dv = a;
+    dth = b;
+}
+
+struct LifBwdArgs {
+    const float *cur, *ps, *v0, *s0, *a0, *gs, *gv, *ga;
+    float *dI, *dv0, *da0, *dbeta, *drho, *dgain;
+    int B, T, D;
+    float slope;
+    int rg;
+};
+
+template <int K, int LEVELS, bool SIGNED, bool ALIF>
+__global__ __launch_bounds__(256) void lif_bwd_kernel(LifBwdArgs p) {
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int D = p.D, T = p.T;
+    if (gid >= p.B * D) return;
+    const int b = gid / D, c = gid - b * D;
+    const float bt = p.ps[c], th0 = p.ps[D + c], rho = p.ps[2 * D + c], gain = p.ps[3 * D + c];
+    const float omr = 1.0f - rho;
+    const size_t col = (size_t)b * T * D + c;
+    const float *x = p.cur + col, *g = p.gs + col;
+    float *o = p.dI + col;
+    const float v0 = p.v0[gid], s0 = p.s0[gid], a0 = ALIF ? p.a0[gid] : 0.0f;
+    const int nseg = (T + K - 1) / K;
+    // segment q (0 = the last) covers [max(0, T - (q + 1) K), T - q K)
+    auto seg0 = [&](int q) { return max(0, T - (q + 1) * K); };
+
+    float buf[K], nxt[K];
+    auto load_cur = [&](int q, float (&dst)[K]) {
+        const int t0 = seg0(q), n = T - q * K - t0;
+#pragma unroll
+        for (int i = 0; i < K; i++)
+            if (i < n) dst[i] = __builtin_nontemporal_load(x + (size_t)(t0 + i) * D);
+    };
+
+    // 1. the forward, parking the state at each segment's start (segments after the first)
+    {
+        float v = v0, sp = s0, a = a0, thp = ALIF ? th0 + a0 * gain : th0;
+        load_cur(nseg - 1, buf);
+        for (int q = nseg - 1; q >= 0; q--) {
+            if (q > 0) load_cur(q - 1, nxt);
+            const int t0 = seg0(q), n = T - q * K - t0;
+            if (t0 > 0) {
+                o[(size_t)t0 * D] = v;
+                o[(size_t)(t0 + 1) * D] = sp;
+                if (ALIF) o[(size_t)(t0 + 2) * D] = a;
+            }
+#pragma unroll
+            for (int i = 0; i < K; i++) {
+                if (i < n) {
+                    float tht = th0;
+                    if (ALIF) {
+                        a = a * rho + fabsf(sp) * omr;
+                        tht = th0 + a * gain;
+                    }
+                    v = (v * bt + buf[i]) - sp * thp;
+                    sp = spike_of<LEVELS, SIGNED>(v, tht);
+                    thp = tht;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < K; i++) buf[i] = nxt[i];
+        }
+    }
+
+    // 2. backwards, segment by segment
+    float cv = p.gv ? p.gv[gid] : 0.0f, ca = (ALIF && p.ga) ? p.ga[gid] : 0.0f;
+    float gb = 0.0f, gr = 0.0f, gg = 0.0f, Gn = 0.0f;  // Gn = dL/dv_{t+1}
+    float gbuf[K], gnxt[K];
+    auto load_g = [&](int q, float (&dst)[K]) {
+        const int t0 = seg0(q), n = T - q * K - t0;
+#pragma unroll
+        for (int i = 0; i < K; i++)
+            if (i < n) dst[i] = g[(size_t)(t0 + i) * D];
+    };
+    float ckv, cks, cka, nkv = 0.0f, nks = 0.0f, nka = 0.0f;
+    auto load_ck = [&](int q, float &kv, float &ks, float &ka) {
+        const int t0 = seg0(q);
+        if (t0 > 0) {
+            kv = o[(size_t)t0 * D];
+            ks = o[(size_t)(t0 + 1) * D];
+            ka = ALIF ? o[(size_t)(t0 + 2) * D] : 0.0f;
+        } else {
+            kv = v0;
+            ks = s0;
+            ka = a0;
+        }
+    };
+    load_cur(0, buf);
+    load_g(0, gbuf);
+    load_ck(0, ckv, cks, cka);
+    for (int q = 0; q < nseg; q++) {
+        if (q + 1 < nseg) {
+            load_cur(q + 1, nxt);
+            load_g(q + 1, gnxt);
+            load_ck(q + 1, nkv, nks, nka);
+        }
+        const int t0 = seg0(q), n = T - q * K - t0;
+        float vs[K], as[K], ss[K];
+        {
+            float v = ckv, sp = cks, a = cka, thp = ALIF ? th0 + cka * gain : th0;
+#pragma unroll
+            for (int i = 0; i < K; i++) {
+                if (i < n) {
+                    float tht = th0;
+                    if (ALIF) {
+                        a = a * rho + fabsf(sp) * omr;
+                        tht = th0 + a * gain;
+                    }
+                    v = (v * bt + buf[i]) - sp * thp;
+                    sp = spike_of<LEVELS, SIGNED>(v, tht);
+                    thp = tht;
+                    vs[i] = v;
+                    as[i] = a;
+                    ss[i] = sp;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = K - 1; i >= 0; i--) {
+            if (i < n) {
+                const float vt = vs[i], at = ALIF ? as[i] : 0.0f;
+                const float tht = ALIF ? th0 + at * gain : th0;
+                float dv, dth;
+                dspike<LEVELS, SIGNED>(vt, tht, p.slope, dv, dth);
+                float gst = gbuf[i];
+                if (p.rg) {
+                    const float qq = tht * dv, cap = 2.0f * bt;
+                    gst -= (qq > cap ? cap / dv : tht) * Gn;
+                }
+                const float G = gst * dv + cv;
+                gb += G * (i > 0 ? vs[i - 1] : ckv);
+                if (ALIF) {
+                    float gth = gst * dth;
+                    if (p.rg) gth -= ss[i] * Gn;
+                    const float gaa = gth * gain + ca;
+                    gg += gth * at;
+                    const float ap = i > 0 ? as[i - 1] : cka;
+                    const float sprev = i > 0 ? ss[i - 1] : cks;
+                    gr += gaa * (ap - fabsf(sprev));
+                    ca = rho * gaa;
+                }
+                o[(size_t)(t0 + i) * D] = G;
+                Gn = G;
+                cv = bt * G;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < K; i++) {
+            buf[i] = nxt[i];
+            gbuf[i] = gnxt[i];
+        }
+        ckv = nkv;
+        cks = nks;
+        cka = nka;
+    }
+    if (ALIF && p.rg) {  // the first step's reset used the initial threshold theta + a0 gain
+        const float g0 = -s0 * Gn;
+        gg += g0 * a0;
+        ca += g0 * gain;
+    }
+    p.dv0[gid] = cv;
+    if (p.da0) p.da0[gid] = ALIF ? ca : 0.0f;
+    p.dbeta[gid] = gb;
+    if (p.drho) p.drho[gid] = ALIF ? gr : 0.0f;
+    if (p.dgain) p.dgain[gid] = ALIF ? gg : 0.0f;
+}
+
+constexpr int SEG = 16;  // steps per segment: 6 x 16 registers of currents, gradients and replayed state
+
+}  // namespace
+
+// The LIF scan's backward. Outputs per (b, c): dI [B][T][D], dv0, da0 and this stream's shares of
+// dbeta, drho, dgain ([B][D] each; the parameter gradients are their sums over b).
+extern "C" int ava_lif_scan_bwd(const float *cur, int B, int T, int D, const float *ps, const float *v0,
+                                const float *s0, const float *a0, int levels, int is_signed, int alif, float slope,
+                                int reset_grad, const float *g_spk, const float *g_vT, const float *g_aT, float *dI,
+                                float *dv0, float *da0, float *dbeta, float *drho, float *dgain, ava_stream stream) {
+    AVA_REQUIRE(cur && ps && v0 && s0 && g_spk && dI && dv0 && dbeta, AVA_ERR_ARG, "lif_scan_bwd: NULL buffer");
+    AVA_REQUIRE(!alif || (a0 && da0 && drho && dgain), AVA_ERR_ARG, "lif_scan_bwd: ALIF needs a0, da0, drho, dgain");
+    AVA_REQUIRE(B > 0 && T > 0 && D > 0 && (long)B * D <= (1L << 30), AVA_ERR_SHAPE, "lif_scan_bwd: B=%d T=%d D=%d",
+                B, T, D);
+    AVA_REQUIRE(levels == 1 || levels == 2, AVA_ERR_ARG, "lif_scan_bwd: levels %d (1 or 2)", levels);
+    AVA_REQUIRE(slope >= 0.0f, AVA_ERR_ARG, "lif_scan_bwd: slope %g (the reset gradient is reset_grad)", slope);
+    LifBwdArgs p{cur, ps, v0, s0, a0, g_spk, g_vT, alif ? g_aT : nullptr, dI, dv0, da0, dbeta, drho, dgain,
+                 B, T, D, slope, reset_grad ? 1 : 0};
+    const hipStream_t st = (hipStream_t)stream;
+    dim3 grid(ava::ceil_div((long)B * D, 256)), block(256);
+#define AVA_LB(L, S, A) lif_bwd_kernel<SEG, L, S, A><<<grid, block, 0, st>>>(p)
+    if (!is_signed) {
+        if (alif) AVA_LB(1, false, true);
+        else AVA_LB(1, false, false);
+    } else if (levels == 1) {
+        if (alif) AVA_LB(1, true, true);
+        else AVA_LB(1, true, false);
+    } else {
+        if (alif) AVA_LB(2, true, true);
+        else AVA_LB(2, true, false);
+    }
+#undef AVA_LB
+    AVA_LAUNCHED("lif_scan_bwd");
+    return AVA_OK;
+}

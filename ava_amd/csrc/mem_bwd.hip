@@ -1,0 +1,365 @@
+// The backward of the fast-weight (delta-rule) memory recurrence for gfx950, one workgroup per head
+// (delta_rec's gradient, gpu/arch.rs:1091-1136; the CUDA forms memg_bwd / memg_bwd4,
+// gpu/lif.cu:3411-3888).
+//
+// Forward, per head and step: r = F^T e;  u_ij = b_i k_i v_j - a_i b_i e_i r_j;  S' = M S + u;
+// P = a_i F_ij + S'_ij (M = 0: + u_ij);  F' = clamp(P, +-cap);  y = F'^T q.
+// Backward, from the last step (dF, dS carried): gP = (dF + q dy^T) where |F'| < cap, else 0;
+//   dq_i = sum_j dy_j F'_ij;  dalpha_i += sum_j gP_ij F_ij;  du = gP + dS;  dS <- M du;
+//   dv_j = sum_i du_ij b_i k_i;  dr_j = -sum_i du_ij a_i b_i e_i;
+//   with sv_i = sum_j du_ij v_j and sr_i = sum_j du_ij r_j:  dk_i = b_i sv_i;
+//   db_i = k_i sv_i - a_i e_i sr_i;  dalpha_i -= b_i e_i sr_i;  de_i = -a_i b_i sr_i + sum_j dr_j F_ij;
+//   dF <- a_i gP_ij + e_i dr_j;  dla = dalpha a (summed over the head's rows for per-head gates).
+//
+// Columns of F never mix in the forward, nor in the carried gradients; only the row sums above
+// (over all 64 columns) couple them. So wave w owns columns 16w..16w+15 outright, and lane l of it
+// a 4 x 4 block: rows 4 (l & 15).., columns 16w + 4 (l >> 4)... A column sum (r, dr, dv) is 4 FMAs
+// in the lane and 4 DPP adds over the 16 lanes of a DPP row; a row sum is 4 in the lane and two
+// lane swaps over the wave's column groups, then the four waves' partials add up in LDS once per
+// CK steps.
+//
+// States for the backward come from recomputation: pass 1 replays the forward and parks (F, S)
+// every CK steps in the caller's workspace; pass 2 walks the checkpoints from the last, replays CK
+// steps from each with every state F_t kept in registers (CK + 1 of them, and r_t), and walks those
+// steps back. The inputs of CK steps are staged in LDS; the next group's are loaded meanwhile.
+// Workspace: BH x ceil(T / CK) x (1 or 2 with momentum) x 16 KB.
+#include "common.h"
+
+namespace {
+
+constexpr int HS = 64, CK = 4;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// The sum over the 16 lanes of v's DPP row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), in every one of them.
+__device__ __forceinline__ float sum16(float v) {
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    v += dppf<0x141>(v);
+    return v + dppf<0x140>(v);
+}
+// v[l] + v[l ^ 16] + v[l ^ 32] + v[l ^ 48] in every lane (the gfx950 lane swaps).
+__device__ __forceinline__ float sum_cols(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+struct MemBwdArgs {
+    const float *q, *k, *e, *v, *la, *b, *F0, *S0, *dy, *dFT, *dST;
+    float *dq, *dk, *de, *dv, *dla, *db, *dF0, *dS0, *ck;
+    int T;
+    float m, cap;
+};
+
+struct Stage {
+    float q[CK][HS], k[CK][HS], e[CK][HS], v[CK][HS], a[CK][HS], b[CK][HS], bk[CK][HS], abe[CK][HS], dy[CK][HS];
+};
+
+// One forward step on the lane's 4 x 4 block (rows i0.., columns j0..): r (the block's 4 columns of
+// e^T F, summed over all rows) is returned for the backward.
+template <bool MOM>
+__device__ __forceinline__ void fwd_step(float (&F)[16], float (&S)[16], const Stage &sg, int s, int i0, int j0,
+                                         float M, float cap, float (&r)[4]) {
+    const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&sg.e[s][i0]);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        float x = e4[0] * F[c];
+        x = fmaf(e4[1], F[4 + c], x);
+        x = fmaf(e4[2], F[8 + c], x);
+        x = fmaf(e4[3], F[12 + c], x);
+        r[c] = sum16(x);
+    }
+    const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sg.v[s][j0]);
+    const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&sg.a[s][i0]);
+    const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&sg.bk[s][i0]);
+    const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&sg.abe[s][i0]);
+#pragma unroll
+    for (int ri = 0; ri < 4; ri++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int m = 4 * ri + c;
+            const float u = fmaf(-x4[ri], r[c], k4[ri] * v4[c]);
+            float f;
+            if (MOM) {
+                S[m] = fmaf(M, S[m], u);
+                f = fmaf(a4[ri], F[m], S[m]);
+            } else {
+                f = fmaf(a4[ri], F[m], u);
+            }
+            F[m] = __builtin_amdgcn_fmed3f(f, -cap, cap);
+        }
+}
+
+template <bool G1, bool MOM>
+__global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
+    __shared__ __attribute__((aligned(16))) Stage sg;
+    __shared__ float red[CK][4][5][HS];  // per step, wave and row: dq, sum gP F, sv, sr, sum dr F
+
+    const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i0 = 4 * (lane & 15), j0 = 16 * wave + 4 * (lane >> 4);
+    const int T = p.T, nck = (T + CK - 1) / CK;
+    constexpr int NS = MOM ? 2 : 1;
+    const size_t hb = (size_t)bh * T * HS;
+    const size_t gb = G1 ? (size_t)bh * T : hb;
+    float *ckh = p.ck + (size_t)bh * nck * NS * HS * HS + (size_t)tid * 16;
+    const float M = p.m, cap = p.cap;
+
+    float F[16], S[16];
+    {
+        const size_t o0 = (size_t)bh * HS * HS;
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            const size_t o = o0 + (size_t)(i0 + (m >> 2)) * HS + j0 + (m & 3);
+            F[m] = p.F0 ? p.F0[o] : 0.0f;
+            S[m] = (MOM && p.S0) ? p.S0[o] : 0.0f;
+        }
+    }
+
+    // staging: thread -> (step st of the group, channel cc); the loads of a group are issued one
+    // group ahead
+    const int st = tid >> 6, cc = tid & 63;
+    float lq = 0, lk = 0, le = 0, lv = 0, ll = 0, lb = 0, ld = 0;
+    auto load = [&](int t0, bool bwd) {
+        const int t = t0 + st;
+        if (t < T && t0 >= 0) {
+            const size_t o = hb + (size_t)t * HS + cc;
+            lk = p.k[o];
+            le = p.e[o];
+            lv = p.v[o];
+            const size_t og = G1 ? gb + t : o;
+            ll = p.la[og];
+            lb = p.b[og];
+            if (bwd) {
+                lq = p.q[o];
+                ld = p.dy[o];
+            }
+        } else {
+            lq = lk = le = lv = ll = lb = ld = 0.0f;
+        }
+    };
+    auto stage = [&]() {
+        const float a = expf(ll);
+        sg.q[st][cc] = lq;
+        sg.k[st][cc] = lk;
+        sg.e[st][cc] = le;
+        sg.v[st][cc] = lv;
+        sg.a[st][cc] = a;
+        sg.b[st][cc] = lb;
+        sg.bk[st][cc] = lb * lk;
+        sg.abe[st][cc] = (a * lb) * le;
+        sg.dy[st][cc] = ld;
+    };
+    auto park = [&](int c, const float (&X)[16], int which) {
+        float *dst = ckh + ((size_t)c * NS + which) * HS * HS;
+#pragma unroll
+        for (int z = 0; z < 4; z++)
+            *reinterpret_cast<f32x4 *>(dst + 4 * z) = f32x4{X[4 * z], X[4 * z + 1], X[4 * z + 2], X[4 * z + 3]};
+    };
+    auto unpark = [&](int c, float (&X)[16], int which) {
+        const float *src = ckh + ((size_t)c * NS + which) * HS * HS;
+#pragma unroll
+        for (int z = 0; z < 4; z++) {
+            const f32x4 x = *reinterpret_cast<const f32x4 *>(src + 4 * z);
+            X[4 * z] = x[0];
+            X[4 * z + 1] = x[1];
+            X[4 * z + 2] = x[2];
+            X[4 * z + 3] = x[3];
+        }
+    };
+
+    // 1. the forward, parking the state at the start of every group of CK steps
+    load(0, false);
+    for (int c = 0; c < nck; c++) {
+        __syncthreads();
+        stage();
+        __syncthreads();
+        load((c + 1) * CK, false);
+        park(c, F, 0);
+        if (MOM) park(c, S, 1);
+        const int n = min(CK, T - c * CK);
+#pragma unroll
+        for (int s = 0; s < CK; s++) {
+            if (s < n) {
+                float r[4];
+                fwd_step<MOM>(F, S, sg, s, i0, j0, M, cap, r);
+            }
+        }
+    }
+
+    // 2. backwards, group by group
+    float dF[16], dS[16];
+    {
+        const size_t o0 = (size_t)bh * HS * HS;
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            const size_t o = o0 + (size_t)(i0 + (m >> 2)) * HS + j0 + (m & 3);
+            dF[m] = p.dFT ? p.dFT[o] : 0.0f;
+            dS[m] = (MOM && p.dST) ? p.dST[o] : 0.0f;
+        }
+    }
+    load((nck - 1) * CK, true);
+    for (int c = nck - 1; c >= 0; c--) {
+        const int t0 = c * CK, n = min(CK, T - t0);
+        __syncthreads();  // the previous group's combine is done with the staging and red
+        stage();
+        __syncthreads();
+        load(t0 - CK, true);  // nothing past the first group (t0 - CK < 0)
+        float Ft[CK + 1][16], rt[CK][4];
+        unpark(c, Ft[0], 0);
+        if (MOM) unpark(c, S, 1);
+#pragma unroll
+        for (int s = 0; s < CK; s++) {
+            if (s < n) {
+#pragma unroll
+                for (int m = 0; m < 16; m++) Ft[s + 1][m] = Ft[s][m];
+                fwd_step<MOM>(Ft[s + 1], S, sg, s, i0, j0, M, cap, rt[s]);
+            }
+        }
+#pragma unroll
+        for (int s = CK - 1; s >= 0; s--) {
+            if (s < n) {
+                const float(&Fa)[16] = Ft[s];      // F before the step
+                const float(&Fb)[16] = Ft[s + 1];  // after it
+                const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&sg.q[s][i0]);
+                const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&sg.e[s][i0]);
+                const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&sg.a[s][i0]);
+                const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&sg.bk[s][i0]);
+                const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&sg.abe[s][i0]);
+                const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sg.v[s][j0]);
+                const f32x4 y4 = *reinterpret_cast<const f32x4 *>(&sg.dy[s][j0]);
+                float pdq[4], pal[4], psv[4], psr[4], pde[4], cdr[4], cdv[4];
+#pragma unroll
+                for (int z = 0; z < 4; z++) pdq[z] = pal[z] = psv[z] = psr[z] = pde[z] = cdr[z] = cdv[z] = 0.0f;
+#pragma unroll
+                for (int ri = 0; ri < 4; ri++)
+#pragma unroll
+                    for (int cj = 0; cj < 4; cj++) {
+                        const int m = 4 * ri + cj;
+                        pdq[ri] = fmaf(y4[cj], Fb[m], pdq[ri]);
+                        float gP = fmaf(q4[ri], y4[cj], dF[m]);
+                        gP = fabsf(Fb[m]) < cap ? gP : 0.0f;
+                        pal[ri] = fmaf(gP, Fa[m], pal[ri]);
+                        float du = gP;
+                        if (MOM) {
+                            du = gP + dS[m];
+                            dS[m] = M * du;
+                        }
+                        psv[ri] = fmaf(du, v4[cj], psv[ri]);
+                        psr[ri] = fmaf(du, rt[s][cj], psr[ri]);
+                        cdr[cj] = fmaf(-du, x4[ri], cdr[cj]);
+                        cdv[cj] = fmaf(du, k4[ri], cdv[cj]);
+                        dF[m] = a4[ri] * gP;
+                    }
+#pragma unroll
+                for (int cj = 0; cj < 4; cj++) {
+                    cdr[cj] = sum16(cdr[cj]);
+                    cdv[cj] = sum16(cdv[cj]);
+                }
+#pragma unroll
+                for (int ri = 0; ri < 4; ri++)
+#pragma unroll
+                    for (int cj = 0; cj < 4; cj++) {
+                        const int m = 4 * ri + cj;
+                        pde[ri] = fmaf(cdr[cj], Fa[m], pde[ri]);
+                        dF[m] = fmaf(e4[ri], cdr[cj], dF[m]);
+                    }
+#pragma unroll
+                for (int ri = 0; ri < 4; ri++) {
+                    pdq[ri] = sum_cols(pdq[ri]);
+                    pal[ri] = sum_cols(pal[ri]);
+                    psv[ri] = sum_cols(psv[ri]);
+                    psr[ri] = sum_cols(psr[ri]);
+                    pde[ri] = sum_cols(pde[ri]);
+                }
+                if ((lane >> 4) == 0) {
+                    *reinterpret_cast<f32x4 *>(&red[s][wave][0][i0]) = f32x4{pdq[0], pdq[1], pdq[2], pdq[3]};
+                    *reinterpret_cast<f32x4 *>(&red[s][wave][1][i0]) = f32x4{pal[0], pal[1], pal[2], pal[3]};
+                    *reinterpret_cast<f32x4 *>(&red[s][wave][2][i0]) = f32x4{psv[0], psv[1], psv[2], psv[3]};
+                    *reinterpret_cast<f32x4 *>(&red[s][wave][3][i0]) = f32x4{psr[0], psr[1], psr[2], psr[3]};
+                    *reinterpret_cast<f32x4 *>(&red[s][wave][4][i0]) = f32x4{pde[0], pde[1], pde[2], pde[3]};
+                }
+                if ((lane & 15) == 0)
+                    *reinterpret_cast<f32x4 *>(p.dv + hb + (size_t)(t0 + s) * HS + j0) =
+                        f32x4{cdv[0], cdv[1], cdv[2], cdv[3]};
+            }
+        }
+        __syncthreads();
+        // the rows' gradients: thread -> (step st, row cc), the four waves' partials added
+        if (st < n) {
+            const int t = t0 + st;
+            float x[5];
+#pragma unroll
+            for (int z = 0; z < 5; z++) x[z] = ((red[st][0][z][cc] + red[st][1][z][cc]) + red[st][2][z][cc]) + red[st][3][z][cc];
+            const float a = sg.a[st][cc], b = sg.b[st][cc], k = sg.k[st][cc], e = sg.e[st][cc];
+            const size_t o = hb + (size_t)t * HS + cc;
+            p.dq[o] = x[0];
+            p.dk[o] = b * x[2];
+            p.de[o] = fmaf(-(a * b), x[3], x[4]);
+            const float dal = fmaf(-(b * e), x[3], x[1]);
+            const float dbr = fmaf(-(a * e), x[3], k * x[2]);
+            if (G1) {
+                const float sa = ava::wave_sum(dal * a), sb = ava::wave_sum(dbr);
+                if (cc == 0) {
+                    p.dla[gb + t] = sa;
+                    p.db[gb + t] = sb;
+                }
+            } else {
+                p.dla[o] = dal * a;
+                p.db[o] = dbr;
+            }
+        }
+    }
+    {
+        const size_t o0 = (size_t)bh * HS * HS;
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            const size_t o = o0 + (size_t)(i0 + (m >> 2)) * HS + j0 + (m & 3);
+            if (p.dF0) p.dF0[o] = dF[m];
+            if (MOM && p.dS0) p.dS0[o] = dS[m];
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" size_t ava_mem_scan_bwd_workspace(int BH, int T, int momentum) {
+    if (BH <= 0 || T <= 0) return 0;
+    return (size_t)BH * ((T + CK - 1) / CK) * (momentum ? 2 : 1) * HS * HS * sizeof(float);
+}
+
+// The backward of ava_mem_scan (same layout and gates), from the initial state F0, S0 (nullable:
+// zeros) and the gradients dy of y and dF_T, dS_T of the final state (nullable: zeros): dq, dk, de,
+// dv [BH][T][hs]; dla, db [BH][T][g]; dF0, dS0 (nullable) the gradients of the initial state.
+extern "C" int ava_mem_scan_bwd(const float *q, const float *k, const float *e, const float *v, const float *la,
+                                const float *b, int BH, int T, int hs, int g, float m, float cap, const float *F0,
+                                const float *S0, const float *dy, const float *dF_T, const float *dS_T, float *dq,
+                                float *dk, float *de, float *dv, float *dla, float *db, float *dF0, float *dS0,
+                                void *work, size_t work_bytes, ava_stream stream) {
+    AVA_REQUIRE(hs == HS, AVA_ERR_UNSUPPORTED, "mem_scan_bwd: head size %d (this build runs 64)", hs);
+    AVA_REQUIRE(g == 1 || g == HS, AVA_ERR_SHAPE, "mem_scan_bwd: g=%d (1 or hs)", g);
+    AVA_REQUIRE(BH > 0 && T > 0, AVA_ERR_SHAPE, "mem_scan_bwd: BH=%d T=%d", BH, T);
+    AVA_REQUIRE(q && k && e && v && la && b && dy && dq && dk && de && dv && dla && db && work, AVA_ERR_ARG,
+                "mem_scan_bwd: NULL buffer");
+    const bool mom = m != 0.0f;
+    const size_t need = ava_mem_scan_bwd_workspace(BH, T, mom);
+    AVA_REQUIRE(work_bytes >= need, AVA_ERR_SHAPE, "mem_scan_bwd: workspace %zu < %zu bytes", work_bytes, need);
+    MemBwdArgs p{q, k, e, v, la, b, F0, mom ? S0 : nullptr, dy, dF_T, mom ? dS_T : nullptr, dq, dk, de, dv, dla, db,
+                 dF0, mom ? dS0 : nullptr, (float *)work, T, m, cap};
+    const hipStream_t st = (hipStream_t)stream;
+    if (g == 1) {
+        if (mom) mem_bwd_kernel<true, true><<<BH, 256, 0, st>>>(p);
+        else mem_bwd_kernel<true, false><<<BH, 256, 0, st>>>(p);
+    } else {
+        if (mom) mem_bwd_kernel<false, true><<<BH, 256, 0, st>>>(p);
+        else mem_bwd_kernel<false, false><<<BH, 256, 0, st>>>(p);
+    }
+    AVA_LAUNCHED("mem_scan_bwd");
+    return AVA_OK;
+}

@@ -12,6 +12,12 @@ status (the reference bail!s on shape, dtype and contiguity errors).
     mem_gen(q, k, e, v, la, b, m)   mem_gen.rs:127-137
     delta_rule_from(q, k, v, beta, la, f0)   model.rs:744-799 (chunked, per-head gates)
     attend(q, ks, vs, n0)        model/fstep.rs:303-329 (one head of 64, causal, over a store)
+
+The backward of the scans (the training step's kernels, gpu/lif.cu):
+    lif_gen_bwd(cur, ps, g_spk, ...)      lifg_bwd_* (lif.cu:3222-3290) / lif_ref's gradient (arch.rs:964-1071)
+    kwta_relu2_bwd(u, kth, ga)            relu2_bwd (lif.cu:4666-4679)
+    mem_gen_bwd(q, k, e, v, la, b, dy, m) memg_bwd* (lif.cu:3411-3888) / delta_rec's gradient (arch.rs:1091-1136)
+    dense_back(S, G, wf, base, ...)       dense_back (lif.cu:4922-4971)
 """
 from __future__ import annotations
 
@@ -177,6 +183,69 @@ def delta_rule_from(q, k, v, beta, la=None, f0=None):
     check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(la), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
           "ava_delta_chunk")
     return y, F
+
+
+def lif_gen_bwd(cur, ps, g_spk, init=None, g_vT=None, g_aT=None, levels=2, signed=True, alif=True, slope=1.0,
+                reset_grad=False):
+    """The LIF scan's backward from the initial state init (LifState; None: zeros), ps = beta | theta |
+    rho | gain [4D]. Returns dict dI [B, T, D], dv0, da0, dbeta, drho, dgain [B, D] (the parameter
+    gradients per stream: sum over dim 0)."""
+    _need(cur, torch.float32, "lif_gen_bwd cur")
+    _need(g_spk, torch.float32, "lif_gen_bwd g_spk")
+    B, T, D = cur.shape
+    dev = cur.device
+    z = torch.zeros((B, D), device=dev)
+    v0, s0, a0 = (z, z, z) if init is None else (init.v, init.s, init.a)
+    out = {n: torch.empty((B, D), device=dev) for n in ("dv0", "da0", "dbeta", "drho", "dgain")}
+    out["dI"] = torch.empty_like(cur)
+    check(lib().ava_lif_scan_bwd(_p(cur), B, T, D, _p(ps), _p(v0), _p(s0), _p(a0), levels, int(signed), int(alif),
+                                 float(slope), int(reset_grad), _p(g_spk), _p(g_vT), _p(g_aT), _p(out["dI"]),
+                                 _p(out["dv0"]), _p(out["da0"]), _p(out["dbeta"]), _p(out["drho"]),
+                                 _p(out["dgain"]), _stream()), "ava_lif_scan_bwd")
+    return out
+
+
+def kwta_relu2_bwd(u, kth, ga):
+    """gu = (u ga) 2 on the units kwta_relu kept (u - kth >= 0) with u > 0, else 0."""
+    _need(u, torch.float32, "kwta_relu2_bwd u")
+    _need(ga, torch.float32, "kwta_relu2_bwd ga")
+    n, h = u.shape
+    gu = torch.empty_like(u)
+    check(lib().ava_kwta_relu2_bwd(_p(u), _p(kth), n, h, _p(ga), _p(gu), _stream()), "ava_kwta_relu2_bwd")
+    return gu
+
+
+def mem_gen_bwd(q, k, e, v, la, b, dy, m=0.0, cap=1e5, F0=None, S0=None, dF_T=None, dS_T=None):
+    """The backward of mem_gen from the initial state (F0, S0; None: zeros) with dL/dy = dy and the
+    final state's gradients (None: zeros). Returns dict dq, dk, de, dv, dla, db, dF0, dS0."""
+    for t, nm in ((q, "q"), (k, "k"), (e, "e"), (v, "v"), (la, "la"), (b, "b"), (dy, "dy")):
+        _need(t, torch.float32, f"mem_gen_bwd {nm}")
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    o = {n: torch.empty_like(q) for n in ("dq", "dk", "de", "dv")}
+    o.update({n: torch.empty_like(la) for n in ("dla", "db")})
+    o["dF0"] = torch.empty((BH, hs, hs), device=q.device)
+    o["dS0"] = torch.zeros((BH, hs, hs), device=q.device)
+    nbytes = lib().ava_mem_scan_bwd_workspace(BH, T, int(m != 0.0))
+    work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    check(lib().ava_mem_scan_bwd(_p(q), _p(k), _p(e), _p(v), _p(la), _p(b), BH, T, hs, g, float(m), float(cap),
+                                 _p(F0), _p(S0), _p(dy), _p(dF_T), _p(dS_T), _p(o["dq"]), _p(o["dk"]), _p(o["de"]),
+                                 _p(o["dv"]), _p(o["dla"]), _p(o["db"]), _p(o["dF0"]), _p(o["dS0"]), _p(work),
+                                 nbytes, _stream()), "ava_mem_scan_bwd")
+    return o
+
+
+def dense_back(S, G, wf, base, col, i0, L, nd):
+    """The dense mix's backward: S [R, M] streams, G [L, M] = dL/d(mix after block k), wf packed weights.
+    Returns (out [M], dw [nd])."""
+    M = base.numel()
+    out = torch.empty_like(base)
+    dw = torch.empty(max(nd, 1), device=base.device)
+    nf = lib().ava_dense_back_part_floats(M, nd)
+    part = torch.empty(max(nf, 1), device=base.device)
+    check(lib().ava_dense_back(_p(S), _p(G), _p(wf), _p(base), _p(out), _p(dw), col, i0, L, nd, M, _p(part), nf,
+                               _stream()), "ava_dense_back")
+    return out, dw[:nd]
 
 
 def attend(q: torch.Tensor, ks: torch.Tensor, vs: torch.Tensor, n0: int, heads: int = 1) -> torch.Tensor:

@@ -100,6 +100,7 @@ class Lif:
     def cpu_baseline(self):
         from oracle import oracle as O
 
+        O.set_threads(1)  # the reference's CPU scan is one loop on one thread (lif_gen.rs:198-212)
         B = 32
         rng = np.random.default_rng(1)
         cur = rng.standard_normal((B, self.T, self.D), dtype=np.float32)
@@ -150,6 +151,7 @@ class Kwta:
     def cpu_baseline(self):
         from oracle import oracle as O
 
+        O.set_threads(1)
         rows = 2048
         u = np.random.default_rng(2).standard_normal((rows, self.h)).astype(np.float32)
         t0 = time.perf_counter()
@@ -266,6 +268,7 @@ class Delta:
     def cpu_baseline(self):
         from oracle import oracle as O
 
+        O.set_threads(1)
         BH, T = 8, 4096
         rng = np.random.default_rng(5)
         q, k, v = (rng.standard_normal((BH, T, 64)).astype(np.float32) for _ in range(3))
@@ -393,6 +396,7 @@ class Stack:
 
         B, T = 2, 2048  # 4096 tokens: about 10-15 s of CPU work
         th = cpu_threads()
+        O.set_threads(th)
         om = O.OracleModel(self.cfg, self.params)
         ids = np.random.default_rng(4).integers(0, self.cfg["vocab"], (B, T)).astype(np.int32)
         t0 = time.perf_counter()
@@ -458,6 +462,7 @@ class Greedy:
 
         new = self.new  # the same generation: the prompt's pass and 128 greedy steps
         th = cpu_threads()
+        O.set_threads(th)
         om = O.OracleModel(self.cfg, self.params)
         t0 = time.perf_counter()
         st = om.new_state(1, eng_cap=self.prompt_len + new)

@@ -149,6 +149,53 @@ int ava_mem_scan(const float *q, const float *k, const float *e, const float *v,
 int ava_delta_chunk(const float *q, const float *k, const float *v, const float *la, const float *beta, int BH,
                     int T, int hs, float *F, float *y, ava_stream stream);
 
+/* ------------------------------------------------------------------ backward (training step) */
+
+/* The LIF scan's backward: the surrogate gradient of the straight-through spikes (ds/dv per spike edge
+ * x = v - k th, -v - k th: 1 / (1 + slope |x|)^2). Inputs as ava_lif_scan's, with the INITIAL state
+ * v0, s0, a0 [B][D] (unchanged); g_spk [B][T][D] = dL/d(spikes), g_vT, g_aT [B][D] = dL/d(final v, a)
+ * (nullable: 0). reset_grad: the reset v -= s th_{t-1} carries gradient too, its carry capped at
+ * 2 beta / (ds/dv) where th ds/dv > 2 beta (the reference's negative slope / rgi = 1). Outputs dI
+ * [B][T][D] = dL/dcur, dv0, da0 [B][D], and per (b, c) the shares of dbeta, drho, dgain [B][D] (the
+ * parameter gradients are their sums over b; theta is detached). da0, drho, dgain may be NULL without
+ * alif. Replaces lifg_bwd_* (gpu/lif.cu:3222-3290, LifGenBwd, gpu/lif_gen.rs:239-361) and the
+ * gradient of lif_ref (gpu/arch.rs:964-1071). */
+int ava_lif_scan_bwd(const float *cur, int B, int T, int D, const float *ps, const float *v0, const float *s0,
+                     const float *a0, int levels, int is_signed, int alif, float slope, int reset_grad,
+                     const float *g_spk, const float *g_vT, const float *g_aT, float *dI, float *dv0, float *da0,
+                     float *dbeta, float *drho, float *dgain, ava_stream stream);
+
+/* The backward of relu² after kWTA: gu = (u ga) 2 where u - kth >= 0 and u > 0, else 0, for u [n][h]
+ * and the row thresholds kth [n] that ava_kwta returned (h a multiple of 4). Replaces relu2_bwd
+ * (gpu/lif.cu:4666-4679), whose input a = kwta_relu(u) is u on the kept units. */
+int ava_kwta_relu2_bwd(const float *u, const float *kth, int n, int h, const float *ga, float *gu,
+                       ava_stream stream);
+
+/* The backward of ava_mem_scan (same layout and gates; hs == 64) from the initial state F0, S0
+ * (nullable: zeros) with dy [BH][T][hs] = dL/dy and dF_T, dS_T = dL/d(final F, S) (nullable: zeros):
+ * dq, dk, de, dv [BH][T][hs]; dla, db [BH][T][g]; dF0, dS0 [BH][hs][hs] (nullable) = dL/d(F0, S0).
+ * The bound clamp(., +-cap) passes no gradient where it holds. work: device memory of
+ * ava_mem_scan_bwd_workspace(BH, T, m != 0) bytes (the states the replay keeps). Replaces memg_bwd_* /
+ * memg_bwd4_* (gpu/lif.cu:3411-3888; MemGenBwd, gpu/mem_gen.rs:296-470) and the gradient of delta_rec
+ * (gpu/arch.rs:1091-1136). */
+size_t ava_mem_scan_bwd_workspace(int BH, int T, int momentum);
+int ava_mem_scan_bwd(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,
+                     int BH, int T, int hs, int g, float m, float cap, const float *F0, const float *S0,
+                     const float *dy, const float *dF_T, const float *dS_T, float *dq, float *dk, float *de,
+                     float *dv, float *dla, float *db, float *dF0, float *dS0, void *work, size_t work_bytes,
+                     ava_stream stream);
+
+/* The dense (DenseFormer) mix's backward over S [R][M] (the streams: 0 the embedding, j + 1 block j's
+ * raw output) and G [L][M] (row k = dL/d(the mix after block k)); wf packs block k's k + 2 weights
+ * from k (k + 3) / 2. out [M] = base + sum_{k = i0 .. L-1} w_k[col] G_k (added in k order);
+ * dw [nd] = sum_e base_e S_j,e. Block i: base = G_i, col = i + 1, i0 = i, nd = i + 2 gives dL/draw_i
+ * and dL/dw_i; the embedding: col 0, i0 0, nd 0. part: ava_dense_back_part_floats(M, nd) floats of
+ * device scratch (NULL with nd == 0). M a multiple of 4, nd <= 32. Replaces dense_back
+ * (gpu/lif.cu:4922-4971). */
+size_t ava_dense_back_part_floats(long long M, int nd);
+int ava_dense_back(const float *S, const float *G, const float *wf, const float *base, float *out, float *dw, int col,
+                   int i0, int L, int nd, long long M, float *part, size_t part_floats, ava_stream stream);
+
 /* ------------------------------------------------------------------ engram read */
 
 /* The engram's causal single-head read (head size 64) over a store that already holds entries

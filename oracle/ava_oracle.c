@@ -20,6 +20,17 @@
 
 #define NORM_EPS 1e-5f /* gpu/model.rs:36 */
 
+/* The thread count of the oracle's parallel loops (OpenMP's default: OMP_NUM_THREADS, else every
+ * CPU). Every parallel loop splits independent units (rows, channels, heads), so any count gives the
+ * same bits. */
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n < 1 ? 1 : n);
+#else
+    (void)n;
+#endif
+}
+
 /* ------------------------------------------------------------------ scalar helpers */
 
 /* candle's sigmoid as gpu/model.rs:465-467 builds it: (exp(-x)·1 + 1)^-1 (gpu/model/fstep.rs:260-262). */
@@ -803,4 +814,265 @@ double orc_cb_learn(const float *logits, int V, int next, const float *E, int d,
     free(p);
     free(delta);
     return ce;
+}
+
+/* ------------------------------------------------------------------ backward (training) */
+
+/* The surrogate derivative of one spike edge, 1 / (1 + S |x|)^2 (the slope of the fast sigmoid
+ * x / (1 + S |x|) that lif_ref's straight-through spikes carry, gpu/arch.rs:953-956). */
+static float sur(float x, float slope) {
+    const float a = 1.0f + slope * fabsf(x);
+    return 1.0f / (a * a);
+}
+
+/* d s / d v and d s / d theta_t of a step's surrogate spike (the soft sum of gpu/arch.rs:1006-1034). */
+static void dspike(float v, float th, int levels, int is_signed, float slope, float *dv, float *dth) {
+    if (!is_signed) {
+        const float g = sur(v - th, slope);
+        *dv = g;
+        *dth = -g;
+        return;
+    }
+    float a = 0.0f, b = 0.0f;
+    for (int k = 1; k <= levels; k++) {
+        const float kth = th * (float)k;
+        const float gu = sur(v - kth, slope), gd = sur(-v - kth, slope);
+        a += gu + gd;
+        b += (float)k * (gd - gu);
+    }
+    *dv = a;
+    *dth = b;
+}
+
+/* The backward of the LIF scan (the gradient lif_ref's autograd gives, gpu/arch.rs:964-1071; the CUDA
+ * form lifg_bwd, gpu/lif.cu:3228-3290). Per (b, c): the forward is replayed from (v0, s0, a0) keeping
+ * v_t and a_t, then walked back: G_t = dL/dv_t = gs_t ds_t/dv_t + beta G_{t+1} (G_T's carry = g_vT);
+ * dbeta += G_t v_{t-1}. With ALIF: dL/dth_t = gs_t ds_t/dth_t, da_t = dth_t gain + rho da_{t+1},
+ * dgain += dth_t a_t, drho += da_t (a_{t-1} - |s_{t-1}|) (the trace's spikes detached). With reset_grad
+ * the reset v_{t+1} -= s_t th_t also carries gradient: gs_t -= te_t G_{t+1} with te_t = th_t, or
+ * 2 beta / (ds/dv) where th_t ds/dv > 2 beta; dL/dth_t -= s_t G_{t+1} (and the first step's reset with
+ * th_{-1} = theta + a0 gain). Outputs: dI [B][T][D], dv0, da0 and this row's shares of dbeta, drho and
+ * dgain ([B][D] each; the caller sums over b). g_aT nullable (0). */
+void orc_lif_bwd(const float *cur, int B, int T, int D, const float *ps, const float *v0, const float *s0,
+                 const float *a0, int levels, int is_signed, int alif, float slope, int reset_grad, const float *g_spk,
+                 const float *g_vT, const float *g_aT, float *dI, float *dv0, float *da0, float *dbeta, float *drho,
+                 float *dgain) {
+#pragma omp parallel
+    {
+        float *vs = (float *)malloc(sizeof(float) * (size_t)T);
+        float *as = (float *)malloc(sizeof(float) * (size_t)T);
+        float *ss = (float *)malloc(sizeof(float) * (size_t)T);
+#pragma omp for schedule(static)
+        for (long i_ = 0; i_ < (long)B * D; i_++) {
+            const int bi = (int)(i_ / D), c = (int)(i_ % D);
+            const int i = bi * D + c;
+            const float bt = ps[c], th0 = ps[D + c], rho = ps[2 * D + c], gain = ps[3 * D + c];
+            const float omr = 1.0f - rho;
+            float vv = v0[i], sp = s0[i], aa = a0[i];
+            float thp = alif ? th0 + aa * gain : th0;
+            for (int t = 0; t < T; t++) {
+                float tht = th0;
+                if (alif) {
+                    aa = aa * rho + fabsf(sp) * omr;
+                    tht = th0 + aa * gain;
+                }
+                vv = (vv * bt + cur[((size_t)bi * T + t) * D + c]) - sp * thp;
+                sp = spike_of(vv, tht, levels, is_signed);
+                thp = tht;
+                vs[t] = vv;
+                as[t] = aa;
+                ss[t] = sp;
+            }
+            float cv = g_vT ? g_vT[i] : 0.0f, ca = (alif && g_aT) ? g_aT[i] : 0.0f;
+            float gb = 0.0f, gr = 0.0f, gg = 0.0f, Gn = 0.0f; /* Gn = G_{t+1} */
+            for (int t = T - 1; t >= 0; t--) {
+                const float vt = vs[t], at = alif ? as[t] : 0.0f;
+                const float tht = alif ? th0 + at * gain : th0;
+                float dv, dth;
+                dspike(vt, tht, levels, is_signed, slope, &dv, &dth);
+                float gs = g_spk[((size_t)bi * T + t) * D + c];
+                if (reset_grad) {
+                    const float q = tht * dv, cap = 2.0f * bt;
+                    gs -= (q > cap ? cap / dv : tht) * Gn;
+                }
+                const float G = gs * dv + cv;
+                gb += G * (t > 0 ? vs[t - 1] : v0[i]);
+                if (alif) {
+                    float gth = gs * dth;
+                    if (reset_grad) gth -= ss[t] * Gn;
+                    const float ga = gth * gain + ca;
+                    gg += gth * at;
+                    const float ap = t > 0 ? as[t - 1] : a0[i];
+                    const float sprev = t > 0 ? ss[t - 1] : s0[i];
+                    gr += ga * (ap - fabsf(sprev));
+                    ca = rho * ga;
+                }
+                dI[((size_t)bi * T + t) * D + c] = G;
+                Gn = G;
+                cv = bt * G;
+            }
+            if (alif && reset_grad) {
+                const float g0 = -s0[i] * Gn; /* the first step's reset threshold theta + a0 gain */
+                gg += g0 * a0[i];
+                ca += g0 * gain;
+            }
+            dv0[i] = cv;
+            da0[i] = ca;
+            dbeta[i] = gb;
+            drho[i] = alif ? gr : 0.0f;
+            dgain[i] = alif ? gg : 0.0f;
+        }
+        free(vs);
+        free(as);
+        free(ss);
+    }
+}
+
+/* The backward of the fast-weight recurrence (orc_mem_rec; gpu/arch.rs:1091-1136 delta_rec's autograd,
+ * the CUDA forms memg_bwd / memg_bwd4, gpu/lif.cu:3413-3890), in float64 over float32 inputs. Per head,
+ * the forward is replayed keeping F_{t-1} and S_{t-1}; then from t = T-1 down, with F' = clamp(P) and
+ * P = alpha F + S' (or + u without momentum), S' = M S + u, u_ij = b_i k_i v_j - alpha_i b_i e_i r_j,
+ * r = F^T e, y = F'^T q:
+ *   dq_i = sum_j dy_j F'_ij;  dF' += q dy^T;  gP = dF' where |P| < cap (else 0);
+ *   dalpha_i += sum_j gP_ij F_ij;  dF = alpha gP (+ e dr^T below);  du = gP + dS' (momentum) ;  dS = M du;
+ *   db_i += sum_j du_ij (k_i v_j - alpha_i e_i r_j); dk_i += b_i sum_j du_ij v_j; dv_j += sum_i du_ij b_i k_i;
+ *   dalpha_i -= b_i e_i sum_j du_ij r_j; de_i -= alpha_i b_i sum_j du_ij r_j; dr_j = -sum_i du_ij alpha_i b_i e_i;
+ *   de_i += sum_j dr_j F_ij;  dF += e dr^T;  dla = dalpha alpha.
+ * With g = 1 (one gate per head) dla and db are the sums over the head's rows. dF_T, dS_T: the carried
+ * gradients at the end (nullable: 0); dF0, dS0 out (dS0 only with momentum; nullable). */
+void orc_mem_rec_bwd(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,
+                     int BH, int T, int hs, int g, float m, float cap, const float *F0, const float *S0, const float *dy,
+                     const float *dF_T, const float *dS_T, float *dq, float *dk, float *de, float *dv, float *dla,
+                     float *db, float *dF0, float *dS0) {
+#pragma omp parallel
+    {
+        const size_t hh = (size_t)hs * hs;
+        double *Fs = (double *)malloc(sizeof(double) * hh * (size_t)(T + 1));
+        double *Ss = (double *)malloc(sizeof(double) * hh * (size_t)(T + 1));
+        double *r = (double *)malloc(sizeof(double) * (size_t)hs);
+        double *dF = (double *)malloc(sizeof(double) * hh), *dS = (double *)malloc(sizeof(double) * hh);
+        double *du = (double *)malloc(sizeof(double) * hh), *dr = (double *)malloc(sizeof(double) * (size_t)hs);
+        double *al = (double *)malloc(sizeof(double) * (size_t)hs), *bb = (double *)malloc(sizeof(double) * (size_t)hs);
+        double *dal = (double *)malloc(sizeof(double) * (size_t)hs), *dbb = (double *)malloc(sizeof(double) * (size_t)hs);
+#pragma omp for schedule(dynamic)
+        for (int bh = 0; bh < BH; bh++) {
+            for (size_t z = 0; z < hh; z++) {
+                Fs[z] = F0 ? F0[(size_t)bh * hh + z] : 0.0;
+                Ss[z] = (m != 0.0f && S0) ? S0[(size_t)bh * hh + z] : 0.0;
+            }
+            for (int t = 0; t < T; t++) { /* F_t, S_t into slot t + 1 */
+                const size_t o = ((size_t)bh * T + t) * hs, og = ((size_t)bh * T + t) * g;
+                const double *F = Fs + hh * t, *S = Ss + hh * t;
+                double *Fn = Fs + hh * (t + 1), *Sn = Ss + hh * (t + 1);
+                for (int j = 0; j < hs; j++) {
+                    double a = 0.0;
+                    for (int i = 0; i < hs; i++) a += (double)e[o + i] * F[i * hs + j];
+                    r[j] = a;
+                }
+                for (int i = 0; i < hs; i++) {
+                    const double a = exp((double)la[og + (g > 1 ? i : 0)]), bi = b[og + (g > 1 ? i : 0)];
+                    for (int j = 0; j < hs; j++) {
+                        const double u = bi * k[o + i] * v[o + j] - a * bi * e[o + i] * r[j];
+                        const int p = i * hs + j;
+                        double P;
+                        if (m != 0.0f) {
+                            Sn[p] = m * S[p] + u;
+                            P = a * F[p] + Sn[p];
+                        } else {
+                            Sn[p] = 0.0;
+                            P = a * F[p] + u;
+                        }
+                        Fn[p] = P < -cap ? -cap : (P > cap ? cap : P);
+                    }
+                }
+            }
+            for (size_t z = 0; z < hh; z++) {
+                dF[z] = dF_T ? dF_T[(size_t)bh * hh + z] : 0.0;
+                dS[z] = (m != 0.0f && dS_T) ? dS_T[(size_t)bh * hh + z] : 0.0;
+            }
+            for (int i = 0; i < hs; i++) {
+                dal[i] = 0.0;
+                dbb[i] = 0.0;
+            }
+            for (int t = T - 1; t >= 0; t--) {
+                const size_t o = ((size_t)bh * T + t) * hs, og = ((size_t)bh * T + t) * g;
+                const double *F = Fs + hh * t, *S = Ss + hh * t, *Fn = Fs + hh * (t + 1);
+                for (int i = 0; i < hs; i++) {
+                    al[i] = exp((double)la[og + (g > 1 ? i : 0)]);
+                    bb[i] = b[og + (g > 1 ? i : 0)];
+                }
+                for (int j = 0; j < hs; j++) {
+                    double a = 0.0;
+                    for (int i = 0; i < hs; i++) a += (double)e[o + i] * F[i * hs + j];
+                    r[j] = a;
+                }
+                for (int i = 0; i < hs; i++) {
+                    double a = 0.0;
+                    for (int j = 0; j < hs; j++) a += (double)dy[o + j] * Fn[i * hs + j];
+                    dq[o + i] = (float)a;
+                }
+                /* gP, dalpha from alpha F, du, dS */
+                for (int i = 0; i < hs; i++)
+                    for (int j = 0; j < hs; j++) {
+                        const int p = i * hs + j;
+                        const double u = bb[i] * k[o + i] * v[o + j] - al[i] * bb[i] * e[o + i] * r[j];
+                        const double P = al[i] * F[p] + (m != 0.0f ? m * S[p] + u : u);
+                        const double gP = (dF[p] + (double)q[o + i] * dy[o + j]) * ((P > -cap && P < cap) ? 1.0 : 0.0);
+                        dal[i] += gP * F[p];
+                        du[p] = gP + (m != 0.0f ? dS[p] : 0.0);
+                        dF[p] = al[i] * gP;
+                        dS[p] = m * du[p];
+                    }
+                for (int j = 0; j < hs; j++) dr[j] = 0.0;
+                for (int i = 0; i < hs; i++) {
+                    double sdv = 0.0, sdr = 0.0, sdkv = 0.0;
+                    for (int j = 0; j < hs; j++) {
+                        const double d = du[i * hs + j];
+                        sdv += d * v[o + j];
+                        sdr += d * r[j];
+                        dr[j] -= d * al[i] * bb[i] * e[o + i];
+                    }
+                    dbb[i] += k[o + i] * sdv - al[i] * e[o + i] * sdr;
+                    sdkv = bb[i] * sdv;
+                    dk[o + i] = (float)sdkv;
+                    dal[i] -= bb[i] * e[o + i] * sdr;
+                    de[o + i] = (float)(-al[i] * bb[i] * sdr);
+                }
+                for (int j = 0; j < hs; j++) {
+                    double a = 0.0;
+                    for (int i = 0; i < hs; i++) a += du[i * hs + j] * bb[i] * k[o + i];
+                    dv[o + j] = (float)a;
+                }
+                for (int i = 0; i < hs; i++) {
+                    double a = 0.0;
+                    for (int j = 0; j < hs; j++) a += dr[j] * F[i * hs + j];
+                    de[o + i] = (float)(de[o + i] + a);
+                    for (int j = 0; j < hs; j++) dF[i * hs + j] += (double)e[o + i] * dr[j];
+                }
+                if (g > 1) {
+                    for (int i = 0; i < hs; i++) {
+                        dla[og + i] = (float)(dal[i] * al[i]);
+                        db[og + i] = (float)dbb[i];
+                        dal[i] = 0.0;
+                        dbb[i] = 0.0;
+                    }
+                } else {
+                    double sa = 0.0, sb = 0.0;
+                    for (int i = 0; i < hs; i++) {
+                        sa += dal[i] * al[i];
+                        sb += dbb[i];
+                        dal[i] = 0.0;
+                        dbb[i] = 0.0;
+                    }
+                    dla[og] = (float)sa;
+                    db[og] = (float)sb;
+                }
+            }
+            if (dF0)
+                for (size_t z = 0; z < hh; z++) dF0[(size_t)bh * hh + z] = (float)dF[z];
+            if (dS0 && m != 0.0f)
+                for (size_t z = 0; z < hh; z++) dS0[(size_t)bh * hh + z] = (float)dS[z];
+        }
+        free(Fs); free(Ss); free(r); free(dF); free(dS); free(du); free(dr); free(al); free(bb); free(dal); free(dbb);
+    }
 }

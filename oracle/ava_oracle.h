@@ -185,6 +185,22 @@ void orc_cb_apply(const float *xf, const float *c, int g, int d, const float *w,
 double orc_cb_learn(const float *logits, int V, int next, const float *E, int d, const float *c, int g, float lr,
                     double half, double *scale, float *tab);
 
+/* The thread count of the parallel loops (same bits at any count). */
+void orc_set_threads(int n);
+
+/* ---------------------------------------------------------------- backward (training) */
+
+/* The LIF scan's backward (lif_ref's surrogate gradient, gpu/arch.rs:964-1071; lifg_bwd, gpu/lif.cu:3228-3290). */
+void orc_lif_bwd(const float *cur, int B, int T, int D, const float *ps, const float *v0, const float *s0,
+                 const float *a0, int levels, int is_signed, int alif, float slope, int reset_grad, const float *g_spk,
+                 const float *g_vT, const float *g_aT, float *dI, float *dv0, float *da0, float *dbeta, float *drho,
+                 float *dgain);
+/* The fast-weight recurrence's backward (delta_rec's autograd, gpu/arch.rs:1091-1136), float64 inside. */
+void orc_mem_rec_bwd(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,
+                     int BH, int T, int hs, int g, float m, float cap, const float *F0, const float *S0, const float *dy,
+                     const float *dF_T, const float *dS_T, float *dq, float *dk, float *de, float *dv, float *dla,
+                     float *db, float *dF0, float *dS0);
+
 /* The same building blocks exposed for tests. orc_round_half: IEEE binary16 round-to-nearest-even. */
 float orc_round_half(float x);
 void orc_rmsnorm(const float *x, int n, int d, const float *gain, float *out);

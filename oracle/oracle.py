@@ -58,11 +58,23 @@ def lib():
         L.orc_cb_learn.restype = C.c_double
         L.orc_cb_learn.argtypes = [f32p, C.c_int, C.c_int, f32p, C.c_int, f32p, C.c_int, C.c_float, C.c_double,
                                    C.POINTER(C.c_double), f32p]
+        L.orc_lif_bwd.argtypes = ([f32p, C.c_int, C.c_int, C.c_int, f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int,
+                                   C.c_float, C.c_int, f32p, C.c_void_p, C.c_void_p] + [f32p] * 6)
+        L.orc_mem_rec_bwd.argtypes = ([f32p] * 6 + [C.c_int] * 4 + [C.c_float, C.c_float] + [C.c_void_p] * 2 +
+                                      [f32p] + [C.c_void_p] * 2 + [f32p] * 6 + [C.c_void_p] * 2)
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_set_threads.restype = None
         L.orc_model_forward.restype = C.c_int
         L.orc_model_forward.argtypes = [C.POINTER(_Cfg), C.POINTER(_Model), C.c_void_p, C.c_int, C.c_int,
                                         C.POINTER(_State), C.c_void_p, C.c_int, C.c_int, C.POINTER(_Trace)]
         _lib = L
     return _lib
+
+
+def set_threads(n: int):
+    """The thread count of the oracle's parallel loops over rows, channels and heads (the same bits
+    at any count)."""
+    lib().orc_set_threads(int(n))
 
 
 def _c(a, dt):
@@ -191,6 +203,70 @@ def mem_rec_f64(q, k, e, v, la, b, m=0.0, F=None, S=None):
     lib().orc_mem_rec_f64(q, k, e, v, la, b, BH, T, hs, g, float(m), F,
                           S.ctypes.data if m != 0.0 else None, y)
     return y, F, S
+
+
+# --------------------------------------------------------------------------- backward (training)
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def lif_bwd(cur, ps, g_spk, v0=None, s0=None, a0=None, g_vT=None, g_aT=None, levels=2, signed=True, alif=True,
+            slope=1.0, reset_grad=False):
+    """The LIF scan's backward (orc_lif_bwd: gpu/arch.rs:964-1071 lif_ref's surrogate gradient,
+    gpu/lif.cu:3228-3290). Returns dict dI [B, T, D], dv0, da0, dbeta, drho, dgain [B, D]."""
+    cur, g_spk = _c(cur, np.float32), _c(g_spk, np.float32)
+    B, T, D = cur.shape
+    z = np.zeros((B, D), np.float32)
+    v0, s0, a0 = (z if x is None else _c(x, np.float32) for x in (v0, s0, a0))
+    g_vT = None if g_vT is None else _c(g_vT, np.float32)
+    g_aT = None if g_aT is None else _c(g_aT, np.float32)
+    out = {k: np.empty((B, D), np.float32) for k in ("dv0", "da0", "dbeta", "drho", "dgain")}
+    dI = np.empty((B, T, D), np.float32)
+    lib().orc_lif_bwd(cur, B, T, D, _c(ps, np.float32), v0, s0, a0, levels, int(signed), int(alif), float(slope),
+                      int(reset_grad), g_spk, _ptr(g_vT), _ptr(g_aT), dI, out["dv0"], out["da0"], out["dbeta"],
+                      out["drho"], out["dgain"])
+    out["dI"] = dI
+    return out
+
+
+def mem_rec_bwd(q, k, e, v, la, b, dy, m=0.0, cap=1e5, F0=None, S0=None, dF_T=None, dS_T=None):
+    """The fast-weight recurrence's backward (orc_mem_rec_bwd: delta_rec's gradient, gpu/arch.rs:1091-1136),
+    float64 inside. Returns dict dq, dk, de, dv [BH, T, hs], dla, db [BH, T, g], dF0, dS0 [BH, hs, hs]."""
+    q, k, e, v, la, b, dy = (_c(x, np.float32) for x in (q, k, e, v, la, b, dy))
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    F0, S0, dF_T, dS_T = (None if x is None else _c(x, np.float32) for x in (F0, S0, dF_T, dS_T))
+    o = {n: np.empty((BH, T, hs), np.float32) for n in ("dq", "dk", "de", "dv")}
+    o.update({n: np.empty((BH, T, g), np.float32) for n in ("dla", "db")})
+    o["dF0"] = np.empty((BH, hs, hs), np.float32)
+    o["dS0"] = np.zeros((BH, hs, hs), np.float32)
+    lib().orc_mem_rec_bwd(q, k, e, v, la, b, BH, T, hs, g, float(m), float(cap), _ptr(F0), _ptr(S0), dy, _ptr(dF_T),
+                          _ptr(dS_T), o["dq"], o["dk"], o["de"], o["dv"], o["dla"], o["db"], _ptr(o["dF0"]),
+                          _ptr(o["dS0"]))
+    return o
+
+
+def kwta_relu2_bwd(u, kth, ga):
+    """The backward of relu² after kWTA (gpu/lif.cu:4666-4679 relu2_bwd; the mask of gpu/lif.cu:4647):
+    gu = (u ga) 2 where u - kth >= 0 and u > 0, else 0; each product rounded alone, in f32."""
+    u, ga = _c(u, np.float32), _c(ga, np.float32)
+    kth = _c(kth, np.float32)[:, None]
+    keep = (u - kth >= 0) & (u > 0)
+    return np.where(keep, (u * ga).astype(np.float32) * np.float32(2), np.float32(0)).astype(np.float32)
+
+
+def dense_back(S, G, wf, base, col, i0, L, nd):
+    """The dense mix's backward (gpu/lif.cu:4922-4971 dense_back, the mix of gpu/arch.rs:1492-1500):
+    out = base + sum_{k=i0..L-1} w_k[col] G_k (added in k order, f32), dw[j] = sum_e base_e S_j,e
+    (float64 here). wf packs block k's k + 2 weights from k (k + 3) / 2."""
+    base = _c(base, np.float32)
+    out = base.copy()
+    for k in range(i0, L):
+        out = (out + np.float32(wf[k * (k + 3) // 2 + col]) * np.asarray(G[k], np.float32)).astype(np.float32)
+    dw = np.array([np.dot(base.astype(np.float64).ravel(), np.asarray(S[j], np.float64).ravel())
+                   for j in range(nd)], np.float64)
+    return out, dw
 
 
 def rmsnorm(x, gain):

@@ -175,3 +175,16 @@ def test_ctypes_structs_match_the_header():
              "ava_params": _lib.Params, "ava_state": _lib.State}
     for name, cls in pairs.items():
         assert fields(cls) == hs[name], name
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every entry point that ava_amd/_lib.py gives argtypes takes the header's number of parameters,
+    so a ctypes call can never shift its arguments."""
+    L = lib()
+    hf = header_functions()
+    wrong = {}
+    for name, n in hf.items():
+        fn = getattr(L, name)
+        if fn.argtypes is not None and len(fn.argtypes) != n:
+            wrong[name] = (len(fn.argtypes), n)
+    assert not wrong, wrong
