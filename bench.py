@@ -283,6 +283,155 @@ class Delta:
                                           f"{dt:.2f} s"}
 
 
+class LifBwd:
+    """The LIF scan's backward at config[1]'s shape: cur ~N(0,1) [64, 2048, 2048] and dL/dspikes ~N(0,1),
+    beta = sigmoid(U(1.5, 4.5)), theta 1, rho 0.95, gain 0.05; int2 spikes, ALIF, surrogate slope 4
+    (gpu/model.rs:39 LIF_SLOPE), the reset gradient on. Outputs dL/dcur [64, 2048, 2048] and the
+    per-stream state and parameter gradients."""
+
+    name = "lif_bwd"
+    kernel = "lif_bwd_kernel"
+
+    def __init__(self, B=64, T=2048, D=2048):
+        import torch
+        from ava_amd import _lib
+
+        self.B, self.T, self.D = B, T, D
+        self.L = _lib.lib()
+        g = torch.Generator(device="cuda").manual_seed(11)
+        self.cur = torch.randn((B, T, D), device="cuda", generator=g, dtype=torch.float32)
+        self.g = torch.randn((B, T, D), device="cuda", generator=g, dtype=torch.float32)
+        beta = torch.sigmoid(torch.rand(D, device="cuda", generator=g) * 3.0 + 1.5)
+        self.ps = torch.cat([beta, torch.ones(D, device="cuda"), torch.full((D,), 0.95, device="cuda"),
+                             torch.full((D,), 0.05, device="cuda")]).contiguous()
+        self.z = torch.zeros((B, D), device="cuda")
+        self.out = [torch.empty((B, D), device="cuda") for _ in range(5)]
+        self.dI = torch.empty_like(self.cur)
+        self.tokens = B * T
+        # algorithmic bytes: read cur and dL/dspikes, write dL/dcur; per (b, c) the initial state and the
+        # final-state gradients in, five gradients out; the parameter rows
+        self.bytes = B * T * D * 12 + B * D * 4 * (5 + 5) + 4 * D * 4
+        self.config = {"workload": "lif_scan backward config[1]", "B": B, "T": T, "C": D, "spikes": "int2",
+                       "alif": True, "slope": 4.0, "reset_grad": True}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        from ava_amd._lib import check
+        import ctypes as C
+
+        p = lambda t: C.c_void_p(t.data_ptr())
+        z = p(self.z)
+        if ev: ev[0].record()
+        check(self.L.ava_lif_scan_bwd(p(self.cur), self.B, self.T, self.D, p(self.ps), z, z, z, 2, 1, 1, 4.0, 1,
+                                      p(self.g), z, z, p(self.dI), *(p(o) for o in self.out), stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.bytes / kernel_s / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
+                "note": "algorithmic 12 B per element; the kernel reads the currents twice (16 B)"}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        O.set_threads(1)
+        B = 8
+        rng = np.random.default_rng(11)
+        cur = rng.standard_normal((B, self.T, self.D), dtype=np.float32)
+        g = rng.standard_normal((B, self.T, self.D), dtype=np.float32)
+        beta = (1.0 / (1.0 + np.exp(-rng.uniform(1.5, 4.5, self.D)))).astype(np.float32)
+        ps = np.concatenate([beta, np.ones(self.D), np.full(self.D, 0.95), np.full(self.D, 0.05)]).astype(np.float32)
+        t0 = time.perf_counter()
+        O.lif_bwd(cur, ps, g, levels=2, signed=True, alif=True, slope=4.0, reset_grad=True)
+        dt = time.perf_counter() - t0
+        return {"value": B * self.T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"oracle lif_bwd (lifg_bwd's recurrence, gpu/lif.cu:3228-3290, restated), B={B} of 64, "
+                          f"T={self.T}, C={self.D}, one thread, {dt:.2f} s"}
+
+
+class MemBwd:
+    """The fast-weight memory's backward at config[3]'s block shape: 64 streams x 16 heads of 64 over
+    T = 2048, per-channel gates, momentum 0.5; unit q, k, e, v ~N(0,1), alpha ~U(0.85, 0.999),
+    b ~U(0.1, 1.9), dL/dy ~N(0,1), from a zero state."""
+
+    name = "mem_bwd"
+    kernel = "mem_bwd_kernel"
+
+    def __init__(self, B=64, H=16, T=2048):
+        import torch
+        from ava_amd import _lib
+
+        BH = B * H
+        self.BH, self.T = BH, T
+        self.L = _lib.lib()
+        g = torch.Generator(device="cuda").manual_seed(12)
+
+        def unit():
+            x = torch.randn((BH, T, 64), device="cuda", generator=g)
+            return (x / x.norm(dim=2, keepdim=True)).contiguous()
+
+        self.q, self.k, self.e = unit(), unit(), unit()
+        self.v = torch.randn((BH, T, 64), device="cuda", generator=g)
+        self.la = torch.log(torch.rand((BH, T, 64), device="cuda", generator=g) * 0.149 + 0.85)
+        self.b = torch.rand((BH, T, 64), device="cuda", generator=g) * 1.8 + 0.1
+        self.dy = torch.randn((BH, T, 64), device="cuda", generator=g)
+        self.out = [torch.empty((BH, T, 64), device="cuda") for _ in range(6)]
+        self.dF0 = torch.empty((BH, 64, 64), device="cuda")
+        self.dS0 = torch.empty((BH, 64, 64), device="cuda")
+        self.work_bytes = self.L.ava_mem_scan_bwd_workspace(BH, T, 1)
+        self.work = torch.empty(self.work_bytes, dtype=torch.uint8, device="cuda")
+        self.tokens = B * T
+        # algorithmic bytes per (head, token): q, k, e, v, log alpha, b, dy in; dq, dk, de, dv, dla, db out
+        self.bytes = BH * T * 64 * 4 * 13
+        # FLOPs per (head, token, element): the step replayed (~9) and walked back (~21)
+        self.flops = BH * T * 64 * 64 * 30
+        self.config = {"workload": "memory backward config[3] block", "B": B, "heads": H, "T": T, "hs": 64,
+                       "gates": "per channel", "momentum": 0.5}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        from ava_amd._lib import check
+        import ctypes as C
+
+        p = lambda t: C.c_void_p(t.data_ptr())
+        if ev: ev[0].record()
+        check(self.L.ava_mem_scan_bwd(p(self.q), p(self.k), p(self.e), p(self.v), p(self.la), p(self.b), self.BH,
+                                      self.T, 64, 64, 0.5, 1e5, None, None, p(self.dy), None, None,
+                                      *(p(o) for o in self.out), p(self.dF0), p(self.dS0), p(self.work),
+                                      self.work_bytes, stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.bytes / kernel_s / 1e9
+        return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
+                "vector_tflops": self.flops / kernel_s / 1e12, "vector_peak_tflops": FP32_PEAK_TFLOPS,
+                "workspace_bytes": self.work_bytes,
+                "note": "a recurrence walked twice per head: latency-bound, not bandwidth-bound"}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        O.set_threads(1)
+        BH, T = 4, self.T
+        rng = np.random.default_rng(12)
+
+        def unit():
+            x = rng.standard_normal((BH, T, 64)).astype(np.float32)
+            return x / np.linalg.norm(x, axis=2, keepdims=True)
+
+        q, k, e = unit(), unit(), unit()
+        v = rng.standard_normal((BH, T, 64)).astype(np.float32)
+        la = np.log(rng.uniform(0.85, 0.999, (BH, T, 64))).astype(np.float32)
+        b = rng.uniform(0.1, 1.9, (BH, T, 64)).astype(np.float32)
+        dy = rng.standard_normal((BH, T, 64)).astype(np.float32)
+        t0 = time.perf_counter()
+        O.mem_rec_bwd(q, k, e, v, la, b, dy, m=0.5)
+        dt = time.perf_counter() - t0
+        return {"value": BH * T / dt / 16, "unit": "tokens/s (B x T per second, 16 heads per token)", "cores": 1,
+                "kind": "port", "sample": f"oracle memory backward (delta_rec's gradient, float64), {BH} of 1024 "
+                                          f"heads, T={T}, one thread, {dt:.2f} s"}
+
+
 class Copy:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the FETCH/WRITE_SIZE counters."""
 
@@ -653,7 +802,8 @@ class Decode:
         return None
 
 
-WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "greedy": Greedy, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy}
+WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "greedy": Greedy, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy,
+             "lif_bwd": LifBwd, "mem_bwd": MemBwd}
 DEFAULT = "stack"
 
 
