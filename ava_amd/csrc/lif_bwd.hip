@@ -6,8 +6,8 @@
 //      segment of K steps (segments are cut from the end, so only the first may be short). That
 //      state (v, s, a) is parked in the segment's own first three rows of dI, which the reverse
 //      pass overwrites last: no workspace and 12 bytes per segment of traffic.
-//   2. segment by segment from the last: the K steps replayed from the parked state with v_t, a_t
-//      and s_t in registers, then walked back. The next (earlier) segment's currents, incoming
+//   2. segment by segment from the last: the K steps replayed from the parked state with v_t and
+//      a_t in registers, then walked back. The next (earlier) segment's currents, incoming
 //      gradients and parked state are loaded while this one is processed.
 // HBM per element: the currents twice, the incoming gradient once and dI once, 16 bytes (a
 // backward that stores the membrane and trace instead moves 28).
@@ -70,7 +70,7 @@ struct LifBwdArgs {
 };
 
 template <int K, int LEVELS, bool SIGNED, bool ALIF>
-__global__ __launch_bounds__(256) void lif_bwd_kernel(LifBwdArgs p) {
+__global__ __launch_bounds__(256, 2) void lif_bwd_kernel(LifBwdArgs p) {
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
     const int D = p.D, T = p.T;
     if (gid >= p.B * D) return;
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void lif_bwd_kernel(LifBwdArgs p) {
             load_ck(q + 1, nkv, nks, nka);
         }
         const int t0 = seg0(q), n = T - q * K - t0;
-        float vs[K], as[K], ss[K];
+        float vs[K], as[K];
         {
             float v = ckv, sp = cks, a = cka, thp = ALIF ? th0 + cka * gain : th0;
 #pragma unroll
@@ -172,7 +172,6 @@ __global__ __launch_bounds__(256) void lif_bwd_kernel(LifBwdArgs p) {
                     thp = tht;
                     vs[i] = v;
                     as[i] = a;
-                    ss[i] = sp;
                 }
             }
         }
@@ -191,12 +190,13 @@ __global__ __launch_bounds__(256) void lif_bwd_kernel(LifBwdArgs p) {
                 const float G = gst * dv + cv;
                 gb += G * (i > 0 ? vs[i - 1] : ckv);
                 if (ALIF) {
+                    // the spikes are re-formed from the kept membranes and thresholds
                     float gth = gst * dth;
-                    if (p.rg) gth -= ss[i] * Gn;
+                    if (p.rg) gth -= spike_of<LEVELS, SIGNED>(vt, tht) * Gn;
                     const float gaa = gth * gain + ca;
                     gg += gth * at;
                     const float ap = i > 0 ? as[i - 1] : cka;
-                    const float sprev = i > 0 ? ss[i - 1] : cks;
+                    const float sprev = i > 0 ? spike_of<LEVELS, SIGNED>(vs[i - 1], th0 + as[i - 1] * gain) : cks;
                     gr += gaa * (ap - fabsf(sprev));
                     ca = rho * gaa;
                 }
@@ -226,7 +226,9 @@ __global__ __launch_bounds__(256) void lif_bwd_kernel(LifBwdArgs p) {
     if (p.dgain) p.dgain[gid] = ALIF ? gg : 0.0f;
 }
 
-constexpr int SEG = 16;  // steps per segment: 6 x 16 registers of currents, gradients and replayed state
+// Steps per segment: 5 x 16 registers of currents, gradients and replayed state. 32-step segments
+// (226 VGPRs, the same two waves per SIMD) measured 7% slower at config[1]'s shape.
+constexpr int SEG = 16;
 
 }  // namespace
 

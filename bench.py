@@ -335,7 +335,7 @@ class LifBwd:
         from oracle import oracle as O
 
         O.set_threads(1)
-        B = 8
+        B = self.B  # the whole workload: about 5 s on one thread
         rng = np.random.default_rng(11)
         cur = rng.standard_normal((B, self.T, self.D), dtype=np.float32)
         g = rng.standard_normal((B, self.T, self.D), dtype=np.float32)
@@ -345,7 +345,7 @@ class LifBwd:
         O.lif_bwd(cur, ps, g, levels=2, signed=True, alif=True, slope=4.0, reset_grad=True)
         dt = time.perf_counter() - t0
         return {"value": B * self.T / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-                "sample": f"oracle lif_bwd (lifg_bwd's recurrence, gpu/lif.cu:3228-3290, restated), B={B} of 64, "
+                "sample": f"oracle lif_bwd (lifg_bwd's recurrence, gpu/lif.cu:3228-3290, restated), B={B} of {self.B}, "
                           f"T={self.T}, C={self.D}, one thread, {dt:.2f} s"}
 
 
@@ -412,7 +412,7 @@ class MemBwd:
         from oracle import oracle as O
 
         O.set_threads(1)
-        BH, T = 4, self.T
+        BH, T = 256, self.T  # a quarter of the heads: about 12 s on one thread
         rng = np.random.default_rng(12)
 
         def unit():
@@ -428,7 +428,7 @@ class MemBwd:
         O.mem_rec_bwd(q, k, e, v, la, b, dy, m=0.5)
         dt = time.perf_counter() - t0
         return {"value": BH * T / dt / 16, "unit": "tokens/s (B x T per second, 16 heads per token)", "cores": 1,
-                "kind": "port", "sample": f"oracle memory backward (delta_rec's gradient, float64), {BH} of 1024 "
+                "kind": "port", "sample": f"oracle memory backward (delta_rec's gradient, float64), {BH} of {self.BH} "
                                           f"heads, T={T}, one thread, {dt:.2f} s"}
 
 
