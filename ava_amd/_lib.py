@@ -114,6 +114,8 @@ def lib():
     if hasattr(L, "ava_model_scratch_bytes"):
         L.ava_model_scratch_bytes.argtypes = [vp]
         L.ava_model_scratch_bytes.restype = sz
+    L.ava_model_nonfinite.argtypes = [vp, vp, C.POINTER(C.c_int), vp]
+    L.ava_model_nonfinite.restype = i32
     L.ava_model_set_trace.argtypes = [vp, vp, vp, vp, sz]
     L.ava_model_set_trace.restype = i32
     if hasattr(L, "ava_model_set_timing"):

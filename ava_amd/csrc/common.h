@@ -173,9 +173,13 @@ int mem_scan_strided(const float *q, const float *k, const float *e, const float
                      int B, int T, int nh, int ld, int g, int ldg, float m, float cap, float *F, float *S, float *y,
                      int ldy, hipStream_t st);
 
+// bad (nullable) [B]: set to 1 for a stream whose memory inputs held a non-finite value in some head;
+// that head's F and S are then left as they were.
 int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const float *ba, const float *bb,
               const float *off, const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out,
-              float m, float cap, float *F, float *S, float *y, hipStream_t st);
+              float m, float cap, float *F, float *S, float *y, int *bad, hipStream_t st);
+// x[0..n) = 0 with a kernel (a graph may hold it: no memset node).
+int zero_ints(int *x, int n, hipStream_t st);
 
 // glue.hip
 int embed(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, hipStream_t st);

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256, 2) void lif_bwd_kernel(LifBwdArgs p) {
     // segment q (0 = the last) covers [max(0, T - (q + 1) K), T - q K)
     auto seg0 = [&](int q) { return max(0, T - (q + 1) * K); };
 
-    float buf[K], nxt[K];
+    float buf[K] = {}, nxt[K] = {};  // (entries past a short segment are never read)
     auto load_cur = [&](int q, float (&dst)[K]) {
         const int t0 = seg0(q), n = T - q * K - t0;
 #pragma unroll
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void lif_bwd_kernel(LifBwdArgs p) {
     // 2. backwards, segment by segment
     float cv = p.gv ? p.gv[gid] : 0.0f, ca = (ALIF && p.ga) ? p.ga[gid] : 0.0f;
     float gb = 0.0f, gr = 0.0f, gg = 0.0f, Gn = 0.0f;  // Gn = dL/dv_{t+1}
-    float gbuf[K], gnxt[K];
+    float gbuf[K] = {}, gnxt[K] = {};
     auto load_g = [&](int q, float (&dst)[K]) {
         const int t0 = seg0(q), n = T - q * K - t0;
 #pragma unroll
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256, 2) void lif_bwd_kernel(LifBwdArgs p) {
             load_ck(q + 1, nkv, nks, nka);
         }
         const int t0 = seg0(q), n = T - q * K - t0;
-        float vs[K], as[K];
+        float vs[K] = {}, as[K] = {};
         {
             float v = ckv, sp = cks, a = cka, thp = ALIF ? th0 + cka * gain : th0;
 #pragma unroll

@@ -235,7 +235,15 @@ struct FusedArgs {
     int T, nh, r;
     float m, cap;
     float *F, *S, *y;  // F, S [B nh][64][64]; y [B T][d]
+    int *bad;          // [B] or NULL: streams that met a non-finite memory input
 };
+
+// The fused step's guard (gpu/model/fstep/arch.rs:780-783, 861-864): a non-finite gate, key, query or
+// value refuses the token before anything is committed. Here a head that stages one leaves its F and
+// S as they were (the scan keeps them in registers until the end) and marks its stream in bad.
+__device__ __forceinline__ bool finite6(float a, float b, float c, float d, float e, float f) {
+    return isfinite(a) && isfinite(b) && isfinite(c) && isfinite(d) && isfinite(e) && isfinite(f);
+}
 
 // The gates as the reference forms them, with the correctly rounded-to-an-ulp expf/logf and an IEEE
 // divide: a bias of a few ulp in alpha would move the fast weights by that bias over (1 - alpha), ~256x
@@ -290,6 +298,7 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
 
     // the raw inputs of this wave's 4 steps of a chunk, prefetched one chunk ahead
     float rq[4], rk[4], rv[4], rw[4], rv0[4], rz[4], rza[4], rzb[4];
+    int nf = 0;  // this lane staged a non-finite value
     auto load = [&](int t0) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -333,12 +342,14 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
             if (p.v0) v = v * p0 + rv0[s] * p1;
             const float a = gate_alpha(((rza[s] + bah) + offc) + lra[s]);
             const float bw = gate_sig((rzb[s] + bbh) + lrb[s]) * 2.0f;
+            const float bk = bw * kn, abe = (a * bw) * en;
+            if (t < p.T && !finite6(qn, en, v, a, bk, abe)) nf = 1;
             s_q[st][lane] = qn;
             s_e[st][lane] = en;
             s_v[st][lane] = v;
             s_a[st][lane] = a;
-            s_bk[st][lane] = bw * kn;
-            s_abe[st][lane] = (a * bw) * en;
+            s_bk[st][lane] = bk;
+            s_abe[st][lane] = abe;
         }
     };
 
@@ -369,6 +380,10 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
         }
     }
 
+    if (__syncthreads_or(nf)) {
+        if (tid == 0 && p.bad) p.bad[bi] = 1;
+        return;  // nothing committed
+    }
 #pragma unroll
     for (int m = 0; m < 16; m++) {
         const int o = (i0 + (m >> 1)) * HS + j0 + (m & 1);
@@ -403,6 +418,7 @@ __global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
     }
     const int c = hh * HS + lane;
     const float *Gr = p.G + row * ldg;
+    int nf = 0;
     {
         // the rank-r gate read-outs, a quarter of the rank per wave (fma chains in jj order)
         const int q = (p.r + 3) / 4, j0 = wave * q, j1 = min(p.r, j0 + q);
@@ -434,14 +450,17 @@ __global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
         }
         const float a = gate_alpha(((Gr[hh] + p.ba[hh]) + p.off[c]) + lra);
         const float bw = gate_sig((Gr[p.nh + hh] + p.bb[hh]) + lrb) * 2.0f;
+        const float bk = bw * kn, abe = (a * bw) * en;
+        nf = !finite6(qn, en, v, a, bk, abe);
         s_q[lane] = qn;
         s_e[lane] = en;
         s_v[lane] = v;
         s_a[lane] = a;
-        s_bk[lane] = bw * kn;
-        s_abe[lane] = (a * bw) * en;
+        s_bk[lane] = bk;
+        s_abe[lane] = abe;
     }
-    __syncthreads();
+    const bool refuse = __syncthreads_or(nf) != 0;  // every thread: a non-finite staged value
+    if (refuse && tid == 0 && p.bad) p.bad[bi] = 1;
     // r_j = sum_i e_i F_ij
     float r = 0.0f;
 #pragma unroll
@@ -465,8 +484,10 @@ __global__ __launch_bounds__(256) void mem_step_kernel(FusedArgs p) {
         f = __builtin_amdgcn_fmed3f(f, -cap, cap);
         Fr[m] = f;
         y = fmaf(s_q[i], f, y);
-        __builtin_nontemporal_store(f, Fh + i * HS + lane);
-        if (MOM) __builtin_nontemporal_store(Sr[m], Sh + i * HS + lane);
+        if (!refuse) {
+            __builtin_nontemporal_store(f, Fh + i * HS + lane);
+            if (MOM) __builtin_nontemporal_store(Sr[m], Sh + i * HS + lane);
+        }
     }
     __syncthreads();  // every wave has read s_part
     s_part[wave][lane] = y;
@@ -505,12 +526,12 @@ int mem_scan_strided(const float *q, const float *k, const float *e, const float
 // The block's memory from the raw projections P and gate projections G (see mem_fused_kernel).
 int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const float *ba, const float *bb,
               const float *off, const float *wa2, const float *wb2, const float *vres, const float *v0, float *v0_out,
-              float m, float cap, float *F, float *S, float *y, hipStream_t st) {
+              float m, float cap, float *F, float *S, float *y, int *bad, hipStream_t st) {
     AVA_REQUIRE(P && G && ba && bb && off && wa2 && wb2 && F && y, AVA_ERR_ARG, "mem_block: NULL buffer");
     AVA_REQUIRE(m == 0.0f || S, AVA_ERR_ARG, "mem_block: momentum needs S");
     AVA_REQUIRE(B > 0 && T > 0 && nh > 0 && r > 0 && r <= 32, AVA_ERR_SHAPE, "mem_block: B=%d T=%d nh=%d r=%d", B, T,
                 nh, r);
-    FusedArgs a{P, G, ba, bb, off, wa2, wb2, vres, v0, v0_out, T, nh, r, m, cap, F, S, y};
+    FusedArgs a{P, G, ba, bb, off, wa2, wb2, vres, v0, v0_out, T, nh, r, m, cap, F, S, y, bad};
     if (T == 1) {
         if (m != 0.0f) mem_step_kernel<true><<<B * nh, 256, 0, st>>>(a);
         else mem_step_kernel<false><<<B * nh, 256, 0, st>>>(a);
@@ -521,6 +542,18 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
     if (m != 0.0f) mem_fused_kernel<true, false><<<B * nh, 256, 0, st>>>(a);
     else mem_fused_kernel<false, false><<<B * nh, 256, 0, st>>>(a);
     AVA_LAUNCHED("mem_block");
+    return AVA_OK;
+}
+
+__global__ void zero_ints_kernel(int *x, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = 0;
+}
+
+int zero_ints(int *x, int n, hipStream_t st) {
+    if (n <= 0) return AVA_OK;
+    zero_ints_kernel<<<ceil_div(n, 256), 256, 0, st>>>(x, n);
+    AVA_LAUNCHED("zero_ints");
     return AVA_OK;
 }
 

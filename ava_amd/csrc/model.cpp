@@ -77,6 +77,9 @@ struct ava_model {
     int8_t *xq = nullptr, *spk = nullptr;
     int32_t *xexp = nullptr;
     std::vector<float *> streams;
+    // [rows]: the last forward's streams that met a non-finite memory input (ava_model_nonfinite)
+    int *bad = nullptr;
+    int bad_n = 0;
 
     // the cerebellum head (cfg.cb_units > 0): the fixed wiring, the read-out (NULL: zero), the fade
     uint32_t *cb_idx = nullptr;
@@ -312,6 +315,7 @@ int ensure_scratch(ava_model *m, size_t rows) {
     A((void **)&m->xq, (size_t)c.planes * rows * ldq);
     A((void **)&m->xexp, rows * 4);
     A((void **)&m->spk, rows * ava::q8_ldk((int)d));
+    A((void **)&m->bad, rows * 4);
     if (c.dense) {
         m->streams.resize(c.layers + 1);
         for (auto &s : m->streams) A((void **)&s, rows * d * 4);
@@ -421,6 +425,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
     m->last_stream = st;
 
     const bool cb = logits && c.cb_units > 0 && s->cb_code;
+    AVA_RUN("zero_ints", ava::zero_ints(m->bad, B, st));
+    m->bad_n = B;
     // the embedding and the first block's norm planes in one pass; after each block the dense mix and
     // the next norm's planes in one pass (ready: the planes of the next norm are already in xq)
     AVA_RUN("embed", ava::embed_rms(ids, m->tok_emb, N, d, c.vocab, m->x, c.dense ? m->streams[0] : nullptr,
@@ -461,7 +467,7 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         AVA_RUN("mem_scan", ava::mem_block(m->P, m->G, B, T, nh, r, b.ba, b.bb, b.off, b.wa2, b.wb2,
                                            vr && i > 0 ? b.vres : nullptr, vr && i > 0 ? m->v0 : nullptr,
                                            vr && i == 0 ? m->v0 : nullptr, c.momentum, c.cap, s->mem_f + sm,
-                                           c.momentum != 0.0f ? s->mem_s + sm : nullptr, m->y, st));
+                                           c.momentum != 0.0f ? s->mem_s + sm : nullptr, m->y, m->bad, st));
         AVA_RUN("mem_post", ava::mem_post(m->y, N, d, m->P + 4 * d, 5 * d, P, m->xq, m->xexp, ldd, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         // the engram read
@@ -669,6 +675,19 @@ extern "C" int ava_model_decode_step(ava_model *m, ava_state *st, const int32_t 
 }
 
 extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }
+
+extern "C" int ava_model_nonfinite(ava_model *m, int32_t *rows, int *count, ava_stream stream) {
+    AVA_REQUIRE(m && count, AVA_ERR_ARG, "model_nonfinite: NULL argument");
+    *count = 0;
+    if (m->bad_n == 0) return AVA_OK;
+    std::vector<int32_t> h(m->bad_n);
+    AVA_HIP(hipSetDevice(m->device));
+    AVA_HIP(hipMemcpyAsync(h.data(), m->bad, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, (hipStream_t)stream));
+    AVA_HIP(hipStreamSynchronize((hipStream_t)stream));
+    for (int32_t v : h) *count += v != 0;
+    if (rows) std::copy(h.begin(), h.end(), rows);
+    return AVA_OK;
+}
 
 extern "C" int ava_model_freeze(ava_model *m, int on) {
     AVA_REQUIRE(m, AVA_ERR_ARG, "freeze: NULL model");

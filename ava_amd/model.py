@@ -191,6 +191,7 @@ class Model:
         if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
             raise ValueError("ids: a contiguous [B, T] int32 GPU tensor is required")
         B, T = ids.shape
+        self._last_B = B
         if want_logits and logits is None:
             logits = torch.empty((B * T, self.cfg["vocab"]), dtype=torch.float32, device=ids.device)
         cst = st.c()
@@ -211,6 +212,7 @@ class Model:
         if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
             raise ValueError("ids: a contiguous [B, T] int32 GPU tensor is required")
         B, T = ids.shape
+        self._last_B = B
         V = self.cfg["vocab"]
         if not (logits.is_cuda and logits.dtype == torch.float32 and logits.is_contiguous()
                 and logits.numel() >= B * T * V):
@@ -331,6 +333,7 @@ class Model:
 
     def forward(self, ids: torch.Tensor):
         B, T = ids.shape
+        self._last_B = B
         st = self.state(B, eng_cap=T if self.cfg["eng_block"] >= 0 else 0)
         return self.forward_with_state(ids, st), st
 
@@ -352,6 +355,17 @@ class Model:
                                         C.c_void_p(tr["kth"].data_ptr()), rows), "ava_model_set_trace")
         self._trace = tr
         return tr
+
+    def nonfinite(self) -> list:
+        """The streams of the last forward whose memory met a non-finite gate, key, query or value (their
+        fast weights were left as they were; gpu/model/fstep/arch.rs:780-783's guard). Waits for the
+        current stream."""
+        n = C.c_int(0)
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        B = getattr(self, "_last_B", 0)
+        rows = (C.c_int32 * max(B, 1))()
+        check(lib().ava_model_nonfinite(self.h, rows, C.byref(n), stream), "ava_model_nonfinite")
+        return [i for i in range(B) if rows[i]] if n.value else []
 
     # launch timing by kernel class (ava_model_set_timing / ava_model_timing)
     def set_timing(self, on: bool):

@@ -121,21 +121,21 @@ def lif_gen(cur, beta, theta=None, alif=None, levels=2, signed=True, init=None, 
     _need(cur, torch.float32, "lif_gen")
     B, T, D = cur.shape
     dev = cur.device
-    theta = torch.ones(D, device=dev) if theta is None else theta
+    theta = torch.ones(D, dtype=torch.float32, device=dev) if theta is None else theta
     if alif is None:
-        rho = torch.zeros(D, device=dev)
-        gain = torch.zeros(D, device=dev)
+        rho = torch.zeros(D, dtype=torch.float32, device=dev)
+        gain = torch.zeros(D, dtype=torch.float32, device=dev)
     else:
         rho, gain = alif
     ps = torch.cat([beta, theta, rho, gain]).to(torch.float32).contiguous()
     if init is None:
-        v = torch.zeros((B, D), device=dev)
-        s = torch.zeros((B, D), device=dev)
-        a = torch.zeros((B, D), device=dev)
+        v = torch.zeros((B, D), dtype=torch.float32, device=dev)
+        s = torch.zeros((B, D), dtype=torch.float32, device=dev)
+        a = torch.zeros((B, D), dtype=torch.float32, device=dev)
     else:
         v, s, a = init.v.clone(), init.s.clone(), init.a.clone()
     spikes = torch.empty((B, T, D), dtype=torch.int8, device=dev)
-    tho = torch.empty((B, D), device=dev) if th_out else None
+    tho = torch.empty((B, D), dtype=torch.float32, device=dev) if th_out else None
     if vec or pf:
         rc = lib().ava_lif_scan_tuned(_p(cur), B, T, D, _p(ps), _p(v), _p(s), _p(a), levels, int(signed),
                                       int(alif is not None), _p(spikes), _p(tho), vec, pf, _stream())
@@ -164,8 +164,8 @@ def mem_gen(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
         _need(t, torch.float32, f"mem_gen {nm}")
     BH, T, hs = q.shape
     g = la.shape[2]
-    F = torch.zeros((BH, hs, hs), device=q.device) if F is None else F.clone()
-    S = torch.zeros((BH, hs, hs), device=q.device) if S is None else S.clone()
+    F = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device) if F is None else F.clone()
+    S = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device) if S is None else S.clone()
     y = torch.empty_like(q)
     check(lib().ava_mem_scan(_p(q), _p(k), _p(e), _p(v), _p(la), _p(b), BH, T, hs, g, float(m), float(cap),
                              _p(F), _p(S), _p(y), _stream()), "ava_mem_scan")
@@ -178,7 +178,7 @@ def delta_rule_from(q, k, v, beta, la=None, f0=None):
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")) + (((la, "la"),) if la is not None else ()):
         _need(t, torch.float32, f"delta_rule {nm}")
     BH, T, hs = q.shape
-    F = torch.zeros((BH, hs, hs), device=q.device) if f0 is None else f0.clone()
+    F = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device) if f0 is None else f0.clone()
     y = torch.empty_like(q)
     check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(la), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
           "ava_delta_chunk")
@@ -192,11 +192,15 @@ def lif_gen_bwd(cur, ps, g_spk, init=None, g_vT=None, g_aT=None, levels=2, signe
     gradients per stream: sum over dim 0)."""
     _need(cur, torch.float32, "lif_gen_bwd cur")
     _need(g_spk, torch.float32, "lif_gen_bwd g_spk")
+    _need(ps, torch.float32, "lif_gen_bwd ps")
     B, T, D = cur.shape
     dev = cur.device
-    z = torch.zeros((B, D), device=dev)
+    z = torch.zeros((B, D), dtype=torch.float32, device=dev)
     v0, s0, a0 = (z, z, z) if init is None else (init.v, init.s, init.a)
-    out = {n: torch.empty((B, D), device=dev) for n in ("dv0", "da0", "dbeta", "drho", "dgain")}
+    for t, nm in ((v0, "v0"), (s0, "s0"), (a0, "a0"), (g_vT, "g_vT"), (g_aT, "g_aT")):
+        if t is not None:
+            _need(t, torch.float32, f"lif_gen_bwd {nm}")
+    out = {n: torch.empty((B, D), dtype=torch.float32, device=dev) for n in ("dv0", "da0", "dbeta", "drho", "dgain")}
     out["dI"] = torch.empty_like(cur)
     check(lib().ava_lif_scan_bwd(_p(cur), B, T, D, _p(ps), _p(v0), _p(s0), _p(a0), levels, int(signed), int(alif),
                                  float(slope), int(reset_grad), _p(g_spk), _p(g_vT), _p(g_aT), _p(out["dI"]),
@@ -209,6 +213,7 @@ def kwta_relu2_bwd(u, kth, ga):
     """gu = (u ga) 2 on the units kwta_relu kept (u - kth >= 0) with u > 0, else 0."""
     _need(u, torch.float32, "kwta_relu2_bwd u")
     _need(ga, torch.float32, "kwta_relu2_bwd ga")
+    _need(kth, torch.float32, "kwta_relu2_bwd kth")
     n, h = u.shape
     gu = torch.empty_like(u)
     check(lib().ava_kwta_relu2_bwd(_p(u), _p(kth), n, h, _p(ga), _p(gu), _stream()), "ava_kwta_relu2_bwd")
@@ -218,14 +223,16 @@ def kwta_relu2_bwd(u, kth, ga):
 def mem_gen_bwd(q, k, e, v, la, b, dy, m=0.0, cap=1e5, F0=None, S0=None, dF_T=None, dS_T=None):
     """The backward of mem_gen from the initial state (F0, S0; None: zeros) with dL/dy = dy and the
     final state's gradients (None: zeros). Returns dict dq, dk, de, dv, dla, db, dF0, dS0."""
-    for t, nm in ((q, "q"), (k, "k"), (e, "e"), (v, "v"), (la, "la"), (b, "b"), (dy, "dy")):
-        _need(t, torch.float32, f"mem_gen_bwd {nm}")
+    for t, nm in ((q, "q"), (k, "k"), (e, "e"), (v, "v"), (la, "la"), (b, "b"), (dy, "dy"), (F0, "F0"), (S0, "S0"),
+                  (dF_T, "dF_T"), (dS_T, "dS_T")):
+        if t is not None:
+            _need(t, torch.float32, f"mem_gen_bwd {nm}")
     BH, T, hs = q.shape
     g = la.shape[2]
     o = {n: torch.empty_like(q) for n in ("dq", "dk", "de", "dv")}
     o.update({n: torch.empty_like(la) for n in ("dla", "db")})
-    o["dF0"] = torch.empty((BH, hs, hs), device=q.device)
-    o["dS0"] = torch.zeros((BH, hs, hs), device=q.device)
+    o["dF0"] = torch.empty((BH, hs, hs), dtype=torch.float32, device=q.device)
+    o["dS0"] = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device)
     nbytes = lib().ava_mem_scan_bwd_workspace(BH, T, int(m != 0.0))
     work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     check(lib().ava_mem_scan_bwd(_p(q), _p(k), _p(e), _p(v), _p(la), _p(b), BH, T, hs, g, float(m), float(cap),
@@ -238,11 +245,13 @@ def mem_gen_bwd(q, k, e, v, la, b, dy, m=0.0, cap=1e5, F0=None, S0=None, dF_T=No
 def dense_back(S, G, wf, base, col, i0, L, nd):
     """The dense mix's backward: S [R, M] streams, G [L, M] = dL/d(mix after block k), wf packed weights.
     Returns (out [M], dw [nd])."""
+    for t, nm in ((S, "S"), (G, "G"), (wf, "wf"), (base, "base")):
+        _need(t, torch.float32, f"dense_back {nm}")
     M = base.numel()
     out = torch.empty_like(base)
-    dw = torch.empty(max(nd, 1), device=base.device)
+    dw = torch.empty(max(nd, 1), dtype=torch.float32, device=base.device)
     nf = lib().ava_dense_back_part_floats(M, nd)
-    part = torch.empty(max(nf, 1), device=base.device)
+    part = torch.empty(max(nf, 1), dtype=torch.float32, device=base.device)
     check(lib().ava_dense_back(_p(S), _p(G), _p(wf), _p(base), _p(out), _p(dw), col, i0, L, nd, M, _p(part), nf,
                                _stream()), "ava_dense_back")
     return out, dw[:nd]

@@ -67,12 +67,12 @@ class Lif:
         g = torch.Generator(device="cuda").manual_seed(1)
         self.cur = torch.randn((B, T, D), device="cuda", generator=g, dtype=torch.float32)
         beta = torch.sigmoid(torch.rand(D, device="cuda", generator=g) * 3.0 + 1.5)
-        self.ps = torch.cat([beta, torch.ones(D, device="cuda"), torch.full((D,), 0.95, device="cuda"),
-                             torch.full((D,), 0.05, device="cuda")]).contiguous()
-        self.v = torch.zeros((B, D), device="cuda")
-        self.s = torch.zeros((B, D), device="cuda")
-        self.a = torch.zeros((B, D), device="cuda")
-        self.th = torch.empty((B, D), device="cuda")
+        self.ps = torch.cat([beta, torch.ones(D, dtype=torch.float32, device="cuda"), torch.full((D,), 0.95, dtype=torch.float32, device="cuda"),
+                             torch.full((D,), 0.05, dtype=torch.float32, device="cuda")]).contiguous()
+        self.v = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+        self.s = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+        self.a = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+        self.th = torch.empty((B, D), dtype=torch.float32, device="cuda")
         self.spikes = torch.empty((B, T, D), dtype=torch.int8, device="cuda")
         self.tokens = B * T
         # algorithmic bytes: read cur, write spikes, write v_T and theta_T, read the 4 parameter rows
@@ -129,7 +129,7 @@ class Kwta:
         g = torch.Generator(device="cuda").manual_seed(2)
         self.u = torch.randn((n, h), device="cuda", generator=g)
         self.a = torch.empty_like(self.u)
-        self.kth = torch.empty(n, device="cuda")
+        self.kth = torch.empty(n, dtype=torch.float32, device="cuda")
         self.tokens = n
         self.bytes = n * h * 8 + n * 4
         self.config = {"workload": "kwta_relu2 config[3] wide layer", "rows": n, "H": h, "k": k}
@@ -177,7 +177,7 @@ class Gemm:
         self.qw = ops.QW.from_tensor(w)
         self.x = torch.randn((m, k), device="cuda", generator=g)
         self.xq, self.xe = ops.quant_rows(self.x, planes)
-        self.y = torch.empty((m, n), device="cuda")
+        self.y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         self.tokens = m
         self.ops = 2.0 * m * k * n * planes  # int8 OPs per launch
         self.config = {"workload": "q8 product config[3] W1", "m": m, "k": k, "n": n, "planes": planes}
@@ -236,7 +236,7 @@ class Delta:
         self.q /= self.q.norm(dim=2, keepdim=True)
         self.k /= self.k.norm(dim=2, keepdim=True)
         self.beta = torch.sigmoid(torch.randn((BH, T), device="cuda", generator=g))
-        self.F = torch.zeros((BH, 64, 64), device="cuda")
+        self.F = torch.zeros((BH, 64, 64), dtype=torch.float32, device="cuda")
         self.y = torch.empty_like(self.q)
         self.tokens = B * T
         # read q, k, v, beta; write y and the final state
@@ -302,10 +302,10 @@ class LifBwd:
         self.cur = torch.randn((B, T, D), device="cuda", generator=g, dtype=torch.float32)
         self.g = torch.randn((B, T, D), device="cuda", generator=g, dtype=torch.float32)
         beta = torch.sigmoid(torch.rand(D, device="cuda", generator=g) * 3.0 + 1.5)
-        self.ps = torch.cat([beta, torch.ones(D, device="cuda"), torch.full((D,), 0.95, device="cuda"),
-                             torch.full((D,), 0.05, device="cuda")]).contiguous()
-        self.z = torch.zeros((B, D), device="cuda")
-        self.out = [torch.empty((B, D), device="cuda") for _ in range(5)]
+        self.ps = torch.cat([beta, torch.ones(D, dtype=torch.float32, device="cuda"), torch.full((D,), 0.95, dtype=torch.float32, device="cuda"),
+                             torch.full((D,), 0.05, dtype=torch.float32, device="cuda")]).contiguous()
+        self.z = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+        self.out = [torch.empty((B, D), dtype=torch.float32, device="cuda") for _ in range(5)]
         self.dI = torch.empty_like(self.cur)
         self.tokens = B * T
         # algorithmic bytes: read cur and dL/dspikes, write dL/dcur; per (b, c) the initial state and the
@@ -375,9 +375,9 @@ class MemBwd:
         self.la = torch.log(torch.rand((BH, T, 64), device="cuda", generator=g) * 0.149 + 0.85)
         self.b = torch.rand((BH, T, 64), device="cuda", generator=g) * 1.8 + 0.1
         self.dy = torch.randn((BH, T, 64), device="cuda", generator=g)
-        self.out = [torch.empty((BH, T, 64), device="cuda") for _ in range(6)]
-        self.dF0 = torch.empty((BH, 64, 64), device="cuda")
-        self.dS0 = torch.empty((BH, 64, 64), device="cuda")
+        self.out = [torch.empty((BH, T, 64), dtype=torch.float32, device="cuda") for _ in range(6)]
+        self.dF0 = torch.empty((BH, 64, 64), dtype=torch.float32, device="cuda")
+        self.dS0 = torch.empty((BH, 64, 64), dtype=torch.float32, device="cuda")
         self.work_bytes = self.L.ava_mem_scan_bwd_workspace(BH, T, 1)
         self.work = torch.empty(self.work_bytes, dtype=torch.uint8, device="cuda")
         self.tokens = B * T
@@ -441,7 +441,7 @@ class Copy:
     def __init__(self, nbytes=1 << 30):
         import torch
 
-        self.src = torch.ones(nbytes // 4, device="cuda")
+        self.src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
         self.dst = torch.empty_like(self.src)
         self.tokens = 1
         self.bytes = 2 * nbytes
@@ -485,7 +485,7 @@ class Stack:
         self.st = self.model.state(B, eng_cap=T)
         g = torch.Generator(device="cuda").manual_seed(4)
         self.ids = torch.randint(0, c["vocab"], (B, T), device="cuda", generator=g, dtype=torch.int32)
-        self.logits = torch.empty((B * T, c["vocab"]), device="cuda")
+        self.logits = torch.empty((B * T, c["vocab"]), dtype=torch.float32, device="cuda")
         self.tokens = B * T
         d, H, V, L = c["d"], c["hidden"], c["vocab"], c["layers"]
         # algorithmic int8 work per forward (2 ops per multiply-add): 16 d^2 per token per block
@@ -673,7 +673,7 @@ class Decode:
         # the step's inputs live in fixed buffers so that it can be captured and replayed; the logits
         # and next buffers alternate between steps, as the overlapped step learns from the previous
         # step's pair while this step's forward writes the other
-        self.logits2 = [torch.empty((B, V), device="cuda") for _ in range(2)]
+        self.logits2 = [torch.empty((B, V), dtype=torch.float32, device="cuda") for _ in range(2)]
         self.nxt2 = [torch.empty(B, dtype=torch.int32, device="cuda") for _ in range(2)]
         self.logits, self.nxt_buf = self.logits2[0], self.nxt2[0]
         self.nats = torch.empty(B, dtype=torch.float64, device="cuda")

@@ -327,6 +327,15 @@ size_t ava_model_scratch_bytes(const ava_model *m);
  * graphs, which keep the scratch's addresses (no reference counterpart: the reference has no graphs). */
 int ava_model_freeze(ava_model *m, int on);
 
+/* The fused step's non-finite guard (gpu/model/fstep/arch.rs:780-783, 861-864: a non-finite gate, key,
+ * query or value refuses the token before anything is committed). Every memory head checks the values
+ * it stages (unit q, k and erase key, value, alpha, b k, alpha b e); a head that meets a non-finite one
+ * leaves its fast weights F and S as they were and marks its stream. After a forward (this call waits
+ * for the stream): count = the streams marked, rows [B of that forward] (nullable, host) = 1 for each.
+ * The stream's LIF state and engram store are committed as usual (as the reference's plain path,
+ * which then takes the token, commits them). */
+int ava_model_nonfinite(ava_model *m, int32_t *rows, int *count, ava_stream stream);
+
 /* The decision trace, for parity checks (no counterpart in the reference, whose tests compare single
  * ops): with the buffers set (all NULL: off), every forward copies per block i the spikes [B*T][d]
  * int8, the wide layer's values before the kWTA u [B*T][hidden] f32 and each row's k-th largest value

@@ -181,3 +181,18 @@ def test_mem_bwd_long():
         e = rel(gpu[n], o[n])
         print(f"  {n}: rel {e:.2e}", flush=True)
         assert e < 1e-4, (n, e)
+
+
+def test_wrappers_ignore_the_default_dtype():
+    """The wrappers allocate float32 whatever torch's default dtype is (a float64 default once gave
+    float64 output buffers that the kernels, writing float32, left mostly unwritten)."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    try:
+        x = lif_inputs(9, 2, 3, 8, 2, True)
+        o = O.lif_bwd(x[0], x[1], x[5], x[2], x[3], x[4], x[6], x[7], slope=2.0)
+        gpu = run_lif(*x, 2, True, True, 2.0, False)
+        for k in ("dI", "dv0", "da0", "dbeta", "drho", "dgain"):
+            assert gpu[k].dtype == np.float32 and np.array_equal(gpu[k], o[k]), k
+    finally:
+        torch.set_default_dtype(old)

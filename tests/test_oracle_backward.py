@@ -18,7 +18,7 @@ import torch
 
 from oracle import oracle as O
 
-torch.set_default_dtype(torch.float64)
+# every tensor here is made float64 explicitly (no global default: the GPU tests share the process)
 
 
 # --------------------------------------------------------------------------- LIF
