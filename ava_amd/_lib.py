@@ -77,6 +77,7 @@ def lib():
         "ava_lif_scan_tuned": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, vp],
         "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
+        "ava_mem_chunk": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
         "ava_lif_scan_bwd": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, f32, i32] + [vp] * 10,
         "ava_kwta_relu2_bwd": [vp, vp, i32, i32, vp, vp, vp],

@@ -392,6 +392,524 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ the chunked form
+
+// The same recurrence in chunks of CK = 16 tokens with the state contractions on the fp32 matrix
+// cores: the algebra of delta_chunk / chunk_core (gpu/arch.rs:1138-1164, 1243-1327). Inside a chunk
+// (positions 0..n-1; everything per key channel): Gamma_i = prod_{t<=i} alpha_t; D_im =
+// prod_{t=m+1..i} alpha_t, a ratio <= 1 formed pair by pair (no division by Gamma, so strong
+// forgetting cannot overflow); the momentum kernel K_ij = sum_{m=j..i} M^(m-j) D_im, i.e. K_ii = 1,
+// K_ij = D_ij + M K_i,j+1 (M = 0: K = D). With the write key w = b k and the erase key ah = alpha b e:
+//   recalls    (I + Ae) R = (e Gamma_{i-1}) F0 + (e M K_{i-1,0}) S0 + Ke V
+//   read-outs  Y = (q Gamma) F0 + (q M K_0) S0 + Qw V - Qa R
+//   state      F' = Gamma_{n-1} F0 + M K_{n-1,0} S0 + sum_j K_{n-1,j} (w_j v_j^T - ah_j r_j^T)
+//              S' = M^n S0 + sum_j M^(n-1-j) (w_j v_j^T - ah_j r_j^T)
+// where Qw_ij = sum_ch q_i K_ij w_j (j <= i), Qa the same with ah, and Ke, Ae the same with e_i and
+// K_{i-1,j} (j < i). A closed form per chunk cannot hold the bound clamp(F, +-cap) per token (the
+// reference's chunked CPU path has none, arch.rs:1138-1141), so the bounded rule is kept this way: a
+// wave whose columns of F start a chunk above cap / 8 runs that chunk token by token with the bound at
+// every step (the runaway heads that approach the bound grow by a few per cent per chunk), and the
+// closed form's result is bounded at the chunk's end.
+//
+// One workgroup of 4 waves per head. Wave w owns the value columns 16w..16w+15 of F and S, in the
+// accumulator layout of v_mfma_f32_16x16x4f32 (tile mt: key rows 16mt + 4(lane/16) + r, column
+// 16w + lane%16, register r). The same registers are the B operand of a product over the key rows
+// (k-step r covers rows 16mt + 4(lane/16) + r, the A operand's columns permuted alike), so both
+// contractions read the state from the wave's own registers and the chunk needs no state in LDS:
+//   [Z_R ; Z_Y] = [e Gamma_{i-1} | e M K_{i-1,0} ; q Gamma_i | q M K_{i,0}] [F0 ; S0]   (32 x 128 x 16)
+//   [F' ; S']  += [K_{n-1,j} w_j | -K_{n-1,j} ah_j ; M^(n-1-j) w_j | -M^(n-1-j) ah_j] [V ; R] (128 x 32 x 16)
+// The recalls are solved per column inside the wave: lane group g = lane/16 holds rows 4g..4g+3 of a
+// column, solves its 4 x 4 block and passes the block's R to the later groups (ds_bpermute).
+// The pair matrices Qw, Qa, Ke, Ae are VALU work: lane (row i, channels 4c..4c+3) walks j = 15..0 with
+// D and K in registers, and the 16 lanes of a row add their partials by a DPP reduce-scatter.
+// The rows of q, e, Gamma and M K_0, which the first contraction reads down a column (16 rows at once),
+// are XOR-swizzled in 16-byte chunks (chunk ^ row); the others in 16-column blocks. 40 KB of LDS.
+constexpr int CK = 16;
+
+struct ChunkLds {
+    float q[CK * HS], e[CK * HS], v[CK * HS], a[CK * HS], w[CK * HS], ah[CK * HS];
+    float G[CK * HS];    // row i: Gamma_i
+    float MK0[CK * HS];  // row i: M K_{i,0}
+    float KL[CK * HS];   // row j: K_{n-1,j}
+    float pm[4][CK][CK];  // Qw, Qa, Ke, Ae (row i, column j)
+};
+
+// Unrolled steps keep their LDS reads next to their uses: the scheduler would otherwise issue the reads
+// of every step at once and spill them.
+#define CK_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+__device__ __forceinline__ int swz(int r, int c) { return r * HS + (c ^ ((r & 15) << 2)); }
+// The arrays read along rows (v, alpha, w, ah, K_last): 16-column blocks XOR-ed with (row / 4) % 4, so
+// the four lane groups, which read rows 4g + r at the same columns, fall on different banks.
+__device__ __forceinline__ int rsw(int r, int c) { return r * HS + (c ^ (((r >> 2) & 3) << 4)); }
+__device__ __forceinline__ f32x4 ld4s(const float *A, int r, int c) {
+    return *reinterpret_cast<const f32x4 *>(A + swz(r, c));
+}
+__device__ __forceinline__ void st4s(float *A, int r, int c, f32x4 x) { *reinterpret_cast<f32x4 *>(A + swz(r, c)) = x; }
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+
+// One stage of a reduce-scatter over the DPP pairing CTRL (the partner differs in the lane bit that
+// `up` tests): lanes with `up` keep x[N..2N) plus the partner's, the others x[0..N) plus the partner's;
+// the kept half lands in x[0..N).
+template <int CTRL, int N>
+__device__ __forceinline__ void rs_stage(float *x, bool up) {
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float lo = x[i], hi = x[i + N];
+        x[i] = (up ? hi : lo) + dppf<CTRL>(up ? lo : hi);
+    }
+}
+
+// M^p in double, rounded once (the reference's m.powi(p) as f32, arch.rs:1289, 1299).
+__device__ __forceinline__ float mpow(float M, int p) {
+    double r = 1.0;
+    for (int i = 0; i < p; i++) r *= (double)M;
+    return (float)r;
+}
+
+// The pair matrices and the per-channel decay rows of one chunk of n valid positions, from the staged
+// alpha, w, ah, q, e (see the comment above). Lane group g of wave w takes row i = w, 7 - w, 8 + w,
+// 15 - w (g = 0..3: every wave walks the same 16 steps and the lanes of a group the same row).
+template <bool MOM>
+__device__ __forceinline__ void chunk_pairs(ChunkLds &s, int wave, int lane, int n, float M) {
+    const int g = lane >> 4, cl = lane & 15, c0 = 4 * cl;
+    const int i = g == 0 ? wave : g == 1 ? 7 - wave : g == 2 ? 8 + wave : 15 - wave;
+    const f32x4 qi = ld4s(s.q, i, c0);
+    const f32x4 ei = i + 1 < CK ? ld4s(s.e, i + 1, c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float D[4] = {0.0f, 0.0f, 0.0f, 0.0f}, K[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int half = 1; half >= 0; half--) {
+        float x[32];
+#pragma unroll
+        for (int z = 0; z < 32; z++) x[z] = 0.0f;
+#pragma unroll
+        for (int jj = 7; jj >= 0; jj--) {
+            const int j = 8 * half + jj;
+            CK_FENCE();  // one step's loads at a time (the unrolled walk would hoist them all)
+            const f32x4 al = ld4(&s.a[rsw(j < CK - 1 ? j + 1 : CK - 1, c0)]);  // alpha_{j+1} (j = 15: unused)
+            const f32x4 wj = ld4(&s.w[rsw(j, c0)]), aj = ld4(&s.ah[rsw(j, c0)]);
+            const float dl = j == i ? 1.0f : 0.0f;  // D_ii = 1; rows j > i keep D = K = 0
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                D[c] = fmaf(D[c], al[c], dl);
+                K[c] = MOM ? fmaf(M, K[c], D[c]) : D[c];
+                const float kw = K[c] * wj[c], ka = K[c] * aj[c];
+                x[jj] = fmaf(qi[c], kw, x[jj]);
+                x[8 + jj] = fmaf(qi[c], ka, x[8 + jj]);
+                x[16 + jj] = fmaf(ei[c], kw, x[16 + jj]);
+                x[24 + jj] = fmaf(ei[c], ka, x[24 + jj]);
+            }
+            if (i == n - 1) *reinterpret_cast<f32x4 *>(&s.KL[rsw(j, c0)]) = f32x4{K[0], K[1], K[2], K[3]};
+        }
+        // x[8 m + jj]: matrix m (Qw, Qa, Ke, Ae) at j = 8 half + jj. After the four stages lane cl holds
+        // matrix cl >> 2 at j = 8 half + 2 (cl & 3) + {0, 1}, summed over the row's 16 lanes.
+        rs_stage<0x140, 16>(x, cl & 8);  // row_mirror: lane cl <-> 15 - cl
+        rs_stage<0x141, 8>(x, cl & 4);   // row_half_mirror: cl <-> 7 - cl within each 8
+        rs_stage<0x1B, 4>(x, cl & 2);    // quad_perm [3,2,1,0]
+        rs_stage<0xB1, 2>(x, cl & 1);    // quad_perm [1,0,3,2]
+        const int mm = cl >> 2, row = mm < 2 ? i : (i + 1) & (CK - 1);  // Ke, Ae: row i + 1 (row 0: zeros)
+        s.pm[mm][row][8 * half + 2 * (cl & 3)] = x[0];
+        s.pm[mm][row][8 * half + 2 * (cl & 3) + 1] = x[1];
+    }
+    const f32x4 a0 = ld4(&s.a[rsw(0, c0)]);
+    f32x4 gm, mk;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        gm[c] = D[c] * a0[c];  // Gamma_i = D_i0 alpha_0
+        mk[c] = M * K[c];
+    }
+    st4s(s.G, i, c0, gm);
+    if (MOM) st4s(s.MK0, i, c0, mk);
+}
+
+// The state contractions, the recalls and the read-outs of one chunk for wave `wave`'s 16 value
+// columns: F and S (in the accumulator layout) advance by the chunk; Y[r] = the read-out at position
+// 4 (lane / 16) + r of column 16 wave + lane % 16. The intra-chunk products Ke V, Qw V and Qa R run on
+// the matrix cores too: their K dimension is the chunk position, with k-step r covering positions
+// 4g + r, so the B operand is the lane's own value or recall at row 4g + r.
+template <bool MOM>
+__device__ __forceinline__ void chunk_state(const ChunkLds &s, int wave, int lane, int n, float Mn, const float (&mu)[4],
+                                            float M, float cap, f32x4 (&Fr)[4], f32x4 (&Sr)[4], float (&Y)[4]) {
+    const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl;
+    // A wave whose columns start the chunk above cap / 8 runs it token by token with the bound applied
+    // at every step (the closed form cannot bound a head inside the chunk). In this layout a column's 64
+    // rows are the wave's four lane groups, so the loop needs no other wave.
+    float fmax = 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) fmax = fmaxf(fmax, fabsf(Fr[mt][r]));
+    fmax = ava::wave_max(fmax);
+    if (__builtin_amdgcn_readfirstlane(__float_as_int(fmax)) > __float_as_int(0.125f * cap)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) Y[r] = 0.0f;
+        for (int t = 0; t < n; t++) {
+            float rp = 0.0f;
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                const f32x4 e4 = ld4s(s.e, t, 16 * mt + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; r++) rp = fmaf(e4[r], Fr[mt][r], rp);
+            }
+            const float rj = xsum32(xsum16(rp)), vj = s.v[rsw(t, col)];
+            float yp = 0.0f;
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                const int k0 = 16 * mt + 4 * g;
+                const f32x4 a4 = ld4(&s.a[rsw(t, k0)]), w4 = ld4(&s.w[rsw(t, k0)]), x4 = ld4(&s.ah[rsw(t, k0)]);
+                const f32x4 q4 = ld4s(s.q, t, k0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float u = fmaf(-x4[r], rj, w4[r] * vj);  // b_i k_i v_j - a_i b_i e_i r_j
+                    float f;
+                    if (MOM) {
+                        Sr[mt][r] = fmaf(M, Sr[mt][r], u);
+                        f = fmaf(a4[r], Fr[mt][r], Sr[mt][r]);
+                    } else {
+                        f = fmaf(a4[r], Fr[mt][r], u);
+                    }
+                    f = __builtin_amdgcn_fmed3f(f, -cap, cap);
+                    Fr[mt][r] = f;
+                    yp = fmaf(q4[r], f, yp);
+                }
+            }
+            const float yj = xsum32(xsum16(yp));
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (t == 4 * g + r) Y[r] = yj;
+        }
+        return;
+    }
+    // [Z_R ; Z_Y]: A rows are chunk positions (cl), the K dimension the key rows of F and S
+    f32x4 zr = {0.0f, 0.0f, 0.0f, 0.0f}, zy = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool first = cl == 0;  // Gamma_{-1} = 1, K_{-1,0} = 0
+    const int im1 = first ? 0 : cl - 1;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++) {
+        CK_FENCE();
+        const int k0 = 16 * mt + 4 * g;
+        const f32x4 e4 = ld4s(s.e, cl, k0), q4 = ld4s(s.q, cl, k0);
+        const f32x4 gp = ld4s(s.G, im1, k0), gc = ld4s(s.G, cl, k0);
+        f32x4 kp = {0.0f, 0.0f, 0.0f, 0.0f}, kc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (MOM) {
+            kp = ld4s(s.MK0, im1, k0);
+            kc = ld4s(s.MK0, cl, k0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            zr = __builtin_amdgcn_mfma_f32_16x16x4f32(first ? e4[r] : e4[r] * gp[r], Fr[mt][r], zr, 0, 0, 0);
+            zy = __builtin_amdgcn_mfma_f32_16x16x4f32(q4[r] * gc[r], Fr[mt][r], zy, 0, 0, 0);
+            if (MOM) {
+                zr = __builtin_amdgcn_mfma_f32_16x16x4f32(first ? 0.0f : e4[r] * kp[r], Sr[mt][r], zr, 0, 0, 0);
+                zy = __builtin_amdgcn_mfma_f32_16x16x4f32(q4[r] * kc[r], Sr[mt][r], zy, 0, 0, 0);
+            }
+        }
+    }
+    CK_FENCE();
+    // this column's values at the lane's rows 4g + r; Z_R + Ke V and Z_Y + Qw V
+    float Vb[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) Vb[r] = s.v[rsw(4 * g + r, col)];
+    {
+        const f32x4 ke = ld4(&s.pm[2][cl][4 * g]), qw = ld4(&s.pm[0][cl][4 * g]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            zr = __builtin_amdgcn_mfma_f32_16x16x4f32(ke[r], Vb[r], zr, 0, 0, 0);
+            zy = __builtin_amdgcn_mfma_f32_16x16x4f32(qw[r], Vb[r], zy, 0, 0, 0);
+        }
+    }
+    // (I + Ae) R = Z_R + Ke V by 4 x 4 blocks: group blk solves its block, the later groups take the
+    // block's R from its lanes and subtract its share
+    float R[4] = {0.0f, 0.0f, 0.0f, 0.0f}, rhs[4] = {zr[0], zr[1], zr[2], zr[3]};
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) {
+        CK_FENCE();
+        if (g == blk) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const f32x4 ae = ld4(&s.pm[3][4 * blk + r][4 * blk]);
+                float x = rhs[r];
+#pragma unroll
+                for (int rr = 0; rr < r; rr++) x = fmaf(-ae[rr], R[rr], x);
+                R[r] = x;
+            }
+        }
+        if (blk < 3) {
+            float Rb[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) Rb[r] = __shfl(R[r], 16 * blk + cl, 64);
+            if (g > blk) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const f32x4 ae = ld4(&s.pm[3][4 * g + r][4 * blk]);
+#pragma unroll
+                    for (int rr = 0; rr < 4; rr++) rhs[r] = fmaf(-ae[rr], Rb[rr], rhs[r]);
+                }
+            }
+        }
+    }
+    CK_FENCE();
+    // read-outs Y = Z_Y + Qw V - Qa R
+    {
+        const f32x4 qa = ld4(&s.pm[1][cl][4 * g]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) zy = __builtin_amdgcn_mfma_f32_16x16x4f32(-qa[r], R[r], zy, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) Y[r] = zy[r];
+    }
+    // the state: F' = Gamma_{n-1} F0 + M K_{n-1,0} S0 + ..., S' = M^n S0 + ...; A rows are key rows,
+    // the K dimension the chunk positions j = 4g + r (V, then R), B the lane's own Vb and R
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++) {
+        CK_FENCE();
+        const int k0 = 16 * mt + 4 * g, ch = 16 * mt + cl;
+        const f32x4 gl = ld4s(s.G, n - 1, k0);
+        f32x4 F2, S2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (MOM) {
+            const f32x4 mk = ld4s(s.MK0, n - 1, k0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                F2[r] = fmaf(mk[r], Sr[mt][r], gl[r] * Fr[mt][r]);
+                S2[r] = Mn * Sr[mt][r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) F2[r] = gl[r] * Fr[mt][r];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int o = rsw(4 * g + r, ch);
+            const float wv = s.w[o], av = s.ah[o], kl = s.KL[o];
+            // F and S alternate, so no product waits on the one just issued
+            F2 = __builtin_amdgcn_mfma_f32_16x16x4f32(wv * kl, Vb[r], F2, 0, 0, 0);
+            if (MOM) S2 = __builtin_amdgcn_mfma_f32_16x16x4f32(wv * mu[r], Vb[r], S2, 0, 0, 0);
+            F2 = __builtin_amdgcn_mfma_f32_16x16x4f32(-(av * kl), R[r], F2, 0, 0, 0);
+            if (MOM) S2 = __builtin_amdgcn_mfma_f32_16x16x4f32(-(av * mu[r]), R[r], S2, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) Fr[mt][r] = __builtin_amdgcn_fmed3f(F2[r], -cap, cap);
+        if (MOM) Sr[mt] = S2;
+    }
+}
+
+// The chunked memory. FUSED: the block's memory from its raw projections (FusedArgs, the staging of
+// mem_fused_kernel: unit q, k, erase key, value residual, gates from the rank-r read-outs); else the
+// staged inputs of ava_mem_scan's layout (MemArgs; G1: one gate per row and head).
+template <bool FUSED, bool G1, bool MOM>
+__global__ __launch_bounds__(256, 2) void mem_chunk_kernel(FusedArgs pf, MemArgs pd) {
+    __shared__ __attribute__((aligned(16))) ChunkLds s;
+    const int T = FUSED ? pf.T : pd.T, nh = FUSED ? pf.nh : pd.nh;
+    const float M = FUSED ? pf.m : pd.m, cap = FUSED ? pf.cap : pd.cap;
+    const int bh = blockIdx.x, bi = bh / nh, hh = bh - bi * nh;
+    const int tid = threadIdx.x, lane_ = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    f32x4 Fr[4], Sr[4];
+    float *Fh = (FUSED ? pf.F : pd.F) + (size_t)bh * HS * HS;
+    float *Sh = MOM ? (FUSED ? pf.S : pd.S) + (size_t)bh * HS * HS : nullptr;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int o = (16 * mt + 4 * (lane_ >> 4) + r) * HS + 16 * wave + (lane_ & 15);
+            Fr[mt][r] = Fh[o];
+            Sr[mt][r] = MOM ? Sh[o] : 0.0f;
+        }
+
+    // FUSED: the head's constants at this lane's channel
+    const int d = nh * HS;
+    const size_t row0 = (size_t)bi * T;
+    float offc = 0.0f, bah = 0.0f, bbh = 0.0f, p0 = 0.0f, p1 = 0.0f;
+    if (FUSED) {
+        offc = pf.off[hh * HS + lane_];
+        bah = pf.ba[hh];
+        bbh = pf.bb[hh];
+        if (pf.vres) {
+            p0 = pf.vres[0] * 1.0f + 1.0f;
+            p1 = pf.vres[1];
+        }
+    }
+    const size_t base = (size_t)bi * T * pd.ld + (size_t)hh * HS;
+    const size_t gbase = G1 ? (size_t)bi * T * pd.ldg + hh : (size_t)bi * T * pd.ldg + (size_t)hh * HS;
+    const size_t ybase = FUSED ? row0 * d + (size_t)hh * HS : (size_t)bi * T * pd.ldy + (size_t)hh * HS;
+    const int ldy = FUSED ? d : pd.ldy;
+    float *yout = FUSED ? pf.y : pd.y;
+
+    // the raw inputs of a chunk, loaded one chunk ahead: FUSED, wave w's positions 4w..4w+3 with lane =
+    // channel; else thread -> (position tid / 16, channels 4 (tid % 16)..+3)
+    const int ldp = 5 * d, ldgf = FUSED ? 2 * nh + 2 * pf.r : 0;
+    float rq[4], rk[4], rv[4], rw[4], rv0[4], rz[4], rza[4], rzb[4];
+    f32x4 dq, dk, de, dv, dl, db;
+    auto load = [&](int t0, int lane) {
+        if (FUSED) {
+            const int c = hh * HS + lane;
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const int t = min(t0 + wave * 4 + st, T - 1);  // past the end: the last position, never used
+                const size_t rw_ = row0 + t;
+                const float *Pr = pf.P + rw_ * ldp, *Gr = pf.G + rw_ * ldgf;
+                rq[st] = Pr[c];
+                rk[st] = Pr[d + c];
+                rv[st] = Pr[2 * d + c];
+                rw[st] = Pr[3 * d + c];
+                rv0[st] = pf.v0 ? pf.v0[rw_ * d + c] : 0.0f;
+                rz[st] = (lane & 31) < pf.r ? Gr[2 * nh + (lane < 32 ? lane : lane - 32 + pf.r)] : 0.0f;
+                rza[st] = Gr[hh];
+                rzb[st] = Gr[nh + hh];
+            }
+        } else {
+            const int t = min(t0 + (tid >> 4), T - 1), si = (tid & 15) * 4;
+            const size_t o = base + (size_t)t * pd.ld + si;
+            dq = ld4(pd.q + o);
+            dk = ld4(pd.k + o);
+            de = ld4(pd.e + o);
+            dv = ld4(pd.v + o);
+            if (G1) {
+                const float l = pd.la[gbase + (size_t)t * pd.ldg], b = pd.b[gbase + (size_t)t * pd.ldg];
+                dl = f32x4{l, l, l, l};
+                db = f32x4{b, b, b, b};
+            } else {
+                const size_t og = gbase + (size_t)t * pd.ldg + si;
+                dl = ld4(pd.la + og);
+                db = ld4(pd.b + og);
+            }
+        }
+    };
+    // FUSED: the B operand of the rank-r read-out product (wa2/wb2 rows 4 ks + lane / 16, column
+    // 16 wave + lane % 16), the same for every chunk
+    float wA[8], wB[8];
+    if (FUSED) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const int jj = 4 * ks + (lane_ >> 4), cc = hh * HS + 16 * wave + (lane_ & 15);
+            wA[ks] = jj < pf.r ? pf.wa2[(size_t)jj * d + cc] : 0.0f;
+            wB[ks] = jj < pf.r ? pf.wb2[(size_t)jj * d + cc] : 0.0f;
+        }
+    }
+    load(0, lane_);
+
+    float mu[4], Mn = 0.0f;  // M^(n-1-j) at j = 4g + r (0 past n), M^n
+    int nf = 0, nprev = -1;
+    for (int t0 = 0; t0 < T; t0 += CK) {
+        const int n = min(CK, T - t0);
+        // the lane index passes through an empty asm each chunk, so the many lane-dependent LDS addresses
+        // are formed where they are used instead of being hoisted out of the loop and held in registers
+        int lane = lane_;
+        asm volatile("" : "+v"(lane));
+        const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl, c = hh * HS + lane;
+        if (n != nprev) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) mu[r] = 4 * g + r < n ? mpow(M, n - 1 - (4 * g + r)) : 0.0f;
+            Mn = mpow(M, n);
+            nprev = n;
+        }
+        if (FUSED) {
+            __syncthreads();  // the previous chunk's LDS reads are done
+            float *zs = &s.pm[0][0][0];  // the z rows (za | zb per position), in the pair matrices' space
+#pragma unroll
+            for (int st = 0; st < 4; st++) zs[swz(4 * wave + st, lane)] = rz[st];
+            __syncthreads();
+            // the rank-r read-outs of all 16 positions for this wave's 16 channels on the matrix cores
+            f32x4 la4 = {0.0f, 0.0f, 0.0f, 0.0f}, lb4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                la4 = __builtin_amdgcn_mfma_f32_16x16x4f32(zs[swz(cl, 4 * ks + g)], wA[ks], la4, 0, 0, 0);
+                lb4 = __builtin_amdgcn_mfma_f32_16x16x4f32(zs[swz(cl, 32 + 4 * ks + g)], wB[ks], lb4, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                s.w[rsw(4 * g + r, col)] = la4[r];
+                s.ah[rsw(4 * g + r, col)] = lb4[r];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const int sp = 4 * wave + st, t = t0 + sp, o = rsw(sp, lane), oz = swz(sp, lane);
+                const float lra = s.w[o], lrb = s.ah[o];
+                const float ek = rk[st] + rw[st];
+                const float sq = wsum(rq[st] * rq[st]), sk = wsum(rk[st] * rk[st]), se = wsum(ek * ek);
+                float qn = rq[st] * rsqrtf(sq + 1e-6f);
+                const float kn = rk[st] * rsqrtf(sk + 1e-6f);
+                float en = ek * rsqrtf(se + 1e-6f);
+                float v = rv[st];
+                if (pf.v0_out && t < T) pf.v0_out[(row0 + t) * d + c] = v;
+                if (pf.v0) v = v * p0 + rv0[st] * p1;
+                float a = gate_alpha(((rza[st] + bah) + offc) + lra);
+                const float bw = gate_sig((rzb[st] + bbh) + lrb) * 2.0f;
+                float bk = bw * kn, abe = (a * bw) * en;
+                if (t < T) {
+                    if (!finite6(qn, en, v, a, bk, abe)) nf = 1;
+                } else {
+                    qn = en = v = bk = abe = 0.0f;  // positions past the end change nothing
+                    a = 1.0f;
+                }
+                s.q[oz] = qn;
+                s.e[oz] = en;
+                s.v[o] = v;
+                s.a[o] = a;
+                s.w[o] = bk;
+                s.ah[o] = abe;
+            }
+        } else {
+            const int sp = tid >> 4, si = (tid & 15) * 4, t = t0 + sp;
+            f32x4 a4 = {1.0f, 1.0f, 1.0f, 1.0f}, w4 = {0.0f, 0.0f, 0.0f, 0.0f}, x4 = w4;
+            if (t < T) {
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    a4[cc] = expf(dl[cc]);
+                    w4[cc] = db[cc] * dk[cc];
+                    x4[cc] = (a4[cc] * db[cc]) * de[cc];
+                }
+            } else {
+                dq = de = dv = w4;  // positions past the end change nothing
+            }
+            __syncthreads();  // the previous chunk's LDS reads are done
+            st4s(s.q, sp, si, dq);
+            st4s(s.e, sp, si, de);
+            *reinterpret_cast<f32x4 *>(&s.v[rsw(sp, si)]) = dv;
+            *reinterpret_cast<f32x4 *>(&s.a[rsw(sp, si)]) = a4;
+            *reinterpret_cast<f32x4 *>(&s.w[rsw(sp, si)]) = w4;
+            *reinterpret_cast<f32x4 *>(&s.ah[rsw(sp, si)]) = x4;
+        }
+        if (t0 + CK < T) load(t0 + CK, lane);  // in flight during this chunk's work
+        __syncthreads();
+        chunk_pairs<MOM>(s, wave, lane, n, M);
+        __syncthreads();
+        float Y[4];
+        chunk_state<MOM>(s, wave, lane, n, Mn, mu, M, cap, Fr, Sr, Y);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (4 * g + r < n) yout[ybase + (size_t)(t0 + 4 * g + r) * ldy + col] = Y[r];
+    }
+
+    if (FUSED) {
+        // any lane that staged a non-finite value: a flag word in the (now unused) pair matrices, so the
+        // workgroup stays at 40 KB of LDS
+        int *flag = reinterpret_cast<int *>(&s.pm[0][0][0]);
+        __syncthreads();
+        if (tid == 0) *flag = 0;
+        __syncthreads();
+        if (nf) *flag = 1;
+        __syncthreads();
+        if (*flag) {
+            if (tid == 0 && pf.bad) pf.bad[bi] = 1;
+            return;  // nothing committed
+        }
+    }
+    // the store addresses from a laundered lane index, so they are not the loads' addresses kept alive
+    // across the scan
+    int ls = lane_;
+    asm volatile("" : "+v"(ls));
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int o = (16 * mt + 4 * (ls >> 4) + r) * HS + 16 * wave + (ls & 15);
+            Fh[o] = Fr[mt][r];
+            if (MOM) Sh[o] = Sr[mt][r];
+        }
+}
+
 // One token per stream (decode, T == 1): the same recurrence step as mem_fused_kernel, laid out for
 // streaming the state rather than for a long scan. Wave w holds rows 16w..16w+15 of F and S and lane
 // j column j, so each of the lane's 16 + 16 state loads and stores is one 256-byte row per wave
@@ -538,10 +1056,35 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
         AVA_LAUNCHED("mem_step");
         return AVA_OK;
     }
-    // the chunk's inputs are staged by the scan's own waves (loading them a chunk ahead measured no faster)
+    // the token loop (the chunk's inputs are staged by the scan's own waves): faster here than the
+    // chunked form, whose VALU and matrix phases do not overlap in one wave
     if (m != 0.0f) mem_fused_kernel<true, false><<<B * nh, 256, 0, st>>>(a);
     else mem_fused_kernel<false, false><<<B * nh, 256, 0, st>>>(a);
     AVA_LAUNCHED("mem_block");
+    return AVA_OK;
+}
+
+// The scan of mem_scan_strided in the chunked form.
+int mem_chunk_strided(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,
+                      int B, int T, int nh, int ld, int g, int ldg, float m, float cap, float *F, float *S, float *y,
+                      int ldy, hipStream_t st) {
+    AVA_REQUIRE(q && k && e && v && la && b && F && y, AVA_ERR_ARG, "mem_chunk: NULL buffer");
+    AVA_REQUIRE(m == 0.0f || S, AVA_ERR_ARG, "mem_chunk: momentum %g needs S", (double)m);
+    AVA_REQUIRE(g == 1 || g == HS, AVA_ERR_ARG, "mem_chunk: gate width %d (1 or 64)", g);
+    AVA_REQUIRE(B >= 0 && T >= 0 && nh > 0 && ld % 4 == 0 && ldy % 4 == 0 && (g == 1 || ldg % 4 == 0), AVA_ERR_SHAPE,
+                "mem_chunk: B=%d T=%d nh=%d ld=%d ldg=%d ldy=%d", B, T, nh, ld, ldg, ldy);
+    if (B == 0 || T == 0) return AVA_OK;
+    MemArgs a{q, k, e, v, la, b, T, nh, ld, ldg, ldy, m, cap, F, S, y};
+    const FusedArgs none{};
+    dim3 grid(B * nh), block(256);
+    if (g == 1) {
+        if (m != 0.0f) mem_chunk_kernel<false, true, true><<<grid, block, 0, st>>>(none, a);
+        else mem_chunk_kernel<false, true, false><<<grid, block, 0, st>>>(none, a);
+    } else {
+        if (m != 0.0f) mem_chunk_kernel<false, false, true><<<grid, block, 0, st>>>(none, a);
+        else mem_chunk_kernel<false, false, false><<<grid, block, 0, st>>>(none, a);
+    }
+    AVA_LAUNCHED("mem_chunk");
     return AVA_OK;
 }
 
@@ -558,6 +1101,14 @@ int zero_ints(int *x, int n, hipStream_t st) {
 }
 
 }  // namespace ava
+
+extern "C" int ava_mem_chunk(const float *q, const float *k, const float *e, const float *v, const float *la,
+                             const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,
+                             float *y, ava_stream stream) {
+    AVA_REQUIRE(hs == HS, AVA_ERR_UNSUPPORTED, "mem_chunk: head size %d (this build runs 64)", hs);
+    AVA_REQUIRE(BH >= 0 && T >= 0, AVA_ERR_SHAPE, "mem_chunk: BH=%d T=%d", BH, T);
+    return ava::mem_chunk_strided(q, k, e, v, la, b, BH, T, 1, HS, g, g, m, cap, F, S, y, HS, (hipStream_t)stream);
+}
 
 extern "C" int ava_mem_scan(const float *q, const float *k, const float *e, const float *v, const float *la,
                             const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,

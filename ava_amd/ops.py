@@ -10,6 +10,7 @@ status (the reference bail!s on shape, dtype and contiguity errors).
     lif_gen(cur, beta, ...)      lif_gen.rs:86-130
     kwta_relu(u, k, relu2)       model.rs:504-528 + arch.rs:1820-1835
     mem_gen(q, k, e, v, la, b, m)   mem_gen.rs:127-137
+    mem_chunk(q, k, e, v, la, b, m) delta_chunk / chunk_core (arch.rs:1151-1164, 1243-1327)
     delta_rule_from(q, k, v, beta, la, f0)   model.rs:744-799 (chunked, per-head gates)
     attend(q, ks, vs, n0)        model/fstep.rs:303-329 (one head of 64, causal, over a store)
 
@@ -169,6 +170,21 @@ def mem_gen(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
     y = torch.empty_like(q)
     check(lib().ava_mem_scan(_p(q), _p(k), _p(e), _p(v), _p(la), _p(b), BH, T, hs, g, float(m), float(cap),
                              _p(F), _p(S), _p(y), _stream()), "ava_mem_scan")
+    return y, F, S
+
+
+def mem_chunk(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
+    """delta_chunk / chunk_core (arch.rs:1151-1164, 1243-1327): mem_gen's rule in chunks of 16 tokens,
+    the bound on F applied at chunk ends. Same arguments and result as mem_gen. Returns (y, F, S)."""
+    for t, nm in ((q, "q"), (k, "k"), (e, "e"), (v, "v"), (la, "la"), (b, "b")):
+        _need(t, torch.float32, f"mem_chunk {nm}")
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    F = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device) if F is None else F.clone()
+    S = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device) if S is None else S.clone()
+    y = torch.empty_like(q)
+    check(lib().ava_mem_chunk(_p(q), _p(k), _p(e), _p(v), _p(la), _p(b), BH, T, hs, g, float(m), float(cap),
+                              _p(F), _p(S), _p(y), _stream()), "ava_mem_chunk")
     return y, F, S
 
 

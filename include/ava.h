@@ -141,6 +141,16 @@ int ava_mem_scan(const float *q, const float *k, const float *e, const float *v,
                  const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,
                  float *y, ava_stream stream);
 
+/* ava_mem_scan's rule (same arguments, layout and result) in its chunked form: chunks of 16 tokens whose
+ * contractions with the carried F and S, and the intra-chunk products, run on the fp32 matrix cores; the
+ * recalls of a chunk solve one unit lower-triangular system. The bound clamp(F, +-cap) is applied at
+ * chunk ends, not per token (equal while no element of F reaches cap inside a chunk). Any T >= 0.
+ * Replaces delta_chunk / chunk_core (arch.rs:1151-1164, 1243-1327), the reference's CPU default for
+ * per-channel gates and momentum. */
+int ava_mem_chunk(const float *q, const float *k, const float *e, const float *v, const float *la,
+                  const float *b, int BH, int T, int hs, int g, float m, float cap, float *F, float *S,
+                  float *y, ava_stream stream);
+
 /* The gated delta rule F_t = alpha_t (I - beta_t k_t k_t^T) F_{t-1} + beta_t k_t v_t^T, y_t = F_t^T q_t
  * (F = W^T: with alpha = 1 this is W += beta (v - W k) k^T, y = W q) in its chunked (WY/UT) form,
  * chunks of 64 tokens: q, k, v [BH][T][64]; la = log alpha per token and head [BH][T] (NULL: alpha = 1);

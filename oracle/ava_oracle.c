@@ -433,6 +433,160 @@ void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float
     }
 }
 
+/* The form of the stack's memory for T > 1: 0 (default) = the token loop delta_rec with the bound at
+ * every token (the reference's GPU kernels and its CPU path under AVA_DELTA_REC=1, arch.rs:1329-1333),
+ * 1 = delta_chunk (the reference's default CPU prefill, no bound). The two agree to rounding until a
+ * head's fast weights reach the bound. */
+static int g_mem_chunked = 0;
+void orc_set_mem_chunked(int on) { g_mem_chunked = on != 0; }
+
+/* gpu/arch.rs:1166-1173 (chunk_len): 64 tokens for per-head gates, 16 per channel, halved until the
+ * length divides T. */
+static int chunk_len(int T, int g) {
+    int c = g == 1 ? 64 : 16;
+    while (c > 1 && T % c != 0) c /= 2;
+    return c;
+}
+
+/* gpu/arch.rs:1151-1164 (delta_chunk) with 1243-1327 (chunk_core): the recurrence of orc_mem_rec in chunks
+ * of c = chunk_len(T, g) tokens, without the bound (the chunked form has none). Inside a chunk, per key
+ * channel: D_im = prod_{t=m+1..i} alpha_t (the decay ratio <= 1, formed pair by pair), Gamma_i = D_i0
+ * alpha_0, K_ij = sum_{m=j..i} M^(m-j) D_im (as K_ij = D_ij + M K_i,j+1); with w = b k, ah = alpha b e:
+ *   Qw_ij = sum_ch q_i K_ij w_j, Qa_ij = sum_ch q_i K_ij ah_j (j <= i); Ke, Ae the same with e_i and
+ *   K_{i-1,j} (j < i);
+ *   (I + Ae) R = (e Gamma_{i-1}) F0 + (e M K_{i-1,0}) S0 + Ke V   (forward substitution);
+ *   Y = (q Gamma) F0 + (q M K_{i,0}) S0 + Qw V - Qa R;
+ *   F' = Gamma_{c-1} F0 + M K_{c-1,0} S0 + sum_j K_{c-1,j} (w_j v_j^T - ah_j r_j^T);
+ *   S' = M^c S0 + sum_j M^(c-1-j) (w_j v_j^T - ah_j r_j^T)   (M^p in double, rounded once).
+ * Arguments as orc_mem_rec (no cap). */
+void orc_mem_chunk(const float *q, const float *k, const float *e, const float *v, const float *la,
+                   const float *b, int BH, int T, int hs, int g, float m, float *F, float *S, float *y) {
+    const int c = chunk_len(T, g);
+    const int mom = m != 0.0f;
+#pragma omp parallel
+    {
+    const size_t cv = (size_t)c * hs, cc = (size_t)c * c;
+    float *al = (float *)malloc(sizeof(float) * cv), *w = (float *)malloc(sizeof(float) * cv);
+    float *ah = (float *)malloc(sizeof(float) * cv), *gm = (float *)malloc(sizeof(float) * cv);
+    float *mk = (float *)malloc(sizeof(float) * cv), *kl = (float *)malloc(sizeof(float) * cv);
+    float *R = (float *)malloc(sizeof(float) * cv);
+    float *qw = (float *)calloc(cc, sizeof(float)), *qa = (float *)calloc(cc, sizeof(float));
+    float *ke = (float *)calloc(cc, sizeof(float)), *ae = (float *)calloc(cc, sizeof(float));
+    float *D = (float *)malloc(sizeof(float) * hs), *K = (float *)malloc(sizeof(float) * hs);
+    float *F2 = (float *)malloc(sizeof(float) * hs * hs), *S2 = (float *)malloc(sizeof(float) * hs * hs);
+    float *mu = (float *)malloc(sizeof(float) * c);
+    double pw = 1.0;
+    for (int p = 0; p < c; p++) pw *= (double)m;
+    const float mc = (float)pw;
+    for (int j = 0; j < c; j++) {
+        double x = 1.0;
+        for (int p = 0; p < c - 1 - j; p++) x *= (double)m;
+        mu[j] = (float)x;
+    }
+#pragma omp for schedule(dynamic)
+    for (int bh = 0; bh < BH; bh++) {
+        float *f = F + (size_t)bh * hs * hs;
+        float *sm = mom ? S + (size_t)bh * hs * hs : NULL;
+        for (int t0 = 0; t0 < T; t0 += c) {
+            const size_t o0 = ((size_t)bh * T + t0) * hs, og0 = ((size_t)bh * T + t0) * g;
+            const float *qc = q + o0, *kc = k + o0, *ec = e + o0, *vc = v + o0;
+            for (int p = 0; p < c; p++)
+                for (int ch = 0; ch < hs; ch++) {
+                    const size_t og = og0 + (size_t)p * g + (g > 1 ? ch : 0);
+                    const float a = expf(la[og]), bw = b[og];
+                    al[p * hs + ch] = a;
+                    w[p * hs + ch] = bw * kc[p * hs + ch];
+                    ah[p * hs + ch] = (a * bw) * ec[p * hs + ch];
+                }
+            memset(qw, 0, sizeof(float) * cc);
+            memset(qa, 0, sizeof(float) * cc);
+            memset(ke, 0, sizeof(float) * cc);
+            memset(ae, 0, sizeof(float) * cc);
+            for (int i = 0; i < c; i++) {
+                for (int ch = 0; ch < hs; ch++) D[ch] = K[ch] = 0.0f;
+                for (int j = i; j >= 0; j--) {
+                    for (int ch = 0; ch < hs; ch++) {
+                        D[ch] = j == i ? 1.0f : D[ch] * al[(j + 1) * hs + ch];
+                        K[ch] = mom ? fmaf(m, K[ch], D[ch]) : D[ch];
+                    }
+                    float sw = 0.0f, sa = 0.0f, tw = 0.0f, ta = 0.0f;
+                    for (int ch = 0; ch < hs; ch++) {
+                        const float kw = K[ch] * w[j * hs + ch], ka = K[ch] * ah[j * hs + ch];
+                        sw = fmaf(qc[i * hs + ch], kw, sw);
+                        sa = fmaf(qc[i * hs + ch], ka, sa);
+                        if (i + 1 < c) {
+                            tw = fmaf(ec[(i + 1) * hs + ch], kw, tw);
+                            ta = fmaf(ec[(i + 1) * hs + ch], ka, ta);
+                        }
+                    }
+                    qw[i * c + j] = sw;
+                    qa[i * c + j] = sa;
+                    if (i + 1 < c) {
+                        ke[(i + 1) * c + j] = tw;
+                        ae[(i + 1) * c + j] = ta;
+                    }
+                    if (i == c - 1)
+                        for (int ch = 0; ch < hs; ch++) kl[j * hs + ch] = K[ch];
+                }
+                for (int ch = 0; ch < hs; ch++) {
+                    gm[i * hs + ch] = D[ch] * al[ch];
+                    mk[i * hs + ch] = m * K[ch];
+                }
+            }
+            /* recalls, then read-outs, column by column */
+            for (int col = 0; col < hs; col++) {
+                for (int i = 0; i < c; i++) {
+                    float x = 0.0f;
+                    for (int ch = 0; ch < hs; ch++) {
+                        const float ea = i == 0 ? ec[ch] : ec[i * hs + ch] * gm[(i - 1) * hs + ch];
+                        x = fmaf(ea, f[ch * hs + col], x);
+                        if (mom && i > 0) x = fmaf(ec[i * hs + ch] * mk[(i - 1) * hs + ch], sm[ch * hs + col], x);
+                    }
+                    for (int j = 0; j < i; j++) x = fmaf(ke[i * c + j], vc[j * hs + col], x);
+                    for (int j = 0; j < i; j++) x = fmaf(-ae[i * c + j], R[j * hs + col], x);
+                    R[i * hs + col] = x;
+                }
+                for (int i = 0; i < c; i++) {
+                    float x = 0.0f;
+                    for (int ch = 0; ch < hs; ch++) {
+                        x = fmaf(qc[i * hs + ch] * gm[i * hs + ch], f[ch * hs + col], x);
+                        if (mom) x = fmaf(qc[i * hs + ch] * mk[i * hs + ch], sm[ch * hs + col], x);
+                    }
+                    for (int j = 0; j <= i; j++) {
+                        x = fmaf(qw[i * c + j], vc[j * hs + col], x);
+                        x = fmaf(-qa[i * c + j], R[j * hs + col], x);
+                    }
+                    y[o0 + (size_t)i * hs + col] = x;
+                }
+            }
+            /* the state at the chunk's end */
+            for (int row = 0; row < hs; row++)
+                for (int col = 0; col < hs; col++) {
+                    const int pq = row * hs + col;
+                    float x = gm[(c - 1) * hs + row] * f[pq];
+                    if (mom) x = fmaf(mk[(c - 1) * hs + row], sm[pq], x);
+                    float z = mom ? mc * sm[pq] : 0.0f;
+                    for (int j = 0; j < c; j++) {
+                        const float wv = w[j * hs + row], av = ah[j * hs + row], kj = kl[j * hs + row];
+                        x = fmaf(wv * kj, vc[j * hs + col], x);
+                        x = fmaf(-(av * kj), R[j * hs + col], x);
+                        if (mom) {
+                            z = fmaf(wv * mu[j], vc[j * hs + col], z);
+                            z = fmaf(-(av * mu[j]), R[j * hs + col], z);
+                        }
+                    }
+                    F2[pq] = x;
+                    S2[pq] = z;
+                }
+            memcpy(f, F2, sizeof(float) * hs * hs);
+            if (mom) memcpy(sm, S2, sizeof(float) * hs * hs);
+        }
+    }
+    free(al); free(w); free(ah); free(gm); free(mk); free(kl); free(R);
+    free(qw); free(qa); free(ke); free(ae); free(D); free(K); free(F2); free(S2); free(mu);
+    }
+}
+
 /* ------------------------------------------------------------------ model */
 
 /* x [m, din] · W: the reference's W8A32 product (planes == 0) or the build's split planes. */
@@ -583,9 +737,17 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
                     memcpy(hla + dst, la + src, sizeof(float) * hs);
                     memcpy(hb + dst, bw + src, sizeof(float) * hs);
                 }
-        orc_mem_rec(hq, hk, he, hv, hla, hb, B * nh, T, hs, hs, cfg->momentum, cfg->cap,
-                    st->mem_f + (size_t)i * B * nh * hs * hs,
-                    cfg->momentum != 0.0f ? st->mem_s + (size_t)i * B * nh * hs * hs : NULL, hy);
+        /* the State path's memory (gpu/state.rs:954 -> arch.rs:1994): the bounded token loop, or with
+         * orc_set_mem_chunked(1) delta_chunk over T > 1 tokens (one token is always the fused step's
+         * bounded recurrence, gpu/model/fstep/arch.rs:256-337) */
+        if (T > 1 && g_mem_chunked)
+            orc_mem_chunk(hq, hk, he, hv, hla, hb, B * nh, T, hs, hs, cfg->momentum,
+                          st->mem_f + (size_t)i * B * nh * hs * hs,
+                          cfg->momentum != 0.0f ? st->mem_s + (size_t)i * B * nh * hs * hs : NULL, hy);
+        else
+            orc_mem_rec(hq, hk, he, hv, hla, hb, B * nh, T, hs, hs, cfg->momentum, cfg->cap,
+                        st->mem_f + (size_t)i * B * nh * hs * hs,
+                        cfg->momentum != 0.0f ? st->mem_s + (size_t)i * B * nh * hs * hs : NULL, hy);
         for (int bi = 0; bi < B; bi++)
             for (int t = 0; t < T; t++)
                 for (int e = 0; e < nh; e++)

@@ -89,6 +89,17 @@ void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float
                      const float *la, const float *b, int BH, int T, int hs, int g, double m,
                      double *F, double *S, double *y);
 
+/* gpu/arch.rs:1151-1164, 1243-1327 (delta_chunk / chunk_core): the same rule in chunks of
+ * chunk_len(T, g) tokens (arch.rs:1166-1173), without the bound (the reference's default CPU prefill,
+ * state.rs:954). Arguments as orc_mem_rec. */
+void orc_mem_chunk(const float *q, const float *k, const float *e, const float *v, const float *la,
+                   const float *b, int BH, int T, int hs, int g, float m, float *F, float *S, float *y);
+
+/* The stack memory's form for T > 1: 0 (default) the bounded token loop orc_mem_rec (the reference's
+ * GPU kernels; its CPU path under AVA_DELTA_REC=1, arch.rs:1329-1333), 1 orc_mem_chunk (the reference's
+ * default CPU prefill, state.rs:954 -> arch.rs:1994, which has no bound). */
+void orc_set_mem_chunked(int on);
+
 /* ---------------------------------------------------------------- model */
 
 typedef struct {

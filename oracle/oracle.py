@@ -44,6 +44,9 @@ def lib():
                                    C.c_int, C.c_int, C.c_int, i8p]
         L.orc_kwta.argtypes = [f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p, f32p]
         L.orc_mem_rec.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_float, C.c_float, f32p, C.c_void_p, f32p]
+        L.orc_mem_chunk.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_float, f32p, C.c_void_p, f32p]
+        L.orc_set_mem_chunked.argtypes = [C.c_int]
+        L.orc_set_mem_chunked.restype = None
         L.orc_mem_rec_f64.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_double, f64p, C.c_void_p, f64p]
         L.orc_rmsnorm.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p]
         L.orc_round_half.argtypes = [C.c_float]
@@ -191,6 +194,23 @@ def mem_rec(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
     lib().orc_mem_rec(q, k, e, v, la, b, BH, T, hs, g, float(m), float(cap), F,
                       S.ctypes.data if m != 0.0 else None, y)
     return y, F, S
+
+
+def mem_chunk(q, k, e, v, la, b, m=0.0, F=None, S=None):
+    """gpu/arch.rs:1151-1164, 1243-1327 (delta_chunk): mem_rec's rule in chunks, no bound. Returns (y, F, S)."""
+    q, k, e, v, la, b = (_c(z, np.float32) for z in (q, k, e, v, la, b))
+    BH, T, hs = q.shape
+    g = la.shape[2]
+    F = np.zeros((BH, hs, hs), np.float32) if F is None else _c(F, np.float32).copy()
+    S = np.zeros((BH, hs, hs), np.float32) if S is None else _c(S, np.float32).copy()
+    y = np.empty((BH, T, hs), np.float32)
+    lib().orc_mem_chunk(q, k, e, v, la, b, BH, T, hs, g, float(m), F, S.ctypes.data if m != 0.0 else None, y)
+    return y, F, S
+
+
+def set_mem_chunked(on: bool):
+    """The block stack's memory form for T > 1: chunked (the reference's default) or the token loop."""
+    lib().orc_set_mem_chunked(int(bool(on)))
 
 
 def mem_rec_f64(q, k, e, v, la, b, m=0.0, F=None, S=None):

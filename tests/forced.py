@@ -115,20 +115,24 @@ def check_state(so, st, envelope=None):
 
 
 def one_ulp_envelope(cfg, prm, ids, dec, so, threads=16):
-    """The oracle's own sensitivity: the same forward with every embedding value moved by one ulp and
-    the same forced decisions, against the unmoved run's state so. Per block, the relative change of
-    the fast weights (mem_f, mem_s). Two correct f32 implementations that sum in different orders
-    differ by about this much; a fast-weight recurrence (with momentum, and heads that grow towards the
-    state bound) can amplify a one-ulp difference far beyond 1e-4 over thousands of tokens."""
-    p2 = dict(prm)
-    p2["tok_emb"] = np.nextafter(np.asarray(prm["tok_emb"], np.float32), np.float32(np.inf)).astype(np.float32)
-    om2 = O.OracleModel(cfg, p2)
-    B = ids.shape[0]
-    _, s2, _ = forced_oracle(om2, ids, dec, om2.new_state(B, eng_cap=ids.shape[1]), threads=threads)
+    """The oracle's own sensitivity: the same forward with every embedding value moved by one ulp up,
+    and again moved one ulp down, with the same forced decisions, against the unmoved run's state so.
+    Per block, the larger relative change of the fast weights (mem_f, mem_s) over the two nudges (one
+    nudge is a single sample of a chaotic response). Two correct f32 implementations that sum in
+    different orders differ by about this much; a fast-weight recurrence (with momentum, and heads that
+    grow towards the state bound) can amplify a one-ulp difference far beyond 1e-4 over thousands of
+    tokens."""
     out = {}
-    for k in ("mem_f", "mem_s"):
-        if so.get(k) is not None and np.any(so[k]):
-            out[k] = [rel(s2[k][i], so[k][i]) for i in range(so[k].shape[0])]
+    B = ids.shape[0]
+    for direction in (np.inf, -np.inf):
+        p2 = dict(prm)
+        p2["tok_emb"] = np.nextafter(np.asarray(prm["tok_emb"], np.float32), np.float32(direction)).astype(np.float32)
+        om2 = O.OracleModel(cfg, p2)
+        _, s2, _ = forced_oracle(om2, ids, dec, om2.new_state(B, eng_cap=ids.shape[1]), threads=threads)
+        for k in ("mem_f", "mem_s"):
+            if so.get(k) is not None and np.any(so[k]):
+                r = [rel(s2[k][i], so[k][i]) for i in range(so[k].shape[0])]
+                out[k] = [max(a, b) for a, b in zip(out[k], r)] if k in out else r
     return out
 
 

@@ -137,3 +137,104 @@ def test_delta_chunk_rejects_ragged_length():
     q = torch.zeros((2, 100, 64), device="cuda")
     with pytest.raises(AvaError):
         ops.delta_rule_from(q, q, q, torch.zeros((2, 100), device="cuda"))
+
+
+# ----------------------------------------------------------------------------- the chunked general memory
+
+
+def chunk_case(BH, T, g, shift, seed):
+    """arch/tests.rs:701-722's inputs at head size 64: unit q, k, e; log alpha = logsigmoid(3 u + shift)
+    (shift -6: rates near 0.0025, products of rates underflow); b = 2 sigmoid(u); u uniform +-sqrt(3)."""
+    rng = np.random.default_rng(seed)
+    u = lambda *s: rng.uniform(-3 ** 0.5, 3 ** 0.5, s).astype(np.float32)
+    unit = lambda x: x / np.linalg.norm(x, axis=2, keepdims=True)
+    q, k, e = unit(u(BH, T, 64)), unit(u(BH, T, 64)), unit(u(BH, T, 64))
+    v = u(BH, T, 64)
+    z = (3.0 * u(BH, T, g) + shift).astype(np.float64)
+    la = (-(np.maximum(-z, 0) + np.log1p(np.exp(-np.abs(z))))).astype(np.float32)
+    b = (2.0 / (1.0 + np.exp(-u(BH, T, g).astype(np.float64)))).astype(np.float32)
+    return q, k, e, v, la, b
+
+
+def rel1(a, b):
+    """arch/tests.rs:705-708: max |a - b| over max(max |b|, 1)."""
+    return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1.0))
+
+
+@pytest.mark.parametrize("g,m,T,shift", [(64, 0.0, 32, 2.0), (1, 0.0, 32, 2.0), (64, 0.5, 40, 2.0), (1, 0.5, 24, 2.0),
+                                         (64, 0.0, 32, -6.0), (64, 0.7, 16, -6.0), (1, 0.0, 128, 1.0),
+                                         (64, 0.5, 5, 2.0), (64, 0.5, 2048, 3.0)])
+def test_mem_chunk_matches_token_loop(g, m, T, shift):
+    """arch/tests.rs:701-736 (chunked_memory_matches_the_token_loop) on the GPU: ava_mem_chunk against the
+    oracle's token loop (f32 and f64) from zero and from a carried state, per-head and per-channel gates,
+    with and without momentum, lengths that are not multiples of 16, strong forgetting (shift -6), and the
+    stack's form (per-channel, M 0.5) over 2048 tokens. Bar: the reference's 1e-4."""
+    BH = 8
+    print(f"mem_chunk g={g} m={m} T={T} shift={shift}", flush=True)
+    q, k, e, v, la, b = chunk_case(BH, T, g, shift, 11 + T + g)
+    if g == 1:
+        e = k.copy()
+    rng = np.random.default_rng(5)
+    init = [(None, None), ((rng.uniform(-1, 1, (BH, 64, 64)) * 0.3).astype(np.float32),
+                           (rng.uniform(-1, 1, (BH, 64, 64)) * 0.3).astype(np.float32) if m else None)]
+    from ava_amd import ops
+    for F0, S0 in init:
+        y, F, S = ops.mem_chunk(cuda(q), cuda(k), cuda(e), cuda(v), cuda(la), cuda(b), m=m,
+                                F=None if F0 is None else cuda(F0), S=None if S0 is None else cuda(S0))
+        y, F, S = host(y), host(F), host(S)
+        assert np.all(np.isfinite(y)) and np.all(np.isfinite(F))
+        for ref in (O.mem_rec(q, k, e, v, la, b, m=m, F=F0, S=S0), O.mem_rec_f64(q, k, e, v, la, b, m=m, F=F0, S=S0)):
+            yo, Fo, So = ref
+            assert rel1(y, yo) < 1e-4, rel1(y, yo)
+            assert rel1(F, Fo) < 1e-4, rel1(F, Fo)
+            if m:
+                assert rel1(S, So) < 1e-4, rel1(S, So)
+
+
+def test_mem_chunk_reads_back_values():
+    """alpha 1, e = k, b 1, no momentum, unit keys: reading k right after writing (k, v) returns v, also
+    inside a chunk (the recall solve) and across chunk ends."""
+    q, k, e, v, la, b = inputs(4, 50, 1, 5)
+    la[:] = 0.0
+    b[:] = 1.0
+    from ava_amd import ops
+    y, _, _ = ops.mem_chunk(cuda(k), cuda(k), cuda(k), cuda(v), cuda(la), cuda(b))
+    assert np.max(np.abs(host(y) - v)) < 5e-5
+
+
+def test_mem_chunk_equals_scan_and_rejects_bad_shapes():
+    """The chunked and the token-loop kernels agree (1e-4) on the general rule with a carried state; shape
+    errors come back as AvaError."""
+    from ava_amd import ops
+    from ava_amd._lib import AvaError
+    q, k, e, v, la, b = inputs(6, 300, 64, 21)
+    rng = np.random.default_rng(1)
+    F0 = (rng.standard_normal((6, 64, 64)) * 0.1).astype(np.float32)
+    S0 = (rng.standard_normal((6, 64, 64)) * 0.05).astype(np.float32)
+    a = ops.mem_chunk(*(cuda(z) for z in (q, k, e, v, la, b)), m=0.5, F=cuda(F0), S=cuda(S0))
+    c = ops.mem_gen(*(cuda(z) for z in (q, k, e, v, la, b)), m=0.5, F=cuda(F0), S=cuda(S0))
+    for x, z in zip(a, c):
+        assert rel(host(x), host(z)) < 1e-4
+    z = torch.zeros((2, 8, 32), device="cuda")
+    with pytest.raises(AvaError):
+        ops.mem_chunk(z, z, z, z, torch.zeros((2, 8, 1), device="cuda"), torch.zeros((2, 8, 1), device="cuda"))
+
+
+def test_mem_chunk_bounds_hot_heads_per_token():
+    """The bound clamp(F, +-cap) acts at every token once a wave's columns of F exceed cap / 8 at a chunk's
+    start (those chunks run token by token): from a state near a small cap the chunked kernel equals the
+    oracle's bounded token loop (gpu/mem_gen.rs:683), and every entry stays within the cap. Unit keys:
+    with keys of norm ~8 the bounded rule is chaotic and no two summation orders agree past ~30 tokens."""
+    q, k, e, v, la, b = inputs(4, 90, 64, 13, unit=True)
+    rng = np.random.default_rng(4)
+    cap = 0.05
+    F0 = rng.uniform(-0.04, 0.04, (4, 64, 64)).astype(np.float32)
+    S0 = rng.uniform(-0.02, 0.02, (4, 64, 64)).astype(np.float32)
+    from ava_amd import ops
+    y, F, S = ops.mem_chunk(cuda(q), cuda(k), cuda(e), cuda(v), cuda(la), cuda(b), m=0.5, cap=cap, F=cuda(F0),
+                            S=cuda(S0))
+    y, F, S = host(y), host(F), host(S)
+    yo, Fo, So = O.mem_rec(q, k, e, v, la, b, m=0.5, cap=cap, F=F0, S=S0)
+    assert np.max(np.abs(F)) <= cap
+    assert np.mean(np.abs(Fo) == np.float32(cap)) > 0.05  # the bound acts
+    assert rel(F, Fo) < 1e-4 and rel(y, yo) < 1e-4 and rel(S, So) < 1e-4

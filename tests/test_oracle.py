@@ -363,22 +363,79 @@ def tiny_model():
 
 
 def test_model_pieces_equal_one_pass():
-    """gpu/state/tests.rs:106 (pieces equal one pass): the forward of T tokens in one pass and in pieces
-    with the carried state (LIF, memory, engram store) give the same logits, bit for bit in the oracle
-    (every op is per row or sequential in time)."""
+    """gpu/state/tests.rs:93-121: a fresh state over the whole text gives the forward exactly, and pieces
+    (32+32, 17+30+17, 5 x 12 + 4, token by token) with the carried state (LIF, memory, engram store) give
+    one pass's logits within 1e-4 -- not bit for bit, since the memory of a piece of T > 1 tokens runs in
+    chunks of chunk_len(T) (arch.rs:1166-1173) and a one-token piece as the fused step's recurrence."""
     mdl, cfg = tiny_model()
     rng = np.random.default_rng(0)
-    ids = rng.integers(0, cfg["vocab"], (2, 12)).astype(np.int32)
-    full, st_full, _ = mdl.forward(ids, state=mdl.new_state(2, eng_cap=12), planes=3)
-    st = mdl.new_state(2, eng_cap=12)
-    parts = []
-    for a, b in [(0, 5), (5, 6), (6, 12)]:
-        lg, st, _ = mdl.forward(ids[:, a:b], state=st, planes=3)
-        parts.append(lg.reshape(2, b - a, -1))
-    pieces = np.concatenate(parts, axis=1).reshape(full.shape)
-    assert np.array_equal(pieces.view(np.uint32), full.view(np.uint32))
-    for key in ("lif_v", "mem_f", "mem_s"):
-        assert np.array_equal(st[key], st_full[key])
+    B, T = 2, 64
+    ids = rng.integers(0, cfg["vocab"], (B, T)).astype(np.int32)
+    full, st_full, _ = mdl.forward(ids, state=mdl.new_state(B, eng_cap=T), planes=3)
+    again, _, _ = mdl.forward(ids, state=mdl.new_state(B, eng_cap=T), planes=3)
+    assert np.array_equal(again.view(np.uint32), full.view(np.uint32))
+    for pieces in ([32, 32], [17, 30, 17], [5] * 12 + [4], [1] * 64):
+        st = mdl.new_state(B, eng_cap=T)
+        parts, a = [], 0
+        for n in pieces:
+            lg, st, _ = mdl.forward(ids[:, a:a + n], state=st, planes=3)
+            parts.append(lg.reshape(B, n, -1))
+            a += n
+        got = np.concatenate(parts, axis=1).reshape(full.shape)
+        assert np.max(np.abs(got - full)) < 1e-4, pieces
+        for key in ("lif_v", "mem_f", "mem_s"):
+            assert np.max(np.abs(st[key] - st_full[key])) <= 1e-4 * max(1.0, np.max(np.abs(st_full[key]))), key
+
+
+def test_mem_chunk_matches_the_token_loop():
+    """gpu/arch/tests.rs:701-736 (chunked_memory_matches_the_token_loop): the chunked form against the
+    float64 token loop, per-head and per-channel gates, with and without momentum, from zero and from a
+    carried state, lengths that are not multiples of 16, and forgetting strong enough that products of
+    rates underflow (shift -6); bar max |d| / max(max |ref|, 1) < 1e-4."""
+    def case(BH, T, g, shift, seed):
+        rng = np.random.default_rng(seed)
+        u = lambda *sh: rng.uniform(-3 ** 0.5, 3 ** 0.5, sh).astype(F)
+        unit = lambda x: x / np.linalg.norm(x, axis=2, keepdims=True)
+        q, k, e, v = unit(u(BH, T, 64)), unit(u(BH, T, 64)), unit(u(BH, T, 64)), u(BH, T, 64)
+        z = (3.0 * u(BH, T, g) + shift).astype(np.float64)
+        la = (-(np.maximum(-z, 0) + np.log1p(np.exp(-np.abs(z))))).astype(F)
+        b = (2.0 / (1.0 + np.exp(-u(BH, T, g).astype(np.float64)))).astype(F)
+        return q, k, e if g > 1 else k, v, la, b
+
+    rel1 = lambda a, b: float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1.0))
+    for n, (g, m, T, shift) in enumerate([(64, 0.0, 32, 2.0), (1, 0.0, 32, 2.0), (64, 0.5, 40, 2.0), (1, 0.5, 24, 2.0),
+                                          (64, 0.0, 32, -6.0), (64, 0.7, 16, -6.0), (1, 0.0, 128, 1.0)]):
+        q, k, e, v, la, b = case(2, T, g, shift, 100 * n)
+        rng = np.random.default_rng(100 * n + 7)
+        F0 = (rng.uniform(-1, 1, (2, 64, 64)) * 0.3).astype(F)
+        S0 = (rng.uniform(-1, 1, (2, 64, 64)) * 0.3).astype(F) if m else None
+        for f0, s0 in ((None, None), (F0, S0)):
+            y, Fo, So = O.mem_chunk(q, k, e, v, la, b, m=m, F=f0, S=s0)
+            y64, F64, S64 = O.mem_rec_f64(q, k, e, v, la, b, m=m, F=f0, S=s0)
+            assert np.all(np.isfinite(y))
+            assert rel1(y, y64) < 1e-4 and rel1(Fo, F64) < 1e-4, (n, rel1(y, y64), rel1(Fo, F64))
+            if m:
+                assert rel1(So, S64) < 1e-4
+
+
+def test_mem_chunk_planted_mistakes_fail():
+    """The chunk-form check catches plausible slips: the same rule with the erase key's rate dropped
+    (ah = b e) or the momentum's power one short differs from the token loop far beyond 1e-4."""
+    rng = np.random.default_rng(3)
+    BH, T = 2, 48
+    unit = lambda x: x / np.linalg.norm(x, axis=2, keepdims=True)
+    q, k, e = (unit(rng.standard_normal((BH, T, 64)).astype(F)) for _ in range(3))
+    v = rng.standard_normal((BH, T, 64)).astype(F)
+    la = (-np.exp(rng.standard_normal((BH, T, 64)) - 1.5)).astype(F)
+    b = (2.0 / (1.0 + np.exp(-rng.standard_normal((BH, T, 64))))).astype(F)
+    y64, F64, _ = O.mem_rec_f64(q, k, e, v, la, b, m=0.5)
+    y, Fo, _ = O.mem_chunk(q, k, e, v, la, b, m=0.5)
+    assert np.max(np.abs(Fo - F64)) < 1e-4 * max(1.0, np.max(np.abs(F64)))
+    # a slipped rate in the erase key, or the momentum applied one step less, is visible
+    y2, F2, _ = O.mem_rec_f64(q, k, e, v, la, b, m=0.25)
+    assert np.max(np.abs(Fo - F2)) > 1e-2 * max(1.0, np.max(np.abs(F64)))
+    y3, F3, _ = O.mem_rec_f64(q, k, e * np.exp(-la), v, la, b, m=0.5)
+    assert np.max(np.abs(y - y3)) > 1e-2 * max(1.0, np.max(np.abs(y64)))
 
 
 def test_model_planes_near_the_reference_products():
