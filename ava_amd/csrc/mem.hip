@@ -692,21 +692,19 @@ __device__ __forceinline__ void chunk_state(const ChunkLds &s, int wave, int lan
     }
 }
 
-// The chunked memory. FUSED: the block's memory from its raw projections (FusedArgs, the staging of
-// mem_fused_kernel: unit q, k, erase key, value residual, gates from the rank-r read-outs); else the
-// staged inputs of ava_mem_scan's layout (MemArgs; G1: one gate per row and head).
-template <bool FUSED, bool G1, bool MOM>
-__global__ __launch_bounds__(256, 2) void mem_chunk_kernel(FusedArgs pf, MemArgs pd) {
+// The chunked memory over the inputs of ava_mem_scan's layout (G1: one gate per row and head).
+template <bool G1, bool MOM>
+__global__ __launch_bounds__(256, 2) void mem_chunk_kernel(MemArgs p) {
     __shared__ __attribute__((aligned(16))) ChunkLds s;
-    const int T = FUSED ? pf.T : pd.T, nh = FUSED ? pf.nh : pd.nh;
-    const float M = FUSED ? pf.m : pd.m, cap = FUSED ? pf.cap : pd.cap;
+    const int T = p.T, nh = p.nh;
+    const float M = p.m, cap = p.cap;
     const int bh = blockIdx.x, bi = bh / nh, hh = bh - bi * nh;
     const int tid = threadIdx.x, lane_ = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     f32x4 Fr[4], Sr[4];
-    float *Fh = (FUSED ? pf.F : pd.F) + (size_t)bh * HS * HS;
-    float *Sh = MOM ? (FUSED ? pf.S : pd.S) + (size_t)bh * HS * HS : nullptr;
+    float *Fh = p.F + (size_t)bh * HS * HS;
+    float *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
@@ -716,162 +714,66 @@ __global__ __launch_bounds__(256, 2) void mem_chunk_kernel(FusedArgs pf, MemArgs
             Sr[mt][r] = MOM ? Sh[o] : 0.0f;
         }
 
-    // FUSED: the head's constants at this lane's channel
-    const int d = nh * HS;
-    const size_t row0 = (size_t)bi * T;
-    float offc = 0.0f, bah = 0.0f, bbh = 0.0f, p0 = 0.0f, p1 = 0.0f;
-    if (FUSED) {
-        offc = pf.off[hh * HS + lane_];
-        bah = pf.ba[hh];
-        bbh = pf.bb[hh];
-        if (pf.vres) {
-            p0 = pf.vres[0] * 1.0f + 1.0f;
-            p1 = pf.vres[1];
-        }
-    }
-    const size_t base = (size_t)bi * T * pd.ld + (size_t)hh * HS;
-    const size_t gbase = G1 ? (size_t)bi * T * pd.ldg + hh : (size_t)bi * T * pd.ldg + (size_t)hh * HS;
-    const size_t ybase = FUSED ? row0 * d + (size_t)hh * HS : (size_t)bi * T * pd.ldy + (size_t)hh * HS;
-    const int ldy = FUSED ? d : pd.ldy;
-    float *yout = FUSED ? pf.y : pd.y;
-
-    // the raw inputs of a chunk, loaded one chunk ahead: FUSED, wave w's positions 4w..4w+3 with lane =
-    // channel; else thread -> (position tid / 16, channels 4 (tid % 16)..+3)
-    const int ldp = 5 * d, ldgf = FUSED ? 2 * nh + 2 * pf.r : 0;
-    float rq[4], rk[4], rv[4], rw[4], rv0[4], rz[4], rza[4], rzb[4];
+    const size_t base = (size_t)bi * T * p.ld + (size_t)hh * HS;
+    const size_t gbase = G1 ? (size_t)bi * T * p.ldg + hh : (size_t)bi * T * p.ldg + (size_t)hh * HS;
+    const size_t ybase = (size_t)bi * T * p.ldy + (size_t)hh * HS;
+    // the raw inputs of a chunk, loaded one chunk ahead: thread -> (position tid / 16, channels
+    // 4 (tid % 16)..+3)
+    const int sp = tid >> 4, si = (tid & 15) * 4;
     f32x4 dq, dk, de, dv, dl, db;
-    auto load = [&](int t0, int lane) {
-        if (FUSED) {
-            const int c = hh * HS + lane;
-#pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const int t = min(t0 + wave * 4 + st, T - 1);  // past the end: the last position, never used
-                const size_t rw_ = row0 + t;
-                const float *Pr = pf.P + rw_ * ldp, *Gr = pf.G + rw_ * ldgf;
-                rq[st] = Pr[c];
-                rk[st] = Pr[d + c];
-                rv[st] = Pr[2 * d + c];
-                rw[st] = Pr[3 * d + c];
-                rv0[st] = pf.v0 ? pf.v0[rw_ * d + c] : 0.0f;
-                rz[st] = (lane & 31) < pf.r ? Gr[2 * nh + (lane < 32 ? lane : lane - 32 + pf.r)] : 0.0f;
-                rza[st] = Gr[hh];
-                rzb[st] = Gr[nh + hh];
-            }
+    auto load = [&](int t0) {
+        const int t = min(t0 + sp, T - 1);  // past the end: the last position, never used
+        const size_t o = base + (size_t)t * p.ld + si;
+        dq = ld4(p.q + o);
+        dk = ld4(p.k + o);
+        de = ld4(p.e + o);
+        dv = ld4(p.v + o);
+        if (G1) {
+            const float l = p.la[gbase + (size_t)t * p.ldg], b = p.b[gbase + (size_t)t * p.ldg];
+            dl = f32x4{l, l, l, l};
+            db = f32x4{b, b, b, b};
         } else {
-            const int t = min(t0 + (tid >> 4), T - 1), si = (tid & 15) * 4;
-            const size_t o = base + (size_t)t * pd.ld + si;
-            dq = ld4(pd.q + o);
-            dk = ld4(pd.k + o);
-            de = ld4(pd.e + o);
-            dv = ld4(pd.v + o);
-            if (G1) {
-                const float l = pd.la[gbase + (size_t)t * pd.ldg], b = pd.b[gbase + (size_t)t * pd.ldg];
-                dl = f32x4{l, l, l, l};
-                db = f32x4{b, b, b, b};
-            } else {
-                const size_t og = gbase + (size_t)t * pd.ldg + si;
-                dl = ld4(pd.la + og);
-                db = ld4(pd.b + og);
-            }
+            const size_t og = gbase + (size_t)t * p.ldg + si;
+            dl = ld4(p.la + og);
+            db = ld4(p.b + og);
         }
     };
-    // FUSED: the B operand of the rank-r read-out product (wa2/wb2 rows 4 ks + lane / 16, column
-    // 16 wave + lane % 16), the same for every chunk
-    float wA[8], wB[8];
-    if (FUSED) {
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            const int jj = 4 * ks + (lane_ >> 4), cc = hh * HS + 16 * wave + (lane_ & 15);
-            wA[ks] = jj < pf.r ? pf.wa2[(size_t)jj * d + cc] : 0.0f;
-            wB[ks] = jj < pf.r ? pf.wb2[(size_t)jj * d + cc] : 0.0f;
-        }
-    }
-    load(0, lane_);
+    load(0);
 
     float mu[4], Mn = 0.0f;  // M^(n-1-j) at j = 4g + r (0 past n), M^n
-    int nf = 0, nprev = -1;
+    int nprev = -1;
     for (int t0 = 0; t0 < T; t0 += CK) {
         const int n = min(CK, T - t0);
         // the lane index passes through an empty asm each chunk, so the many lane-dependent LDS addresses
         // are formed where they are used instead of being hoisted out of the loop and held in registers
         int lane = lane_;
         asm volatile("" : "+v"(lane));
-        const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl, c = hh * HS + lane;
+        const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl;
         if (n != nprev) {
 #pragma unroll
             for (int r = 0; r < 4; r++) mu[r] = 4 * g + r < n ? mpow(M, n - 1 - (4 * g + r)) : 0.0f;
             Mn = mpow(M, n);
             nprev = n;
         }
-        if (FUSED) {
-            __syncthreads();  // the previous chunk's LDS reads are done
-            float *zs = &s.pm[0][0][0];  // the z rows (za | zb per position), in the pair matrices' space
+        f32x4 a4 = {1.0f, 1.0f, 1.0f, 1.0f}, w4 = {0.0f, 0.0f, 0.0f, 0.0f}, x4 = w4;
+        if (t0 + sp < T) {
 #pragma unroll
-            for (int st = 0; st < 4; st++) zs[swz(4 * wave + st, lane)] = rz[st];
-            __syncthreads();
-            // the rank-r read-outs of all 16 positions for this wave's 16 channels on the matrix cores
-            f32x4 la4 = {0.0f, 0.0f, 0.0f, 0.0f}, lb4 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                la4 = __builtin_amdgcn_mfma_f32_16x16x4f32(zs[swz(cl, 4 * ks + g)], wA[ks], la4, 0, 0, 0);
-                lb4 = __builtin_amdgcn_mfma_f32_16x16x4f32(zs[swz(cl, 32 + 4 * ks + g)], wB[ks], lb4, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                s.w[rsw(4 * g + r, col)] = la4[r];
-                s.ah[rsw(4 * g + r, col)] = lb4[r];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const int sp = 4 * wave + st, t = t0 + sp, o = rsw(sp, lane), oz = swz(sp, lane);
-                const float lra = s.w[o], lrb = s.ah[o];
-                const float ek = rk[st] + rw[st];
-                const float sq = wsum(rq[st] * rq[st]), sk = wsum(rk[st] * rk[st]), se = wsum(ek * ek);
-                float qn = rq[st] * rsqrtf(sq + 1e-6f);
-                const float kn = rk[st] * rsqrtf(sk + 1e-6f);
-                float en = ek * rsqrtf(se + 1e-6f);
-                float v = rv[st];
-                if (pf.v0_out && t < T) pf.v0_out[(row0 + t) * d + c] = v;
-                if (pf.v0) v = v * p0 + rv0[st] * p1;
-                float a = gate_alpha(((rza[st] + bah) + offc) + lra);
-                const float bw = gate_sig((rzb[st] + bbh) + lrb) * 2.0f;
-                float bk = bw * kn, abe = (a * bw) * en;
-                if (t < T) {
-                    if (!finite6(qn, en, v, a, bk, abe)) nf = 1;
-                } else {
-                    qn = en = v = bk = abe = 0.0f;  // positions past the end change nothing
-                    a = 1.0f;
-                }
-                s.q[oz] = qn;
-                s.e[oz] = en;
-                s.v[o] = v;
-                s.a[o] = a;
-                s.w[o] = bk;
-                s.ah[o] = abe;
+            for (int cc = 0; cc < 4; cc++) {
+                a4[cc] = expf(dl[cc]);
+                w4[cc] = db[cc] * dk[cc];
+                x4[cc] = (a4[cc] * db[cc]) * de[cc];
             }
         } else {
-            const int sp = tid >> 4, si = (tid & 15) * 4, t = t0 + sp;
-            f32x4 a4 = {1.0f, 1.0f, 1.0f, 1.0f}, w4 = {0.0f, 0.0f, 0.0f, 0.0f}, x4 = w4;
-            if (t < T) {
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    a4[cc] = expf(dl[cc]);
-                    w4[cc] = db[cc] * dk[cc];
-                    x4[cc] = (a4[cc] * db[cc]) * de[cc];
-                }
-            } else {
-                dq = de = dv = w4;  // positions past the end change nothing
-            }
-            __syncthreads();  // the previous chunk's LDS reads are done
-            st4s(s.q, sp, si, dq);
-            st4s(s.e, sp, si, de);
-            *reinterpret_cast<f32x4 *>(&s.v[rsw(sp, si)]) = dv;
-            *reinterpret_cast<f32x4 *>(&s.a[rsw(sp, si)]) = a4;
-            *reinterpret_cast<f32x4 *>(&s.w[rsw(sp, si)]) = w4;
-            *reinterpret_cast<f32x4 *>(&s.ah[rsw(sp, si)]) = x4;
+            dq = de = dv = w4;  // positions past the end change nothing
         }
-        if (t0 + CK < T) load(t0 + CK, lane);  // in flight during this chunk's work
+        __syncthreads();  // the previous chunk's LDS reads are done
+        st4s(s.q, sp, si, dq);
+        st4s(s.e, sp, si, de);
+        *reinterpret_cast<f32x4 *>(&s.v[rsw(sp, si)]) = dv;
+        *reinterpret_cast<f32x4 *>(&s.a[rsw(sp, si)]) = a4;
+        *reinterpret_cast<f32x4 *>(&s.w[rsw(sp, si)]) = w4;
+        *reinterpret_cast<f32x4 *>(&s.ah[rsw(sp, si)]) = x4;
+        if (t0 + CK < T) load(t0 + CK);  // in flight during this chunk's work
         __syncthreads();
         chunk_pairs<MOM>(s, wave, lane, n, M);
         __syncthreads();
@@ -879,22 +781,7 @@ __global__ __launch_bounds__(256, 2) void mem_chunk_kernel(FusedArgs pf, MemArgs
         chunk_state<MOM>(s, wave, lane, n, Mn, mu, M, cap, Fr, Sr, Y);
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            if (4 * g + r < n) yout[ybase + (size_t)(t0 + 4 * g + r) * ldy + col] = Y[r];
-    }
-
-    if (FUSED) {
-        // any lane that staged a non-finite value: a flag word in the (now unused) pair matrices, so the
-        // workgroup stays at 40 KB of LDS
-        int *flag = reinterpret_cast<int *>(&s.pm[0][0][0]);
-        __syncthreads();
-        if (tid == 0) *flag = 0;
-        __syncthreads();
-        if (nf) *flag = 1;
-        __syncthreads();
-        if (*flag) {
-            if (tid == 0 && pf.bad) pf.bad[bi] = 1;
-            return;  // nothing committed
-        }
+            if (4 * g + r < n) p.y[ybase + (size_t)(t0 + 4 * g + r) * p.ldy + col] = Y[r];
     }
     // the store addresses from a laundered lane index, so they are not the loads' addresses kept alive
     // across the scan
@@ -1056,8 +943,8 @@ int mem_block(const float *P, const float *G, int B, int T, int nh, int r, const
         AVA_LAUNCHED("mem_step");
         return AVA_OK;
     }
-    // the token loop (the chunk's inputs are staged by the scan's own waves): faster here than the
-    // chunked form, whose VALU and matrix phases do not overlap in one wave
+    // the token loop (the chunk's inputs are staged by the scan's own waves); the chunked form
+    // (mem_chunk_strided) measures slower on this shape
     if (m != 0.0f) mem_fused_kernel<true, false><<<B * nh, 256, 0, st>>>(a);
     else mem_fused_kernel<false, false><<<B * nh, 256, 0, st>>>(a);
     AVA_LAUNCHED("mem_block");
@@ -1075,14 +962,13 @@ int mem_chunk_strided(const float *q, const float *k, const float *e, const floa
                 "mem_chunk: B=%d T=%d nh=%d ld=%d ldg=%d ldy=%d", B, T, nh, ld, ldg, ldy);
     if (B == 0 || T == 0) return AVA_OK;
     MemArgs a{q, k, e, v, la, b, T, nh, ld, ldg, ldy, m, cap, F, S, y};
-    const FusedArgs none{};
     dim3 grid(B * nh), block(256);
     if (g == 1) {
-        if (m != 0.0f) mem_chunk_kernel<false, true, true><<<grid, block, 0, st>>>(none, a);
-        else mem_chunk_kernel<false, true, false><<<grid, block, 0, st>>>(none, a);
+        if (m != 0.0f) mem_chunk_kernel<true, true><<<grid, block, 0, st>>>(a);
+        else mem_chunk_kernel<true, false><<<grid, block, 0, st>>>(a);
     } else {
-        if (m != 0.0f) mem_chunk_kernel<false, false, true><<<grid, block, 0, st>>>(none, a);
-        else mem_chunk_kernel<false, false, false><<<grid, block, 0, st>>>(none, a);
+        if (m != 0.0f) mem_chunk_kernel<false, true><<<grid, block, 0, st>>>(a);
+        else mem_chunk_kernel<false, false><<<grid, block, 0, st>>>(a);
     }
     AVA_LAUNCHED("mem_chunk");
     return AVA_OK;

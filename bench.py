@@ -432,6 +432,114 @@ class MemBwd:
                                           f"heads, T={T}, one thread, {dt:.2f} s"}
 
 
+class MemChunk:
+    """The chunked fast-weight memory (ava_mem_chunk, delta_chunk / chunk_core) at config[3]'s per-block
+    shape: 64 streams x 16 heads x 2048 tokens, unit q, k, e, v ~N(0,1), per-channel log alpha =
+    log U(0.85, 0.999), b ~U(0.1, 1.9), momentum 0.5, from a zero state. The token loop (ava_mem_scan) on
+    the same inputs is timed beside it."""
+
+    name = "mem_chunk"
+    kernel = "mem_chunk_kernel"
+
+    def __init__(self, B=64, H=16, T=2048):
+        import torch
+        from ava_amd import _lib
+
+        BH = B * H
+        self.BH, self.T = BH, T
+        self.L = _lib.lib()
+        g = torch.Generator(device="cuda").manual_seed(13)
+
+        def unit():
+            x = torch.randn((BH, T, 64), device="cuda", generator=g)
+            return (x / x.norm(dim=2, keepdim=True)).contiguous()
+
+        self.q, self.k, self.e = unit(), unit(), unit()
+        self.v = torch.randn((BH, T, 64), device="cuda", generator=g)
+        self.la = torch.log(torch.rand((BH, T, 64), device="cuda", generator=g) * 0.149 + 0.85)
+        self.b = torch.rand((BH, T, 64), device="cuda", generator=g) * 1.8 + 0.1
+        self.F = torch.zeros((BH, 64, 64), dtype=torch.float32, device="cuda")
+        self.S = torch.zeros_like(self.F)
+        self.y = torch.empty_like(self.q)
+        self.tokens = B * T
+        # per chunk of 16 and head: the contractions with F and S (32 x 128 x 64 and 128 x 32 x 64 MACs)
+        # and the intra-chunk products Ke V, Qw V, Qa R (3 x 16 x 16 x 64), 2 FLOPs per MAC
+        self.flops = BH * (T // 16) * 2 * (2 * 32 * 128 * 64 + 3 * 16 * 16 * 64)
+        self.bytes = BH * T * 64 * 4 * 7 + 2 * 2 * BH * 64 * 64 * 4  # 6 inputs + y; F, S in and out
+        self.config = {"workload": "memory forward chunked config[3] block", "B": B, "heads": H, "T": T, "hs": 64,
+                       "gates": "per channel", "momentum": 0.5, "chunk": 16}
+        self.dtype = "f32"
+
+    def _run(self, fn, stream):
+        import ctypes as C
+        from ava_amd._lib import check
+
+        p = lambda t: C.c_void_p(t.data_ptr())
+        self.F.zero_()
+        self.S.zero_()
+        check(fn(p(self.q), p(self.k), p(self.e), p(self.v), p(self.la), p(self.b), self.BH, self.T, 64, 64, 0.5, 1e5,
+                 p(self.F), p(self.S), p(self.y), stream))
+
+    def step(self, stream, ev=None):
+        # the events bracket the launch only (the state is cleared before)
+        import ctypes as C
+        from ava_amd._lib import check
+
+        p = lambda t: C.c_void_p(t.data_ptr())
+        self.F.zero_()
+        self.S.zero_()
+        if ev: ev[0].record()
+        check(self.L.ava_mem_chunk(p(self.q), p(self.k), p(self.e), p(self.v), p(self.la), p(self.b), self.BH,
+                                   self.T, 64, 64, 0.5, 1e5, p(self.F), p(self.S), p(self.y), stream))
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.flops / kernel_s / 1e12
+        return {"bound": "mfma", "achieved": a, "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": a / F32_MFMA_PEAK_TFLOPS, "flops_per_launch": self.flops, "hbm_bytes_per_launch": self.bytes,
+                "hbm_gbs": self.bytes / kernel_s / 1e9}
+
+    def extra(self):
+        # the token loop on the same inputs, same stream, 5 launches
+        import torch
+
+        st = torch.cuda.current_stream()
+        sp = __import__("ctypes").c_void_p(st.cuda_stream)
+        self._run(self.L.ava_mem_scan, sp)
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            self._run(self.L.ava_mem_scan, sp)
+            b.record()
+            torch.cuda.synchronize()
+            ms.append(a.elapsed_time(b))
+        return {"token_loop_ms": float(np.median(ms)), "token_loop_kernel": "mem_scan_kernel"}
+
+    def cpu_baseline(self):
+        from oracle import oracle as O
+
+        O.set_threads(1)
+        BH, T = 256, self.T  # a quarter of the 1024 heads: about 12 s on one thread
+        rng = np.random.default_rng(13)
+
+        def unit():
+            x = rng.standard_normal((BH, T, 64)).astype(np.float32)
+            return x / np.linalg.norm(x, axis=2, keepdims=True)
+
+        q, k, e = unit(), unit(), unit()
+        v = rng.standard_normal((BH, T, 64)).astype(np.float32)
+        la = np.log(rng.uniform(0.85, 0.999, (BH, T, 64))).astype(np.float32)
+        b = rng.uniform(0.1, 1.9, (BH, T, 64)).astype(np.float32)
+        t0 = time.perf_counter()
+        O.mem_chunk(q, k, e, v, la, b, m=0.5)
+        dt = time.perf_counter() - t0
+        return {"value": BH * T / dt / 16, "unit": "tokens/s (B x T per second, 16 heads per token)", "cores": 1,
+                "kind": "port", "sample": f"oracle chunked memory (chunk_core, arch.rs:1243-1327), {BH} of {self.BH} "
+                                          f"heads, T={T}, one thread, {dt:.2f} s"}
+
+
 class Copy:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the FETCH/WRITE_SIZE counters."""
 
@@ -803,7 +911,7 @@ class Decode:
 
 
 WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "greedy": Greedy, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy,
-             "lif_bwd": LifBwd, "mem_bwd": MemBwd}
+             "lif_bwd": LifBwd, "mem_bwd": MemBwd, "mem_chunk": MemChunk}
 DEFAULT = "stack"
 
 
