@@ -200,6 +200,38 @@ class Gemm:
         a = self.ops / kernel_s / 1e12
         return {"bound": "mfma", "achieved": a, "peak": I8_PEAK_TOPS, "unit": "TOP/s", "frac": a / I8_PEAK_TOPS}
 
+    def extra(self):
+        """The same integer work through the platform's library GEMM (torch._int_mm, hipBLASLt on ROCm):
+        the planes stacked as rows, [P m, k] x [k, n] int8 -> int32 (no plane combine, no f32 output
+        scaling), 5 launches; and its 8192-cube rate. A reference point for the product kernel only."""
+        import torch
+
+        out = {}
+        try:
+            a = self.xq.reshape(self.planes * self.m, -1)[:, :self.k].contiguous()
+            b = self.qw.qt[:, :self.k].t() if hasattr(self.qw, "qt") else None
+            if b is None:
+                g = torch.Generator(device="cuda").manual_seed(4)
+                b = torch.randint(-127, 128, (self.n, self.k), dtype=torch.int8, device="cuda", generator=g).t()
+            for name, (x, y) in (("library_int_mm", (a, b)),
+                                 ("library_int_mm_8192", (torch.ones((8192, 8192), dtype=torch.int8, device="cuda"),
+                                                          torch.ones((8192, 8192), dtype=torch.int8,
+                                                                     device="cuda").t()))):
+                torch._int_mm(x, y)
+                torch.cuda.synchronize()
+                s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s0.record()
+                for _ in range(5):
+                    torch._int_mm(x, y)
+                s1.record()
+                torch.cuda.synchronize()
+                ms = s0.elapsed_time(s1) / 5
+                ops = 2.0 * x.shape[0] * x.shape[1] * y.shape[1]
+                out[name] = {"ms": ms, "tops": ops / ms / 1e9, "shape": [x.shape[0], x.shape[1], y.shape[1]]}
+        except Exception as ex:  # the reference point is optional
+            out["library_int_mm_error"] = str(ex)
+        return out
+
     def cpu_baseline(self):
         from oracle import oracle as O
 
