@@ -47,7 +47,8 @@ class Params(C.Structure):
 class State(C.Structure):
     _fields_ = [("lif_v", vp), ("lif_s", vp), ("lif_a", vp), ("mem_f", vp), ("mem_s", vp),
                 ("eng_k", vp), ("eng_v", vp), ("eng_cap", i32), ("eng_len", i32),
-                ("cb_tab", vp), ("cb_scale", vp), ("cb_code", vp), ("eng_len_dev", vp)]
+                ("cb_tab", vp), ("cb_scale", vp), ("cb_code", vp), ("eng_len_dev", vp), ("eng_reads", vp),
+                ("eng_age", vp)]
 
 
 _lib = None

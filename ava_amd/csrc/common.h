@@ -213,6 +213,11 @@ int engram_read(const float *qkv, int ldqkv, int B, int T, int de, int nh, void 
                 int n0, int *n0p, float *out, float *part, size_t part_floats, hipStream_t st,
                 const PostRead &post = {});
 int engram_advance(int *n0p, int T, int cap, hipStream_t st);
+// The least-read rule's counts after a read of T queries per stream (q rows ldq floats apart, the store
+// already holding the T new keys after its n0 old ones): reads and age [B][cap] advance as
+// gpu/memory.rs:700-738 keeps them. ml: 2 B T nh floats of scratch.
+int engram_count(const float *q, int ldq, const void *ks, int kv_half, int cap, int n0, int B, int T, int de, int nh,
+                 float *ml, float *reads, float *age, hipStream_t st);
 // cb.hip: the cerebellum head (code with its unit lists, read-out with the online table, learning)
 int cb_code(const float *xf, const int32_t *ids, const float *emb, int n, int d, int vocab, const uint32_t *widx,
             const float *wsgn, int g, int k, int T, float *code, float *keep, int *lcnt, int *lidx, float *lval,

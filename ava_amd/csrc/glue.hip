@@ -799,6 +799,84 @@ __global__ __launch_bounds__(256) void embed_rms_kernel(const int32_t *__restric
     row_rms_planes<P, NV>(v, lane, d, gain, (size_t)n, (size_t)row, xq, xexp, ldq, nullptr);
 }
 
+// ------------------------------------------------------------------ the least-read rule's counts
+//
+// gpu/memory.rs:700-738 (StoreUse::count_reads): after a read of T queries per stream, slot j of the
+// store gets the attention mass of every query that sees it before its own key (the old slots j < n0,
+// and new slot n0 + i for the queries after i), averaged over the heads, and its age (the number of
+// later queries that could see it) advances: old slots by T, new slot n0 + i to T - 1 - i. The read
+// kernels keep their softmax online and never form a probability, so the counts take two passes of
+// their own: the max and the sum of each (query, head)'s scores, then each slot's mass. Scores are the
+// oracle's: s = (q . k) with the dot product as one fma chain in dim order, times 1 / sqrt(hd).
+
+template <class KV>
+__device__ __forceinline__ float kv_at(const KV *p) {
+    if constexpr (sizeof(KV) == 2) return __half2float(*reinterpret_cast<const __half *>(p));
+    else return *reinterpret_cast<const float *>(p);
+}
+
+template <class KV>
+__device__ __forceinline__ float eng_score(const float *qr, const KV *kr, int hd) {
+    float s = kv_at(kr) * qr[0];
+    for (int a = 1; a < hd; a++) s = fmaf(kv_at(kr + a), qr[a], s);
+    return s;
+}
+
+// One wave per (query row b T + t, head h): ml[2 w] = max_j s_j, ml[2 w + 1] = sum_j exp(s_j - max) over
+// the slots 0..n0 + t.
+template <class KV>
+__global__ __launch_bounds__(256) void engram_ml_kernel(const float *__restrict__ q, int ldq, const KV *__restrict__ ks,
+                                                        int cap, int de, int hd, int nh, int B, int T, int n0,
+                                                        float scale, float *__restrict__ ml) {
+    const int w = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (w >= B * T * nh) return;
+    const int row = w / nh, h = w - row * nh, b = row / T, t = row - b * T, n = n0 + t + 1;
+    const float *qr = q + (size_t)row * ldq + h * hd;
+    const KV *kb = ks + (size_t)b * cap * de + h * hd;
+    float mx = -INFINITY;
+    for (int j = lane; j < n; j += 64) mx = fmaxf(mx, eng_score(qr, kb + (size_t)j * de, hd) * scale + 0.0f);
+    mx = ava::wave_max(mx);
+    float l = 0.0f;
+    for (int j = lane; j < n; j += 64) l += expf((eng_score(qr, kb + (size_t)j * de, hd) * scale + 0.0f) - mx);
+    l = ava::wave_sum(l);
+    if (lane == 0) {
+        ml[2 * w] = mx;
+        ml[2 * w + 1] = l;
+    }
+}
+
+// One thread per (stream b, slot j < n0 + T): the mass from the queries that see j before their own
+// key, summed over queries within each head and then over heads, times 1 / nh; then the counts.
+template <class KV>
+__global__ __launch_bounds__(256) void engram_got_kernel(const float *__restrict__ q, int ldq, const KV *__restrict__ ks,
+                                                         int cap, int de, int hd, int nh, int T, int n0, float scale,
+                                                         const float *__restrict__ ml, float *__restrict__ reads,
+                                                         float *__restrict__ age) {
+    const int b = blockIdx.y, j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= n0 + T) return;
+    const KV *kr = ks + ((size_t)b * cap + j) * de;
+    const int t0 = j < n0 ? 0 : j - n0 + 1;  // the first query that sees j before its own key
+    float got = 0.0f;
+    for (int h = 0; h < nh; h++) {
+        float acc = 0.0f;
+        for (int t = t0; t < T; t++) {
+            const size_t row = (size_t)b * T + t, w = row * nh + h;
+            const float s = eng_score(q + row * ldq + h * hd, kr + h * hd, hd) * scale + 0.0f;
+            acc += expf(s - ml[2 * w]) / ml[2 * w + 1];
+        }
+        got += acc;
+    }
+    got = got * (1.0f / (float)nh);
+    float *rd = reads + (size_t)b * cap, *ag = age + (size_t)b * cap;
+    if (j < n0) {
+        rd[j] = rd[j] + got;
+        ag[j] = ag[j] + (float)T;
+    } else {
+        rd[j] = 0.0f + got;
+        ag[j] = (float)(T - 1 - (j - n0));
+    }
+}
+
 }  // namespace
 
 namespace ava {
@@ -1161,6 +1239,29 @@ int engram_read(const float *qkv, int ldqkv, int B, int T, int de, int nh, void 
 int engram_advance(int *n0p, int T, int cap, hipStream_t st) {
     store_advance_kernel<<<1, 64, 0, st>>>(n0p, T, cap);
     AVA_LAUNCHED("store_advance");
+    return AVA_OK;
+}
+
+int engram_count(const float *q, int ldq, const void *ks, int kv_half, int cap, int n0, int B, int T, int de, int nh,
+                 float *ml, float *reads, float *age, hipStream_t st) {
+    AVA_REQUIRE(q && ks && ml && reads && age, AVA_ERR_ARG, "engram_count: NULL buffer");
+    AVA_REQUIRE(B > 0 && T > 0 && nh > 0 && de % nh == 0 && n0 >= 0 && n0 + T <= cap, AVA_ERR_SHAPE,
+                "engram_count: B=%d T=%d n0=%d cap=%d de=%d heads=%d", B, T, n0, cap, de, nh);
+    const int hd = de / nh;
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    const int waves = B * T * nh;
+    if (kv_half) {
+        engram_ml_kernel<__half><<<ceil_div(waves, 4), 256, 0, st>>>(q, ldq, (const __half *)ks, cap, de, hd, nh, B, T,
+                                                                    n0, scale, ml);
+        engram_got_kernel<__half><<<dim3(ceil_div(n0 + T, 256), B), 256, 0, st>>>(
+            q, ldq, (const __half *)ks, cap, de, hd, nh, T, n0, scale, ml, reads, age);
+    } else {
+        engram_ml_kernel<float><<<ceil_div(waves, 4), 256, 0, st>>>(q, ldq, (const float *)ks, cap, de, hd, nh, B, T, n0,
+                                                                   scale, ml);
+        engram_got_kernel<float><<<dim3(ceil_div(n0 + T, 256), B), 256, 0, st>>>(
+            q, ldq, (const float *)ks, cap, de, hd, nh, T, n0, scale, ml, reads, age);
+    }
+    AVA_LAUNCHED("engram_count");
     return AVA_OK;
 }
 

@@ -97,6 +97,8 @@ struct ava_model {
     // the decode engram read's chunk partials (grow-only)
     float *att_part = nullptr;
     size_t att_part_floats = 0;
+    float *eml = nullptr;  // the least-read counts' per-(query, head) max and sum
+    size_t eml_floats = 0;
     // set while captured graphs hold the scratch's addresses: nothing is freed or reallocated
     bool frozen = false;
 
@@ -418,6 +420,16 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             AVA_HIP(hipMalloc(&m->att_part, need * sizeof(float)));
             m->att_part_floats = need;
         }
+        const size_t need_ml = (s->eng_reads && s->eng_age) ? 2 * (size_t)N * eng_nh(c) : 0;
+        if (need_ml > m->eml_floats) {
+            AVA_REQUIRE(!m->frozen, AVA_ERR_ARG, "forward: the store's read counts need more scratch, and the "
+                        "model's scratch is frozen (a captured graph uses it)");
+            (void)hipFree(m->eml);
+            m->eml = nullptr;
+            m->eml_floats = 0;
+            AVA_HIP(hipMalloc(&m->eml, need_ml * sizeof(float)));
+            m->eml_floats = need_ml;
+        }
     }
     if (m->timing && m->last_stream != st) {
         if (int e = collect(m)) return e;
@@ -486,6 +498,9 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             }
             AVA_RUN("attend", ava::engram_read(m->qkv, 3 * de, B, T, de, eng_nh(c), s->eng_k, s->eng_v, c.eng_half, s->eng_cap, s->eng_len,
                                                    s->eng_len_dev, m->eo, m->att_part, m->att_part_floats, st, post));
+            if (s->eng_reads && s->eng_age)  // the least-read rule's counts (gpu/memory.rs:700-738)
+                AVA_RUN("engram_count", ava::engram_count(m->qkv, 3 * de, s->eng_k, c.eng_half, s->eng_cap, s->eng_len, B,
+                                                          T, de, eng_nh(c), m->eml, s->eng_reads, s->eng_age, st));
             if (!post.xq) AVA_RUN("quant_rows", ava::launch_quant_rows(m->eo, N, de, de, P, m->xq, m->xexp, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.ewo.w, ava::Q8_ADD, m->x, d, nullptr, st));
         }
@@ -607,6 +622,7 @@ extern "C" void ava_model_free(ava_model *m) {
     for (hipEvent_t e : m->timer.pool) (void)hipEventDestroy(e);
     for (void *p : {(void *)m->cb_err, (void *)m->cb_part, (void *)m->cb_delta, (void *)m->cb_fold}) (void)hipFree(p);
     (void)hipFree(m->att_part);
+    (void)hipFree(m->eml);
     if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
     if (m->ev_join) (void)hipEventDestroy(m->ev_join);
     if (m->side) (void)hipStreamDestroy(m->side);

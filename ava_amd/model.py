@@ -56,9 +56,12 @@ class State:
         self.cb_code = z(B, g) if g else None
         self.eng_len_dev = torch.zeros(1, dtype=torch.int32, device=device) if device_len else None
         self.seen = 0  # tokens each stream has consumed (State::seen, state.rs:94-116)
-        # the store's cap (EngramCap with the oldest-first rule, state.rs:37-69): after a forward the
-        # store keeps its last eng_max entries (0: no cap); the capacity must hold eng_max + T
+        # the store's cap (EngramCap, state.rs:37-69): after a forward the store keeps eng_max entries
+        # (0: no cap; the capacity must hold eng_max + T), the last ones (rule "oldest") or those read
+        # most per later query ("least-read", which keeps the per-slot counts eng_reads, eng_age)
         self.eng_max = 0
+        self.eng_rule = "oldest"
+        self.eng_reads = self.eng_age = None
 
     def select(self, rows) -> "State":
         """A state of the given streams only, in that order (State::select): every tensor's stream axis
@@ -69,21 +72,44 @@ class State:
         out.B = len(rows)
         for f in ("lif_v", "lif_s", "lif_a", "mem_f", "mem_s"):
             setattr(out, f, getattr(self, f).index_select(1, idx).contiguous())
-        for f in ("eng_k", "eng_v", "cb_tab", "cb_scale", "cb_code"):
+        for f in ("eng_k", "eng_v", "cb_tab", "cb_scale", "cb_code", "eng_reads", "eng_age"):
             t = getattr(self, f)
             setattr(out, f, t.index_select(0, idx).contiguous() if t is not None else None)
         out.eng_len_dev = self.eng_len_dev.clone() if self.eng_len_dev is not None else None
         return out
 
     def evict(self):
-        """Keep the store's last eng_max entries (evict with Evict::Oldest, state.rs:518-540), on the
-        store's device, in order. Called by the model after each forward of a capped state."""
+        """Keep eng_max of the store's entries, in store order (evict, state.rs:518-590), on the store's
+        device. Called by the model after each forward of a capped state. "oldest": the last eng_max.
+        "least-read": per stream, the slots rank by (class, value, index) -- class 1 for a slot some
+        later query could see (age >= 1; value reads / age, its mean mass per later query), class 2 for
+        the slots no later query has seen yet -- and the last eng_max of the ranking stay (the ranking
+        runs on the host, as the reference's sort does; the kept entries are gathered on the device)."""
         n, mx = self.eng_len, self.eng_max
         if not mx or n <= mx:
             return
-        drop = n - mx
-        for t in (self.eng_k, self.eng_v):
-            t[:, :mx].copy_(t[:, drop:n].clone())  # the ranges overlap when drop < mx
+        if self.eng_rule == "least-read":
+            reads = self.eng_reads[:, :n].cpu().numpy()
+            age = self.eng_age[:, :n].cpu().numpy()
+            keep = np.empty((self.B, mx), np.int64)
+            for r in range(self.B):
+                seen = age[r] >= 1.0
+                value = np.where(seen, reads[r] / np.where(seen, age[r], np.float32(1.0)), np.float32(0.0))
+                order = np.lexsort((np.arange(n), value.astype(np.float32), np.where(seen, 1, 2)))
+                keep[r] = np.sort(order[n - mx:])
+            idx = torch.from_numpy(keep).to(self.eng_k.device)
+            for t in (self.eng_k, self.eng_v):
+                g = torch.gather(t[:, :n], 1, idx[:, :, None].expand(-1, -1, t.shape[2]))
+                t[:, :mx].copy_(g)
+            for t in (self.eng_reads, self.eng_age):
+                t[:, :mx].copy_(torch.gather(t[:, :n], 1, idx))
+        else:
+            drop = n - mx
+            for t in (self.eng_k, self.eng_v):
+                t[:, :mx].copy_(t[:, drop:n].clone())  # the ranges overlap when drop < mx
+            for t in (self.eng_reads, self.eng_age):
+                if t is not None:
+                    t[:, :mx].copy_(t[:, drop:n].clone())
         self.eng_len = mx
         if self.eng_len_dev is not None:
             self.eng_len_dev.fill_(mx)
@@ -93,7 +119,8 @@ class State:
         return _CState(lif_v=p(self.lif_v), lif_s=p(self.lif_s), lif_a=p(self.lif_a), mem_f=p(self.mem_f),
                        mem_s=p(self.mem_s), eng_k=p(self.eng_k), eng_v=p(self.eng_v), eng_cap=self.eng_cap,
                        eng_len=self.eng_len, cb_tab=p(self.cb_tab), cb_scale=p(self.cb_scale),
-                       cb_code=p(self.cb_code), eng_len_dev=p(self.eng_len_dev))
+                       cb_code=p(self.cb_code), eng_len_dev=p(self.eng_len_dev), eng_reads=p(self.eng_reads),
+                       eng_age=p(self.eng_age))
 
 
 class Model:
@@ -145,14 +172,21 @@ class Model:
             lib().ava_model_free(self.h)
             self.h = None
 
-    def state(self, B: int, eng_cap: int = 0, device_len: bool = False, eng_max: int = 0) -> State:
+    def state(self, B: int, eng_cap: int = 0, device_len: bool = False, eng_max: int = 0,
+              eng_rule: str = "oldest") -> State:
         """A fresh state of B streams. eng_cap: the store's capacity in entries; eng_max > 0 caps the
-        store (oldest entries evicted after each forward; eng_cap must hold eng_max + the tokens of
-        the longest forward)."""
+        store (EngramCap, state.rs:37-69: eng_cap must hold eng_max + the tokens of the longest
+        forward), evicting after each forward by eng_rule, "oldest" or "least-read" (the state then
+        keeps per-slot read counts, advanced by each forward)."""
         st = State(self.cfg, B, eng_cap, device_len=device_len)
         if eng_max < 0 or (eng_max and eng_max >= max(eng_cap, 1)):
             raise ValueError(f"eng_max {eng_max}: 0 (no cap) or below the capacity {eng_cap}")
-        st.eng_max = eng_max
+        if eng_rule not in ("oldest", "least-read"):
+            raise ValueError(f"engram cap rule {eng_rule!r}: oldest or least-read")
+        st.eng_max, st.eng_rule = eng_max, eng_rule
+        if eng_rule == "least-read":
+            z = lambda: torch.zeros((B, max(eng_cap, 1)), dtype=torch.float32, device=st.lif_v.device)
+            st.eng_reads, st.eng_age = z(), z()
         return st
 
     def save_state(self, st: State, path: str) -> None:

@@ -12,7 +12,8 @@ Tensor names, where the reference has the same quantity (state.rs:1113-1197):
     meta.model [2] u32      the fingerprint, high word first
     meta.blocks [1] u32     the layer count
     meta.seen [B] u32       tokens each stream has consumed
-    meta.cap [2] u32        the store's cap and rule: [0, 0] none, [max, 0] oldest first
+    meta.cap [2] u32        the store's cap and rule: [0, 0] none, [max, 0] oldest first, [max, 1] least read
+    eng.reads / eng.age     [B, len] f32 the least-read rule's per-slot read mass and later-query count
     lif.{i}.v / .s / .a     [B, d] membrane, last spikes, adaptation (.a with ALIF)
     mem.{i}.f / .s          [B, nh, hs, hs] the fast weights F and the momentum S (.s with momentum)
     eng.k / eng.v           [B, heads, len, eng_dim / heads] the engram store's filled entries, its dtype
@@ -114,7 +115,7 @@ def state_tensors(st, cfg: dict, fp: int) -> dict:
     n = st.eng_len
     m = {"meta.model": _u32([fp >> 32, fp & 0xFFFFFFFF]), "meta.blocks": _u32([L]),
          "meta.seen": _u32([st.seen] * st.B), "meta.store": _u32([st.eng_cap, n]),
-         "meta.cap": _u32([getattr(st, "eng_max", 0), 0])}
+         "meta.cap": _u32([getattr(st, "eng_max", 0), 1 if getattr(st, "eng_rule", "oldest") == "least-read" else 0])}
     cpu = lambda t: t.detach().to("cpu").contiguous()
     for i in range(L):
         m[f"lif.{i}.v"], m[f"lif.{i}.s"] = cpu(st.lif_v[i]), cpu(st.lif_s[i])
@@ -127,6 +128,9 @@ def state_tensors(st, cfg: dict, fp: int) -> dict:
         m["eng.k"] = cpu(_heads(cfg, st.eng_k[:, :n]))
         m["eng.v"] = cpu(_heads(cfg, st.eng_v[:, :n]))
         m["eng.valid"] = _u32([n] * st.B)
+        if getattr(st, "eng_reads", None) is not None:
+            m["eng.reads"] = cpu(st.eng_reads[:, :n])
+            m["eng.age"] = cpu(st.eng_age[:, :n])
     if st.cb_tab is not None:
         m["cb.tab"], m["cb.scale"], m["cb.code"] = cpu(st.cb_tab), cpu(st.cb_scale), cpu(st.cb_code)
     return m
@@ -143,6 +147,7 @@ def save_state(path: str, st, cfg: dict, fp: int) -> None:
 def load_state(path: str, cfg: dict, fp: int, device="cuda", device_len: bool = False):
     """The state save_state wrote, for the model of fingerprint fp (State::load / State::from_map,
     gpu/state.rs:1236-1330). ValueError when the file holds another model's state or does not fit."""
+    import torch
     from safetensors.torch import load_file
     from .model import State
     t = load_file(path)
@@ -164,9 +169,14 @@ def load_state(path: str, cfg: dict, fp: int, device="cuda", device_len: bool = 
     cap, n = _ints(get("meta.store"))
     st = State(cfg, B, cap, device=device, device_len=device_len)
     emax, rule = _ints(get("meta.cap"))
-    if rule != 0:
-        raise ValueError(f"{path}: eviction rule {rule} (this build evicts oldest first only)")
+    if rule not in (0, 1):
+        raise ValueError(f"{path}: eviction rule {rule} (0 oldest first, 1 least read)")
     st.eng_max = emax
+    if rule == 1:
+        # counts start at 0 reads and age 0 for a store saved without them (gpu/memory.rs:718)
+        st.eng_rule = "least-read"
+        st.eng_reads = torch.zeros((B, max(cap, 1)), dtype=torch.float32, device=device)
+        st.eng_age = torch.zeros((B, max(cap, 1)), dtype=torch.float32, device=device)
 
     def put(dst, k):
         src = get(k)
@@ -190,6 +200,9 @@ def load_state(path: str, cfg: dict, fp: int, device="cuda", device_len: bool = 
         put(_heads(cfg, st.eng_v[:, :n]), "eng.v")
         if _ints(get("eng.valid")) != [n] * B:
             raise ValueError(f"{path}: eng.valid does not match the store length {n}")
+        if st.eng_reads is not None and "eng.reads" in t:
+            put(st.eng_reads[:, :n], "eng.reads")
+            put(st.eng_age[:, :n], "eng.age")
     st.eng_len = n
     if st.eng_len_dev is not None:
         st.eng_len_dev.fill_(n)

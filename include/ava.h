@@ -292,6 +292,12 @@ typedef struct {
      * forward captured in a HIP graph stays correct on replay (the host's eng_len only advances on
      * real calls; the caller keeps replays within eng_cap, and the device length saturates there). */
     int32_t *eng_len_dev;
+    /* Optional (NULL: not kept), for the least-read cap (Evict::LeastRead, state.rs:37-69, 518-590):
+     * per stream and slot [B][eng_cap], the attention mass the slot received from later queries (the
+     * mean over heads, each query's own key left out) and how many later queries could see it; each
+     * forward advances them as memory::read does with count_reads (memory.rs:700-738). The caller
+     * evicts between forwards (ranking slots by reads / age). */
+    float *eng_reads, *eng_age;
 } ava_state;
 
 typedef struct ava_model ava_model;

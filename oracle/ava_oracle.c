@@ -785,13 +785,42 @@ int orc_model_forward(const orc_cfg *cfg, const orc_model *mdl, const int32_t *i
                 }
             const int enh = cfg->eng_heads > 1 ? cfg->eng_heads : 1, hd = de / enh;
             float scale = (float)(1.0 / sqrt((double)hd));
-            for (int bi = 0; bi < B; bi++)
-                for (int t = 0; t < T; t++)
+            const int counts = st->eng_reads && st->eng_age;
+            float *hsum = counts ? ALLOC(float, n0 + T) : NULL, *got = counts ? ALLOC(float, n0 + T) : NULL;
+            for (int bi = 0; bi < B; bi++) {
+                if (counts)
+                    for (int j = 0; j < n0 + T; j++) got[j] = 0.0f;
+                for (int t = 0; t < T; t++) {
+                    if (counts)
+                        for (int j = 0; j < n0 + t; j++) hsum[j] = 0.0f;
                     for (int hh = 0; hh < enh; hh++) {
                         size_t base = (size_t)bi * st->eng_cap * de + (size_t)hh * hd;
                         size_t row = ((size_t)bi * T + t) * de + (size_t)hh * hd;
                         attend(eq + row, st->eng_k + base, st->eng_v + base, n0 + t + 1, hd, de, scale, sc, eo + row);
+                        if (counts)
+                            for (int j = 0; j < n0 + t; j++) hsum[j] += sc[j];
                     }
+                    /* gpu/memory.rs:709-714: the mean over heads of the mass each slot got from this
+                     * query, for the slots it sees before its own (the old ones and the earlier new ones) */
+                    if (counts)
+                        for (int j = 0; j < n0 + t; j++) got[j] += hsum[j] * (1.0f / (float)enh);
+                }
+                if (counts) {
+                    /* gpu/memory.rs:716-736: old slots add their mass and age by T; new slot j is seen
+                     * by the T - 1 - j later queries of this call */
+                    float *rd = st->eng_reads + (size_t)bi * st->eng_cap, *ag = st->eng_age + (size_t)bi * st->eng_cap;
+                    for (int j = 0; j < n0; j++) {
+                        rd[j] = rd[j] + got[j];
+                        ag[j] = ag[j] + (float)T;
+                    }
+                    for (int j = n0; j < n0 + T; j++) {
+                        rd[j] = 0.0f + got[j];
+                        ag[j] = (float)(T - 1 - (j - n0));
+                    }
+                }
+            }
+            free(hsum);
+            free(got);
             st->eng_len = n0 + T;
             mm(eo, (int)N, &bk->ewo, h, planes, threads);
             for (size_t j = 0; j < N * d; j++) x[j] = x[j] + h[j];

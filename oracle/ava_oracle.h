@@ -152,6 +152,10 @@ typedef struct {
     float *mem_f, *mem_s;           /* [layers][B][nh][hs][hs] */
     float *eng_k, *eng_v;           /* [B][eng_cap][de] */
     int eng_cap, eng_len;           /* entries held per stream */
+    /* The least-read rule's counts (gpu/memory.rs:592-594, 700-738; NULL: not kept): per stream and
+     * slot, the attention mass the slot received from later queries (the mean over heads, the query's
+     * own key left out) and how many later queries could see it. [B][eng_cap] each. */
+    float *eng_reads, *eng_age;
 } orc_state;
 
 /* Optional copies of what each block computed (NULL fields are skipped). Layer-major. */

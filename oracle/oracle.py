@@ -208,6 +208,41 @@ def mem_chunk(q, k, e, v, la, b, m=0.0, F=None, S=None):
     return y, F, S
 
 
+def evict_engram(state, eng_max, rule="oldest"):
+    """gpu/state.rs:518-590 (evict): when a stream's store holds more than eng_max slots, keep eng_max.
+    oldest: the last eng_max. least-read (needs the state's counts): rank every slot by (class, value,
+    index), class 1 for a slot some later query could see (age >= 1; value = reads / age, the mean mass
+    per later query) and class 2 for the slots no later query has seen yet (value 0); keep the last
+    eng_max of the ranking, in store order. The store, counts and length are updated in place. The ranking is written out as plain
+    Python sorts over (class, value, index) tuples, as the reference's sort_by."""
+    n = state["eng_len"]
+    if not eng_max or n <= eng_max:
+        return
+    B = state["eng_k"].shape[0]
+    if rule == "oldest" or "eng_reads" not in state:
+        keeps = [list(range(n - eng_max, n))] * B
+    else:
+        keeps = []
+        for r in range(B):
+            reads, age = state["eng_reads"][r], state["eng_age"][r]
+            order = []
+            for j in range(n):
+                if age[j] >= 1.0:
+                    order.append((1, float(np.float32(reads[j]) / np.float32(age[j])), j))
+                else:
+                    order.append((2, 0.0, j))
+            order.sort()
+            keeps.append(sorted(j for _, _, j in order[n - eng_max:]))
+    for r in range(B):
+        idx = np.asarray(keeps[r], np.int64)
+        for key in ("eng_k", "eng_v"):
+            state[key][r, :eng_max] = state[key][r, idx].copy()
+        for key in ("eng_reads", "eng_age"):
+            if key in state:
+                state[key][r, :eng_max] = state[key][r, idx].copy()
+    state["eng_len"] = eng_max
+
+
 def set_mem_chunked(on: bool):
     """The block stack's memory form for T > 1: chunked (the reference's default) or the token loop."""
     lib().orc_set_mem_chunked(int(bool(on)))
@@ -384,7 +419,7 @@ class _Model(C.Structure):
 class _State(C.Structure):
     _fields_ = [("lif_v", C.c_void_p), ("lif_s", C.c_void_p), ("lif_a", C.c_void_p), ("mem_f", C.c_void_p),
                 ("mem_s", C.c_void_p), ("eng_k", C.c_void_p), ("eng_v", C.c_void_p), ("eng_cap", C.c_int),
-                ("eng_len", C.c_int)]
+                ("eng_len", C.c_int), ("eng_reads", C.c_void_p), ("eng_age", C.c_void_p)]
 
 
 class _Trace(C.Structure):
@@ -451,7 +486,8 @@ class OracleModel:
         self.q8[id(w)] = (q, s)
         return _QW(q=q.ctypes.data, scale=s.ctypes.data, din=w.shape[0], dout=w.shape[1])
 
-    def new_state(self, B, eng_cap=0):
+    def new_state(self, B, eng_cap=0, counts=False):
+        """A zero state of B streams; counts: keep the least-read rule's per-slot reads and ages."""
         c = self.cfg
         L, d, hs = c["layers"], c["d"], c["head_size"]
         nh = d // hs
@@ -464,6 +500,9 @@ class OracleModel:
             "eng_v": np.zeros((B, max(eng_cap, 1), de), np.float32),
             "eng_cap": eng_cap, "eng_len": 0,
         }
+        if counts:
+            st["eng_reads"] = np.zeros((B, max(eng_cap, 1)), np.float32)
+            st["eng_age"] = np.zeros((B, max(eng_cap, 1)), np.float32)
         if self.cb:
             # the online table per stream (gpu/v51b.rs:340-367: delta, scale) and the last position's code
             st["cb_tab"] = np.zeros((B, self.cb, d), np.float32)
@@ -483,7 +522,9 @@ class OracleModel:
             state = self.new_state(B, eng_cap=T if c["eng_block"] >= 0 else 0)
         cst = _State(**{k: state[k].ctypes.data for k in ("lif_v", "lif_s", "lif_a", "mem_f", "mem_s",
                                                          "eng_k", "eng_v")},
-                     eng_cap=state["eng_cap"], eng_len=state["eng_len"])
+                     eng_cap=state["eng_cap"], eng_len=state["eng_len"],
+                     eng_reads=state["eng_reads"].ctypes.data if "eng_reads" in state else None,
+                     eng_age=state["eng_age"].ctypes.data if "eng_age" in state else None)
         N = B * T
         cb = self.cb and logits
         out = np.empty((N, c["vocab"]), np.float32) if logits and not cb else None

@@ -181,3 +181,39 @@ def test_capped_store_matches_oracle_with_the_same_eviction():
         assert st.eng_len == min(b, mx)
     assert rel(host(st.eng_k)[:, :mx], so["eng_k"][:, :mx]) < 1e-4
     assert np.max(np.abs(lu - lg)) > 1e-4  # the cap changed what the last steps read
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_heads"])
+def test_least_read_store_matches_oracle(name):
+    """A store capped at 16 entries with the least-read rule (Evict::LeastRead, state.rs:540-590) through
+    a prefill of 20 and single-token steps, one head of 64 and heads of 32: after every forward the
+    per-slot read mass and age of both sides agree (1e-5, gpu/memory.rs:700-738), both keep the same
+    slots (the GPU's State.evict and the oracle's evict_engram rank them apart), and the logits of every
+    step agree. The kept sets differ from the oldest-first rule's."""
+    cfg = synth.config(name)
+    prm = synth.params(cfg, seed=14)
+    B, T0, steps, mx = 2, 20, 10, 16
+    ids = np.random.default_rng(15).integers(0, cfg["vocab"], (B, T0 + steps)).astype(np.int32)
+    print(f"least-read store {name} B={B} prefill={T0} steps={steps} max={mx}", flush=True)
+    om = O.OracleModel(cfg, prm)
+    so = om.new_state(B, eng_cap=mx + T0, counts=True)
+    from ava_amd.model import Model
+    m = Model(cfg, prm)
+    st = m.state(B, eng_cap=mx + T0, eng_max=mx, eng_rule="least-read")
+    pieces = [(0, T0)] + [(t, t + 1) for t in range(T0, T0 + steps)]
+    for a, b in pieces:
+        x = np.ascontiguousarray(ids[:, a:b])
+        lo, so, _ = om.forward(x, state=so, planes=3, threads=8)
+        n = so["eng_len"]
+        lg = host(m.forward_with_state(torch.from_numpy(x).cuda(), st))
+        assert np.max(np.abs(lg - lo)) < 1e-2, (a, b)
+        # the counts before the eviction: the GPU's State evicted already, so compare after both evicted
+        O.evict_engram(so, mx, "least-read")
+        k = so["eng_len"]
+        assert st.eng_len == k
+        r_g, a_g = host(st.eng_reads)[:, :k], host(st.eng_age)[:, :k]
+        assert np.array_equal(a_g, so["eng_age"][:, :k]), (a, b)
+        assert np.max(np.abs(r_g - so["eng_reads"][:, :k])) <= 1e-5 * max(1.0, np.max(np.abs(so["eng_reads"][:, :k])))
+        assert rel(host(st.eng_k)[:, :k], so["eng_k"][:, :k]) < 1e-5, (a, b)
+    # the rule kept something the oldest-first rule would have dropped
+    assert np.any(so["eng_age"][:, :mx] >= mx)

@@ -122,16 +122,57 @@ def test_evict_keeps_the_last_entries_in_order():
     assert st.eng_len == 5 and torch.equal(st.eng_k[:, :5], k0[:, 8:13])
 
 
+def test_evict_least_read_ranks_by_reads_per_later_query():
+    """Evict::LeastRead (state.rs:540-590): per stream the slots rank by (seen by a later query, reads /
+    age, index) and the last eng_max stay, in store order, with their counts; slots no later query
+    has seen (age 0) rank last; ties go oldest first."""
+    cfg = synth.config("tiny")
+    st = _filled(cfg, 2, 20, 10, seed=11)
+    k0 = st.eng_k.clone()
+    st.eng_rule, st.eng_max = "least-read", 4
+    reads = torch.tensor([[5.0, 1.0, 3.0, 0.2, 2.0, 2.0, 9.0, 0.0, 0.0, 0.0],
+                          [0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]])
+    age = torch.tensor([[9.0, 8.0, 7.0, 6.0, 4.0, 4.0, 3.0, 2.0, 1.0, 0.0],
+                        [9.0, 8.0, 7.0, 6.0, 5.0, 4.0, 3.0, 2.0, 1.0, 0.0]])
+    st.eng_reads = torch.zeros((2, 20))
+    st.eng_age = torch.zeros((2, 20))
+    st.eng_reads[:, :10], st.eng_age[:, :10] = reads, age
+    st.evict()
+    # row 0: reads / age = .556 .125 .429 .033 .5 .5 3 0 0 | unseen slot 9 last; kept: 0, 5 (tie with 4:
+    # the older 4 goes first), 6, 9; row 1: all zero reads, so the newest seen slots and the unseen one
+    want = [[0, 5, 6, 9], [6, 7, 8, 9]]
+    assert st.eng_len == 4
+    for r in range(2):
+        assert torch.equal(st.eng_k[r, :4], k0[r, want[r]])
+        assert torch.equal(st.eng_reads[r, :4], reads[r, want[r]]) and torch.equal(st.eng_age[r, :4], age[r, want[r]])
+
+
 def test_cap_saved_and_refused_rules(tmp_path):
+    """meta.cap = [max, rule] (gpu/state.rs:1130, 1262): 0 oldest first, 1 least read with the store's
+    counts as eng.reads / eng.age (zeros when a file has none, gpu/memory.rs:718); other rules refused."""
     cfg = synth.config("tiny")
     st = _filled(cfg, 2, 20, 5, seed=9)
     st.eng_max = 12
     path = str(tmp_path / "s.safetensors")
     sio.save_state(path, st, cfg, 3)
-    assert sio.load_state(path, cfg, 3, device="cpu").eng_max == 12
+    back = sio.load_state(path, cfg, 3, device="cpu")
+    assert back.eng_max == 12 and back.eng_rule == "oldest" and back.eng_reads is None
+    # least read: the counts travel with the store
+    st.eng_rule = "least-read"
+    st.eng_reads = torch.rand((2, st.eng_cap), generator=torch.Generator().manual_seed(1))
+    st.eng_age = torch.arange(st.eng_cap, dtype=torch.float32).repeat(2, 1)
+    sio.save_state(path, st, cfg, 3)
+    back = sio.load_state(path, cfg, 3, device="cpu")
+    n = st.eng_len
+    assert back.eng_rule == "least-read" and back.eng_max == 12
+    assert torch.equal(back.eng_reads[:, :n], st.eng_reads[:, :n]) and torch.equal(back.eng_age[:, :n], st.eng_age[:, :n])
     t = sio.state_tensors(st, cfg, 3)
-    t["meta.cap"] = sio._u32([12, 1])  # least-read: not built
+    del t["eng.reads"], t["eng.age"]
     from safetensors.torch import save_file
+    save_file(t, path)
+    back = sio.load_state(path, cfg, 3, device="cpu")
+    assert back.eng_rule == "least-read" and not torch.any(back.eng_reads) and not torch.any(back.eng_age)
+    t["meta.cap"] = sio._u32([12, 2])  # no such rule
     save_file(t, path)
     with pytest.raises(ValueError, match="eviction rule"):
         sio.load_state(path, cfg, 3, device="cpu")
