@@ -9,13 +9,11 @@
 // rounding, so a P = 3 product differs from the reference's f32 fma chain only by its 2^-22
 // relative activation error, and integer inputs (spikes) give the reference's bits exactly.
 //
-// Product kernel: 256 threads = 4 waves in 2 x 2, a 128 x 128 output tile, K in steps of 64 bytes
-// staged through LDS (double buffered: the next step's global loads are in flight during this
-// step's MFMAs). Each wave owns 64 x 64 outputs per plane: 2 x 2 32x32 MFMA blocks, 2 k-substeps of
-// 32 per LDS step, the B fragment shared by every plane. LDS rows are padded to 80 bytes so the
-// 16-byte fragment reads of 8 consecutive rows hit distinct banks. Tiles are ordered so that the
-// workgroups of one XCD (hardware id mod 8) walk consecutive tiles: the N tiles of one row block
-// run back to back on one XCD and share its L2 for the A rows.
+// Product kernels: for many rows, a persistent grid of 8-wave workgroups over 128 x 256 output
+// tiles with the operands brought into LDS by direct-to-LDS buffer loads (two stages; the next
+// tile's first K step loads during the current tile's epilogue); for few rows (decode), 32-row
+// blocks whose K steps are spread over the waves. Both order the tiles so that the workgroups of one
+// XCD share its L2 for the rows and weight columns they read.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -113,15 +111,17 @@ struct EpiArgs {
     ava::LifEpi lif;  // EPI_LIF (few-rows kernel only): the LIF step on the product
 };
 
-// The output tile of this workgroup. Workgroups are dealt round-robin to the 8 XCDs, each with its
-// own L2, so XCD x is given the x-th contiguous eighth of the tiles. The tiles go in groups of
+// The output tile of tile index idx in a grid of `grid` workgroups (a workgroup takes indices
+// blockIdx.x, blockIdx.x + grid, ...). Workgroups are dealt round-robin to the 8 XCDs, each with its
+// own L2, so when both counts are multiples of 8 the indices of XCD x (idx mod 8 = x) are mapped to
+// the x-th contiguous eighth of the tiles. The tiles go in groups of
 // `group` row blocks, rows fastest: a weight column tile is then fetched from beyond L2 once per
 // group, not once per row block, while the group's activation rows stay in L2 as the group sweeps
 // the columns. group <= 1 is plain row-major order.
-__device__ __forceinline__ void tile_origin(int tiles_m, int tiles_n, int group, int &mt, int &nt) {
+__device__ __forceinline__ void tile_origin(int idx, int grid, int tiles_m, int tiles_n, int group, int &mt, int &nt) {
     const int total = tiles_m * tiles_n;
-    int t = blockIdx.x;
-    if (total % 8 == 0) t = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    int t = idx;
+    if (total % 8 == 0 && grid % 8 == 0) t = (idx & 7) * (total >> 3) + (idx >> 3);
     if (group <= 1) {
         mt = t / tiles_n;
         nt = t - mt * tiles_n;
@@ -194,8 +194,7 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
             sc[j] = scale[col];
             cv[j] = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
         }
-        // row block i of every column block at a time: its FN x 16 prior values (EPI_ADD) are all in
-        // flight before the first add
+        // block (i, j) at a time: its 16 prior values (EPI_ADD) are all in flight before the first add
 #pragma unroll
         for (int i = 0; i < FM; i++) {
             int ex[16];
@@ -205,91 +204,66 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
 #pragma unroll
                 for (int z = 0; z < 4; z++) ex[g * 4 + z] = e4[z];
             }
-            float prev[FN][16];
-            if (EPI == EPI_ADD) {
 #pragma unroll
-                for (int j = 0; j < FN; j++)
+            for (int j = 0; j < FN; j++) {
+                float prev[16];
+                if (EPI == EPI_ADD) {
 #pragma unroll
                     for (int r = 0; r < 16; r++)
-                        prev[j][r] = load_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
-                AVA_ISSUE_FENCE();
-            }
-#pragma unroll
-            for (int j = 0; j < FN; j++)
+                        prev[r] = load_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
+                    AVA_ISSUE_FENCE();
+                }
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     float v = ldexpf(value(i, j, r), ex[r]) * sc[j];
                     if (EPI == EPI_MUL) v = v * cv[j];
-                    if (EPI == EPI_ADD) v = prev[j][r] + v;
+                    if (EPI == EPI_ADD) v = prev[r] + v;
                     store_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4, v);
                 }
+            }
         }
         return;
     }
+    // an edge tile: every access goes through a resource over the tile's existing rows with the whole
+    // offset in the lane operand, so the range check drops rows past m (loads read 0); columns past n
+    // are masked per lane
+    // (the lane index passes through an empty asm: in a persistent caller, the lane offsets of this
+    // rare path are then formed here, per tile, instead of before the tile loop and kept in registers)
+    int el = lane;
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(el));
+#endif
+    const int eccol = el & 31, ersub = (el >> 5) * 4;
+    const unsigned rows_ok = (unsigned)min(BM, m - m0);
+    const BufRes yr = buf_res(ybase + (size_t)m0 * ep.ldy, rows_ok * (unsigned)ep.ldy * 4u);
 #pragma unroll
     for (int j = 0; j < FN; j++) {
-        const int col = n0 + cw0 + j * 32 + ccol;
+        const int col = n0 + cw0 + j * 32 + eccol;
         const bool col_ok = col < n;
         const int colc = col_ok ? col : n - 1;
         const float sc = scale[colc];
         const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
 #pragma unroll
         for (int i = 0; i < FM; i++) {
-            const int rbase = rw0 + i * 32 + rsub;  // tile row of r = 0
+            const int rbase = rw0 + i * 32 + ersub;  // tile row of r = 0
+            auto off = [&](int r) {
+                return ((unsigned)(rbase + (r >> 2) * 8 + (r & 3)) * (unsigned)ep.ldy + (unsigned)col) * 4u;
+            };
             float prev[16];
             if (EPI == EPI_ADD) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = min(m0 + rbase + (r >> 2) * 8 + (r & 3), m - 1);
-                    prev[r] = ybase[(size_t)row * ep.ldy + colc];
-                }
+                for (int r = 0; r < 16; r++) prev[r] = col_ok ? load_f32(yr, off(r), 0u) : 0.0f;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int tr = rbase + (r >> 2) * 8 + (r & 3), row = m0 + tr;
+                const int tr = rbase + (r >> 2) * 8 + (r & 3);
                 float v = ldexpf(value(i, j, r), s_exp[tr]) * sc;
                 if (EPI == EPI_MUL) v = v * cv;
                 if (EPI == EPI_ADD) v = prev[r] + v;
-                if (row < m && col_ok) ybase[(size_t)row * ep.ldy + col] = v;
+                if (col_ok) store_f32(yr, off(r), 0u, v);
             }
         }
     }
-}
-
-// ------------------------------------------------------------------ the product, direct-to-LDS form
-//
-// The same product with the operands brought into LDS by global_load_lds_dwordx4 (gfx950): each
-// load instruction writes 64 lanes x 16 bytes = 16 rows of 64 bytes contiguously, lane l taking
-// row r0 + l/4 and the 16-byte chunk that lands in slot l%4 under the row's swizzle, so no register
-// holds staged data. S LDS stages form a ring: at step kt a wave waits for its own loads of step kt,
-// one barrier makes every wave's loads visible (and frees the stage of step kt-1), the loads of step
-// kt+S-1 are issued into that freed stage, and step kt is multiplied. NW waves = WM x WN.
-
-// ds_read_b128 of an LDS pointer, issued as inline assembly so the compiler's wait insertion, which
-// cannot tell the stages apart and would wait for every direct-to-LDS load in flight, does not see it.
-// The caller waits with lgkm_wait<N>() and passes every fragment through tie() before using it.
-__device__ __forceinline__ i32x4 lds_read128(const int8_t *p) {
-    i32x4 v;
-#if defined(__HIP_DEVICE_COMPILE__)
-    const unsigned a = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) int8_t *)p;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
-#else
-    v = *reinterpret_cast<const i32x4 *>(p);
-#endif
-    return v;
-}
-template <int N>
-__device__ __forceinline__ void lgkm_wait() {
-    static_assert(N >= 0 && N < 16, "lgkmcnt");
-#if defined(__HIP_DEVICE_COMPILE__)
-    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
-#endif
-}
-// An empty asm that "rewrites" v after the wait above it, so no use of v can move before the wait.
-__device__ __forceinline__ void tie(i32x4 &v) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    asm volatile("" : "+v"(v));
-#endif
 }
 
 template <int N>
@@ -297,6 +271,12 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt");
     // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] in [15:14]
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// Every LDS access of this wave is done.
+__device__ __forceinline__ void lgkm_wait0() {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
 }
 
 // global_load_lds_dwordx4: 16 bytes per lane from `g` to LDS at `l` + 16 x lane (l wave-uniform). The
@@ -307,113 +287,191 @@ __device__ __forceinline__ void dma16(const void *g, void *l) {
 #endif
 }
 
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S, int MINB, int BKB>
-__global__ __launch_bounds__(64 * WM * WN, MINB) void q8_gemm_dma_kernel(const int8_t *__restrict__ xq,
-                                                                     const int32_t *__restrict__ xexp, int m, int n,
-                                                                     int ldk, const int8_t *__restrict__ qt,
-                                                                     const float *__restrict__ scale, EpiArgs ep) {
-    // K step of BK = 64 or 128 bytes per row: a 1 KB load instruction covers RPI = 1024 / BK rows,
-    // CPR = BK / 16 lanes per row (at 128 bytes every request is one whole cache line)
-    constexpr int NT = 64 * WM * WN, BK = BKB, CPR = BK / 16, RPI = 1024 / BK, LDS_ROW = BK;
+// A raw buffer resource over [base, base + bytes) of int8 data (the int8 twin of common.h's buf_res).
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t BufRes8;
+__device__ __forceinline__ BufRes8 buf_res8(const int8_t *base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, (int)bytes, 0x00020000);
+}
+#else
+typedef const int8_t *BufRes8;
+__device__ inline BufRes8 buf_res8(const int8_t *base, unsigned) { return base; }
+#endif
+
+// ------------------------------------------------------------------ the product for many rows
+//
+// A persistent grid (at most one 8-wave workgroup per CU) walks the 128 x 256 output tiles:
+// workgroup b takes tile indices b, b + G, b + 2G, ... (G = the grid), placed by tile_origin.
+// Operands reach LDS through buffer_load_dwordx4 ... lds: one load instruction writes 64 lanes x 16
+// bytes = 1 KB of stage rows contiguously (lane l takes row r0 + l / CPR and the 16-byte chunk that
+// lands in slot l % CPR under the row's swizzle). Each operand (a plane of the tile's rows, or the
+// tile's weight columns) is read through a buffer resource based at the tile's first row: a lane
+// keeps one 32-bit offset per load instruction, the K step is the instruction's uniform offset, and
+// rows past the operand's end read as zeros (the resource's range check), so edge tiles need no
+// clamping. Load instruction i of wave w covers stage rows (8 i + w) RPI .. + RPI - 1, so instruction
+// i reads the same operand in every wave and its resource is fixed at compile time.
+//
+// Two LDS stages of BK-byte K steps: at step kt a wave waits for its own loads, one barrier makes
+// every wave's loads visible and frees the other stage, the loads of step kt + 1 go there (after a
+// tile's last step: the next tile's first step, whose latency then hides behind this tile's
+// epilogue), and step kt is multiplied. Each wave owns 64 x 64 outputs per plane, 2 x 2 blocks of
+// v_mfma_i32_32x32x32_i8; the fragment reads of the next (K sub-step, plane) group are issued before
+// the MFMAs of the current group (sched_group_barrier), so four MFMAs cover their LDS latency.
+constexpr int GEMM_BM = 128, GEMM_BN = 256, GEMM_WM = 2, GEMM_WN = 4;
+
+__device__ __forceinline__ void dma16_buf(BufRes8 r, unsigned voff, unsigned soff, void *l) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)l, 16, (int)voff,
+                                             (int)soff, 0, 0);
+#endif
+}
+
+// The instruction order of one K step: the first group's fragment reads, then per group g the reads
+// of group g + 1 (if any) followed by the FM x FN MFMAs of group g (mask 0x100: LDS reads, 0x008: MFMA).
+template <int G, int KS, int P, int FM, int FN>
+__device__ __forceinline__ void frag_schedule() {
+    if constexpr (G < KS * P) {
+        constexpr int p = G % P, ks = G / P;
+        constexpr int reads = (p + 1 < P) ? FM : (ks + 1 < KS ? FN + FM : 0);
+        if constexpr (reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+        frag_schedule<G + 1, KS, P, FM, FN>();
+    }
+}
+
+template <int P, int EPI, int BK>
+__global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(const int8_t *__restrict__ xq,
+                                                                        const int32_t *__restrict__ xexp, int m,
+                                                                        int n, int ldk, const int8_t *__restrict__ qt,
+                                                                        const float *__restrict__ scale, EpiArgs ep) {
+    constexpr int BM = GEMM_BM, BN = GEMM_BN, WM = GEMM_WM, WN = GEMM_WN, NWAVE = WM * WN, NT = 64 * NWAVE;
+    constexpr int CPR = BK / 16, RPI = 1024 / BK, KS = BK / 32;
     static_assert(BK == 64 || BK == 128, "K step");
     constexpr int MW = BM / WM, NW = BN / WN, FM = MW / 32, FN = NW / 32;
-    static_assert(FM >= 1 && FN >= 1 && MW % 32 == 0 && NW % 32 == 0, "tile");
-    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * LDS_ROW;  // bytes per stage
-    constexpr int A_INS = A_ROWS / RPI, B_INS = BN / RPI;            // 1 KB load instructions per stage
-    constexpr int NWAVE = WM * WN;
-    static_assert((A_INS + B_INS) % NWAVE == 0, "load instructions per wave");
-    constexpr int LPW = (A_INS + B_INS) / NWAVE;  // load instructions per wave per stage
+    constexpr int A_ROWS = P * BM, STAGE = (A_ROWS + BN) * BK;
+    constexpr int ROUND = NWAVE * RPI;  // stage rows per load instruction index
+    static_assert(BM % ROUND == 0 && BN % ROUND == 0, "an instruction index reads one operand");
+    constexpr int LPW = (A_ROWS + BN) / ROUND;  // load instructions per wave per step
+    static_assert(BM <= NT, "one row exponent per thread");
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
-    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM;
-    int mt, nt;
-    tile_origin(tiles_m, tiles_n, ep.group, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tiles_n = (n + BN - 1) / BN, tiles_m = (m + BM - 1) / BM, total = tiles_m * tiles_n;
+    const int grid = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
 
-    // this lane's source for each of the wave's load instructions (instruction ins covers stage rows
-    // 16 ins .. 16 ins + 15; A rows first (plane-major), then B rows)
-    const int8_t *src[LPW];
-    int dst_off[LPW];
+    // per lane, the offset of each load instruction's 16 bytes within its operand (any tile)
+    unsigned voff[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
-        const int ins = wave * LPW + i;
-        const int srow = ins * RPI + lane / CPR;  // stage row
-        if (srow < A_ROWS) {
-            const int p = srow / BM, rr = srow % BM;
-            const int c = swz<CPR>(rr, lane % CPR);  // the logical chunk whose swizzled slot is lane % CPR
-            const int row = min(m0 + rr, m - 1);
-            src[i] = xq + ((size_t)p * m + row) * ldk + c * 16;
-        } else {
-            const int rr = srow - A_ROWS;
-            const int c = swz<CPR>(rr, lane % CPR);
-            const int col = min(n0 + rr, n - 1);
-            src[i] = qt + (size_t)col * ldk + c * 16;
-        }
-        dst_off[i] = ins * 1024;
+        const int srow0 = (i * NWAVE + wave) * RPI, srow = srow0 + lane / CPR;
+        const int rr = i * ROUND < A_ROWS ? srow - (i * ROUND / BM) * BM : srow - A_ROWS;
+        voff[i] = (unsigned)rr * (unsigned)ldk + swz<CPR>(rr, lane % CPR) * 16;
     }
-    auto issue = [&](int kt, int stage) {
-        const int k0 = kt * BK;
+    BufRes8 rs[P + 1];  // the current tile's planes, then its weight columns
+    auto set_rs = [&](int m0, int n0) {
+        const unsigned arows = (unsigned)min(BM, m - m0), brows = (unsigned)min(BN, n - n0);
 #pragma unroll
-        for (int i = 0; i < LPW; i++) dma16(src[i] + k0, smem + stage * STAGE + dst_off[i]);
+        for (int p = 0; p < P; p++) rs[p] = buf_res8(xq + ((size_t)p * m + m0) * ldk, arows * (unsigned)ldk);
+        rs[P] = buf_res8(qt + (size_t)n0 * ldk, brows * (unsigned)ldk);
+    };
+    // the loads of step kt of the tile of rs into `stage`
+    auto issue = [&](int kt, int stage) {
+#pragma unroll
+        for (int i = 0; i < LPW; i++) {
+            const int op = i * ROUND < A_ROWS ? i * ROUND / BM : P;
+            dma16_buf(rs[op], voff[i], (unsigned)(kt * BK), smem + stage * STAGE + (i * NWAVE + wave) * 1024);
+        }
     };
 
-    i32x16 acc[P][FM][FN];
-#pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
-
     const int KT = ldk / BK;
-#pragma unroll
-    for (int s0 = 0; s0 < S - 1; s0++) issue(min(s0, KT - 1), s0);
-
     const int frow = lane & 31, fc = lane >> 5;
-    for (int kt = 0; kt < KT; kt++) {
-        const int stage = kt % S;
-        wait_vm<(S - 2) * LPW>();  // this wave's loads of step kt are in LDS
-        __syncthreads();            // ... and every wave's; the stage of step kt-1 is free
-        issue(min(kt + S - 1, KT - 1), (kt + S - 1) % S);
-        const int8_t *la = smem + stage * STAGE;
-        const int8_t *lb = la + A_ROWS * LDS_ROW;
+    int idx = blockIdx.x, mt, nt;
+    tile_origin(idx, grid, tiles_m, tiles_n, ep.group, mt, nt);
+    int m0 = mt * BM, n0 = nt * BN;
+    set_rs(m0, n0);
+    issue(0, 0);
+    int sbase = 0;  // the stage holding the tile's first step
+    for (; idx < total; idx += grid) {
+        // the tile's row exponents: waited for with the first step's loads
+        const int ex = EPI != EPI_ACC && tid < BM && xexp ? xexp[min(m0 + tid, m - 1)] : 0;
+        i32x16 acc[P][FM][FN];
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
-            i32x4 bf[FN];
+        for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int j = 0; j < FN; j++) {
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
+        int st = sbase;
+#pragma nounroll
+        for (int kt = 0; kt < KT; kt++) {
+            st = (sbase + kt) & 1;
+            wait_vm<0>();  // this wave's loads of step kt (and the previous tile's stores) are done
+            __builtin_amdgcn_s_barrier();  // every wave's are; every wave is done with the other stage
+            if (kt + 1 < KT) {
+                issue(kt + 1, st ^ 1);
+            } else if (idx + grid < total) {
+                tile_origin(idx + grid, grid, tiles_m, tiles_n, ep.group, mt, nt);
+                set_rs(mt * BM, nt * BN);
+                issue(0, st ^ 1);
+            }
+            const int8_t *la = smem + st * STAGE, *lb = la + A_ROWS * BK;
+            auto afr = [&](int ks, int p, int i) {
+                const int r = wm * MW + i * 32 + frow;
+                return *reinterpret_cast<const i32x4 *>(la + (p * BM + r) * BK + swz<CPR>(r, ks * 2 + fc) * 16);
+            };
+            auto bfr = [&](int ks, int j) {
                 const int r = wn * NW + j * 32 + frow;
-                bf[j] = *reinterpret_cast<const i32x4 *>(lb + r * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
-            }
+                return *reinterpret_cast<const i32x4 *>(lb + r * BK + swz<CPR>(r, ks * 2 + fc) * 16);
+            };
+            // group g = (ks, p): fragments double-buffered across groups
+            i32x4 bb[2][FN], aa[2][FM];
 #pragma unroll
-            for (int p = 0; p < P; p++) {
-                i32x4 af[FM];
+            for (int j = 0; j < FN; j++) bb[0][j] = bfr(0, j);
 #pragma unroll
-                for (int i = 0; i < FM; i++) {
-                    const int r = wm * MW + i * 32 + frow;
-                    af[i] = *reinterpret_cast<const i32x4 *>(la + (p * BM + r) * LDS_ROW + swz<CPR>(r, ks * 2 + fc) * 16);
+            for (int i = 0; i < FM; i++) aa[0][i] = afr(0, 0, i);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+                for (int p = 0; p < P; p++) {
+                    const int cur = (ks * P + p) & 1;
+                    if (p + 1 < P) {
+#pragma unroll
+                        for (int i = 0; i < FM; i++) aa[cur ^ 1][i] = afr(ks, p + 1, i);
+                    } else if (ks + 1 < KS) {
+#pragma unroll
+                        for (int j = 0; j < FN; j++) bb[(ks + 1) & 1][j] = bfr(ks + 1, j);
+#pragma unroll
+                        for (int i = 0; i < FM; i++) aa[cur ^ 1][i] = afr(ks + 1, 0, i);
+                    }
+#pragma unroll
+                    for (int i = 0; i < FM; i++)
+#pragma unroll
+                        for (int j = 0; j < FN; j++)
+                            acc[p][i][j] =
+                                __builtin_amdgcn_mfma_i32_32x32x32_i8(aa[cur][i], bb[ks & 1][j], acc[p][i][j], 0, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[p][i][j], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, FN + FM, 0);
+            frag_schedule<0, KS, P, FM, FN>();
         }
+        // the stage of the last step is free once every wave has read it: the row exponents (less
+        // 7 (P - 1)) go there
+        int *s_exp = reinterpret_cast<int *>(smem + st * STAGE);
+        if (EPI != EPI_ACC) {
+            lgkm_wait0();
+            __builtin_amdgcn_s_barrier();
+            if (tid < BM) s_exp[tid] = ex - 7 * (P - 1);
+            lgkm_wait0();
+            __builtin_amdgcn_s_barrier();
+        }
+        epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
+        m0 = mt * BM;  // the next tile (tile_origin ran at the last step)
+        n0 = nt * BN;
+        sbase = st ^ 1;
     }
-    wait_vm<0>();
-    __syncthreads();
-
-    // epilogue: the tile's row exponents (less 7 (P - 1)) go to LDS, free after the K loop
-    int *s_exp = reinterpret_cast<int *>(smem);
-    if (EPI != EPI_ACC) {
-        for (int i = tid; i < BM; i += NT) s_exp[i] = (xexp ? xexp[min(m0 + i, m - 1)] : 0) - 7 * (P - 1);
-        __syncthreads();
-    }
-    epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
+    wait_vm<0>();  // no load into LDS outlives the workgroup
 }
 
 // Products of at most this many rows take the few-rows kernel.
@@ -592,7 +650,7 @@ __global__ __launch_bounds__(64 * NW) void q8_small_kernel(const int8_t *__restr
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     const int tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
     int mt, nt;
-    tile_origin(tiles_m, tiles_n, tiles_m, mt, nt);  // a weight block's row blocks on one XCD
+    tile_origin(blockIdx.x, gridDim.x, tiles_m, tiles_n, tiles_m, mt, nt);  // a weight block's row blocks on one XCD
     const int m0 = mt * BM, n0 = nt * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int8_t *wbuf = smem + wave * D * BUF;
@@ -696,15 +754,33 @@ int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, c
 // Row blocks per tile group (tile_origin): a weight column tile is fetched past L2 once per 8 row blocks.
 constexpr int TILE_GROUP = 8;
 
-template <int P, int EPI, int BM, int BN, int WM, int WN, int S, int MINB = 1, int BKB = 64>
-int launch_dma(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
-               EpiArgs ep, hipStream_t st) {
-    const int total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    size_t lds = (size_t)S * (P * BM + BN) * BKB;
-    if (lds < (size_t)BM * 4) lds = (size_t)BM * 4;
-    if (int r = ava::lds_opt_in((const void *)q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB>, lds)) return r;
-    q8_gemm_dma_kernel<P, EPI, BM, BN, WM, WN, S, MINB, BKB><<<dim3(total), dim3(64 * WM * WN), lds, st>>>(
-        xq, xexp, m, n, ldk, qt, scale, ep);
+// Workgroups for the persistent product: one per CU of the current device (looked up once per device).
+int gemm_grid(int tiles, int *grid) {
+    static std::mutex mu;
+    static int cus[64] = {};
+    int dev = 0;
+    AVA_HIP(hipGetDevice(&dev));
+    AVA_REQUIRE(dev >= 0 && dev < 64, AVA_ERR_UNSUPPORTED, "q8 product: device %d (0..63)", dev);
+    int c = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!cus[dev]) AVA_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));
+        c = cus[dev];
+    }
+    *grid = std::max(1, std::min(tiles, c));
+    return AVA_OK;
+}
+
+template <int P, int EPI, int BK>
+int launch_tiled(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, const int8_t *qt, const float *scale,
+                 EpiArgs ep, hipStream_t st) {
+    const int tiles = ((m + GEMM_BM - 1) / GEMM_BM) * ((n + GEMM_BN - 1) / GEMM_BN);
+    int grid = 0;
+    if (int r = gemm_grid(tiles, &grid)) return r;
+    const size_t lds = (size_t)2 * (P * GEMM_BM + GEMM_BN) * BK;
+    if (int r = ava::lds_opt_in((const void *)q8_gemm_kernel<P, EPI, BK>, lds)) return r;
+    q8_gemm_kernel<P, EPI, BK><<<dim3(grid), dim3(64 * GEMM_WM * GEMM_WN), lds, st>>>(xq, xexp, m, n, ldk, qt, scale,
+                                                                                     ep);
     AVA_LAUNCHED("q8_gemm");
     return AVA_OK;
 }
@@ -714,12 +790,11 @@ int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
                 EpiArgs ep, hipStream_t st) {
     // few rows (decode): 32-row blocks with the K steps spread over the waves
     if (m <= SMALL_ROWS) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    // the direct-to-LDS 128 x 256 tile, 8 waves, two stages: 128-byte K steps for split-plane inputs,
-    // 64-byte ones for the single spike plane (measured best on every config[3] shape)
+    // 128-byte K steps for split-plane inputs, 64-byte ones for the single spike plane
     if constexpr (P == 1)
-        return launch_dma<P, EPI, 128, 256, 2, 4, 2, 1, 64>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+        return launch_tiled<P, EPI, 64>(xq, xexp, m, n, ldk, qt, scale, ep, st);
     else
-        return launch_dma<P, EPI, 128, 256, 2, 4, 2, 1, 128>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+        return launch_tiled<P, EPI, 128>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 template <int EPI>

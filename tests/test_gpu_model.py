@@ -73,6 +73,14 @@ def test_tiny_stack_matches_oracle(B, T):
     assert st.eng_len == T
 
 
+def test_many_tiles_stack_matches_oracle():
+    """32 streams of 1037 tokens (33,184 rows: 260 row tiles of 128, the last one partial) through the
+    tiny stack: every product has more tiles than an MI355X has CUs, so the persistent product grid
+    gives workgroups several tiles, in each epilogue (store, scaled, accumulate into the residual
+    stream); the oracle replays the GPU's decisions (tests/forced.py)."""
+    F.run_forced("tiny", 32, 1037, seed=21)
+
+
 def test_fp16_engram_store_decode_matches_oracle():
     """The fp16 engram store (config[4]'s KV cache) through a prefill and single-token steps: the oracle
     rounds the stored keys and values to binary16 (round-to-nearest-even) the same way."""

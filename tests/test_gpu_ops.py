@@ -126,9 +126,11 @@ def test_kwta_matches_oracle(relu2, dev):
 
 # ----------------------------------------------------------------------------- int8 products
 
-# m <= 512 takes the few-rows kernel (32 x 32 blocks, K steps over the waves), larger m the tiled ones
+# m <= 512 takes the few-rows kernel (32 x 32 blocks, K steps over the waves), larger m the tiled ones;
+# the last shape has more 128 x 256 tiles (65 x 5, edge tiles in both directions) than an MI355X has
+# CUs, so workgroups of the persistent grid take several tiles each
 SHAPES = [(32, 32, 3), (128, 128, 1), (96, 200, 5), (64, 4112, 2), (1024, 1024, 300), (1024, 192, 129),
-          (4096, 1024, 257), (1024, 1024, 700), (512, 4112, 530)]
+          (4096, 1024, 257), (1024, 1024, 700), (512, 4112, 530), (256, 1100, 8300)]
 
 
 @pytest.mark.parametrize("din,dout,m", SHAPES)
