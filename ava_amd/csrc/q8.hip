@@ -312,12 +312,15 @@ __device__ inline BufRes8 buf_res8(const int8_t *base, unsigned) { return base; 
 // i reads the same operand in every wave and its resource is fixed at compile time.
 //
 // Two LDS stages of BK-byte K steps: at step kt a wave waits for its own loads, one barrier makes
-// every wave's loads visible and frees the other stage, the loads of step kt + 1 go there (after a
-// tile's last step: the next tile's first step, whose latency then hides behind this tile's
-// epilogue), and step kt is multiplied. Each wave owns 64 x 64 outputs per plane, 2 x 2 blocks of
-// v_mfma_i32_32x32x32_i8; the fragment reads of the next (K sub-step, plane) group are issued before
-// the MFMAs of the current group (sched_group_barrier), so four MFMAs cover their LDS latency.
-constexpr int GEMM_BM = 128, GEMM_BN = 256, GEMM_WM = 2, GEMM_WN = 4;
+// every wave's loads visible and frees the other stage, and step kt is multiplied while the loads of
+// step kt + 1 go into the other stage, two after each group of MFMAs (after a tile's last step they
+// fetch the next tile's first step, whose latency then hides behind this tile's epilogue; after the
+// grid's last tile, this tile's first step again, unused). Each wave owns 64 x 64 outputs per plane,
+// 2 x 2 blocks of v_mfma_i32_32x32x32_i8; the fragment reads of the next (K sub-step, plane) group are
+// issued before the MFMAs of the current group, so four MFMAs cover their LDS latency (the order is
+// fixed with sched_group_barrier). A tile's first step multiplies into zero accumulators (no
+// register clearing).
+constexpr int GEMM_BM = 128, GEMM_BN = 256, GEMM_WM = 2, GEMM_WN = 4, GEMM_ILV = 2;
 
 __device__ __forceinline__ void dma16_buf(BufRes8 r, unsigned voff, unsigned soff, void *l) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -328,14 +331,18 @@ __device__ __forceinline__ void dma16_buf(BufRes8 r, unsigned voff, unsigned sof
 
 // The instruction order of one K step: the first group's fragment reads, then per group g the reads
 // of group g + 1 (if any) followed by the FM x FN MFMAs of group g (mask 0x100: LDS reads, 0x008: MFMA).
-template <int G, int KS, int P, int FM, int FN>
+// After the MFMAs of group g come the next step's global loads ILV g .. ILV g + ILV - 1 (mask 0x020),
+// so that they leave between the MFMAs instead of all at once after the barrier.
+template <int G, int KS, int P, int FM, int FN, int LPW, int ILV>
 __device__ __forceinline__ void frag_schedule() {
     if constexpr (G < KS * P) {
         constexpr int p = G % P, ks = G / P;
         constexpr int reads = (p + 1 < P) ? FM : (ks + 1 < KS ? FN + FM : 0);
         if constexpr (reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, reads, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
-        frag_schedule<G + 1, KS, P, FM, FN>();
+        constexpr int left = LPW - G * ILV;
+        if constexpr (left > 0) __builtin_amdgcn_sched_group_barrier(0x020, left < ILV ? left : ILV, 0);
+        frag_schedule<G + 1, KS, P, FM, FN, LPW, ILV>();
     }
 }
 
@@ -376,13 +383,10 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
         for (int p = 0; p < P; p++) rs[p] = buf_res8(xq + ((size_t)p * m + m0) * ldk, arows * (unsigned)ldk);
         rs[P] = buf_res8(qt + (size_t)n0 * ldk, brows * (unsigned)ldk);
     };
-    // the loads of step kt of the tile of rs into `stage`
-    auto issue = [&](int kt, int stage) {
-#pragma unroll
-        for (int i = 0; i < LPW; i++) {
-            const int op = i * ROUND < A_ROWS ? i * ROUND / BM : P;
-            dma16_buf(rs[op], voff[i], (unsigned)(kt * BK), smem + stage * STAGE + (i * NWAVE + wave) * 1024);
-        }
+    // load instruction i of step kt of the tile of rs, into `stage`
+    auto issue_one = [&](int i, int kt, int stage) {
+        const int op = i * ROUND < A_ROWS ? i * ROUND / BM : P;
+        dma16_buf(rs[op], voff[i], (unsigned)(kt * BK), smem + stage * STAGE + (i * NWAVE + wave) * 1024);
     };
 
     const int KT = ldk / BK;
@@ -391,30 +395,26 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
     tile_origin(idx, grid, tiles_m, tiles_n, ep.group, mt, nt);
     int m0 = mt * BM, n0 = nt * BN;
     set_rs(m0, n0);
-    issue(0, 0);
+#pragma unroll
+    for (int i = 0; i < LPW; i++) issue_one(i, 0, 0);
     int sbase = 0;  // the stage holding the tile's first step
     for (; idx < total; idx += grid) {
         // the tile's row exponents: waited for with the first step's loads
         const int ex = EPI != EPI_ACC && tid < BM && xexp ? xexp[min(m0 + tid, m - 1)] : 0;
         i32x16 acc[P][FM][FN];
-#pragma unroll
-        for (int p = 0; p < P; p++)
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int j = 0; j < FN; j++) acc[p][i][j] = i32x16{};
         int st = sbase;
-#pragma nounroll
-        for (int kt = 0; kt < KT; kt++) {
+        auto step = [&](auto first, int kt) {
+            constexpr bool FIRST = decltype(first)::value;
             st = (sbase + kt) & 1;
             wait_vm<0>();  // this wave's loads of step kt (and the previous tile's stores) are done
             __builtin_amdgcn_s_barrier();  // every wave's are; every wave is done with the other stage
-            if (kt + 1 < KT) {
-                issue(kt + 1, st ^ 1);
-            } else if (idx + grid < total) {
-                tile_origin(idx + grid, grid, tiles_m, tiles_n, ep.group, mt, nt);
-                set_rs(mt * BM, nt * BN);
-                issue(0, st ^ 1);
+            int knext = kt + 1;
+            if (kt + 1 == KT) {
+                knext = 0;
+                if (idx + grid < total) {
+                    tile_origin(idx + grid, grid, tiles_m, tiles_n, ep.group, mt, nt);
+                    set_rs(mt * BM, nt * BN);
+                }
             }
             const int8_t *la = smem + st * STAGE, *lb = la + A_ROWS * BK;
             auto afr = [&](int ks, int p, int i) {
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
             for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
                 for (int p = 0; p < P; p++) {
-                    const int cur = (ks * P + p) & 1;
+                    const int g = ks * P + p, cur = g & 1;
                     if (p + 1 < P) {
 #pragma unroll
                         for (int i = 0; i < FM; i++) aa[cur ^ 1][i] = afr(ks, p + 1, i);
@@ -448,14 +448,23 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
 #pragma unroll
                     for (int i = 0; i < FM; i++)
 #pragma unroll
-                        for (int j = 0; j < FN; j++)
-                            acc[p][i][j] =
-                                __builtin_amdgcn_mfma_i32_32x32x32_i8(aa[cur][i], bb[ks & 1][j], acc[p][i][j], 0, 0, 0);
+                        for (int j = 0; j < FN; j++) {
+                            const i32x16 c = (FIRST && ks == 0) ? i32x16{} : acc[p][i][j];
+                            acc[p][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aa[cur][i], bb[ks & 1][j], c, 0, 0, 0);
+                        }
+#pragma unroll
+                    for (int q = 0; q < GEMM_ILV; q++) {
+                        const int li = g * GEMM_ILV + q;
+                        if (li < LPW) issue_one(li, knext, st ^ 1);
+                    }
                 }
             }
             __builtin_amdgcn_sched_group_barrier(0x100, FN + FM, 0);
-            frag_schedule<0, KS, P, FM, FN>();
-        }
+            frag_schedule<0, KS, P, FM, FN, LPW, GEMM_ILV>();
+        };
+        step(std::integral_constant<bool, true>{}, 0);
+#pragma nounroll
+        for (int kt = 1; kt < KT; kt++) step(std::integral_constant<bool, false>{}, kt);
         // the stage of the last step is free once every wave has read it: the row exponents (less
         // 7 (P - 1)) go there
         int *s_exp = reinterpret_cast<int *>(smem + st * STAGE);
