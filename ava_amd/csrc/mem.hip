@@ -380,7 +380,13 @@ __global__ __launch_bounds__(256, 4) void mem_fused_kernel(FusedArgs p) {
         }
     }
 
-    if (__syncthreads_or(nf)) {
+    // the workgroup's vote on nf, through LDS the scan no longer reads (a row of s_q): a block-wide
+    // vote primitive would add LDS of its own, and 4 x 40 KB is what lets four heads share a CU
+    __syncthreads();  // every wave is past its last read of s_q
+    const bool wave_nf = __any(nf);
+    if (lane == 0) s_q[0][wave] = wave_nf ? 1.0f : 0.0f;
+    __syncthreads();
+    if (s_q[0][0] + s_q[0][1] + s_q[0][2] + s_q[0][3] != 0.0f) {
         if (tid == 0 && p.bad) p.bad[bi] = 1;
         return;  // nothing committed
     }
