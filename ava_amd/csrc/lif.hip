@@ -165,8 +165,8 @@ int launch_vp(const float *cur, int B, int T, int D, const float *ps, float *v, 
 
 namespace ava {
 
-// vec/pf 0 = the defaults: 1 channel per lane; 64 steps in flight with 131,072 lanes or more
-// (config[1]), 32 with fewer (the block stack's 65,536), each measured best.
+// vec/pf 0 = the defaults: 1 channel per lane, 32 steps in flight (the fastest of 16, 32, 48 and 64 at
+// config[1]'s 131,072 lanes and at the block stack's 65,536).
 int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
                    int levels, int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf,
                    hipStream_t st) {
@@ -174,7 +174,7 @@ int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float
     AVA_REQUIRE(B > 0 && T > 0 && D > 0, AVA_ERR_SHAPE, "lif_scan: B=%d T=%d D=%d", B, T, D);
     AVA_REQUIRE(levels == 1 || levels == 2, AVA_ERR_ARG, "lif_scan: levels %d (1 or 2)", levels);
     if (vec == 0) vec = 1;
-    if (pf == 0) pf = (long)B * D >= 131072 ? 64 : 32;  // deeper when there are lanes enough to hold it
+    if (pf == 0) pf = 32;
     if (D % vec) vec = 1;
 #define AVA_VP(VV, PP)                                                                              \
     if (vec == VV && pf == PP)                                                                      \

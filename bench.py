@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "tokens/sec int8 block-stack forward @B=64,T=2048, 1 GPU; % HBM / MFMA roofline"
 HBM_PEAK_GBS = 8000.0
+WARM_S = 0.25  # minimum warm-up time, seconds (the stack's three default warm-up steps take longer)
 I8_PEAK_TOPS = 5000.0  # dense int8 MFMA, TOP/s
 F32_MFMA_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 FP32_PEAK_TFLOPS = 157.3
@@ -56,6 +57,7 @@ class Lif:
     gain 0.05; int2 spikes, subtract reset; outputs int8 spikes, final v and theta."""
 
     name = "lif"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "lif_scan_kernel"
 
     def __init__(self, B=64, T=2048, D=2048):
@@ -80,17 +82,21 @@ class Lif:
         self.config = {"workload": "lif_scan config[1]", "B": B, "T": T, "C": D, "spikes": "int2",
                        "alif": True, "rho": 0.95, "gain": 0.05}
         self.dtype = "f32"
+        self.pf = 0  # steps in flight per lane; 0 = the library's default
 
     def step(self, stream, ev=None):
         from ava_amd._lib import check
         import ctypes as C
 
         # the state carries over from step to step (a stream read in pieces, state.rs:4-12)
+        args = (C.c_void_p(self.cur.data_ptr()), self.B, self.T, self.D, C.c_void_p(self.ps.data_ptr()),
+                C.c_void_p(self.v.data_ptr()), C.c_void_p(self.s.data_ptr()), C.c_void_p(self.a.data_ptr()), 2, 1, 1,
+                C.c_void_p(self.spikes.data_ptr()), C.c_void_p(self.th.data_ptr()))
         if ev: ev[0].record()
-        check(self.L.ava_lif_scan(C.c_void_p(self.cur.data_ptr()), self.B, self.T, self.D,
-                                  C.c_void_p(self.ps.data_ptr()), C.c_void_p(self.v.data_ptr()),
-                                  C.c_void_p(self.s.data_ptr()), C.c_void_p(self.a.data_ptr()), 2, 1, 1,
-                                  C.c_void_p(self.spikes.data_ptr()), C.c_void_p(self.th.data_ptr()), stream))
+        if self.pf:
+            check(self.L.ava_lif_scan_tuned(*args, 1, self.pf, stream))
+        else:
+            check(self.L.ava_lif_scan(*args, stream))
         if ev: ev[1].record()
 
     def roofline(self, kernel_s):
@@ -118,6 +124,7 @@ class Kwta:
     """kWTA + relu2 over config[3]'s wide layer: u [131072, 4096] ~N(0,1), k = 1024."""
 
     name = "kwta"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "kwta_kernel"
 
     def __init__(self, n=131072, h=4096, k=1024):
@@ -165,6 +172,7 @@ class Gemm:
     """One dense int8 product of config[3]: x [131072, 1024] f32 -> 3 planes -> i8 MFMA -> y [131072, 4096]."""
 
     name = "gemm"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "q8_gemm_kernel"
 
     def __init__(self, m=131072, k=1024, n=4096, planes=3):
@@ -253,6 +261,7 @@ class Delta:
     token and head, W_0 = 0."""
 
     name = "delta"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "delta_chunk_kernel"
 
     def __init__(self, B=32, H=8, T=4096):
@@ -322,6 +331,7 @@ class LifBwd:
     per-stream state and parameter gradients."""
 
     name = "lif_bwd"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "lif_bwd_kernel"
 
     def __init__(self, B=64, T=2048, D=2048):
@@ -387,6 +397,7 @@ class MemBwd:
     b ~U(0.1, 1.9), dL/dy ~N(0,1), from a zero state."""
 
     name = "mem_bwd"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "mem_bwd_kernel"
 
     def __init__(self, B=64, H=16, T=2048):
@@ -471,6 +482,7 @@ class MemChunk:
     the same inputs is timed beside it."""
 
     name = "mem_chunk"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "mem_chunk_kernel"
 
     def __init__(self, B=64, H=16, T=2048):
@@ -576,6 +588,7 @@ class Copy:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the FETCH/WRITE_SIZE counters."""
 
     name = "copy"
+    warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "copy"
 
     def __init__(self, nbytes=1 << 30):
@@ -961,6 +974,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--lif-pf", type=int, default=0,
+                    help="lif workload: time steps in flight per lane (ava_lif_scan_tuned; 0 = the library default)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -977,15 +992,29 @@ def main():
     default = extra_workloads()
     wname = args.workload or default
     W = WORKLOADS[wname]()
+    if wname == "lif" and args.lif_pf:
+        W.pf = args.lif_pf
+        W.config["pf"] = args.lif_pf
     if args.steps is None:
         args.steps = getattr(W, "default_steps", 10)
     stream = torch.cuda.current_stream()
     sptr = __import__("ctypes").c_void_p(stream.cuda_stream)
 
     log(f"bench: workload={wname} warmup={args.warmup} steps={args.steps}")
+    # untimed warm-up: W steps and, for the single-kernel workloads, more until the GPU has been busy
+    # for WARM_S seconds (the clocks take a few hundred milliseconds of load to settle: a
+    # sub-millisecond kernel timed right after three warm-up launches runs 15-25% slower than in
+    # steady state)
+    tw = time.perf_counter()
     for _ in range(args.warmup):
         W.step(sptr)
     torch.cuda.synchronize()
+    warm_run = args.warmup
+    while getattr(W, "warm_extend", False) and args.warmup > 0 and time.perf_counter() - tw < WARM_S:
+        for _ in range(args.warmup):
+            W.step(sptr)
+        torch.cuda.synchronize()
+        warm_run += args.warmup
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     W.nsteps = args.steps
@@ -1020,6 +1049,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_run,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",

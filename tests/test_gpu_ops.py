@@ -71,7 +71,7 @@ def test_lif_matches_oracle_every_option(levels, signed, alif, theta_on, init_on
     assert 0.02 < rate < 0.98
 
 
-@pytest.mark.parametrize("vec,pf", [(1, 8), (1, 32), (2, 16), (4, 8), (4, 16)])
+@pytest.mark.parametrize("vec,pf", [(1, 8), (1, 32), (1, 64), (2, 16), (4, 8), (4, 16)])
 def test_lif_config1_shape_bit_exact(vec, pf, dev):
     """config[1] semantics (int2, ALIF rho 0.95 gain 0.05, theta 1, beta = sigmoid(U(1.5, 4.5))) on a
     reduced batch, every kernel variant: spikes, v_T, a_T and theta_T bit for bit."""
