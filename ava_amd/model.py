@@ -342,6 +342,20 @@ class Model:
             ids = torch.tensor([prompts[r] for r in group], dtype=torch.int32, device="cuda")
             last = self.forward_with_state(ids, st).view(len(group), n0, -1)[:, -1]
             live = list(group)
+            if pick is None and stop is None and eos is None:
+                # greedy with nothing that ends a row early: every step's token stays on the device and
+                # feeds the next step, so the host reads the tokens once, at the end
+                toks = []
+                for step in range(max_new):
+                    x = torch.argmax(last, dim=1).to(torch.int32).view(-1, 1)
+                    toks.append(x)
+                    if step + 1 == max_new:
+                        break
+                    last = self.forward_with_state(x, st)
+                got = torch.cat(toks, dim=1).tolist()
+                for k, r in enumerate(live):
+                    out[r].extend(got[k])
+                continue
             for step in range(max_new):
                 if pick is None:
                     toks = torch.argmax(last, dim=1).tolist()  # the first (lowest) id of the maximum

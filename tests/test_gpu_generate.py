@@ -56,3 +56,17 @@ def test_generate_refuses_empty_prompt_and_honours_eos():
         m.generate([[1, 2], []], 4)
     first = m.generate([[3, 4, 5]], 1, eos=None)[0][0]
     assert m.generate([[3, 4, 5]], 6, eos=first) == [[]]  # eos is not included, and ends the row
+
+
+def test_device_side_greedy_equals_host_loop():
+    """With no stop rule and no eos, the tokens stay on the device between steps; the same rows with
+    a stop rule that never fires take the host loop: identical tokens, prompts of two lengths."""
+    from ava_amd.model import Model
+    cfg = synth.config("tiny")
+    m = Model(cfg, synth.params(cfg, seed=23))
+    rng = np.random.default_rng(24)
+    prompts = [rng.integers(0, cfg["vocab"], n).tolist() for n in (7, 4, 7)]
+    print(f"device-side greedy prompts={[len(p) for p in prompts]}", flush=True)
+    dev = m.generate(prompts, 12, eos=None)
+    host = m.generate(prompts, 12, eos=None, stop=lambda toks: False)
+    assert dev == host and all(len(t) == 12 for t in dev)
