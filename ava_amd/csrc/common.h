@@ -234,9 +234,11 @@ int cb_apply_list(const float *xf, const float *code, int n, int g, int d, const
 int cb_learn(const float *logits, int ldl, int V, const int32_t *next, int B, const float *emb, int d,
              const float *keep, int g, float lr, double fade, double *scale, float *tab, float *err, float *part,
              int nks, float *delta, double *fold, double *nats, hipStream_t st);
+// The dense mix into x of the ns streams, the last of which is the block's output (x before the mix:
+// the caller exchanges the two buffers instead of copying); x must not be any of the streams.
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st);
-// The dense mix of [n][d] rows, then the planes of rmsnorm(row) * gain (and the normed row when hout);
-// the embedding rows, then the first norm's planes. d <= 1024.
+// The same dense mix of [n][d] rows, then the planes of rmsnorm(row) * gain (and the normed row when
+// hout); the embedding rows, then the first norm's planes. d <= 1024.
 int dense_rms(float *x, float *const *streams, const float *w, int ns, int n, int d, const float *gain, int planes,
               int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st);
 int embed_rms(const int32_t *ids, const float *emb, int n, int d, int vocab, float *x, float *x0, const float *gain,

@@ -689,20 +689,20 @@ __global__ void store_append_kernel(const float *__restrict__ kv, int ldkv, int 
 // ------------------------------------------------------------------ dense mix
 
 // DenseFormer (gpu/arch.rs:1492-1500): stream[i+1] = x; x <- x + sum_{j <= i+1} w_j stream_j, the
-// terms added one at a time in j order.
+// terms added one at a time in j order. The caller hands the block's output over as stream[i+1]
+// itself (a buffer exchange on the host, not a copy), and the mixed rows go to a separate `x`.
 struct DenseArgs {
-    float *x;
-    float *streams[17];
+    float *x;                    // out: the mixed rows
+    const float *streams[17];    // streams[ns - 1]: the block's output (x before the mix)
     float w[17];
-    int ns;  // i + 2 terms (the last is the stream being written)
+    int ns;  // i + 2 terms (the last is the block's output)
     size_t n4;
 };
 
 __global__ __launch_bounds__(256) void dense_mix_kernel(DenseArgs a) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.n4) return;
-    const f32x4 x = reinterpret_cast<const f32x4 *>(a.x)[i];
-    reinterpret_cast<f32x4 *>(a.streams[a.ns - 1])[i] = x;
+    const f32x4 x = reinterpret_cast<const f32x4 *>(a.streams[a.ns - 1])[i];
     f32x4 mix = x;
     for (int j = 0; j < a.ns; j++) {
         const f32x4 s = j == a.ns - 1 ? x : reinterpret_cast<const f32x4 *>(a.streams[j])[i];
@@ -730,12 +730,9 @@ __global__ __launch_bounds__(256) void dense_rms_kernel(DenseArgs a, int n, int 
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int c = min(i * 64 + lane, nq - 1);
-        x[i] = reinterpret_cast<const f32x4 *>(a.x)[base + c];
+        x[i] = reinterpret_cast<const f32x4 *>(a.streams[a.ns - 1])[base + c];
         v[i] = x[i];
     }
-#pragma unroll
-    for (int i = 0; i < NV; i++)
-        if (i * 64 + lane < nq) reinterpret_cast<f32x4 *>(a.streams[a.ns - 1])[base + i * 64 + lane] = x[i];
     for (int j0 = 0; j0 < a.ns - 1; j0 += 4) {
         f32x4 sv[4][NV];
 #pragma unroll
@@ -1269,6 +1266,7 @@ int dense_rms(float *x, float *const *streams, const float *w, int ns, int n, in
               int8_t *xq, int32_t *xexp, int ldq, float *hout, hipStream_t st) {
     AVA_REQUIRE(ns >= 2 && ns <= 17 && d % 4 == 0 && d <= 1024 && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE,
                 "dense_rms: %d streams, d=%d", ns, d);
+    for (int j = 0; j < ns; j++) AVA_REQUIRE(streams[j] != x, AVA_ERR_ARG, "dense_rms: x is stream %d", j);
     DenseArgs a;
     a.x = x;
     for (int j = 0; j < ns; j++) {
@@ -1300,6 +1298,7 @@ int embed_rms(const int32_t *ids, const float *emb, int n, int d, int vocab, flo
 
 int dense_mix(float *x, float *const *streams, const float *w, int ns, size_t n, hipStream_t st) {
     AVA_REQUIRE(ns >= 2 && ns <= 17 && n % 4 == 0, AVA_ERR_SHAPE, "dense_mix: %d streams", ns);
+    for (int j = 0; j < ns; j++) AVA_REQUIRE(streams[j] != x, AVA_ERR_ARG, "dense_mix: x is stream %d", j);
     DenseArgs a;
     a.x = x;
     for (int j = 0; j < ns; j++) {

@@ -514,6 +514,9 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
                                         (size_t)H * 4, (size_t)H * 4, N, st));
         AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.w2.w, ava::Q8_ADD, m->x, d, nullptr, st));
         if (c.dense) {
+            // the block's output becomes stream i + 1 by a buffer exchange; the mix lands in the
+            // buffer that stream held (nothing reads a stream or x across forwards)
+            std::swap(m->x, m->streams[i + 1]);
             if (i + 1 < L) {
                 AVA_RUN("dense_mix", ava::dense_rms(m->x, m->streams.data(), b.dense.data(), i + 2, N, d,
                                                     m->blocks[i + 1].lif_norm, P, m->xq, m->xexp, ldd, nullptr, st));
