@@ -186,6 +186,11 @@ int embed(const int32_t *ids, const float *emb, int n, int d, int vocab, float *
 int rms_planes(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
                float *hout, hipStream_t st);
 // G = h . W in f32 (fp32 MFMA tiles; few rows: a VALU kernel over 4 rows per workgroup).
+// rms_planes (no h) and gate_gemm of the normed rows in one launch, the same bits as the two; many
+// rows (rms_gate_many_fits: at least 65,536, d = 1024, nc <= 96).
+bool rms_gate_many_fits(int n, int d, int nc);
+int rms_gate_many(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
+                  const float *w, int nc, float *g, hipStream_t st);
 int gate_gemm(const float *h, int n, int d, const float *w, int nc, float *g, hipStream_t st);
 // For few rows: the norm's planes and the gate projections of the normed rows in one launch.
 bool rms_gate_fits(int n, int d, int nc);

@@ -86,9 +86,9 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t *__restrict__ 
 // h = x (mean(x^2) + eps)^-1/2 * gain (gpu/model.rs:458-462) of one row held in a wave's registers
 // (NV float4 chunks per lane, zero past d); its planes, and h itself when hout.
 template <int P, int NV>
-__device__ __forceinline__ void row_rms_planes(f32x4 (&v)[NV], int lane, int d, const float *__restrict__ gain,
-                                               size_t n, size_t row, int8_t *__restrict__ xq,
-                                               int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
+__device__ __forceinline__ float row_rms_planes(f32x4 (&v)[NV], int lane, int d, const float *__restrict__ gain,
+                                                size_t n, size_t row, int8_t *__restrict__ xq,
+                                                int32_t *__restrict__ xexp, int ldq, float *__restrict__ hout) {
     const int nq = d >> 2;
     float ss = 0.0f;
 #pragma unroll
@@ -109,6 +109,7 @@ __device__ __forceinline__ void row_rms_planes(f32x4 (&v)[NV], int lane, int d, 
         }
     }
     put_planes<P, NV>(v, lane, d, ldq, n, row, xq, xexp);
+    return inv;  // the row's 1 / rms, the same value for every lane
 }
 
 template <int P, int NV>
@@ -138,27 +139,33 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
 // the next step's tiles in flight meanwhile.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int GR = 128, GK = 32;
-template <int NCB>  // column blocks of 32
-__global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict__ h, int n, int d,
-                                                        const float *__restrict__ w, int nc, float *__restrict__ g) {
+// The K loop and stores of gate_mfma_kernel for the 128-row block at r0. The block's rows come from
+// h, or, with NORM, from x normed as they are staged: h = (x * s_inv[row]) * gain[k], the two
+// roundings of row_rms_planes, so G gets the same bits either way.
+template <int NCB, bool NORM>
+__device__ __forceinline__ void gate_block(const float *__restrict__ h, int n, int d, const float *__restrict__ w,
+                                           int nc, float *__restrict__ g, int r0, const float *s_inv,
+                                           const float *__restrict__ gain) {
     __shared__ float sh[GR][GK + 1];
     __shared__ float sw[GK][NCB * 32 + 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * GR;
+    const int last = min(GR, n - r0) - 1;  // the block's last row (rows past n repeat it, unstored)
     f32x16 acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[cb] = f32x16{};
     // the next K step's tiles are loaded into registers while this one is multiplied: h 128 rows x 32
     // floats (8 threads per row, a float4 each, HR per thread), W 32 x 32 NCB (WR floats per thread)
     constexpr int HR = GR * GK / 4 / 256, WR = GK * NCB * 32 / 256;
-    f32x4 hr[HR];
+    f32x4 hr[HR], gr = {1.0f, 1.0f, 1.0f, 1.0f};
     float wr[WR];
+    const int kk0 = (tid & 7) * 4;  // every j of a thread stages the same 4 columns of K
     auto fetch = [&](int k0) {
 #pragma unroll
         for (int j = 0; j < HR; j++) {
-            const int i = tid + j * 256, rr = i >> 3, kk = (i & 7) * 4;
-            hr[j] = *reinterpret_cast<const f32x4 *>(h + (size_t)min(r0 + rr, n - 1) * d + k0 + kk);
+            const int i = tid + j * 256, rr = min(i >> 3, last);
+            hr[j] = *reinterpret_cast<const f32x4 *>(h + (size_t)(r0 + rr) * d + k0 + kk0);
         }
+        if (NORM) gr = *reinterpret_cast<const f32x4 *>(gain + k0 + kk0);
 #pragma unroll
         for (int j = 0; j < WR; j++) {
             const int i = tid + j * 256, kk = i / (NCB * 32), cc = i % (NCB * 32);
@@ -170,9 +177,15 @@ __global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict_
         __syncthreads();  // the previous step's tiles are read
 #pragma unroll
         for (int j = 0; j < HR; j++) {
-            const int i = tid + j * 256, rr = i >> 3, kk = (i & 7) * 4;
+            const int i = tid + j * 256, rr = i >> 3;
+            if (NORM) {
+                const float inv = s_inv[min(rr, last)];
 #pragma unroll
-            for (int z = 0; z < 4; z++) sh[rr][kk + z] = hr[j][z];
+                for (int z = 0; z < 4; z++) sh[rr][kk0 + z] = (hr[j][z] * inv) * gr[z];
+            } else {
+#pragma unroll
+                for (int z = 0; z < 4; z++) sh[rr][kk0 + z] = hr[j][z];
+            }
         }
 #pragma unroll
         for (int j = 0; j < WR; j++) {
@@ -202,6 +215,50 @@ __global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict_
             if (row < n) g[(size_t)row * nc + col] = acc[cb][r];
         }
     }
+}
+
+template <int NCB>  // column blocks of 32
+__global__ __launch_bounds__(256) void gate_mfma_kernel(const float *__restrict__ h, int n, int d,
+                                                        const float *__restrict__ w, int nc, float *__restrict__ g) {
+    gate_block<NCB, false>(h, n, d, w, nc, g, blockIdx.x * GR, nullptr, nullptr);
+}
+
+// RMSNorm, planes and gate projections of many rows in one launch (the prefill form of
+// rms_gate_kernel), d = 1024, a 128-row block per workgroup: wave w norms the block's rows
+// 32w..32w+31 one at a time as rms_planes_kernel does (planes to xq; each row's loads issued before
+// the previous row's norm), keeping the rows' 1 / rms in LDS; the block then runs gate_mfma_kernel's
+// K loop on the rows normed again as they are staged. G and the planes get the bits of
+// rms_planes_kernel + gate_mfma_kernel, and h makes no round trip through HBM (x is read a second
+// time, partly from the cache hierarchy).
+template <int P, int NCB>
+__global__ __launch_bounds__(256, 2) void rms_gate_mfma_kernel(const float *__restrict__ x, int n,
+                                                               const float *__restrict__ gain, int8_t *__restrict__ xq,
+                                                               int32_t *__restrict__ xexp, int ldq,
+                                                               const float *__restrict__ w, int nc,
+                                                               float *__restrict__ g) {
+    constexpr int d = 1024, NV = 4;
+    __shared__ float s_inv[GR];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * GR, w0 = r0 + wave * 32;
+    f32x4 cur[NV], nxt[NV];
+    auto load_row = [&](int row, f32x4 (&v)[NV]) {
+        const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)min(row, n - 1) * d);
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = xr[i * 64 + lane];
+    };
+    load_row(w0, cur);
+    for (int j = 0; j < 32; j++) {
+        if (j + 1 < 32) load_row(w0 + j + 1, nxt);
+        if (w0 + j < n) {  // wave-uniform
+            const float inv =
+                row_rms_planes<P, NV>(cur, lane, d, gain, (size_t)n, (size_t)(w0 + j), xq, xexp, ldq, nullptr);
+            if (lane == 0) s_inv[wave * 32 + j] = inv;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) cur[i] = nxt[i];
+    }
+    __syncthreads();  // every row's 1 / rms is in s_inv (gate_block's first barrier follows too)
+    gate_block<NCB, true>(x, n, d, w, nc, g, r0, s_inv, gain);
 }
 
 // ------------------------------------------------------------------ memory read-out
@@ -1122,6 +1179,31 @@ int rms_gate(const float *x, int n, int d, const float *gain, int planes, int8_t
     else AVA_RG(3);
 #undef AVA_RG
     AVA_LAUNCHED("rms_gate");
+    return AVA_OK;
+}
+
+// From 512 blocks of rows (two per CU) the one launch beats the two (131,072 rows: 430 against 520 us);
+// with fewer, its norms run on too few workgroups.
+bool rms_gate_many_fits(int n, int d, int nc) { return n >= 512 * GR && d == 1024 && nc > 0 && nc <= 96; }
+
+int rms_gate_many(const float *x, int n, int d, const float *gain, int planes, int8_t *xq, int32_t *xexp, int ldq,
+                  const float *w, int nc, float *g, hipStream_t st) {
+    AVA_REQUIRE(rms_gate_many_fits(n, d, nc) && ldq >= d && ldq % 4 == 0, AVA_ERR_SHAPE,
+                "rms_gate_many: n=%d d=%d nc=%d", n, d, nc);
+    const int blocks = ceil_div(n, GR);
+#define AVA_RGM(P_, C_) rms_gate_mfma_kernel<P_, C_><<<blocks, 256, 0, st>>>(x, n, gain, xq, xexp, ldq, w, nc, g)
+#define AVA_RGMP(P_)                                  \
+    switch ((nc + 31) / 32) {                         \
+    case 1: AVA_RGM(P_, 1); break;                    \
+    case 2: AVA_RGM(P_, 2); break;                    \
+    default: AVA_RGM(P_, 3); break;                   \
+    }
+    if (planes == 1) AVA_RGMP(1)
+    else if (planes == 2) AVA_RGMP(2)
+    else AVA_RGMP(3)
+#undef AVA_RGMP
+#undef AVA_RGM
+    AVA_LAUNCHED("rms_gate_many");
     return AVA_OK;
 }
 

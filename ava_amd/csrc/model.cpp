@@ -469,6 +469,10 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
             AVA_RUN("rms_planes", ava::rms_gate(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, b.wgate, 2 * nh + 2 * r,
                                                 m->G, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
+        } else if (ava::rms_gate_many_fits(N, d, 2 * nh + 2 * r)) {
+            AVA_RUN("rms_gate", ava::rms_gate_many(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, b.wgate,
+                                                   2 * nh + 2 * r, m->G, st));
+            AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));
         } else {
             AVA_RUN("rms_planes", ava::rms_planes(m->x, N, d, b.mem_norm, P, m->xq, m->xexp, ldd, m->h, st));
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.wproj.w, ava::Q8_STORE, m->P, 5 * d, nullptr, st));

@@ -103,6 +103,36 @@ def test_config3_stack_full_length(dev):
     F.run_forced("ava04_d1024", 2, 2048, seed=41, envelope=True)
 
 
+def test_config3_rows_split_across_forwards_give_the_same_bits(dev):
+    """config[3]'s model over 32 streams of 2048 tokens (65,536 rows: the memory norm and its gate
+    projections in one launch, rms_gate_many) equals the same streams run as two forwards of 16 (32,768
+    rows: rms_planes then gate_gemm, no fused launch) bit for bit: logits and every carried state. Every
+    kernel of the stack computes a row (or a stream) the same way at any row count, so any difference
+    is a fused-path defect; the oracle pins the two-launch path (test_config3_stack_full_length)."""
+    from ava_amd.model import Model
+    cfg = synth.config("ava04_d1024")
+    m = Model(cfg, synth.params(cfg, seed=43))
+    B, T = 32, 2048
+    ids = torch.from_numpy(np.random.default_rng(44).integers(0, cfg["vocab"], (B, T)).astype(np.int32)).cuda()
+    print(f"config[3] rows split B={B} T={T}", flush=True)
+    st = m.state(B, eng_cap=T)
+    whole = m.forward_with_state(ids, st)
+    halves, sts = [], []
+    for h in range(2):
+        sh = m.state(B // 2, eng_cap=T)
+        halves.append(m.forward_with_state(ids[h * B // 2:(h + 1) * B // 2].contiguous(), sh))
+        sts.append(sh)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, torch.cat(halves, dim=0))
+    for name in ("lif_v", "lif_s", "lif_a", "mem_f", "mem_s"):
+        full = getattr(st, name)
+        parts = [getattr(x, name) for x in sts]
+        # state tensors are [L][B][...]: the stream axis is 1
+        assert torch.equal(full, torch.cat(parts, dim=1)), name
+    for name in ("eng_k", "eng_v"):  # [B][cap][de]
+        assert torch.equal(getattr(st, name), torch.cat([getattr(x, name) for x in sts], dim=0)), name
+
+
 def test_config0_greedy_512_prompt_128_steps(dev):
     """config[0]: the d=512 model, one stream, a 512-token prompt and 128 greedy steps (argmax, the
     lowest id on ties) as Model.generate runs them (one forward per token with carried state). The
