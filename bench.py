@@ -57,6 +57,7 @@ class Lif:
     gain 0.05; int2 spikes, subtract reset; outputs int8 spikes, final v and theta."""
 
     name = "lif"
+    metric = "tokens/sec LIF scan @B=64,T=2048,C=2048 (config[1]), int2 spikes, ALIF, 1 GPU; % HBM roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "lif_scan_kernel"
 
@@ -124,6 +125,7 @@ class Kwta:
     """kWTA + relu2 over config[3]'s wide layer: u [131072, 4096] ~N(0,1), k = 1024."""
 
     name = "kwta"
+    metric = "tokens/sec kWTA + relu2 planes @131072 rows (tokens) x 4096, k=1024 (config[3] wide layer), 1 GPU; % HBM roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "kwta_kernel"
 
@@ -172,6 +174,7 @@ class Gemm:
     """One dense int8 product of config[3]: x [131072, 1024] f32 -> 3 planes -> i8 MFMA -> y [131072, 4096]."""
 
     name = "gemm"
+    metric = "tokens/sec int8 product @131072 rows (tokens) x 1024 -> 4096, 3 activation planes (config[3] W1), 1 GPU; % i8 MFMA roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "q8_gemm_kernel"
 
@@ -261,6 +264,7 @@ class Delta:
     token and head, W_0 = 0."""
 
     name = "delta"
+    metric = "tokens/sec chunked delta rule @B=32,H=8,T=4096,d=64, chunks of 64 (config[2]), 1 GPU; % fp32 MFMA roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "delta_chunk_kernel"
 
@@ -331,6 +335,7 @@ class LifBwd:
     per-stream state and parameter gradients."""
 
     name = "lif_bwd"
+    metric = "tokens/sec LIF scan backward @B=64,T=2048,C=2048 (config[1] shape), 1 GPU; % HBM roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "lif_bwd_kernel"
 
@@ -397,6 +402,7 @@ class MemBwd:
     b ~U(0.1, 1.9), dL/dy ~N(0,1), from a zero state."""
 
     name = "mem_bwd"
+    metric = "tokens/sec fast-weight memory backward @64 streams x 16 heads x 2048 (config[3] block), 1 GPU"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "mem_bwd_kernel"
 
@@ -482,6 +488,7 @@ class MemChunk:
     the same inputs is timed beside it."""
 
     name = "mem_chunk"
+    metric = "tokens/sec chunked fast-weight memory @64 streams x 16 heads x 2048 (config[3] block), 1 GPU; % fp32 MFMA roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "mem_chunk_kernel"
 
@@ -588,6 +595,8 @@ class Copy:
     """A plain 1 GiB device-to-device copy: the calibration kernel for the FETCH/WRITE_SIZE counters."""
 
     name = "copy"
+    metric = "calls/sec 1 GiB device copy (counter calibration), 1 GPU; % HBM roofline"
+    unit = "calls/s"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
     kernel = "copy"
 
@@ -786,6 +795,7 @@ class StackHeads(Stack):
     head of 64. Not the headline line: it shows what the reference's own engram costs on this path."""
 
     name = "stack_heads"
+    metric = "tokens/sec int8 block-stack forward @B=64,T=2048, engram of 32 heads of 32, 1 GPU; % HBM / MFMA roofline"
 
     def __init__(self, B=64, T=2048, planes=3):
         super().__init__(B=B, T=T, cfg_name="ava04_d1024_heads", planes=planes)
@@ -1045,7 +1055,7 @@ def main():
     out = {
         "metric": getattr(W, "metric", METRIC),
         "value": value,
-        "unit": "tokens/s",
+        "unit": getattr(W, "unit", "tokens/s"),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
