@@ -136,7 +136,7 @@ def guide_functions():
 
 
 def test_binding_guide_structs_match_the_header():
-    """INTEGRATION.md's #[repr(C)] structs have the header's fields in the header's order and widths,
+    """The binding guide's #[repr(C)] structs have the header's fields in the header's order and widths,
     so a binding written from the guide passes structs of the right size and layout."""
     hs, gs = header_structs(), guide_structs()
     for name in ("ava_qw", "ava_config", "ava_block_params", "ava_params", "ava_state"):
