@@ -331,14 +331,15 @@ __device__ __forceinline__ void kv_put(float *p, size_t i, float v) { p[i] = v; 
 __device__ __forceinline__ void kv_put(__half *p, size_t i, float v) { p[i] = __float2half_rn(v); }
 
 // 16-byte loads of the store: DPL elements per lane (4 f32 or 8 fp16), widened to f32; load16: 16
-// consecutive elements.
+// consecutive elements. `load` (the decode read, which streams each entry once) is non-temporal:
+// 386 -> 370 us for 256 streams x 32,768 fp16 entries of 64 dims (5.55 -> 5.81 TB/s, the same bits).
 template <typename KV>
 struct KvLane;
 template <>
 struct KvLane<float> {
     static constexpr int DPL = 4;
     static __device__ __forceinline__ void load(const float *p, float (&x)[4]) {
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
+        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
 #pragma unroll
         for (int z = 0; z < 4; z++) x[z] = v[z];
     }
@@ -356,8 +357,9 @@ template <>
 struct KvLane<__half> {
     static constexpr int DPL = 8;
     static __device__ __forceinline__ void load(const __half *p, float (&x)[8]) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(p);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+        const uint32_t w[4] = {u[0], u[1], u[2], u[3]};
 #pragma unroll
         for (int z = 0; z < 4; z++) {
             const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[z]));
