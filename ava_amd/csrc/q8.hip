@@ -218,7 +218,9 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
                     float v = ldexpf(value(i, j, r), ex[r]) * sc[j];
                     if (EPI == EPI_MUL) v = v * cv[j];
                     if (EPI == EPI_ADD) v = prev[r] + v;
-                    store_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4, v);
+                    const unsigned so = (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4;
+                    if (EPI == EPI_ADD) store_f32(yr, voff + j * 128u, so, v);
+                    else store_f32_nt(yr, voff + j * 128u, so, v);
                 }
             }
         }
