@@ -349,7 +349,8 @@ __global__ __launch_bounds__(NTH) void cb_code_kernel(const float *__restrict__ 
                         for (int q0 = 0; q0 < cnt; q0 += QB) {
                             float v[QB];
 #pragma unroll
-                            for (int z = 0; z < QB; z++) v[z] = tb[(size_t)s_lu[min(q0 + z, cnt - 1)] * d];
+                            for (int z = 0; z < QB; z++)  // non-temporal: rows of a 12.9 GB table, read once
+                                v[z] = __builtin_nontemporal_load(tb + (size_t)s_lu[min(q0 + z, cnt - 1)] * d);
                             AVA_ISSUE_FENCE();
 #pragma unroll
                             for (int z = 0; z < QB; z++)
@@ -650,10 +651,10 @@ __global__ __launch_bounds__(NT) void cb_table_kernel(const float *__restrict__ 
             for (int q = 0; q < total; q++) {
                 f4 *tr = reinterpret_cast<f4 *>(tb + (size_t)s_u[q] * d + c4);
                 const float s = s_s[q];
-                f4 t = *tr;
+                f4 t = __builtin_nontemporal_load(tr);  // a kept unit's row, read and written once
 #pragma unroll
                 for (int z = 0; z < 4; z++) t[z] -= s * dv[z];
-                *tr = t;
+                __builtin_nontemporal_store(t, tr);
             }
         }
     }
