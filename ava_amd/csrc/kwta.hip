@@ -306,8 +306,8 @@ __global__ __launch_bounds__(RW > 4 ? 64 * RW : 256) void kwta_kernel(const floa
                 ava::to_planes<P>(x[i][3], e, q3);
 #pragma unroll
                 for (int p = 0; p < P; p++)
-                    reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq)[c] =
-                        ava::pack4(q0[p], q1[p], q2[p], q3[p]);
+                    __builtin_nontemporal_store(ava::pack4(q0[p], q1[p], q2[p], q3[p]),
+                                                reinterpret_cast<uint32_t *>(xq + ((size_t)p * n + row) * ldq) + c);
             }
         }
         // zero the K padding of the planes (ldq > h)
