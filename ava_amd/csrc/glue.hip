@@ -820,7 +820,7 @@ __global__ __launch_bounds__(256) void dense_rms_kernel(DenseArgs a, int n, int 
         if (c < nq) {
 #pragma unroll
             for (int z = 0; z < 4; z++) v[i][z] = v[i][z] + x[i][z] * wl;
-            reinterpret_cast<f32x4 *>(a.x)[base + c] = v[i];
+            __builtin_nontemporal_store(v[i], reinterpret_cast<f32x4 *>(a.x) + base + c);
         } else {
             v[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
