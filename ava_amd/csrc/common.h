@@ -22,6 +22,9 @@ __device__ __forceinline__ void store_f32(BufRes r, unsigned voff, unsigned soff
 __device__ __forceinline__ float load_f32(BufRes r, unsigned voff, unsigned soff) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
+__device__ __forceinline__ float load_f32_nt(BufRes r, unsigned voff, unsigned soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 2));
+}
 // the same store, non-temporal (cache policy bit 1: `nt`)
 __device__ __forceinline__ void store_f32_nt(BufRes r, unsigned voff, unsigned soff, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, (int)soff, 2);
@@ -32,6 +35,7 @@ __device__ inline BufRes buf_res(float *base, unsigned) { return base; }
 __device__ inline void store_f32(BufRes, unsigned, unsigned, float) {}
 __device__ inline float load_f32(BufRes, unsigned, unsigned) { return 0.0f; }
 __device__ inline void store_f32_nt(BufRes, unsigned, unsigned, float) {}
+__device__ inline float load_f32_nt(BufRes, unsigned, unsigned) { return 0.0f; }
 #endif
 
 // A compiler-only barrier: memory operations are not moved across it. Placed after a batch of

@@ -210,7 +210,7 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
                 if (EPI == EPI_ADD) {
 #pragma unroll
                     for (int r = 0; r < 16; r++)
-                        prev[r] = load_f32(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
+                        prev[r] = load_f32_nt(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
                     AVA_ISSUE_FENCE();
                 }
 #pragma unroll
