@@ -75,7 +75,6 @@ def lib():
         "ava_q8_matmul_noalloc": [vp, i32, C.POINTER(QW), i32, vp, vp],
         "ava_q8_matmul_planes": [vp, vp, i32, i32, C.POINTER(QW), vp, vp],
         "ava_lif_scan": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp],
-        "ava_lif_scan_tuned": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, vp, vp, i32, i32, vp],
         "ava_kwta": [vp, i32, i32, i32, i32, vp, vp, vp],
         "ava_mem_scan": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_mem_chunk": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
@@ -116,7 +115,7 @@ def lib():
     if hasattr(L, "ava_model_scratch_bytes"):
         L.ava_model_scratch_bytes.argtypes = [vp]
         L.ava_model_scratch_bytes.restype = sz
-    L.ava_model_nonfinite.argtypes = [vp, vp, C.POINTER(C.c_int), vp]
+    L.ava_model_nonfinite.argtypes = [vp, vp, i32, C.POINTER(C.c_int), vp]
     L.ava_model_nonfinite.restype = i32
     L.ava_model_set_trace.argtypes = [vp, vp, vp, vp, sz]
     L.ava_model_set_trace.restype = i32

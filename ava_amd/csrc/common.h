@@ -174,8 +174,8 @@ __device__ __forceinline__ float lif_spike(float v, float th, int levels, int is
 }
 
 // lif.hip / kwta.hip / mem.hip
-int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
-                   int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf, hipStream_t st);
+int lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
+             int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st);
 int kwta_planes(const float *u, int n, int h, int k, int relu2, int planes, int8_t *xq, int32_t *xexp, int ldq,
                 float *kth, hipStream_t st);
 int mem_scan_strided(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,

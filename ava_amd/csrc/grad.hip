@@ -24,72 +24,97 @@ __global__ __launch_bounds__(256) void relu2_bwd_kernel(const float *__restrict_
     reinterpret_cast<f32x4 *>(gu)[i] = o;
 }
 
-// The dense mix of block i, out = raw + sum_{j <= i + 1} w_ij S_j (S_{i+1} = raw), has the backward
-//   dL/dS_c = base + sum_{k = i0 .. L-1} w_k[c] G_k    (G_k = dL/d(the mix after block k)),
-//   dL/dw_ij = sum_e G_i,e S_j,e.
-// Here: out = base + sum_k w_k[col] G_k over e, and part[wg][j] = this workgroup's share of
-// sum_e base_e S_j,e for j < nd (the products, as gpu/lif.cu:4922-4971's dense_back). wf holds block
-// k's k + 2 weights from k (k + 3) / 2.
-constexpr int DENSE_MAXD = 32, DENSE_WG = 1024;
+// The dense mix of block i, mix_i = raw_i + sum_{j <= i + 1} w_ij S_j, has the backward
+//   dL/dS_c  = base + sum_{k = i0 .. L-1} w_k[c] G_k   (G_k = dL/d(the mix after block k), base = the
+//              gradient that reaches S_c directly),
+//   dL/dw_ij = <G_i, S_j>  (a dot product over all rows and channels).
+// wf holds block k's k + 2 weights from offset k (k + 3) / 2.
+//
+// One workgroup owns a chunk of DB_CHUNK consecutive floats. It loads its chunk of `base` into
+// registers once and uses it twice: as the start of the gradient sum (the G_k streamed through, each
+// term rounded in block order, so the sum has the oracle's bits), and as the left operand of the nd
+// dot products, each of which streams one S_j chunk through and leaves one partial per (j, chunk).
+// The partials are stored j-major (part[j][chunk]) and reduced by one wave per j in a fixed order,
+// so dw does not depend on scheduling.
+constexpr int DB_THREADS = 256, DB_PER_THREAD = 4;  // f32x4 vectors per thread
+constexpr int DB_CHUNK4 = DB_THREADS * DB_PER_THREAD;  // f32x4 vectors per workgroup
+constexpr int DB_MAXD = 32;
 
 struct DenseBackArgs {
     const float *S, *G, *wf, *base;
     float *out, *part;
-    int col, i0, L, nd;
+    int col, i0, L, nd, nchunk;
     size_t M4;
 };
 
-__global__ __launch_bounds__(256) void dense_back_kernel(DenseBackArgs a) {
-    __shared__ float red[4][DENSE_MAXD];
-    float acc[DENSE_MAXD];
-#pragma unroll
-    for (int j = 0; j < DENSE_MAXD; j++) acc[j] = 0.0f;
+__global__ __launch_bounds__(DB_THREADS) void dense_grad_kernel(DenseBackArgs a) {
+    __shared__ float wsum[DB_MAXD][DB_THREADS / 64];
     const size_t M = a.M4 * 4;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < a.M4; i += (size_t)gridDim.x * 256) {
-        const f32x4 g = reinterpret_cast<const f32x4 *>(a.base)[i];
-        f32x4 x = g;
-        for (int k = a.i0; k < a.L; k++) {
-            const float w = a.wf[k * (k + 3) / 2 + a.col];
-            const f32x4 gk = reinterpret_cast<const f32x4 *>(a.G + (size_t)k * M)[i];
+    const size_t c0 = (size_t)blockIdx.x * DB_CHUNK4;
+    f32x4 bs[DB_PER_THREAD];
+    bool in[DB_PER_THREAD];
 #pragma unroll
-            for (int z = 0; z < 4; z++) x[z] = x[z] + w * gk[z];
-        }
-        reinterpret_cast<f32x4 *>(a.out)[i] = x;
-#pragma unroll
-        for (int j = 0; j < DENSE_MAXD; j++)
-            if (j < a.nd) {
-                const f32x4 s = reinterpret_cast<const f32x4 *>(a.S + (size_t)j * M)[i];
-                acc[j] = fmaf(g[0], s[0], acc[j]);
-                acc[j] = fmaf(g[1], s[1], acc[j]);
-                acc[j] = fmaf(g[2], s[2], acc[j]);
-                acc[j] = fmaf(g[3], s[3], acc[j]);
-            }
+    for (int r = 0; r < DB_PER_THREAD; r++) {
+        const size_t i = c0 + r * DB_THREADS + threadIdx.x;
+        in[r] = i < a.M4;
+        bs[r] = in[r] ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.base) + i) : f32x4{0, 0, 0, 0};
     }
-    if (a.nd == 0) return;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // the gradient into stream `col`, block terms in order
+    f32x4 acc[DB_PER_THREAD];
 #pragma unroll
-    for (int j = 0; j < DENSE_MAXD; j++)
-        if (j < a.nd) {
-            const float s = ava::wave_sum(acc[j]);
-            if (lane == 0) red[w][j] = s;
+    for (int r = 0; r < DB_PER_THREAD; r++) acc[r] = bs[r];
+    for (int k = a.i0; k < a.L; k++) {
+        const float w = a.wf[k * (k + 3) / 2 + a.col];
+        const f32x4 *gk = reinterpret_cast<const f32x4 *>(a.G + (size_t)k * M);
+        f32x4 g[DB_PER_THREAD];
+#pragma unroll
+        for (int r = 0; r < DB_PER_THREAD; r++)
+            g[r] = in[r] ? __builtin_nontemporal_load(gk + c0 + r * DB_THREADS + threadIdx.x) : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < DB_PER_THREAD; r++)
+#pragma unroll
+            for (int z = 0; z < 4; z++) acc[r][z] = acc[r][z] + w * g[r][z];
+    }
+#pragma unroll
+    for (int r = 0; r < DB_PER_THREAD; r++)
+        if (in[r]) __builtin_nontemporal_store(acc[r], reinterpret_cast<f32x4 *>(a.out) + c0 + r * DB_THREADS + threadIdx.x);
+    if (a.nd == 0) return;
+    // the weight gradients: <base, S_j> over this chunk, one j at a time
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int j = 0; j < a.nd; j++) {
+        const f32x4 *sj = reinterpret_cast<const f32x4 *>(a.S + (size_t)j * M);
+        float d = 0.0f;
+#pragma unroll
+        for (int r = 0; r < DB_PER_THREAD; r++) {
+            const f32x4 s = in[r] ? __builtin_nontemporal_load(sj + c0 + r * DB_THREADS + threadIdx.x) : f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int z = 0; z < 4; z++) d = fmaf(bs[r][z], s[z], d);
         }
+        d = ava::wave_sum(d);
+        if (lane == 0) wsum[j][wv] = d;
+    }
     __syncthreads();
     if ((int)threadIdx.x < a.nd) {
         const int j = threadIdx.x;
-        a.part[(size_t)blockIdx.x * a.nd + j] = ((red[0][j] + red[1][j]) + red[2][j]) + red[3][j];
+        float s = wsum[j][0];
+#pragma unroll
+        for (int w = 1; w < DB_THREADS / 64; w++) s += wsum[j][w];
+        a.part[(size_t)j * a.nchunk + blockIdx.x] = s;
     }
 }
 
-// dw[j] = the workgroups' shares added in workgroup order (one thread per j).
-__global__ void dense_back_sum_kernel(const float *__restrict__ part, int nwg, int nd, float *__restrict__ dw) {
-    const int j = threadIdx.x;
-    if (j >= nd) return;
+// dw[j] = the sum of row j of part [nd][nchunk]: one wave per j, lane l adding chunks l, l + 64, ...
+// in order, then the wave's butterfly.
+__global__ __launch_bounds__(64) void dense_grad_sum_kernel(const float *__restrict__ part, int nchunk,
+                                                            float *__restrict__ dw) {
+    const float *row = part + (size_t)blockIdx.x * nchunk;
     float s = 0.0f;
-    for (int g = 0; g < nwg; g++) s += part[(size_t)g * nd + j];
-    dw[j] = s;
+    for (int c = threadIdx.x; c < nchunk; c += 64) s += row[c];
+    s = ava::wave_sum(s);
+    if (threadIdx.x == 0) dw[blockIdx.x] = s;
 }
 
-int dense_back_grid(size_t M4) { return (int)std::min<size_t>(DENSE_WG, std::max<size_t>(1, (M4 + 255) / 256)); }
+int dense_back_chunks(size_t M4) { return (int)std::max<size_t>(1, (M4 + DB_CHUNK4 - 1) / DB_CHUNK4); }
 
 }  // namespace
 
@@ -105,7 +130,7 @@ extern "C" int ava_kwta_relu2_bwd(const float *u, const float *kth, int n, int h
 }
 
 extern "C" size_t ava_dense_back_part_floats(long long M, int nd) {
-    return M > 0 && nd > 0 ? (size_t)dense_back_grid((size_t)M / 4) * nd : 0;
+    return M > 0 && nd > 0 ? (size_t)dense_back_chunks((size_t)M / 4) * nd : 0;
 }
 
 extern "C" int ava_dense_back(const float *S, const float *G, const float *wf, const float *base, float *out, float *dw,
@@ -113,21 +138,21 @@ extern "C" int ava_dense_back(const float *S, const float *G, const float *wf, c
                               ava_stream stream) {
     AVA_REQUIRE(G && wf && base && out, AVA_ERR_ARG, "dense_back: NULL buffer");
     AVA_REQUIRE(M > 0 && M % 4 == 0, AVA_ERR_SHAPE, "dense_back: M=%lld (a multiple of 4)", M);
-    AVA_REQUIRE(nd >= 0 && nd <= DENSE_MAXD && i0 >= 0 && i0 <= L && col >= 0 && col <= L + 1, AVA_ERR_SHAPE,
-                "dense_back: col=%d i0=%d L=%d nd=%d (nd <= %d)", col, i0, L, nd, DENSE_MAXD);
+    AVA_REQUIRE(nd >= 0 && nd <= DB_MAXD && i0 >= 0 && i0 <= L && col >= 0 && col <= L + 1, AVA_ERR_SHAPE,
+                "dense_back: col=%d i0=%d L=%d nd=%d (nd <= %d)", col, i0, L, nd, DB_MAXD);
     for (int k = i0; k < L; k++)
         AVA_REQUIRE(col <= k + 1, AVA_ERR_SHAPE, "dense_back: block %d has no weight %d", k, col);
     AVA_REQUIRE(nd == 0 || (S && dw && part), AVA_ERR_ARG, "dense_back: nd=%d needs S, dw and part", nd);
     const size_t M4 = (size_t)M / 4;
-    const int grid = dense_back_grid(M4);
-    AVA_REQUIRE(nd == 0 || part_floats >= (size_t)grid * nd, AVA_ERR_SHAPE, "dense_back: part holds %zu < %zu floats",
-                part_floats, (size_t)grid * nd);
+    const int nchunk = dense_back_chunks(M4);
+    AVA_REQUIRE(nd == 0 || part_floats >= (size_t)nchunk * nd, AVA_ERR_SHAPE,
+                "dense_back: part holds %zu < %zu floats", part_floats, (size_t)nchunk * nd);
     const hipStream_t st = (hipStream_t)stream;
-    DenseBackArgs a{S, G, wf, base, out, part, col, i0, L, nd, M4};
-    dense_back_kernel<<<grid, 256, 0, st>>>(a);
+    DenseBackArgs a{S, G, wf, base, out, part, col, i0, L, nd, nchunk, M4};
+    dense_grad_kernel<<<nchunk, DB_THREADS, 0, st>>>(a);
     AVA_LAUNCHED("dense_back");
     if (nd > 0) {
-        dense_back_sum_kernel<<<1, 64, 0, st>>>(part, grid, nd, dw);
+        dense_grad_sum_kernel<<<nd, 64, 0, st>>>(part, nchunk, dw);
         AVA_LAUNCHED("dense_back_sum");
     }
     return AVA_OK;

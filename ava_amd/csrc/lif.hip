@@ -165,25 +165,16 @@ int launch_vp(const float *cur, int B, int T, int D, const float *ps, float *v, 
 
 namespace ava {
 
-// vec/pf 0 = the defaults: 1 channel per lane, 32 steps in flight (the fastest of 16, 32, 48 and 64 at
-// config[1]'s 131,072 lanes and at the block stack's 65,536).
-int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
-                   int levels, int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf,
-                   hipStream_t st) {
+// One channel per lane, 32 steps in flight: the fastest of 16, 32, 48 and 64 steps and of 1, 2 or 4
+// channels per lane at config[1]'s 131,072 lanes and at the block stack's 65,536.
+constexpr int LIF_VEC = 1, LIF_PF = 32;
+
+int lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
+             int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st) {
     AVA_REQUIRE(cur && ps && v && s && a && spikes, AVA_ERR_ARG, "lif_scan: NULL buffer");
     AVA_REQUIRE(B > 0 && T > 0 && D > 0, AVA_ERR_SHAPE, "lif_scan: B=%d T=%d D=%d", B, T, D);
     AVA_REQUIRE(levels == 1 || levels == 2, AVA_ERR_ARG, "lif_scan: levels %d (1 or 2)", levels);
-    if (vec == 0) vec = 1;
-    if (pf == 0) pf = 32;
-    if (D % vec) vec = 1;
-#define AVA_VP(VV, PP)                                                                              \
-    if (vec == VV && pf == PP)                                                                      \
-        return launch_vp<VV, PP>(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, st);
-    AVA_VP(1, 8) AVA_VP(1, 16) AVA_VP(1, 32) AVA_VP(1, 48) AVA_VP(1, 64)
-    AVA_VP(2, 8) AVA_VP(2, 16) AVA_VP(2, 32) AVA_VP(2, 48)
-    AVA_VP(4, 8) AVA_VP(4, 16)
-#undef AVA_VP
-    return fail(AVA_ERR_ARG, "lif_scan: no kernel for vec=%d pf=%d", vec, pf);
+    return launch_vp<LIF_VEC, LIF_PF>(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, st);
 }
 
 }  // namespace ava
@@ -191,14 +182,5 @@ int lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float
 extern "C" int ava_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s,
                             float *a, int levels, int is_signed, int alif, int8_t *spikes, float *th_out,
                             ava_stream stream) {
-    return ava::lif_scan_tuned(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, 0, 0,
-                               (hipStream_t)stream);
-}
-
-// ava_lif_scan with the kernel variant named (channels per lane, steps in flight).
-extern "C" int ava_lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v,
-                                  float *s, float *a, int levels, int is_signed, int alif, int8_t *spikes,
-                                  float *th_out, int vec, int pf, ava_stream stream) {
-    return ava::lif_scan_tuned(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, vec, pf,
-                               (hipStream_t)stream);
+    return ava::lif_scan(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, (hipStream_t)stream);
 }

@@ -395,6 +395,7 @@ int trace_copy(void *dst, size_t dpitch, const void *src, size_t spitch, size_t 
 // read and overwrite the code, the table and its scale).
 int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float *logits, hipStream_t st,
             hipEvent_t join = nullptr) {
+    m->bad_n = 0;  // a forward refused below reports no rows of an earlier one
     const ava_config &c = m->cfg;
     const int d = c.d, nh = d / c.head_size, r = c.gate_rank, H = c.hidden, de = c.eng_dim, L = c.layers;
     const int P = c.planes, N = B * T, ldd = ava::q8_ldk(d), ldh = ava::q8_ldk(H);
@@ -458,8 +459,8 @@ int forward(ava_model *m, ava_state *s, const int32_t *ids, int B, int T, float 
         } else {
             AVA_RUN("q8_gemm", ava::q8_gemm(m->xq, m->xexp, P, N, &b.win.w, c.lif_scale ? ava::Q8_MUL : ava::Q8_STORE,
                                             m->cur, d, b.omb, st));
-            AVA_RUN("lif_scan", ava::lif_scan_tuned(m->cur, B, T, d, b.ps, s->lif_v + sbd, s->lif_s + sbd,
-                                                    s->lif_a + sbd, c.levels, 1, c.alif, m->spk, nullptr, 0, 0, st));
+            AVA_RUN("lif_scan", ava::lif_scan(m->cur, B, T, d, b.ps, s->lif_v + sbd, s->lif_s + sbd,
+                                              s->lif_a + sbd, c.levels, 1, c.alif, m->spk, nullptr, st));
         }
         if (tracing)
             AVA_RUN("trace", trace_copy(m->tr_spk + ((size_t)i * m->tr_rows + m->tr_pos) * d, d, m->spk, ldd, d, N, st));
@@ -699,9 +700,11 @@ extern "C" int ava_model_decode_step(ava_model *m, ava_state *st, const int32_t 
 
 extern "C" size_t ava_model_scratch_bytes(const ava_model *m) { return m ? m->scratch_bytes : 0; }
 
-extern "C" int ava_model_nonfinite(ava_model *m, int32_t *rows, int *count, ava_stream stream) {
+extern "C" int ava_model_nonfinite(ava_model *m, int32_t *rows, int rows_cap, int *count, ava_stream stream) {
     AVA_REQUIRE(m && count, AVA_ERR_ARG, "model_nonfinite: NULL argument");
     *count = 0;
+    AVA_REQUIRE(!rows || rows_cap >= m->bad_n, AVA_ERR_SHAPE,
+                "model_nonfinite: rows holds %d entries, the last forward had %d streams", rows_cap, m->bad_n);
     if (m->bad_n == 0) return AVA_OK;
     std::vector<int32_t> h(m->bad_n);
     AVA_HIP(hipSetDevice(m->device));

@@ -225,7 +225,7 @@ class Model:
         if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
             raise ValueError("ids: a contiguous [B, T] int32 GPU tensor is required")
         B, T = ids.shape
-        self._last_B = B
+        self._last_B = 0  # set once the forward is accepted
         if want_logits and logits is None:
             logits = torch.empty((B * T, self.cfg["vocab"]), dtype=torch.float32, device=ids.device)
         cst = st.c()
@@ -233,6 +233,7 @@ class Model:
         check(lib().ava_model_forward(self.h, C.byref(cst), C.c_void_p(ids.data_ptr()), B, T,
                                       C.c_void_p(logits.data_ptr()) if want_logits else None, stream),
               "ava_model_forward")
+        self._last_B = B
         st.eng_len = cst.eng_len
         st.seen += T
         st.evict()
@@ -246,7 +247,7 @@ class Model:
         if not (ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous() and ids.dim() == 2):
             raise ValueError("ids: a contiguous [B, T] int32 GPU tensor is required")
         B, T = ids.shape
-        self._last_B = B
+        self._last_B = 0  # set once the step is accepted
         V = self.cfg["vocab"]
         if not (logits.is_cuda and logits.dtype == torch.float32 and logits.is_contiguous()
                 and logits.numel() >= B * T * V):
@@ -275,6 +276,7 @@ class Model:
         check(lib().ava_model_decode_step(self.h, C.byref(cst), C.c_void_p(ids.data_ptr()), B, T,
                                           C.c_void_p(logits.data_ptr()), pl, ld, pn, pz, stream),
               "ava_model_decode_step")
+        self._last_B = B
         st.eng_len = cst.eng_len
         st.seen += T
         st.evict()
@@ -330,6 +332,8 @@ class Model:
         if any(len(p) == 0 for p in prompts):
             raise ValueError("generate: an empty prompt")
         out = [[] for _ in prompts]
+        if max_new <= 0:
+            return out
         order = sorted(range(len(prompts)), key=lambda r: (len(prompts[r]), r))
         br = max(batch_rows, 1)
         eng = self.cfg["eng_block"] >= 0
@@ -381,7 +385,6 @@ class Model:
 
     def forward(self, ids: torch.Tensor):
         B, T = ids.shape
-        self._last_B = B
         st = self.state(B, eng_cap=T if self.cfg["eng_block"] >= 0 else 0)
         return self.forward_with_state(ids, st), st
 
@@ -412,7 +415,7 @@ class Model:
         stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
         B = getattr(self, "_last_B", 0)
         rows = (C.c_int32 * max(B, 1))()
-        check(lib().ava_model_nonfinite(self.h, rows, C.byref(n), stream), "ava_model_nonfinite")
+        check(lib().ava_model_nonfinite(self.h, rows, max(B, 1), C.byref(n), stream), "ava_model_nonfinite")
         return [i for i in range(B) if rows[i]] if n.value else []
 
     # launch timing by kernel class (ava_model_set_timing / ava_model_timing)

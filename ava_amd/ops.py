@@ -117,7 +117,7 @@ class LifState:
     a: torch.Tensor
 
 
-def lif_gen(cur, beta, theta=None, alif=None, levels=2, signed=True, init=None, vec=0, pf=0, th_out=False):
+def lif_gen(cur, beta, theta=None, alif=None, levels=2, signed=True, init=None, th_out=False):
     """lif_gen.rs:86-130: the LIF scan of cur [B, T, d]. Returns (spikes int8 [B, T, d], LifState[, th_T])."""
     _need(cur, torch.float32, "lif_gen")
     B, T, D = cur.shape
@@ -137,12 +137,8 @@ def lif_gen(cur, beta, theta=None, alif=None, levels=2, signed=True, init=None, 
         v, s, a = init.v.clone(), init.s.clone(), init.a.clone()
     spikes = torch.empty((B, T, D), dtype=torch.int8, device=dev)
     tho = torch.empty((B, D), dtype=torch.float32, device=dev) if th_out else None
-    if vec or pf:
-        rc = lib().ava_lif_scan_tuned(_p(cur), B, T, D, _p(ps), _p(v), _p(s), _p(a), levels, int(signed),
-                                      int(alif is not None), _p(spikes), _p(tho), vec, pf, _stream())
-    else:
-        rc = lib().ava_lif_scan(_p(cur), B, T, D, _p(ps), _p(v), _p(s), _p(a), levels, int(signed),
-                                int(alif is not None), _p(spikes), _p(tho), _stream())
+    rc = lib().ava_lif_scan(_p(cur), B, T, D, _p(ps), _p(v), _p(s), _p(a), levels, int(signed),
+                            int(alif is not None), _p(spikes), _p(tho), _stream())
     check(rc, "ava_lif_scan")
     st = LifState(v, s, a)
     return (spikes, st, tho) if th_out else (spikes, st)

@@ -83,7 +83,6 @@ class Lif:
         self.config = {"workload": "lif_scan config[1]", "B": B, "T": T, "C": D, "spikes": "int2",
                        "alif": True, "rho": 0.95, "gain": 0.05}
         self.dtype = "f32"
-        self.pf = 0  # steps in flight per lane; 0 = the library's default
 
     def step(self, stream, ev=None):
         from ava_amd._lib import check
@@ -94,10 +93,7 @@ class Lif:
                 C.c_void_p(self.v.data_ptr()), C.c_void_p(self.s.data_ptr()), C.c_void_p(self.a.data_ptr()), 2, 1, 1,
                 C.c_void_p(self.spikes.data_ptr()), C.c_void_p(self.th.data_ptr()))
         if ev: ev[0].record()
-        if self.pf:
-            check(self.L.ava_lif_scan_tuned(*args, 1, self.pf, stream))
-        else:
-            check(self.L.ava_lif_scan(*args, stream))
+        check(self.L.ava_lif_scan(*args, stream))
         if ev: ev[1].record()
 
     def roofline(self, kernel_s):
@@ -962,7 +958,40 @@ class Decode:
                 "after the timed region, per step"}
 
     def cpu_baseline(self):
-        return None
+        """The oracle's decode step (forward of one token with the reference's W8A32 products, then the
+        table's learning step) on a subset of the streams, from the GPU's state after the prefill and
+        the timed steps, reported per stream-step (the reference's talking engine runs one stream per
+        call, gpu/model/fstep/arch.rs:525-1073)."""
+        import torch
+        from oracle import oracle as O
+
+        S = 4
+        th = cpu_threads()
+        O.set_threads(th)
+        sub = self.st.select(list(range(S)))
+        om = O.OracleModel(self.cfg, self.params)
+        n = self.st.eng_len
+        so = om.new_state(S, eng_cap=n + 64)
+        for k in ("lif_v", "lif_s", "lif_a", "mem_f", "mem_s"):
+            so[k][...] = getattr(sub, k).cpu().numpy()
+        for k in ("eng_k", "eng_v"):
+            so[k][:, :n] = getattr(sub, k)[:, :n].float().cpu().numpy()
+        so["eng_len"] = n
+        so["cb_tab"][...] = sub.cb_tab.cpu().numpy()
+        so["cb_scale"][...] = sub.cb_scale.cpu().numpy()
+        so["cb_code"][...] = sub.cb_code.cpu().numpy()
+        del sub
+        toks = self.toks[:, :S, 0].cpu().numpy()
+        steps, t0 = 0, time.perf_counter()
+        while steps < 64 and (steps < 2 or time.perf_counter() - t0 < 15.0):
+            lo, so, _ = om.forward(toks[steps][:, None].astype(np.int32), state=so, planes=0, threads=th)
+            om.cb_learn(lo, toks[steps + 1], so)
+            steps += 1
+        dt = time.perf_counter() - t0
+        return {"value": S * steps / dt, "unit": "tokens/s (stream-steps per second)", "cores": th, "kind": "port",
+                "sample": f"oracle decode steps (forward with the reference's W8A32 products + the online table's "
+                          f"step) of {S} streams from the GPU's state ({n} stored tokens), {steps} steps, {th} "
+                          f"threads, {dt:.2f} s"}
 
 
 WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "greedy": Greedy, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy,
@@ -984,8 +1013,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--lif-pf", type=int, default=0,
-                    help="lif workload: time steps in flight per lane (ava_lif_scan_tuned; 0 = the library default)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1002,9 +1029,6 @@ def main():
     default = extra_workloads()
     wname = args.workload or default
     W = WORKLOADS[wname]()
-    if wname == "lif" and args.lif_pf:
-        W.pf = args.lif_pf
-        W.config["pf"] = args.lif_pf
     if args.steps is None:
         args.steps = getattr(W, "default_steps", 10)
     stream = torch.cuda.current_stream()
@@ -1051,6 +1075,12 @@ def main():
     if not args.no_cpu:
         log("bench: cpu baseline")
         cpu = W.cpu_baseline()
+        if cpu is not None:
+            # the host's core count beside the threads the baseline used (nproc = the CPUs this process
+            # may run on; the machine may have more)
+            cpu["threads"] = cpu["cores"]
+            cpu["nproc"] = len(os.sched_getaffinity(0))
+            cpu["host_cpus"] = os.cpu_count()
 
     out = {
         "metric": getattr(W, "metric", METRIC),

@@ -113,13 +113,6 @@ int ava_q8_matmul_i8(const int8_t *s, int m, const ava_qw *w, float *y, ava_stre
 int ava_lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
                  int levels, int is_signed, int alif, int8_t *spikes, float *th_out, ava_stream stream);
 
-/* ava_lif_scan with the kernel variant named: vec channels per lane (1, 2 or 4) and pf time steps
- * in flight per lane (8 .. 64); 0 = the default ava_lif_scan picks. Every variant gives the same bits
- * (the GPU tests check each one); AVA_ERR_ARG for a pair that has no kernel. Same reference op. */
-int ava_lif_scan_tuned(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
-                       int levels, int is_signed, int alif, int8_t *spikes, float *th_out, int vec, int pf,
-                       ava_stream stream);
-
 /* ------------------------------------------------------------------ kWTA */
 
 /* Per row of u [n][h]: kth = the k-th largest value (duplicates counted); keep u_i when
@@ -347,10 +340,11 @@ int ava_model_freeze(ava_model *m, int on);
  * query or value refuses the token before anything is committed). Every memory head checks the values
  * it stages (unit q, k and erase key, value, alpha, b k, alpha b e); a head that meets a non-finite one
  * leaves its fast weights F and S as they were and marks its stream. After a forward (this call waits
- * for the stream): count = the streams marked, rows [B of that forward] (nullable, host) = 1 for each.
- * The stream's LIF state and engram store are committed as usual (as the reference's plain path,
- * which then takes the token, commits them). */
-int ava_model_nonfinite(ava_model *m, int32_t *rows, int *count, ava_stream stream);
+ * for the stream): count = the streams marked, rows [B of that forward] (nullable, host, rows_cap
+ * entries; AVA_ERR_SHAPE when fewer than that forward's B) = 1 for each. A forward that was refused
+ * reports no streams. The stream's LIF state and engram store are committed as usual (as the
+ * reference's plain path, which then takes the token, commits them). */
+int ava_model_nonfinite(ava_model *m, int32_t *rows, int rows_cap, int *count, ava_stream stream);
 
 /* The decision trace, for parity checks (no counterpart in the reference, whose tests compare single
  * ops): with the buffers set (all NULL: off), every forward copies per block i the spikes [B*T][d]

@@ -433,6 +433,52 @@ void orc_mem_rec_f64(const float *q, const float *k, const float *e, const float
     }
 }
 
+/* The bounded rule (gpu/arch.rs:1091-1136 with the +-cap bound of mem_gen.rs:20-28) entirely in float64,
+ * inputs included: q, k, e, v, al (alpha itself, not its log) and b [BH][T][hs], F, S [BH][hs][hs]
+ * in/out (S NULL with m = 0), y [BH][T][hs]. The float64 reference forward's memory (forward64.py). */
+void orc_mem_rec_f64d(const double *q, const double *k, const double *e, const double *v, const double *al,
+                      const double *b, int BH, int T, int hs, double m, double cap, double *F, double *S,
+                      double *y) {
+#pragma omp parallel
+    {
+    double *r = (double *)malloc(sizeof(double) * (size_t)hs);
+#pragma omp for schedule(dynamic)
+    for (int bh = 0; bh < BH; bh++) {
+        double *f = F + (size_t)bh * hs * hs;
+        double *sm = S ? S + (size_t)bh * hs * hs : NULL;
+        for (int t = 0; t < T; t++) {
+            size_t o = ((size_t)bh * T + t) * hs;
+            for (int j = 0; j < hs; j++) {
+                double sacc = 0.0;
+                for (int i = 0; i < hs; i++) sacc += e[o + i] * f[i * hs + j];
+                r[j] = sacc;
+            }
+            for (int i = 0; i < hs; i++) {
+                const double a = al[o + i], bk = b[o + i] * k[o + i], abe = a * b[o + i] * e[o + i];
+                for (int j = 0; j < hs; j++) {
+                    const double u = bk * v[o + j] - abe * r[j];
+                    const int p = i * hs + j;
+                    double fp;
+                    if (sm) {
+                        sm[p] = m * sm[p] + u;
+                        fp = a * f[p] + sm[p];
+                    } else {
+                        fp = a * f[p] + u;
+                    }
+                    f[p] = fp < -cap ? -cap : (fp > cap ? cap : fp);
+                }
+            }
+            for (int j = 0; j < hs; j++) {
+                double sacc = 0.0;
+                for (int i = 0; i < hs; i++) sacc += q[o + i] * f[i * hs + j];
+                y[o + j] = sacc;
+            }
+        }
+    }
+    free(r);
+    }
+}
+
 /* The form of the stack's memory for T > 1: 0 (default) = the token loop delta_rec with the bound at
  * every token (the reference's GPU kernels and its CPU path under AVA_DELTA_REC=1, arch.rs:1329-1333),
  * 1 = delta_chunk (the reference's default CPU prefill, no bound). The two agree to rounding until a

@@ -100,6 +100,12 @@ void orc_mem_chunk(const float *q, const float *k, const float *e, const float *
  * default CPU prefill, state.rs:954 -> arch.rs:1994, which has no bound). */
 void orc_set_mem_chunked(int on);
 
+/* The bounded rule entirely in float64 (inputs, alpha itself rather than its log, state and read-outs):
+ * the memory of the float64 reference forward (forward64.py). S NULL without momentum. */
+void orc_mem_rec_f64d(const double *q, const double *k, const double *e, const double *v, const double *al,
+                      const double *b, int BH, int T, int hs, double m, double cap, double *F, double *S,
+                      double *y);
+
 /* ---------------------------------------------------------------- model */
 
 typedef struct {

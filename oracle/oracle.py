@@ -48,6 +48,7 @@ def lib():
         L.orc_set_mem_chunked.argtypes = [C.c_int]
         L.orc_set_mem_chunked.restype = None
         L.orc_mem_rec_f64.argtypes = [f32p] * 6 + [C.c_int] * 4 + [C.c_double, f64p, C.c_void_p, f64p]
+        L.orc_mem_rec_f64d.argtypes = [f64p] * 6 + [C.c_int] * 3 + [C.c_double, C.c_double, f64p, C.c_void_p, f64p]
         L.orc_rmsnorm.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p]
         L.orc_round_half.argtypes = [C.c_float]
         L.orc_round_half.restype = C.c_float
@@ -246,6 +247,19 @@ def evict_engram(state, eng_max, rule="oldest"):
 def set_mem_chunked(on: bool):
     """The block stack's memory form for T > 1: chunked (the reference's default) or the token loop."""
     lib().orc_set_mem_chunked(int(bool(on)))
+
+
+def mem_rec_f64d(q, k, e, v, al, b, m=0.0, cap=np.inf):
+    """The bounded rule in float64 from a zero state: float64 inputs [BH, T, hs] (al = alpha per channel).
+    Returns (y, F, S) float64 (S zeros without momentum)."""
+    q, k, e, v, al, b = (_c(z, np.float64) for z in (q, k, e, v, al, b))
+    BH, T, hs = q.shape
+    F = np.zeros((BH, hs, hs), np.float64)
+    S = np.zeros((BH, hs, hs), np.float64)
+    y = np.empty((BH, T, hs), np.float64)
+    lib().orc_mem_rec_f64d(q, k, e, v, al, b, BH, T, hs, float(m), float(cap), F,
+                           S.ctypes.data if m != 0.0 else None, y)
+    return y, F, S
 
 
 def mem_rec_f64(q, k, e, v, la, b, m=0.0, F=None, S=None):

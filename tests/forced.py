@@ -19,7 +19,7 @@ from oracle import oracle as O
 
 # The relative margin of a decision that two correct summation orders may take either way. At the end
 # of a deep stack over thousands of tokens the two sides' inputs to a decision differ by ~1e-4
-# relative (the conditioning of the recurrences; see one_ulp_envelope), so a flip is a near-tie when
+# relative (the conditioning of the recurrences; see check_state), so a flip is a near-tie when
 # its margin is within 10x that; a wrong selection or spike rule would flip decisions with margins
 # of order one.
 NEAR_TIE = 1e-3
@@ -89,51 +89,45 @@ def check_decisions(cfg, dec, otr, label=""):
     return n_s, n_k
 
 
-ENVELOPE = 4.0  # the fast-weight bar of a deep stack: this many times the oracle's own one-ulp response
+F64_FACTOR = 1.5  # the GPU may be at most this much farther from the float64 forward than the f32 oracle
 
 
-def check_state(so, st, envelope=None):
-    """BASELINE.json's state bars: membranes and fast weights within 1e-4 relative, spike state
-    mismatch <= 1e-4 of units (st: the GPU State, or a dict of numpy arrays). With `envelope` (the
-    oracle's own per-block relative response to a one-ulp nudge of its inputs, {name: [per block]}),
-    the fast weights of block i may differ by up to max(1e-4, ENVELOPE x envelope[i]): the bar of a
-    recurrence whose conditioning is worse than 1e-4 at that depth (see one_ulp_envelope)."""
+def check_state(so, st, s64=None):
+    """BASELINE.json's state bars: membranes and fast weights within 1e-4 relative of the oracle, spike
+    state mismatch <= 1e-4 of units (st: the GPU State, or a dict of numpy arrays).
+
+    With s64 (the state of the same forced forward in float64, oracle/forward64.py) the fast weights
+    are measured against float64 instead: in a deep stack over thousands of tokens their conditioning
+    (heads growing towards the +-1e5 bound) turns f32 rounding into more than 1e-4, and two f32
+    implementations that add in different orders (the oracle's is the reference's) then both sit about
+    that far from the exact result. Per block the two distances fluctuate against each other by up to
+    ~2x in either direction (the reference's own order would fail a per-block 1.5x bar measured
+    against the GPU's), so the bar compares the two orders over the whole stack: the GPU's distances
+    summed over blocks, and its largest block distance, are each at most F64_FACTOR x the oracle's
+    (and a block within 1e-4 of the oracle passes as is)."""
     get = (lambda k: host(getattr(st, k))) if not isinstance(st, dict) else (lambda k: st[k])
     names = ["lif_v", "mem_f"] + (["mem_s"] if so.get("mem_s") is not None and np.any(so["mem_s"]) else [])
     for k in names:
         g = get(k)
         per = [rel(g[i], so[k][i]) for i in range(g.shape[0])]
-        env = envelope.get(k) if envelope and k != "lif_v" else None
-        print(f"state {k}: rel {rel(g, so[k]):.2e}; per block " + " ".join(f"{e:.1e}" for e in per) +
-              ("; one-ulp envelope " + " ".join(f"{e:.1e}" for e in env) if env is not None else ""), flush=True)
-        for i, e in enumerate(per):
-            bar = max(1e-4, ENVELOPE * env[i]) if env is not None else 1e-4
-            assert e < bar, (k, i, e, bar)
+        print(f"state {k}: rel {rel(g, so[k]):.2e}; per block " + " ".join(f"{e:.1e}" for e in per), flush=True)
+        if s64 is None or k == "lif_v":
+            for i, e in enumerate(per):
+                assert e < 1e-4, (k, i, e)
+        if s64 is None:
+            continue
+        dg = np.array([rel(g[i], s64[k][i]) for i in range(g.shape[0])])
+        do = np.array([rel(so[k][i], s64[k][i]) for i in range(g.shape[0])])
+        print(f"state {k} vs float64: GPU " + " ".join(f"{e:.1e}" for e in dg) + "; oracle f32 " +
+              " ".join(f"{e:.1e}" for e in do) + f"; sums {dg.sum():.2e} / {do.sum():.2e}, largest "
+              f"{dg.max():.2e} / {do.max():.2e}", flush=True)
+        if k == "lif_v" or max(per) < 1e-4:
+            continue
+        assert dg.sum() <= F64_FACTOR * do.sum(), (k, dg.sum(), do.sum())
+        assert dg.max() <= F64_FACTOR * do.max(), (k, dg.max(), do.max())
     flips = float(np.mean(get("lif_s") != so["lif_s"]))
     print(f"state lif_s: mismatch {flips:.2e}", flush=True)
     assert flips <= 1e-4
-
-
-def one_ulp_envelope(cfg, prm, ids, dec, so, threads=16):
-    """The oracle's own sensitivity: the same forward with every embedding value moved by one ulp up,
-    and again moved one ulp down, with the same forced decisions, against the unmoved run's state so.
-    Per block, the larger relative change of the fast weights (mem_f, mem_s) over the two nudges (one
-    nudge is a single sample of a chaotic response). Two correct f32 implementations that sum in
-    different orders differ by about this much; a fast-weight recurrence (with momentum, and heads that
-    grow towards the state bound) can amplify a one-ulp difference far beyond 1e-4 over thousands of
-    tokens."""
-    out = {}
-    B = ids.shape[0]
-    for direction in (np.inf, -np.inf):
-        p2 = dict(prm)
-        p2["tok_emb"] = np.nextafter(np.asarray(prm["tok_emb"], np.float32), np.float32(direction)).astype(np.float32)
-        om2 = O.OracleModel(cfg, p2)
-        _, s2, _ = forced_oracle(om2, ids, dec, om2.new_state(B, eng_cap=ids.shape[1]), threads=threads)
-        for k in ("mem_f", "mem_s"):
-            if so.get(k) is not None and np.any(so[k]):
-                r = [rel(s2[k][i], so[k][i]) for i in range(so[k].shape[0])]
-                out[k] = [max(a, b) for a, b in zip(out[k], r)] if k in out else r
-    return out
 
 
 def forced_oracle(om, ids, dec, state, threads=16):
@@ -142,11 +136,11 @@ def forced_oracle(om, ids, dec, state, threads=16):
                       force={"spikes": dec["spikes"], "keep": dec["keep"]})
 
 
-def run_forced(name, B, T, seed, pieces=None, threads=16, envelope=False, **over):
+def run_forced(name, B, T, seed, pieces=None, threads=16, f64=False, **over):
     """The GPU's forward of seeded ids [B, T] (in pieces when given) with its decision trace, and the
-    oracle's forward with those decisions forced: every row meets the full bars (with envelope, the
-    fast weights the conditioning bar of check_state). Returns (cfg, GPU logits, oracle logits, GPU
-    state, oracle state)."""
+    oracle's forward with those decisions forced: every row meets the full bars (with f64, the fast
+    weights are also measured against the float64 forward, check_state). Returns (cfg, GPU logits,
+    oracle logits, GPU state, oracle state)."""
     from ava_amd import synth
     from ava_amd.model import Model
     cfg = synth.config(name)
@@ -170,7 +164,13 @@ def run_forced(name, B, T, seed, pieces=None, threads=16, envelope=False, **over
     err = float(np.max(np.abs(lg - lo)))
     print(f"{name}: logits max abs err {err:.2e}, rel {err / np.max(np.abs(lo)):.2e}", flush=True)
     assert err < 1e-2
-    env = one_ulp_envelope(cfg, prm, ids, dec, so, threads) if envelope else None
-    check_state(so, st, env)
+    s64 = None
+    if f64:
+        from oracle.forward64 import forward64
+        print(f"forced parity {name}: float64 forward", flush=True)
+        lo64, s64 = forward64(cfg, prm, ids, dec)
+        print(f"{name}: logits vs the float64 forward: GPU {np.max(np.abs(lg - lo64)):.2e}, oracle f32 "
+              f"{np.max(np.abs(lo - lo64)):.2e}", flush=True)
+    check_state(so, st, s64)
     check_decisions(cfg, dec, otr, name)
     return cfg, lg, lo, st, so

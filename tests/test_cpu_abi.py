@@ -41,6 +41,9 @@ def test_argument_errors_return_status_and_message():
                         None, None, None)
     assert rc == 4 and b"head size" in L.ava_last_error()
     assert L.ava_q8_ldk(1) == 128 and L.ava_q8_ldk(1024) == 1024 and L.ava_q8_ldk(1025) == 1152
+    n = C.c_int(7)
+    rows = (C.c_int32 * 4)()
+    assert L.ava_model_nonfinite(None, rows, 4, C.byref(n), None) == 1 and b"NULL" in L.ava_last_error()
 
 
 def test_ops_refuse_host_tensors():

@@ -56,6 +56,9 @@ def test_generate_refuses_empty_prompt_and_honours_eos():
         m.generate([[1, 2], []], 4)
     first = m.generate([[3, 4, 5]], 1, eos=None)[0][0]
     assert m.generate([[3, 4, 5]], 6, eos=first) == [[]]  # eos is not included, and ends the row
+    # no new tokens: empty continuations on both the device-side and the host loop
+    assert m.generate([[3, 4, 5], [6, 7]], 0, eos=None) == [[], []]
+    assert m.generate([[3, 4, 5]], 0) == [[]]
 
 
 def test_device_side_greedy_equals_host_loop():

@@ -51,3 +51,32 @@ def test_nonfinite_memory_input_commits_no_fast_weights(T):
         assert np.array_equal(F[:, b], host(st2.mem_f)[:, b])
     # and their fast weights moved
     assert not np.array_equal(F[:, 0], F0[:, 0])
+
+
+def test_refused_forward_reports_no_rows_of_an_earlier_one():
+    """A forward refused by its checks (here: the engram store is full) after one that marked a stream
+    reports no streams, and a rows buffer smaller than the last forward's streams is refused."""
+    import ctypes as C
+    from ava_amd import synth
+    from ava_amd._lib import lib
+    from ava_amd.model import Model
+    cfg = synth.config("tiny")
+    prm = synth.params(cfg, seed=22)
+    bad_id = cfg["vocab"] - 1
+    prm["tok_emb"] = np.array(prm["tok_emb"], np.float32, copy=True)
+    prm["tok_emb"][bad_id] = np.nan
+    print("guard refused forward", flush=True)
+    m = Model(cfg, prm)
+    st = m.state(4, eng_cap=8)
+    ids = np.zeros((4, 4), np.int32)
+    ids[3, 1] = bad_id
+    m.forward_with_state(torch.from_numpy(ids).cuda(), st)
+    assert m.nonfinite() == [3]
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows, n = (C.c_int32 * 2)(), C.c_int(0)
+    assert lib().ava_model_nonfinite(m.h, rows, 2, C.byref(n), stream) != 0  # 2 < the 4 streams
+    small = m.state(2, eng_cap=4)
+    with pytest.raises(RuntimeError):  # 8 > the 4 entries the store holds: refused before it runs
+        m.forward_with_state(torch.zeros((2, 8), dtype=torch.int32, device="cuda"), small)
+    assert m.nonfinite() == []
+    assert lib().ava_model_nonfinite(m.h, rows, 2, C.byref(n), stream) == 0 and n.value == 0

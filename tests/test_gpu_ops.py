@@ -71,12 +71,12 @@ def test_lif_matches_oracle_every_option(levels, signed, alif, theta_on, init_on
     assert 0.02 < rate < 0.98
 
 
-@pytest.mark.parametrize("vec,pf", [(1, 8), (1, 32), (1, 64), (2, 16), (4, 8), (4, 16)])
-def test_lif_config1_shape_bit_exact(vec, pf, dev):
+@pytest.mark.parametrize("B,T,D", [(4, 300, 256), (3, 31, 200), (1, 65, 64)])
+def test_lif_config1_shape_bit_exact(B, T, D, dev):
     """config[1] semantics (int2, ALIF rho 0.95 gain 0.05, theta 1, beta = sigmoid(U(1.5, 4.5))) on a
-    reduced batch, every kernel variant: spikes, v_T, a_T and theta_T bit for bit."""
+    reduced batch, with T shorter than, equal to and past the steps in flight and a partial workgroup:
+    spikes, v_T, a_T and theta_T bit for bit."""
     rng = np.random.default_rng(11)
-    B, T, D = 4, 300, 256
     cur = rng.standard_normal((B, T, D), dtype=np.float32)
     beta = sig(rng.uniform(1.5, 4.5, D).astype(np.float32))
     ps = np.concatenate([beta, np.ones(D, np.float32), np.full(D, 0.95, np.float32),
@@ -84,7 +84,7 @@ def test_lif_config1_shape_bit_exact(vec, pf, dev):
     spk_o, v_o, s_o, a_o = O.lif_scan(cur, ps, levels=2, signed=True, alif=True)
     from ava_amd import ops
     spk, st, th = ops.lif_gen(cuda(cur), cuda(beta), cuda(ps[D:2 * D]), (cuda(ps[2 * D:3 * D]), cuda(ps[3 * D:])),
-                              levels=2, signed=True, vec=vec, pf=pf, th_out=True)
+                              levels=2, signed=True, th_out=True)
     assert np.array_equal(host(spk), spk_o)
     assert np.array_equal(host(st.v).view(np.uint32), v_o.view(np.uint32))
     assert np.array_equal(host(st.a).view(np.uint32), a_o.view(np.uint32))

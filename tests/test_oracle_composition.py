@@ -369,3 +369,49 @@ def test_large_gate_projection_makes_silu_the_identity():
     gated = head_norm(tr2["memy"][i], hs) * (g * sigmoid(g))
     plain = head_norm(tr2["memy"][i], hs) * g
     assert np.max(np.abs(gated - plain)[big] / np.abs(plain[big])) < 1e-7
+
+
+def test_every_path_on_reads_the_stream_after_the_previous_path():
+    """Every output path on (no dense mix), one float64 statement of each whole block from its traced
+    input: the memory reads rms(x_in + s . Wout), not the block input (gpu/arch.rs:1695-1705); the engram
+    reads the stream after the memory's read-out was added; the MLP reads the stream after the engram's
+    add; the block's output is the sum of all four. The other tests turn one path on at a time, so
+    they do not fix which stream each later part reads."""
+    cfg, prm, ids, lo, so, tr = setup(keep=("wout", "wo", "ewo", "w2"), dense_zero=True)
+    L, B, T, d, hs = cfg["layers"], ids.shape[0], ids.shape[1], cfg["d"], cfg["head_size"]
+    nh = d // hs
+    xin = block_inputs(prm, ids, tr, L)
+    v_first = [None]
+    heads = max(1, int(cfg.get("eng_heads", 1) or 1))
+    for i in range(L):
+        b = prm["blocks"][i]
+        x1 = xin[i] + mm(tr["spikes"][i].astype(f64), b["wout"])
+        h = rms(x1, b["mem_norm"])
+        # the spiking layer's add moves the memory's input visibly, so reading x_in would fail below
+        assert relerr(rms(xin[i], b["mem_norm"]), h) > 1e-2
+        q, k, e, v, la, bw = memory_inputs(cfg, prm, i, h, v_first)
+        y = np.zeros((B * T, d))
+        for bi in range(B):
+            rows = slice(bi * T, (bi + 1) * T)
+            for hh in range(nh):
+                c = slice(hh * hs, (hh + 1) * hs)
+                y[rows, c] = delta_rec(q[rows, c], k[rows, c], e[rows, c], v[rows, c], la[rows, c], bw[rows, c],
+                                       cfg["momentum"], cfg["cap"])[0]
+        assert relerr(tr["memy"][i], y) < 1e-4, i
+        g = mm(h, b["wg"])
+        x2 = x1 + mm(head_norm(tr["memy"][i], hs) * (g * sigmoid(g)), b["wo"])
+        x3 = x2
+        if i == cfg["eng_block"]:
+            he = rms(x2, b["eng_norm"])
+            assert relerr(rms(x1, b["eng_norm"]), he) > 1e-2
+            eq, ek, ev = mm(he, b["ewq"]), mm(he, b["ewk"]), mm(he, b["ewv"])
+            hd = cfg["eng_dim"] // heads
+            o = np.concatenate([attend(eq[r * T:(r + 1) * T], ek[r * T:(r + 1) * T], ev[r * T:(r + 1) * T], hd)
+                                for r in range(B)])
+            x3 = x2 + mm(o, b["ewo"])
+        hm = rms(x3, b["mlp_norm"])
+        assert relerr(rms(x1 if i != cfg["eng_block"] else x2, b["mlp_norm"]), hm) > 1e-3
+        u = mm(hm, b["w1"])
+        assert relerr(tr["u"][i], u) < 1e-4, i
+        x4 = x3 + mm(kwta_relu2(tr["u"][i].astype(f64), cfg["kwta_k"]), b["w2"])
+        assert relerr(tr["x"][i], x4) < 1e-4, i
