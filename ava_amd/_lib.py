@@ -36,6 +36,17 @@ BLOCK_FIELDS = ["lif_norm", "win", "beta_p", "theta", "arho", "again", "wout",
                 "mlp_norm", "w1", "w2", "dense"]
 
 
+def config_struct(c: dict, planes: int = 3, cb_lr: float = 0.0) -> Config:
+    """ava_config from a configuration dict (ava_amd.synth's keys)."""
+    return Config(vocab=c["vocab"], d=c["d"], layers=c["layers"], hidden=c["hidden"], kwta_k=c["kwta_k"],
+                  head_size=c["head_size"], gate_rank=c["gate_rank"], eng_block=c["eng_block"],
+                  eng_dim=c["eng_dim"], levels=c["levels"], alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
+                  value_residual=int(c["value_residual"]), dense=int(c["dense"]), relu2=int(c["relu2"]),
+                  momentum=c["momentum"], cap=c["cap"], planes=planes, cb_units=c.get("cb_units", 0),
+                  cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0),
+                  eng_half=int(bool(c.get("eng_half", False))), eng_heads=int(c.get("eng_heads", 1) or 1))
+
+
 class BlockParams(C.Structure):
     _fields_ = [(n, vp) for n in BLOCK_FIELDS]
 
@@ -89,6 +100,10 @@ def lib():
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
         "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],
         "ava_model_decode_step": [vp, C.POINTER(State), vp, i32, i32, vp, vp, i32, vp, vp, vp],
+        "ava_train_new": [C.POINTER(Config), f32, i32, C.POINTER(vp)],
+        "ava_train_param_slot": [vp, C.c_char_p, i32, C.POINTER(sz), C.POINTER(sz)],
+        "ava_train_step": [vp, vp, vp, vp, i32, i32, vp, vp, vp],
+        "ava_train_decisions": [vp, vp, vp, vp, vp],
     }
     for name, args in sig.items():
         fn = getattr(L, name, None)
@@ -104,6 +119,10 @@ def lib():
     L.ava_mem_scan_bwd_workspace.restype = sz
     L.ava_dense_back_part_floats.argtypes = [C.c_longlong, i32]
     L.ava_dense_back_part_floats.restype = sz
+    L.ava_train_free.argtypes = [vp]
+    L.ava_train_free.restype = None
+    L.ava_train_param_floats.argtypes = [vp]
+    L.ava_train_param_floats.restype = sz
     L.ava_q8_workspace.argtypes = [i32, i32, i32]
     L.ava_q8_workspace.restype = sz
     if hasattr(L, "ava_model_free"):

@@ -19,7 +19,7 @@ import ctypes as C
 import numpy as np
 import torch
 
-from ._lib import BLOCK_FIELDS, BlockParams, Config, Params, State as _CState, check, lib
+from ._lib import BLOCK_FIELDS, BlockParams, Params, State as _CState, check, config_struct, lib
 
 # The end-of-text id of the reference's byte-pair vocabulary (ava_data::bpe::EOS, data/src/bpe.rs:57),
 # at which its generate ends a row (gpu/state.rs:1402, 1436).
@@ -144,13 +144,7 @@ class Model:
             from .synth import cb_rate
             cb_lr = c["cb_lr"] if c.get("cb_lr") is not None else cb_rate(params["tok_emb"], c["cb_eta"])
         self.cb_lr = cb_lr
-        ccfg = Config(vocab=c["vocab"], d=c["d"], layers=L, hidden=c["hidden"], kwta_k=c["kwta_k"],
-                      head_size=c["head_size"], gate_rank=c["gate_rank"], eng_block=c["eng_block"],
-                      eng_dim=c["eng_dim"], levels=c["levels"], alif=int(c["alif"]), lif_scale=int(c["lif_scale"]),
-                      value_residual=int(c["value_residual"]), dense=int(c["dense"]), relu2=int(c["relu2"]),
-                      momentum=c["momentum"], cap=c["cap"], planes=planes, cb_units=c.get("cb_units", 0),
-                      cb_lr=float(cb_lr), cb_half=float(c.get("cb_half", 0.0) or 0.0),
-                      eng_half=int(bool(c.get("eng_half", False))), eng_heads=int(c.get("eng_heads", 1) or 1))
+        ccfg = config_struct(c, planes=planes, cb_lr=cb_lr)
         from .state_io import fingerprint
         self.fingerprint = fingerprint(self.cfg, params)  # keys saved states (Model::fingerprint)
         torch.cuda.init()

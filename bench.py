@@ -477,6 +477,57 @@ class MemBwd:
                                           f"heads, T={T}, one thread, {dt:.2f} s"}
 
 
+class Train:
+    """The float32 training step (ava_train_step) on config[3]'s model: the loss and every parameter's
+    gradient of a teacher-forced batch of B x T random tokens from a zero state (the reference's
+    hand-written step, gpu/model/fwin.rs). Random-init f32 weights N(0, 0.02) as synth.params."""
+
+    name = "train"
+    kernel = "whole training step"
+    metric = "tokens/sec f32 training step (loss and gradients) of config[3]'s model, 1 GPU; % fp32 MFMA roofline"
+    default_steps = 3
+
+    def __init__(self, B=4, T=2048):
+        import torch
+        from ava_amd import synth
+        from ava_amd.train import Trainer
+
+        self.cfg = c = synth.config("ava04_d1024")
+        self.B, self.T = B, T
+        log("bench: building weights")
+        prm = synth.params(c, seed=0)
+        self.tr = Trainer(c, slope=4.0)
+        self.flat = self.tr.pack(prm)
+        self.grads = torch.empty_like(self.flat)
+        g = torch.Generator(device="cuda").manual_seed(6)
+        self.ids = torch.randint(0, c["vocab"], (B, T), device="cuda", generator=g, dtype=torch.int32)
+        self.tgt = torch.randint(0, c["vocab"], (B, T), device="cuda", generator=g, dtype=torch.int32)
+        self.tokens = B * T
+        d, H, V, L, r = c["d"], c["hidden"], c["vocab"], c["layers"], c["gate_rank"]
+        nh = d // c["head_size"]
+        # the step's product FLOPs: forward 2 N P, backward 4 N P over the matrices' P multiply-adds per
+        # token (8 d^2 + 2 d H + 2 d nh + 4 d r per block, the engram's 4 d de, the head d V)
+        P = L * (8 * d * d + 2 * d * H + 2 * d * nh + 4 * d * r) + 4 * d * c["eng_dim"] + d * V
+        self.flops = 6.0 * self.tokens * P
+        self.config = {"workload": "f32 training step config[3] model", "B": B, "T": T, "d": d, "blocks": L,
+                       "hidden": H, "vocab": V, "engram_block": c["eng_block"]}
+        self.dtype = "f32"
+
+    def step(self, stream, ev=None):
+        if ev: ev[0].record()
+        self.tr.step(self.flat, self.ids, self.tgt, self.grads)
+        if ev: ev[1].record()
+
+    def roofline(self, kernel_s):
+        a = self.flops / kernel_s / 1e12
+        return {"bound": "mfma", "achieved": a, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": a / FP32_PEAK_TFLOPS, "scope": "the step's product FLOPs over the whole step's time",
+                "product_flops_per_step": self.flops}
+
+    def cpu_baseline(self):
+        return None
+
+
 class MemChunk:
     """The chunked fast-weight memory (ava_mem_chunk, delta_chunk / chunk_core) at config[3]'s per-block
     shape: 64 streams x 16 heads x 2048 tokens, unit q, k, e, v ~N(0,1), per-channel log alpha =
@@ -995,7 +1046,7 @@ class Decode:
 
 
 WORKLOADS = {"stack": Stack, "stack_heads": StackHeads, "greedy": Greedy, "decode": Decode, "lif": Lif, "delta": Delta, "kwta": Kwta, "gemm": Gemm, "copy": Copy,
-             "lif_bwd": LifBwd, "mem_bwd": MemBwd, "mem_chunk": MemChunk}
+             "lif_bwd": LifBwd, "mem_bwd": MemBwd, "mem_chunk": MemChunk, "train": Train}
 DEFAULT = "stack"
 
 

@@ -364,6 +364,41 @@ int ava_model_set_trace(ava_model *m, int8_t *spikes, float *u, float *kth, size
 int ava_model_set_timing(ava_model *m, int on);
 int ava_model_timing(ava_model *m, const char **names, int *calls, double *ms, int cap, int reset);
 
+/* ------------------------------------------------------------------ the training step */
+
+/* The float32 training step of the block stack (the reference's hand-written step, gpu/model/fwin.rs:1-40:
+ * every forward op a kernel and every backward the matching one, no autograd): one teacher-forced batch
+ * from a zero state, its mean cross-entropy and the gradient of every parameter. The forward is the
+ * block of ava_model_forward in f32 (f32 weights, no int8): rms -> Win (1 - beta) -> LIF scan -> Wout;
+ * rms -> q, k, v, e, g and the gates -> the memory scan -> read-out -> Wo; the engram read (one block,
+ * heads of 32 or 64); rms -> W1 -> kWTA relu^2 -> W2; the dense mix; the final norm and the tied head
+ * E^T. slope: the LIF surrogate's slope (the reference's --surrogate-slope, 4 by default); reset_grad:
+ * carry the gradient through the reset (--lif-reset-grad). theta is detached and the gate offsets are
+ * constants (their gradients are 0). Needs head size 64, relu2, no cerebellum head, an f32 store. */
+typedef struct ava_trainer ava_trainer;
+int ava_train_new(const ava_config *cfg, float slope, int reset_grad, ava_trainer **out);
+void ava_train_free(ava_trainer *t);
+
+/* The parameters (and gradients) are one flat f32 device buffer of ava_train_param_floats floats. A tensor's
+ * place: name "tok_emb" or "final_norm" with block -1, or a block tensor named as in ava_block_params
+ * ("win", "beta_p", ..., "dense") with its block; shapes as there ([din][dout] for matrices). The dense
+ * weights of all blocks are contiguous, block k's k + 2 weights from k (k + 3) / 2 after the first.
+ * AVA_ERR_ARG for an unknown name; count 0 for the engram tensors of other blocks. */
+size_t ava_train_param_floats(const ava_trainer *t);
+int ava_train_param_slot(const ava_trainer *t, const char *name, int block, size_t *offset, size_t *count);
+
+/* One step: ids, targets [B][T] (device int32; a target outside [0, vocab) does not count); params as
+ * above; grads (same layout) are overwritten; loss [1] (device f32) = the mean over counted positions of
+ * -log softmax(logits)[target]. Scratch for B*T rows is allocated on first use and kept. Replaces the
+ * reference's loss_and_grads for the Ava-0.4 recipe (gpu/model/fwin.rs). */
+int ava_train_step(ava_trainer *t, const float *params, const int32_t *ids, const int32_t *targets, int B, int T,
+                   float *grads, float *loss, ava_stream stream);
+
+/* The last step's discrete decisions (no counterpart in the reference; for parity checks): spikes
+ * [layers][B*T][d] int8, the wide layer's u [layers][B*T][hidden] and its k-th values kth [layers][B*T]
+ * (device, nullable each). */
+int ava_train_decisions(const ava_trainer *t, int8_t *spikes, float *u, float *kth, ava_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

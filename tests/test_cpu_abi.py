@@ -44,6 +44,17 @@ def test_argument_errors_return_status_and_message():
     n = C.c_int(7)
     rows = (C.c_int32 * 4)()
     assert L.ava_model_nonfinite(None, rows, 4, C.byref(n), None) == 1 and b"NULL" in L.ava_last_error()
+    # the training step refuses what it does not build before touching the GPU
+    from ava_amd import synth
+    from ava_amd._lib import config_struct
+    h = C.c_void_p()
+    assert L.ava_train_new(None, C.c_float(4.0), 0, C.byref(h)) == 1
+    bad = synth.config("tiny")
+    bad["head_size"] = 32
+    assert L.ava_train_new(C.byref(config_struct(bad)), C.c_float(4.0), 0, C.byref(h)) == 2
+    assert b"head size 64" in L.ava_last_error() and not h.value
+    cb = synth.config("tiny_cb")
+    assert L.ava_train_new(C.byref(config_struct(cb)), C.c_float(4.0), 0, C.byref(h)) == 1
 
 
 def test_ops_refuse_host_tensors():
