@@ -184,16 +184,19 @@ def mem_chunk(q, k, e, v, la, b, m=0.0, cap=1e5, F=None, S=None):
     return y, F, S
 
 
-def delta_rule_from(q, k, v, beta, la=None, f0=None):
+def delta_rule_from(q, k, v, beta, la=None, f0=None, workspace=True):
     """model.rs:744-799 (per-head gates): q, k, v [BH, T, 64], beta and la (log alpha, None: alpha = 1)
-    [BH, T]. Returns (y, F)."""
+    [BH, T]. Without gates and with workspace, the chunks' inverses are formed first for all chunks (the
+    two-phase form, a workspace of BH x T x 64 floats); else one kernel walks the chunks. Returns (y, F)."""
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")) + (((la, "la"),) if la is not None else ()):
         _need(t, torch.float32, f"delta_rule {nm}")
     BH, T, hs = q.shape
     F = torch.zeros((BH, hs, hs), dtype=torch.float32, device=q.device) if f0 is None else f0.clone()
     y = torch.empty_like(q)
-    check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(la), _p(beta), BH, T, hs, _p(F), _p(y), _stream()),
-          "ava_delta_chunk")
+    nb = lib().ava_delta_chunk_workspace(BH, T) if (la is None and workspace) else 0
+    work = torch.empty(nb, dtype=torch.uint8, device=q.device) if nb else None
+    check(lib().ava_delta_chunk(_p(q), _p(k), _p(v), _p(la), _p(beta), BH, T, hs, _p(F), _p(y), _p(work), nb,
+                                _stream()), "ava_delta_chunk")
     return y, F
 
 

@@ -279,10 +279,16 @@ class Delta:
         self.beta = torch.sigmoid(torch.randn((BH, T), device="cuda", generator=g))
         self.F = torch.zeros((BH, 64, 64), dtype=torch.float32, device="cuda")
         self.y = torch.empty_like(self.q)
+        # the two-phase form's workspace (the chunks' inverses); AVA_DELTA_ONE_KERNEL=1 times the
+        # single-kernel walk instead
+        one = os.environ.get("AVA_DELTA_ONE_KERNEL", "0") != "0"
+        self.work_bytes = 0 if one else self.L.ava_delta_chunk_workspace(BH, T)
+        self.work = torch.empty(self.work_bytes, dtype=torch.uint8, device="cuda") if self.work_bytes else None
         self.tokens = B * T
         # read q, k, v, beta; write y and the final state
         self.bytes = 3 * BH * T * 64 * 4 + BH * T * 4 + BH * T * 64 * 4 + BH * 64 * 64 * 4
-        self.config = {"workload": "delta rule chunked config[2]", "B": B, "H": H, "T": T, "d": 64, "chunk": 64}
+        self.config = {"workload": "delta rule chunked config[2]", "B": B, "H": H, "T": T, "d": 64, "chunk": 64,
+                       "form": "one kernel" if one else "two-phase"}
         self.dtype = "f32"
 
     def step(self, stream, ev=None):
@@ -293,7 +299,8 @@ class Delta:
         self.F.zero_()
         if ev: ev[0].record()
         check(self.L.ava_delta_chunk(p(self.q), p(self.k), p(self.v), None, p(self.beta), self.BH, self.T, 64,
-                                     p(self.F), p(self.y), stream))
+                                     p(self.F), p(self.y), p(self.work) if self.work is not None else None,
+                                     self.work_bytes, stream))
         if ev: ev[1].record()
 
     def roofline(self, kernel_s):

@@ -150,7 +150,12 @@ int ava_mem_chunk(const float *q, const float *k, const float *e, const float *v
  * beta [BH][T]; F [BH][64][64] carried in and out; y [BH][T][64]. T a multiple of 64.
  * Replaces model::delta_rule_from (model.rs:744-799) for per-head gates. */
 int ava_delta_chunk(const float *q, const float *k, const float *v, const float *la, const float *beta, int BH,
-                    int T, int hs, float *F, float *y, ava_stream stream);
+                    int T, int hs, float *F, float *y, void *work, size_t work_bytes, ava_stream stream);
+/* work (nullable): device scratch of ava_delta_chunk_workspace(BH, T) bytes. Without gates (la NULL) and
+ * with it, the chunks' triangular inverses are formed for every chunk at once first, and the walk over
+ * the chunks is six products per chunk; otherwise one kernel walks the chunks with the solve inside. The
+ * results agree to rounding. */
+size_t ava_delta_chunk_workspace(int BH, int T);
 
 /* ------------------------------------------------------------------ backward (training step) */
 

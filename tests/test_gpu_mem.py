@@ -109,20 +109,22 @@ def delta_inputs(BH, T, seed, gated, shift=None):
     return q, k, v, beta, la
 
 
-@pytest.mark.parametrize("gated,T,shift", [(False, 64, None), (False, 256, None), (True, 192, None),
-                                           (True, 128, -6.0), (True, 128, 2.0)])
-def test_delta_chunk_matches_recurrence(gated, T, shift):
+@pytest.mark.parametrize("gated,T,shift,ws", [(False, 64, None, True), (False, 256, None, True),
+                                              (False, 256, None, False), (True, 192, None, True),
+                                              (True, 128, -6.0, True), (True, 128, 2.0, True)])
+def test_delta_chunk_matches_recurrence(gated, T, shift, ws):
     """model.rs:744-799 vs the token loop (arch/tests.rs:704-750: chunked = recurrence within 1e-4, including
     forgetting strong enough that products of rates underflow), with a carried initial state; config[2]'s rule
     (alpha = 1, e = k, one beta per token and head, no momentum) and its per-head gated form."""
     BH = 6
-    print(f"delta_chunk gated={gated} T={T} shift={shift}", flush=True)
+    print(f"delta_chunk gated={gated} T={T} shift={shift} workspace={ws}", flush=True)
     q, k, v, beta, la = delta_inputs(BH, T, 3 + T, gated, shift)
     if shift is not None:
         assert np.exp(la.astype(np.float64)[:, :64].sum(axis=1)).min() < 1e-38 or shift > 0
     F0 = (np.random.default_rng(2).standard_normal((BH, 64, 64)) * 0.1).astype(np.float32)
     from ava_amd import ops
-    y, F = ops.delta_rule_from(cuda(q), cuda(k), cuda(v), cuda(beta), cuda(la) if gated else None, f0=cuda(F0))
+    y, F = ops.delta_rule_from(cuda(q), cuda(k), cuda(v), cuda(beta), cuda(la) if gated else None, f0=cuda(F0),
+                               workspace=ws)
     y, F = host(y), host(F)
     g3 = lambda a: a[:, :, None]
     y64, F64, _ = O.mem_rec_f64(q, k, k, v, g3(la), g3(beta), F=F0)
