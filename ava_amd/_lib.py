@@ -100,6 +100,7 @@ def lib():
         "ava_model_forward": [vp, C.POINTER(State), vp, i32, i32, vp, vp],
         "ava_model_cb_learn": [vp, C.POINTER(State), vp, i32, vp, i32, vp, vp],
         "ava_model_decode_step": [vp, C.POINTER(State), vp, i32, i32, vp, vp, i32, vp, vp, vp],
+        "ava_engram_evict": [vp, vp, vp, vp, i32, i32, i32, vp, i32, i32, i32, i32, vp],
         "ava_train_new": [C.POINTER(Config), f32, i32, C.POINTER(vp)],
         "ava_train_param_slot": [vp, C.c_char_p, i32, C.POINTER(sz), C.POINTER(sz)],
         "ava_train_step": [vp, vp, vp, vp, i32, i32, vp, vp, vp],

@@ -79,40 +79,25 @@ class State:
         return out
 
     def evict(self):
-        """Keep eng_max of the store's entries, in store order (evict, state.rs:518-590), on the store's
-        device. Called by the model after each forward of a capped state. "oldest": the last eng_max.
-        "least-read": per stream, the slots rank by (class, value, index) -- class 1 for a slot some
-        later query could see (age >= 1; value reads / age, its mean mass per later query), class 2 for
-        the slots no later query has seen yet -- and the last eng_max of the ranking stay (the ranking
-        runs on the host, as the reference's sort does; the kept entries are gathered on the device)."""
+        """Keep eng_max of the store's entries, in store order (evict, state.rs:518-590), on the device
+        (ava_engram_evict: no host round trip). Called by the model after each forward of a capped state.
+        "oldest": the last eng_max. "least-read": per stream, the slots rank by (class, value, index) --
+        class 1 for a slot some later query could see (age >= 1; value reads / age, its mean mass per later
+        query), class 2 for the slots no later query has seen yet -- and the last eng_max of the ranking
+        stay."""
         n, mx = self.eng_len, self.eng_max
-        if not mx or n <= mx:
+        # with the length on the device the kernel decides there (a captured step evicts on replay)
+        if not mx or (n <= mx and self.eng_len_dev is None):
             return
-        if self.eng_rule == "least-read":
-            reads = self.eng_reads[:, :n].cpu().numpy()
-            age = self.eng_age[:, :n].cpu().numpy()
-            keep = np.empty((self.B, mx), np.int64)
-            for r in range(self.B):
-                seen = age[r] >= 1.0
-                value = np.where(seen, reads[r] / np.where(seen, age[r], np.float32(1.0)), np.float32(0.0))
-                order = np.lexsort((np.arange(n), value.astype(np.float32), np.where(seen, 1, 2)))
-                keep[r] = np.sort(order[n - mx:])
-            idx = torch.from_numpy(keep).to(self.eng_k.device)
-            for t in (self.eng_k, self.eng_v):
-                g = torch.gather(t[:, :n], 1, idx[:, :, None].expand(-1, -1, t.shape[2]))
-                t[:, :mx].copy_(g)
-            for t in (self.eng_reads, self.eng_age):
-                t[:, :mx].copy_(torch.gather(t[:, :n], 1, idx))
-        else:
-            drop = n - mx
-            for t in (self.eng_k, self.eng_v):
-                t[:, :mx].copy_(t[:, drop:n].clone())  # the ranges overlap when drop < mx
-            for t in (self.eng_reads, self.eng_age):
-                if t is not None:
-                    t[:, :mx].copy_(t[:, drop:n].clone())
-        self.eng_len = mx
-        if self.eng_len_dev is not None:
-            self.eng_len_dev.fill_(mx)
+        if not self.eng_k.is_cuda:
+            raise ValueError("evict: the store must be on the GPU (ava_engram_evict runs there)")
+        p = lambda t: C.c_void_p(t.data_ptr()) if t is not None else None
+        rule = 1 if self.eng_rule == "least-read" else 0
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        check(lib().ava_engram_evict(p(self.eng_k), p(self.eng_v), p(self.eng_reads), p(self.eng_age), self.B,
+                                     self.eng_cap, n, p(self.eng_len_dev), self.eng_k.shape[2],
+                                     int(self.eng_k.dtype == torch.float16), mx, rule, stream), "ava_engram_evict")
+        self.eng_len = min(n, mx)
 
     def c(self):
         p = lambda t: t.data_ptr() if t is not None else None
@@ -203,8 +188,8 @@ class Model:
         on first use, and a capture must not allocate)."""
         if st.eng_len_dev is None:
             raise ValueError("capture_decode: the state needs device_len=True")
-        if st.eng_max:
-            raise ValueError("capture_decode: a capped store (eng_max) evicts on the host between steps")
+        if st.eng_max and st.eng_rule == "least-read":
+            raise ValueError("capture_decode: the least-read counts take the store's length from the host")
         check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")  # the graph keeps the scratch's addresses
         g = torch.cuda.CUDAGraph()
         n0, s0 = st.eng_len, st.seen
@@ -281,8 +266,8 @@ class Model:
         """decode_step over fixed buffers as a HIP graph (both streams' work; see capture_decode)."""
         if st.eng_len_dev is None:
             raise ValueError("capture_decode_step: the state needs device_len=True")
-        if st.eng_max:
-            raise ValueError("capture_decode_step: a capped store (eng_max) evicts on the host between steps")
+        if st.eng_max and st.eng_rule == "least-read":
+            raise ValueError("capture_decode_step: the least-read counts take the store's length from the host")
         check(lib().ava_model_freeze(self.h, 1), "ava_model_freeze")
         g = torch.cuda.CUDAGraph()
         n0, s0 = st.eng_len, st.seen
@@ -443,4 +428,6 @@ class DecodeGraph:
             raise ValueError(f"decode graph: the engram store holds {st.eng_len} of {st.eng_cap} entries")
         self.graph.replay()
         st.eng_len += self.T
+        if st.eng_max:
+            st.eng_len = min(st.eng_len, st.eng_max)  # the captured eviction ran on the device
         st.seen += self.T

@@ -369,6 +369,17 @@ int ava_model_set_trace(ava_model *m, int8_t *spikes, float *u, float *kth, size
 int ava_model_set_timing(ava_model *m, int on);
 int ava_model_timing(ava_model *m, const char **names, int *calls, double *ms, int cap, int reset);
 
+/* The store's cap after a forward (EngramCap / evict, gpu/state.rs:37-69, 518-590), on the device: each
+ * of the B streams' stores [B][cap][de] (f32, or fp16 with kv_half) that holds more than eng_max entries
+ * keeps eng_max of them, moved to the front in store order. rule 0 (oldest): the last eng_max. rule 1
+ * (least-read): every slot ranks by (class, value, index), class 1 for a slot some later query could
+ * see (age >= 1; value = reads / age), class 2 for the slots no later query has seen; the last eng_max of
+ * the ranking stay. reads, age [B][cap] (rule 1; nullable for rule 0) move with their slots. n: the
+ * store length, or len_dev (nullable): the length on the device, read there and set to eng_max (so a
+ * captured step may evict). No host synchronisation. */
+int ava_engram_evict(void *k, void *v, float *reads, float *age, int B, int cap, int n, int32_t *len_dev, int de,
+                     int kv_half, int eng_max, int rule, ava_stream stream);
+
 /* ------------------------------------------------------------------ the training step */
 
 /* The float32 training step of the block stack (the reference's hand-written step, gpu/model/fwin.rs:1-40:

@@ -78,3 +78,47 @@ def test_decode_graph_replays_equal_eager_steps():
     big = m.state(2 * B, eng_cap=4)
     with pytest.raises(AvaError):
         m.forward_with_state(torch.zeros((2 * B, 4), dtype=torch.int32, device="cuda"), big)
+
+
+def test_capped_decode_graph_evicts_on_replay():
+    """A capped store (eng_max, oldest first) under a captured decode step: the eviction runs inside the
+    graph on the device length, so replays past the cap keep going, and every replay equals the eager
+    step (the same kernels: the same bits); the stores and device lengths agree at the end."""
+    from ava_amd.model import Model
+    cfg = synth.config("tiny")
+    prm = synth.params(cfg, seed=21)
+    B, prefill, steps, mx = 2, 12, 8, 14
+    V = cfg["vocab"]
+    toks = np.random.default_rng(22).integers(0, V, (B, prefill + steps + 1)).astype(np.int32)
+    print(f"capped decode graph B={B} prefill={prefill} steps={steps} max={mx}", flush=True)
+    m = Model(cfg, prm)
+    sa = m.state(B, eng_cap=mx + prefill, eng_max=mx, device_len=True)
+    sb = m.state(B, eng_cap=mx + prefill, eng_max=mx, device_len=True)
+    pre = torch.from_numpy(np.ascontiguousarray(toks[:, :prefill])).cuda()
+    m.forward_with_state(pre, sa, want_logits=False)
+    m.forward_with_state(pre, sb, want_logits=False)
+    col = lambda t: torch.from_numpy(np.ascontiguousarray(toks[:, t:t + 1])).cuda()
+    want = [host(m.forward_with_state(col(t), sa)).copy() for t in range(prefill, prefill + steps)]
+    assert sa.eng_len == mx and int(host(sa.eng_len_dev)[0]) == mx
+
+    ids_buf = col(prefill).clone()
+    lg_buf = torch.empty((B, V), device="cuda")
+    m.forward_with_state(ids_buf, sb, lg_buf)
+    assert np.array_equal(host(lg_buf), want[0])
+    g = m.capture_decode(sb, ids_buf, lg_buf)
+    for i, t in enumerate(range(prefill + 1, prefill + steps)):
+        ids_buf.copy_(col(t))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(lg_buf), want[i + 1]), f"replay {i}"
+        m.forward_with_state(col(t).clone(), m.state(B, eng_cap=4), want_logits=True)
+        torch.cuda.synchronize()
+    assert sb.eng_len == sa.eng_len == mx
+    assert int(host(sb.eng_len_dev)[0]) == mx
+    for name in ("eng_k", "eng_v", "mem_f", "lif_v"):
+        assert np.array_equal(host(getattr(sb, name))[:, :mx] if name.startswith("eng") else host(getattr(sb, name)),
+                              host(getattr(sa, name))[:, :mx] if name.startswith("eng") else host(getattr(sa, name))), name
+    # the least-read rule's counts take the length from the host: its capture is refused
+    sc = m.state(B, eng_cap=mx + prefill, eng_max=mx, eng_rule="least-read", device_len=True)
+    with pytest.raises(ValueError):
+        m.capture_decode(sc, ids_buf, lg_buf)

@@ -108,43 +108,18 @@ def test_refusals(tmp_path):
     assert not sio.load_state(path, cfg0, 7, device="cpu").mem_s.any()
 
 
-def test_evict_keeps_the_last_entries_in_order():
-    """Evict::Oldest (state.rs:518-540): the store keeps its last eng_max entries, oldest first."""
+def test_evict_refuses_a_host_store():
+    """The store's cap evicts on the GPU only (ava_engram_evict): a host-side state over its cap is
+    refused before anything is launched; under the cap nothing happens."""
     cfg = synth.config("tiny")
     st = _filled(cfg, 2, 20, 13, seed=8)
-    k0, v0 = st.eng_k.clone(), st.eng_v.clone()
-    st.eng_max = 5
-    st.evict()
-    assert st.eng_len == 5
-    assert torch.equal(st.eng_k[:, :5], k0[:, 8:13]) and torch.equal(st.eng_v[:, :5], v0[:, 8:13])
     st.eng_max = 16
-    st.evict()  # under the cap: nothing moves
-    assert st.eng_len == 5 and torch.equal(st.eng_k[:, :5], k0[:, 8:13])
-
-
-def test_evict_least_read_ranks_by_reads_per_later_query():
-    """Evict::LeastRead (state.rs:540-590): per stream the slots rank by (seen by a later query, reads /
-    age, index) and the last eng_max stay, in store order, with their counts; slots no later query
-    has seen (age 0) rank last; ties go oldest first."""
-    cfg = synth.config("tiny")
-    st = _filled(cfg, 2, 20, 10, seed=11)
-    k0 = st.eng_k.clone()
-    st.eng_rule, st.eng_max = "least-read", 4
-    reads = torch.tensor([[5.0, 1.0, 3.0, 0.2, 2.0, 2.0, 9.0, 0.0, 0.0, 0.0],
-                          [0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]])
-    age = torch.tensor([[9.0, 8.0, 7.0, 6.0, 4.0, 4.0, 3.0, 2.0, 1.0, 0.0],
-                        [9.0, 8.0, 7.0, 6.0, 5.0, 4.0, 3.0, 2.0, 1.0, 0.0]])
-    st.eng_reads = torch.zeros((2, 20))
-    st.eng_age = torch.zeros((2, 20))
-    st.eng_reads[:, :10], st.eng_age[:, :10] = reads, age
     st.evict()
-    # row 0: reads / age = .556 .125 .429 .033 .5 .5 3 0 0 | unseen slot 9 last; kept: 0, 5 (tie with 4:
-    # the older 4 goes first), 6, 9; row 1: all zero reads, so the newest seen slots and the unseen one
-    want = [[0, 5, 6, 9], [6, 7, 8, 9]]
-    assert st.eng_len == 4
-    for r in range(2):
-        assert torch.equal(st.eng_k[r, :4], k0[r, want[r]])
-        assert torch.equal(st.eng_reads[r, :4], reads[r, want[r]]) and torch.equal(st.eng_age[r, :4], age[r, want[r]])
+    assert st.eng_len == 13
+    st.eng_max = 5
+    with pytest.raises(ValueError):
+        st.evict()
+    assert st.eng_len == 13
 
 
 def test_cap_saved_and_refused_rules(tmp_path):
