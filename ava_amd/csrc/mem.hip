@@ -803,6 +803,489 @@ __global__ __launch_bounds__(256, 2) void mem_chunk_kernel(MemArgs p) {
         }
 }
 
+// ------------------------------------------------------------------ the chunked form on bf16 matrix cores
+//
+// mem_chunk_kernel's algebra (chunks of CK = 16) with its two state contractions as bf16 products on
+// v_mfma_f32_16x16x32_bf16, every operand split in three terms (x = t0 + t1 + t2, each term the bf16
+// rounding of what the terms before it leave), of which the six products t_i s_j with i + j < 3 are
+// formed: the dropped ones are below 2^-24 of the product, so the contractions keep f32's precision.
+//   [Z_R ; Z_Y]  = Lhs [F0 ; S0]        32 x 128 by 128 x 64 (per wave: 2 row tiles x 4 K blocks)
+//   [F' ; S']   += Wm [V ; R]           128 x 32 by 32 x 64  (per wave: 8 row tiles x 1 K block)
+// Lhs (rows e Gamma_{i-1} | e M K_{i-1,0}, then q Gamma_i | q M K_{i,0}) and Wm (rows K_{n-1,j} w_j |
+// -K_{n-1,j} ah_j, then M^(n-1-j) w_j | -M^(n-1-j) ah_j) are the same for the four waves, so they are
+// formed once per chunk, split, and stored in LDS already in the A-operand layout of the instruction
+// (lane l of a tile: row l % 16, K slots 8 (l / 16) .. + 7; one 16-byte read per term). Each wave splits
+// its own right operands, and the K order is chosen so that they are the lane's own registers: K block
+// kb of the first product takes state tiles 2 kb and 2 kb + 1 of [F0 tiles 0..3 | S0 tiles 0..3], slot s
+// of lane group g being row 4 g + s of the first tile (s < 4) or 4 g + s - 4 of the second, exactly the
+// rows the accumulator layout leaves in the lane; in the second product slot s of group g is position
+// 4 g + s of V (s < 4) or of R (the recalls, in the same accumulator layout). The pair walk writes Lhs
+// directly (a lane ends its row's walk with Gamma_i and M K_i0 for its four channels); Wm is formed after
+// it from the last row's K_{n-1,j}, in the LDS the walk's q, e and alpha leave. The intra-chunk products
+// (Ke V, Qw V, Qa R) and the recalls' solve stay f32 (v_mfma_f32_16x16x4f32), as in mem_chunk_kernel.
+// The bound: when any wave's columns of F start a chunk above cap / 8, the whole workgroup runs that
+// chunk token by token with the bound at every step. 69 KB of LDS: two heads per CU.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int SP = HS + 4;  // row stride of the staged rows (column reads of four rows 4 apart miss each other's banks)
+
+struct ChunkBfLds {
+    float v[CK * SP], w[CK * SP], ah[CK * SP], KL[CK * SP];
+    float pm[4][CK][CK];  // Qw, Qa, Ke, Ae
+    float gl[HS];         // Gamma_{n-1}
+    int fb[4];            // per wave: its columns of F start the chunk above cap / 8
+    bf16x8 lhs[3][2][4][64];  // term, (recall rows, read rows), K block, lane
+    union {
+        struct {
+            float q[CK * SP], e[CK * SP], a[CK * SP];
+        } in;
+        bf16x8 wm[3][8][64];  // term, state row tile (F 0..3, S 4..7), lane
+    } x;
+};
+
+__device__ __forceinline__ void split3(float x, __bf16 &t0, __bf16 &t1, __bf16 &t2) {
+    t0 = (__bf16)x;
+    x = x - (float)t0;
+    t1 = (__bf16)x;
+    x = x - (float)t1;
+    t2 = (__bf16)x;
+}
+struct Terms {
+    bf16x8 t[3];
+};
+__device__ __forceinline__ Terms split8(const float (&x)[8]) {
+    Terms r;
+#pragma unroll
+    for (int z = 0; z < 8; z++) {
+        __bf16 a, b, c;
+        split3(x[z], a, b, c);
+        r.t[0][z] = a;
+        r.t[1][z] = b;
+        r.t[2][z] = c;
+    }
+    return r;
+}
+// acc m (+)= a0 b0, x (+)= a0 b1 + a1 b0, y (+)= a0 b2 + a1 b1 + a2 b0 (three chains, so consecutive
+// instructions rarely wait on each other); the total is m + (x + y)
+struct Acc4 {
+    f32x4 m, x, y;
+};
+__device__ __forceinline__ void mfma3(Acc4 &c, const bf16x8 *a, const Terms &b) {
+    c.m = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b.t[0], c.m, 0, 0, 0);
+    c.x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b.t[1], c.x, 0, 0, 0);
+    c.y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b.t[2], c.y, 0, 0, 0);
+    c.x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b.t[0], c.x, 0, 0, 0);
+    c.y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b.t[1], c.y, 0, 0, 0);
+    c.y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b.t[0], c.y, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 total4(const Acc4 &c) { return c.m + (c.x + c.y); }
+
+// The LDS slot of lane ln's A operand in K block kb of Lhs: the slot index's low bits XOR-ed with the lane
+// group and kb's parity, so that the pair walk's 8-byte writes (16 lanes of one row, four lane groups,
+// two K blocks, two halves) fall on distinct banks; any 16 consecutive lanes still read 16 distinct
+// bank groups.
+__device__ __forceinline__ int lhs_slot(int ln, int kb) { return ln ^ (((ln >> 4) & 3) << 2) ^ ((kb & 1) << 1); }
+
+// Four consecutive K rows kr0 .. kr0 + 3 (kr0 = 64 part + 4 cl: F channels, then S channels) of Lhs row
+// `row` of tile ot, split, into their A-operand slots.
+__device__ __forceinline__ void lhs_put(ChunkBfLds &s, int ot, int row, int part, int cl, const f32x4 &x) {
+    const int kb = 2 * part + (cl >> 3), ln = lhs_slot(row + 16 * (cl & 3), kb), s0 = 4 * ((cl >> 2) & 1);
+    bf16x4 t0, t1, t2;
+#pragma unroll
+    for (int z = 0; z < 4; z++) {
+        __bf16 a, b, c;
+        split3(x[z], a, b, c);
+        t0[z] = a;
+        t1[z] = b;
+        t2[z] = c;
+    }
+    *reinterpret_cast<bf16x4 *>(reinterpret_cast<__bf16 *>(&s.lhs[0][ot][kb][ln]) + s0) = t0;
+    *reinterpret_cast<bf16x4 *>(reinterpret_cast<__bf16 *>(&s.lhs[1][ot][kb][ln]) + s0) = t1;
+    *reinterpret_cast<bf16x4 *>(reinterpret_cast<__bf16 *>(&s.lhs[2][ot][kb][ln]) + s0) = t2;
+}
+
+// The pair walk of chunk_pairs (same rows per lane, same order of operations) over the padded rows,
+// ending in the lane's Lhs entries: read row i (q_i Gamma_i, q_i M K_i0) and recall row i + 1
+// (e_{i+1} Gamma_i, e_{i+1} M K_i0); the lanes of row 15 write recall row 0 (e_0, 0).
+template <bool MOM>
+__device__ __forceinline__ void chunk_walk_bf(ChunkBfLds &s, int wave, int lane, int n, float M) {
+    const int g = lane >> 4, cl = lane & 15, c0 = 4 * cl;
+    const int i = g == 0 ? wave : g == 1 ? 7 - wave : g == 2 ? 8 + wave : 15 - wave;
+    const f32x4 qi = ld4(&s.x.in.q[i * SP + c0]);
+    const f32x4 ei = i + 1 < CK ? ld4(&s.x.in.e[(i + 1) * SP + c0]) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float D[4] = {0.0f, 0.0f, 0.0f, 0.0f}, K[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int half = 1; half >= 0; half--) {
+        float x[32];
+#pragma unroll
+        for (int z = 0; z < 32; z++) x[z] = 0.0f;
+#pragma unroll
+        for (int jj = 7; jj >= 0; jj--) {
+            const int j = 8 * half + jj;
+            CK_FENCE();
+            const f32x4 al = ld4(&s.x.in.a[(j < CK - 1 ? j + 1 : CK - 1) * SP + c0]);
+            const f32x4 wj = ld4(&s.w[j * SP + c0]), aj = ld4(&s.ah[j * SP + c0]);
+            const float dl = j == i ? 1.0f : 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                D[c] = fmaf(D[c], al[c], dl);
+                K[c] = MOM ? fmaf(M, K[c], D[c]) : D[c];
+                const float kw = K[c] * wj[c], ka = K[c] * aj[c];
+                x[jj] = fmaf(qi[c], kw, x[jj]);
+                x[8 + jj] = fmaf(qi[c], ka, x[8 + jj]);
+                x[16 + jj] = fmaf(ei[c], kw, x[16 + jj]);
+                x[24 + jj] = fmaf(ei[c], ka, x[24 + jj]);
+            }
+            if (i == n - 1) *reinterpret_cast<f32x4 *>(&s.KL[j * SP + c0]) = f32x4{K[0], K[1], K[2], K[3]};
+        }
+        rs_stage<0x140, 16>(x, cl & 8);
+        rs_stage<0x141, 8>(x, cl & 4);
+        rs_stage<0x1B, 4>(x, cl & 2);
+        rs_stage<0xB1, 2>(x, cl & 1);
+        const int mm = cl >> 2, row = mm < 2 ? i : (i + 1) & (CK - 1);
+        s.pm[mm][row][8 * half + 2 * (cl & 3)] = x[0];
+        s.pm[mm][row][8 * half + 2 * (cl & 3) + 1] = x[1];
+    }
+    const f32x4 a0 = ld4(&s.x.in.a[c0]);
+    f32x4 gm, mk;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        gm[c] = D[c] * a0[c];
+        mk[c] = M * K[c];
+    }
+    if (i == n - 1) *reinterpret_cast<f32x4 *>(&s.gl[c0]) = gm;
+    f32x4 y0, y1;
+#pragma unroll
+    for (int c = 0; c < 4; c++) y0[c] = qi[c] * gm[c];
+    lhs_put(s, 1, i, 0, cl, y0);
+    if (MOM) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) y1[c] = qi[c] * mk[c];
+        lhs_put(s, 1, i, 1, cl, y1);
+    }
+    if (i + 1 < CK) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) y0[c] = ei[c] * gm[c];
+        lhs_put(s, 0, i + 1, 0, cl, y0);
+        if (MOM) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) y1[c] = ei[c] * mk[c];
+            lhs_put(s, 0, i + 1, 1, cl, y1);
+        }
+    } else {
+        lhs_put(s, 0, 0, 0, cl, ld4(&s.x.in.e[c0]));  // Gamma_{-1} = 1
+        if (MOM) lhs_put(s, 0, 0, 1, cl, f32x4{0.0f, 0.0f, 0.0f, 0.0f});  // K_{-1,0} = 0
+    }
+}
+
+// Wm's A operands: thread tid forms lane tid % 64 of state tile tid / 64 (and, with momentum, of tile
+// 4 + tid / 64): slots 0..3 the V positions 4 g .., 4..7 the R positions, g = (tid % 64) / 16.
+template <bool MOM>
+__device__ __forceinline__ void chunk_wm_bf(ChunkBfLds &s, int tid, const float (&mu)[4]) {
+    const int lane = tid & 63, g = lane >> 4, ch = 16 * (tid >> 6) + (lane & 15);
+    float wv[4], av[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        wv[r] = s.w[(4 * g + r) * SP + ch];
+        av[r] = s.ah[(4 * g + r) * SP + ch];
+    }
+    {
+        float x[8];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float kl = s.KL[(4 * g + r) * SP + ch];
+            x[r] = wv[r] * kl;
+            x[4 + r] = -(av[r] * kl);
+        }
+        const Terms t = split8(x);
+#pragma unroll
+        for (int z = 0; z < 3; z++) s.x.wm[z][tid >> 6][lane] = t.t[z];
+    }
+    if (MOM) {
+        float x[8];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            x[r] = wv[r] * mu[r];
+            x[4 + r] = -(av[r] * mu[r]);
+        }
+        const Terms t = split8(x);
+#pragma unroll
+        for (int z = 0; z < 3; z++) s.x.wm[z][4 + (tid >> 6)][lane] = t.t[z];
+    }
+}
+
+// One chunk of wave `wave`'s 16 columns by the closed form (chunk_state's algebra, the contractions on
+// the bf16 matrix cores).
+template <bool MOM>
+__device__ __forceinline__ void chunk_state_bf(const ChunkBfLds &s, int wave, int lane, float Mn, float M, float cap,
+                                               f32x4 (&Fr)[4], f32x4 (&Sr)[4], float (&Y)[4]) {
+    const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl;
+    // [Z_R ; Z_Y] = Lhs [F0 ; S0]
+    Acc4 cr{{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, cy = cr;
+#pragma unroll
+    for (int kb = 0; kb < (MOM ? 4 : 2); kb++) {
+        CK_FENCE();
+        float xb[8];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            xb[r] = kb < 2 ? Fr[2 * kb][r] : Sr[2 * kb - 4][r];
+            xb[4 + r] = kb < 2 ? Fr[2 * kb + 1][r] : Sr[2 * kb - 3][r];
+        }
+        const Terms b = split8(xb);
+        const int sl = lhs_slot(lane, kb);
+        const bf16x8 ar[3] = {s.lhs[0][0][kb][sl], s.lhs[1][0][kb][sl], s.lhs[2][0][kb][sl]};
+        const bf16x8 ay[3] = {s.lhs[0][1][kb][sl], s.lhs[1][1][kb][sl], s.lhs[2][1][kb][sl]};
+        mfma3(cr, ar, b);
+        mfma3(cy, ay, b);
+    }
+    f32x4 zr = total4(cr), zy = total4(cy);
+    CK_FENCE();
+    float Vb[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) Vb[r] = s.v[(4 * g + r) * SP + col];
+    {
+        const f32x4 ke = ld4(&s.pm[2][cl][4 * g]), qw = ld4(&s.pm[0][cl][4 * g]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            zr = __builtin_amdgcn_mfma_f32_16x16x4f32(ke[r], Vb[r], zr, 0, 0, 0);
+            zy = __builtin_amdgcn_mfma_f32_16x16x4f32(qw[r], Vb[r], zy, 0, 0, 0);
+        }
+    }
+    // (I + Ae) R = Z_R + Ke V (mem_chunk_kernel's blocked solve)
+    float R[4] = {0.0f, 0.0f, 0.0f, 0.0f}, rhs[4] = {zr[0], zr[1], zr[2], zr[3]};
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) {
+        CK_FENCE();
+        if (g == blk) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const f32x4 ae = ld4(&s.pm[3][4 * blk + r][4 * blk]);
+                float x = rhs[r];
+#pragma unroll
+                for (int rr = 0; rr < r; rr++) x = fmaf(-ae[rr], R[rr], x);
+                R[r] = x;
+            }
+        }
+        if (blk < 3) {
+            float Rb[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) Rb[r] = __shfl(R[r], 16 * blk + cl, 64);
+            if (g > blk) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const f32x4 ae = ld4(&s.pm[3][4 * g + r][4 * blk]);
+#pragma unroll
+                    for (int rr = 0; rr < 4; rr++) rhs[r] = fmaf(-ae[rr], Rb[rr], rhs[r]);
+                }
+            }
+        }
+    }
+    CK_FENCE();
+    {
+        const f32x4 qa = ld4(&s.pm[1][cl][4 * g]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) zy = __builtin_amdgcn_mfma_f32_16x16x4f32(-qa[r], R[r], zy, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) Y[r] = zy[r];
+    }
+    // [F' ; S'] = prefill + Wm [V ; R]; the F tiles first (their prefill reads the old S)
+    float xb[8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        xb[r] = Vb[r];
+        xb[4 + r] = R[r];
+    }
+    const Terms b = split8(xb);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++) {
+        CK_FENCE();
+        const int k0 = 16 * mt + 4 * g;
+        const f32x4 gl = ld4(&s.gl[k0]);
+        Acc4 c{{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        if (MOM) {
+            const f32x4 k0r = ld4(&s.KL[k0]);  // K_{n-1,0}
+#pragma unroll
+            for (int r = 0; r < 4; r++) c.m[r] = fmaf(M * k0r[r], Sr[mt][r], gl[r] * Fr[mt][r]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) c.m[r] = gl[r] * Fr[mt][r];
+        }
+        const bf16x8 a[3] = {s.x.wm[0][mt][lane], s.x.wm[1][mt][lane], s.x.wm[2][mt][lane]};
+        mfma3(c, a, b);
+        const f32x4 f = total4(c);
+#pragma unroll
+        for (int r = 0; r < 4; r++) Fr[mt][r] = __builtin_amdgcn_fmed3f(f[r], -cap, cap);
+    }
+    if (MOM) {
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            CK_FENCE();
+            Acc4 c{{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+            for (int r = 0; r < 4; r++) c.m[r] = Mn * Sr[mt][r];
+            const bf16x8 a[3] = {s.x.wm[0][4 + mt][lane], s.x.wm[1][4 + mt][lane], s.x.wm[2][4 + mt][lane]};
+            mfma3(c, a, b);
+            Sr[mt] = total4(c);
+        }
+    }
+}
+
+// One chunk of wave `wave`'s columns token by token with the bound at every step (mem_chunk_kernel's
+// fallback over the padded rows).
+template <bool MOM>
+__device__ __forceinline__ void chunk_tokens_bf(const ChunkBfLds &s, int wave, int lane, int n, float M, float cap,
+                                                f32x4 (&Fr)[4], f32x4 (&Sr)[4], float (&Y)[4]) {
+    const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl;
+#pragma unroll
+    for (int r = 0; r < 4; r++) Y[r] = 0.0f;
+    for (int t = 0; t < n; t++) {
+        float rp = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const f32x4 e4 = ld4(&s.x.in.e[t * SP + 16 * mt + 4 * g]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) rp = fmaf(e4[r], Fr[mt][r], rp);
+        }
+        const float rj = xsum32(xsum16(rp)), vj = s.v[t * SP + col];
+        float yp = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const int k0 = 16 * mt + 4 * g;
+            const f32x4 a4 = ld4(&s.x.in.a[t * SP + k0]), w4 = ld4(&s.w[t * SP + k0]), x4 = ld4(&s.ah[t * SP + k0]);
+            const f32x4 q4 = ld4(&s.x.in.q[t * SP + k0]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float u = fmaf(-x4[r], rj, w4[r] * vj);
+                float f;
+                if (MOM) {
+                    Sr[mt][r] = fmaf(M, Sr[mt][r], u);
+                    f = fmaf(a4[r], Fr[mt][r], Sr[mt][r]);
+                } else {
+                    f = fmaf(a4[r], Fr[mt][r], u);
+                }
+                f = __builtin_amdgcn_fmed3f(f, -cap, cap);
+                Fr[mt][r] = f;
+                yp = fmaf(q4[r], f, yp);
+            }
+        }
+        const float yj = xsum32(xsum16(yp));
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (t == 4 * g + r) Y[r] = yj;
+    }
+}
+
+template <bool G1, bool MOM>
+__global__ __launch_bounds__(256, 2) void mem_chunk_bf_kernel(MemArgs p) {
+    __shared__ __attribute__((aligned(16))) ChunkBfLds s;
+    const int T = p.T, nh = p.nh;
+    const float M = p.m, cap = p.cap;
+    const int bh = blockIdx.x, bi = bh / nh, hh = bh - bi * nh;
+    const int tid = threadIdx.x, lane_ = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    f32x4 Fr[4], Sr[4];
+    float *Fh = p.F + (size_t)bh * HS * HS;
+    float *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int o = (16 * mt + 4 * (lane_ >> 4) + r) * HS + 16 * wave + (lane_ & 15);
+            Fr[mt][r] = Fh[o];
+            Sr[mt][r] = MOM ? Sh[o] : 0.0f;
+        }
+
+    const size_t base = (size_t)bi * T * p.ld + (size_t)hh * HS;
+    const size_t gbase = G1 ? (size_t)bi * T * p.ldg + hh : (size_t)bi * T * p.ldg + (size_t)hh * HS;
+    const size_t ybase = (size_t)bi * T * p.ldy + (size_t)hh * HS;
+    const int sp = tid >> 4, si = (tid & 15) * 4;
+    f32x4 dq, dk, de, dv, dl, db;
+    auto load = [&](int t0) {
+        const int t = min(t0 + sp, T - 1);
+        const size_t o = base + (size_t)t * p.ld + si;
+        dq = ld4(p.q + o);
+        dk = ld4(p.k + o);
+        de = ld4(p.e + o);
+        dv = ld4(p.v + o);
+        if (G1) {
+            const float l = p.la[gbase + (size_t)t * p.ldg], b = p.b[gbase + (size_t)t * p.ldg];
+            dl = f32x4{l, l, l, l};
+            db = f32x4{b, b, b, b};
+        } else {
+            const size_t og = gbase + (size_t)t * p.ldg + si;
+            dl = ld4(p.la + og);
+            db = ld4(p.b + og);
+        }
+    };
+    load(0);
+
+    float mu[4], Mn = 0.0f;
+    int nprev = -1;
+    for (int t0 = 0; t0 < T; t0 += CK) {
+        const int n = min(CK, T - t0);
+        int lane = lane_;
+        asm volatile("" : "+v"(lane));
+        const int g = lane >> 4, cl = lane & 15, col = 16 * wave + cl;
+        if (n != nprev) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) mu[r] = 4 * g + r < n ? mpow(M, n - 1 - (4 * g + r)) : 0.0f;
+            Mn = mpow(M, n);
+            nprev = n;
+        }
+        f32x4 a4 = {1.0f, 1.0f, 1.0f, 1.0f}, w4 = {0.0f, 0.0f, 0.0f, 0.0f}, x4 = w4;
+        if (t0 + sp < T) {
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                a4[cc] = expf(dl[cc]);
+                w4[cc] = db[cc] * dk[cc];
+                x4[cc] = (a4[cc] * db[cc]) * de[cc];
+            }
+        } else {
+            dq = de = dv = w4;
+        }
+        float fmax = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) fmax = fmaxf(fmax, fabsf(Fr[mt][r]));
+        fmax = ava::wave_max(fmax);
+        __syncthreads();  // the previous chunk's LDS reads are done
+        *reinterpret_cast<f32x4 *>(&s.x.in.q[sp * SP + si]) = dq;
+        *reinterpret_cast<f32x4 *>(&s.x.in.e[sp * SP + si]) = de;
+        *reinterpret_cast<f32x4 *>(&s.x.in.a[sp * SP + si]) = a4;
+        *reinterpret_cast<f32x4 *>(&s.v[sp * SP + si]) = dv;
+        *reinterpret_cast<f32x4 *>(&s.w[sp * SP + si]) = w4;
+        *reinterpret_cast<f32x4 *>(&s.ah[sp * SP + si]) = x4;
+        if (lane == 0) s.fb[wave] = fmax > 0.125f * cap ? 1 : 0;
+        if (t0 + CK < T) load(t0 + CK);
+        __syncthreads();
+        float Y[4];
+        if (s.fb[0] | s.fb[1] | s.fb[2] | s.fb[3]) {
+            chunk_tokens_bf<MOM>(s, wave, lane, n, M, cap, Fr, Sr, Y);
+        } else {
+            chunk_walk_bf<MOM>(s, wave, lane, n, M);
+            __syncthreads();  // KL, pm, Lhs written; q, e, alpha no longer read
+            chunk_wm_bf<MOM>(s, tid, mu);
+            __syncthreads();
+            chunk_state_bf<MOM>(s, wave, lane, Mn, M, cap, Fr, Sr, Y);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (4 * g + r < n) p.y[ybase + (size_t)(t0 + 4 * g + r) * p.ldy + col] = Y[r];
+    }
+    int ls = lane_;
+    asm volatile("" : "+v"(ls));
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int o = (16 * mt + 4 * (ls >> 4) + r) * HS + 16 * wave + (ls & 15);
+            Fh[o] = Fr[mt][r];
+            if (MOM) Sh[o] = Sr[mt][r];
+        }
+}
+
 // One token per stream (decode, T == 1): the same recurrence step as mem_fused_kernel, laid out for
 // streaming the state rather than for a long scan. Wave w holds rows 16w..16w+15 of F and S and lane
 // j column j, so each of the lane's 16 + 16 state loads and stores is one 256-byte row per wave
@@ -969,12 +1452,22 @@ int mem_chunk_strided(const float *q, const float *k, const float *e, const floa
     if (B == 0 || T == 0) return AVA_OK;
     MemArgs a{q, k, e, v, la, b, T, nh, ld, ldg, ldy, m, cap, F, S, y};
     dim3 grid(B * nh), block(256);
-    if (g == 1) {
-        if (m != 0.0f) mem_chunk_kernel<true, true><<<grid, block, 0, st>>>(a);
-        else mem_chunk_kernel<true, false><<<grid, block, 0, st>>>(a);
+    // the contractions on the bf16 matrix cores; AVA_MEM_CHUNK_FP32=1 runs them on the f32 ones
+    static const bool f32 = getenv("AVA_MEM_CHUNK_FP32") && atoi(getenv("AVA_MEM_CHUNK_FP32")) == 1;
+    if (f32) {
+        if (g == 1) {
+            if (m != 0.0f) mem_chunk_kernel<true, true><<<grid, block, 0, st>>>(a);
+            else mem_chunk_kernel<true, false><<<grid, block, 0, st>>>(a);
+        } else {
+            if (m != 0.0f) mem_chunk_kernel<false, true><<<grid, block, 0, st>>>(a);
+            else mem_chunk_kernel<false, false><<<grid, block, 0, st>>>(a);
+        }
+    } else if (g == 1) {
+        if (m != 0.0f) mem_chunk_bf_kernel<true, true><<<grid, block, 0, st>>>(a);
+        else mem_chunk_bf_kernel<true, false><<<grid, block, 0, st>>>(a);
     } else {
-        if (m != 0.0f) mem_chunk_kernel<false, true><<<grid, block, 0, st>>>(a);
-        else mem_chunk_kernel<false, false><<<grid, block, 0, st>>>(a);
+        if (m != 0.0f) mem_chunk_bf_kernel<false, true><<<grid, block, 0, st>>>(a);
+        else mem_chunk_bf_kernel<false, false><<<grid, block, 0, st>>>(a);
     }
     AVA_LAUNCHED("mem_chunk");
     return AVA_OK;

@@ -539,12 +539,14 @@ class MemChunk:
     """The chunked fast-weight memory (ava_mem_chunk, delta_chunk / chunk_core) at config[3]'s per-block
     shape: 64 streams x 16 heads x 2048 tokens, unit q, k, e, v ~N(0,1), per-channel log alpha =
     log U(0.85, 0.999), b ~U(0.1, 1.9), momentum 0.5, from a zero state. The token loop (ava_mem_scan) on
-    the same inputs is timed beside it."""
+    the same inputs is timed beside it. The state contractions run as bf16 products of three-term splits
+    (mem_chunk_bf_kernel); AVA_MEM_CHUNK_FP32=1 runs them on the f32 matrix cores (mem_chunk_kernel). The
+    FLOPs are priced at the fp32 peak either way: the arithmetic is f32's."""
 
     name = "mem_chunk"
     metric = "tokens/sec chunked fast-weight memory @64 streams x 16 heads x 2048 (config[3] block), 1 GPU; % fp32 MFMA roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
-    kernel = "mem_chunk_kernel"
+    kernel = "mem_chunk_kernel" if os.environ.get("AVA_MEM_CHUNK_FP32") == "1" else "mem_chunk_bf_kernel"
 
     def __init__(self, B=64, H=16, T=2048):
         import torch
@@ -572,7 +574,8 @@ class MemChunk:
         self.flops = BH * (T // 16) * 2 * (2 * 32 * 128 * 64 + 3 * 16 * 16 * 64)
         self.bytes = BH * T * 64 * 4 * 7 + 2 * 2 * BH * 64 * 64 * 4  # 6 inputs + y; F, S in and out
         self.config = {"workload": "memory forward chunked config[3] block", "B": B, "heads": H, "T": T, "hs": 64,
-                       "gates": "per channel", "momentum": 0.5, "chunk": 16}
+                       "gates": "per channel", "momentum": 0.5, "chunk": 16,
+                       "contractions": "f32 MFMA" if MemChunk.kernel == "mem_chunk_kernel" else "bf16 MFMA, 3-term splits"}
         self.dtype = "f32"
 
     def _run(self, fn, stream):

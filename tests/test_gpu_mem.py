@@ -237,8 +237,8 @@ def test_mem_chunk_equals_scan_and_rejects_bad_shapes():
 
 
 def test_mem_chunk_bounds_hot_heads_per_token():
-    """The bound clamp(F, +-cap) acts at every token once a wave's columns of F exceed cap / 8 at a chunk's
-    start (those chunks run token by token): from a state near a small cap the chunked kernel equals the
+    """The bound clamp(F, +-cap) acts at every token once columns of F exceed cap / 8 at a chunk's start
+    (those chunks run token by token): from a state near a small cap the chunked kernel equals the
     oracle's bounded token loop (gpu/mem_gen.rs:683), and every entry stays within the cap. Unit keys:
     with keys of norm ~8 the bounded rule is chaotic and no two summation orders agree past ~30 tokens."""
     q, k, e, v, la, b = inputs(4, 90, 64, 13, unit=True)
