@@ -530,6 +530,215 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
     }
 }
 
+// The same read with S, P and O in registers (flash-attention form), one wave per (32 queries, stream,
+// head); used for heads of 32. S^T = K Q^T on v_mfma_f32_32x32x2f32: A is 32 key rows x 2 dims (lane l:
+// key l % 32, dim slot l / 32), B the wave's Q^T, loaded once; k-step s takes dims s (lanes 0..31) and
+// HD/2 + s (lanes 32..63), so a lane's key and query operands are HD/2 contiguous dims of one row. The
+// accumulator gives lane l query l % 32 and keys kappa(r, l / 32) = 8 (r / 4) + 4 (l / 32) + r % 4,
+// r = 0..15: a query's 32 scores are two lanes' 16, and the online softmax's max and sum take one lane
+// swap each. O^T += V^T P^T with the keys taken in the order kappa(t, 0), kappa(t, 1) at k-step t, so B
+// is the lane's own P[t] and A is value dims read in place (lanes 0..31 one key row, 32..63 another:
+// 128-byte rows). No LDS and no barrier; the next key tile's loads are in flight during each tile. The
+// query blocks go heaviest (latest) first. Equal to the reference's two-pass softmax up to rounding.
+template <typename KV, int N>
+__device__ __forceinline__ void load_row(const KV *p, float (&x)[N]) {
+    if constexpr (sizeof(KV) == 4) {
+#pragma unroll
+        for (int c = 0; c < N / 4; c++) {
+            const f32x4 v = reinterpret_cast<const f32x4 *>(p)[c];
+#pragma unroll
+            for (int z = 0; z < 4; z++) x[4 * c + z] = v[z];
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < N / 8; c++) {
+            const uint4 u = reinterpret_cast<const uint4 *>(p)[c];
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int z = 0; z < 4; z++) {
+                const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[z]));
+                x[8 * c + 2 * z] = f.x;
+                x[8 * c + 2 * z + 1] = f.y;
+            }
+        }
+    }
+}
+__device__ __forceinline__ float swap32max(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float swap32sum(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Buffer loads of the store (rows past the resource's range read 0).
+template <typename KV>
+__device__ __forceinline__ float kv_load(BufRes r, unsigned voff, unsigned soff) {
+    if constexpr (sizeof(KV) == 4) {
+        return load_f32(r, voff, soff);
+    } else {
+#if defined(__HIP_DEVICE_COMPILE__)
+        const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+        return __half2float(__ushort_as_half(u));
+#else
+        return 0.0f;
+#endif
+    }
+}
+template <typename KV, int N>
+__device__ __forceinline__ void kv_load_row(BufRes r, unsigned voff, float (&x)[N]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef int i32x4_ __attribute__((ext_vector_type(4)));
+    if constexpr (sizeof(KV) == 4) {
+#pragma unroll
+        for (int c = 0; c < N / 4; c++) {
+            const i32x4_ v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(voff + 16 * c), 0, 0);
+#pragma unroll
+            for (int z = 0; z < 4; z++) x[4 * c + z] = __int_as_float(v[z]);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < N / 8; c++) {
+            const i32x4_ v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(voff + 16 * c), 0, 0);
+#pragma unroll
+            for (int z = 0; z < 4; z++) {
+                const unsigned w = (unsigned)v[z];
+                const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w));
+                x[8 * c + 2 * z] = f.x;
+                x[8 * c + 2 * z + 1] = f.y;
+            }
+        }
+    }
+#endif
+}
+
+template <typename KV, int HD>
+__global__ __launch_bounds__(64, 4) void attend_fa_kernel(const float *__restrict__ q, int ldq,
+                                                      const KV *__restrict__ ks, const KV *__restrict__ vs, int cap,
+                                                      int n0, const int *n0p, int T, float scale, int de, int nh,
+                                                      float *__restrict__ out) {
+    static_assert(HD == 32 || HD == 64, "head size 32 or 64");
+    constexpr int HH = HD / 2;   // dims per lane half in S^T's k-steps
+    constexpr int NO = HD / 32;  // 32-dim tiles of O^T
+    constexpr unsigned SZ = sizeof(KV);
+    if (n0p) n0 = min(*n0p, cap - T);
+    const int nqb = (T + 31) >> 5, nsh = (int)gridDim.x / nqb;
+    // workgroups are dealt to the 8 XCDs round-robin: with (stream, head) pairs a multiple of 8, every
+    // query block of a pair gets the same id mod 8, so one XCD's L2 holds the pair's keys and values
+    const int L = (int)blockIdx.x;
+    int sh, qi;
+    if (nsh % 8 == 0) {
+        sh = (L & 7) + 8 * ((L >> 3) / nqb);
+        qi = (L >> 3) % nqb;
+    } else {
+        sh = L / nqb;
+        qi = L % nqb;
+    }
+    const int qb = (nqb - 1 - qi) * 32;  // the latest (heaviest) query blocks first
+    const int bi = sh / nh, hh = sh - bi * nh;
+    const int lane = threadIdx.x, lq = lane & 31, h = lane >> 5;
+    const float scale2 = scale * 1.44269504088896341f;  // scores in base-2 units (as attend_mfma_kernel)
+    const int qrow = qb + lq;
+    float qf[HH];
+    load_row<float, HH>(q + ((size_t)bi * T + min(qrow, T - 1)) * ldq + hh * HD + HH * h, qf);
+    const int qpos = n0 + qrow;                // this lane's store position
+    const int kend = n0 + min(qb + 32, T);     // keys the block reads: 0 .. kend - 1
+    const int kmax = n0 + T - 1;               // the store's last key
+    const int nt = (kend + 31) >> 5;           // key tiles
+    // the stream's rows 0 .. kmax of the store; lane offsets carry the head's dims
+    const unsigned rowb = (unsigned)de * SZ, range = (unsigned)(kmax + 1) * rowb;
+    const BufRes kr = buf_res((float *)(ks + (size_t)bi * cap * de), range);
+    const BufRes vr = buf_res((float *)(vs + (size_t)bi * cap * de), range);
+    const unsigned kcol = (unsigned)(hh * HD + HH * h) * SZ, vcol = (unsigned)(hh * HD + lq) * SZ;
+    // K rows of tile k0: lane row k0 + lq (past kmax: zeros)
+    auto fetchK = [&](int k0, float (&kx)[HH]) { kv_load_row<KV, HH>(kr, (unsigned)(k0 + lq) * rowb + kcol, kx); };
+    // V of tile k0 in the order of the P V k-steps: t -> key k0 + 8 (t / 4) + 4 h + t % 4
+    auto fetchV = [&](int k0, float (&vx)[NO][16]) {
+        if (k0 + 31 <= kmax) {
+            const unsigned vo = (unsigned)(k0 + 4 * h) * rowb + vcol;
+#pragma unroll
+            for (int t = 0; t < 16; t++)
+#pragma unroll
+                for (int u = 0; u < NO; u++)
+                    vx[u][t] = kv_load<KV>(vr, vo + 32u * u * SZ, (unsigned)(8 * (t >> 2) + (t & 3)) * rowb);
+        } else {  // the store's last tile: rows past kmax fall outside the resource and read 0
+#pragma unroll
+            for (int t = 0; t < 16; t++)
+#pragma unroll
+                for (int u = 0; u < NO; u++)
+                    vx[u][t] = kv_load<KV>(vr, (unsigned)(k0 + 8 * (t >> 2) + 4 * h + (t & 3)) * rowb + vcol + 32u * u * SZ, 0u);
+        }
+    };
+    auto scores = [&](const float (&kx)[HH]) {
+        f32x16 sa = {};
+#pragma unroll
+        for (int s = 0; s < HH; s++) sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kx[s], qf[s], sa, 0, 0, 0);
+        return sa;
+    };
+    float m = -INFINITY, den = 0.0f;
+    f32x16 o[NO];
+#pragma unroll
+    for (int u = 0; u < NO; u++) o[u] = f32x16{};
+    float kx[HH], vx[NO][16];
+    // tile j's scores are formed during tile j - 1 (its softmax does not wait on them): the loop enters
+    // each tile with its scores sc and the next tile's keys in kx
+    fetchK(0, kx);
+    fetchV(0, vx);
+    f32x16 sc = scores(kx);
+    if (nt > 1) fetchK(32, kx);
+    for (int j = 0; j < nt; j++) {
+        const int k0 = 32 * j;
+        const bool more = j + 1 < nt;
+        f32x16 sn = {};
+        if (more) sn = scores(kx);
+        if (j + 2 < nt) fetchK(k0 + 64, kx);
+        const bool edge = k0 + 31 > n0 + qb;  // a key of the tile lies past the block's first query
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float x = sc[r] * scale2;
+            if (edge && k0 + 8 * (r >> 2) + 4 * h + (r & 3) > qpos) x = -INFINITY;
+            sc[r] = x;
+            tmax = fmaxf(tmax, x);
+        }
+        tmax = swap32max(tmax);
+        const float nm = fmaxf(m, tmax);
+        const float corr = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - nm);
+        float psum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float e = (sc[r] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - nm);
+            sc[r] = e;
+            psum += e;
+        }
+        psum = swap32sum(psum);
+        den = den * corr + psum;
+        m = nm;
+#pragma unroll
+        for (int u = 0; u < NO; u++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[u][r] *= corr;
+#pragma unroll
+            for (int t = 0; t < 16; t++) o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(vx[u][t], sc[t], o[u], 0, 0, 0);
+        }
+        if (more) fetchV(k0 + 32, vx);
+        sc = sn;
+    }
+    if (qrow < T) {
+        float *op = out + ((size_t)bi * T + qrow) * de + hh * HD + 4 * h;
+#pragma unroll
+        for (int u = 0; u < NO; u++)
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                f32x4 w;
+#pragma unroll
+                for (int z = 0; z < 4; z++) w[z] = o[u][4 * a + z] / den;
+                *reinterpret_cast<f32x4 *>(op + 32 * u + 8 * a) = w;
+            }
+    }
+}
+
 // The decode form of the same read (flash-decoding), for a few queries per stream: query row
 // (b, t) at store position n0 + t reads keys 0..n0 + t. Its keys are cut into chunks of ACH; workgroup
 // (s, row) reads chunk s, each wave a quarter of it, 32 keys per iteration, 16 bytes per lane per
@@ -1276,8 +1485,21 @@ int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n
         AVA_LAUNCHED("attend_combine");
         return AVA_OK;
     }
-    dim3 grid(ceil_div(T, 64), B * nh);
-    attend_mfma_kernel<KV, HD><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, de, nh, out);
+    // heads of 32: the register-resident form (AVA_ATTEND_FA=0: the LDS-tiled one)
+    static const bool fa = !(getenv("AVA_ATTEND_FA") && atoi(getenv("AVA_ATTEND_FA")) == 0);
+    bool done = false;
+    if constexpr (HD == 32) {
+        // the buffer resources' byte offsets are 32-bit
+        if (fa && (size_t)cap * de * sizeof(KV) < (1ull << 31)) {
+            attend_fa_kernel<KV, HD><<<ceil_div(T, 32) * B * nh, 64, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale,
+                                                                               de, nh, out);
+            done = true;
+        }
+    }
+    if (!done) {
+        dim3 grid(ceil_div(T, 64), B * nh);
+        attend_mfma_kernel<KV, HD><<<grid, 256, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale, de, nh, out);
+    }
     AVA_LAUNCHED("attend");
     return AVA_OK;
 }
