@@ -531,7 +531,7 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(const float *__restric
 }
 
 // The same read with S, P and O in registers (flash-attention form), one wave per (32 queries, stream,
-// head); used for heads of 32. S^T = K Q^T on v_mfma_f32_32x32x2f32: A is 32 key rows x 2 dims (lane l:
+// head); the tiled read of both head sizes. S^T = K Q^T on v_mfma_f32_32x32x2f32: A is 32 key rows x 2 dims (lane l:
 // key l % 32, dim slot l / 32), B the wave's Q^T, loaded once; k-step s takes dims s (lanes 0..31) and
 // HD/2 + s (lanes 32..63), so a lane's key and query operands are HD/2 contiguous dims of one row. The
 // accumulator gives lane l query l % 32 and keys kappa(r, l / 32) = 8 (r / 4) + 4 (l / 32) + r % 4,
@@ -614,7 +614,7 @@ __device__ __forceinline__ void kv_load_row(BufRes r, unsigned voff, float (&x)[
 }
 
 template <typename KV, int HD>
-__global__ __launch_bounds__(64, 4) void attend_fa_kernel(const float *__restrict__ q, int ldq,
+__global__ __launch_bounds__(64, HD == 32 ? 4 : 2) void attend_fa_kernel(const float *__restrict__ q, int ldq,
                                                       const KV *__restrict__ ks, const KV *__restrict__ vs, int cap,
                                                       int n0, const int *n0p, int T, float scale, int de, int nh,
                                                       float *__restrict__ out) {
@@ -1485,10 +1485,10 @@ int attend_t(const float *q, int ldq, const KV *ks, const KV *vs, int cap, int n
         AVA_LAUNCHED("attend_combine");
         return AVA_OK;
     }
-    // heads of 32: the register-resident form (AVA_ATTEND_FA=0: the LDS-tiled one)
+    // the register-resident form (AVA_ATTEND_FA=0: the LDS-tiled one)
     static const bool fa = !(getenv("AVA_ATTEND_FA") && atoi(getenv("AVA_ATTEND_FA")) == 0);
     bool done = false;
-    if constexpr (HD == 32) {
+    {
         // the buffer resources' byte offsets are 32-bit
         if (fa && (size_t)cap * de * sizeof(KV) < (1ull << 31)) {
             attend_fa_kernel<KV, HD><<<ceil_div(T, 32) * B * nh, 64, 0, st>>>(q, ldq, ks, vs, cap, n0, n0p, T, scale,
