@@ -23,6 +23,8 @@
 // steps from each with every state F_t kept in registers (CK + 1 of them, and r_t), and walks those
 // steps back. The inputs of CK steps are staged in LDS; the next group's are loaded meanwhile.
 // Workspace: BH x ceil(T / CK) x (1 or 2 with momentum) x 16 KB.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace {
@@ -53,7 +55,7 @@ __device__ __forceinline__ float sum_cols(float v) {
 
 struct MemBwdArgs {
     const float *q, *k, *e, *v, *la, *b, *F0, *S0, *dy, *dFT, *dST;
-    float *dq, *dk, *de, *dv, *dla, *db, *dF0, *dS0, *ck;
+    float *dq, *dk, *de, *dv, *dla, *db, *dF0, *dS0, *ck, *part;
     int T;
     float m, cap;
 };
@@ -62,29 +64,31 @@ struct Stage {
     float q[CK][HS], k[CK][HS], e[CK][HS], v[CK][HS], a[CK][HS], b[CK][HS], bk[CK][HS], abe[CK][HS], dy[CK][HS];
 };
 
-// One forward step on the lane's 4 x 4 block (rows i0.., columns j0..): r (the block's 4 columns of
+// One forward step on the lane's 4 x CPL block (rows i0.., columns j0..): r (the block's CPL columns of
 // e^T F, summed over all rows) is returned for the backward.
-template <bool MOM>
-__device__ __forceinline__ void fwd_step(float (&F)[16], float (&S)[16], const Stage &sg, int s, int i0, int j0,
-                                         float M, float cap, float (&r)[4]) {
+template <bool MOM, int CPL>
+__device__ __forceinline__ void fwd_step(float (&F)[4 * CPL], float (&S)[4 * CPL], const Stage &sg, int s, int i0,
+                                         int j0, float M, float cap, float (&r)[CPL]) {
     const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&sg.e[s][i0]);
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
+    for (int c = 0; c < CPL; c++) {
         float x = e4[0] * F[c];
-        x = fmaf(e4[1], F[4 + c], x);
-        x = fmaf(e4[2], F[8 + c], x);
-        x = fmaf(e4[3], F[12 + c], x);
+        x = fmaf(e4[1], F[CPL + c], x);
+        x = fmaf(e4[2], F[2 * CPL + c], x);
+        x = fmaf(e4[3], F[3 * CPL + c], x);
         r[c] = sum16(x);
     }
-    const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sg.v[s][j0]);
+    float v4[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) v4[c] = sg.v[s][j0 + c];
     const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&sg.a[s][i0]);
     const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&sg.bk[s][i0]);
     const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&sg.abe[s][i0]);
 #pragma unroll
     for (int ri = 0; ri < 4; ri++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int m = 4 * ri + c;
+        for (int c = 0; c < CPL; c++) {
+            const int m = CPL * ri + c;
             const float u = fmaf(-x4[ri], r[c], k4[ri] * v4[c]);
             float f;
             if (MOM) {
@@ -97,26 +101,35 @@ __device__ __forceinline__ void fwd_step(float (&F)[16], float (&S)[16], const S
         }
 }
 
-template <bool G1, bool MOM>
+// NCG workgroups per head, each owning 64 / NCG of its value columns: NCG = 1, wave w owns columns
+// 16w.. and lane group g = lane / 16 four of them (CPL = 4); NCG = 4 (few heads: four times the
+// workgroups), workgroup cg owns columns 16cg.., wave w four of them and lane group g one (CPL = 1).
+// The rows' sums over the workgroup's columns then go to `part` [BH][NCG][T][5][64] and mem_bwd_rows
+// adds the column groups in order.
+template <bool G1, bool MOM, int NCG>
 __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
+    constexpr int CPL = 4 / NCG, NE = 4 * CPL;
     __shared__ __attribute__((aligned(16))) Stage sg;
     __shared__ float red[CK][4][5][HS];  // per step, wave and row: dq, sum gP F, sv, sr, sum dr F
 
-    const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int i0 = 4 * (lane & 15), j0 = 16 * wave + 4 * (lane >> 4);
+    const int wg = blockIdx.x, bh = wg / NCG, cg = wg - bh * NCG;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i0 = 4 * (lane & 15);
+    const int j0 = (NCG == 1 ? 16 * wave : 16 * cg + 4 * wave) + CPL * (lane >> 4);
     const int T = p.T, nck = (T + CK - 1) / CK;
     constexpr int NS = MOM ? 2 : 1;
     const size_t hb = (size_t)bh * T * HS;
     const size_t gb = G1 ? (size_t)bh * T : hb;
-    float *ckh = p.ck + (size_t)bh * nck * NS * HS * HS + (size_t)tid * 16;
+    // a workgroup's checkpoints: 256 lanes x NE floats per state
+    float *ckh = p.ck + (size_t)wg * nck * NS * (256 * NE) + (size_t)tid * NE;
     const float M = p.m, cap = p.cap;
 
-    float F[16], S[16];
+    float F[NE], S[NE];
     {
         const size_t o0 = (size_t)bh * HS * HS;
 #pragma unroll
-        for (int m = 0; m < 16; m++) {
-            const size_t o = o0 + (size_t)(i0 + (m >> 2)) * HS + j0 + (m & 3);
+        for (int m = 0; m < NE; m++) {
+            const size_t o = o0 + (size_t)(i0 + m / CPL) * HS + j0 + m % CPL;
             F[m] = p.F0 ? p.F0[o] : 0.0f;
             S[m] = (MOM && p.S0) ? p.S0[o] : 0.0f;
         }
@@ -156,16 +169,16 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
         sg.abe[st][cc] = (a * lb) * le;
         sg.dy[st][cc] = ld;
     };
-    auto park = [&](int c, const float (&X)[16], int which) {
-        float *dst = ckh + ((size_t)c * NS + which) * HS * HS;
+    auto park = [&](int c, const float (&X)[NE], int which) {
+        float *dst = ckh + ((size_t)c * NS + which) * (256 * NE);
 #pragma unroll
-        for (int z = 0; z < 4; z++)
+        for (int z = 0; z < NE / 4; z++)
             *reinterpret_cast<f32x4 *>(dst + 4 * z) = f32x4{X[4 * z], X[4 * z + 1], X[4 * z + 2], X[4 * z + 3]};
     };
-    auto unpark = [&](int c, float (&X)[16], int which) {
-        const float *src = ckh + ((size_t)c * NS + which) * HS * HS;
+    auto unpark = [&](int c, float (&X)[NE], int which) {
+        const float *src = ckh + ((size_t)c * NS + which) * (256 * NE);
 #pragma unroll
-        for (int z = 0; z < 4; z++) {
+        for (int z = 0; z < NE / 4; z++) {
             const f32x4 x = *reinterpret_cast<const f32x4 *>(src + 4 * z);
             X[4 * z] = x[0];
             X[4 * z + 1] = x[1];
@@ -187,19 +200,19 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
 #pragma unroll
         for (int s = 0; s < CK; s++) {
             if (s < n) {
-                float r[4];
-                fwd_step<MOM>(F, S, sg, s, i0, j0, M, cap, r);
+                float r[CPL];
+                fwd_step<MOM, CPL>(F, S, sg, s, i0, j0, M, cap, r);
             }
         }
     }
 
     // 2. backwards, group by group
-    float dF[16], dS[16];
+    float dF[NE], dS[NE];
     {
         const size_t o0 = (size_t)bh * HS * HS;
 #pragma unroll
-        for (int m = 0; m < 16; m++) {
-            const size_t o = o0 + (size_t)(i0 + (m >> 2)) * HS + j0 + (m & 3);
+        for (int m = 0; m < NE; m++) {
+            const size_t o = o0 + (size_t)(i0 + m / CPL) * HS + j0 + m % CPL;
             dF[m] = p.dFT ? p.dFT[o] : 0.0f;
             dS[m] = (MOM && p.dST) ? p.dST[o] : 0.0f;
         }
@@ -211,37 +224,43 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
         stage();
         __syncthreads();
         load(t0 - CK, true);  // nothing past the first group (t0 - CK < 0)
-        float Ft[CK + 1][16], rt[CK][4];
+        float Ft[CK + 1][NE], rt[CK][CPL];
         unpark(c, Ft[0], 0);
         if (MOM) unpark(c, S, 1);
 #pragma unroll
         for (int s = 0; s < CK; s++) {
             if (s < n) {
 #pragma unroll
-                for (int m = 0; m < 16; m++) Ft[s + 1][m] = Ft[s][m];
-                fwd_step<MOM>(Ft[s + 1], S, sg, s, i0, j0, M, cap, rt[s]);
+                for (int m = 0; m < NE; m++) Ft[s + 1][m] = Ft[s][m];
+                fwd_step<MOM, CPL>(Ft[s + 1], S, sg, s, i0, j0, M, cap, rt[s]);
             }
         }
 #pragma unroll
         for (int s = CK - 1; s >= 0; s--) {
             if (s < n) {
-                const float(&Fa)[16] = Ft[s];      // F before the step
-                const float(&Fb)[16] = Ft[s + 1];  // after it
+                const float(&Fa)[NE] = Ft[s];      // F before the step
+                const float(&Fb)[NE] = Ft[s + 1];  // after it
                 const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&sg.q[s][i0]);
                 const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&sg.e[s][i0]);
                 const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&sg.a[s][i0]);
                 const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&sg.bk[s][i0]);
                 const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&sg.abe[s][i0]);
-                const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sg.v[s][j0]);
-                const f32x4 y4 = *reinterpret_cast<const f32x4 *>(&sg.dy[s][j0]);
-                float pdq[4], pal[4], psv[4], psr[4], pde[4], cdr[4], cdv[4];
+                float v4[CPL], y4[CPL];
 #pragma unroll
-                for (int z = 0; z < 4; z++) pdq[z] = pal[z] = psv[z] = psr[z] = pde[z] = cdr[z] = cdv[z] = 0.0f;
+                for (int cj = 0; cj < CPL; cj++) {
+                    v4[cj] = sg.v[s][j0 + cj];
+                    y4[cj] = sg.dy[s][j0 + cj];
+                }
+                float pdq[4], pal[4], psv[4], psr[4], pde[4], cdr[CPL], cdv[CPL];
+#pragma unroll
+                for (int z = 0; z < 4; z++) pdq[z] = pal[z] = psv[z] = psr[z] = pde[z] = 0.0f;
+#pragma unroll
+                for (int z = 0; z < CPL; z++) cdr[z] = cdv[z] = 0.0f;
 #pragma unroll
                 for (int ri = 0; ri < 4; ri++)
 #pragma unroll
-                    for (int cj = 0; cj < 4; cj++) {
-                        const int m = 4 * ri + cj;
+                    for (int cj = 0; cj < CPL; cj++) {
+                        const int m = CPL * ri + cj;
                         pdq[ri] = fmaf(y4[cj], Fb[m], pdq[ri]);
                         float gP = fmaf(q4[ri], y4[cj], dF[m]);
                         gP = fabsf(Fb[m]) < cap ? gP : 0.0f;
@@ -258,15 +277,15 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
                         dF[m] = a4[ri] * gP;
                     }
 #pragma unroll
-                for (int cj = 0; cj < 4; cj++) {
+                for (int cj = 0; cj < CPL; cj++) {
                     cdr[cj] = sum16(cdr[cj]);
                     cdv[cj] = sum16(cdv[cj]);
                 }
 #pragma unroll
                 for (int ri = 0; ri < 4; ri++)
 #pragma unroll
-                    for (int cj = 0; cj < 4; cj++) {
-                        const int m = 4 * ri + cj;
+                    for (int cj = 0; cj < CPL; cj++) {
+                        const int m = CPL * ri + cj;
                         pde[ri] = fmaf(cdr[cj], Fa[m], pde[ri]);
                         dF[m] = fmaf(e4[ri], cdr[cj], dF[m]);
                     }
@@ -285,9 +304,11 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
                     *reinterpret_cast<f32x4 *>(&red[s][wave][3][i0]) = f32x4{psr[0], psr[1], psr[2], psr[3]};
                     *reinterpret_cast<f32x4 *>(&red[s][wave][4][i0]) = f32x4{pde[0], pde[1], pde[2], pde[3]};
                 }
-                if ((lane & 15) == 0)
-                    *reinterpret_cast<f32x4 *>(p.dv + hb + (size_t)(t0 + s) * HS + j0) =
-                        f32x4{cdv[0], cdv[1], cdv[2], cdv[3]};
+                if ((lane & 15) == 0) {
+                    float *dvp = p.dv + hb + (size_t)(t0 + s) * HS + j0;
+                    if (CPL == 4) *reinterpret_cast<f32x4 *>(dvp) = f32x4{cdv[0], cdv[CPL > 1 ? 1 : 0], cdv[CPL > 2 ? 2 : 0], cdv[CPL > 3 ? 3 : 0]};
+                    else dvp[0] = cdv[0];
+                }
             }
         }
         __syncthreads();
@@ -297,41 +318,93 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
             float x[5];
 #pragma unroll
             for (int z = 0; z < 5; z++) x[z] = ((red[st][0][z][cc] + red[st][1][z][cc]) + red[st][2][z][cc]) + red[st][3][z][cc];
-            const float a = sg.a[st][cc], b = sg.b[st][cc], k = sg.k[st][cc], e = sg.e[st][cc];
-            const size_t o = hb + (size_t)t * HS + cc;
-            p.dq[o] = x[0];
-            p.dk[o] = b * x[2];
-            p.de[o] = fmaf(-(a * b), x[3], x[4]);
-            const float dal = fmaf(-(b * e), x[3], x[1]);
-            const float dbr = fmaf(-(a * e), x[3], k * x[2]);
-            if (G1) {
-                const float sa = ava::wave_sum(dal * a), sb = ava::wave_sum(dbr);
-                if (cc == 0) {
-                    p.dla[gb + t] = sa;
-                    p.db[gb + t] = sb;
-                }
+            if (NCG > 1) {
+                // this workgroup's columns only: mem_bwd_rows adds the groups
+                float *pp = p.part + (((size_t)bh * NCG + cg) * T + t) * (5 * HS) + cc;
+#pragma unroll
+                for (int z = 0; z < 5; z++) pp[z * HS] = x[z];
             } else {
-                p.dla[o] = dal * a;
-                p.db[o] = dbr;
+                const float a = sg.a[st][cc], b = sg.b[st][cc], k = sg.k[st][cc], e = sg.e[st][cc];
+                const size_t o = hb + (size_t)t * HS + cc;
+                p.dq[o] = x[0];
+                p.dk[o] = b * x[2];
+                p.de[o] = fmaf(-(a * b), x[3], x[4]);
+                const float dal = fmaf(-(b * e), x[3], x[1]);
+                const float dbr = fmaf(-(a * e), x[3], k * x[2]);
+                if (G1) {
+                    const float sa = ava::wave_sum(dal * a), sb = ava::wave_sum(dbr);
+                    if (cc == 0) {
+                        p.dla[gb + t] = sa;
+                        p.db[gb + t] = sb;
+                    }
+                } else {
+                    p.dla[o] = dal * a;
+                    p.db[o] = dbr;
+                }
             }
         }
     }
     {
         const size_t o0 = (size_t)bh * HS * HS;
 #pragma unroll
-        for (int m = 0; m < 16; m++) {
-            const size_t o = o0 + (size_t)(i0 + (m >> 2)) * HS + j0 + (m & 3);
+        for (int m = 0; m < NE; m++) {
+            const size_t o = o0 + (size_t)(i0 + m / CPL) * HS + j0 + m % CPL;
             if (p.dF0) p.dF0[o] = dF[m];
             if (MOM && p.dS0) p.dS0[o] = dS[m];
         }
     }
 }
 
+// The rows' gradients from the column groups' partial sums (NCG > 1): thread -> (step, row), the groups
+// added in order, then the combine of mem_bwd_kernel.
+template <bool G1, int NCG>
+__global__ __launch_bounds__(256) void mem_bwd_rows(MemBwdArgs p) {
+    const int T = p.T, tid = threadIdx.x, cc = tid & 63;
+    const int t = blockIdx.x * 4 + (tid >> 6), bh = blockIdx.y;
+    if (t >= T) return;  // whole waves (4 steps per workgroup, one wave each)
+    float x[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < NCG; g++) {
+        const float *pp = p.part + (((size_t)bh * NCG + g) * T + t) * (5 * HS) + cc;
+#pragma unroll
+        for (int z = 0; z < 5; z++) x[z] = g ? x[z] + pp[z * HS] : pp[z * HS];
+    }
+    const size_t hb = (size_t)bh * T * HS, gb = G1 ? (size_t)bh * T : hb;
+    const size_t o = hb + (size_t)t * HS + cc, og = G1 ? gb + t : o;
+    const float a = expf(p.la[og]), b = p.b[og], k = p.k[o], e = p.e[o];
+    p.dq[o] = x[0];
+    p.dk[o] = b * x[2];
+    p.de[o] = fmaf(-(a * b), x[3], x[4]);
+    const float dal = fmaf(-(b * e), x[3], x[1]);
+    const float dbr = fmaf(-(a * e), x[3], k * x[2]);
+    if (G1) {
+        const float sa = ava::wave_sum(dal * a), sb = ava::wave_sum(dbr);
+        if (cc == 0) {
+            p.dla[gb + t] = sa;
+            p.db[gb + t] = sb;
+        }
+    } else {
+        p.dla[o] = dal * a;
+        p.db[o] = dbr;
+    }
+}
+
+// Column groups per head: four when there are too few heads to fill the GPU with one workgroup each
+// (AVA_MEM_BWD_GROUPS=1 or 4 chooses).
+int mem_bwd_groups(int BH) {
+    static const int forced = getenv("AVA_MEM_BWD_GROUPS") ? atoi(getenv("AVA_MEM_BWD_GROUPS")) : 0;
+    if (forced == 1 || forced == 4) return forced;
+    return BH < 512 ? 4 : 1;
+}
+
 }  // namespace
 
 extern "C" size_t ava_mem_scan_bwd_workspace(int BH, int T, int momentum) {
     if (BH <= 0 || T <= 0) return 0;
-    return (size_t)BH * ((T + CK - 1) / CK) * (momentum ? 2 : 1) * HS * HS * sizeof(float);
+    const int ncg = mem_bwd_groups(BH);
+    const size_t ck = (size_t)BH * ((T + CK - 1) / CK) * (momentum ? 2 : 1) * HS * HS * sizeof(float);
+    const size_t part = ncg > 1 ? (size_t)BH * ncg * T * 5 * HS * sizeof(float) : 0;
+    return ck + part;
 }
 
 // The backward of ava_mem_scan (same layout and gates), from the initial state F0, S0 (nullable:
@@ -350,16 +423,29 @@ extern "C" int ava_mem_scan_bwd(const float *q, const float *k, const float *e, 
     const bool mom = m != 0.0f;
     const size_t need = ava_mem_scan_bwd_workspace(BH, T, mom);
     AVA_REQUIRE(work_bytes >= need, AVA_ERR_SHAPE, "mem_scan_bwd: workspace %zu < %zu bytes", work_bytes, need);
+    const int ncg = mem_bwd_groups(BH);
+    float *ck = (float *)work;
+    float *part = ncg > 1 ? ck + (size_t)BH * ((T + CK - 1) / CK) * (mom ? 2 : 1) * HS * HS : nullptr;
     MemBwdArgs p{q, k, e, v, la, b, F0, mom ? S0 : nullptr, dy, dF_T, mom ? dS_T : nullptr, dq, dk, de, dv, dla, db,
-                 dF0, mom ? dS0 : nullptr, (float *)work, T, m, cap};
+                 dF0, mom ? dS0 : nullptr, ck, part, T, m, cap};
     const hipStream_t st = (hipStream_t)stream;
+#define AVA_MB(G1_, MOM_)                                                                           \
+    do {                                                                                             \
+        if (ncg > 1) {                                                                               \
+            mem_bwd_kernel<G1_, MOM_, 4><<<BH * 4, 256, 0, st>>>(p);                                 \
+            mem_bwd_rows<G1_, 4><<<dim3(ava::ceil_div(T, 4), BH), 256, 0, st>>>(p);                       \
+        } else {                                                                                     \
+            mem_bwd_kernel<G1_, MOM_, 1><<<BH, 256, 0, st>>>(p);                                     \
+        }                                                                                            \
+    } while (0)
     if (g == 1) {
-        if (mom) mem_bwd_kernel<true, true><<<BH, 256, 0, st>>>(p);
-        else mem_bwd_kernel<true, false><<<BH, 256, 0, st>>>(p);
+        if (mom) AVA_MB(true, true);
+        else AVA_MB(true, false);
     } else {
-        if (mom) mem_bwd_kernel<false, true><<<BH, 256, 0, st>>>(p);
-        else mem_bwd_kernel<false, false><<<BH, 256, 0, st>>>(p);
+        if (mom) AVA_MB(false, true);
+        else AVA_MB(false, false);
     }
+#undef AVA_MB
     AVA_LAUNCHED("mem_scan_bwd");
     return AVA_OK;
 }

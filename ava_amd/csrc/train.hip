@@ -325,114 +325,201 @@ __global__ __launch_bounds__(WG) void readout_bwd_kernel(const float *__restrict
 
 // ---------------------------------------------------------------- causal attention's backward
 
-// Rows of q, k, v, o, do: [B*T][de], head hh at dims hh*hd .. (hd = 32 or 64; lanes c < hd carry a dim).
-// Stage 1, one wave per (query row, head): the row's log-sum-exp of its scaled scores over keys 0..t,
-// D = <do, o>, and dq = scale sum_j p_j (dp_j - D) k_j with dp_j = <do, v_j>.
-__global__ __launch_bounds__(WG) void attn_bwd_q_kernel(TrainAttn a) {
-    __shared__ float s_p[WG / 64][64];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int item = blockIdx.x * (WG / 64) + wv;
-    const int N = a.B * a.T;
-    if (item >= N * a.nh) return;
-    const int row = item / a.nh, h = item - row * a.nh, bi = row / a.T, t = row - bi * a.T;
-    const int hd = a.hd, de = a.de;
-    const bool on = lane < hd;
-    const float *qr = a.q + (size_t)row * de + h * hd;
-    const float qv = on ? qr[lane] : 0.0f;
-    const float dov = on ? a.dout[(size_t)row * de + h * hd + lane] : 0.0f;
-    const float ov = on ? a.o[(size_t)row * de + h * hd + lane] : 0.0f;
-    const float D = ava::wave_sum(dov * ov);
-    const size_t base = (size_t)bi * a.T * de + h * hd;  // key 0 of this stream and head
-    // pass 1: max and sum of exp over keys j <= t, lane j within a 64-key chunk
-    float m = -INFINITY, l = 0.0f;
-    for (int j0 = 0; j0 <= t; j0 += 64) {
-        const int j = j0 + lane;
-        float s = -INFINITY;
-        if (j <= t) {
-            const float *kr = a.k + base + (size_t)j * de;
-            float acc = 0.0f;
-            for (int c = 0; c < hd; c++) acc = fmaf(qr[c], kr[c], acc);
-            s = acc * a.scale;
+// Rows of q, k, v, o, do: [B*T][de], head hh at dims hh*hd .. (hd = 32 or 64). Both kernels run the
+// forward read's register layout (the engram read's attend_fa_kernel): v_mfma_f32_32x32x2f32 products
+// whose k-step s takes dims s and HD/2 + s in the two lane halves (so a lane's row operand is HD/2
+// contiguous dims), and an accumulator that leaves lane l column l % 32 and rows
+// kappa(r, l / 32) = 8 (r / 4) + 4 (l / 32) + r % 4, r = 0..15; products over those rows take them in
+// the order kappa(t, 0), kappa(t, 1) at k-step t, so the lane's own register t is the B operand and A is
+// read in place (lanes 0..31 one row, 32..63 another). Scores are kept in base-2 units (s log2 e).
+typedef float f32x16t __attribute__((ext_vector_type(16)));
+typedef float f32x4t __attribute__((ext_vector_type(4)));
+constexpr float LOG2E = 1.44269504088896341f;
+
+template <int N>
+__device__ __forceinline__ void row_load(const float *p, float (&x)[N]) {
+#pragma unroll
+    for (int c = 0; c < N / 4; c++) {
+        const f32x4t v = reinterpret_cast<const f32x4t *>(p)[c];
+#pragma unroll
+        for (int z = 0; z < 4; z++) x[4 * c + z] = v[z];
+    }
+}
+__device__ __forceinline__ float swap_max(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float swap_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ int kap(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// One wave per (32 queries, stream, head): first the rows' log-sum-exp over keys 0..t (base 2) and
+// D = <do, o>, then per key tile S^T = K Q^T, P = 2^(S - lse), dP^T = V dO^T, dS = P (dP - D) and
+// dQ^T += K^T dS^T; dq = scale dQ. lse and D are kept for the second kernel.
+template <int HD>
+__global__ __launch_bounds__(64) void attn_bwd_dq_kernel(TrainAttn a) {
+    constexpr int HH = HD / 2, NO = HD / 32;
+    const int T = a.T, de = a.de, nh = a.nh, nqb = (T + 31) >> 5;
+    const int L = (int)blockIdx.x, sh = L / nqb, qb = (nqb - 1 - (L - sh * nqb)) * 32;
+    const int bi = sh / nh, hh = sh - bi * nh;
+    const int lane = threadIdx.x, lq = lane & 31, h = lane >> 5;
+    const int qrow = qb + lq, qc = min(qrow, T - 1);
+    const float sc2 = a.scale * LOG2E;
+    const size_t rb = (size_t)bi * T;  // the stream's first row
+    const float *kb = a.k + rb * de + hh * HD, *vb = a.v + rb * de + hh * HD;
+    float qf[HH], df[HH];
+    row_load<HH>(a.q + (rb + qc) * de + hh * HD + HH * h, qf);
+    row_load<HH>(a.dout + (rb + qc) * de + hh * HD + HH * h, df);
+    float D;
+    {
+        float of[HH];
+        row_load<HH>(a.o + (rb + qc) * de + hh * HD + HH * h, of);
+        float x = 0.0f;
+#pragma unroll
+        for (int c = 0; c < HH; c++) x = fmaf(df[c], of[c], x);
+        D = swap_sum(x);
+    }
+    const int kend = min(qb + 32, T), nt = (kend + 31) >> 5;
+    auto scores = [&](int k0) {
+        float kx[HH];
+        row_load<HH>(kb + (size_t)min(k0 + lq, T - 1) * de + HH * h, kx);
+        f32x16t s = {};
+#pragma unroll
+        for (int c = 0; c < HH; c++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kx[c], qf[c], s, 0, 0, 0);
+        const bool edge = k0 + 31 > qb;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float x = s[r] * sc2;
+            if (edge && k0 + kap(r, h) > qrow) x = -INFINITY;
+            s[r] = x;
         }
-        const float cm = ava::wave_max(s);
-        const float nm = fmaxf(m, cm);
-        const float e = (j <= t) ? expf(s - nm) : 0.0f;
-        l = l * expf(m - nm) + ava::wave_sum(e);
+        return s;
+    };
+    // the log-sum-exp (base 2)
+    float m = -INFINITY, den = 0.0f;
+    for (int j = 0; j < nt; j++) {
+        const f32x16t s = scores(32 * j);
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s[r]);
+        const float nm = fmaxf(m, swap_max(tmax));
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) ps += s[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r] - nm);
+        den = (m == -INFINITY ? 0.0f : den * __builtin_amdgcn_exp2f(m - nm)) + swap_sum(ps);
         m = nm;
     }
-    const float lse = m + logf(l);
-    // pass 2: dq
-    float dq = 0.0f;
-    for (int j0 = 0; j0 <= t; j0 += 64) {
-        const int j = j0 + lane;
-        float ds = 0.0f;
-        if (j <= t) {
-            const float *kr = a.k + base + (size_t)j * de, *vr = a.v + base + (size_t)j * de;
-            const float *dr = a.dout + (size_t)row * de + h * hd;
-            float acc = 0.0f, dp = 0.0f;
-            for (int c = 0; c < hd; c++) {
-                acc = fmaf(qr[c], kr[c], acc);
-                dp = fmaf(dr[c], vr[c], dp);
-            }
-            const float p = expf(acc * a.scale - lse);
-            ds = p * (dp - D);
+    const float lse = m + __log2f(den);
+    f32x16t dq[NO];
+#pragma unroll
+    for (int u = 0; u < NO; u++) dq[u] = f32x16t{};
+    for (int j = 0; j < nt; j++) {
+        const int k0 = 32 * j;
+        f32x16t s = scores(k0);
+        float vx[HH];
+        row_load<HH>(vb + (size_t)min(k0 + lq, T - 1) * de + HH * h, vx);
+        f32x16t dp = {};
+#pragma unroll
+        for (int c = 0; c < HH; c++) dp = __builtin_amdgcn_mfma_f32_32x32x2f32(vx[c], df[c], dp, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float p = s[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r] - lse);
+            s[r] = p * (dp[r] - D);  // dS
         }
-        s_p[wv][lane] = ds;
-        __builtin_amdgcn_wave_barrier();
-        const int n = min(64, t + 1 - j0);
-        if (on)
-            for (int jj = 0; jj < n; jj++) dq = fmaf(s_p[wv][jj], a.k[base + (size_t)(j0 + jj) * de + lane], dq);
-        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < NO; u++)
+#pragma unroll
+            for (int t = 0; t < 16; t++) {
+                const float kt = kb[(size_t)min(k0 + kap(t, h), T - 1) * de + 32 * u + lq];
+                dq[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(kt, s[t], dq[u], 0, 0, 0);
+            }
     }
-    if (on) a.dq[(size_t)row * de + h * hd + lane] = dq * a.scale;
-    if (lane == 0) {
-        a.lse[(size_t)row * a.nh + h] = lse;
-        a.dsum[(size_t)row * a.nh + h] = D;
+    if (qrow < T) {
+        float *op = a.dq + (rb + qrow) * de + hh * HD + 4 * h;
+#pragma unroll
+        for (int u = 0; u < NO; u++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                f32x4t w;
+#pragma unroll
+                for (int z = 0; z < 4; z++) w[z] = dq[u][4 * g + z] * a.scale;
+                *reinterpret_cast<f32x4t *>(op + 32 * u + 8 * g) = w;
+            }
+        if (h == 0) {
+            a.lse[(rb + qrow) * nh + hh] = lse;
+            a.dsum[(rb + qrow) * nh + hh] = D;
+        }
     }
 }
 
-// Stage 2, one wave per (key row, head): dv_j = sum_{i >= j} p_ij do_i, dk_j = scale sum_i p_ij (dp_ij - D_i) q_i
-__global__ __launch_bounds__(WG) void attn_bwd_kv_kernel(TrainAttn a) {
-    __shared__ float s_p[WG / 64][64], s_s[WG / 64][64];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int item = blockIdx.x * (WG / 64) + wv;
-    const int N = a.B * a.T;
-    if (item >= N * a.nh) return;
-    const int row = item / a.nh, h = item - row * a.nh, bi = row / a.T, j = row - bi * a.T;
-    const int hd = a.hd, de = a.de;
-    const bool on = lane < hd;
-    const float *kr = a.k + (size_t)row * de + h * hd, *vr = a.v + (size_t)row * de + h * hd;
-    const size_t base = (size_t)bi * a.T * de + h * hd;
-    float dk = 0.0f, dv = 0.0f;
-    for (int i0 = j; i0 < a.T; i0 += 64) {
-        const int i = i0 + lane;
-        float p = 0.0f, ds = 0.0f;
-        if (i < a.T) {
-            const float *qr = a.q + base + (size_t)i * de, *dr = a.dout + base + (size_t)i * de;
-            float acc = 0.0f, dp = 0.0f;
-            for (int c = 0; c < hd; c++) {
-                acc = fmaf(qr[c], kr[c], acc);
-                dp = fmaf(dr[c], vr[c], dp);
-            }
-            const size_t ri = ((size_t)bi * a.T + i) * a.nh + h;
-            p = expf(acc * a.scale - a.lse[ri]);
-            ds = p * (dp - a.dsum[ri]);
+// One wave per (32 keys, stream, head), over the query tiles at and after the keys: S = Q K^T (lane:
+// key, registers: queries), P = 2^(S - lse), dP = dO V^T, dS = P (dP - D); dV^T += dO^T P and
+// dK^T += Q^T dS; dk = scale dK.
+template <int HD>
+__global__ __launch_bounds__(64) void attn_bwd_dkv_kernel(TrainAttn a) {
+    constexpr int HH = HD / 2, NO = HD / 32;
+    const int T = a.T, de = a.de, nh = a.nh, nkb = (T + 31) >> 5;
+    const int L = (int)blockIdx.x, sh = L / nkb, kb0 = (L - sh * nkb) * 32;  // the earliest keys (most queries) first
+    const int bi = sh / nh, hh = sh - bi * nh;
+    const int lane = threadIdx.x, lq = lane & 31, h = lane >> 5;
+    const int key = kb0 + lq, kc = min(key, T - 1);
+    const float sc2 = a.scale * LOG2E;
+    const size_t rb = (size_t)bi * T;
+    const float *qb = a.q + rb * de + hh * HD, *ob = a.dout + rb * de + hh * HD;
+    float kf[HH], vf[HH];
+    row_load<HH>(a.k + (rb + kc) * de + hh * HD + HH * h, kf);
+    row_load<HH>(a.v + (rb + kc) * de + hh * HD + HH * h, vf);
+    f32x16t dk[NO], dv[NO];
+#pragma unroll
+    for (int u = 0; u < NO; u++) dk[u] = dv[u] = f32x16t{};
+    for (int q0 = kb0; q0 < T; q0 += 32) {
+        float qx[HH], ox[HH];
+        const int qr = min(q0 + lq, T - 1);
+        row_load<HH>(qb + (size_t)qr * de + HH * h, qx);
+        row_load<HH>(ob + (size_t)qr * de + HH * h, ox);
+        f32x16t s = {}, dp = {};
+#pragma unroll
+        for (int c = 0; c < HH; c++) {
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(qx[c], kf[c], s, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ox[c], vf[c], dp, 0, 0, 0);
         }
-        s_p[wv][lane] = p;
-        s_s[wv][lane] = ds;
-        __builtin_amdgcn_wave_barrier();
-        const int n = min(64, a.T - i0);
-        if (on)
-            for (int ii = 0; ii < n; ii++) {
-                const size_t r = base + (size_t)(i0 + ii) * de + lane;
-                dv = fmaf(s_p[wv][ii], a.dout[r], dv);
-                dk = fmaf(s_s[wv][ii], a.q[r], dk);
+        const bool edge = q0 < kb0 + 31;  // a query of the tile lies before the block's last key
+        float pr[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int qi = q0 + kap(r, h);
+            const bool ok = qi < T && (!edge || qi >= key);
+            const size_t ri = (rb + min(qi, T - 1)) * nh + hh;
+            const float p = ok ? __builtin_amdgcn_exp2f(s[r] * sc2 - a.lse[ri]) : 0.0f;
+            pr[r] = p;
+            s[r] = p * (dp[r] - a.dsum[ri]);  // dS
+        }
+#pragma unroll
+        for (int u = 0; u < NO; u++)
+#pragma unroll
+            for (int t = 0; t < 16; t++) {
+                const size_t rr = (size_t)min(q0 + kap(t, h), T - 1) * de + 32 * u + lq;
+                dv[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(ob[rr], pr[t], dv[u], 0, 0, 0);
+                dk[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(qb[rr], s[t], dk[u], 0, 0, 0);
             }
-        __builtin_amdgcn_wave_barrier();
     }
-    if (on) {
-        a.dk[(size_t)row * de + h * hd + lane] = dk * a.scale;
-        a.dv[(size_t)row * de + h * hd + lane] = dv;
+    if (key < T) {
+        float *kp = a.dk + (rb + key) * de + hh * HD + 4 * h, *vp = a.dv + (rb + key) * de + hh * HD + 4 * h;
+#pragma unroll
+        for (int u = 0; u < NO; u++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                f32x4t wk, wv;
+#pragma unroll
+                for (int z = 0; z < 4; z++) {
+                    wk[z] = dk[u][4 * g + z] * a.scale;
+                    wv[z] = dv[u][4 * g + z];
+                }
+                *reinterpret_cast<f32x4t *>(kp + 32 * u + 8 * g) = wk;
+                *reinterpret_cast<f32x4t *>(vp + 32 * u + 8 * g) = wv;
+            }
     }
 }
 
@@ -629,11 +716,15 @@ int readout_bwd(const float *y, const float *g, const float *dout, int B, int T,
 
 int attn_bwd(const TrainAttn &a, hipStream_t st) {
     AVA_REQUIRE(a.hd == 32 || a.hd == 64, AVA_ERR_SHAPE, "train attn_bwd: head size %d (32 or 64)", a.hd);
-    const size_t items = (size_t)a.B * a.T * a.nh;
-    attn_bwd_q_kernel<<<grid1(items, WG / 64), WG, 0, st>>>(a);
-    AVA_LAUNCHED("train attn_bwd_q");
-    attn_bwd_kv_kernel<<<grid1(items, WG / 64), WG, 0, st>>>(a);
-    AVA_LAUNCHED("train attn_bwd_kv");
+    AVA_REQUIRE(a.de % 4 == 0 && a.de == a.nh * a.hd && a.T > 0 && a.B > 0, AVA_ERR_SHAPE,
+                "train attn_bwd: B=%d T=%d de=%d nh=%d hd=%d", a.B, a.T, a.de, a.nh, a.hd);
+    const int blocks = ceil_div(a.T, 32) * a.B * a.nh;
+    if (a.hd == 32) attn_bwd_dq_kernel<32><<<blocks, 64, 0, st>>>(a);
+    else attn_bwd_dq_kernel<64><<<blocks, 64, 0, st>>>(a);
+    AVA_LAUNCHED("train attn_bwd_dq");
+    if (a.hd == 32) attn_bwd_dkv_kernel<32><<<blocks, 64, 0, st>>>(a);
+    else attn_bwd_dkv_kernel<64><<<blocks, 64, 0, st>>>(a);
+    AVA_LAUNCHED("train attn_bwd_dkv");
     return AVA_OK;
 }
 

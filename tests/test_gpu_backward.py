@@ -183,6 +183,18 @@ def test_mem_bwd_long():
         assert e < 1e-4, (n, e)
 
 
+def test_mem_bwd_many_heads():
+    """512 heads: one workgroup per head and 16 columns per wave (fewer heads take four workgroups per
+    head, a wave's 4 columns each, and add the rows' sums of the four in a second kernel)."""
+    x = mem_inputs(91, 512, 9, 64)
+    print("mem_bwd BH=512 T=9", flush=True)
+    o = O.mem_rec_bwd(*x[:6], x[8], m=0.5, F0=x[6], S0=x[7], dF_T=x[9], dS_T=x[10])
+    gpu = run_mem(x, 0.5, 1e5)
+    for n in MEM_OUT + ("dS0",):
+        e = rel(gpu[n], o[n])
+        assert e < 1e-5, (n, e)
+
+
 def test_wrappers_ignore_the_default_dtype():
     """The wrappers allocate float32 whatever torch's default dtype is (a float64 default once gave
     float64 output buffers that the kernels, writing float32, left mostly unwritten)."""
