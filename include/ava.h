@@ -183,7 +183,8 @@ int ava_kwta_relu2_bwd(const float *u, const float *kth, int n, int h, const flo
  * (nullable: zeros) with dy [BH][T][hs] = dL/dy and dF_T, dS_T = dL/d(final F, S) (nullable: zeros):
  * dq, dk, de, dv [BH][T][hs]; dla, db [BH][T][g]; dF0, dS0 [BH][hs][hs] (nullable) = dL/d(F0, S0).
  * The bound clamp(., +-cap) passes no gradient where it holds. work: device memory of
- * ava_mem_scan_bwd_workspace(BH, T, m != 0) bytes (the states the replay keeps). Replaces memg_bwd_* /
+ * ava_mem_scan_bwd_workspace(BH, T, m != 0) bytes (the states the replay keeps and, below 512 heads,
+ * where each head's columns are split over four workgroups, their partial row sums). Replaces memg_bwd_* /
  * memg_bwd4_* (gpu/lif.cu:3411-3888; MemGenBwd, gpu/mem_gen.rs:296-470) and the gradient of delta_rec
  * (gpu/arch.rs:1091-1136). */
 size_t ava_mem_scan_bwd_workspace(int BH, int T, int momentum);
