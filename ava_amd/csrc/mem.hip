@@ -217,6 +217,133 @@ __global__ __launch_bounds__(256) void mem_scan_kernel(MemArgs p) {
     }
 }
 
+// The same scan for few heads: each head's 64 value columns in four workgroups (the recurrence never
+// mixes columns), so B nh < 512 heads still fill the GPU. Workgroup (head, cg) owns columns 16 cg ..;
+// wave w four of them, lane l rows 4 (l & 15) .. + 3 of column 16 cg + 4 w + l / 16: a column sum is 4
+// FMAs and a sum over the 16 lanes of a DPP row. The staging is mem_scan_kernel's (every workgroup
+// stages all 64 rows of its head's inputs).
+__device__ __forceinline__ float sum16r(float v) {
+    v = sum8(v);
+    return v + dppf<0x140>(v);
+}
+
+template <bool G1, bool MOM>
+__global__ __launch_bounds__(256) void mem_scan_cols_kernel(MemArgs p) {
+    __shared__ __attribute__((aligned(16))) float s_q[TS][HS], s_e[TS][HS], s_v[TS][HS];
+    __shared__ __attribute__((aligned(16))) float s_a[TS][HS], s_bk[TS][HS], s_abe[TS][HS];
+    __shared__ __attribute__((aligned(16))) float s_y[TS][16];
+
+    const int bh = blockIdx.x >> 2, cg = blockIdx.x & 3;
+    const int bi = bh / p.nh, hh = bh - bi * p.nh;
+    const size_t base = (size_t)bi * p.T * p.ld + (size_t)hh * HS;
+    const size_t gbase = G1 ? (size_t)bi * p.T * p.ldg + hh : (size_t)bi * p.T * p.ldg + (size_t)hh * HS;
+    const size_t ybase = (size_t)bi * p.T * p.ldy + (size_t)hh * HS + 16 * cg;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i0 = 4 * (lane & 15), jl = 4 * wave + (lane >> 4), j = 16 * cg + jl;
+
+    float Fr[4], Sr[4];
+    float *Fh = p.F + (size_t)bh * HS * HS, *Sh = MOM ? p.S + (size_t)bh * HS * HS : nullptr;
+#pragma unroll
+    for (int ri = 0; ri < 4; ri++) {
+        const int o = (i0 + ri) * HS + j;
+        Fr[ri] = Fh[o];
+        Sr[ri] = MOM ? Sh[o] : 0.0f;
+    }
+
+    const int st = tid >> 4, si = (tid & 15) * 4;
+    f32x4 rq, rk, re, rv, rla, rb;
+    auto load = [&](int t0) {
+        const int t = t0 + st;
+        if (t < p.T) {
+            const size_t o = base + (size_t)t * p.ld + si;
+            rq = *reinterpret_cast<const f32x4 *>(p.q + o);
+            rk = *reinterpret_cast<const f32x4 *>(p.k + o);
+            re = *reinterpret_cast<const f32x4 *>(p.e + o);
+            rv = *reinterpret_cast<const f32x4 *>(p.v + o);
+            if (G1) {
+                const float l = p.la[gbase + (size_t)t * p.ldg], b = p.b[gbase + (size_t)t * p.ldg];
+                rla = f32x4{l, l, l, l};
+                rb = f32x4{b, b, b, b};
+            } else {
+                const size_t og = gbase + (size_t)t * p.ldg + si;
+                rla = *reinterpret_cast<const f32x4 *>(p.la + og);
+                rb = *reinterpret_cast<const f32x4 *>(p.b + og);
+            }
+        } else {
+            rq = rk = re = rv = rla = rb = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    auto stage = [&]() {
+        f32x4 a, bk, abe;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            a[c] = expf(rla[c]);
+            bk[c] = rb[c] * rk[c];
+            abe[c] = (a[c] * rb[c]) * re[c];
+        }
+        *reinterpret_cast<f32x4 *>(&s_q[st][si]) = rq;
+        *reinterpret_cast<f32x4 *>(&s_e[st][si]) = re;
+        *reinterpret_cast<f32x4 *>(&s_v[st][si]) = rv;
+        *reinterpret_cast<f32x4 *>(&s_a[st][si]) = a;
+        *reinterpret_cast<f32x4 *>(&s_bk[st][si]) = bk;
+        *reinterpret_cast<f32x4 *>(&s_abe[st][si]) = abe;
+    };
+
+    const float M = p.m, cap = p.cap;
+    load(0);
+    for (int t0 = 0; t0 < p.T; t0 += TS) {
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (t0 + TS < p.T) load(t0 + TS);
+        const int n = min(TS, p.T - t0);
+        for (int s = 0; s < n; s++) {
+            const f32x4 e4 = *reinterpret_cast<const f32x4 *>(&s_e[s][i0]);
+            float r = e4[0] * Fr[0];
+            r = fmaf(e4[1], Fr[1], r);
+            r = fmaf(e4[2], Fr[2], r);
+            r = fmaf(e4[3], Fr[3], r);
+            r = sum16r(r);
+            const float vj = s_v[s][j];
+            const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&s_q[s][i0]);
+            const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&s_a[s][i0]);
+            const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&s_bk[s][i0]);
+            const f32x4 x4 = *reinterpret_cast<const f32x4 *>(&s_abe[s][i0]);
+            float ya = 0.0f;
+#pragma unroll
+            for (int ri = 0; ri < 4; ri++) {
+                const float u = fmaf(-x4[ri], r, k4[ri] * vj);
+                float f;
+                if (MOM) {
+                    Sr[ri] = fmaf(M, Sr[ri], u);
+                    f = fmaf(a4[ri], Fr[ri], Sr[ri]);
+                } else {
+                    f = fmaf(a4[ri], Fr[ri], u);
+                }
+                f = __builtin_amdgcn_fmed3f(f, -cap, cap);
+                Fr[ri] = f;
+                ya = fmaf(q4[ri], f, ya);
+            }
+            ya = sum16r(ya);
+            if ((lane & 15) == 0) s_y[s][jl] = ya;
+        }
+        __syncthreads();
+        // the chunk's read-outs of the workgroup's 16 columns: thread -> (step, 4 columns)
+        if (tid < 4 * n) {
+            const int sy = tid >> 2, c4 = (tid & 3) * 4;
+            *reinterpret_cast<f32x4 *>(p.y + ybase + (size_t)(t0 + sy) * p.ldy + c4) =
+                *reinterpret_cast<const f32x4 *>(&s_y[sy][c4]);
+        }
+    }
+#pragma unroll
+    for (int ri = 0; ri < 4; ri++) {
+        const int o = (i0 + ri) * HS + j;
+        Fh[o] = Fr[ri];
+        if (MOM) Sh[o] = Sr[ri];
+    }
+}
+
 // ------------------------------------------------------------------ the block's memory, prep fused
 
 // The memory of one Ava-0.4 block in one kernel: the preparation of gpu/arch.rs:1873-1941 (unit q, k
@@ -1405,13 +1532,28 @@ int mem_scan_strided(const float *q, const float *k, const float *e, const float
                 "mem_scan: B=%d T=%d nh=%d ld=%d ldg=%d ldy=%d", B, T, nh, ld, ldg, ldy);
     if (B == 0 || T == 0) return AVA_OK;
     MemArgs a{q, k, e, v, la, b, T, nh, ld, ldg, ldy, m, cap, F, S, y};
-    dim3 grid(B * nh), block(256);
-    if (g == 1) {
-        if (m != 0.0f) mem_scan_kernel<true, true><<<grid, block, 0, st>>>(a);
-        else mem_scan_kernel<true, false><<<grid, block, 0, st>>>(a);
+    dim3 block(256);
+    // fewer than 512 heads: four workgroups per head (AVA_MEM_SCAN_GROUPS=1 or 4 chooses)
+    static const int forced = getenv("AVA_MEM_SCAN_GROUPS") ? atoi(getenv("AVA_MEM_SCAN_GROUPS")) : 0;
+    const bool cols = forced == 4 || (forced != 1 && B * nh < 512);
+    if (cols) {
+        dim3 grid(B * nh * 4);
+        if (g == 1) {
+            if (m != 0.0f) mem_scan_cols_kernel<true, true><<<grid, block, 0, st>>>(a);
+            else mem_scan_cols_kernel<true, false><<<grid, block, 0, st>>>(a);
+        } else {
+            if (m != 0.0f) mem_scan_cols_kernel<false, true><<<grid, block, 0, st>>>(a);
+            else mem_scan_cols_kernel<false, false><<<grid, block, 0, st>>>(a);
+        }
     } else {
-        if (m != 0.0f) mem_scan_kernel<false, true><<<grid, block, 0, st>>>(a);
-        else mem_scan_kernel<false, false><<<grid, block, 0, st>>>(a);
+        dim3 grid(B * nh);
+        if (g == 1) {
+            if (m != 0.0f) mem_scan_kernel<true, true><<<grid, block, 0, st>>>(a);
+            else mem_scan_kernel<true, false><<<grid, block, 0, st>>>(a);
+        } else {
+            if (m != 0.0f) mem_scan_kernel<false, true><<<grid, block, 0, st>>>(a);
+            else mem_scan_kernel<false, false><<<grid, block, 0, st>>>(a);
+        }
     }
     AVA_LAUNCHED("mem_scan");
     return AVA_OK;

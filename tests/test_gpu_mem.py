@@ -37,10 +37,11 @@ def rel(a, b):
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
 
 
-@pytest.mark.parametrize("g,m,T", [(1, 0.0, 37), (64, 0.0, 64), (64, 0.5, 100), (1, 0.5, 16), (64, 0.5, 1)])
-def test_mem_scan_matches_recurrence(g, m, T):
-    BH = 5
-    print(f"mem_scan g={g} m={m} T={T}", flush=True)
+# 5 heads take four workgroups per head (columns split), 512 heads one workgroup per head
+@pytest.mark.parametrize("g,m,T,BH", [(1, 0.0, 37, 5), (64, 0.0, 64, 5), (64, 0.5, 100, 5), (1, 0.5, 16, 5),
+                                      (64, 0.5, 1, 5), (64, 0.5, 19, 512), (1, 0.0, 21, 512)])
+def test_mem_scan_matches_recurrence(g, m, T, BH):
+    print(f"mem_scan g={g} m={m} T={T} BH={BH}", flush=True)
     q, k, e, v, la, b = inputs(BH, T, g, 3 + g + T)
     rng = np.random.default_rng(7)
     F0 = (rng.standard_normal((BH, 64, 64)) * 0.1).astype(np.float32)
