@@ -251,7 +251,8 @@ class Gemm:
         O.q8_matmul_ref(x, q, s, threads=th)
         dt = time.perf_counter() - t0
         return {"value": rows / dt, "unit": "rows/s", "cores": th, "kind": "port",
-                "sample": f"oracle W8A32 product (int8.rs:301-331 fma chain), {rows} rows, {dt:.2f} s"}
+                "sample": f"oracle W8A32 product (int8.rs:301-331 fma chain, in int8/block.rs's 6 x 16 register blocks), "
+                          f"{rows} rows, {dt:.2f} s"}
 
 
 class Delta:
@@ -762,7 +763,7 @@ class Stack:
     def cpu_baseline(self):
         from oracle import oracle as O
 
-        B, T = 2, 2048  # 4096 tokens: about 10-15 s of CPU work
+        B, T = 2, 2048  # 4096 tokens: a few seconds on the box's 16 threads
         th = cpu_threads()
         O.set_threads(th)
         om = O.OracleModel(self.cfg, self.params)
@@ -771,7 +772,8 @@ class Stack:
         om.forward(ids, state=om.new_state(B, eng_cap=T), planes=0, threads=th)
         dt = time.perf_counter() - t0
         return {"value": B * T / dt, "unit": "tokens/s", "cores": th, "kind": "port",
-                "sample": f"oracle block-stack forward with the reference's W8A32 products (int8.rs:301-331) on "
+                "sample": f"oracle block-stack forward with the reference's W8A32 products (int8.rs:301-331 fma chain, "
+                          f"int8/block.rs's 6 x 16 register blocks from 6 rows) on "
                           f"config[3]'s model, B={B}, T={T}, {th} threads for the products, {dt:.2f} s"}
 
 
@@ -841,7 +843,8 @@ class Greedy:
             last = lg[-1]
         dt = time.perf_counter() - t0
         return {"value": new / dt, "unit": "tokens/s", "cores": th, "kind": "port",
-                "sample": f"oracle greedy loop with the reference's W8A32 products (int8.rs:301-331) on config[0]'s "
+                "sample": f"oracle greedy loop with the reference's W8A32 products (int8.rs:301-331; the prompt in "
+                          f"int8/block.rs's 6 x 16 register blocks) on config[0]'s "
                           f"model: the {self.prompt_len}-token prompt and {new} steps, {th} threads, {dt:.2f} s "
                           f"(prefill included, as in the GPU figure; the same tokens are not checked here)"}
 

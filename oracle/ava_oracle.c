@@ -165,8 +165,9 @@ static void tile_row(const float *x, int din, const int8_t *q, int dout, int c0,
     for (int c = 0; c < nc; c++) y[c0 + c] = acc[c] * scale[c0 + c];
 }
 
-void orc_q8_matmul_ref(const float *x, int m, int din, const int8_t *q, const float *scale,
-                       int dout, float *y, int threads) {
+/* The per-row form (gpu/int8.rs:166-211): every row through tile_row, each (row, tile) a unit. */
+void orc_q8_matmul_rows(const float *x, int m, int din, const int8_t *q, const float *scale, int dout, float *y,
+                        int threads) {
     int tiles = (dout + TILE - 1) / TILE;
     long units = (long)m * tiles;
     if (threads < 1) threads = 1;
@@ -176,6 +177,140 @@ void orc_q8_matmul_ref(const float *x, int m, int din, const int8_t *q, const fl
         int c0 = t * TILE, nc = dout - c0 < TILE ? dout - c0 : TILE;
         tile_row(x + (size_t)r * din, din, q, dout, c0, nc, scale, y + (size_t)r * dout);
     }
+}
+
+/* The row-blocked form of batched products (gpu/int8/block.rs:1-225): a unit is one 64-column tile
+ * and up to BLK_CHUNK consecutive rows; the tile is widened to f32 once per unit as four 16-column
+ * sub-tiles [4][din][16]; the unit's dense rows go 6 at a time through a 6 x 16 register block (12
+ * AVX2 accumulators: two weight loads and six broadcasts per input j), the last 1..5 rows through the
+ * same block with fewer rows; rows with at most a tenth of their inputs non-zero keep the per-row
+ * event sum. The same bits as tile_row: each output starts at +0 and adds fma(x[j], w[j][c], acc) for
+ * j = 0, 1, ...; a zero x[j] leaves acc as it was (acc is never -0: an exact cancellation rounds to
+ * +0), so skipping it or not changes nothing; the scale multiplies at the end. */
+#define BLK_ROWS 6
+#define BLK_SUB 16
+#define BLK_CHUNK 48
+#if defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+/* NR rows (a compile-time count, so the 2 NR accumulators stay in registers) */
+#define BLOCK_ROWS_N(NR)                                                                                       \
+    static void block_rows_##NR(const float *x, int din, const float *tf, float *acc) {                       \
+        __m256 a[NR][2];                                                                                       \
+        for (int r = 0; r < NR; r++) a[r][0] = a[r][1] = _mm256_setzero_ps();                                 \
+        for (int j = 0; j < din; j++) {                                                                        \
+            const __m256 w0 = _mm256_loadu_ps(tf + (size_t)j * BLK_SUB);                                       \
+            const __m256 w1 = _mm256_loadu_ps(tf + (size_t)j * BLK_SUB + 8);                                   \
+            for (int r = 0; r < NR; r++) {                                                                     \
+                const __m256 xb = _mm256_broadcast_ss(x + (size_t)r * din + j);                                \
+                a[r][0] = _mm256_fmadd_ps(xb, w0, a[r][0]);                                                    \
+                a[r][1] = _mm256_fmadd_ps(xb, w1, a[r][1]);                                                    \
+            }                                                                                                  \
+        }                                                                                                      \
+        for (int r = 0; r < NR; r++) {                                                                         \
+            _mm256_storeu_ps(acc + r * BLK_SUB, a[r][0]);                                                      \
+            _mm256_storeu_ps(acc + r * BLK_SUB + 8, a[r][1]);                                                  \
+        }                                                                                                      \
+    }
+BLOCK_ROWS_N(1)
+BLOCK_ROWS_N(2)
+BLOCK_ROWS_N(3)
+BLOCK_ROWS_N(4)
+BLOCK_ROWS_N(5)
+BLOCK_ROWS_N(6)
+static void block_rows(const float *x, int din, const float *tf, int nr, float *acc /* [nr][16] */) {
+    switch (nr) {
+    case 6: block_rows_6(x, din, tf, acc); break;
+    case 5: block_rows_5(x, din, tf, acc); break;
+    case 4: block_rows_4(x, din, tf, acc); break;
+    case 3: block_rows_3(x, din, tf, acc); break;
+    case 2: block_rows_2(x, din, tf, acc); break;
+    default: block_rows_1(x, din, tf, acc); break;
+    }
+}
+#else
+static void block_rows(const float *x, int din, const float *tf, int nr, float *acc) {
+    for (int r = 0; r < nr; r++)
+        for (int c = 0; c < BLK_SUB; c++) acc[r * BLK_SUB + c] = 0.0f;
+    for (int j = 0; j < din; j++)
+        for (int r = 0; r < nr; r++)
+            for (int c = 0; c < BLK_SUB; c++)
+                acc[r * BLK_SUB + c] = fmaf(x[(size_t)r * din + j], tf[(size_t)j * BLK_SUB + c], acc[r * BLK_SUB + c]);
+}
+#endif
+
+static void blocked_unit(const float *x, int din, const int8_t *q, int dout, int c0, int nc, int r0, int nr,
+                         const unsigned char *dense, const float *scale, float *y, float *tf, float *gath, int *have) {
+    /* the tile's f32 copy: sub-tile s holds columns c0 + 16 s .. + 15 (zeros past dout); kept while the
+     * thread's next unit reads the same tile */
+    if (*have != c0)
+        for (int s = 0; s < TILE / BLK_SUB; s++)
+        for (int j = 0; j < din; j++)
+            for (int c = 0; c < BLK_SUB; c++) {
+                const int cc = BLK_SUB * s + c;
+                tf[((size_t)s * din + j) * BLK_SUB + c] = cc < nc ? (float)q[(size_t)j * dout + c0 + cc] : 0.0f;
+            }
+    *have = c0;
+    int rows[BLK_CHUNK], nd = 0;
+    for (int r = r0; r < r0 + nr; r++) {
+        if (dense[r]) rows[nd++] = r;
+        else tile_row(x + (size_t)r * din, din, q, dout, c0, nc, scale, y + (size_t)r * dout);
+    }
+    for (int i = 0; i < nd; i += BLK_ROWS) {
+        const int k = nd - i < BLK_ROWS ? nd - i : BLK_ROWS;
+        /* consecutive dense rows read x in place; otherwise they are gathered */
+        const float *xr = x + (size_t)rows[i] * din;
+        int contiguous = rows[i + k - 1] - rows[i] == k - 1;
+        if (!contiguous) {
+            for (int z = 0; z < k; z++) memcpy(gath + (size_t)z * din, x + (size_t)rows[i + z] * din, sizeof(float) * din);
+            xr = gath;
+        }
+        for (int s = 0; s < TILE / BLK_SUB; s++) {
+            const int cs = BLK_SUB * s;
+            if (cs >= nc) break;
+            float acc[BLK_ROWS * BLK_SUB];
+            block_rows(xr, din, tf + (size_t)s * din * BLK_SUB, k, acc);
+            for (int z = 0; z < k; z++)
+                for (int c = 0; c < BLK_SUB && cs + c < nc; c++)
+                    y[(size_t)rows[i + z] * dout + c0 + cs + c] = acc[z * BLK_SUB + c] * scale[c0 + cs + c];
+        }
+    }
+}
+
+void orc_q8_matmul_blocked(const float *x, int m, int din, const int8_t *q, const float *scale, int dout, float *y,
+                           int threads) {
+    unsigned char *dense = (unsigned char *)malloc((size_t)m);
+    for (int r = 0; r < m; r++) {
+        int nnz = 0;
+        for (int j = 0; j < din; j++) nnz += x[(size_t)r * din + j] != 0.0f;
+        dense[r] = (double)nnz > 0.1 * din; /* gpu/int8/block.rs:35 (BLOCK_EVENT_MAX) */
+    }
+    const int tiles = (dout + TILE - 1) / TILE, nch = (m + BLK_CHUNK - 1) / BLK_CHUNK;
+    const long units = (long)tiles * nch;
+    if (threads < 1) threads = 1;
+#pragma omp parallel num_threads(threads)
+    {
+        float *tf = (float *)malloc(sizeof(float) * (size_t)din * TILE);
+        float *gath = (float *)malloc(sizeof(float) * (size_t)din * BLK_ROWS);
+        int have = -1;
+#pragma omp for schedule(static)
+        for (long u = 0; u < units; u++) {
+            const int t = (int)(u / nch), ch = (int)(u % nch);
+            const int c0 = t * TILE, nc = dout - c0 < TILE ? dout - c0 : TILE;
+            const int r0 = ch * BLK_CHUNK, nr = m - r0 < BLK_CHUNK ? m - r0 : BLK_CHUNK;
+            blocked_unit(x, din, q, dout, c0, nc, r0, nr, dense, scale, y, tf, gath, &have);
+        }
+        free(tf);
+        free(gath);
+    }
+    free(dense);
+}
+
+/* y = x W with the reference's CPU int8 product: the blocked form from 6 rows (BLOCK_MIN,
+ * gpu/int8/block.rs:33), else the per-row form. Same bits either way. */
+void orc_q8_matmul_ref(const float *x, int m, int din, const int8_t *q, const float *scale, int dout, float *y,
+                       int threads) {
+    if (m >= 6) orc_q8_matmul_blocked(x, m, din, q, scale, dout, y, threads);
+    else orc_q8_matmul_rows(x, m, din, q, scale, dout, y, threads);
 }
 
 void orc_quant_planes(const float *x, int m, int k, int planes, int8_t *xq, int32_t *xexp) {

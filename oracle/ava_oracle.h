@@ -37,6 +37,13 @@ void orc_quantize_int8(const float *w, int din, int dout, int8_t *q, float *scal
  * `threads` OpenMP threads; each output is written by one thread, so any count gives the same bits. */
 void orc_q8_matmul_ref(const float *x, int m, int din, const int8_t *q, const float *scale,
                        int dout, float *y, int threads);
+/* The two forms orc_q8_matmul_ref chooses between (from 6 rows the blocked one, gpu/int8/block.rs:
+ * 6 x 16 register blocks over an f32 copy of each 64-column tile, sparse rows as event sums): the same
+ * bits as each other. */
+void orc_q8_matmul_rows(const float *x, int m, int din, const int8_t *q, const float *scale, int dout, float *y,
+                        int threads);
+void orc_q8_matmul_blocked(const float *x, int m, int din, const int8_t *q, const float *scale, int dout,
+                           float *y, int threads);
 
 /* The build's split-plane activation quantizer (no reference counterpart). For each row:
  * e = the smallest exponent with max|x| * 2^-e < 127.5 (e = 0 for an all-zero row);

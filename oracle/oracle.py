@@ -36,6 +36,8 @@ def lib():
         L = C.CDLL(_LIB)
         L.orc_quantize_int8.argtypes = [f32p, C.c_int, C.c_int, i8p, f32p]
         L.orc_q8_matmul_ref.argtypes = [f32p, C.c_int, C.c_int, i8p, f32p, C.c_int, f32p, C.c_int]
+        L.orc_q8_matmul_rows.argtypes = L.orc_q8_matmul_ref.argtypes
+        L.orc_q8_matmul_blocked.argtypes = L.orc_q8_matmul_ref.argtypes
         L.orc_quant_planes.argtypes = [f32p, C.c_int, C.c_int, C.c_int, i8p, i32p]
         L.orc_q8_acc.argtypes = [i8p, C.c_int, C.c_int, i8p, C.c_int, i32p, C.c_int]
         L.orc_q8_combine.argtypes = [i32p, C.c_int, C.c_void_p, C.c_int, f32p, C.c_int, f32p]
@@ -97,13 +99,16 @@ def quantize_int8(w):
     return q, s
 
 
-def q8_matmul_ref(x, q, scale, threads=1):
-    """gpu/int8.rs:301-331: W8A32, f32 fma chain in j order, times the column scale."""
+def q8_matmul_ref(x, q, scale, threads=1, form="auto"):
+    """gpu/int8.rs:301-331: W8A32, f32 fma chain in j order, times the column scale. form: "rows" (the
+    per-row kernel), "blocked" (gpu/int8/block.rs's 6 x 16 register blocks) or "auto" (blocked from 6
+    rows, as the reference chooses); the same bits every way."""
     x = _c(x, np.float32)
     m, din = x.shape
     dout = q.shape[1]
     y = np.empty((m, dout), np.float32)
-    lib().orc_q8_matmul_ref(x, m, din, _c(q, np.int8), _c(scale, np.float32), dout, y, threads)
+    fn = {"auto": lib().orc_q8_matmul_ref, "rows": lib().orc_q8_matmul_rows, "blocked": lib().orc_q8_matmul_blocked}[form]
+    fn(x, m, din, _c(q, np.int8), _c(scale, np.float32), dout, y, threads)
     return y
 
 

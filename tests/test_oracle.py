@@ -239,6 +239,26 @@ def test_q8_matmul_ref_near_dequantized_and_thread_invariant(din, dout, m):
         assert np.array_equal(O.q8_matmul_ref(x, q, s, threads=th).view(np.uint32), y.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,din,dout", [(6, 64, 64), (7, 200, 100), (50, 1030, 130), (97, 256, 256), (13, 4112, 70)])
+def test_q8_blocked_form_gives_the_row_form_bits(m, din, dout):
+    """gpu/int8/block.rs:15-18: the row-blocked product (6 x 16 register blocks over an f32 copy of each
+    tile, sparse rows as event sums) gives the per-row kernel's bits: dense rows in runs and apart, sparse
+    rows (under a tenth non-zero), zero and -0 inputs, a partial tile and rows past a multiple of 6."""
+    rng = np.random.default_rng(m + din + dout)
+    w = (rng.standard_normal((din, dout)) * 0.05).astype(F)
+    x = rng.standard_normal((m, din)).astype(F)
+    x[:, ::3] = 0.0
+    x[:, 1::7] = -0.0
+    for r in range(1, m, 4):  # every fourth row sparse
+        keep = rng.random(din) < 0.05
+        x[r] = np.where(keep, x[r], F(0.0))
+    q, s = O.quantize_int8(w)
+    rows = O.q8_matmul_ref(x, q, s, threads=3, form="rows")
+    blocked = O.q8_matmul_ref(x, q, s, threads=3, form="blocked")
+    assert np.array_equal(rows.view(np.uint32), blocked.view(np.uint32))
+    assert np.array_equal(O.q8_matmul_ref(x, q, s, threads=1).view(np.uint32), rows.view(np.uint32))
+
+
 def test_q8_integer_inputs_are_exact():
     """Spike inputs (-2..2): the f32 chain of integer products is exact (|acc| < 2^24), so the product is
     float(exact integer sum) * scale, the identity the i8 MFMA spike path relies on."""
