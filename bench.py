@@ -242,13 +242,14 @@ class Gemm:
     def cpu_baseline(self):
         from oracle import oracle as O
 
-        rows = 48
         rng = np.random.default_rng(3)
-        x = rng.standard_normal((rows, self.k)).astype(np.float32)
+        x = rng.standard_normal((1024, self.k)).astype(np.float32)
         q, s = O.quantize_int8((rng.standard_normal((self.k, self.n)) * 0.02).astype(np.float32))
         th = cpu_threads()
-        t0 = time.perf_counter()
-        O.q8_matmul_ref(x, q, s, threads=th)
+        rows, t0 = 0, time.perf_counter()
+        while rows == 0 or time.perf_counter() - t0 < 3.0:  # calls of 1024 rows for about 3 s
+            O.q8_matmul_ref(x, q, s, threads=th)
+            rows += x.shape[0]
         dt = time.perf_counter() - t0
         return {"value": rows / dt, "unit": "rows/s", "cores": th, "kind": "port",
                 "sample": f"oracle W8A32 product (int8.rs:301-331 fma chain, in int8/block.rs's 6 x 16 register blocks), "
