@@ -53,6 +53,24 @@ __device__ __forceinline__ float sum_cols(float v) {
     return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
+// v[0..19] summed over the four 16-lane groups of the wave; lane group g gets the sums of
+// v[5 g .. 5 g + 4] in w. Each lane swap exchanges a pair of values between groups, so a stage adds
+// two values per swap: v_permlane32_swap pairs v[q] with v[q + 10] across the wave's halves, then
+// v_permlane16_swap pairs u[q] with u[q + 5] across the 16-lane groups of each half.
+__device__ __forceinline__ void rs_rows(const float (&v)[20], float (&w)[5]) {
+    float u[10];
+#pragma unroll
+    for (int q = 0; q < 10; q++) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[q]), __float_as_uint(v[q + 10]), false, false);
+        u[q] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int q = 0; q < 5; q++) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[q]), __float_as_uint(u[q + 5]), false, false);
+        w[q] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+}
+
 struct MemBwdArgs {
     const float *q, *k, *e, *v, *la, *b, *F0, *S0, *dy, *dFT, *dST;
     float *dq, *dk, *de, *dv, *dla, *db, *dF0, *dS0, *ck, *part;
@@ -289,20 +307,26 @@ __global__ __launch_bounds__(256, 2) void mem_bwd_kernel(MemBwdArgs p) {
                         pde[ri] = fmaf(cdr[cj], Fa[m], pde[ri]);
                         dF[m] = fmaf(e4[ri], cdr[cj], dF[m]);
                     }
+                {
+                    // the 20 row partials (quantity z, row ri: index 4 z + ri) summed over the wave's four
+                    // lane groups by a reduce-scatter: lane group g ends with the sums of 5 g .. 5 g + 4
+                    float v[20];
 #pragma unroll
-                for (int ri = 0; ri < 4; ri++) {
-                    pdq[ri] = sum_cols(pdq[ri]);
-                    pal[ri] = sum_cols(pal[ri]);
-                    psv[ri] = sum_cols(psv[ri]);
-                    psr[ri] = sum_cols(psr[ri]);
-                    pde[ri] = sum_cols(pde[ri]);
-                }
-                if ((lane >> 4) == 0) {
-                    *reinterpret_cast<f32x4 *>(&red[s][wave][0][i0]) = f32x4{pdq[0], pdq[1], pdq[2], pdq[3]};
-                    *reinterpret_cast<f32x4 *>(&red[s][wave][1][i0]) = f32x4{pal[0], pal[1], pal[2], pal[3]};
-                    *reinterpret_cast<f32x4 *>(&red[s][wave][2][i0]) = f32x4{psv[0], psv[1], psv[2], psv[3]};
-                    *reinterpret_cast<f32x4 *>(&red[s][wave][3][i0]) = f32x4{psr[0], psr[1], psr[2], psr[3]};
-                    *reinterpret_cast<f32x4 *>(&red[s][wave][4][i0]) = f32x4{pde[0], pde[1], pde[2], pde[3]};
+                    for (int ri = 0; ri < 4; ri++) {
+                        v[ri] = pdq[ri];
+                        v[4 + ri] = pal[ri];
+                        v[8 + ri] = psv[ri];
+                        v[12 + ri] = psr[ri];
+                        v[16 + ri] = pde[ri];
+                    }
+                    float w[5];
+                    rs_rows(v, w);
+                    const int g = lane >> 4;
+#pragma unroll
+                    for (int z = 0; z < 5; z++) {
+                        const int k = 5 * g + z;
+                        red[s][wave][k >> 2][i0 + (k & 3)] = w[z];
+                    }
                 }
                 if ((lane & 15) == 0) {
                     float *dvp = p.dv + hb + (size_t)(t0 + s) * HS + j0;
