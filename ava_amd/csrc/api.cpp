@@ -41,6 +41,18 @@ int lds_opt_in(const void *fn, size_t bytes) {
     return AVA_OK;
 }
 
+int device_cus(int *cus) {
+    static std::mutex mu;
+    static int n[64] = {};
+    int dev = 0;
+    AVA_HIP(hipGetDevice(&dev));
+    AVA_REQUIRE(dev >= 0 && dev < 64, AVA_ERR_UNSUPPORTED, "device %d (0..63)", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!n[dev]) AVA_HIP(hipDeviceGetAttribute(&n[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    *cus = n[dev];
+    return AVA_OK;
+}
+
 }  // namespace ava
 
 extern "C" const char *ava_last_error(void) { return g_err; }

@@ -53,6 +53,9 @@ int fail(int code, const char *fmt, ...);
 // under a lock (launches may come from several host threads).
 int lds_opt_in(const void *fn, size_t bytes);
 
+// The current device's compute units (looked up once per device).
+int device_cus(int *cus);
+
 }  // namespace ava
 
 #define AVA_REQUIRE(cond, code, ...)                     \

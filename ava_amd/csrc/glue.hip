@@ -132,13 +132,30 @@ __global__ __launch_bounds__(256) void rms_planes_kernel(const float *__restrict
 
 // ------------------------------------------------------------------ f32 gate projections
 
-// G [n][nc] = h [n][d] . W [d][nc] in f32 (the reference keeps the gate projections f32:
-// gpu/arch.rs:1914-1936), on the fp32 MFMA (v_mfma_f32_32x32x2_f32). Block = 128 rows x NC columns
-// (NC = nc rounded up to 32, <= 128); wave w owns rows 32w..32w+31; K in steps of 32 through LDS
-// (h tile row-major, W tile row-major, both padded), each step 16 MFMA k-substeps per column block,
-// the next step's tiles in flight meanwhile.
+// G [n][nc] = h [n][d] . W [d][nc] at f32 accuracy (the reference keeps the gate projections f32:
+// gpu/arch.rs:1914-1936) on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16): every operand value is
+// split into three bf16 terms, x = t0 + t1 + t2 (each term the rest rounded again), and the products
+// a_i b_j with i + j < 3 are kept, which leaves about 2^-24 of |a b| per product as an f32 product
+// does; the leading product t0 t0 and the five cross products accumulate apart (f32) and are added at
+// the end. Six bf16 products per 16 k cost a third of the eight f32 ones (v_mfma_f32_32x32x2_f32) they
+// replace. Block = 128 rows x NC columns (NC = nc rounded up to 32, <= 128); wave w owns rows
+// 32w..32w+31; K in steps of 32 through LDS, where each operand is held as its three term planes with
+// k contiguous (a 16-byte fragment read per lane and term); the next step's tiles are in flight meanwhile.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-constexpr int GR = 128, GK = 32;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int GR = 128, GK = 32, GKP = GK + 8;  // GKP: bf16 per LDS row (80 bytes: conflict-free fragments)
+__device__ __forceinline__ void split3(const float (&x)[8], bf16x8 (&t)[3]) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        float r = x[e];
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const __bf16 o = (__bf16)r;
+            t[i][e] = o;
+            r = r - (float)o;
+        }
+    }
+}
 // The K loop and stores of gate_mfma_kernel for the 128-row block at r0. The block's rows come from
 // h, or, with NORM, from x normed as they are staged: h = (x * s_inv[row]) * gain[k], the two
 // roundings of row_rms_planes, so G gets the same bits either way.
@@ -146,61 +163,91 @@ template <int NCB, bool NORM>
 __device__ __forceinline__ void gate_block(const float *__restrict__ h, int n, int d, const float *__restrict__ w,
                                            int nc, float *__restrict__ g, int r0, const float *s_inv,
                                            const float *__restrict__ gain) {
-    __shared__ float sh[GR][GK + 1];
-    __shared__ float sw[GK][NCB * 32 + 4];
+    __shared__ __attribute__((aligned(16))) __bf16 sh[3][GR][GKP];        // h rows: k contiguous
+    __shared__ __attribute__((aligned(16))) __bf16 sw[3][NCB * 32][GKP];  // W columns: k contiguous
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int last = min(GR, n - r0) - 1;  // the block's last row (rows past n repeat it, unstored)
-    f32x16 acc[NCB];
+    f32x16 acc[NCB], crs[NCB];
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) acc[cb] = f32x16{};
-    // the next K step's tiles are loaded into registers while this one is multiplied: h 128 rows x 32
-    // floats (8 threads per row, a float4 each, HR per thread), W 32 x 32 NCB (WR floats per thread)
-    constexpr int HR = GR * GK / 4 / 256, WR = GK * NCB * 32 / 256;
-    f32x4 hr[HR], gr = {1.0f, 1.0f, 1.0f, 1.0f};
-    float wr[WR];
-    const int kk0 = (tid & 7) * 4;  // every j of a thread stages the same 4 columns of K
+    for (int cb = 0; cb < NCB; cb++) {
+        acc[cb] = f32x16{};
+        crs[cb] = f32x16{};
+    }
+    // staging items of 8 consecutive k: h (row, k group) 128 x 4, W (column, k group) NCB 32 x 4
+    constexpr int HI = GR * (GK / 8) / 256, WI = (NCB * 32 * (GK / 8) + 255) / 256;
+    float hv[HI][8], wv[WI][8];
+    f32x4 gr[HI][2];
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < HR; j++) {
-            const int i = tid + j * 256, rr = min(i >> 3, last);
-            hr[j] = *reinterpret_cast<const f32x4 *>(h + (size_t)(r0 + rr) * d + k0 + kk0);
-        }
-        if (NORM) gr = *reinterpret_cast<const f32x4 *>(gain + k0 + kk0);
+        for (int j = 0; j < HI; j++) {
+            const int it = tid + j * 256, rr = min(it >> 2, last), kk = k0 + (it & 3) * 8;
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(h + (size_t)(r0 + rr) * d + kk);
+            const f32x4 u0 = src[0], u1 = src[1];
 #pragma unroll
-        for (int j = 0; j < WR; j++) {
-            const int i = tid + j * 256, kk = i / (NCB * 32), cc = i % (NCB * 32);
-            wr[j] = cc < nc ? w[(size_t)(k0 + kk) * nc + cc] : 0.0f;
+            for (int e = 0; e < 4; e++) {
+                hv[j][e] = u0[e];
+                hv[j][4 + e] = u1[e];
+            }
+            if (NORM) {
+                gr[j][0] = reinterpret_cast<const f32x4 *>(gain + kk)[0];
+                gr[j][1] = reinterpret_cast<const f32x4 *>(gain + kk)[1];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < WI; j++) {
+            const int it = tid + j * 256, cc = it % (NCB * 32), kk = k0 + (it / (NCB * 32)) * 8;
+            const bool on = it < NCB * 32 * (GK / 8) && cc < nc;
+#pragma unroll
+            for (int e = 0; e < 8; e++) wv[j][e] = on ? w[(size_t)(kk + e) * nc + cc] : 0.0f;
         }
     };
     fetch(0);
     for (int k0 = 0; k0 < d; k0 += GK) {
         __syncthreads();  // the previous step's tiles are read
 #pragma unroll
-        for (int j = 0; j < HR; j++) {
-            const int i = tid + j * 256, rr = i >> 3;
-            if (NORM) {
-                const float inv = s_inv[min(rr, last)];
+        for (int j = 0; j < HI; j++) {
+            const int it = tid + j * 256, rr = it >> 2, kg = (it & 3) * 8;
+            float x[8];
 #pragma unroll
-                for (int z = 0; z < 4; z++) sh[rr][kk0 + z] = (hr[j][z] * inv) * gr[z];
-            } else {
-#pragma unroll
-                for (int z = 0; z < 4; z++) sh[rr][kk0 + z] = hr[j][z];
+            for (int e = 0; e < 8; e++) {
+                x[e] = hv[j][e];
+                if (NORM) x[e] = (x[e] * s_inv[min(rr, last)]) * gr[j][e >> 2][e & 3];
             }
+            bf16x8 t[3];
+            split3(x, t);
+#pragma unroll
+            for (int i = 0; i < 3; i++) *reinterpret_cast<bf16x8 *>(&sh[i][rr][kg]) = t[i];
         }
 #pragma unroll
-        for (int j = 0; j < WR; j++) {
-            const int i = tid + j * 256, kk = i / (NCB * 32), cc = i % (NCB * 32);
-            sw[kk][cc] = wr[j];
+        for (int j = 0; j < WI; j++) {
+            const int it = tid + j * 256;
+            if (it < NCB * 32 * (GK / 8)) {
+                const int cc = it % (NCB * 32), kg = (it / (NCB * 32)) * 8;
+                bf16x8 t[3];
+                split3(wv[j], t);
+#pragma unroll
+                for (int i = 0; i < 3; i++) *reinterpret_cast<bf16x8 *>(&sw[i][cc][kg]) = t[i];
+            }
         }
         if (k0 + GK < d) fetch(k0 + GK);
         __syncthreads();
 #pragma unroll
-        for (int ks = 0; ks < GK; ks += 2) {
-            const float a = sh[wave * 32 + (lane & 31)][ks + (lane >> 5)];
+        for (int ks = 0; ks < GK; ks += 16) {
+            const int kf = ks + 8 * (lane >> 5);
+            bf16x8 a[3];
+#pragma unroll
+            for (int i = 0; i < 3; i++) a[i] = *reinterpret_cast<const bf16x8 *>(&sh[i][wave * 32 + (lane & 31)][kf]);
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
-                const float b = sw[ks + (lane >> 5)][cb * 32 + (lane & 31)];
-                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[cb], 0, 0, 0);
+                bf16x8 b[3];
+#pragma unroll
+                for (int i = 0; i < 3; i++) b[i] = *reinterpret_cast<const bf16x8 *>(&sw[i][cb * 32 + (lane & 31)][kf]);
+                acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc[cb], 0, 0, 0);
+                crs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], crs[cb], 0, 0, 0);
+                crs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], crs[cb], 0, 0, 0);
+                crs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], crs[cb], 0, 0, 0);
+                crs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], crs[cb], 0, 0, 0);
+                crs[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], crs[cb], 0, 0, 0);
             }
         }
     }
@@ -212,7 +259,7 @@ __device__ __forceinline__ void gate_block(const float *__restrict__ h, int n, i
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int row = r0 + wave * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            if (row < n) g[(size_t)row * nc + col] = acc[cb][r];
+            if (row < n) g[(size_t)row * nc + col] = acc[cb][r] + crs[cb][r];
         }
     }
 }
@@ -240,22 +287,27 @@ __global__ __launch_bounds__(256, 2) void rms_gate_mfma_kernel(const float *__re
     __shared__ float s_inv[GR];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = blockIdx.x * GR, w0 = r0 + wave * 32;
-    f32x4 cur[NV], nxt[NV];
+    // the next two rows' loads in flight while a row is normed
+    f32x4 cur[NV], nx1[NV], nx2[NV];
     auto load_row = [&](int row, f32x4 (&v)[NV]) {
         const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + (size_t)min(row, n - 1) * d);
 #pragma unroll
         for (int i = 0; i < NV; i++) v[i] = xr[i * 64 + lane];
     };
     load_row(w0, cur);
+    load_row(w0 + 1, nx1);
     for (int j = 0; j < 32; j++) {
-        if (j + 1 < 32) load_row(w0 + j + 1, nxt);
+        if (j + 2 < 32) load_row(w0 + j + 2, nx2);
         if (w0 + j < n) {  // wave-uniform
             const float inv =
                 row_rms_planes<P, NV>(cur, lane, d, gain, (size_t)n, (size_t)(w0 + j), xq, xexp, ldq, nullptr);
             if (lane == 0) s_inv[wave * 32 + j] = inv;
         }
 #pragma unroll
-        for (int i = 0; i < NV; i++) cur[i] = nxt[i];
+        for (int i = 0; i < NV; i++) {
+            cur[i] = nx1[i];
+            nx1[i] = nx2[i];
+        }
     }
     __syncthreads();  // every row's 1 / rms is in s_inv (gate_block's first barrier follows too)
     gate_block<NCB, true>(x, n, d, w, nc, g, r0, s_inv, gain);

@@ -765,19 +765,10 @@ int launch_small(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, c
 // Row blocks per tile group (tile_origin): a weight column tile is fetched past L2 once per 8 row blocks.
 constexpr int TILE_GROUP = 8;
 
-// Workgroups for the persistent product: one per CU of the current device (looked up once per device).
+// Workgroups for the persistent product: one per CU of the current device.
 int gemm_grid(int tiles, int *grid) {
-    static std::mutex mu;
-    static int cus[64] = {};
-    int dev = 0;
-    AVA_HIP(hipGetDevice(&dev));
-    AVA_REQUIRE(dev >= 0 && dev < 64, AVA_ERR_UNSUPPORTED, "q8 product: device %d (0..63)", dev);
     int c = 0;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        if (!cus[dev]) AVA_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));
-        c = cus[dev];
-    }
+    if (int r = ava::device_cus(&c)) return r;
     *grid = std::max(1, std::min(tiles, c));
     return AVA_OK;
 }
