@@ -513,14 +513,66 @@ struct SmallCfg {
     static constexpr size_t DBL = (size_t)NW * FN * 16 * 64 * 8;             // doubles, other epilogues
 };
 
+// The values the few-rows epilogue reads from memory besides the accumulators: each column's scale (and
+// colv, and for EPI_LIF the channel's four parameters), each finished row's exponent and, for EPI_ADD,
+// the prior y, for EPI_LIF the membrane state. They are loaded at the start of the kernel, so their
+// latency passes during the K loop instead of after it. Wave w finishes rows r = w + NW q of the block
+// (q < 16 / NW) in columns n0 + 32 j + (lane & 31); rows past m and columns past n load the last ones
+// (in bounds, unused).
+template <int EPI, int FN, int NW>
+struct SmallPre {
+    static constexpr int Q = 16 / NW;
+    float sc[FN], cv[FN];
+    int ex[Q];
+    float y[FN][Q];                            // EPI_ADD: y; EPI_LIF: the membrane v
+    float ls[EPI == EPI_LIF ? FN : 1][Q];      // EPI_LIF: the last spike
+    float la[EPI == EPI_LIF ? FN : 1][Q];      // EPI_LIF: the trace
+    float lp[EPI == EPI_LIF ? FN : 1][4];      // EPI_LIF: beta, theta0, rho, gain
+};
+template <int P, int EPI, int FN, int NW>
+__device__ __forceinline__ void small_prefetch(SmallPre<EPI, FN, NW> &pre, int m, int n, int m0, int n0,
+                                               const int32_t *__restrict__ xexp, const float *__restrict__ scale,
+                                               const EpiArgs &ep, int lane, int wave) {
+    constexpr int Q = 16 / NW;
+    if constexpr (EPI == EPI_ACC) return;
+    const int rsub = (lane >> 5) * 4;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int r = wave + NW * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
+        pre.ex[q] = (xexp ? xexp[row] : 0) - 7 * (P - 1);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int col = min(n0 + j * 32 + (lane & 31), n - 1);
+        pre.sc[j] = scale[col];
+        pre.cv[j] = (EPI == EPI_MUL || (EPI == EPI_LIF && ep.colv)) ? ep.colv[col] : 1.0f;
+        if constexpr (EPI == EPI_LIF) {
+            const ava::LifEpi &L = ep.lif;
+#pragma unroll
+            for (int z = 0; z < 4; z++) pre.lp[j][z] = L.ps[z * n + col];
+        }
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            const int r = wave + NW * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
+            if constexpr (EPI == EPI_ADD) pre.y[j][q] = reinterpret_cast<const float *>(ep.y)[(size_t)row * ep.ldy + col];
+            if constexpr (EPI == EPI_LIF) {
+                const size_t o = (size_t)row * n + col;
+                pre.y[j][q] = ep.lif.v[o];
+                pre.ls[j][q] = ep.lif.s[o];
+                pre.la[j][q] = ep.lif.a[o];
+            }
+        }
+    }
+}
+
 // The few-rows products' epilogue: wave w's P-plane accumulators of the 32 x 32 FN block combine
 // exactly in double; the NW waves' partials add in LDS (smem, 8 NW FN KB; int32 planes for EPI_ACC);
 // then one rounding and the epilogue kind, as the tiled kernels' epilogue. Wave w finishes the
 // accumulator rows r = w + NW q.
 template <int P, int EPI, int FN, int NW>
 __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_t *smem, int m, int n, int m0, int n0,
-                                               const int32_t *__restrict__ xexp, const float *__restrict__ scale,
-                                               const EpiArgs &ep, int lane, int wave) {
+                                               const SmallPre<EPI, FN, NW> &pre, const EpiArgs &ep, int lane,
+                                               int wave) {
     const int rsub = (lane >> 5) * 4;
     if (EPI == EPI_ACC) {
         int *si = reinterpret_cast<int *>(smem);  // [wave][p][j][16][64]
@@ -565,24 +617,12 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
     for (int j = 0; j < FN; j++) {
         const int col = n0 + j * 32 + (lane & 31);
         if (col >= n) continue;
-        const float sc = scale[col];
-        const float cv = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+        const float sc = pre.sc[j];
         if constexpr (EPI == EPI_LIF) {
             // cur (times colv: the lif-scale factor) into one step of the channel's scan, as
-            // lif_scan_kernel's loop body; the 4 rows' state loads are all issued before any use
+            // lif_scan_kernel's loop body
             const ava::LifEpi &L = ep.lif;
-            const float bt = L.ps[col], th0 = L.ps[n + col], rho = L.ps[2 * n + col], gain = L.ps[3 * n + col];
-            const float cf = ep.colv ? ep.colv[col] : 1.0f;
-            float sv[16 / NW], ss[16 / NW], sa[16 / NW];
-#pragma unroll
-            for (int q = 0; q < 16 / NW; q++) {
-                const int r = wave + NW * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
-                const size_t o = (size_t)row * n + col;
-                sv[q] = L.v[o];
-                ss[q] = L.s[o];
-                sa[q] = L.a[o];
-            }
-            AVA_ISSUE_FENCE();
+            const float bt = pre.lp[j][0], th0 = pre.lp[j][1], rho = pre.lp[j][2], gain = pre.lp[j][3];
 #pragma unroll
             for (int q = 0; q < 16 / NW; q++) {
                 const int r = wave + NW * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
@@ -591,10 +631,9 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
                 double A = sd[e];
 #pragma unroll
                 for (int w = 1; w < NW; w++) A += sd[w * ws + e];
-                const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
-                float v = ldexpf((float)A, ex) * sc;
-                if (ep.colv) v = v * cf;
-                float vv = sv[q], sp = ss[q], aa = sa[q];
+                float v = ldexpf((float)A, pre.ex[q]) * sc;
+                if (ep.colv) v = v * pre.cv[j];
+                float vv = pre.y[j][q], sp = pre.ls[j][q], aa = pre.la[j][q];
                 const float thp = L.alif ? th0 + aa * gain : th0;
                 float tht = th0;
                 if (L.alif) {
@@ -611,15 +650,6 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
             }
             continue;
         }
-        float prev[16 / NW] = {};
-        if (EPI == EPI_ADD) {  // the rows' loads all in flight before any add
-#pragma unroll
-            for (int q = 0; q < 16 / NW; q++) {
-                const int r = wave + NW * q, row = min(m0 + (r >> 2) * 8 + rsub + (r & 3), m - 1);
-                prev[q] = ybase[(size_t)row * ep.ldy + col];
-            }
-            AVA_ISSUE_FENCE();
-        }
 #pragma unroll
         for (int q = 0; q < 16 / NW; q++) {
             const int r = wave + NW * q, row = m0 + (r >> 2) * 8 + rsub + (r & 3);
@@ -628,10 +658,9 @@ __device__ __forceinline__ void small_epilogue(const i32x16 (&acc)[P][FN], int8_
             double A = sd[e];
 #pragma unroll
             for (int w = 1; w < NW; w++) A += sd[w * ws + e];
-            const int ex = (xexp ? xexp[row] : 0) - 7 * (P - 1);
-            float v = ldexpf((float)A, ex) * sc;
-            if (EPI == EPI_MUL) v = v * cv;
-            if (EPI == EPI_ADD) v = prev[q] + v;
+            float v = ldexpf((float)A, pre.ex[q]) * sc;
+            if (EPI == EPI_MUL) v = v * pre.cv[j];
+            if (EPI == EPI_ADD) v = pre.y[j][q] + v;
             ybase[(size_t)row * ep.ldy + col] = v;
         }
     }
@@ -688,6 +717,8 @@ __global__ __launch_bounds__(64 * NW) void q8_small_kernel(const int8_t *__restr
         for (int i = 0; i < LPS; i++) dma16(src[i] + off, dst + i * 1024);
     };
 
+    SmallPre<EPI, FN, NW> pre;
+    small_prefetch<P, EPI, FN, NW>(pre, m, n, m0, n0, xexp, scale, ep, lane, wave);
     i32x16 acc[P][FN];
 #pragma unroll
     for (int p = 0; p < P; p++)
@@ -725,7 +756,7 @@ __global__ __launch_bounds__(64 * NW) void q8_small_kernel(const int8_t *__restr
 #endif
     }
     __syncthreads();  // every wave is done with its buffers
-    small_epilogue<P, EPI, FN, NW>(acc, smem, m, n, m0, n0, xexp, scale, ep, lane, wave);
+    small_epilogue<P, EPI, FN, NW>(acc, smem, m, n, m0, n0, pre, ep, lane, wave);
 }
 
 template <int P, int EPI, int FN, int D, int NW>
