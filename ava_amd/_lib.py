@@ -91,6 +91,7 @@ def lib():
         "ava_mem_chunk": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, f32, vp, vp, vp, vp],
         "ava_delta_chunk": [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, sz, vp],
         "ava_lif_scan_bwd": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, f32, i32] + [vp] * 10,
+        "ava_lif_scan_bwd_segments": [vp, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, f32, i32] + [vp] * 10 + [sz, vp],
         "ava_kwta_relu2_bwd": [vp, vp, i32, i32, vp, vp, vp],
         "ava_mem_scan_bwd": [vp] * 6 + [i32] * 4 + [f32, f32] + [vp] * 14 + [sz, vp],
         "ava_dense_back": [vp] * 6 + [i32] * 4 + [C.c_longlong, vp, sz, vp],
@@ -120,6 +121,8 @@ def lib():
     L.ava_mem_scan_bwd_workspace.restype = sz
     L.ava_delta_chunk_workspace.argtypes = [i32, i32]
     L.ava_delta_chunk_workspace.restype = sz
+    L.ava_lif_scan_bwd_segments_workspace.argtypes = [i32, i32, i32]
+    L.ava_lif_scan_bwd_segments_workspace.restype = sz
     L.ava_dense_back_part_floats.argtypes = [C.c_longlong, i32]
     L.ava_dense_back_part_floats.restype = sz
     L.ava_train_free.argtypes = [vp]

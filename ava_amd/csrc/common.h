@@ -177,8 +177,22 @@ __device__ __forceinline__ float lif_spike(float v, float th, int levels, int is
 }
 
 // lif.hip / kwta.hip / mem.hip
+// park (nullable): the state (v, s, a) at the start of every LIF_SEG_STEPS-step segment, as
+// park [segment][3][B D] (lif_park_floats), for lif_scan_bwd_seg.
 int lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
-             int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st);
+             int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st, float *park = nullptr);
+// The LIF backward in parallel segments of LIF_SEG_STEPS steps (lif_bwd.hip), for few (stream, channel)
+// chains; ws holds lif_bwd_seg_floats(B, T, D) floats; park (nullable) the forward's parked states.
+constexpr int LIF_SEG_STEPS = 32;
+inline size_t lif_park_floats(int B, int T, int D) {
+    return (size_t)((T + LIF_SEG_STEPS - 1) / LIF_SEG_STEPS) * 3 * (size_t)B * D;
+}
+size_t lif_bwd_seg_floats(int B, int T, int D);
+int lif_scan_bwd_seg(const float *cur, int B, int T, int D, const float *ps, const float *v0, const float *s0,
+                     const float *a0, int levels, int is_signed, int alif, float slope, int reset_grad,
+                     const float *g_spk, const float *g_vT, const float *g_aT, float *dI, float *dv0, float *da0,
+                     float *dbeta, float *drho, float *dgain, float *ws, size_t ws_floats, const float *park,
+                     hipStream_t st);
 int kwta_planes(const float *u, int n, int h, int k, int relu2, int planes, int8_t *xq, int32_t *xexp, int ldq,
                 float *kth, hipStream_t st);
 int mem_scan_strided(const float *q, const float *k, const float *e, const float *v, const float *la, const float *b,

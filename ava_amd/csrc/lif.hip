@@ -62,11 +62,14 @@ __device__ __forceinline__ void store_spikes(int8_t *dst, const float (&s)[VEC])
     }
 }
 
+// park (VEC = 1 only; nullable): the state (v, s, a) at the start of every ava::LIF_SEG_STEPS-step
+// segment, park [segment][3][B D], for the backward in parallel segments.
 template <int VEC, int PF, int LEVELS, bool SIGNED, bool ALIF>
 __global__ __launch_bounds__(256) void lif_scan_kernel(const float *__restrict__ cur, int B, int T, int D,
                                                        const float *__restrict__ ps, float *__restrict__ v,
                                                        float *__restrict__ s, float *__restrict__ a,
-                                                       int8_t *__restrict__ spikes, float *__restrict__ th_out) {
+                                                       int8_t *__restrict__ spikes, float *__restrict__ th_out,
+                                                       float *__restrict__ park) {
     typedef typename Vec<VEC>::T V;
     const int nv = D / VEC;
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -87,6 +90,17 @@ __global__ __launch_bounds__(256) void lif_scan_kernel(const float *__restrict__
         aa[i] = a[st];
         thp[i] = ALIF ? th0[i] + aa[i] * gain[i] : th0[i];
     }
+
+    const size_t chains = (size_t)B * D;
+    auto put_park = [&](int sg) {
+        if constexpr (VEC == 1) {
+            float *pk = park + (size_t)sg * 3 * chains + (size_t)b * D + c0;
+            pk[0] = vv[0];
+            pk[chains] = sp[0];
+            pk[2 * chains] = aa[0];
+        }
+    };
+    if (park) put_park(0);
 
     const V *src = reinterpret_cast<const V *>(cur + (size_t)b * T * D + c0);
     int8_t *dst = spikes + (size_t)b * T * D + c0;
@@ -123,6 +137,7 @@ __global__ __launch_bounds__(256) void lif_scan_kernel(const float *__restrict__
                     out[j] = sp[j];
                 }
                 store_spikes<VEC>(dst + (size_t)t * D, out);
+                if (park && (t + 1) % ava::LIF_SEG_STEPS == 0 && t + 1 < T) put_park((t + 1) / ava::LIF_SEG_STEPS);
             }
         }
 #pragma unroll
@@ -141,11 +156,13 @@ __global__ __launch_bounds__(256) void lif_scan_kernel(const float *__restrict__
 
 template <int VEC, int PF>
 int launch_vp(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
-              int levels, int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st) {
+              int levels, int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st,
+              float *park = nullptr) {
+    AVA_REQUIRE(!park || VEC == 1, AVA_ERR_ARG, "lif_scan: parked states need one channel per lane");
     const long threads = (long)B * (D / VEC);
     dim3 grid(ava::ceil_div(threads, 256)), block(256);
 #define AVA_LIF_GO(L, S, A) \
-    lif_scan_kernel<VEC, PF, L, S, A><<<grid, block, 0, st>>>(cur, B, T, D, ps, v, s, a, spikes, th_out)
+    lif_scan_kernel<VEC, PF, L, S, A><<<grid, block, 0, st>>>(cur, B, T, D, ps, v, s, a, spikes, th_out, park)
     if (!is_signed) {
         if (alif) AVA_LIF_GO(1, false, true);
         else AVA_LIF_GO(1, false, false);
@@ -170,11 +187,11 @@ namespace ava {
 constexpr int LIF_VEC = 1, LIF_PF = 32;
 
 int lif_scan(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a, int levels,
-             int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st) {
+             int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st, float *park) {
     AVA_REQUIRE(cur && ps && v && s && a && spikes, AVA_ERR_ARG, "lif_scan: NULL buffer");
     AVA_REQUIRE(B > 0 && T > 0 && D > 0, AVA_ERR_SHAPE, "lif_scan: B=%d T=%d D=%d", B, T, D);
     AVA_REQUIRE(levels == 1 || levels == 2, AVA_ERR_ARG, "lif_scan: levels %d (1 or 2)", levels);
-    return launch_vp<LIF_VEC, LIF_PF>(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, st);
+    return launch_vp<LIF_VEC, LIF_PF>(cur, B, T, D, ps, v, s, a, levels, is_signed, alif, spikes, th_out, st, park);
 }
 
 }  // namespace ava

@@ -47,6 +47,7 @@ struct Acts {  // one block's saved forward values
     float *inv4, *h4, *u, *kth, *a;
     int8_t *spk;
     float *ps, *omb;
+    float *lpark = nullptr;  // the LIF state at each segment start (few chains: the backward in segments)
 };
 
 }  // namespace
@@ -78,6 +79,9 @@ struct ava_trainer {
     size_t part_floats = 0;
     void *mwork = nullptr;
     size_t mwork_bytes = 0;
+    bool lif_seg = false;  // the LIF backward in parallel segments (few chains)
+    float *lws = nullptr;
+    size_t lws_floats = 0;
     float *att_part = nullptr;
     size_t att_part_floats = 0;
 
@@ -98,6 +102,12 @@ struct ava_trainer {
 namespace {
 
 int eng_nh(const ava_config &c) { return c.eng_heads > 1 ? c.eng_heads : 1; }
+
+// The LIF backward walks each (stream, channel) chain in one lane; up to this many chains (a quarter of
+// the SIMDs at B d = 16,384) and from this many steps, it runs in parallel segments instead
+// (ava::lif_scan_bwd_seg).
+constexpr size_t LIF_SEG_CHAINS = 16384;
+constexpr int LIF_SEG_MIN_T = 128;
 
 size_t block_count(const ava_config &c, int i, const std::string &nm) {
     const size_t d = c.d, nh = c.d / c.head_size, r = c.gate_rank, H = c.hidden, de = c.eng_dim;
@@ -192,6 +202,13 @@ int ensure(ava_trainer *t, int B, int T) {
     AF(t->dvec, d); AF(t->dvec2, d);
     t->mwork_bytes = ava_mem_scan_bwd_workspace((int)(B * nh), T, c.momentum != 0.0f);
     TR(alloc(t, &t->mwork, t->mwork_bytes));
+    // few LIF chains (B d): the backward in parallel segments, with its workspace
+    t->lif_seg = (size_t)B * d <= LIF_SEG_CHAINS && T >= LIF_SEG_MIN_T;
+    t->lws_floats = t->lif_seg ? ava::lif_bwd_seg_floats(B, T, (int)d) : 0;
+    if (t->lif_seg) {
+        AF(t->lws, t->lws_floats);
+        for (size_t i = 0; i < L; i++) AF(t->acts[i].lpark, ava::lif_park_floats(B, T, (int)d));
+    }
     t->N = (int)N;
     t->B = B;
     t->T = T;
@@ -243,7 +260,8 @@ int step(ava_trainer *t, const float *prm, const int32_t *ids, const int32_t *tg
         AVA_HIP(hipMemsetAsync(t->lv, 0, (size_t)B * d * 4, st));
         AVA_HIP(hipMemsetAsync(t->ls, 0, (size_t)B * d * 4, st));
         AVA_HIP(hipMemsetAsync(t->la, 0, (size_t)B * d * 4, st));
-        TR(ava_lif_scan(a.cur, B, T, d, a.ps, t->lv, t->ls, t->la, c.levels, 1, c.alif, a.spk, nullptr, st));
+        TR(ava::lif_scan(a.cur, B, T, d, a.ps, t->lv, t->ls, t->la, c.levels, 1, c.alif, a.spk, nullptr, st,
+                         t->lif_seg ? a.lpark : nullptr));
         TR(ava::train::i8_to_f32(a.spk, Nd, a.S, st));
         AVA_HIP(hipMemcpyAsync(a.x1, xin, Nd * 4, hipMemcpyDeviceToDevice, st));
         TR(gemm(hb, false, false, N, d, d, 1.0f, a.S, d, w("wout"), d, 1.0f, a.x1, d));
@@ -387,9 +405,15 @@ int step(ava_trainer *t, const float *prm, const int32_t *ids, const int32_t *tg
         TR(gemm(hb, true, false, d, d, N, 1.0f, a.S, d, t->dx, d, 0.0f, gw("wout"), d));
         TR(gemm(hb, false, true, N, d, d, 1.0f, t->dx, d, w("wout"), d, 0.0f, t->dA, d));  // dL/dspikes
         AVA_HIP(hipMemsetAsync(t->lv, 0, (size_t)B * d * 4, st));
-        TR(ava_lif_scan_bwd(a.cur, B, T, d, a.ps, t->lv, t->lv, t->lv, c.levels, 1, c.alif, t->slope, t->reset_grad,
-                            t->dA, nullptr, nullptr, t->dI, t->dv0, c.alif ? t->da0 : nullptr, t->dbsh,
-                            c.alif ? t->drsh : nullptr, c.alif ? t->dgsh : nullptr, st));
+        if (t->lif_seg)
+            TR(ava::lif_scan_bwd_seg(a.cur, B, T, d, a.ps, t->lv, t->lv, t->lv, c.levels, 1, c.alif, t->slope,
+                                     t->reset_grad, t->dA, nullptr, nullptr, t->dI, t->dv0, c.alif ? t->da0 : nullptr,
+                                     t->dbsh, c.alif ? t->drsh : nullptr, c.alif ? t->dgsh : nullptr, t->lws,
+                                     t->lws_floats, a.lpark, st));
+        else
+            TR(ava_lif_scan_bwd(a.cur, B, T, d, a.ps, t->lv, t->lv, t->lv, c.levels, 1, c.alif, t->slope,
+                                t->reset_grad, t->dA, nullptr, nullptr, t->dI, t->dv0, c.alif ? t->da0 : nullptr,
+                                t->dbsh, c.alif ? t->drsh : nullptr, c.alif ? t->dgsh : nullptr, st));
         // cur = z (1 - beta): dz = dI (1 - beta); d beta = (the scan's shares over streams) - sum_n dI z
         float *dz = t->dI;
         if (c.lif_scale) {

@@ -201,10 +201,11 @@ def delta_rule_from(q, k, v, beta, la=None, f0=None, workspace=True):
 
 
 def lif_gen_bwd(cur, ps, g_spk, init=None, g_vT=None, g_aT=None, levels=2, signed=True, alif=True, slope=1.0,
-                reset_grad=False):
+                reset_grad=False, segments=False):
     """The LIF scan's backward from the initial state init (LifState; None: zeros), ps = beta | theta |
     rho | gain [4D]. Returns dict dI [B, T, D], dv0, da0, dbeta, drho, dgain [B, D] (the parameter
-    gradients per stream: sum over dim 0)."""
+    gradients per stream: sum over dim 0). segments=True: ava_lif_scan_bwd_segments (parallel segments
+    for few chains; the same values up to the association of the sums)."""
     _need(cur, torch.float32, "lif_gen_bwd cur")
     _need(g_spk, torch.float32, "lif_gen_bwd g_spk")
     _need(ps, torch.float32, "lif_gen_bwd ps")
@@ -217,6 +218,15 @@ def lif_gen_bwd(cur, ps, g_spk, init=None, g_vT=None, g_aT=None, levels=2, signe
             _need(t, torch.float32, f"lif_gen_bwd {nm}")
     out = {n: torch.empty((B, D), dtype=torch.float32, device=dev) for n in ("dv0", "da0", "dbeta", "drho", "dgain")}
     out["dI"] = torch.empty_like(cur)
+    if segments:
+        nb = lib().ava_lif_scan_bwd_segments_workspace(B, T, D)
+        ws = torch.empty(nb // 4, dtype=torch.float32, device=dev)
+        check(lib().ava_lif_scan_bwd_segments(_p(cur), B, T, D, _p(ps), _p(v0), _p(s0), _p(a0), levels, int(signed),
+                                              int(alif), float(slope), int(reset_grad), _p(g_spk), _p(g_vT),
+                                              _p(g_aT), _p(out["dI"]), _p(out["dv0"]), _p(out["da0"]),
+                                              _p(out["dbeta"]), _p(out["drho"]), _p(out["dgain"]), _p(ws), nb,
+                                              _stream()), "ava_lif_scan_bwd_segments")
+        return out
     check(lib().ava_lif_scan_bwd(_p(cur), B, T, D, _p(ps), _p(v0), _p(s0), _p(a0), levels, int(signed), int(alif),
                                  float(slope), int(reset_grad), _p(g_spk), _p(g_vT), _p(g_aT), _p(out["dI"]),
                                  _p(out["dv0"]), _p(out["da0"]), _p(out["dbeta"]), _p(out["drho"]),

@@ -173,6 +173,21 @@ int ava_lif_scan_bwd(const float *cur, int B, int T, int D, const float *ps, con
                      const float *g_spk, const float *g_vT, const float *g_aT, float *dI, float *dv0, float *da0,
                      float *dbeta, float *drho, float *dgain, ava_stream stream);
 
+/* ava_lif_scan_bwd in parallel segments of 32 steps, for few (stream, channel) chains (B D of a few
+ * thousand, as at a training batch of 4): the forward is replayed once to park each segment's state,
+ * every (chain, segment) then walks its steps back as affine functions of what the later steps carry
+ * (the walk is linear in it given the forward), the segments' functions are applied in order, and each
+ * segment is walked again with its entering carry to write dI. The same arguments and outputs as
+ * ava_lif_scan_bwd, equal up to the association of the backward sums (ava_lif_scan_bwd's walk is the
+ * CPU's order), plus a device workspace ws of ava_lif_scan_bwd_segments_workspace(B, T, D) bytes.
+ * Replaces lifg_bwd_* (gpu/lif.cu:3222-3290) where its per-chain loop leaves the GPU idle. */
+size_t ava_lif_scan_bwd_segments_workspace(int B, int T, int D);
+int ava_lif_scan_bwd_segments(const float *cur, int B, int T, int D, const float *ps, const float *v0,
+                              const float *s0, const float *a0, int levels, int is_signed, int alif, float slope,
+                              int reset_grad, const float *g_spk, const float *g_vT, const float *g_aT, float *dI,
+                              float *dv0, float *da0, float *dbeta, float *drho, float *dgain, void *ws,
+                              size_t ws_bytes, ava_stream stream);
+
 /* The backward of relu² after kWTA: gu = (u ga) 2 where u - kth >= 0 and u > 0, else 0, for u [n][h]
  * and the row thresholds kth [n] that ava_kwta returned (h a multiple of 4). Replaces relu2_bwd
  * (gpu/lif.cu:4666-4679), whose input a = kwta_relu(u) is u on the kept units. */

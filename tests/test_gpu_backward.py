@@ -84,6 +84,49 @@ def test_lif_bwd_long():
         assert np.array_equal(gpu[k], o[k]), (k, e)
 
 
+def run_lif_seg(cur, ps, v0, s0, a0, g, gv, ga, levels, signed, alif, slope, rg):
+    from ava_amd import ops
+    st = ops.LifState(dev(v0), dev(s0), dev(a0))
+    return {k: host(v) for k, v in ops.lif_gen_bwd(dev(cur), dev(ps), dev(g), init=st, g_vT=dev(gv),
+                                                    g_aT=dev(ga) if alif else None, levels=levels, signed=signed,
+                                                    alif=alif, slope=slope, reset_grad=rg, segments=True).items()}
+
+
+@pytest.mark.parametrize("T", [1, 33, 200])
+@pytest.mark.parametrize("levels,signed", [(2, True), (1, True), (1, False)])
+@pytest.mark.parametrize("alif", [True, False])
+@pytest.mark.parametrize("rg", [False, True])
+def test_lif_bwd_segments(T, levels, signed, alif, rg):
+    """ava_lif_scan_bwd_segments against the oracle's walk (which the one-lane kernel equals bit for bit):
+    one step, a 32-step segment and a 1-step one, seven segments the last of them short. The segments'
+    affine functions associate the backward sums differently: within 2e-6 of each output's largest
+    value here."""
+    slope = 0.5 if rg else 2.0
+    x = lif_inputs(T * 11 + levels + 2 * alif + 4 * rg, 3, T, 40, levels, signed)
+    print(f"lif_bwd segments T={T} levels={levels} signed={signed} alif={alif} rg={rg}", flush=True)
+    o = O.lif_bwd(x[0], x[1], x[5], x[2], x[3], x[4], x[6], x[7] if alif else None, levels=levels, signed=signed,
+                  alif=alif, slope=slope, reset_grad=rg)
+    gpu = run_lif_seg(*x, levels, signed, alif, slope, rg)
+    for k in ("dI", "dv0", "dbeta") + (("da0", "drho", "dgain") if alif else ()):
+        e = rel(gpu[k], o[k])
+        assert e < 2e-6, (k, e)
+
+
+def test_lif_bwd_segments_long():
+    """The training step's shape (4 streams x 1024 channels, T 2048: 64 segments per chain), int2 with
+    ALIF and the reset gradient, against the oracle's walk."""
+    B, T, D = 4, 2048, 1024
+    x = lif_inputs(6, B, T, D, 2, True)
+    print(f"lif_bwd segments long B={B} T={T} D={D}", flush=True)
+    o = O.lif_bwd(x[0], x[1], x[5], x[2], x[3], x[4], x[6], x[7], levels=2, signed=True, alif=True, slope=0.5,
+                  reset_grad=True)
+    gpu = run_lif_seg(*x, 2, True, True, 0.5, True)
+    for k in ("dI", "dv0", "da0", "dbeta", "drho", "dgain"):
+        e = rel(gpu[k], o[k])
+        print(f"  {k}: rel {e:.2e}", flush=True)
+        assert e < 1e-5, (k, e)
+
+
 def test_kwta_relu2_bwd():
     from ava_amd import ops
     rng = np.random.default_rng(3)

@@ -17,9 +17,10 @@ def rel(a, b):
     return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
 
 
-# T 45 and 70 take the attention's backward over several 32-token tiles with a ragged last one
+# T 45 and 70 take the attention's backward over several 32-token tiles with a ragged last one; T 200
+# (from 128 steps, with few chains) the LIF backward in parallel segments, the last one short
 @pytest.mark.parametrize("name,B,T", [("tiny", 2, 16), ("tiny_heads", 2, 12), ("small", 1, 24), ("tiny", 1, 45),
-                                      ("tiny_heads", 1, 70)])
+                                      ("tiny_heads", 1, 70), ("tiny", 2, 200)])
 def test_train_step_matches_autograd(name, B, T):
     from ava_amd.train import Trainer
     cfg = synth.config(name)
