@@ -149,14 +149,16 @@ __device__ __forceinline__ int swz(int r, int c) {
 // rw0 + 32 i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3) and column cw0 + 32 j + (lane & 31).
 // s_exp [BM] holds each tile row's exponent less 7 (P - 1). The planes combine exactly in double
 // (sum_p acc_p 2^(7(P-1-p)): integers below 2^53, so the fma is exact) and round once to f32.
+// sc[j] and cv[j] are column (n0 + cw0 + 32 j + (lane & 31), clamped to n - 1)'s scale and colv
+// (EPI_MUL), loaded by the caller.
 // An interior tile stores (and, for EPI_ADD, loads) through a buffer resource based at its first
 // row: the lane's offset is one VGPR and each register's row offset a wave-uniform SGPR, so no
 // element forms a 64-bit address or tests a bound. Edge tiles and the int32 planes take the
 // checked path.
 template <int P, int EPI, int BM, int BN, int FM, int FN>
 __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const int *s_exp, int m, int n, int m0,
-                                         int n0, int rw0, int cw0, const float *__restrict__ scale, const EpiArgs &ep,
-                                         int lane) {
+                                         int n0, int rw0, int cw0, const float (&sc)[FN], const float (&cv)[FN],
+                                         const EpiArgs &ep, int lane) {
     const int ccol = lane & 31, rsub = (lane >> 5) * 4;
     auto value = [&](int i, int j, int r) {
         if (P == 1) return (float)acc[0][i][j][r];
@@ -187,41 +189,47 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
         const BufRes yr = buf_res(ybase + (size_t)m0 * ep.ldy, (unsigned)(BM * ep.ldy) * 4u);
         const unsigned ld4 = (unsigned)ep.ldy * 4u;
         const unsigned voff = ((unsigned)(rw0 + rsub) * (unsigned)ep.ldy + (unsigned)(n0 + cw0 + ccol)) * 4u;
-        float sc[FN], cv[FN];
+        // block b = (i, j) = (b / FN, b % FN) at a time. EPI_ADD: block b + 1's 16 prior values are
+        // loaded after block b's values are formed (in the registers its accumulators held) and before
+        // block b's stores: vmcnt counts loads and stores in issue order, so a load issued behind a
+        // block's stores is not seen done before those stores are
+        constexpr int NB = FM * FN;
+        auto row_off = [&](int i, int r) { return (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4; };
+        float prev[2][16];
+        auto load_prev = [&](int blk, float (&pv)[16]) {
+            const int i = blk / FN, j = blk % FN;
 #pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int col = n0 + cw0 + j * 32 + ccol;
-            sc[j] = scale[col];
-            cv[j] = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+            for (int r = 0; r < 16; r++) pv[r] = load_f32_nt(yr, voff + j * 128u, row_off(i, r));
+        };
+        if (EPI == EPI_ADD) {
+            load_prev(0, prev[0]);
+            AVA_ISSUE_FENCE();
         }
-        // block (i, j) at a time: its 16 prior values (EPI_ADD) are all in flight before the first add
 #pragma unroll
-        for (int i = 0; i < FM; i++) {
-            int ex[16];
+        for (int blk = 0; blk < NB; blk++) {
+            const int i = blk / FN, j = blk % FN;
+            float v[16];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
+                // the exponents of rows r = 4 g .. 4 g + 3, read when needed (fewer live registers)
                 const i32x4 e4 = *reinterpret_cast<const i32x4 *>(s_exp + rw0 + i * 32 + g * 8 + rsub);
 #pragma unroll
-                for (int z = 0; z < 4; z++) ex[g * 4 + z] = e4[z];
+                for (int z = 0; z < 4; z++) {
+                    const int r = g * 4 + z;
+                    v[r] = ldexpf(value(i, j, r), e4[z]) * sc[j];
+                    if (EPI == EPI_MUL) v[r] = v[r] * cv[j];
+                    if (EPI == EPI_ADD) v[r] = prev[blk & 1][r] + v[r];
+                }
+            }
+            if (EPI == EPI_ADD && blk + 1 < NB) {
+                AVA_ISSUE_FENCE();
+                load_prev(blk + 1, prev[(blk + 1) & 1]);
+                AVA_ISSUE_FENCE();
             }
 #pragma unroll
-            for (int j = 0; j < FN; j++) {
-                float prev[16];
-                if (EPI == EPI_ADD) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        prev[r] = load_f32_nt(yr, voff + j * 128u, (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4);
-                    AVA_ISSUE_FENCE();
-                }
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float v = ldexpf(value(i, j, r), ex[r]) * sc[j];
-                    if (EPI == EPI_MUL) v = v * cv[j];
-                    if (EPI == EPI_ADD) v = prev[r] + v;
-                    const unsigned so = (unsigned)(i * 32 + (r >> 2) * 8 + (r & 3)) * ld4;
-                    if (EPI == EPI_ADD) store_f32(yr, voff + j * 128u, so, v);
-                    else store_f32_nt(yr, voff + j * 128u, so, v);
-                }
+            for (int r = 0; r < 16; r++) {
+                if (EPI == EPI_ADD) store_f32(yr, voff + j * 128u, row_off(i, r), v[r]);
+                else store_f32_nt(yr, voff + j * 128u, row_off(i, r), v[r]);
             }
         }
         return;
@@ -242,9 +250,6 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
     for (int j = 0; j < FN; j++) {
         const int col = n0 + cw0 + j * 32 + eccol;
         const bool col_ok = col < n;
-        const int colc = col_ok ? col : n - 1;
-        const float sc = scale[colc];
-        const float cv = EPI == EPI_MUL ? ep.colv[colc] : 0.0f;
 #pragma unroll
         for (int i = 0; i < FM; i++) {
             const int rbase = rw0 + i * 32 + ersub;  // tile row of r = 0
@@ -259,8 +264,8 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int tr = rbase + (r >> 2) * 8 + (r & 3);
-                float v = ldexpf(value(i, j, r), s_exp[tr]) * sc;
-                if (EPI == EPI_MUL) v = v * cv;
+                float v = ldexpf(value(i, j, r), s_exp[tr]) * sc[j];
+                if (EPI == EPI_MUL) v = v * cv[j];
                 if (EPI == EPI_ADD) v = prev[r] + v;
                 if (col_ok) store_f32(yr, off(r), 0u, v);
             }
@@ -400,15 +405,41 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
 #pragma unroll
     for (int i = 0; i < LPW; i++) issue_one(i, 0, 0);
     int sbase = 0;  // the stage holding the tile's first step
+    // Whether the previous tile's epilogue issued at least 63 vector memory instructions after this
+    // tile's first-step loads. On gfx9 vmcnt counts loads and stores together, decrements in issue
+    // order and holds at most 63, so an instruction issued with 63 older ones outstanding waits for
+    // the oldest: the first-step loads had then landed before the last of those was issued, and the
+    // first step needs no wait (which would also wait for the epilogue's stores to reach L2).
+    static_assert(FM * FN * 16 >= 63, "an interior epilogue issues at least 63 stores per wave");
+    bool loaded = false;
+    // the row exponents through a resource of 0 bytes when there are none: its loads read 0, so the
+    // load needs no branch (a branch would make the compiler wait for the value at its join)
+    const BufRes xer = buf_res(const_cast<float *>(reinterpret_cast<const float *>(xexp)),
+                               EPI != EPI_ACC && xexp ? (unsigned)m * 4u : 0u);
     for (; idx < total; idx += grid) {
-        // the tile's row exponents: waited for with the first step's loads
-        const int ex = EPI != EPI_ACC && tid < BM && xexp ? xexp[min(m0 + tid, m - 1)] : 0;
+        // the tile's row exponents (every lane loads, lanes past BM a copy) and each lane's column
+        // scales, used by the epilogue: issued before the K loop, so the epilogue does not wait for
+        // the next tile's first-step loads issued in the last step. EPI_ADD waits for those anyway
+        // (its prior values are loaded after them) and loads its scales after the K loop, which keeps
+        // two registers free during it.
+        const int ex = __float_as_int(load_f32(xer, (unsigned)min(m0 + min(tid, BM - 1), m - 1) * 4u, 0u));
+        float sc[FN], cv[FN];
+        auto load_cols = [&]() {
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int col = min(n0 + wn * NW + j * 32 + (lane & 31), n - 1);
+                sc[j] = EPI != EPI_ACC ? scale[col] : 0.0f;
+                cv[j] = EPI == EPI_MUL ? ep.colv[col] : 0.0f;
+            }
+        };
+        if (EPI != EPI_ADD) load_cols();
         i32x16 acc[P][FM][FN];
         int st = sbase;
         auto step = [&](auto first, int kt) {
             constexpr bool FIRST = decltype(first)::value;
             st = (sbase + kt) & 1;
-            wait_vm<0>();  // this wave's loads of step kt (and the previous tile's stores) are done
+            if (FIRST && loaded) wait_vm<63>();  // holds by itself: see `loaded`
+            else wait_vm<0>();  // this wave's loads of step kt (and the previous tile's stores) are done
             __builtin_amdgcn_s_barrier();  // every wave's are; every wave is done with the other stage
             int knext = kt + 1;
             if (kt + 1 == KT) {
@@ -477,7 +508,9 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
             lgkm_wait0();
             __builtin_amdgcn_s_barrier();
         }
-        epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, scale, ep, lane);
+        if (EPI == EPI_ADD) load_cols();
+        epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, sc, cv, ep, lane);
+        loaded = EPI != EPI_ACC && m0 + BM <= m && n0 + BN <= n;  // the interior path ran
         m0 = mt * BM;  // the next tile (tile_origin ran at the last step)
         n0 = nt * BN;
         sbase = st ^ 1;
