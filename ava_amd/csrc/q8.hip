@@ -147,25 +147,58 @@ __device__ __forceinline__ int swz(int r, int c) {
 // The product's epilogue for one wave's FM x FN blocks of 32 x 32 outputs at tile rows rw0..,
 // columns cw0..: in block (i, j) the lane holds, in register r, plane p's int32 sum for tile row
 // rw0 + 32 i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3) and column cw0 + 32 j + (lane & 31).
-// s_exp [BM] holds each tile row's exponent less 7 (P - 1). The planes combine exactly in double
-// (sum_p acc_p 2^(7(P-1-p)): integers below 2^53, so the fma is exact) and round once to f32.
+// exw is, in lane l, the exponent of wave row rw0 + l less 7 (P - 1); a register's row takes it with
+// ds_bpermute. The planes combine exactly (sum_p acc_p 2^(7(P-1-p)), an integer below 2^53) and round
+// once to f32: in double (CMB_F64), or for K <= 1024 (CMB_I32) the top two planes first in int32
+// (|acc_p| <= 128 x 127 x 1024, so |acc_0 2^7 + acc_1| < 2^31), which leaves P = 2 one int32 -> f32
+// conversion (correctly rounded, as the rounding of the double) and P = 3 one fma in double. Spike
+// products (one plane, no row exponents: every exponent 0) skip the exponent (CMB_NOEXP).
 // sc[j] and cv[j] are column (n0 + cw0 + 32 j + (lane & 31), clamped to n - 1)'s scale and colv
 // (EPI_MUL), loaded by the caller.
 // An interior tile stores (and, for EPI_ADD, loads) through a buffer resource based at its first
 // row: the lane's offset is one VGPR and each register's row offset a wave-uniform SGPR, so no
 // element forms a 64-bit address or tests a bound. Edge tiles and the int32 planes take the
 // checked path.
-template <int P, int EPI, int BM, int BN, int FM, int FN>
-__device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const int *s_exp, int m, int n, int m0,
-                                         int n0, int rw0, int cw0, const float (&sc)[FN], const float (&cv)[FN],
+enum { CMB_F64 = 0, CMB_I32 = 1, CMB_NOEXP = 2 };
+template <int P, int EPI, int BM, int BN, int FM, int FN, int CMB>
+__device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], int exw, int m, int n, int m0, int n0,
+                                         int rw0, int cw0, const float (&sc)[FN], const float (&cv)[FN],
                                          const EpiArgs &ep, int lane) {
     const int ccol = lane & 31, rsub = (lane >> 5) * 4;
+    auto row_exp = [&](int wr) { return __builtin_amdgcn_ds_bpermute(wr << 2, exw); };  // wave row wr's
+    // Block row i's exponents in one register: lane 16 q + z holds that of wave row 32 i + 8 (z >> 2) +
+    // (z & 3) + 4 (q >> 1), and register r of a block reads it from lane z = r of its DPP row by
+    // row_newbcast (every lane of a 16-lane row takes the row's lane r).
+    auto exp_row = [&](int i) {
+        const int z = lane & 15, q = lane >> 4;
+        return row_exp(32 * i + 8 * (z >> 2) + (z & 3) + 4 * (q >> 1));
+    };
+    auto bcast = [&](int e, int r) {
+        switch (r) {  // a constant in the unrolled loops (the DPP control must be one)
+#define AVA_BC(R) \
+    case R: return __builtin_amdgcn_mov_dpp(e, 0x150 + R, 0xf, 0xf, true);
+            AVA_BC(0) AVA_BC(1) AVA_BC(2) AVA_BC(3) AVA_BC(4) AVA_BC(5) AVA_BC(6) AVA_BC(7)
+            AVA_BC(8) AVA_BC(9) AVA_BC(10) AVA_BC(11) AVA_BC(12) AVA_BC(13) AVA_BC(14)
+#undef AVA_BC
+            default: return __builtin_amdgcn_mov_dpp(e, 0x150 + 15, 0xf, 0xf, true);
+        }
+    };
     auto value = [&](int i, int j, int r) {
         if (P == 1) return (float)acc[0][i][j][r];
+        if (CMB == CMB_I32) {
+            const int t = (int)((unsigned)acc[0][i][j][r] * 128u + (unsigned)acc[1][i][j][r]);
+            if (P == 2) return (float)t;
+            return (float)fma((double)t, 128.0, (double)acc[2][i][j][r]);
+        }
         double A = (double)acc[0][i][j][r];
 #pragma unroll
         for (int p = 1; p < P; p++) A = fma(A, 128.0, (double)acc[p][i][j][r]);
         return (float)A;
+    };
+    // the value under its row's exponent e (ldexp is exact; CMB_NOEXP: every e is 0)
+    auto scaled = [&](int i, int j, int r, int e) {
+        const float x = value(i, j, r);
+        return CMB == CMB_NOEXP ? x : ldexpf(x, e);
     };
     if (EPI == EPI_ACC) {
 #pragma unroll
@@ -201,22 +234,51 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
 #pragma unroll
             for (int r = 0; r < 16; r++) pv[r] = load_f32_nt(yr, voff + j * 128u, row_off(i, r));
         };
-        if (EPI == EPI_ADD) {
-            load_prev(0, prev[0]);
-            AVA_ISSUE_FENCE();
+        if (EPI != EPI_ADD) {
+            // a block row's FN blocks together: each broadcast exponent serves FN outputs
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const int er = exp_row(i);
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    int eg = er;  // a fresh copy per group of 4 rows (see below)
+#if defined(__HIP_DEVICE_COMPILE__)
+                    asm volatile("" : "+v"(eg));
+#endif
+#pragma unroll
+                    for (int z = 0; z < 4; z++) {
+                        const int r = g * 4 + z, e = CMB == CMB_NOEXP ? 0 : bcast(eg, r);
+#pragma unroll
+                        for (int j = 0; j < FN; j++) {
+                            float v = scaled(i, j, r, e) * sc[j];
+                            if (EPI == EPI_MUL) v = v * cv[j];
+                            store_f32_nt(yr, voff + j * 128u, row_off(i, r), v);
+                        }
+                    }
+                }
+            }
+            return;
         }
+        load_prev(0, prev[0]);
+        AVA_ISSUE_FENCE();
+        int er = 0;
 #pragma unroll
         for (int blk = 0; blk < NB; blk++) {
             const int i = blk / FN, j = blk % FN;
+            if (j == 0) er = exp_row(i);
             float v[16];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                // the exponents of rows r = 4 g .. 4 g + 3, read when needed (fewer live registers)
-                const i32x4 e4 = *reinterpret_cast<const i32x4 *>(s_exp + rw0 + i * 32 + g * 8 + rsub);
+                // a fresh copy per group of 4 rows: the broadcasts are not shared between blocks and
+                // formed when needed (16 held exponents cost registers the accumulators need)
+                int eg = er;
+#if defined(__HIP_DEVICE_COMPILE__)
+                asm volatile("" : "+v"(eg));
+#endif
 #pragma unroll
                 for (int z = 0; z < 4; z++) {
                     const int r = g * 4 + z;
-                    v[r] = ldexpf(value(i, j, r), e4[z]) * sc[j];
+                    v[r] = scaled(i, j, r, CMB == CMB_NOEXP ? 0 : bcast(eg, r)) * sc[j];
                     if (EPI == EPI_MUL) v[r] = v[r] * cv[j];
                     if (EPI == EPI_ADD) v[r] = prev[blk & 1][r] + v[r];
                 }
@@ -264,7 +326,7 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[P][FM][FN], const i
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int tr = rbase + (r >> 2) * 8 + (r & 3);
-                float v = ldexpf(value(i, j, r), s_exp[tr]) * sc[j];
+                float v = scaled(i, j, r, CMB == CMB_NOEXP ? 0 : row_exp(tr - rw0)) * sc[j];
                 if (EPI == EPI_MUL) v = v * cv[j];
                 if (EPI == EPI_ADD) v = prev[r] + v;
                 if (col_ok) store_f32(yr, off(r), 0u, v);
@@ -278,12 +340,6 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt");
     // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] in [15:14]
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-// Every LDS access of this wave is done.
-__device__ __forceinline__ void lgkm_wait0() {
-#if defined(__HIP_DEVICE_COMPILE__)
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#endif
 }
 
 // global_load_lds_dwordx4: 16 bytes per lane from `g` to LDS at `l` + 16 x lane (l wave-uniform). The
@@ -353,7 +409,7 @@ __device__ __forceinline__ void frag_schedule() {
     }
 }
 
-template <int P, int EPI, int BK>
+template <int P, int EPI, int BK, int CMB>
 __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(const int8_t *__restrict__ xq,
                                                                         const int32_t *__restrict__ xexp, int m,
                                                                         int n, int ldk, const int8_t *__restrict__ qt,
@@ -417,12 +473,12 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
     const BufRes xer = buf_res(const_cast<float *>(reinterpret_cast<const float *>(xexp)),
                                EPI != EPI_ACC && xexp ? (unsigned)m * 4u : 0u);
     for (; idx < total; idx += grid) {
-        // the tile's row exponents (every lane loads, lanes past BM a copy) and each lane's column
-        // scales, used by the epilogue: issued before the K loop, so the epilogue does not wait for
-        // the next tile's first-step loads issued in the last step. EPI_ADD waits for those anyway
-        // (its prior values are loaded after them) and loads its scales after the K loop, which keeps
-        // two registers free during it.
-        const int ex = __float_as_int(load_f32(xer, (unsigned)min(m0 + min(tid, BM - 1), m - 1) * 4u, 0u));
+        // the exponent of this wave's row wm MW + lane of the tile and each lane's column scales, used
+        // by the epilogue: issued before the K loop, so the epilogue does not wait for the next tile's
+        // first-step loads issued in the last step. EPI_ADD waits for those anyway (its prior values
+        // are loaded after them) and loads its scales after the K loop, which keeps two registers free
+        // during it.
+        const int ex = __float_as_int(load_f32(xer, (unsigned)min(m0 + wm * MW + lane, m - 1) * 4u, 0u));
         float sc[FN], cv[FN];
         auto load_cols = [&]() {
 #pragma unroll
@@ -498,18 +554,9 @@ __global__ __launch_bounds__(64 * GEMM_WM * GEMM_WN, 1) void q8_gemm_kernel(cons
         step(std::integral_constant<bool, true>{}, 0);
 #pragma nounroll
         for (int kt = 1; kt < KT; kt++) step(std::integral_constant<bool, false>{}, kt);
-        // the stage of the last step is free once every wave has read it: the row exponents (less
-        // 7 (P - 1)) go there
-        int *s_exp = reinterpret_cast<int *>(smem + st * STAGE);
-        if (EPI != EPI_ACC) {
-            lgkm_wait0();
-            __builtin_amdgcn_s_barrier();
-            if (tid < BM) s_exp[tid] = ex - 7 * (P - 1);
-            lgkm_wait0();
-            __builtin_amdgcn_s_barrier();
-        }
         if (EPI == EPI_ADD) load_cols();
-        epilogue<P, EPI, BM, BN, FM, FN>(acc, s_exp, m, n, m0, n0, wm * MW, wn * NW, sc, cv, ep, lane);
+        epilogue<P, EPI, BM, BN, FM, FN, CMB>(acc, ex - 7 * (P - 1), m, n, m0, n0, wm * MW, wn * NW, sc, cv, ep,
+                                              lane);
         loaded = EPI != EPI_ACC && m0 + BM <= m && n0 + BN <= n;  // the interior path ran
         m0 = mt * BM;  // the next tile (tile_origin ran at the last step)
         n0 = nt * BN;
@@ -844,11 +891,19 @@ int launch_tiled(const int8_t *xq, const int32_t *xexp, int m, int n, int ldk, c
     int grid = 0;
     if (int r = gemm_grid(tiles, &grid)) return r;
     const size_t lds = (size_t)2 * (P * GEMM_BM + GEMM_BN) * BK;
-    if (int r = ava::lds_opt_in((const void *)q8_gemm_kernel<P, EPI, BK>, lds)) return r;
-    q8_gemm_kernel<P, EPI, BK><<<dim3(grid), dim3(64 * GEMM_WM * GEMM_WN), lds, st>>>(xq, xexp, m, n, ldk, qt, scale,
-                                                                                     ep);
-    AVA_LAUNCHED("q8_gemm");
-    return AVA_OK;
+    auto go = [&](auto kern) -> int {
+        if (int r = ava::lds_opt_in((const void *)kern, lds)) return r;
+        kern<<<dim3(grid), dim3(64 * GEMM_WM * GEMM_WN), lds, st>>>(xq, xexp, m, n, ldk, qt, scale, ep);
+        AVA_LAUNCHED("q8_gemm");
+        return AVA_OK;
+    };
+    // the int32 plane combine holds for K <= 1024; spike products have no row exponents (see epilogue)
+    if constexpr (P == 1) {
+        if (EPI != EPI_ACC && !xexp) return go(q8_gemm_kernel<P, EPI, BK, CMB_NOEXP>);
+    } else {
+        if (EPI != EPI_ACC && ldk <= 1024) return go(q8_gemm_kernel<P, EPI, BK, CMB_I32>);
+    }
+    return go(q8_gemm_kernel<P, EPI, BK, CMB_F64>);
 }
 
 template <int P, int EPI>
