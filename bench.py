@@ -724,7 +724,7 @@ class Stack:
         # HBM bytes per q8 product launch, the mean over one forward's 51 launches, measured with
         # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this workload (2.0 x FETCH_SIZE + WRITE_SIZE,
         # KiB; the factor from the 1 GiB copy kernel of --workload copy)
-        self.traffic = 2.669e9
+        self.traffic = 2.740e9
 
     def _reset(self):
         st = self.st
