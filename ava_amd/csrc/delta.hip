@@ -309,9 +309,9 @@ __global__ __launch_bounds__(256) void delta_inv_kernel(DeltaInvArgs p) {
 // The six products of a chunk run as v_mfma_f32_32x32x16_bf16 on operands split into bf16 terms,
 // x = t0 + t1 + t2 (each term the rest rounded again to bf16). A product of order P keeps the terms
 // a_i b_j with i + j < P, with f32 accumulation: order 3 (six products per k step) leaves about 2^-24
-// of |a b|, as an f32 product does; order 2 (three) about 2^-17. The subtraction R = V - K F cancels
-// when the state already holds a key's value (a key read right after its write), so K F and Q F are
-// of order 3; the other four products (no cancellation downstream) are of order 2.
+// of |a b|, as an f32 product does; order 2 (three) about 2^-17. All six products are of order 3:
+// with order 2 the config[2] walk came 1.1e-5 from the float64 recurrence (order 3: 2.4e-7) and a key
+// read right after its write missed the 1e-4 read-back bar (R = V - K F cancels there).
 // Every operand lives in LDS as a term buffer: up to three planes of a 64 x 64 matrix, each row (the
 // output row of an A operand, the output column of a B operand) holding its 64 k values
 // contiguously, 72 apart (a 16-byte load per lane per k step, no bank conflicts across 8 lanes). The

@@ -154,6 +154,84 @@ __global__ __launch_bounds__(256) void lif_scan_kernel(const float *__restrict__
     }
 }
 
+// The same scan for one channel per lane when D is a multiple of 64 (a wave's lanes are 64
+// consecutive channels of one stream): the currents are read and the spikes written through buffer
+// resources based at the wave's first channel, with the lane's channel as the 32-bit lane offset and
+// the time step t D as the wave-uniform offset, so a step costs no 64-bit address arithmetic; whole
+// blocks of PF steps run without per-step bound checks, and a segment's parked state is written at the
+// end of its block (PF = LIF_SEG_STEPS). The same arithmetic as lif_scan_kernel, so the same bits.
+template <int PF, int LEVELS, bool SIGNED, bool ALIF>
+__global__ __launch_bounds__(256) void lif_scan_buf_kernel(const float *__restrict__ cur, int B, int T, int D,
+                                                           const float *__restrict__ ps, float *__restrict__ v,
+                                                           float *__restrict__ s, float *__restrict__ a,
+                                                           int8_t *__restrict__ spikes, float *__restrict__ th_out,
+                                                           float *__restrict__ park) {
+    static_assert(PF == ava::LIF_SEG_STEPS, "a parked segment is one block");
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= B * D) return;  // whole waves (B D is a multiple of 64)
+    const int lane = threadIdx.x & 63;
+    const int gw = __builtin_amdgcn_readfirstlane(gid - lane);  // the wave's first chain
+    const int bw = gw / D, cw = gw - bw * D, c = cw + lane, st = gw + lane;
+
+    const float bt = ps[c], th0 = ps[D + c], rho = ps[2 * D + c], gain = ps[3 * D + c];
+    const float omr = 1.0f - rho;
+    float vv = v[st], sp = s[st], aa = a[st];
+    float thp = ALIF ? th0 + aa * gain : th0;
+
+    const size_t chains = (size_t)B * D;
+    auto put_park = [&](int sg) {
+        float *pk = park + (size_t)sg * 3 * chains + st;
+        pk[0] = vv;
+        pk[chains] = sp;
+        pk[2 * chains] = aa;
+    };
+    if (park) put_park(0);
+
+    const size_t slab = (size_t)bw * T * D + cw;  // the wave's first channel at t = 0
+    const unsigned span = (unsigned)(T * D - cw);  // elements from there to the slab's end
+    const BufRes cr = buf_res(const_cast<float *>(cur) + slab, span * 4u);
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(spikes + slab, 0, (int)span, 0x00020000);
+#endif
+    const unsigned lv = (unsigned)lane * 4u, row4 = (unsigned)D * 4u;
+    auto step = [&](float x, unsigned t) {
+        float tht = th0;
+        if (ALIF) {
+            aa = aa * rho + fabsf(sp) * omr;
+            tht = th0 + aa * gain;
+        }
+        vv = (vv * bt + x) - sp * thp;
+        sp = spike_of<LEVELS, SIGNED>(vv, tht);
+        thp = tht;
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int8_t)sp, sr, lane, (int)(t * (unsigned)D), 0);
+#endif
+    };
+
+    float buf[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) buf[i] = load_f32_nt(cr, lv, (unsigned)min(i, T - 1) * row4);
+    const int full = T / PF;
+    for (int blk = 0; blk < full; blk++) {
+        const unsigned t0 = (unsigned)blk * PF;
+        float nxt[PF];
+        // the next block's currents (past T: the last step again, unused)
+#pragma unroll
+        for (int i = 0; i < PF; i++) nxt[i] = load_f32_nt(cr, lv, (unsigned)min((int)t0 + PF + i, T - 1) * row4);
+#pragma unroll
+        for (int i = 0; i < PF; i++) step(buf[i], t0 + i);
+        if (park && (int)t0 + PF < T) put_park(blk + 1);
+#pragma unroll
+        for (int i = 0; i < PF; i++) buf[i] = nxt[i];
+    }
+    for (int t = full * PF; t < T; t++) step(buf[t - full * PF], (unsigned)t);
+
+    v[st] = vv;
+    s[st] = sp;
+    a[st] = aa;
+    if (th_out) th_out[st] = thp;
+}
+
 template <int VEC, int PF>
 int launch_vp(const float *cur, int B, int T, int D, const float *ps, float *v, float *s, float *a,
               int levels, int is_signed, int alif, int8_t *spikes, float *th_out, hipStream_t st,
@@ -161,8 +239,17 @@ int launch_vp(const float *cur, int B, int T, int D, const float *ps, float *v, 
     AVA_REQUIRE(!park || VEC == 1, AVA_ERR_ARG, "lif_scan: parked states need one channel per lane");
     const long threads = (long)B * (D / VEC);
     dim3 grid(ava::ceil_div(threads, 256)), block(256);
-#define AVA_LIF_GO(L, S, A) \
-    lif_scan_kernel<VEC, PF, L, S, A><<<grid, block, 0, st>>>(cur, B, T, D, ps, v, s, a, spikes, th_out, park)
+    // the buffer form: whole waves per stream, and every offset of a stream's slab in 32 bits
+    const bool bufd = VEC == 1 && PF == ava::LIF_SEG_STEPS && D % 64 == 0 && (long)T * D * 4 < (1L << 31);
+#define AVA_LIF_GO(L, S, A)                                                                                         \
+    do {                                                                                                            \
+        if (bufd)                                                                                                   \
+            lif_scan_buf_kernel<PF, L, S, A><<<grid, block, 0, st>>>(cur, B, T, D, ps, v, s, a, spikes, th_out,    \
+                                                                     park);                                         \
+        else                                                                                                        \
+            lif_scan_kernel<VEC, PF, L, S, A><<<grid, block, 0, st>>>(cur, B, T, D, ps, v, s, a, spikes, th_out,   \
+                                                                      park);                                        \
+    } while (0)
     if (!is_signed) {
         if (alif) AVA_LIF_GO(1, false, true);
         else AVA_LIF_GO(1, false, false);
