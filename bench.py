@@ -59,7 +59,7 @@ class Lif:
     name = "lif"
     metric = "tokens/sec LIF scan @B=64,T=2048,C=2048 (config[1]), int2 spikes, ALIF, 1 GPU; % HBM roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
-    kernel = "lif_scan_kernel"
+    kernel = "lif_scan_buf_kernel"  # the scan for D a multiple of 64 (lif_scan_kernel otherwise)
 
     def __init__(self, B=64, T=2048, D=2048):
         import torch
@@ -264,7 +264,7 @@ class Delta:
     name = "delta"
     metric = "tokens/sec chunked delta rule @B=32,H=8,T=4096,d=64, chunks of 64 (config[2]), 1 GPU; % fp32 MFMA roofline"
     warm_extend = True  # short, repeatable steps: warm up for WARM_S seconds
-    kernel = "delta_chunk_kernel"
+    kernel = "delta_inv_kernel + delta_seq_bf_kernel"  # the two-phase form (see __init__)
 
     def __init__(self, B=32, H=8, T=4096):
         import torch
@@ -286,6 +286,7 @@ class Delta:
         one = os.environ.get("AVA_DELTA_ONE_KERNEL", "0") != "0"
         self.work_bytes = 0 if one else self.L.ava_delta_chunk_workspace(BH, T)
         self.work = torch.empty(self.work_bytes, dtype=torch.uint8, device="cuda") if self.work_bytes else None
+        self.kernel = "delta_plain_kernel" if one else "delta_inv_kernel + delta_seq_bf_kernel"
         self.tokens = B * T
         # read q, k, v, beta; write y and the final state
         self.bytes = 3 * BH * T * 64 * 4 + BH * T * 4 + BH * T * 64 * 4 + BH * 64 * 64 * 4
@@ -724,7 +725,7 @@ class Stack:
         # HBM bytes per q8 product launch, the mean over one forward's 51 launches, measured with
         # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this workload (2.0 x FETCH_SIZE + WRITE_SIZE,
         # KiB; the factor from the 1 GiB copy kernel of --workload copy)
-        self.traffic = 2.740e9
+        self.traffic = 2.746e9
 
     def _reset(self):
         st = self.st
