@@ -96,14 +96,15 @@ def run_lif_seg(cur, ps, v0, s0, a0, g, gv, ga, levels, signed, alif, slope, rg)
 @pytest.mark.parametrize("levels,signed", [(2, True), (1, True), (1, False)])
 @pytest.mark.parametrize("alif", [True, False])
 @pytest.mark.parametrize("rg", [False, True])
-def test_lif_bwd_segments(T, levels, signed, alif, rg):
+@pytest.mark.parametrize("D", [40, 64])
+def test_lif_bwd_segments(T, levels, signed, alif, rg, D):
     """ava_lif_scan_bwd_segments against the oracle's walk (which the one-lane kernel equals bit for bit):
     one step, a 32-step segment and a 1-step one, seven segments the last of them short. The segments'
     affine functions associate the backward sums differently: within 2e-6 of each output's largest
-    value here."""
+    value here. D=40 parks the states from the general scan, D=64 from the buffer-resource one."""
     slope = 0.5 if rg else 2.0
-    x = lif_inputs(T * 11 + levels + 2 * alif + 4 * rg, 3, T, 40, levels, signed)
-    print(f"lif_bwd segments T={T} levels={levels} signed={signed} alif={alif} rg={rg}", flush=True)
+    x = lif_inputs(T * 11 + levels + 2 * alif + 4 * rg + D, 3, T, D, levels, signed)
+    print(f"lif_bwd segments T={T} D={D} levels={levels} signed={signed} alif={alif} rg={rg}", flush=True)
     o = O.lif_bwd(x[0], x[1], x[5], x[2], x[3], x[4], x[6], x[7] if alif else None, levels=levels, signed=signed,
                   alif=alif, slope=slope, reset_grad=rg)
     gpu = run_lif_seg(*x, levels, signed, alif, slope, rg)

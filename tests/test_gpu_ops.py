@@ -41,10 +41,12 @@ def sig(x):
 @pytest.mark.parametrize("alif", [False, True])
 @pytest.mark.parametrize("theta_on", [False, True])
 @pytest.mark.parametrize("init_on", [False, True])
-def test_lif_matches_oracle_every_option(levels, signed, alif, theta_on, init_on, dev):
-    """lif_gen.rs:377-453: every option, spikes and final state exactly (B=3, T=37, D=8)."""
-    b, t, d = 3, 37, 8
-    seed = levels * 16 + signed * 8 + alif * 4 + theta_on * 2 + init_on + 1
+@pytest.mark.parametrize("d", [8, 64])
+def test_lif_matches_oracle_every_option(levels, signed, alif, theta_on, init_on, d, dev):
+    """lif_gen.rs:377-453: every option, spikes and final state exactly (B=3, T=37: one 32-step block
+    and a ragged tail). D=8 takes the general scan, D=64 the buffer-resource one (D a multiple of 64)."""
+    b, t = 3, 37
+    seed = levels * 16 + signed * 8 + alif * 4 + theta_on * 2 + init_on + 1 + d
     cur = ref_noise((b, t, d), seed, 1.3)
     beta = sig(ref_noise((d,), seed, 0.8))
     rho = sig(ref_noise((d,), seed, 1.0) + np.float32(2.5))
