@@ -198,6 +198,22 @@ def test_q8_matmul_planes_bit_exact_and_near_f32(din, dout, m, dev):
     assert np.max(np.abs(ref - exact) / (scale + 1e-30)) < 1e-5
 
 
+@pytest.mark.parametrize("din,dout,m", [(1024, 512, 600), (4096, 512, 600), (2048, 300, 530)])
+@pytest.mark.parametrize("planes", [2, 3])
+def test_q8_tiled_plane_combines_bit_exact(din, dout, m, planes, dev):
+    """The tiled product's two exact plane combinations, against the oracle's bits: K <= 1024 adds the top
+    two planes in int32 first, longer K combines every plane in double (2048 x 300: edge tiles in both
+    directions). Rows spread over 40 binades so the row exponents differ."""
+    rng = np.random.default_rng(din + dout + m + planes)
+    w = (rng.standard_normal((din, dout)) * 0.02).astype(np.float32)
+    x = (rng.standard_normal((m, din)) * np.exp2(rng.integers(-20, 20, (m, 1)))).astype(np.float32)
+    q_o, s_o = O.quantize_int8(w)
+    from ava_amd import ops
+    qw = ops.QW.from_tensor(cuda(w))
+    y = host(ops.mm(cuda(x), qw, planes=planes))
+    assert np.array_equal(y.view(np.uint32), O.q8_matmul_planes(x, planes, q_o, s_o).view(np.uint32))
+
+
 @pytest.mark.parametrize("din,dout,m", SHAPES)
 def test_q8_spike_product_is_the_reference_bits(din, dout, m, dev):
     """Integer inputs: the i8 MFMA product equals the reference's f32 fma chain bit for bit."""
