@@ -57,11 +57,13 @@ def run_lif(cur, ps, v0, s0, a0, g, gv, ga, levels, signed, alif, slope, rg):
 @pytest.mark.parametrize("levels,signed", [(2, True), (1, True), (1, False)])
 @pytest.mark.parametrize("alif", [True, False])
 @pytest.mark.parametrize("rg", [False, True])
-def test_lif_bwd(T, levels, signed, alif, rg):
-    """Segment edges: T below, at and above the 16-step segment (77 = a short first segment + 4)."""
+@pytest.mark.parametrize("D", [40, 64])
+def test_lif_bwd(T, levels, signed, alif, rg, D):
+    """Segment edges: T below, at and above the 16-step segment (77 = a short first segment + 4), on a
+    ragged last wave (D=40) and on whole waves of one stream (D=64)."""
     slope = 0.5 if rg else 2.0
-    x = lif_inputs(T * 7 + levels + 2 * alif + 4 * rg, 3, T, 40, levels, signed)
-    print(f"lif_bwd T={T} levels={levels} signed={signed} alif={alif} rg={rg}", flush=True)
+    x = lif_inputs(T * 7 + levels + 2 * alif + 4 * rg + D, 3, T, D, levels, signed)
+    print(f"lif_bwd T={T} D={D} levels={levels} signed={signed} alif={alif} rg={rg}", flush=True)
     o = O.lif_bwd(x[0], x[1], x[5], x[2], x[3], x[4], x[6], x[7] if alif else None, levels=levels, signed=signed,
                   alif=alif, slope=slope, reset_grad=rg)
     gpu = run_lif(*x, levels, signed, alif, slope, rg)
