@@ -57,6 +57,29 @@ def test_argument_errors_return_status_and_message():
     assert L.ava_train_new(C.byref(config_struct(cb)), C.c_float(4.0), 0, C.byref(h)) == 1
 
 
+def test_scan_and_product_argument_errors():
+    """The segmented LIF backward refuses a short workspace and a bad level count, the product a plane
+    count outside 1..3, a short workspace and weights whose K padding is wrong, all before touching the
+    GPU (the pointers below are never dereferenced)."""
+    from ava_amd._lib import QW
+    L = lib()
+    d = C.c_void_p(64)
+    B, T, D = 2, 100, 64
+    need = L.ava_lif_scan_bwd_segments_workspace(B, T, D)
+    assert need > 0 and L.ava_lif_scan_bwd_segments_workspace(0, T, D) == 0
+    args = lambda levels, ws_bytes: (d, B, T, D, d, d, d, d, levels, 1, 1, C.c_float(1.0), 1, d, d, d, d, d, d, d, d,
+                                     d, d, ws_bytes, None)
+    assert L.ava_lif_scan_bwd_segments(*args(2, need - 4)) == 2 and b"workspace" in L.ava_last_error()
+    assert L.ava_lif_scan_bwd_segments(*args(3, need)) == 1 and b"levels" in L.ava_last_error()
+    w = QW(din=100, dout=8, ldk=L.ava_q8_ldk(100), qt=64, scale=64)
+    ws = L.ava_q8_workspace(10, 100, 3)
+    assert L.ava_q8_matmul(d, 10, C.byref(w), 4, d, d, ws, None) == 1 and b"planes" in L.ava_last_error()
+    assert L.ava_q8_matmul(d, 10, C.byref(w), 3, d, d, ws - 1, None) == 2 and b"workspace" in L.ava_last_error()
+    bad = QW(din=100, dout=8, ldk=100, qt=64, scale=64)
+    assert L.ava_q8_matmul(d, 10, C.byref(bad), 3, d, d, ws, None) == 2 and b"ldk" in L.ava_last_error()
+    assert L.ava_q8_matmul(d, 0, C.byref(w), 3, d, d, ws, None) == 0  # no rows: nothing to do
+
+
 def test_ops_refuse_host_tensors():
     import torch
     from ava_amd import ops
