@@ -214,6 +214,37 @@ def test_q8_tiled_plane_combines_bit_exact(din, dout, m, planes, dev):
     assert np.array_equal(y.view(np.uint32), O.q8_matmul_planes(x, planes, q_o, s_o).view(np.uint32))
 
 
+@pytest.mark.parametrize("din,dout,m", [(1024, 512, 600), (4096, 512, 600), (1024, 1100, 300), (2048, 300, 530)])
+@pytest.mark.parametrize("kind", [2, 3])
+def test_q8_epilogues_scale_and_accumulate_bit_exact(din, dout, m, kind, dev):
+    """The stack's two other product epilogues through the library's own ava::q8_gemm: kind 2 stores
+    v * colv[col], kind 3 adds v to the prior y, each one f32 rounding after the oracle's product v, on
+    the tiled kernel (both plane combinations, edge tiles) and the few-rows one (300 rows)."""
+    import ctypes as C
+    import torch
+    from ava_amd import ops, _lib
+    f = getattr(_lib.lib(), "_ZN3ava7q8_gemmEPKaPKiiiPK6ava_qwiPfiPKfP12ihipStream_t")
+    f.restype = C.c_int
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                  C.c_void_p]
+    rng = np.random.default_rng(din + dout + m + kind)
+    w = (rng.standard_normal((din, dout)) * 0.02).astype(np.float32)
+    x = (rng.standard_normal((m, din)) * np.exp2(rng.integers(-8, 8, (m, 1)))).astype(np.float32)
+    y0 = rng.standard_normal((m, dout)).astype(np.float32)
+    cv = rng.uniform(0.5, 2.0, dout).astype(np.float32)
+    q_o, s_o = O.quantize_int8(w)
+    v = O.q8_matmul_planes(x, 3, q_o, s_o)
+    want = (v * cv).astype(np.float32) if kind == 2 else (y0 + v).astype(np.float32)
+    qw = ops.QW.from_tensor(cuda(w))
+    xq, xe = ops.quant_rows(cuda(x), 3)
+    y = cuda(y0)
+    colv = cuda(cv)
+    rc = f(xq.data_ptr(), xe.data_ptr(), 3, m, C.addressof(qw.c), kind, y.data_ptr(), dout, colv.data_ptr(),
+           torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("din,dout,m", SHAPES)
 def test_q8_spike_product_is_the_reference_bits(din, dout, m, dev):
     """Integer inputs: the i8 MFMA product equals the reference's f32 fma chain bit for bit."""
